@@ -1,0 +1,134 @@
+/*
+ * shannon_prime.h -- core types and the sp_shadow_cache_t write/read API,
+ * implemented on MI355X (gfx950) by libshannon_prime_hip.so.
+ *
+ * This re-declares the core C API that the reference bridge and engine call.
+ * The reference header (lib/shannon-prime/core/shannon_prime.h, included at
+ * src/tools/shannon_prime_llama.h:87) is absent from the reference checkout;
+ * the signatures below are inferred from its call sites, cited per entry.
+ *
+ * Every codec call below runs on the GPU: host vectors are staged to device
+ * memory, the HIP kernels compress or reconstruct them, and results come back
+ * to the caller's host buffers. There is no CPU codec path in this library;
+ * when no gfx950 device is present the init calls fail (return -1 / NULL).
+ */
+#ifndef SHANNON_PRIME_H
+#define SHANNON_PRIME_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SP_MAX_BANDS    16
+#define SP_MAX_HEAD_DIM 1024
+
+/* VHT2 p=2 normalisation convention (extension; the reference's CPU core and
+ * its CUDA kernel disagree, see shannon_prime_adreno.c:276-309 vs
+ * shannon_prime_cuda.cu:54-69). FINAL is the default. */
+#define SP_VHT2_NORM_FINAL 0
+#define SP_VHT2_NORM_STAGE 1
+
+/* Codec configuration. Fields used by the reference bridge:
+ * shannon_prime_llama.c:219-294 (head_dim, n_layers, n_heads_kv, k/v_n_bands,
+ * k/v_band_bits, use_mobius_mask, k/v_ternary_mask, use_fp8). */
+typedef struct {
+    int      head_dim;
+    int      n_layers;
+    int      n_heads_kv;
+    int      k_n_bands;
+    int      k_band_bits[SP_MAX_BANDS];
+    int      v_n_bands;
+    int      v_band_bits[SP_MAX_BANDS];
+    int      use_mobius_mask;
+    uint32_t k_ternary_mask;
+    uint32_t v_ternary_mask;
+    int      use_fp8;    /* advisory; this library has no fp8 path (int codes) */
+    int      vht2_norm;  /* SP_VHT2_NORM_FINAL (default) or SP_VHT2_NORM_STAGE */
+} sp_config_t;
+
+/* Banded quantizer geometry (sp_band_config_t; fields used at
+ * shannon_prime_cuda.cu:360-375, shannon_prime_vulkan.c:559-578). */
+typedef struct {
+    int      head_dim;
+    int      n_bands;
+    int      band_bits[SP_MAX_BANDS];
+    int      band_size;     /* head_dim / n_bands; last band absorbs remainder */
+    int      total_bytes;   /* sum_b 2 + ceil(size_b * bits_b / 8) */
+    uint32_t ternary_mask;  /* bit b: band b stored as {-1,0,+1} at 2 bits */
+} sp_band_config_t;
+
+/* Mobius squarefree-first permutation (sp_mobius_mask_t; .order used at
+ * shannon_prime_cuda.cu:428-445). order[r] = coefficient at position r. */
+typedef struct {
+    int  n;
+    int *order;
+} sp_mobius_mask_t;
+
+/* Ship shadow cache (sp_shadow_cache_t; fields used at
+ * shannon_prime_llama.c:413-428 and kv_cache.cpp:361-376). k_cache/v_cache are
+ * allocated by the CALLER: n_slots pointers, each max_seq * total_bytes bytes,
+ * slot = layer * n_heads_kv + head, record at pos * total_bytes. */
+typedef struct {
+    sp_config_t      config;
+    sp_band_config_t k_bands;
+    sp_band_config_t v_bands;
+    sp_mobius_mask_t mobius_mask;
+    uint8_t        **k_cache;
+    uint8_t        **v_cache;
+    void            *dev;   /* device-side state owned by the library */
+} sp_shadow_cache_t;
+
+/* ---- config (sp_config_init: shannon_prime_llama.c:220; kv_cache.cpp:298) ---- */
+void sp_config_init(sp_config_t *cfg, int head_dim, int n_layers, int n_heads_kv);
+void sp_config_print(const sp_config_t *cfg);
+
+/* ---- band geometry (sp_band_config_init: shannon_prime_cuda.cu:413-416;
+ *      _ext: CHANGELOG.md:109-116; sp_band_span: shannon_prime_vulkan.c:559) ---- */
+void sp_band_config_init(sp_band_config_t *bc, int head_dim, int n_bands, const int *band_bits);
+void sp_band_config_init_ext(sp_band_config_t *bc, int head_dim, int n_bands,
+                             const int *band_bits, uint32_t ternary_mask);
+void sp_band_span(const sp_band_config_t *bc, int band, int *offset, int *size);
+
+/* ---- Mobius mask (shannon_prime_cuda.cu:428-445) ---- */
+int  sp_mobius_mask_init(sp_mobius_mask_t *mask, int n);
+void sp_mobius_mask_free(sp_mobius_mask_t *mask);
+
+/* ---- shadow cache (shannon_prime_llama.c:413, 596-825) ----
+ * init returns 0 on success, -1 on bad config or when no GPU is usable. */
+int  sp_shadow_cache_init(sp_shadow_cache_t *sc, const sp_config_t *cfg);
+void sp_shadow_cache_free(sp_shadow_cache_t *sc);
+
+void sp_shadow_write_k(sp_shadow_cache_t *sc, int layer, int head, int pos, const float *k_vec);
+void sp_shadow_write_v(sp_shadow_cache_t *sc, int layer, int head, int pos, const float *v_vec);
+void sp_shadow_write_k_batch(sp_shadow_cache_t *sc, int layer, int head,
+                             int start_pos, int n_pos, const float *k_vecs);
+void sp_shadow_write_v_batch(sp_shadow_cache_t *sc, int layer, int head,
+                             int start_pos, int n_pos, const float *v_vecs);
+
+void sp_shadow_read_k(const sp_shadow_cache_t *sc, int layer, int head, int pos, float *k_out);
+void sp_shadow_read_v(const sp_shadow_cache_t *sc, int layer, int head, int pos, float *v_out);
+void sp_shadow_read_k_partial(const sp_shadow_cache_t *sc, int layer, int head, int pos,
+                              float *k_out, int max_bands);
+void sp_shadow_read_v_partial(const sp_shadow_cache_t *sc, int layer, int head, int pos,
+                              float *v_out, int max_bands);
+void sp_shadow_read_k_batch(const sp_shadow_cache_t *sc, int layer, int head,
+                            int start_pos, int n_pos, float *k_out);
+void sp_shadow_read_v_batch(const sp_shadow_cache_t *sc, int layer, int head,
+                            int start_pos, int n_pos, float *v_out);
+
+/* ---- utilities (shannon_prime_llama.c:919, 932; shannon_prime_hexagon.c:234-242) ---- */
+float    sp_correlation_f32(const float *a, const float *b, int n);
+float    sp_compression_ratio(const sp_config_t *cfg);
+float    sp_f16_to_f32(uint16_t h);
+uint16_t sp_f32_to_f16(float f);
+
+/* ---- sqfree geometry (sp_sqfree_pad_dim: shannon_prime_sqfree.cu:600) ---- */
+int sp_sqfree_pad_dim(int head_dim);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SHANNON_PRIME_H */

@@ -1,0 +1,290 @@
+/*
+ * sp_hip.h -- MI355X (gfx950) device API of the Shannon-Prime KV codec.
+ *
+ * Replaces the reference's CUDA backend boundary (src/backends/cuda/
+ * shannon_prime_cuda.h:29-378): the same cache objects (ship, sqfree, hier)
+ * with device pointers and a stream (void* = hipStream_t, NULL = default
+ * stream), plus fp16 entry points, layer-wide device-resident writes/reads
+ * and the fused decompress-attention launcher (replacing the CPU ggml custom
+ * op llama_sp_kq_compute, src/engine/llama_sp_fused_kq.h:95-99).
+ *
+ * Conventions: functions returning int give 0 on success and -1 on a bad
+ * argument (nothing is launched); void functions ignore bad arguments like the
+ * reference's. All launches are asynchronous on the cache's stream.
+ */
+#ifndef SP_HIP_H
+#define SP_HIP_H
+
+#include "shannon_prime.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SP_DTYPE_F32 0
+#define SP_DTYPE_F16 1
+
+/* ======================================================================== */
+/* Ship cache  (sp_cuda_cache_t, shannon_prime_cuda.h:29-46)                */
+/* ======================================================================== */
+
+typedef struct {
+    sp_config_t      config;
+    sp_band_config_t k_bands;
+    sp_band_config_t v_bands;
+    void            *d_k_cache;       /* [n_layers*n_heads_kv][max_seq][k_bytes] */
+    void            *d_v_cache;       /* [n_layers*n_heads_kv][max_seq][v_bytes] */
+    int              max_seq_len;
+    int             *d_mobius_order;  /* [head_dim] r -> coefficient (NULL: no Mobius) */
+    int             *d_mobius_inv;    /* [head_dim] coefficient -> r */
+    void            *stream;
+    void            *priv;            /* library-owned launch plans and workspace */
+} sp_hip_cache_t;
+
+/* shannon_prime_cuda.h:50-52 */
+int  sp_hip_cache_init(sp_hip_cache_t *cc, const sp_config_t *cfg, int max_seq_len, void *stream);
+void sp_hip_cache_free(sp_hip_cache_t *cc);
+
+/* single vector, device fp32 (shannon_prime_cuda.h:61-81) */
+void sp_hip_write_k(sp_hip_cache_t *cc, int layer, int head, int pos, const float *d_k_vec);
+void sp_hip_write_v(sp_hip_cache_t *cc, int layer, int head, int pos, const float *d_v_vec);
+void sp_hip_read_k(const sp_hip_cache_t *cc, int layer, int head, int pos, float *d_k_out);
+void sp_hip_read_v(const sp_hip_cache_t *cc, int layer, int head, int pos, float *d_v_out);
+
+/* batches of one slot, [n_pos][head_dim] contiguous (shannon_prime_cuda.h:91-110) */
+void sp_hip_write_k_batch(sp_hip_cache_t *cc, int layer, int head, int start_pos, int n_pos,
+                          const float *d_k_vecs);
+void sp_hip_write_v_batch(sp_hip_cache_t *cc, int layer, int head, int start_pos, int n_pos,
+                          const float *d_v_vecs);
+void sp_hip_read_k_batch(const sp_hip_cache_t *cc, int layer, int head, int start_pos, int n_pos,
+                         float *d_k_out);
+void sp_hip_read_v_batch(const sp_hip_cache_t *cc, int layer, int head, int start_pos, int n_pos,
+                         float *d_v_out);
+
+/* Partial-band batch reads (semantics of shannon_prime_llama.h:240-255). */
+void sp_hip_read_k_batch_partial(const sp_hip_cache_t *cc, int layer, int head, int start_pos,
+                                 int n_pos, float *d_k_out, int max_bands);
+void sp_hip_read_v_batch_partial(const sp_hip_cache_t *cc, int layer, int head, int start_pos,
+                                 int n_pos, float *d_v_out, int max_bands);
+
+/* fp16 batches (precedent: sp_adreno_write_k_f16, shannon_prime_adreno.h). */
+void sp_hip_write_k_batch_f16(sp_hip_cache_t *cc, int layer, int head, int start_pos, int n_pos,
+                              const void *d_k_f16);
+void sp_hip_write_v_batch_f16(sp_hip_cache_t *cc, int layer, int head, int start_pos, int n_pos,
+                              const void *d_v_f16);
+void sp_hip_read_k_batch_f16(const sp_hip_cache_t *cc, int layer, int head, int start_pos,
+                             int n_pos, void *d_k_f16);
+void sp_hip_read_v_batch_f16(const sp_hip_cache_t *cc, int layer, int head, int start_pos,
+                             int n_pos, void *d_v_f16);
+
+/* Layer-wide, device-resident (replaces the per-token x per-head loops of
+ * KvCache::write_gpu/read_gpu, kv_cache.cpp:1045-1228, and the gather/scatter
+ * of llama_sp_post_compute, llama-cpp-b8861-full-engine.patch:997-1360).
+ * K/V rows use llama.cpp's cache layout: element (t, h, d) at
+ * t*row_stride + h*head_dim + d, row_stride >= n_heads_kv*head_dim elements.
+ * One launch covers every head and token of the layer for K and one for V. */
+int sp_hip_write_layer(sp_hip_cache_t *cc, int layer, int start_pos, int n_tok,
+                       const void *d_k, const void *d_v, long long row_stride, int dtype);
+int sp_hip_read_layer(const sp_hip_cache_t *cc, int layer, int start_pos, int n_tok,
+                      void *d_k, void *d_v, long long row_stride, int dtype, int max_bands);
+
+/* Every slot at once: src/dst [n_layers*n_heads_kv][n_pos][head_dim] for positions
+ * [start_pos, start_pos+n_pos) of each slot (bulk prefill / bulk reconstruct). */
+int sp_hip_write_all(sp_hip_cache_t *cc, int start_pos, int n_pos,
+                     const void *d_k, const void *d_v, int dtype);
+int sp_hip_read_all(const sp_hip_cache_t *cc, int start_pos, int n_pos,
+                    void *d_k, void *d_v, int dtype, int max_bands);
+
+/* Host-buffer I/O on the device cache (stages through device memory and
+ * returns after the copy back): used by the bridge's HIP backend for the
+ * host-pointer sp_llama_write_* / sp_llama_read_* calls. */
+int sp_hip_write_host(sp_hip_cache_t *cc, int is_v, int layer, int head, int start_pos, int n_pos,
+                      const float *h_vecs);
+int sp_hip_read_host(const sp_hip_cache_t *cc, int is_v, int layer, int head, int start_pos,
+                     int n_pos, float *h_out, int max_bands);
+
+/* ---- stage launchers exposed for testing (shannon_prime_cuda.h:116-134) ---- */
+void sp_hip_vht2_forward(float *d_data, int n, int n_vecs, int vht2_norm, void *stream);
+void sp_hip_mobius_reorder(float *d_data, const int *d_order, int n, int n_vecs, void *stream);
+void sp_hip_mobius_unreorder(float *d_data, const int *d_order, int n, int n_vecs, void *stream);
+void sp_hip_band_quantize(const float *d_input, void *d_output, const sp_band_config_t *bc,
+                          int n_vecs, void *stream);
+void sp_hip_band_dequantize(const void *d_input, float *d_output, const sp_band_config_t *bc,
+                            int n_vecs, void *stream);
+
+/* ---- generic strided codec (what every ship entry point above launches) ----
+ * encode: vector (o, i) for o < n_outer, i < n_inner is read at element offset
+ *   o*src_outer + i*src_inner of d_src (dtype) and written as a record at byte
+ *   offset o*dst_outer + i*bc->total_bytes of d_dst.
+ * decode: the reverse; max_bands < 0 reconstructs every band.
+ * d_order: device [head_dim] Mobius order or NULL. */
+int sp_hip_ship_encode(const sp_band_config_t *bc, const int *d_order, int vht2_norm,
+                       const void *d_src, int src_dtype, long long src_outer, long long src_inner,
+                       void *d_dst, long long dst_outer, int n_outer, int n_inner, void *stream);
+int sp_hip_ship_decode(const sp_band_config_t *bc, const int *d_order, int vht2_norm,
+                       int max_bands, const void *d_src, long long src_outer,
+                       void *d_dst, int dst_dtype, long long dst_outer, long long dst_inner,
+                       int n_outer, int n_inner, void *stream);
+
+/* ======================================================================== */
+/* Fused decompress-attention decode (replaces llama_sp_kq_compute,        */
+/* src/engine/llama_sp_fused_kq.cpp:83-165, and the ggml softmax . V after  */
+/* it). Scores are taken against the spectral-domain keys: the query is     */
+/* transformed and Mobius-reordered once, packed K codes are dotted in      */
+/* place, and sum_t p_t * dequant(V_t) is accumulated in the spectral       */
+/* domain with one inverse transform per head, so no full-precision K or V  */
+/* is materialized.                                                         */
+/* ======================================================================== */
+
+/* q: [n_q][head_dim] fp32 for one decode token. Query head h reads KV head
+ * h / (n_q / n_heads_kv) (llama.cpp GQA grouping). Positions [0, n_kv) of
+ * `layer` are attended. scores (optional): [n_q][n_kv] fp32 = kq_scale*q.K~.
+ * out (optional): [n_q][head_dim] fp32 = softmax(scores) . V~.
+ * Returns -1 for bad arguments or n_kv beyond the workspace sized at init. */
+int sp_hip_attn_decode(const sp_hip_cache_t *cc, int layer, int n_kv,
+                       const float *d_q, int n_q, float kq_scale,
+                       float *d_scores, float *d_out, void *stream);
+
+/* Every layer of one decode step in one launch sequence: q [n_layers][n_q][hd],
+ * out [n_layers][n_q][hd] (benchmark helper; per-layer semantics above). */
+int sp_hip_attn_decode_all_layers(const sp_hip_cache_t *cc, int n_kv, const float *d_q,
+                                  int n_q, float kq_scale, float *d_out, void *stream);
+
+/* fp16 reference attention over an uncompressed cache, same layout contract
+ * as the compressed one ([slot][pos][head_dim] fp16): the baseline the fused
+ * kernel is compared against. */
+int sp_hip_attn_decode_f16(const void *d_k, const void *d_v, int n_heads_kv, int max_seq,
+                           int head_dim, int layer, int n_kv, const float *d_q, int n_q,
+                           float kq_scale, float *d_scores, float *d_out, void *stream);
+
+/* ======================================================================== */
+/* Sqfree + spinor cache (sp_cuda_sqfree_cache_t, shannon_prime_cuda.h:153-230) */
+/* ======================================================================== */
+
+typedef struct {
+    sp_config_t      config;
+    int              pad_dim;
+    int              sk_k;
+    int              n_res;
+    int              n_terms;
+    int              residual_bits;
+    int              use_spinor;
+    sp_band_config_t k_bands;   /* over the sk_k skeleton coefficients */
+    sp_band_config_t v_bands;
+    int             *d_skeleton_idx;
+    int             *d_residual_idx;
+    int             *d_csr_offsets;
+    int             *d_csr_skel_slot;
+    int             *d_csr_mu_sign;
+    unsigned char   *d_k_cache;
+    unsigned char   *d_v_cache;
+    int              bytes_per_pos_k;
+    int              bytes_per_pos_v;
+    int              max_seq_len;
+    int              n_slots;
+    void            *stream;
+    void            *priv;
+} sp_hip_sqfree_cache_t;
+
+/* shannon_prime_cuda.h:197-203. Skeleton = pad_dim/2 as the reference CUDA
+ * path (shannon_prime_sqfree.cu:606). */
+int  sp_hip_sqfree_cache_init(sp_hip_sqfree_cache_t *cc, const sp_config_t *cfg, int max_seq_len,
+                              int residual_bits, int use_spinor, void *stream);
+/* Extension: explicit skeleton size (SHANNON_PRIME_SK_FRAC * pad_dim, parsed by
+ * shannon_prime_llama_sqfree.c:68-71); sk_k <= 0 selects pad_dim/2. */
+int  sp_hip_sqfree_cache_init_ex(sp_hip_sqfree_cache_t *cc, const sp_config_t *cfg,
+                                 int max_seq_len, int residual_bits, int use_spinor, int sk_k,
+                                 void *stream);
+void sp_hip_sqfree_cache_free(sp_hip_sqfree_cache_t *cc);
+
+void sp_hip_sqfree_write_k(sp_hip_sqfree_cache_t *cc, int layer, int head, int pos, const float *d_k_vec);
+void sp_hip_sqfree_write_v(sp_hip_sqfree_cache_t *cc, int layer, int head, int pos, const float *d_v_vec);
+void sp_hip_sqfree_read_k(const sp_hip_sqfree_cache_t *cc, int layer, int head, int pos, float *d_k_out);
+void sp_hip_sqfree_read_v(const sp_hip_sqfree_cache_t *cc, int layer, int head, int pos, float *d_v_out);
+void sp_hip_sqfree_read_k_batch(const sp_hip_sqfree_cache_t *cc, int layer, int head,
+                                int start_pos, int n_pos, float *d_k_out);
+void sp_hip_sqfree_read_v_batch(const sp_hip_sqfree_cache_t *cc, int layer, int head,
+                                int start_pos, int n_pos, float *d_v_out);
+/* Extension: batched writes, fp32 or fp16 source [n_pos][head_dim]. */
+int  sp_hip_sqfree_write_batch(sp_hip_sqfree_cache_t *cc, int is_v, int layer, int head,
+                               int start_pos, int n_pos, const void *d_src, int dtype);
+int  sp_hip_sqfree_read_batch(const sp_hip_sqfree_cache_t *cc, int is_v, int layer, int head,
+                              int start_pos, int n_pos, void *d_dst, int dtype);
+/* Host copies of the Knight tables (for tests and calibration tools). */
+int  sp_hip_sqfree_get_tables(const sp_hip_sqfree_cache_t *cc, int *skeleton_idx,
+                              int *residual_idx, int *csr_offsets, int *csr_skel_slot,
+                              int *csr_mu_sign);
+
+/* ======================================================================== */
+/* Hierarchical cache (sp_cuda_hier_cache_t, shannon_prime_cuda.h:300-377)   */
+/* ======================================================================== */
+
+typedef struct {
+    sp_config_t      config;
+    int              pad_dim;
+    int              n_skeleton;
+    int              n_target;
+    int              target_res_bits;
+    int              n_slots;
+    int              max_seq_len;
+    uint16_t        *d_W;             /* [n_slots][n_target][n_skeleton] fp16 */
+    int             *d_skeleton_idx;
+    int             *d_target_idx;
+    sp_band_config_t skel_bands;
+    unsigned char   *d_k_cache;
+    unsigned char   *d_v_cache;
+    int              bytes_per_pos_k;
+    int              bytes_per_pos_v;
+    void            *stream;
+    void            *priv;
+} sp_hip_hier_cache_t;
+
+int  sp_hip_hier_cache_init(sp_hip_hier_cache_t *hc, const sp_config_t *cfg,
+                            int pad_dim, int n_skeleton, int n_target, int target_res_bits,
+                            const int *skeleton_idx, const int *target_idx,
+                            const sp_band_config_t *skel_bands, int max_seq_len, int n_slots,
+                            void *stream);
+void sp_hip_hier_cache_free(sp_hip_hier_cache_t *hc);
+int  sp_hip_hier_cache_upload_W(sp_hip_hier_cache_t *hc, const uint16_t *W_all);
+
+void sp_hip_hier_write_k(sp_hip_hier_cache_t *hc, int layer, int head, int pos, const float *d_k_vec);
+void sp_hip_hier_write_v(sp_hip_hier_cache_t *hc, int layer, int head, int pos, const float *d_v_vec);
+void sp_hip_hier_read_k(const sp_hip_hier_cache_t *hc, int layer, int head, int pos, float *d_k_out);
+void sp_hip_hier_read_v(const sp_hip_hier_cache_t *hc, int layer, int head, int pos, float *d_v_out);
+/* Extension: batched writes/reads of one slot, fp32 or fp16 [n_pos][head_dim]. */
+int  sp_hip_hier_write_batch(sp_hip_hier_cache_t *hc, int is_v, int layer, int head,
+                             int start_pos, int n_pos, const void *d_src, int dtype);
+int  sp_hip_hier_read_batch(const sp_hip_hier_cache_t *hc, int is_v, int layer, int head,
+                            int start_pos, int n_pos, void *d_dst, int dtype);
+
+/* ======================================================================== */
+/* Runtime                                                                  */
+/* ======================================================================== */
+
+/* 1 when a gfx950 device is visible and usable, else 0. */
+int         sp_hip_available(void);
+/* Last error text of the calling thread ("" when none). */
+const char *sp_hip_last_error(void);
+/* Stream-ordered event timing helpers (milliseconds between two records). */
+void       *sp_hip_event_create(void);
+void        sp_hip_event_destroy(void *ev);
+int         sp_hip_event_record(void *ev, void *stream);
+float       sp_hip_event_elapsed_ms(void *ev_start, void *ev_end);
+int         sp_hip_stream_sync(void *stream);
+/* Stream-ordered byte fill of device memory (used by sp_llama_clear_range). */
+int         sp_hip_memset(void *d_ptr, int value, size_t bytes, void *stream);
+/* Test hooks: the same codec through the generic (one vector per wave)
+ * kernels only, to cross-check the two kernel families. */
+int sp_hip_ship_encode_generic(const sp_band_config_t *bc, const int *d_order, int vht2_norm,
+                               const void *d_src, int src_dtype, long long src_outer,
+                               long long src_inner, void *d_dst, long long dst_outer, int n_outer,
+                               int n_inner, void *stream);
+int sp_hip_ship_decode_generic(const sp_band_config_t *bc, const int *d_order, int vht2_norm,
+                               int max_bands, const void *d_src, long long src_outer, void *d_dst,
+                               int dst_dtype, long long dst_outer, long long dst_inner, int n_outer,
+                               int n_inner, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SP_HIP_H */

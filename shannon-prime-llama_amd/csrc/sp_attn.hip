@@ -1,0 +1,314 @@
+// sp_attn.hip -- fused decompress-attention decode on gfx950.
+//
+// Replaces the CPU ggml custom op llama_sp_kq_compute
+// (src/engine/llama_sp_fused_kq.cpp:83-165), which decompresses each packed K
+// row (dequantize + inverse VHT2) and dots it with every query head, and the
+// ggml softmax . V that follows it.
+//
+// Because the VHT2 is symmetric and orthonormal and the Mobius reorder is a
+// permutation, q . K~_t = q~ . dq_t with q~ = reorder(VHT2(q)) and dq_t the
+// dequantized spectral record. Likewise sum_t p_t V~_t = VHT2(sum_t p_t dq_t).
+// So:
+//   1. k_attn_prep:   q~ = kq_scale * reorder(VHT2(q))        (one wave / head)
+//   2. k_attn_split:  per (kv head, 256-position split): scores straight from
+//                     the packed K codes, partial softmax (m, l), and the
+//                     spectral accumulation o~ = sum_t p_t dq(V_t); each packed
+//                     K and V record is read once for all query heads of its
+//                     GQA group.
+//   3. k_attn_combine: merge splits (log-sum-exp), one inverse VHT2 per head.
+// No full-precision K or V is materialized anywhere.
+#include "sp_internal.h"
+
+#define ATT_CHUNK 256
+#define ATT_MAX_G 8
+#define ATT_MAX_HD 256
+
+__global__ void __launch_bounds__(64)
+k_attn_prep(const SpPlan KP, const int *__restrict__ order, const float *__restrict__ q, int hd,
+            float kq_scale, float *__restrict__ qt) {
+    __shared__ float c[ATT_MAX_HD];
+    const int h = blockIdx.x, lane = threadIdx.x;
+    for (int k = lane; k < hd; k += SP_WAVE) c[k] = q[(long long)h * hd + k];
+    __syncthreads();
+    sp_transform_lds(c, hd, KP, lane);
+    for (int k = lane; k < hd; k += SP_WAVE) qt[(long long)h * hd + k] = kq_scale * (order ? c[order[k]] : c[k]);
+}
+
+__device__ __forceinline__ void att_tile_load(unsigned char *lds, const unsigned char *g, int nbytes,
+                                              int tid, int nthr) {
+    const int shift = (int)((uintptr_t)g & 3);
+    int head = (4 - shift) & 3;
+    if (head > nbytes) head = nbytes;
+    if (tid < head) lds[tid] = g[tid];
+    const int nw = (nbytes - head) >> 2;
+    const uint32_t *gw = reinterpret_cast<const uint32_t *>(g + head);
+    uint32_t *lw = reinterpret_cast<uint32_t *>(lds + head);
+    for (int k = tid; k < nw; k += nthr) lw[k] = gw[k];
+    for (int k = head + 4 * nw + tid; k < nbytes; k += nthr) lds[k] = g[k];
+}
+
+// ws layout per (q head, split): [m, l, o~[hd]]
+__global__ void __launch_bounds__(256)
+k_attn_split(const SpPlan KP, const SpPlan VP, const SpAttnArgs A, const float *__restrict__ qt,
+             float *__restrict__ ws, int n_splits, int want_out) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    __shared__ float q_s[ATT_MAX_G][ATT_MAX_HD];
+    __shared__ float s_s[ATT_MAX_G][ATT_CHUNK];
+    __shared__ float ml_s[ATT_MAX_G][2];
+
+    const int kvh = blockIdx.x, split = blockIdx.y, tid = threadIdx.x;
+    const int w = tid >> 6, lane = tid & 63;
+    const int G = A.n_q / A.n_kvh, h0 = kvh * G, hd = A.hd;
+    const int t0 = split * ATT_CHUNK;
+    const int nt = min(ATT_CHUNK, A.n_kv - t0);
+
+    const unsigned char *kg = A.kpack + (long long)kvh * A.k_head_stride + (long long)t0 * A.kB;
+    unsigned char *krec = smem + ((uintptr_t)kg & 3);
+    att_tile_load(krec, kg, nt * A.kB, tid, 256);
+    unsigned char *vbase = smem + ((ATT_CHUNK * A.kB + 8 + 15) & ~15);
+    const unsigned char *vg = A.vpack + (long long)kvh * A.v_head_stride + (long long)t0 * A.vB;
+    unsigned char *vrec = vbase + ((uintptr_t)vg & 3);
+    if (want_out) att_tile_load(vrec, vg, nt * A.vB, tid, 256);
+    for (int k = tid; k < G * hd; k += 256) q_s[k / hd][k % hd] = qt[(long long)(h0 + k / hd) * hd + (k % hd)];
+    __syncthreads();
+
+    // ---- scores: one position per thread, straight from the packed codes ----
+    if (tid < nt) {
+        const unsigned char *rec = krec + tid * A.kB;
+        float acc[ATT_MAX_G];
+#pragma unroll
+        for (int h = 0; h < ATT_MAX_G; h++) acc[h] = 0.0f;
+        for (int b = 0; b < KP.n_bands; b++) {
+            const int off = KP.band_off[b], sz = KP.band_sz[b], bits = KP.band_bits[b];
+            const int maxv = (1 << (bits - 1)) - 1;
+            const int bo = KP.band_byte_off[b];
+            const float scale = sp_scale_from_bits((uint32_t)rec[bo] | ((uint32_t)rec[bo + 1] << 8));
+            float part[ATT_MAX_G];
+#pragma unroll
+            for (int h = 0; h < ATT_MAX_G; h++) part[h] = 0.0f;
+            const unsigned char *data = rec + bo + 2;
+            for (int k = 0; k < sz; k++) {
+                const float d = (float)((int)sp_unpack_bits_lds(data, k, bits) - maxv);
+#pragma unroll
+                for (int h = 0; h < ATT_MAX_G; h++)
+                    if (h < G) part[h] = fmaf(q_s[h][off + k], d, part[h]);
+            }
+#pragma unroll
+            for (int h = 0; h < ATT_MAX_G; h++) acc[h] = fmaf(scale, part[h], acc[h]);
+        }
+#pragma unroll
+        for (int h = 0; h < ATT_MAX_G; h++)
+            if (h < G) {
+                s_s[h][tid] = acc[h];
+                if (A.scores) A.scores[(long long)(h0 + h) * A.n_kv + t0 + tid] = acc[h];
+            }
+    }
+    __syncthreads();
+    if (!want_out) return;
+
+    // ---- partial softmax per head (wave w handles heads w, w+4) ----
+    for (int h = w; h < G; h += 4) {
+        float m = -INFINITY;
+        for (int t = lane; t < nt; t += SP_WAVE) m = fmaxf(m, s_s[h][t]);
+        m = sp_wave_max(m);
+        float l = 0.0f;
+        for (int t = lane; t < nt; t += SP_WAVE) {
+            const float p = __expf(s_s[h][t] - m);
+            s_s[h][t] = p;
+            l += p;
+        }
+#pragma unroll
+        for (int s = 32; s >= 1; s >>= 1) l += __shfl_xor(l, s, SP_WAVE);
+        if (lane == 0) { ml_s[h][0] = m; ml_s[h][1] = l; }
+    }
+    __syncthreads();
+
+    // ---- spectral accumulation of V: thread owns element i ----
+    for (int i = tid; i < hd; i += 256) {
+        int b = 0;
+        while (b + 1 < VP.n_bands && i >= VP.band_off[b + 1]) b++;
+        const int bits = VP.band_bits[b], maxv = (1 << (bits - 1)) - 1;
+        const int bo = VP.band_byte_off[b], k = i - VP.band_off[b];
+        float o[ATT_MAX_G];
+#pragma unroll
+        for (int h = 0; h < ATT_MAX_G; h++) o[h] = 0.0f;
+        for (int t = 0; t < nt; t++) {
+            const unsigned char *rec = vrec + t * A.vB;
+            const float scale = sp_scale_from_bits((uint32_t)rec[bo] | ((uint32_t)rec[bo + 1] << 8));
+            const float d = (float)((int)sp_unpack_bits_lds(rec + bo + 2, k, bits) - maxv) * scale;
+#pragma unroll
+            for (int h = 0; h < ATT_MAX_G; h++)
+                if (h < G) o[h] = fmaf(s_s[h][t], d, o[h]);
+        }
+#pragma unroll
+        for (int h = 0; h < ATT_MAX_G; h++)
+            if (h < G) ws[((long long)(h0 + h) * n_splits + split) * (hd + 2) + 2 + i] = o[h];
+    }
+    if (tid < G) {
+        ws[((long long)(h0 + tid) * n_splits + split) * (hd + 2) + 0] = ml_s[tid][0];
+        ws[((long long)(h0 + tid) * n_splits + split) * (hd + 2) + 1] = ml_s[tid][1];
+    }
+}
+
+__global__ void __launch_bounds__(64)
+k_attn_combine(const SpPlan VP, const float *__restrict__ ws, int n_splits, int hd,
+               float *__restrict__ out) {
+    __shared__ float c[ATT_MAX_HD];
+    const int h = blockIdx.x, lane = threadIdx.x;
+    const float *base = ws + (long long)h * n_splits * (hd + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < n_splits; s++) M = fmaxf(M, base[(long long)s * (hd + 2)]);
+    float L = 0.0f;
+    for (int s = 0; s < n_splits; s++) L += base[(long long)s * (hd + 2) + 1] * __expf(base[(long long)s * (hd + 2)] - M);
+    const float invL = 1.0f / L;
+    for (int i = lane; i < hd; i += SP_WAVE) {
+        float acc = 0.0f;
+        for (int s = 0; s < n_splits; s++) {
+            const float *p = base + (long long)s * (hd + 2);
+            acc = fmaf(p[2 + i], __expf(p[0] - M), acc);
+        }
+        c[i] = acc * invL;
+    }
+    __syncthreads();
+    sp_transform_lds(c, hd, VP, lane);
+    for (int i = lane; i < hd; i += SP_WAVE) out[(long long)h * hd + i] = c[i];
+}
+
+size_t sp_attn_workspace_floats(int n_q, int hd, int max_kv) {
+    const int n_splits = (max_kv + ATT_CHUNK - 1) / ATT_CHUNK;
+    return (size_t)n_q * hd + (size_t)n_q * n_splits * (hd + 2);
+}
+
+hipError_t sp_launch_attn_decode(const SpPlan &KP, const SpPlan &VP, const int *order,
+                                 const SpAttnArgs &A, float *workspace, size_t ws_floats,
+                                 hipStream_t s) {
+    if (A.n_kv <= 0 || A.n_q <= 0 || A.n_kvh <= 0 || A.n_q % A.n_kvh) return hipErrorInvalidValue;
+    if (A.n_q / A.n_kvh > ATT_MAX_G || A.hd > ATT_MAX_HD) return hipErrorInvalidValue;
+    if (sp_attn_workspace_floats(A.n_q, A.hd, A.n_kv) > ws_floats) return hipErrorInvalidValue;
+    const int n_splits = (A.n_kv + ATT_CHUNK - 1) / ATT_CHUNK;
+    float *qt = workspace;
+    float *part = workspace + (size_t)A.n_q * A.hd;
+    hipLaunchKernelGGL(k_attn_prep, dim3(A.n_q), dim3(64), 0, s, KP, order, A.q, A.hd, A.kq_scale, qt);
+    const size_t lds = (size_t)((ATT_CHUNK * A.kB + 8 + 15) & ~15) + (size_t)ATT_CHUNK * A.vB + 8;
+    const int want_out = A.out != nullptr;
+    hipLaunchKernelGGL(k_attn_split, dim3(A.n_kvh, n_splits), dim3(256), lds, s, KP, VP, A, qt, part,
+                       n_splits, want_out);
+    if (want_out)
+        hipLaunchKernelGGL(k_attn_combine, dim3(A.n_q), dim3(64), 0, s, VP, part, n_splits, A.hd, A.out);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// fp16 uncompressed baseline with the same split structure
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+k_attn_f16_split(const unsigned short *__restrict__ K, const unsigned short *__restrict__ V,
+                 long long head_stride, int n_kv, int n_q, int n_kvh, int hd, float kq_scale,
+                 const float *__restrict__ q, float *__restrict__ scores, float *__restrict__ ws,
+                 int n_splits, int want_out) {
+    __shared__ float q_s[ATT_MAX_G][ATT_MAX_HD];
+    __shared__ float s_s[ATT_MAX_G][ATT_CHUNK];
+    __shared__ float ml_s[ATT_MAX_G][2];
+    const int kvh = blockIdx.x, split = blockIdx.y, tid = threadIdx.x;
+    const int w = tid >> 6, lane = tid & 63;
+    const int G = n_q / n_kvh, h0 = kvh * G;
+    const int t0 = split * ATT_CHUNK, nt = min(ATT_CHUNK, n_kv - t0);
+    for (int k = tid; k < G * hd; k += 256) q_s[k / hd][k % hd] = q[(long long)(h0 + k / hd) * hd + (k % hd)] * kq_scale;
+    __syncthreads();
+    const unsigned short *Kh = K + (long long)kvh * head_stride;
+    const unsigned short *Vh = V + (long long)kvh * head_stride;
+    if (tid < nt) {
+        const unsigned short *row = Kh + (long long)(t0 + tid) * hd;
+        float acc[ATT_MAX_G];
+#pragma unroll
+        for (int h = 0; h < ATT_MAX_G; h++) acc[h] = 0.0f;
+        for (int d0 = 0; d0 < hd; d0 += 8) {
+            const uint4 wv = *reinterpret_cast<const uint4 *>(row + d0);
+            const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float kv = sp_f16_bits_to_f32((ww[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+#pragma unroll
+                for (int h = 0; h < ATT_MAX_G; h++)
+                    if (h < G) acc[h] = fmaf(q_s[h][d0 + e], kv, acc[h]);
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < ATT_MAX_G; h++)
+            if (h < G) {
+                s_s[h][tid] = acc[h];
+                if (scores) scores[(long long)(h0 + h) * n_kv + t0 + tid] = acc[h];
+            }
+    }
+    __syncthreads();
+    if (!want_out) return;
+    for (int h = w; h < G; h += 4) {
+        float m = -INFINITY;
+        for (int t = lane; t < nt; t += SP_WAVE) m = fmaxf(m, s_s[h][t]);
+        m = sp_wave_max(m);
+        float l = 0.0f;
+        for (int t = lane; t < nt; t += SP_WAVE) {
+            const float p = __expf(s_s[h][t] - m);
+            s_s[h][t] = p;
+            l += p;
+        }
+#pragma unroll
+        for (int s = 32; s >= 1; s >>= 1) l += __shfl_xor(l, s, SP_WAVE);
+        if (lane == 0) { ml_s[h][0] = m; ml_s[h][1] = l; }
+    }
+    __syncthreads();
+    for (int i = tid; i < hd; i += 256) {
+        float o[ATT_MAX_G];
+#pragma unroll
+        for (int h = 0; h < ATT_MAX_G; h++) o[h] = 0.0f;
+        for (int t = 0; t < nt; t++) {
+            const float vv = sp_f16_bits_to_f32(Vh[(long long)(t0 + t) * hd + i]);
+#pragma unroll
+            for (int h = 0; h < ATT_MAX_G; h++)
+                if (h < G) o[h] = fmaf(s_s[h][t], vv, o[h]);
+        }
+#pragma unroll
+        for (int h = 0; h < ATT_MAX_G; h++)
+            if (h < G) ws[((long long)(h0 + h) * n_splits + split) * (hd + 2) + 2 + i] = o[h];
+    }
+    if (tid < G) {
+        ws[((long long)(h0 + tid) * n_splits + split) * (hd + 2) + 0] = ml_s[tid][0];
+        ws[((long long)(h0 + tid) * n_splits + split) * (hd + 2) + 1] = ml_s[tid][1];
+    }
+}
+
+__global__ void __launch_bounds__(64)
+k_attn_f16_combine(const float *__restrict__ ws, int n_splits, int hd, float *__restrict__ out) {
+    const int h = blockIdx.x, lane = threadIdx.x;
+    const float *base = ws + (long long)h * n_splits * (hd + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < n_splits; s++) M = fmaxf(M, base[(long long)s * (hd + 2)]);
+    float L = 0.0f;
+    for (int s = 0; s < n_splits; s++) L += base[(long long)s * (hd + 2) + 1] * __expf(base[(long long)s * (hd + 2)] - M);
+    const float invL = 1.0f / L;
+    for (int i = lane; i < hd; i += SP_WAVE) {
+        float acc = 0.0f;
+        for (int s = 0; s < n_splits; s++) {
+            const float *p = base + (long long)s * (hd + 2);
+            acc = fmaf(p[2 + i], __expf(p[0] - M), acc);
+        }
+        out[(long long)h * hd + i] = acc * invL;
+    }
+}
+
+hipError_t sp_launch_attn_f16(const unsigned short *k, const unsigned short *v,
+                              long long head_stride, int n_kv, int n_q, int n_kvh, int hd,
+                              float kq_scale, const float *q, float *scores, float *out,
+                              float *workspace, size_t ws_floats, hipStream_t s) {
+    if (n_kv <= 0 || n_q <= 0 || n_kvh <= 0 || n_q % n_kvh) return hipErrorInvalidValue;
+    if (n_q / n_kvh > ATT_MAX_G || hd > ATT_MAX_HD || hd % 8) return hipErrorInvalidValue;
+    if (sp_attn_workspace_floats(n_q, hd, n_kv) > ws_floats) return hipErrorInvalidValue;
+    const int n_splits = (n_kv + ATT_CHUNK - 1) / ATT_CHUNK;
+    float *part = workspace + (size_t)n_q * hd;
+    const int want_out = out != nullptr;
+    hipLaunchKernelGGL(k_attn_f16_split, dim3(n_kvh, n_splits), dim3(256), 0, s, k, v, head_stride,
+                       n_kv, n_q, n_kvh, hd, kq_scale, q, scores, part, n_splits, want_out);
+    if (want_out)
+        hipLaunchKernelGGL(k_attn_f16_combine, dim3(n_q), dim3(64), 0, s, part, n_splits, hd, out);
+    return hipGetLastError();
+}

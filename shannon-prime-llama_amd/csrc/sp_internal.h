@@ -1,0 +1,217 @@
+// sp_internal.h -- declarations shared by the kernel files and the host runtime.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "sp_device.h"
+#include "../../include/shannon_prime.h"
+
+#define SP_DT_F32 0
+#define SP_DT_F16 1
+
+template <int DT>
+__device__ __forceinline__ float sp_load1(const void *src, long long off) {
+    if (DT == SP_DT_F16)
+        return sp_f16_bits_to_f32(reinterpret_cast<const unsigned short *>(src)[off]);
+    return reinterpret_cast<const float *>(src)[off];
+}
+
+template <int DT>
+__device__ __forceinline__ void sp_store1(void *dst, long long off, float v) {
+    if (DT == SP_DT_F16) {
+        __asm__ volatile("" : "+v"(v));  // keep the fp32 rounding before the f16 one
+        _Float16 h = (_Float16)v;
+        reinterpret_cast<unsigned short *>(dst)[off] = __builtin_bit_cast(unsigned short, h);
+    } else {
+        reinterpret_cast<float *>(dst)[off] = v;
+    }
+}
+
+// Pack n codes (< 2^bits each, bits <= 8) as one LSB-first bit stream into
+// out[0, ceil(n*bits/8)). Each lane assembles whole output bytes.
+__device__ __forceinline__ void sp_pack_bits_lds(const unsigned char *codes, int n, int bits,
+                                                 unsigned char *out, int lane) {
+    const int nb = (n * bits + 7) / 8;
+    for (int kk = lane; kk < nb; kk += SP_WAVE) {
+        const int bit0 = kk * 8;
+        uint32_t acc = 0;
+        for (int e = bit0 / bits; e < n && e * bits < bit0 + 8; e++) {
+            const int sh = e * bits - bit0;
+            const uint32_t u = codes[e];
+            acc |= sh >= 0 ? (u << sh) : (u >> (-sh));
+        }
+        out[kk] = (unsigned char)(acc & 0xffu);
+    }
+}
+
+// Code k of an LSB-first stream (reads one byte past the code; callers pad).
+__device__ __forceinline__ uint32_t sp_unpack_bits_lds(const unsigned char *in, int k, int bits) {
+    const int bit = k * bits;
+    const uint32_t v = (uint32_t)in[bit >> 3] | ((uint32_t)in[(bit >> 3) + 1] << 8);
+    return (v >> (bit & 7)) & ((1u << bits) - 1u);
+}
+
+// ---- LDS-staged stages used by the one-vector-per-wave kernels ----
+// In-place transform of c[0, n) in LDS by the 64 lanes of one wave. Every wave
+// of the block calls it with the same n, so the block barriers are uniform.
+__device__ inline void sp_transform_lds(float *c, int n, const SpPlan &P, int lane) {
+    if (P.skip_transform) return;
+    if ((n & (n - 1)) == 0) {
+        const float s2 = 0.70710678118654752440f;
+        for (int len = 1; len < n; len <<= 1) {
+            for (int k = lane; k < n / 2; k += SP_WAVE) {
+                const int base = (k / len) * 2 * len + (k % len);
+                const float u = c[base], v = c[base + len];
+                if (P.norm == 1) {
+                    c[base] = (u + v) * s2;
+                    c[base + len] = (u - v) * s2;
+                } else {
+                    c[base] = u + v;
+                    c[base + len] = u - v;
+                }
+            }
+            __syncthreads();
+        }
+        if (P.norm != 1) {
+            for (int k = lane; k < n; k += SP_WAVE) c[k] *= P.inv_sqrt_n;
+            __syncthreads();
+        }
+        return;
+    }
+    int stride = 1;
+    for (int f = 0; f < P.n_factors; f++) {
+        const int p = P.factors[f];
+        const float *C = P.cas + sp_cas_off(p);
+        const float isp = P.isp[sp_prime_idx(p)];
+        const int block = stride * p;
+        for (int wi = lane; wi < n / p; wi += SP_WAVE) {
+            const int base = (wi / stride) * block + (wi % stride);
+            float gv[11], rv[11];
+            for (int k = 0; k < p; k++) gv[k] = c[base + k * stride];
+            for (int k = 0; k < p; k++) {
+                float sum = 0.0f;
+                for (int jj = 0; jj < p; jj++) sum += C[k * p + jj] * gv[jj];
+                rv[k] = sum * isp;
+            }
+            for (int k = 0; k < p; k++) c[base + k * stride] = rv[k];
+        }
+        stride *= p;
+        __syncthreads();
+    }
+}
+
+// Quantize coefficients r[0, P.hd) (LDS) into record bytes rec (LDS);
+// codes (LDS, >= P.hd bytes) is scratch. Ends with a block barrier.
+__device__ inline void sp_band_quantize_lds(const float *r, unsigned char *rec, unsigned char *codes,
+                                     const SpPlan &P, int lane) {
+    for (int b = 0; b < P.n_bands; b++) {
+        const int off = P.band_off[b], sz = P.band_sz[b], bits = P.band_bits[b];
+        const int maxv = (1 << (bits - 1)) - 1;
+        float m = 0.0f;
+        for (int k = lane; k < sz; k += SP_WAVE) {
+            float a = fabsf(r[off + k]);
+            m = a > m ? a : m;
+        }
+        const float amax = sp_wave_max(m);
+        const float scale = (amax > 0.0f) ? sp_div(amax, (float)maxv) : 0.0f;
+        const uint32_t h = sp_f32_to_f16_bits(scale);
+        const float ss = sp_f16_bits_to_f32(h);
+        const float inv = (ss > 0.0f) ? sp_div(1.0f, ss) : 0.0f;
+        for (int k = lane; k < sz; k += SP_WAVE)
+            codes[off + k] = (unsigned char)(sp_q_rint_clamp(r[off + k] * inv, maxv) + maxv);
+        if (lane == 0) {
+            rec[P.band_byte_off[b]] = (unsigned char)(h & 0xffu);
+            rec[P.band_byte_off[b] + 1] = (unsigned char)(h >> 8);
+        }
+    }
+    __syncthreads();
+    for (int b = 0; b < P.n_bands; b++)
+        sp_pack_bits_lds(codes + P.band_off[b], P.band_sz[b], P.band_bits[b],
+                         rec + P.band_byte_off[b] + 2, lane);
+    __syncthreads();
+}
+
+// Dequantize record rec (LDS) into out[0, P.hd) (LDS). Ends with a barrier.
+__device__ inline void sp_band_dequantize_lds(const unsigned char *rec, float *out, const SpPlan &P,
+                                       int lane) {
+    for (int b = 0; b < P.n_bands; b++) {
+        const int off = P.band_off[b], sz = P.band_sz[b], bits = P.band_bits[b];
+        const int maxv = (1 << (bits - 1)) - 1;
+        const int bo = P.band_byte_off[b];
+        const float scale = sp_scale_from_bits((uint32_t)rec[bo] | ((uint32_t)rec[bo + 1] << 8));
+        const bool live = b < P.max_bands;
+        for (int k = lane; k < sz; k += SP_WAVE) {
+            const int u = (int)sp_unpack_bits_lds(rec + bo + 2, k, bits);
+            out[off + k] = live ? (float)(u - maxv) * scale : 0.0f;
+        }
+    }
+    __syncthreads();
+}
+
+// ---- host side ----
+// Build the launch plan for band config bc with transform length n_transform.
+int sp_build_plan(const sp_band_config_t *bc, int n_transform, int norm, int max_bands, SpPlan *P);
+
+hipError_t sp_launch_ship_encode(const SpPlan &P, const int *order, const void *src, int dtype,
+                                 long long so, long long si, unsigned char *dst, long long dout,
+                                 int n_outer, int n_inner, hipStream_t s);
+hipError_t sp_launch_ship_decode(const SpPlan &P, const int *order, const unsigned char *src,
+                                 long long so, void *dst, int dtype, long long dout, long long din,
+                                 int n_outer, int n_inner, hipStream_t s);
+hipError_t sp_launch_ship_encode_generic(const SpPlan &P, const int *order, const void *src,
+                                         int dtype, long long so, long long si, unsigned char *dst,
+                                         long long dout, int n_outer, int n_inner, hipStream_t s);
+hipError_t sp_launch_ship_decode_generic(const SpPlan &P, const int *order,
+                                         const unsigned char *src, long long so, void *dst,
+                                         int dtype, long long dout, long long din, int n_outer,
+                                         int n_inner, hipStream_t s);
+hipError_t sp_launch_transform(const SpPlan &P, float *data, int n_vecs, hipStream_t s);
+hipError_t sp_launch_permute(float *data, const int *order, int n, int n_vecs, int inverse,
+                             hipStream_t s);
+
+// Sqfree / hier geometry handed to their kernels.
+struct SpSqGeo {
+    int hd, pad, sk_k, n_res, rbits, spinor, bytes;
+    const int *skel_idx, *res_idx, *csr_off, *csr_slot, *csr_mu;
+};
+struct SpHierGeo {
+    int hd, pad, n_skel, n_target, rbits, bytes;
+    const int *skel_idx, *target_idx;
+    const uint16_t *W;       // slot 0 predictor
+    long long w_outer;       // elements between consecutive outer slots' W
+};
+
+hipError_t sp_launch_sqfree_encode(const SpPlan &P, const SpSqGeo &G, const void *src, int dtype,
+                                   long long so, long long si, unsigned char *dst, long long dout,
+                                   int n_outer, int n_inner, hipStream_t s);
+hipError_t sp_launch_sqfree_decode(const SpPlan &P, const SpSqGeo &G, const unsigned char *src,
+                                   long long so, void *dst, int dtype, long long dout,
+                                   long long din, int n_outer, int n_inner, hipStream_t s);
+hipError_t sp_launch_hier_encode(const SpPlan &P, const SpHierGeo &G, const void *src, int dtype,
+                                 long long so, long long si, unsigned char *dst, long long dout,
+                                 int n_outer, int n_inner, hipStream_t s);
+hipError_t sp_launch_hier_decode(const SpPlan &P, const SpHierGeo &G, const unsigned char *src,
+                                 long long so, void *dst, int dtype, long long dout, long long din,
+                                 int n_outer, int n_inner, hipStream_t s);
+
+// Fused decode attention (sp_attn.hip).
+struct SpAttnArgs {
+    const unsigned char *kpack;  // layer base: [n_kvh][max_seq][kB]
+    const unsigned char *vpack;
+    long long k_head_stride, v_head_stride;  // bytes between KV heads
+    int kB, vB;
+    int n_kv, n_q, n_kvh, hd;
+    float kq_scale;
+    const float *q;     // [n_q][hd]
+    float *scores;      // [n_q][n_kv] or null
+    float *out;         // [n_q][hd] or null
+};
+hipError_t sp_launch_attn_decode(const SpPlan &KP, const SpPlan &VP, const int *order,
+                                 const SpAttnArgs &A, float *workspace, size_t ws_floats,
+                                 hipStream_t s);
+size_t sp_attn_workspace_floats(int n_q, int hd, int max_kv);
+hipError_t sp_launch_attn_f16(const unsigned short *k, const unsigned short *v,
+                              long long head_stride, int n_kv, int n_q, int n_kvh, int hd,
+                              float kq_scale, const float *q, float *scores, float *out,
+                              float *workspace, size_t ws_floats, hipStream_t s);

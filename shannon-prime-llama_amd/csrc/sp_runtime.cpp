@@ -1,0 +1,1203 @@
+// sp_runtime.cpp -- host runtime of libshannon_prime_hip.so: config and band
+// geometry, launch plans, the ship / sqfree / hier device caches, the
+// sp_shadow_cache_t host API over the GPU, fused attention wrappers.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <mutex>
+#include <vector>
+
+#include "../../include/shannon_prime.h"
+#include "../../include/sp_hip.h"
+#include "sp_internal.h"
+
+// ===========================================================================
+// errors
+// ===========================================================================
+static thread_local char g_err[512];
+
+static void set_err(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    if (getenv("SHANNON_PRIME_VERBOSE")) fprintf(stderr, "[Shannon-Prime HIP] %s\n", g_err);
+}
+
+static bool hip_ok(hipError_t e, const char *what) {
+    if (e == hipSuccess) return true;
+    set_err("%s: %s", what, hipGetErrorString(e));
+    return false;
+}
+
+extern "C" const char *sp_hip_last_error(void) { return g_err; }
+
+extern "C" int sp_hip_available(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return 0;
+    return strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+// ===========================================================================
+// core config / geometry (host)
+// ===========================================================================
+extern "C" void sp_config_init(sp_config_t *cfg, int head_dim, int n_layers, int n_heads_kv) {
+    memset(cfg, 0, sizeof(*cfg));
+    cfg->head_dim = head_dim;
+    cfg->n_layers = n_layers;
+    cfg->n_heads_kv = n_heads_kv;
+    // ship defaults (shannon_prime_llama.c:238-252): K 5/5/4/3, V flat 3
+    cfg->k_n_bands = 4;
+    cfg->k_band_bits[0] = 5;
+    cfg->k_band_bits[1] = 5;
+    cfg->k_band_bits[2] = 4;
+    cfg->k_band_bits[3] = 3;
+    cfg->v_n_bands = 1;
+    cfg->v_band_bits[0] = 3;
+    cfg->use_mobius_mask = 1;
+    cfg->vht2_norm = SP_VHT2_NORM_FINAL;
+}
+
+extern "C" void sp_band_config_init_ext(sp_band_config_t *bc, int head_dim, int n_bands,
+                                        const int *band_bits, uint32_t ternary_mask) {
+    memset(bc, 0, sizeof(*bc));
+    if (n_bands < 1) n_bands = 1;
+    if (n_bands > SP_MAX_BANDS) n_bands = SP_MAX_BANDS;
+    bc->head_dim = head_dim;
+    bc->n_bands = n_bands;
+    bc->band_size = head_dim / n_bands;
+    bc->ternary_mask = ternary_mask;
+    int total = 0;
+    for (int b = 0; b < n_bands; b++) {
+        const int bits = (ternary_mask & (1u << b)) ? 2 : band_bits[b];
+        bc->band_bits[b] = bits;
+        const int off = b * bc->band_size;
+        const int sz = (b == n_bands - 1) ? head_dim - off : bc->band_size;
+        total += 2 + (sz * bits + 7) / 8;
+    }
+    bc->total_bytes = total;
+}
+
+extern "C" void sp_band_config_init(sp_band_config_t *bc, int head_dim, int n_bands,
+                                    const int *band_bits) {
+    sp_band_config_init_ext(bc, head_dim, n_bands, band_bits, 0u);
+}
+
+extern "C" void sp_band_span(const sp_band_config_t *bc, int band, int *offset, int *size) {
+    const int off = band * bc->band_size;
+    *offset = off;
+    *size = (band == bc->n_bands - 1) ? bc->head_dim - off : bc->band_size;
+}
+
+static int is_squarefree(int n) {
+    if (n < 1) return 0;
+    for (int p = 2; p * p <= n; p++)
+        if (n % (p * p) == 0) return 0;
+    return 1;
+}
+
+static int mobius_mu(int n) {
+    if (n < 1) return 0;
+    int mu = 1;
+    for (int p = 2; p * p <= n; p++)
+        if (n % p == 0) {
+            n /= p;
+            if (n % p == 0) return 0;
+            mu = -mu;
+        }
+    return n > 1 ? -mu : mu;
+}
+
+// Squarefree-first order: coefficients i with i+1 squarefree (ascending), then
+// the rest (ascending). The reference's table builder lives in its absent core
+// (sp_mobius_mask_init, used at shannon_prime_cuda.cu:428-445); the kernels
+// take the table as data.
+static void build_mobius_order(int n, int *order) {
+    int r = 0;
+    for (int i = 0; i < n; i++) if (is_squarefree(i + 1)) order[r++] = i;
+    for (int i = 0; i < n; i++) if (!is_squarefree(i + 1)) order[r++] = i;
+}
+
+extern "C" int sp_mobius_mask_init(sp_mobius_mask_t *mask, int n) {
+    if (!mask || n <= 0) return -1;
+    mask->n = n;
+    mask->order = (int *)malloc(sizeof(int) * (size_t)n);
+    if (!mask->order) return -1;
+    build_mobius_order(n, mask->order);
+    return 0;
+}
+
+extern "C" void sp_mobius_mask_free(sp_mobius_mask_t *mask) {
+    if (!mask) return;
+    free(mask->order);
+    mask->order = nullptr;
+    mask->n = 0;
+}
+
+static int is_11_smooth(int n) {
+    static const int primes[5] = {2, 3, 5, 7, 11};
+    for (int i = 0; i < 5; i++) while (n % primes[i] == 0) n /= primes[i];
+    return n == 1;
+}
+
+extern "C" int sp_sqfree_pad_dim(int head_dim) {
+    if (head_dim <= 0) return -1;
+    for (int n = head_dim; n < 16 * head_dim + 64; n++)
+        if (is_squarefree(n) && is_11_smooth(n)) return n;
+    return -1;
+}
+
+static int factor_small(int n, unsigned char *f, int maxf) {
+    static const int primes[5] = {2, 3, 5, 7, 11};
+    int nf = 0, d = n;
+    for (int i = 0; i < 5; i++)
+        while (d % primes[i] == 0 && nf < maxf) { f[nf++] = (unsigned char)primes[i]; d /= primes[i]; }
+    return d == 1 ? nf : -1;
+}
+
+int sp_build_plan(const sp_band_config_t *bc, int n_transform, int norm, int max_bands, SpPlan *P) {
+    memset(P, 0, sizeof(*P));
+    if (bc->head_dim <= 0 || bc->n_bands < 1 || bc->n_bands > SP_MAX_BANDS) return -1;
+    P->hd = bc->head_dim;
+    P->n_bands = bc->n_bands;
+    P->norm = norm;
+    P->inv_sqrt_n = 1.0f / sqrtf((float)n_transform);
+    P->max_bands = (max_bands < 0 || max_bands > bc->n_bands) ? bc->n_bands : max_bands;
+    int byte_off = 0, chunk_ok = (bc->head_dim % 8 == 0) && (bc->head_dim / 8 <= SP_MAX_CHUNKS);
+    for (int b = 0; b < bc->n_bands; b++) {
+        const int bits = bc->band_bits[b];
+        if (bits < 1 || bits > 8) return -1;
+        const int off = b * bc->band_size;
+        const int sz = (b == bc->n_bands - 1) ? bc->head_dim - off : bc->band_size;
+        if (sz <= 0) return -1;
+        P->band_bits[b] = (unsigned char)bits;
+        P->band_off[b] = (short)off;
+        P->band_sz[b] = (short)sz;
+        P->band_byte_off[b] = (short)byte_off;
+        byte_off += 2 + (sz * bits + 7) / 8;
+        if (off % 8 || sz % 8) chunk_ok = 0;
+    }
+    P->total_bytes = byte_off;
+    P->chunk_ok = chunk_ok;
+    if (chunk_ok) {
+        for (int b = 0; b < bc->n_bands; b++) {
+            P->chunk_first[b] = (unsigned char)(P->band_off[b] / 8);
+            P->chunk_last[b] = (unsigned char)((P->band_off[b] + P->band_sz[b]) / 8 - 1);
+            for (int c = P->band_off[b] / 8; c <= P->chunk_last[b]; c++) {
+                P->chunk_band[c] = (unsigned char)b;
+                P->chunk_byte_off[c] =
+                    (short)(P->band_byte_off[b] + 2 + (c * 8 - P->band_off[b]) * P->band_bits[b] / 8);
+            }
+        }
+    }
+    const int pw2 = n_transform > 0 && (n_transform & (n_transform - 1)) == 0;
+    if (!pw2) {
+        const int nf = factor_small(n_transform, P->factors, 16);
+        if (nf <= 0) return -1;
+        P->n_factors = nf;
+    }
+    static const int primes[5] = {2, 3, 5, 7, 11};
+    static const int offs[5] = {SP_CAS_OFF2, SP_CAS_OFF3, SP_CAS_OFF5, SP_CAS_OFF7, SP_CAS_OFF11};
+    for (int pi = 0; pi < 5; pi++) {
+        const int p = primes[pi];
+        for (int k = 0; k < p; k++)
+            for (int j = 0; j < p; j++) {
+                const double a = 2.0 * M_PI * (double)((k * j) % p) / (double)p;
+                P->cas[offs[pi] + k * p + j] = (float)(cos(a) + sin(a));
+            }
+        P->isp[pi] = 1.0f / sqrtf((float)p);
+    }
+    return 0;
+}
+
+static bool valid_bits(const int *bits, int n) {
+    if (n < 1 || n > SP_MAX_BANDS) return false;
+    for (int i = 0; i < n; i++)
+        if (bits[i] < 1 || bits[i] > 8) return false;
+    return true;
+}
+
+extern "C" float sp_compression_ratio(const sp_config_t *cfg) {
+    sp_band_config_t k, v;
+    sp_band_config_init_ext(&k, cfg->head_dim, cfg->k_n_bands, cfg->k_band_bits, cfg->k_ternary_mask);
+    sp_band_config_init_ext(&v, cfg->head_dim, cfg->v_n_bands, cfg->v_band_bits, cfg->v_ternary_mask);
+    return (float)(4.0 * cfg->head_dim / (double)(k.total_bytes + v.total_bytes));
+}
+
+extern "C" void sp_config_print(const sp_config_t *cfg) {
+    fprintf(stderr, "  head_dim=%d n_layers=%d n_heads_kv=%d mobius=%d norm=%s\n", cfg->head_dim,
+            cfg->n_layers, cfg->n_heads_kv, cfg->use_mobius_mask,
+            cfg->vht2_norm == SP_VHT2_NORM_STAGE ? "stage" : "final");
+    fprintf(stderr, "  K bands:");
+    for (int i = 0; i < cfg->k_n_bands; i++) fprintf(stderr, " %d", cfg->k_band_bits[i]);
+    fprintf(stderr, "  V bands:");
+    for (int i = 0; i < cfg->v_n_bands; i++) fprintf(stderr, " %d", cfg->v_band_bits[i]);
+    fprintf(stderr, "  ratio %.2fx\n", sp_compression_ratio(cfg));
+}
+
+extern "C" float sp_correlation_f32(const float *a, const float *b, int n) {
+    if (!a || !b || n <= 0) return 0.0f;
+    double ma = 0, mb = 0;
+    for (int i = 0; i < n; i++) { ma += a[i]; mb += b[i]; }
+    ma /= n;
+    mb /= n;
+    double sab = 0, saa = 0, sbb = 0;
+    for (int i = 0; i < n; i++) {
+        const double x = a[i] - ma, y = b[i] - mb;
+        sab += x * y;
+        saa += x * x;
+        sbb += y * y;
+    }
+    if (saa <= 0 || sbb <= 0) return 0.0f;
+    return (float)(sab / sqrt(saa * sbb));
+}
+
+extern "C" float sp_f16_to_f32(uint16_t h) {
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu, f;
+    if (e == 0) {
+        if (m == 0) f = sign;
+        else {
+            int ee = -14;
+            while (!(m & 0x400u)) { m <<= 1; ee--; }
+            f = sign | ((uint32_t)(ee + 127) << 23) | ((m & 0x3ffu) << 13);
+        }
+    } else if (e == 31) f = sign | 0x7f800000u | (m << 13);
+    else f = sign | ((e + 112u) << 23) | (m << 13);
+    float r;
+    memcpy(&r, &f, 4);
+    return r;
+}
+
+extern "C" uint16_t sp_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) return (uint16_t)(sign | (ax > 0x7f800000u ? 0x7e00u : 0x7c00u));
+    int e = (int)(ax >> 23) - 127;
+    uint32_t m = ax & 0x7fffffu;
+    if (e > 15) return (uint16_t)(sign | 0x7c00u);
+    if (e >= -14) {
+        uint32_t keep = m >> 13, rem = m & 0x1fffu, r = ((uint32_t)(e + 15) << 10) | keep;
+        if (rem > 0x1000u || (rem == 0x1000u && (keep & 1u))) r += 1;
+        return (uint16_t)(sign | r);
+    }
+    if (ax == 0) return (uint16_t)sign;
+    int shift = -e - 1;
+    if (shift > 24) return (uint16_t)sign;
+    uint32_t mfull = m | 0x800000u, keep = mfull >> shift, rem = mfull & ((1u << shift) - 1u);
+    uint32_t half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (keep & 1u))) keep += 1;
+    return (uint16_t)(sign | keep);
+}
+
+// ===========================================================================
+// generic codec entry points
+// ===========================================================================
+extern "C" int sp_hip_ship_encode(const sp_band_config_t *bc, const int *d_order, int vht2_norm,
+                                  const void *d_src, int src_dtype, long long src_outer,
+                                  long long src_inner, void *d_dst, long long dst_outer,
+                                  int n_outer, int n_inner, void *stream) {
+    if (!bc || !d_src || !d_dst || n_outer < 0 || n_inner < 0) { set_err("encode: bad args"); return -1; }
+    SpPlan P;
+    if (sp_build_plan(bc, bc->head_dim, vht2_norm, -1, &P)) { set_err("encode: bad band config"); return -1; }
+    return hip_ok(sp_launch_ship_encode(P, d_order, d_src, src_dtype, src_outer, src_inner,
+                                        (unsigned char *)d_dst, dst_outer, n_outer, n_inner,
+                                        (hipStream_t)stream), "encode launch") ? 0 : -1;
+}
+
+extern "C" int sp_hip_ship_decode(const sp_band_config_t *bc, const int *d_order, int vht2_norm,
+                                  int max_bands, const void *d_src, long long src_outer,
+                                  void *d_dst, int dst_dtype, long long dst_outer,
+                                  long long dst_inner, int n_outer, int n_inner, void *stream) {
+    if (!bc || !d_src || !d_dst || n_outer < 0 || n_inner < 0) { set_err("decode: bad args"); return -1; }
+    SpPlan P;
+    if (sp_build_plan(bc, bc->head_dim, vht2_norm, max_bands, &P)) { set_err("decode: bad band config"); return -1; }
+    return hip_ok(sp_launch_ship_decode(P, d_order, (const unsigned char *)d_src, src_outer, d_dst,
+                                        dst_dtype, dst_outer, dst_inner, n_outer, n_inner,
+                                        (hipStream_t)stream), "decode launch") ? 0 : -1;
+}
+
+// test hook: force the generic (one vector per wave) kernels
+extern "C" int sp_hip_ship_encode_generic(const sp_band_config_t *bc, const int *d_order,
+                                          int vht2_norm, const void *d_src, int src_dtype,
+                                          long long src_outer, long long src_inner, void *d_dst,
+                                          long long dst_outer, int n_outer, int n_inner,
+                                          void *stream) {
+    SpPlan P;
+    if (!bc || sp_build_plan(bc, bc->head_dim, vht2_norm, -1, &P)) return -1;
+    return hip_ok(sp_launch_ship_encode_generic(P, d_order, d_src, src_dtype, src_outer, src_inner,
+                                                (unsigned char *)d_dst, dst_outer, n_outer, n_inner,
+                                                (hipStream_t)stream), "encode_generic") ? 0 : -1;
+}
+
+extern "C" int sp_hip_ship_decode_generic(const sp_band_config_t *bc, const int *d_order,
+                                          int vht2_norm, int max_bands, const void *d_src,
+                                          long long src_outer, void *d_dst, int dst_dtype,
+                                          long long dst_outer, long long dst_inner, int n_outer,
+                                          int n_inner, void *stream) {
+    SpPlan P;
+    if (!bc || sp_build_plan(bc, bc->head_dim, vht2_norm, max_bands, &P)) return -1;
+    return hip_ok(sp_launch_ship_decode_generic(P, d_order, (const unsigned char *)d_src, src_outer,
+                                                d_dst, dst_dtype, dst_outer, dst_inner, n_outer,
+                                                n_inner, (hipStream_t)stream), "decode_generic") ? 0 : -1;
+}
+
+extern "C" void sp_hip_vht2_forward(float *d_data, int n, int n_vecs, int vht2_norm, void *stream) {
+    sp_band_config_t bc;
+    int bits = 8;
+    sp_band_config_init(&bc, n, 1, &bits);
+    SpPlan P;
+    if (!d_data || n <= 0 || sp_build_plan(&bc, n, vht2_norm, -1, &P)) { set_err("vht2: bad dim %d", n); return; }
+    hip_ok(sp_launch_transform(P, d_data, n_vecs, (hipStream_t)stream), "vht2");
+}
+
+extern "C" void sp_hip_mobius_reorder(float *d_data, const int *d_order, int n, int n_vecs, void *stream) {
+    if (!d_data || !d_order || n <= 0) return;
+    hip_ok(sp_launch_permute(d_data, d_order, n, n_vecs, 0, (hipStream_t)stream), "reorder");
+}
+
+extern "C" void sp_hip_mobius_unreorder(float *d_data, const int *d_order, int n, int n_vecs, void *stream) {
+    if (!d_data || !d_order || n <= 0) return;
+    hip_ok(sp_launch_permute(d_data, d_order, n, n_vecs, 1, (hipStream_t)stream), "unreorder");
+}
+
+// Quantize / dequantize without transform: a plan whose transform is the
+// identity is not expressible, so these run the generic kernels on a plan with
+// zero transform stages (n_transform = 1).
+extern "C" void sp_hip_band_quantize(const float *d_input, void *d_output, const sp_band_config_t *bc,
+                                     int n_vecs, void *stream) {
+    SpPlan P;
+    if (!bc || !d_input || !d_output || sp_build_plan(bc, 1, 0, -1, &P)) return;
+    P.chunk_ok = 0;
+    P.skip_transform = 1;
+    hip_ok(sp_launch_ship_encode_generic(P, nullptr, d_input, SP_DT_F32, 0, bc->head_dim,
+                                         (unsigned char *)d_output, 0, 1, n_vecs, (hipStream_t)stream),
+           "band_quantize");
+}
+
+extern "C" void sp_hip_band_dequantize(const void *d_input, float *d_output, const sp_band_config_t *bc,
+                                       int n_vecs, void *stream) {
+    SpPlan P;
+    if (!bc || !d_input || !d_output || sp_build_plan(bc, 1, 0, -1, &P)) return;
+    P.chunk_ok = 0;
+    P.skip_transform = 1;
+    hip_ok(sp_launch_ship_decode_generic(P, nullptr, (const unsigned char *)d_input, 0, d_output,
+                                         SP_DT_F32, 0, bc->head_dim, 1, n_vecs, (hipStream_t)stream),
+           "band_dequantize");
+}
+
+// ===========================================================================
+// ship device cache
+// ===========================================================================
+struct ShipPriv {
+    SpPlan kplan, vplan;
+    float *ws = nullptr;
+    size_t ws_floats = 0;
+    int max_q = 0;
+};
+
+static bool check_cfg(const sp_config_t *cfg) {
+    if (!cfg || cfg->head_dim <= 0 || cfg->head_dim > SP_MAX_HEAD_DIM || cfg->n_layers <= 0 ||
+        cfg->n_heads_kv <= 0) return false;
+    if (!valid_bits(cfg->k_band_bits, cfg->k_n_bands) || !valid_bits(cfg->v_band_bits, cfg->v_n_bands))
+        return false;
+    return true;
+}
+
+extern "C" int sp_hip_cache_init(sp_hip_cache_t *cc, const sp_config_t *cfg, int max_seq_len, void *stream) {
+    if (!cc) return -1;
+    memset(cc, 0, sizeof(*cc));
+    if (!check_cfg(cfg) || max_seq_len <= 0) { set_err("cache_init: bad config"); return -1; }
+    if (!sp_hip_available()) { set_err("cache_init: no gfx950 device"); return -1; }
+    cc->config = *cfg;
+    cc->max_seq_len = max_seq_len;
+    cc->stream = stream;
+    const int hd = cfg->head_dim;
+    sp_band_config_init_ext(&cc->k_bands, hd, cfg->k_n_bands, cfg->k_band_bits, cfg->k_ternary_mask);
+    sp_band_config_init_ext(&cc->v_bands, hd, cfg->v_n_bands, cfg->v_band_bits, cfg->v_ternary_mask);
+    ShipPriv *pv = new ShipPriv();
+    if (sp_build_plan(&cc->k_bands, hd, cfg->vht2_norm, -1, &pv->kplan) ||
+        sp_build_plan(&cc->v_bands, hd, cfg->vht2_norm, -1, &pv->vplan)) {
+        delete pv;
+        set_err("cache_init: head_dim %d does not factor over {2,3,5,7,11}", hd);
+        return -1;
+    }
+    if (hd > SP_GEN_MAX_N && !(pv->kplan.chunk_ok && pv->vplan.chunk_ok)) {
+        delete pv;
+        set_err("cache_init: head_dim %d needs the generic kernels (max %d)", hd, SP_GEN_MAX_N);
+        return -1;
+    }
+    cc->priv = pv;
+    const size_t n_slots = (size_t)cfg->n_layers * cfg->n_heads_kv;
+    const size_t kb = n_slots * max_seq_len * cc->k_bands.total_bytes;
+    const size_t vb = n_slots * max_seq_len * cc->v_bands.total_bytes;
+    bool ok = hip_ok(hipMalloc(&cc->d_k_cache, kb), "hipMalloc K cache") &&
+              hip_ok(hipMalloc(&cc->d_v_cache, vb), "hipMalloc V cache") &&
+              hip_ok(hipMemsetAsync(cc->d_k_cache, 0, kb, (hipStream_t)stream), "memset K") &&
+              hip_ok(hipMemsetAsync(cc->d_v_cache, 0, vb, (hipStream_t)stream), "memset V");
+    if (ok && cfg->use_mobius_mask) {
+        std::vector<int> order(hd), inv(hd);
+        build_mobius_order(hd, order.data());
+        for (int i = 0; i < hd; i++) inv[order[i]] = i;
+        ok = hip_ok(hipMalloc((void **)&cc->d_mobius_order, sizeof(int) * hd), "hipMalloc order") &&
+             hip_ok(hipMalloc((void **)&cc->d_mobius_inv, sizeof(int) * hd), "hipMalloc inv") &&
+             hip_ok(hipMemcpy(cc->d_mobius_order, order.data(), sizeof(int) * hd, hipMemcpyHostToDevice), "order H2D") &&
+             hip_ok(hipMemcpy(cc->d_mobius_inv, inv.data(), sizeof(int) * hd, hipMemcpyHostToDevice), "inv H2D");
+    }
+    if (ok) {
+        pv->max_q = cfg->n_heads_kv * 8;
+        pv->ws_floats = sp_attn_workspace_floats(pv->max_q, hd, max_seq_len);
+        ok = hip_ok(hipMalloc((void **)&pv->ws, pv->ws_floats * sizeof(float)), "hipMalloc attention workspace");
+    }
+    if (ok) ok = hip_ok(hipStreamSynchronize((hipStream_t)stream), "init sync");
+    if (!ok) {
+        sp_hip_cache_free(cc);
+        return -1;
+    }
+    return 0;
+}
+
+extern "C" void sp_hip_cache_free(sp_hip_cache_t *cc) {
+    if (!cc) return;
+    if (cc->d_k_cache) (void)hipFree(cc->d_k_cache);
+    if (cc->d_v_cache) (void)hipFree(cc->d_v_cache);
+    if (cc->d_mobius_order) (void)hipFree(cc->d_mobius_order);
+    if (cc->d_mobius_inv) (void)hipFree(cc->d_mobius_inv);
+    ShipPriv *pv = (ShipPriv *)cc->priv;
+    if (pv) {
+        if (pv->ws) (void)hipFree(pv->ws);
+        delete pv;
+    }
+    memset(cc, 0, sizeof(*cc));
+}
+
+static inline bool slot_ok(const sp_hip_cache_t *cc, int layer, int head, int pos, int n) {
+    return cc && cc->priv && layer >= 0 && layer < cc->config.n_layers && head >= 0 &&
+           head < cc->config.n_heads_kv && pos >= 0 && n >= 0 && (long long)pos + n <= cc->max_seq_len;
+}
+
+static unsigned char *slot_ptr(const sp_hip_cache_t *cc, int is_v, int layer, int head, int pos) {
+    const int B = is_v ? cc->v_bands.total_bytes : cc->k_bands.total_bytes;
+    unsigned char *base = (unsigned char *)(is_v ? cc->d_v_cache : cc->d_k_cache);
+    const long long slot = (long long)layer * cc->config.n_heads_kv + head;
+    return base + (slot * cc->max_seq_len + pos) * B;
+}
+
+static int ship_write(sp_hip_cache_t *cc, int is_v, int layer, int head, int pos, int n,
+                      const void *src, int dtype) {
+    if (!slot_ok(cc, layer, head, pos, n) || !src) { set_err("write: bad slot/pos"); return -1; }
+    ShipPriv *pv = (ShipPriv *)cc->priv;
+    const SpPlan &P = is_v ? pv->vplan : pv->kplan;
+    const int *ord = is_v ? nullptr : cc->d_mobius_order;
+    return hip_ok(sp_launch_ship_encode(P, ord, src, dtype, 0, cc->config.head_dim,
+                                        slot_ptr(cc, is_v, layer, head, pos), 0, 1, n,
+                                        (hipStream_t)cc->stream), "write") ? 0 : -1;
+}
+
+static int ship_read(const sp_hip_cache_t *cc, int is_v, int layer, int head, int pos, int n,
+                     void *dst, int dtype, int max_bands) {
+    if (!slot_ok(cc, layer, head, pos, n) || !dst) { set_err("read: bad slot/pos"); return -1; }
+    ShipPriv *pv = (ShipPriv *)cc->priv;
+    SpPlan P = is_v ? pv->vplan : pv->kplan;
+    if (max_bands >= 0 && max_bands < P.n_bands) P.max_bands = max_bands;
+    const int *ord = is_v ? nullptr : cc->d_mobius_order;
+    return hip_ok(sp_launch_ship_decode(P, ord, slot_ptr(cc, is_v, layer, head, pos), 0, dst, dtype,
+                                        0, cc->config.head_dim, 1, n, (hipStream_t)cc->stream),
+                  "read") ? 0 : -1;
+}
+
+extern "C" void sp_hip_write_k(sp_hip_cache_t *cc, int l, int h, int p, const float *d) { ship_write(cc, 0, l, h, p, 1, d, SP_DT_F32); }
+extern "C" void sp_hip_write_v(sp_hip_cache_t *cc, int l, int h, int p, const float *d) { ship_write(cc, 1, l, h, p, 1, d, SP_DT_F32); }
+extern "C" void sp_hip_read_k(const sp_hip_cache_t *cc, int l, int h, int p, float *d) { ship_read(cc, 0, l, h, p, 1, d, SP_DT_F32, -1); }
+extern "C" void sp_hip_read_v(const sp_hip_cache_t *cc, int l, int h, int p, float *d) { ship_read(cc, 1, l, h, p, 1, d, SP_DT_F32, -1); }
+extern "C" void sp_hip_write_k_batch(sp_hip_cache_t *cc, int l, int h, int s, int n, const float *d) { ship_write(cc, 0, l, h, s, n, d, SP_DT_F32); }
+extern "C" void sp_hip_write_v_batch(sp_hip_cache_t *cc, int l, int h, int s, int n, const float *d) { ship_write(cc, 1, l, h, s, n, d, SP_DT_F32); }
+extern "C" void sp_hip_read_k_batch(const sp_hip_cache_t *cc, int l, int h, int s, int n, float *d) { ship_read(cc, 0, l, h, s, n, d, SP_DT_F32, -1); }
+extern "C" void sp_hip_read_v_batch(const sp_hip_cache_t *cc, int l, int h, int s, int n, float *d) { ship_read(cc, 1, l, h, s, n, d, SP_DT_F32, -1); }
+extern "C" void sp_hip_read_k_batch_partial(const sp_hip_cache_t *cc, int l, int h, int s, int n, float *d, int mb) { ship_read(cc, 0, l, h, s, n, d, SP_DT_F32, mb); }
+extern "C" void sp_hip_read_v_batch_partial(const sp_hip_cache_t *cc, int l, int h, int s, int n, float *d, int mb) { ship_read(cc, 1, l, h, s, n, d, SP_DT_F32, mb); }
+extern "C" void sp_hip_write_k_batch_f16(sp_hip_cache_t *cc, int l, int h, int s, int n, const void *d) { ship_write(cc, 0, l, h, s, n, d, SP_DT_F16); }
+extern "C" void sp_hip_write_v_batch_f16(sp_hip_cache_t *cc, int l, int h, int s, int n, const void *d) { ship_write(cc, 1, l, h, s, n, d, SP_DT_F16); }
+extern "C" void sp_hip_read_k_batch_f16(const sp_hip_cache_t *cc, int l, int h, int s, int n, void *d) { ship_read(cc, 0, l, h, s, n, d, SP_DT_F16, -1); }
+extern "C" void sp_hip_read_v_batch_f16(const sp_hip_cache_t *cc, int l, int h, int s, int n, void *d) { ship_read(cc, 1, l, h, s, n, d, SP_DT_F16, -1); }
+
+extern "C" int sp_hip_write_layer(sp_hip_cache_t *cc, int layer, int start_pos, int n_tok,
+                                  const void *d_k, const void *d_v, long long row_stride, int dtype) {
+    if (!slot_ok(cc, layer, 0, start_pos, n_tok)) { set_err("write_layer: bad layer/pos"); return -1; }
+    const int H = cc->config.n_heads_kv, hd = cc->config.head_dim;
+    if (row_stride < (long long)H * hd) { set_err("write_layer: row_stride"); return -1; }
+    ShipPriv *pv = (ShipPriv *)cc->priv;
+    hipStream_t s = (hipStream_t)cc->stream;
+    if (d_k && !hip_ok(sp_launch_ship_encode(pv->kplan, cc->d_mobius_order, d_k, dtype, hd, row_stride,
+                                             slot_ptr(cc, 0, layer, 0, start_pos),
+                                             (long long)cc->max_seq_len * cc->k_bands.total_bytes, H,
+                                             n_tok, s), "write_layer K")) return -1;
+    if (d_v && !hip_ok(sp_launch_ship_encode(pv->vplan, nullptr, d_v, dtype, hd, row_stride,
+                                             slot_ptr(cc, 1, layer, 0, start_pos),
+                                             (long long)cc->max_seq_len * cc->v_bands.total_bytes, H,
+                                             n_tok, s), "write_layer V")) return -1;
+    return 0;
+}
+
+extern "C" int sp_hip_read_layer(const sp_hip_cache_t *cc, int layer, int start_pos, int n_tok,
+                                 void *d_k, void *d_v, long long row_stride, int dtype, int max_bands) {
+    if (!slot_ok(cc, layer, 0, start_pos, n_tok)) { set_err("read_layer: bad layer/pos"); return -1; }
+    const int H = cc->config.n_heads_kv, hd = cc->config.head_dim;
+    if (row_stride < (long long)H * hd) { set_err("read_layer: row_stride"); return -1; }
+    ShipPriv *pv = (ShipPriv *)cc->priv;
+    hipStream_t s = (hipStream_t)cc->stream;
+    SpPlan kp = pv->kplan, vp = pv->vplan;
+    if (max_bands >= 0) {
+        if (max_bands < kp.n_bands) kp.max_bands = max_bands;
+        if (max_bands < vp.n_bands) vp.max_bands = max_bands;
+    }
+    if (d_k && !hip_ok(sp_launch_ship_decode(kp, cc->d_mobius_order, slot_ptr(cc, 0, layer, 0, start_pos),
+                                             (long long)cc->max_seq_len * cc->k_bands.total_bytes, d_k,
+                                             dtype, hd, row_stride, H, n_tok, s), "read_layer K")) return -1;
+    if (d_v && !hip_ok(sp_launch_ship_decode(vp, nullptr, slot_ptr(cc, 1, layer, 0, start_pos),
+                                             (long long)cc->max_seq_len * cc->v_bands.total_bytes, d_v,
+                                             dtype, hd, row_stride, H, n_tok, s), "read_layer V")) return -1;
+    return 0;
+}
+
+extern "C" int sp_hip_write_all(sp_hip_cache_t *cc, int start_pos, int n_pos, const void *d_k,
+                                const void *d_v, int dtype) {
+    if (!slot_ok(cc, 0, 0, start_pos, n_pos)) { set_err("write_all: bad pos"); return -1; }
+    const int n_slots = cc->config.n_layers * cc->config.n_heads_kv, hd = cc->config.head_dim;
+    ShipPriv *pv = (ShipPriv *)cc->priv;
+    hipStream_t s = (hipStream_t)cc->stream;
+    if (d_k && !hip_ok(sp_launch_ship_encode(pv->kplan, cc->d_mobius_order, d_k, dtype, (long long)n_pos * hd, hd,
+                                             slot_ptr(cc, 0, 0, 0, start_pos),
+                                             (long long)cc->max_seq_len * cc->k_bands.total_bytes, n_slots,
+                                             n_pos, s), "write_all K")) return -1;
+    if (d_v && !hip_ok(sp_launch_ship_encode(pv->vplan, nullptr, d_v, dtype, (long long)n_pos * hd, hd,
+                                             slot_ptr(cc, 1, 0, 0, start_pos),
+                                             (long long)cc->max_seq_len * cc->v_bands.total_bytes, n_slots,
+                                             n_pos, s), "write_all V")) return -1;
+    return 0;
+}
+
+extern "C" int sp_hip_read_all(const sp_hip_cache_t *cc, int start_pos, int n_pos, void *d_k, void *d_v,
+                               int dtype, int max_bands) {
+    if (!slot_ok(cc, 0, 0, start_pos, n_pos)) { set_err("read_all: bad pos"); return -1; }
+    const int n_slots = cc->config.n_layers * cc->config.n_heads_kv, hd = cc->config.head_dim;
+    ShipPriv *pv = (ShipPriv *)cc->priv;
+    hipStream_t s = (hipStream_t)cc->stream;
+    SpPlan kp = pv->kplan, vp = pv->vplan;
+    if (max_bands >= 0) {
+        if (max_bands < kp.n_bands) kp.max_bands = max_bands;
+        if (max_bands < vp.n_bands) vp.max_bands = max_bands;
+    }
+    if (d_k && !hip_ok(sp_launch_ship_decode(kp, cc->d_mobius_order, slot_ptr(cc, 0, 0, 0, start_pos),
+                                             (long long)cc->max_seq_len * cc->k_bands.total_bytes, d_k,
+                                             dtype, (long long)n_pos * hd, hd, n_slots, n_pos, s), "read_all K")) return -1;
+    if (d_v && !hip_ok(sp_launch_ship_decode(vp, nullptr, slot_ptr(cc, 1, 0, 0, start_pos),
+                                             (long long)cc->max_seq_len * cc->v_bands.total_bytes, d_v,
+                                             dtype, (long long)n_pos * hd, hd, n_slots, n_pos, s), "read_all V")) return -1;
+    return 0;
+}
+
+// ===========================================================================
+// fused attention
+// ===========================================================================
+extern "C" int sp_hip_attn_decode(const sp_hip_cache_t *cc, int layer, int n_kv, const float *d_q,
+                                  int n_q, float kq_scale, float *d_scores, float *d_out, void *stream) {
+    if (!cc || !cc->priv || layer < 0 || layer >= cc->config.n_layers || n_kv <= 0 ||
+        n_kv > cc->max_seq_len || !d_q || n_q <= 0) { set_err("attn: bad args"); return -1; }
+    ShipPriv *pv = (ShipPriv *)cc->priv;
+    if (n_q > pv->max_q) { set_err("attn: n_q %d > %d", n_q, pv->max_q); return -1; }
+    SpAttnArgs A;
+    const int H = cc->config.n_heads_kv;
+    A.kB = cc->k_bands.total_bytes;
+    A.vB = cc->v_bands.total_bytes;
+    A.k_head_stride = (long long)cc->max_seq_len * A.kB;
+    A.v_head_stride = (long long)cc->max_seq_len * A.vB;
+    A.kpack = slot_ptr(cc, 0, layer, 0, 0);
+    A.vpack = slot_ptr(cc, 1, layer, 0, 0);
+    A.n_kv = n_kv;
+    A.n_q = n_q;
+    A.n_kvh = H;
+    A.hd = cc->config.head_dim;
+    A.kq_scale = kq_scale;
+    A.q = d_q;
+    A.scores = d_scores;
+    A.out = d_out;
+    return hip_ok(sp_launch_attn_decode(pv->kplan, pv->vplan, cc->d_mobius_order, A, pv->ws,
+                                        pv->ws_floats, (hipStream_t)(stream ? stream : cc->stream)),
+                  "attn launch") ? 0 : -1;
+}
+
+extern "C" int sp_hip_attn_decode_all_layers(const sp_hip_cache_t *cc, int n_kv, const float *d_q, int n_q,
+                                             float kq_scale, float *d_out, void *stream) {
+    if (!cc) return -1;
+    const int hd = cc->config.head_dim;
+    for (int l = 0; l < cc->config.n_layers; l++)
+        if (sp_hip_attn_decode(cc, l, n_kv, d_q + (size_t)l * n_q * hd, n_q, kq_scale, nullptr,
+                               d_out + (size_t)l * n_q * hd, stream)) return -1;
+    return 0;
+}
+
+static std::mutex g_f16ws_mu;
+static float *g_f16ws = nullptr;
+static size_t g_f16ws_n = 0;
+
+extern "C" int sp_hip_attn_decode_f16(const void *d_k, const void *d_v, int n_heads_kv, int max_seq,
+                                      int head_dim, int layer, int n_kv, const float *d_q, int n_q,
+                                      float kq_scale, float *d_scores, float *d_out, void *stream) {
+    if (!d_k || !d_v || !d_q || n_kv <= 0 || n_kv > max_seq || layer < 0) { set_err("attn_f16: bad args"); return -1; }
+    const size_t need = sp_attn_workspace_floats(n_q, head_dim, n_kv);
+    std::lock_guard<std::mutex> lk(g_f16ws_mu);
+    if (need > g_f16ws_n) {
+        if (g_f16ws) (void)hipFree(g_f16ws);
+        g_f16ws = nullptr;
+        g_f16ws_n = 0;
+        if (!hip_ok(hipMalloc((void **)&g_f16ws, need * sizeof(float)), "attn_f16 workspace")) return -1;
+        g_f16ws_n = need;
+    }
+    const long long hs = (long long)max_seq * head_dim;
+    const unsigned short *k = (const unsigned short *)d_k + (long long)layer * n_heads_kv * hs;
+    const unsigned short *v = (const unsigned short *)d_v + (long long)layer * n_heads_kv * hs;
+    return hip_ok(sp_launch_attn_f16(k, v, hs, n_kv, n_q, n_heads_kv, head_dim, kq_scale, d_q,
+                                     d_scores, d_out, g_f16ws, g_f16ws_n, (hipStream_t)stream),
+                  "attn_f16") ? 0 : -1;
+}
+
+// ===========================================================================
+// sqfree cache
+// ===========================================================================
+struct SqPriv {
+    SpPlan kplan, vplan;   // bands over sk_k, transform over pad_dim
+};
+
+static SpSqGeo sq_geo(const sp_hip_sqfree_cache_t *cc, int is_v) {
+    SpSqGeo G;
+    G.hd = cc->config.head_dim;
+    G.pad = cc->pad_dim;
+    G.sk_k = cc->sk_k;
+    G.n_res = cc->n_res;
+    G.rbits = cc->residual_bits;
+    G.spinor = cc->use_spinor;
+    G.bytes = is_v ? cc->bytes_per_pos_v : cc->bytes_per_pos_k;
+    G.skel_idx = cc->d_skeleton_idx;
+    G.res_idx = cc->d_residual_idx;
+    G.csr_off = cc->d_csr_offsets;
+    G.csr_slot = cc->d_csr_skel_slot;
+    G.csr_mu = cc->d_csr_mu_sign;
+    return G;
+}
+
+// Knight mask: skeleton = first sk_k entries of the squarefree-first order over
+// [0, pad); residuals = the rest; CSR terms of residual c (n = c+1): proper
+// divisors d of n whose coefficient d-1 is in the skeleton with mu(n/d) != 0,
+// sign mu(n/d). The reference builder (sp_knight_mask_init, called at
+// shannon_prime_sqfree.cu:606) is absent; this is the build's documented rule.
+static void build_knight(int pad, int sk_k, std::vector<int> &skel, std::vector<int> &res,
+                         std::vector<int> &off, std::vector<int> &slot, std::vector<int> &mu) {
+    std::vector<int> order(pad), slot_of(pad, -1);
+    build_mobius_order(pad, order.data());
+    skel.assign(order.begin(), order.begin() + sk_k);
+    res.assign(order.begin() + sk_k, order.end());
+    for (int s = 0; s < sk_k; s++) slot_of[skel[s]] = s;
+    off.assign(1, 0);
+    slot.clear();
+    mu.clear();
+    for (size_t r = 0; r < res.size(); r++) {
+        const int n = res[r] + 1;
+        for (int d = 1; d < n; d++) {
+            if (n % d) continue;
+            const int m = mobius_mu(n / d);
+            if (m == 0 || slot_of[d - 1] < 0) continue;
+            slot.push_back(slot_of[d - 1]);
+            mu.push_back(m);
+        }
+        off.push_back((int)slot.size());
+    }
+}
+
+template <typename T>
+static bool upload(T **dptr, const std::vector<T> &h) {
+    const size_t n = h.empty() ? 1 : h.size();
+    if (!hip_ok(hipMalloc((void **)dptr, n * sizeof(T)), "hipMalloc table")) return false;
+    if (h.empty()) return true;
+    return hip_ok(hipMemcpy(*dptr, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice), "table H2D");
+}
+
+extern "C" int sp_hip_sqfree_cache_init_ex(sp_hip_sqfree_cache_t *cc, const sp_config_t *cfg, int max_seq_len,
+                                           int residual_bits, int use_spinor, int sk_k, void *stream) {
+    if (!cc) return -1;
+    memset(cc, 0, sizeof(*cc));
+    if (!cfg || cfg->head_dim <= 0 || cfg->n_layers <= 0 || cfg->n_heads_kv <= 0 || max_seq_len <= 0 ||
+        residual_bits < 1 || residual_bits > 8) { set_err("sqfree_init: bad config"); return -1; }
+    if (!sp_hip_available()) { set_err("sqfree_init: no gfx950 device"); return -1; }
+    const int pad = sp_sqfree_pad_dim(cfg->head_dim);
+    if (pad <= 0 || pad > SP_GEN_MAX_N) { set_err("sqfree_init: pad %d unsupported", pad); return -1; }
+    if (sk_k <= 0) sk_k = pad / 2;
+    if (sk_k > pad) sk_k = pad;
+    cc->config = *cfg;
+    cc->pad_dim = pad;
+    cc->sk_k = sk_k;
+    cc->n_res = pad - sk_k;
+    cc->residual_bits = residual_bits;
+    cc->use_spinor = use_spinor ? 1 : 0;
+    cc->max_seq_len = max_seq_len;
+    cc->n_slots = cfg->n_layers * cfg->n_heads_kv;
+    cc->stream = stream;
+    // bands over the skeleton; reference defaults 5/4/4/4/5 (shannon_prime_sqfree.cu:615-624)
+    static const int defb[5] = {5, 4, 4, 4, 5};
+    int kb[SP_MAX_BANDS], vb[SP_MAX_BANDS];
+    const int knb = (cfg->k_n_bands > 0 && cfg->k_n_bands <= SP_MAX_BANDS) ? cfg->k_n_bands : 5;
+    const int vnb = (cfg->v_n_bands > 0 && cfg->v_n_bands <= SP_MAX_BANDS) ? cfg->v_n_bands : 5;
+    for (int i = 0; i < knb; i++) kb[i] = cfg->k_band_bits[i] > 0 ? cfg->k_band_bits[i] : defb[i % 5];
+    for (int i = 0; i < vnb; i++) vb[i] = cfg->v_band_bits[i] > 0 ? cfg->v_band_bits[i] : defb[i % 5];
+    if (!valid_bits(kb, knb) || !valid_bits(vb, vnb)) { set_err("sqfree_init: band bits"); return -1; }
+    sp_band_config_init(&cc->k_bands, sk_k, knb, kb);
+    sp_band_config_init(&cc->v_bands, sk_k, vnb, vb);
+    SqPriv *pv = new SqPriv();
+    cc->priv = pv;
+    if (sp_build_plan(&cc->k_bands, pad, 0, -1, &pv->kplan) || sp_build_plan(&cc->v_bands, pad, 0, -1, &pv->vplan)) {
+        set_err("sqfree_init: plan");
+        sp_hip_sqfree_cache_free(cc);
+        return -1;
+    }
+    std::vector<int> skel, res, off, slot, mu;
+    build_knight(pad, sk_k, skel, res, off, slot, mu);
+    cc->n_terms = (int)slot.size();
+    const int res_bytes = (cc->n_res * residual_bits + 7) / 8;
+    const int sheet = cc->use_spinor ? (cc->n_res + 7) / 8 : 0;
+    cc->bytes_per_pos_k = cc->k_bands.total_bytes + 4 + res_bytes + sheet;
+    cc->bytes_per_pos_v = cc->v_bands.total_bytes + 4 + res_bytes + sheet;
+    if (cc->bytes_per_pos_k + 8 > SP_GEN_MAX_REC || cc->bytes_per_pos_v + 8 > SP_GEN_MAX_REC) {
+        set_err("sqfree_init: record too large");
+        sp_hip_sqfree_cache_free(cc);
+        return -1;
+    }
+    const size_t kbytes = (size_t)cc->n_slots * max_seq_len * cc->bytes_per_pos_k;
+    const size_t vbytes = (size_t)cc->n_slots * max_seq_len * cc->bytes_per_pos_v;
+    bool ok = upload(&cc->d_skeleton_idx, skel) && upload(&cc->d_residual_idx, res) &&
+              upload(&cc->d_csr_offsets, off) && upload(&cc->d_csr_skel_slot, slot) &&
+              upload(&cc->d_csr_mu_sign, mu) &&
+              hip_ok(hipMalloc((void **)&cc->d_k_cache, kbytes), "hipMalloc sqfree K") &&
+              hip_ok(hipMalloc((void **)&cc->d_v_cache, vbytes), "hipMalloc sqfree V") &&
+              hip_ok(hipMemsetAsync(cc->d_k_cache, 0, kbytes, (hipStream_t)stream), "memset") &&
+              hip_ok(hipMemsetAsync(cc->d_v_cache, 0, vbytes, (hipStream_t)stream), "memset") &&
+              hip_ok(hipStreamSynchronize((hipStream_t)stream), "sync");
+    if (!ok) {
+        sp_hip_sqfree_cache_free(cc);
+        return -1;
+    }
+    return 0;
+}
+
+extern "C" int sp_hip_sqfree_cache_init(sp_hip_sqfree_cache_t *cc, const sp_config_t *cfg, int max_seq_len,
+                                        int residual_bits, int use_spinor, void *stream) {
+    return sp_hip_sqfree_cache_init_ex(cc, cfg, max_seq_len, residual_bits, use_spinor, 0, stream);
+}
+
+extern "C" void sp_hip_sqfree_cache_free(sp_hip_sqfree_cache_t *cc) {
+    if (!cc) return;
+    void *ptrs[] = {cc->d_skeleton_idx, cc->d_residual_idx, cc->d_csr_offsets, cc->d_csr_skel_slot,
+                    cc->d_csr_mu_sign, cc->d_k_cache, cc->d_v_cache};
+    for (void *p : ptrs)
+        if (p) (void)hipFree(p);
+    delete (SqPriv *)cc->priv;
+    memset(cc, 0, sizeof(*cc));
+}
+
+static bool sq_slot_ok(const sp_hip_sqfree_cache_t *cc, int layer, int head, int pos, int n) {
+    return cc && cc->priv && layer >= 0 && layer < cc->config.n_layers && head >= 0 &&
+           head < cc->config.n_heads_kv && pos >= 0 && n >= 0 && (long long)pos + n <= cc->max_seq_len;
+}
+
+extern "C" int sp_hip_sqfree_write_batch(sp_hip_sqfree_cache_t *cc, int is_v, int layer, int head,
+                                         int start_pos, int n_pos, const void *d_src, int dtype) {
+    if (!sq_slot_ok(cc, layer, head, start_pos, n_pos) || !d_src) { set_err("sqfree write: bad args"); return -1; }
+    SqPriv *pv = (SqPriv *)cc->priv;
+    const SpSqGeo G = sq_geo(cc, is_v);
+    unsigned char *base = is_v ? cc->d_v_cache : cc->d_k_cache;
+    const long long slot = (long long)layer * cc->config.n_heads_kv + head;
+    unsigned char *dst = base + (slot * cc->max_seq_len + start_pos) * G.bytes;
+    return hip_ok(sp_launch_sqfree_encode(is_v ? pv->vplan : pv->kplan, G, d_src, dtype, 0,
+                                          cc->config.head_dim, dst, 0, 1, n_pos, (hipStream_t)cc->stream),
+                  "sqfree encode") ? 0 : -1;
+}
+
+extern "C" int sp_hip_sqfree_read_batch(const sp_hip_sqfree_cache_t *cc, int is_v, int layer, int head,
+                                        int start_pos, int n_pos, void *d_dst, int dtype) {
+    if (!sq_slot_ok(cc, layer, head, start_pos, n_pos) || !d_dst) { set_err("sqfree read: bad args"); return -1; }
+    SqPriv *pv = (SqPriv *)cc->priv;
+    const SpSqGeo G = sq_geo(cc, is_v);
+    const unsigned char *base = is_v ? cc->d_v_cache : cc->d_k_cache;
+    const long long slot = (long long)layer * cc->config.n_heads_kv + head;
+    const unsigned char *src = base + (slot * cc->max_seq_len + start_pos) * G.bytes;
+    return hip_ok(sp_launch_sqfree_decode(is_v ? pv->vplan : pv->kplan, G, src, 0, d_dst, dtype, 0,
+                                          cc->config.head_dim, 1, n_pos, (hipStream_t)cc->stream),
+                  "sqfree decode") ? 0 : -1;
+}
+
+extern "C" void sp_hip_sqfree_write_k(sp_hip_sqfree_cache_t *cc, int l, int h, int p, const float *d) { sp_hip_sqfree_write_batch(cc, 0, l, h, p, 1, d, SP_DT_F32); }
+extern "C" void sp_hip_sqfree_write_v(sp_hip_sqfree_cache_t *cc, int l, int h, int p, const float *d) { sp_hip_sqfree_write_batch(cc, 1, l, h, p, 1, d, SP_DT_F32); }
+extern "C" void sp_hip_sqfree_read_k(const sp_hip_sqfree_cache_t *cc, int l, int h, int p, float *d) { sp_hip_sqfree_read_batch(cc, 0, l, h, p, 1, d, SP_DT_F32); }
+extern "C" void sp_hip_sqfree_read_v(const sp_hip_sqfree_cache_t *cc, int l, int h, int p, float *d) { sp_hip_sqfree_read_batch(cc, 1, l, h, p, 1, d, SP_DT_F32); }
+extern "C" void sp_hip_sqfree_read_k_batch(const sp_hip_sqfree_cache_t *cc, int l, int h, int s, int n, float *d) { sp_hip_sqfree_read_batch(cc, 0, l, h, s, n, d, SP_DT_F32); }
+extern "C" void sp_hip_sqfree_read_v_batch(const sp_hip_sqfree_cache_t *cc, int l, int h, int s, int n, float *d) { sp_hip_sqfree_read_batch(cc, 1, l, h, s, n, d, SP_DT_F32); }
+
+extern "C" int sp_hip_sqfree_get_tables(const sp_hip_sqfree_cache_t *cc, int *skeleton_idx, int *residual_idx,
+                                        int *csr_offsets, int *csr_skel_slot, int *csr_mu_sign) {
+    if (!cc || !cc->priv) return -1;
+    bool ok = true;
+    if (skeleton_idx) ok &= hip_ok(hipMemcpy(skeleton_idx, cc->d_skeleton_idx, sizeof(int) * cc->sk_k, hipMemcpyDeviceToHost), "D2H");
+    if (residual_idx && cc->n_res) ok &= hip_ok(hipMemcpy(residual_idx, cc->d_residual_idx, sizeof(int) * cc->n_res, hipMemcpyDeviceToHost), "D2H");
+    if (csr_offsets) ok &= hip_ok(hipMemcpy(csr_offsets, cc->d_csr_offsets, sizeof(int) * (cc->n_res + 1), hipMemcpyDeviceToHost), "D2H");
+    if (csr_skel_slot && cc->n_terms) ok &= hip_ok(hipMemcpy(csr_skel_slot, cc->d_csr_skel_slot, sizeof(int) * cc->n_terms, hipMemcpyDeviceToHost), "D2H");
+    if (csr_mu_sign && cc->n_terms) ok &= hip_ok(hipMemcpy(csr_mu_sign, cc->d_csr_mu_sign, sizeof(int) * cc->n_terms, hipMemcpyDeviceToHost), "D2H");
+    return ok ? 0 : -1;
+}
+
+// ===========================================================================
+// hierarchical cache
+// ===========================================================================
+struct HierPriv {
+    SpPlan plan;
+};
+
+extern "C" int sp_hip_hier_cache_init(sp_hip_hier_cache_t *hc, const sp_config_t *cfg, int pad_dim,
+                                      int n_skeleton, int n_target, int target_res_bits,
+                                      const int *skeleton_idx, const int *target_idx,
+                                      const sp_band_config_t *skel_bands, int max_seq_len, int n_slots,
+                                      void *stream) {
+    if (!hc) return -1;
+    memset(hc, 0, sizeof(*hc));
+    if (!cfg || !skeleton_idx || !target_idx || !skel_bands || pad_dim <= 0 || pad_dim > SP_GEN_MAX_N ||
+        n_skeleton <= 0 || n_target <= 0 || n_skeleton + n_target > pad_dim || target_res_bits < 1 ||
+        target_res_bits > 8 || max_seq_len <= 0 || n_slots <= 0 || cfg->head_dim > pad_dim ||
+        skel_bands->head_dim != n_skeleton) { set_err("hier_init: bad args"); return -1; }
+    for (int i = 0; i < n_skeleton; i++) if (skeleton_idx[i] < 0 || skeleton_idx[i] >= pad_dim) { set_err("hier_init: skeleton idx"); return -1; }
+    for (int i = 0; i < n_target; i++) if (target_idx[i] < 0 || target_idx[i] >= pad_dim) { set_err("hier_init: target idx"); return -1; }
+    if (!sp_hip_available()) { set_err("hier_init: no gfx950 device"); return -1; }
+    hc->config = *cfg;
+    hc->pad_dim = pad_dim;
+    hc->n_skeleton = n_skeleton;
+    hc->n_target = n_target;
+    hc->target_res_bits = target_res_bits;
+    hc->n_slots = n_slots;
+    hc->max_seq_len = max_seq_len;
+    hc->skel_bands = *skel_bands;
+    hc->stream = stream;
+    HierPriv *pv = new HierPriv();
+    hc->priv = pv;
+    if (sp_build_plan(skel_bands, pad_dim, 0, -1, &pv->plan)) { set_err("hier_init: plan"); sp_hip_hier_cache_free(hc); return -1; }
+    const int res_bytes = (n_target * target_res_bits + 7) / 8;
+    hc->bytes_per_pos_k = hc->bytes_per_pos_v = skel_bands->total_bytes + 4 + res_bytes;
+    if (hc->bytes_per_pos_k + 8 > SP_GEN_MAX_REC) { set_err("hier_init: record too large"); sp_hip_hier_cache_free(hc); return -1; }
+    const size_t cb = (size_t)n_slots * max_seq_len * hc->bytes_per_pos_k;
+    const size_t wb = (size_t)n_slots * n_target * n_skeleton * sizeof(uint16_t);
+    std::vector<int> sk(skeleton_idx, skeleton_idx + n_skeleton), tg(target_idx, target_idx + n_target);
+    bool ok = upload(&hc->d_skeleton_idx, sk) && upload(&hc->d_target_idx, tg) &&
+              hip_ok(hipMalloc((void **)&hc->d_k_cache, cb), "hipMalloc hier K") &&
+              hip_ok(hipMalloc((void **)&hc->d_v_cache, cb), "hipMalloc hier V") &&
+              hip_ok(hipMalloc((void **)&hc->d_W, wb), "hipMalloc W") &&
+              hip_ok(hipMemsetAsync(hc->d_k_cache, 0, cb, (hipStream_t)stream), "memset") &&
+              hip_ok(hipMemsetAsync(hc->d_v_cache, 0, cb, (hipStream_t)stream), "memset") &&
+              hip_ok(hipMemsetAsync(hc->d_W, 0, wb, (hipStream_t)stream), "memset") &&
+              hip_ok(hipStreamSynchronize((hipStream_t)stream), "sync");
+    if (!ok) {
+        sp_hip_hier_cache_free(hc);
+        return -1;
+    }
+    return 0;
+}
+
+extern "C" void sp_hip_hier_cache_free(sp_hip_hier_cache_t *hc) {
+    if (!hc) return;
+    void *ptrs[] = {hc->d_W, hc->d_skeleton_idx, hc->d_target_idx, hc->d_k_cache, hc->d_v_cache};
+    for (void *p : ptrs)
+        if (p) (void)hipFree(p);
+    delete (HierPriv *)hc->priv;
+    memset(hc, 0, sizeof(*hc));
+}
+
+extern "C" int sp_hip_hier_cache_upload_W(sp_hip_hier_cache_t *hc, const uint16_t *W_all) {
+    if (!hc || !hc->priv || !W_all) return -1;
+    const size_t wb = (size_t)hc->n_slots * hc->n_target * hc->n_skeleton * sizeof(uint16_t);
+    return hip_ok(hipMemcpy(hc->d_W, W_all, wb, hipMemcpyHostToDevice), "upload_W") ? 0 : -1;
+}
+
+static SpHierGeo hier_geo(const sp_hip_hier_cache_t *hc, int slot) {
+    SpHierGeo G;
+    G.hd = hc->config.head_dim;
+    G.pad = hc->pad_dim;
+    G.n_skel = hc->n_skeleton;
+    G.n_target = hc->n_target;
+    G.rbits = hc->target_res_bits;
+    G.bytes = hc->bytes_per_pos_k;
+    G.skel_idx = hc->d_skeleton_idx;
+    G.target_idx = hc->d_target_idx;
+    G.W = hc->d_W + (size_t)slot * hc->n_target * hc->n_skeleton;
+    G.w_outer = (long long)hc->n_target * hc->n_skeleton;
+    return G;
+}
+
+static bool hier_slot_ok(const sp_hip_hier_cache_t *hc, int layer, int head, int pos, int n) {
+    if (!hc || !hc->priv || layer < 0 || head < 0 || head >= hc->config.n_heads_kv || pos < 0 || n < 0 ||
+        (long long)pos + n > hc->max_seq_len) return false;
+    const long long slot = (long long)layer * hc->config.n_heads_kv + head;
+    return slot < hc->n_slots;
+}
+
+extern "C" int sp_hip_hier_write_batch(sp_hip_hier_cache_t *hc, int is_v, int layer, int head, int start_pos,
+                                       int n_pos, const void *d_src, int dtype) {
+    if (!hier_slot_ok(hc, layer, head, start_pos, n_pos) || !d_src) { set_err("hier write: bad args"); return -1; }
+    const int slot = layer * hc->config.n_heads_kv + head;
+    const SpHierGeo G = hier_geo(hc, slot);
+    unsigned char *base = is_v ? hc->d_v_cache : hc->d_k_cache;
+    unsigned char *dst = base + ((long long)slot * hc->max_seq_len + start_pos) * G.bytes;
+    return hip_ok(sp_launch_hier_encode(((HierPriv *)hc->priv)->plan, G, d_src, dtype, 0, hc->config.head_dim,
+                                        dst, 0, 1, n_pos, (hipStream_t)hc->stream), "hier encode") ? 0 : -1;
+}
+
+extern "C" int sp_hip_hier_read_batch(const sp_hip_hier_cache_t *hc, int is_v, int layer, int head, int start_pos,
+                                      int n_pos, void *d_dst, int dtype) {
+    if (!hier_slot_ok(hc, layer, head, start_pos, n_pos) || !d_dst) { set_err("hier read: bad args"); return -1; }
+    const int slot = layer * hc->config.n_heads_kv + head;
+    const SpHierGeo G = hier_geo(hc, slot);
+    const unsigned char *base = is_v ? hc->d_v_cache : hc->d_k_cache;
+    const unsigned char *src = base + ((long long)slot * hc->max_seq_len + start_pos) * G.bytes;
+    return hip_ok(sp_launch_hier_decode(((HierPriv *)hc->priv)->plan, G, src, 0, d_dst, dtype, 0,
+                                        hc->config.head_dim, 1, n_pos, (hipStream_t)hc->stream),
+                  "hier decode") ? 0 : -1;
+}
+
+extern "C" void sp_hip_hier_write_k(sp_hip_hier_cache_t *hc, int l, int h, int p, const float *d) { sp_hip_hier_write_batch(hc, 0, l, h, p, 1, d, SP_DT_F32); }
+extern "C" void sp_hip_hier_write_v(sp_hip_hier_cache_t *hc, int l, int h, int p, const float *d) { sp_hip_hier_write_batch(hc, 1, l, h, p, 1, d, SP_DT_F32); }
+extern "C" void sp_hip_hier_read_k(const sp_hip_hier_cache_t *hc, int l, int h, int p, float *d) { sp_hip_hier_read_batch(hc, 0, l, h, p, 1, d, SP_DT_F32); }
+extern "C" void sp_hip_hier_read_v(const sp_hip_hier_cache_t *hc, int l, int h, int p, float *d) { sp_hip_hier_read_batch(hc, 1, l, h, p, 1, d, SP_DT_F32); }
+
+// ===========================================================================
+// events / streams
+// ===========================================================================
+extern "C" void *sp_hip_event_create(void) {
+    hipEvent_t e = nullptr;
+    if (!hip_ok(hipEventCreate(&e), "event create")) return nullptr;
+    return (void *)e;
+}
+extern "C" void sp_hip_event_destroy(void *ev) {
+    if (ev) (void)hipEventDestroy((hipEvent_t)ev);
+}
+extern "C" int sp_hip_event_record(void *ev, void *stream) {
+    return hip_ok(hipEventRecord((hipEvent_t)ev, (hipStream_t)stream), "event record") ? 0 : -1;
+}
+extern "C" float sp_hip_event_elapsed_ms(void *a, void *b) {
+    float ms = -1.0f;
+    if (!hip_ok(hipEventSynchronize((hipEvent_t)b), "event sync")) return -1.0f;
+    if (!hip_ok(hipEventElapsedTime(&ms, (hipEvent_t)a, (hipEvent_t)b), "elapsed")) return -1.0f;
+    return ms;
+}
+extern "C" int sp_hip_memset(void *d_ptr, int value, size_t bytes, void *stream) {
+    if (!d_ptr) return -1;
+    return hip_ok(hipMemsetAsync(d_ptr, value, bytes, (hipStream_t)stream), "memset") ? 0 : -1;
+}
+extern "C" int sp_hip_stream_sync(void *stream) {
+    return hip_ok(hipStreamSynchronize((hipStream_t)stream), "stream sync") ? 0 : -1;
+}
+
+// ===========================================================================
+// host-buffer staging over a device cache
+// ===========================================================================
+// Host API calls stage through one device buffer per cache (not reentrant per
+// cache, like the reference's per-context scratch) and return after the copy
+// back completes.
+struct HostStage {
+    float *d_vec = nullptr;          // [cap][hd] fp32
+    unsigned char *d_rec = nullptr;  // [cap][max(kB, vB)]
+    int cap = 0, hd = 0, rec = 0;
+    hipStream_t stream = nullptr;
+    int order_n = 0;
+    int *d_order = nullptr;
+};
+
+static HostStage *stage_create(int hd, int rec_bytes, int cap, const int *h_order) {
+    HostStage *st = new HostStage();
+    st->cap = cap;
+    st->hd = hd;
+    st->rec = rec_bytes;
+    bool ok = hip_ok(hipStreamCreate(&st->stream), "stream create") &&
+              hip_ok(hipMalloc((void **)&st->d_vec, sizeof(float) * (size_t)cap * hd), "stage vec") &&
+              hip_ok(hipMalloc((void **)&st->d_rec, (size_t)cap * rec_bytes), "stage rec");
+    if (ok && h_order) {
+        st->order_n = hd;
+        ok = hip_ok(hipMalloc((void **)&st->d_order, sizeof(int) * hd), "stage order") &&
+             hip_ok(hipMemcpy(st->d_order, h_order, sizeof(int) * hd, hipMemcpyHostToDevice), "order H2D");
+    }
+    if (!ok) {
+        if (st->d_vec) (void)hipFree(st->d_vec);
+        if (st->d_rec) (void)hipFree(st->d_rec);
+        if (st->d_order) (void)hipFree(st->d_order);
+        if (st->stream) (void)hipStreamDestroy(st->stream);
+        delete st;
+        return nullptr;
+    }
+    return st;
+}
+
+static void stage_destroy(HostStage *st) {
+    if (!st) return;
+    (void)hipStreamSynchronize(st->stream);
+    (void)hipFree(st->d_vec);
+    (void)hipFree(st->d_rec);
+    if (st->d_order) (void)hipFree(st->d_order);
+    (void)hipStreamDestroy(st->stream);
+    delete st;
+}
+
+// ===========================================================================
+// sp_shadow_cache_t over the GPU
+// ===========================================================================
+struct ShadowDev {
+    HostStage *st;
+    SpPlan kplan, vplan;
+};
+
+extern "C" int sp_shadow_cache_init(sp_shadow_cache_t *sc, const sp_config_t *cfg) {
+    if (!sc) return -1;
+    memset(sc, 0, sizeof(*sc));
+    if (!check_cfg(cfg)) { set_err("shadow_init: bad config"); return -1; }
+    if (!sp_hip_available()) { set_err("shadow_init: no gfx950 device"); return -1; }
+    sc->config = *cfg;
+    const int hd = cfg->head_dim;
+    sp_band_config_init_ext(&sc->k_bands, hd, cfg->k_n_bands, cfg->k_band_bits, cfg->k_ternary_mask);
+    sp_band_config_init_ext(&sc->v_bands, hd, cfg->v_n_bands, cfg->v_band_bits, cfg->v_ternary_mask);
+    if (cfg->use_mobius_mask && sp_mobius_mask_init(&sc->mobius_mask, hd)) return -1;
+    ShadowDev *dv = new ShadowDev();
+    if (sp_build_plan(&sc->k_bands, hd, cfg->vht2_norm, -1, &dv->kplan) ||
+        sp_build_plan(&sc->v_bands, hd, cfg->vht2_norm, -1, &dv->vplan)) {
+        delete dv;
+        sp_mobius_mask_free(&sc->mobius_mask);
+        set_err("shadow_init: head_dim %d unsupported", hd);
+        return -1;
+    }
+    const int rec = sc->k_bands.total_bytes > sc->v_bands.total_bytes ? sc->k_bands.total_bytes : sc->v_bands.total_bytes;
+    dv->st = stage_create(hd, rec, 4096, cfg->use_mobius_mask ? sc->mobius_mask.order : nullptr);
+    if (!dv->st) {
+        delete dv;
+        sp_mobius_mask_free(&sc->mobius_mask);
+        return -1;
+    }
+    sc->dev = dv;
+    return 0;
+}
+
+extern "C" void sp_shadow_cache_free(sp_shadow_cache_t *sc) {
+    if (!sc) return;
+    ShadowDev *dv = (ShadowDev *)sc->dev;
+    if (dv) {
+        stage_destroy(dv->st);
+        delete dv;
+    }
+    sp_mobius_mask_free(&sc->mobius_mask);
+    sc->dev = nullptr;
+}
+
+static uint8_t *shadow_rec(const sp_shadow_cache_t *sc, int is_v, int layer, int head, int pos) {
+    if (!sc || !sc->dev || layer < 0 || layer >= sc->config.n_layers || head < 0 ||
+        head >= sc->config.n_heads_kv || pos < 0) return nullptr;
+    uint8_t **slots = is_v ? sc->v_cache : sc->k_cache;
+    if (!slots) return nullptr;
+    uint8_t *s = slots[layer * sc->config.n_heads_kv + head];
+    if (!s) return nullptr;
+    return s + (size_t)pos * (is_v ? sc->v_bands.total_bytes : sc->k_bands.total_bytes);
+}
+
+static void shadow_write(sp_shadow_cache_t *sc, int is_v, int layer, int head, int start, int n,
+                         const float *vecs) {
+    uint8_t *dst = shadow_rec(sc, is_v, layer, head, start);
+    if (!dst || !vecs || n <= 0) return;
+    ShadowDev *dv = (ShadowDev *)sc->dev;
+    HostStage *st = dv->st;
+    const int hd = sc->config.head_dim, B = is_v ? sc->v_bands.total_bytes : sc->k_bands.total_bytes;
+    const int *ord = is_v ? nullptr : st->d_order;
+    for (int done = 0; done < n; done += st->cap) {
+        const int m = (n - done) < st->cap ? (n - done) : st->cap;
+        if (!hip_ok(hipMemcpyAsync(st->d_vec, vecs + (size_t)done * hd, sizeof(float) * (size_t)m * hd,
+                                   hipMemcpyHostToDevice, st->stream), "shadow H2D") ||
+            !hip_ok(sp_launch_ship_encode(is_v ? dv->vplan : dv->kplan, ord, st->d_vec, SP_DT_F32, 0, hd,
+                                          st->d_rec, 0, 1, m, st->stream), "shadow encode") ||
+            !hip_ok(hipMemcpyAsync(dst + (size_t)done * B, st->d_rec, (size_t)m * B, hipMemcpyDeviceToHost,
+                                   st->stream), "shadow D2H") ||
+            !hip_ok(hipStreamSynchronize(st->stream), "shadow sync"))
+            return;
+    }
+}
+
+static void shadow_read(const sp_shadow_cache_t *sc, int is_v, int layer, int head, int start, int n,
+                        float *out, int max_bands) {
+    const uint8_t *src = shadow_rec(sc, is_v, layer, head, start);
+    if (!src || !out || n <= 0) return;
+    ShadowDev *dv = (ShadowDev *)sc->dev;
+    HostStage *st = dv->st;
+    const int hd = sc->config.head_dim, B = is_v ? sc->v_bands.total_bytes : sc->k_bands.total_bytes;
+    SpPlan P = is_v ? dv->vplan : dv->kplan;
+    if (max_bands >= 0 && max_bands < P.n_bands) P.max_bands = max_bands;
+    const int *ord = is_v ? nullptr : st->d_order;
+    for (int done = 0; done < n; done += st->cap) {
+        const int m = (n - done) < st->cap ? (n - done) : st->cap;
+        if (!hip_ok(hipMemcpyAsync(st->d_rec, src + (size_t)done * B, (size_t)m * B, hipMemcpyHostToDevice,
+                                   st->stream), "shadow H2D") ||
+            !hip_ok(sp_launch_ship_decode(P, ord, st->d_rec, 0, st->d_vec, SP_DT_F32, 0, hd, 1, m, st->stream),
+                    "shadow decode") ||
+            !hip_ok(hipMemcpyAsync(out + (size_t)done * hd, st->d_vec, sizeof(float) * (size_t)m * hd,
+                                   hipMemcpyDeviceToHost, st->stream), "shadow D2H") ||
+            !hip_ok(hipStreamSynchronize(st->stream), "shadow sync"))
+            return;
+    }
+}
+
+extern "C" void sp_shadow_write_k(sp_shadow_cache_t *sc, int l, int h, int p, const float *v) { shadow_write(sc, 0, l, h, p, 1, v); }
+extern "C" void sp_shadow_write_v(sp_shadow_cache_t *sc, int l, int h, int p, const float *v) { shadow_write(sc, 1, l, h, p, 1, v); }
+extern "C" void sp_shadow_write_k_batch(sp_shadow_cache_t *sc, int l, int h, int s, int n, const float *v) { shadow_write(sc, 0, l, h, s, n, v); }
+extern "C" void sp_shadow_write_v_batch(sp_shadow_cache_t *sc, int l, int h, int s, int n, const float *v) { shadow_write(sc, 1, l, h, s, n, v); }
+extern "C" void sp_shadow_read_k(const sp_shadow_cache_t *sc, int l, int h, int p, float *o) { shadow_read(sc, 0, l, h, p, 1, o, -1); }
+extern "C" void sp_shadow_read_v(const sp_shadow_cache_t *sc, int l, int h, int p, float *o) { shadow_read(sc, 1, l, h, p, 1, o, -1); }
+extern "C" void sp_shadow_read_k_partial(const sp_shadow_cache_t *sc, int l, int h, int p, float *o, int mb) { shadow_read(sc, 0, l, h, p, 1, o, mb); }
+extern "C" void sp_shadow_read_v_partial(const sp_shadow_cache_t *sc, int l, int h, int p, float *o, int mb) { shadow_read(sc, 1, l, h, p, 1, o, mb); }
+extern "C" void sp_shadow_read_k_batch(const sp_shadow_cache_t *sc, int l, int h, int s, int n, float *o) { shadow_read(sc, 0, l, h, s, n, o, -1); }
+extern "C" void sp_shadow_read_v_batch(const sp_shadow_cache_t *sc, int l, int h, int s, int n, float *o) { shadow_read(sc, 1, l, h, s, n, o, -1); }
+
+// ===========================================================================
+// host-buffer I/O on a device cache (bridge HIP backend)
+// ===========================================================================
+extern "C" int sp_hip_write_host(sp_hip_cache_t *cc, int is_v, int layer, int head, int start_pos,
+                                 int n_pos, const float *h_vecs) {
+    if (!slot_ok(cc, layer, head, start_pos, n_pos) || !h_vecs) { set_err("write_host: bad args"); return -1; }
+    const int hd = cc->config.head_dim;
+    const size_t bytes = sizeof(float) * (size_t)n_pos * hd;
+    float *d = nullptr;
+    if (!hip_ok(hipMalloc((void **)&d, bytes), "write_host staging")) return -1;
+    bool ok = hip_ok(hipMemcpyAsync(d, h_vecs, bytes, hipMemcpyHostToDevice, (hipStream_t)cc->stream), "H2D") &&
+              ship_write(cc, is_v, layer, head, start_pos, n_pos, d, SP_DT_F32) == 0 &&
+              hip_ok(hipStreamSynchronize((hipStream_t)cc->stream), "sync");
+    (void)hipFree(d);
+    return ok ? 0 : -1;
+}
+
+extern "C" int sp_hip_read_host(const sp_hip_cache_t *cc, int is_v, int layer, int head, int start_pos,
+                                int n_pos, float *h_out, int max_bands) {
+    if (!slot_ok(cc, layer, head, start_pos, n_pos) || !h_out) { set_err("read_host: bad args"); return -1; }
+    const int hd = cc->config.head_dim;
+    const size_t bytes = sizeof(float) * (size_t)n_pos * hd;
+    float *d = nullptr;
+    if (!hip_ok(hipMalloc((void **)&d, bytes), "read_host staging")) return -1;
+    bool ok = ship_read(cc, is_v, layer, head, start_pos, n_pos, d, SP_DT_F32, max_bands) == 0 &&
+              hip_ok(hipMemcpyAsync(h_out, d, bytes, hipMemcpyDeviceToHost, (hipStream_t)cc->stream), "D2H") &&
+              hip_ok(hipStreamSynchronize((hipStream_t)cc->stream), "sync");
+    (void)hipFree(d);
+    return ok ? 0 : -1;
+}

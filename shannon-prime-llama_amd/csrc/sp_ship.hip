@@ -1,0 +1,574 @@
+// sp_ship.hip -- gfx950 kernels of the ship codec (write path and read path).
+//
+// Write path per vector: fp16/fp32 load -> VHT2 (p=2 butterfly or staged
+// Vilenkin) -> Mobius reorder (K) -> per-band absmax -> fp16 scale -> rint
+// quantize -> LSB-first bit-pack, as one kernel. Read path: unpack ->
+// dequantize (partial bands) -> unreorder -> VHT2 (self-inverse) -> store.
+// Semantics follow the reference CUDA kernels shannon_prime_cuda.cu:37-270
+// (transform, gather/scatter, band quantize/dequantize) with the CPU core's
+// final-normalisation op order (shannon_prime_adreno.c:276-309) by default.
+//
+// Two kernel families:
+//  * fast: power-of-2 head_dim with band boundaries on multiples of 8. Each lane
+//    owns 8 consecutive coefficients (one 16-byte fp16 load); head_dim/8 lanes
+//    hold a vector, so butterfly stages len=1,2,4 run in registers and the
+//    longer strides run as lane-xor exchanges. After the Mobius permute through
+//    LDS a lane's 8 coefficients lie inside one band, its codes occupy exactly
+//    `bits` whole bytes of the record, and band maxima are segmented scans
+//    over the band's lanes. Records of a 64-vector tile are assembled in LDS
+//    and written (or read) as coalesced dwords.
+//  * generic: any factorisable length and band geometry; one vector per wave,
+//    transform stages and packing staged through LDS.
+#include "sp_device.h"
+#include "sp_internal.h"
+
+#define SP_TILE 64
+
+// ---------------------------------------------------------------------------
+// register-resident p=2 VHT2 over 8 coefficients/lane, head_dim/8 lanes/vector
+// ---------------------------------------------------------------------------
+template <int HD, int NORM>
+__device__ __forceinline__ void sp_vht2_regs(float (&x)[8], int j, float inv_sqrt_n) {
+    const float s2 = 0.70710678118654752440f;
+#pragma unroll
+    for (int len = 1; len < 8; len <<= 1) {
+#pragma unroll
+        for (int i = 0; i < 8; i += 2 * len) {
+#pragma unroll
+            for (int k = 0; k < len; k++) {
+                float u = x[i + k], v = x[i + k + len];
+                if (NORM == 1) {
+                    x[i + k] = (u + v) * s2;
+                    x[i + k + len] = (u - v) * s2;
+                } else {
+                    x[i + k] = u + v;
+                    x[i + k + len] = u - v;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 1; m < HD / 8; m <<= 1) {
+        const bool hi = (j & m) != 0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            float p = __shfl_xor(x[e], m, SP_WAVE);
+            float r = hi ? (p - x[e]) : (x[e] + p);
+            x[e] = (NORM == 1) ? r * s2 : r;
+        }
+    }
+    if (NORM == 0) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) x[e] *= inv_sqrt_n;
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void sp_load8(const void *src, long long off, float (&x)[8]) {
+    if (DT == SP_DT_F16) {
+        const uint4 w = *reinterpret_cast<const uint4 *>(reinterpret_cast<const unsigned short *>(src) + off);
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            x[2 * k] = sp_f16_bits_to_f32(ww[k] & 0xffffu);
+            x[2 * k + 1] = sp_f16_bits_to_f32(ww[k] >> 16);
+        }
+    } else {
+        const float4 *p = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(src) + off);
+        float4 a = p[0], b = p[1];
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+        x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ void sp_store8(void *dst, long long off, const float (&x)[8]) {
+    if (DT == SP_DT_F16) {
+        uint32_t ww[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            // Materialise the fp32 value first: otherwise the compiler folds the
+            // preceding multiply into the f16 conversion (v_fma_mix), rounding
+            // once to f16 instead of to f32 and then to f16.
+            float xa = x[2 * k], xb = x[2 * k + 1];
+            __asm__ volatile("" : "+v"(xa), "+v"(xb));
+            _Float16 a = (_Float16)xa, b = (_Float16)xb;
+            ww[k] = (uint32_t)__builtin_bit_cast(unsigned short, a) |
+                    ((uint32_t)__builtin_bit_cast(unsigned short, b) << 16);
+        }
+        *reinterpret_cast<uint4 *>(reinterpret_cast<unsigned short *>(dst) + off) =
+            make_uint4(ww[0], ww[1], ww[2], ww[3]);
+    } else {
+        float4 *p = reinterpret_cast<float4 *>(reinterpret_cast<float *>(dst) + off);
+        p[0] = make_float4(x[0], x[1], x[2], x[3]);
+        p[1] = make_float4(x[4], x[5], x[6], x[7]);
+    }
+}
+
+// Copy nbytes from LDS (starting at an offset congruent to the global address
+// mod 4) to global memory: edge bytes singly, interior as aligned dwords.
+__device__ __forceinline__ void sp_tile_store(unsigned char *g, const unsigned char *lds, int nbytes,
+                                              int tid, int nthr) {
+    const int shift = (int)((uintptr_t)g & 3);
+    int head = (4 - shift) & 3;
+    if (head > nbytes) head = nbytes;
+    if (tid < head) g[tid] = lds[tid];
+    const int nw = (nbytes - head) >> 2;
+    uint32_t *gw = reinterpret_cast<uint32_t *>(g + head);
+    const uint32_t *lw = reinterpret_cast<const uint32_t *>(lds + head);
+    for (int k = tid; k < nw; k += nthr) gw[k] = lw[k];
+    for (int k = head + 4 * nw + tid; k < nbytes; k += nthr) g[k] = lds[k];
+}
+
+__device__ __forceinline__ void sp_tile_load(unsigned char *lds, const unsigned char *g, int nbytes,
+                                             int tid, int nthr) {
+    const int shift = (int)((uintptr_t)g & 3);
+    int head = (4 - shift) & 3;
+    if (head > nbytes) head = nbytes;
+    if (tid < head) lds[tid] = g[tid];
+    const int nw = (nbytes - head) >> 2;
+    const uint32_t *gw = reinterpret_cast<const uint32_t *>(g + head);
+    uint32_t *lw = reinterpret_cast<uint32_t *>(lds + head);
+    for (int k = tid; k < nw; k += nthr) lw[k] = gw[k];
+    for (int k = head + 4 * nw + tid; k < nbytes; k += nthr) lds[k] = g[k];
+}
+
+// ---------------------------------------------------------------------------
+// fast encode
+// ---------------------------------------------------------------------------
+template <int HD, int DT, bool MOB, int NORM>
+__global__ void __launch_bounds__(256)
+k_ship_encode_fast(const SpPlan P, const int *__restrict__ order, const void *__restrict__ src,
+                   long long src_outer, long long src_inner, unsigned char *__restrict__ dst,
+                   long long dst_outer, int n_inner, int tiles_per_outer) {
+    constexpr int LPV = HD / 8, VPW = 64 / LPV, ITERS = SP_TILE / (4 * VPW);
+    __shared__ float coef[MOB ? 4 : 1][MOB ? VPW : 1][MOB ? HD : 1];
+    extern __shared__ __attribute__((aligned(16))) unsigned char rec_raw[];
+
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int g = lane / LPV, j = lane % LPV;
+    const int o = blockIdx.x / tiles_per_outer;
+    const int i0 = (blockIdx.x % tiles_per_outer) * SP_TILE;
+    const int nvalid = min(SP_TILE, n_inner - i0);
+    const int B = P.total_bytes;
+
+    unsigned char *gdst = dst + (long long)o * dst_outer + (long long)i0 * B;
+    unsigned char *rec = rec_raw + ((uintptr_t)gdst & 3);
+
+    const int b = P.chunk_band[j];
+    const int bits = P.band_bits[b];
+    const int maxv = (1 << (bits - 1)) - 1;
+    const int cf = P.chunk_first[b], cl = P.chunk_last[b];
+    const int data_off = P.chunk_byte_off[j];
+    const int scale_off = P.band_byte_off[b];
+    int ord[8];
+    if (MOB) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) ord[e] = order[j * 8 + e];
+    }
+
+#pragma unroll 1
+    for (int it = 0; it < ITERS; it++) {
+        const int lv = (it * 4 + w) * VPW + g;
+        const bool valid = lv < nvalid;
+        float x[8];
+        if (valid) {
+            sp_load8<DT>(src, (long long)o * src_outer + (long long)(i0 + lv) * src_inner + j * 8, x);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[e] = 0.0f;
+        }
+        sp_vht2_regs<HD, NORM>(x, j, P.inv_sqrt_n);
+
+        float r[8];
+        if (MOB) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) coef[w][g][j * 8 + e] = x[e];
+            __syncthreads();
+#pragma unroll
+            for (int e = 0; e < 8; e++) r[e] = coef[w][g][ord[e]];
+            __syncthreads();
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) r[e] = x[e];
+        }
+
+        // band absmax: local then segmented scans over the band's lanes
+        float m = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            float a = fabsf(r[e]);
+            m = a > m ? a : m;
+        }
+        float mf = m, mb = m;
+#pragma unroll
+        for (int d = 1; d < LPV; d <<= 1) {
+            float t = __shfl_up(mf, d, LPV);
+            if (j - d >= cf) mf = fmaxf(mf, t);
+        }
+#pragma unroll
+        for (int d = 1; d < LPV; d <<= 1) {
+            float t = __shfl_down(mb, d, LPV);
+            if (j + d <= cl) mb = fmaxf(mb, t);
+        }
+        const float amax = fmaxf(mf, mb);
+        const float scale = (amax > 0.0f) ? sp_div(amax, (float)maxv) : 0.0f;
+        const uint32_t h = sp_f32_to_f16_bits(scale);
+        const float ss = sp_f16_bits_to_f32(h);
+        const float inv = (ss > 0.0f) ? sp_div(1.0f, ss) : 0.0f;
+
+        uint64_t acc = 0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int q = sp_q_rint_clamp(r[e] * inv, maxv);
+            acc |= (uint64_t)(uint32_t)(q + maxv) << (e * bits);
+        }
+        if (valid) {
+            unsigned char *pr = rec + lv * B;
+            for (int k = 0; k < bits; k++) pr[data_off + k] = (unsigned char)(acc >> (8 * k));
+            if (j == cf) {
+                pr[scale_off] = (unsigned char)(h & 0xffu);
+                pr[scale_off + 1] = (unsigned char)(h >> 8);
+            }
+        }
+    }
+    __syncthreads();
+    sp_tile_store(gdst, rec, nvalid * B, tid, 256);
+}
+
+// ---------------------------------------------------------------------------
+// fast decode
+// ---------------------------------------------------------------------------
+template <int HD, int DT, bool MOB, int NORM>
+__global__ void __launch_bounds__(256)
+k_ship_decode_fast(const SpPlan P, const int *__restrict__ order,
+                   const unsigned char *__restrict__ src, long long src_outer,
+                   void *__restrict__ dst, long long dst_outer, long long dst_inner, int n_inner,
+                   int tiles_per_outer) {
+    constexpr int LPV = HD / 8, VPW = 64 / LPV, ITERS = SP_TILE / (4 * VPW);
+    __shared__ float coef[MOB ? 4 : 1][MOB ? VPW : 1][MOB ? HD : 1];
+    extern __shared__ __attribute__((aligned(16))) unsigned char rec_raw[];
+
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int g = lane / LPV, j = lane % LPV;
+    const int o = blockIdx.x / tiles_per_outer;
+    const int i0 = (blockIdx.x % tiles_per_outer) * SP_TILE;
+    const int nvalid = min(SP_TILE, n_inner - i0);
+    const int B = P.total_bytes;
+
+    const unsigned char *gsrc = src + (long long)o * src_outer + (long long)i0 * B;
+    unsigned char *rec = rec_raw + ((uintptr_t)gsrc & 3);
+    sp_tile_load(rec, gsrc, nvalid * B, tid, 256);
+
+    const int b = P.chunk_band[j];
+    const int bits = P.band_bits[b];
+    const int maxv = (1 << (bits - 1)) - 1;
+    const uint32_t mask = (1u << bits) - 1u;
+    const int data_off = P.chunk_byte_off[j];
+    const int scale_off = P.band_byte_off[b];
+    const bool live = b < P.max_bands;
+    int ord[8];
+    if (MOB) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) ord[e] = order[j * 8 + e];
+    }
+    __syncthreads();
+
+#pragma unroll 1
+    for (int it = 0; it < ITERS; it++) {
+        const int lv = (it * 4 + w) * VPW + g;
+        const bool valid = lv < nvalid;
+        float x[8];
+        uint64_t acc = 0;
+        float scale = 0.0f;
+        if (valid) {
+            const unsigned char *pr = rec + lv * B;
+            for (int k = 0; k < bits; k++) acc |= (uint64_t)pr[data_off + k] << (8 * k);
+            scale = sp_scale_from_bits((uint32_t)pr[scale_off] | ((uint32_t)pr[scale_off + 1] << 8));
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int u = (int)((uint32_t)(acc >> (e * bits)) & mask);
+            x[e] = live ? (float)(u - maxv) * scale : 0.0f;
+        }
+        if (MOB) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) coef[w][g][ord[e]] = x[e];
+            __syncthreads();
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[e] = coef[w][g][j * 8 + e];
+            __syncthreads();
+        }
+        sp_vht2_regs<HD, NORM>(x, j, P.inv_sqrt_n);
+        if (valid)
+            sp_store8<DT>(dst, (long long)o * dst_outer + (long long)(i0 + lv) * dst_inner + j * 8, x);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// generic one-vector-per-wave kernels (LDS staged)
+// ---------------------------------------------------------------------------
+
+template <int DT>
+__global__ void __launch_bounds__(256)
+k_ship_encode_generic(const SpPlan P, const int *__restrict__ order, const void *__restrict__ src,
+                      long long src_outer, long long src_inner, unsigned char *__restrict__ dst,
+                      long long dst_outer, int n_outer, int n_inner) {
+    __shared__ float c_s[4][SP_GEN_MAX_N];
+    __shared__ float r_s[4][SP_GEN_MAX_N];
+    __shared__ unsigned char codes_s[4][SP_GEN_MAX_N];
+    __shared__ __attribute__((aligned(16))) unsigned char rec_s[4][SP_GEN_MAX_REC];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const long long v = (long long)blockIdx.x * 4 + w;
+    const bool valid = v < (long long)n_outer * n_inner;
+    const int o = valid ? (int)(v / n_inner) : 0, i = valid ? (int)(v % n_inner) : 0;
+    const int n = P.hd;
+    float *c = c_s[w], *r = r_s[w];
+    for (int k = lane; k < n; k += SP_WAVE)
+        c[k] = valid ? sp_load1<DT>(src, (long long)o * src_outer + (long long)i * src_inner + k) : 0.0f;
+    __syncthreads();
+    sp_transform_lds(c, n, P, lane);
+    for (int k = lane; k < n; k += SP_WAVE) r[k] = order ? c[order[k]] : c[k];
+    __syncthreads();
+    sp_band_quantize_lds(r, rec_s[w], codes_s[w], P, lane);
+    if (valid) {
+        unsigned char *g = dst + (long long)o * dst_outer + (long long)i * P.total_bytes;
+        for (int k = lane; k < P.total_bytes; k += SP_WAVE) g[k] = rec_s[w][k];
+    }
+}
+
+template <int DT>
+__global__ void __launch_bounds__(256)
+k_ship_decode_generic(const SpPlan P, const int *__restrict__ order,
+                      const unsigned char *__restrict__ src, long long src_outer,
+                      void *__restrict__ dst, long long dst_outer, long long dst_inner,
+                      int n_outer, int n_inner) {
+    __shared__ float c_s[4][SP_GEN_MAX_N];
+    __shared__ float r_s[4][SP_GEN_MAX_N];
+    __shared__ __attribute__((aligned(16))) unsigned char rec_s[4][SP_GEN_MAX_REC + 8];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const long long v = (long long)blockIdx.x * 4 + w;
+    const bool valid = v < (long long)n_outer * n_inner;
+    const int o = valid ? (int)(v / n_inner) : 0, i = valid ? (int)(v % n_inner) : 0;
+    const int n = P.hd;
+    float *c = c_s[w], *r = r_s[w];
+    const unsigned char *g = src + (long long)o * src_outer + (long long)i * P.total_bytes;
+    for (int k = lane; k < P.total_bytes + 8; k += SP_WAVE)
+        rec_s[w][k] = (valid && k < P.total_bytes) ? g[k] : (unsigned char)0;
+    __syncthreads();
+    sp_band_dequantize_lds(rec_s[w], r, P, lane);
+    for (int k = lane; k < n; k += SP_WAVE) {
+        if (order) c[order[k]] = r[k];
+        else c[k] = r[k];
+    }
+    __syncthreads();
+    sp_transform_lds(c, n, P, lane);
+    if (valid)
+        for (int k = lane; k < n; k += SP_WAVE)
+            sp_store1<DT>(dst, (long long)o * dst_outer + (long long)i * dst_inner + k, c[k]);
+}
+
+// transform-only (sp_hip_vht2_forward): in place on [n_vecs][n] fp32
+__global__ void __launch_bounds__(256)
+k_transform_only(const SpPlan P, float *__restrict__ data, int n_vecs) {
+    __shared__ float c_s[4][SP_GEN_MAX_N];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const long long v = (long long)blockIdx.x * 4 + w;
+    const bool valid = v < n_vecs;
+    const int n = P.hd;
+    float *c = c_s[w];
+    for (int k = lane; k < n; k += SP_WAVE) c[k] = valid ? data[v * n + k] : 0.0f;
+    __syncthreads();
+    sp_transform_lds(c, n, P, lane);
+    if (valid)
+        for (int k = lane; k < n; k += SP_WAVE) data[v * n + k] = c[k];
+}
+
+// permutation in place: out[r] = in[order[r]] (gather) or out[order[r]] = in[r]
+__global__ void __launch_bounds__(256)
+k_permute(float *__restrict__ data, const int *__restrict__ order, int n, int n_vecs, int inverse) {
+    __shared__ float c_s[4][SP_GEN_MAX_N];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const long long v = (long long)blockIdx.x * 4 + w;
+    const bool valid = v < n_vecs;
+    float *c = c_s[w];
+    for (int k = lane; k < n; k += SP_WAVE) c[k] = valid ? data[v * n + k] : 0.0f;
+    __syncthreads();
+    if (valid)
+        for (int k = lane; k < n; k += SP_WAVE) {
+            if (inverse) data[v * n + order[k]] = c[k];
+            else data[v * n + k] = c[order[k]];
+        }
+}
+
+// ---------------------------------------------------------------------------
+// host launchers
+// ---------------------------------------------------------------------------
+namespace {
+
+template <int HD, int DT>
+hipError_t launch_encode_fast_hd(const SpPlan &P, const int *order, const void *src,
+                                 long long so, long long si, unsigned char *dst, long long dout,
+                                 int n_outer, int n_inner, hipStream_t s) {
+    const int tpo = (n_inner + SP_TILE - 1) / SP_TILE;
+    const dim3 grid((unsigned)((long long)n_outer * tpo)), block(256);
+    const size_t lds = (size_t)SP_TILE * P.total_bytes + 8;
+    if (order) {
+        if (P.norm == 1)
+            hipLaunchKernelGGL((k_ship_encode_fast<HD, DT, true, 1>), grid, block, lds, s, P, order, src, so, si, dst, dout, n_inner, tpo);
+        else
+            hipLaunchKernelGGL((k_ship_encode_fast<HD, DT, true, 0>), grid, block, lds, s, P, order, src, so, si, dst, dout, n_inner, tpo);
+    } else {
+        if (P.norm == 1)
+            hipLaunchKernelGGL((k_ship_encode_fast<HD, DT, false, 1>), grid, block, lds, s, P, order, src, so, si, dst, dout, n_inner, tpo);
+        else
+            hipLaunchKernelGGL((k_ship_encode_fast<HD, DT, false, 0>), grid, block, lds, s, P, order, src, so, si, dst, dout, n_inner, tpo);
+    }
+    return hipGetLastError();
+}
+
+template <int HD, int DT>
+hipError_t launch_decode_fast_hd(const SpPlan &P, const int *order, const unsigned char *src,
+                                 long long so, void *dst, long long dout, long long din,
+                                 int n_outer, int n_inner, hipStream_t s) {
+    const int tpo = (n_inner + SP_TILE - 1) / SP_TILE;
+    const dim3 grid((unsigned)((long long)n_outer * tpo)), block(256);
+    const size_t lds = (size_t)SP_TILE * P.total_bytes + 8;
+    if (order) {
+        if (P.norm == 1)
+            hipLaunchKernelGGL((k_ship_decode_fast<HD, DT, true, 1>), grid, block, lds, s, P, order, src, so, dst, dout, din, n_inner, tpo);
+        else
+            hipLaunchKernelGGL((k_ship_decode_fast<HD, DT, true, 0>), grid, block, lds, s, P, order, src, so, dst, dout, din, n_inner, tpo);
+    } else {
+        if (P.norm == 1)
+            hipLaunchKernelGGL((k_ship_decode_fast<HD, DT, false, 1>), grid, block, lds, s, P, order, src, so, dst, dout, din, n_inner, tpo);
+        else
+            hipLaunchKernelGGL((k_ship_decode_fast<HD, DT, false, 0>), grid, block, lds, s, P, order, src, so, dst, dout, din, n_inner, tpo);
+    }
+    return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_encode_fast(const SpPlan &P, const int *order, const void *src, long long so,
+                              long long si, unsigned char *dst, long long dout, int n_outer,
+                              int n_inner, hipStream_t s) {
+    switch (P.hd) {
+    case 64: return launch_encode_fast_hd<64, DT>(P, order, src, so, si, dst, dout, n_outer, n_inner, s);
+    case 128: return launch_encode_fast_hd<128, DT>(P, order, src, so, si, dst, dout, n_outer, n_inner, s);
+    case 256: return launch_encode_fast_hd<256, DT>(P, order, src, so, si, dst, dout, n_outer, n_inner, s);
+    case 512: return launch_encode_fast_hd<512, DT>(P, order, src, so, si, dst, dout, n_outer, n_inner, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+template <int DT>
+hipError_t launch_decode_fast(const SpPlan &P, const int *order, const unsigned char *src,
+                              long long so, void *dst, long long dout, long long din, int n_outer,
+                              int n_inner, hipStream_t s) {
+    switch (P.hd) {
+    case 64: return launch_decode_fast_hd<64, DT>(P, order, src, so, dst, dout, din, n_outer, n_inner, s);
+    case 128: return launch_decode_fast_hd<128, DT>(P, order, src, so, dst, dout, din, n_outer, n_inner, s);
+    case 256: return launch_decode_fast_hd<256, DT>(P, order, src, so, dst, dout, din, n_outer, n_inner, s);
+    case 512: return launch_decode_fast_hd<512, DT>(P, order, src, so, dst, dout, din, n_outer, n_inner, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+bool fast_eligible(const SpPlan &P, long long src_or_dst_inner, int dtype) {
+    if (!P.chunk_ok) return false;
+    if (!(P.hd == 64 || P.hd == 128 || P.hd == 256 || P.hd == 512)) return false;
+    (void)src_or_dst_inner;
+    (void)dtype;
+    return true;
+}
+
+bool aligned16(const void *p, long long outer_elems, long long inner_elems, int esize) {
+    return ((uintptr_t)p % 16 == 0) && ((outer_elems * esize) % 16 == 0) &&
+           ((inner_elems * esize) % 16 == 0);
+}
+
+}  // namespace
+
+hipError_t sp_launch_ship_encode(const SpPlan &P, const int *order, const void *src, int dtype,
+                                 long long so, long long si, unsigned char *dst, long long dout,
+                                 int n_outer, int n_inner, hipStream_t s) {
+    if (n_outer <= 0 || n_inner <= 0) return hipSuccess;
+    const int esize = dtype == SP_DT_F16 ? 2 : 4;
+    if (fast_eligible(P, si, dtype) && aligned16(src, so, si, esize)) {
+        if (dtype == SP_DT_F16)
+            return launch_encode_fast<SP_DT_F16>(P, order, src, so, si, dst, dout, n_outer, n_inner, s);
+        return launch_encode_fast<SP_DT_F32>(P, order, src, so, si, dst, dout, n_outer, n_inner, s);
+    }
+    if (P.hd > SP_GEN_MAX_N || P.total_bytes > SP_GEN_MAX_REC) return hipErrorInvalidValue;
+    const long long nv = (long long)n_outer * n_inner;
+    const dim3 grid((unsigned)((nv + 3) / 4)), block(256);
+    if (dtype == SP_DT_F16)
+        hipLaunchKernelGGL((k_ship_encode_generic<SP_DT_F16>), grid, block, 0, s, P, order, src, so, si, dst, dout, n_outer, n_inner);
+    else
+        hipLaunchKernelGGL((k_ship_encode_generic<SP_DT_F32>), grid, block, 0, s, P, order, src, so, si, dst, dout, n_outer, n_inner);
+    return hipGetLastError();
+}
+
+hipError_t sp_launch_ship_decode(const SpPlan &P, const int *order, const unsigned char *src,
+                                 long long so, void *dst, int dtype, long long dout, long long din,
+                                 int n_outer, int n_inner, hipStream_t s) {
+    if (n_outer <= 0 || n_inner <= 0) return hipSuccess;
+    const int esize = dtype == SP_DT_F16 ? 2 : 4;
+    if (fast_eligible(P, din, dtype) && aligned16(dst, dout, din, esize)) {
+        if (dtype == SP_DT_F16)
+            return launch_decode_fast<SP_DT_F16>(P, order, src, so, dst, dout, din, n_outer, n_inner, s);
+        return launch_decode_fast<SP_DT_F32>(P, order, src, so, dst, dout, din, n_outer, n_inner, s);
+    }
+    if (P.hd > SP_GEN_MAX_N || P.total_bytes > SP_GEN_MAX_REC) return hipErrorInvalidValue;
+    const long long nv = (long long)n_outer * n_inner;
+    const dim3 grid((unsigned)((nv + 3) / 4)), block(256);
+    if (dtype == SP_DT_F16)
+        hipLaunchKernelGGL((k_ship_decode_generic<SP_DT_F16>), grid, block, 0, s, P, order, src, so, dst, dout, din, n_outer, n_inner);
+    else
+        hipLaunchKernelGGL((k_ship_decode_generic<SP_DT_F32>), grid, block, 0, s, P, order, src, so, dst, dout, din, n_outer, n_inner);
+    return hipGetLastError();
+}
+
+// Generic-only variants (used by tests to cross-check both kernel families).
+hipError_t sp_launch_ship_encode_generic(const SpPlan &P, const int *order, const void *src, int dtype,
+                                         long long so, long long si, unsigned char *dst,
+                                         long long dout, int n_outer, int n_inner, hipStream_t s) {
+    if (n_outer <= 0 || n_inner <= 0) return hipSuccess;
+    if (P.hd > SP_GEN_MAX_N || P.total_bytes > SP_GEN_MAX_REC) return hipErrorInvalidValue;
+    const long long nv = (long long)n_outer * n_inner;
+    const dim3 grid((unsigned)((nv + 3) / 4)), block(256);
+    if (dtype == SP_DT_F16)
+        hipLaunchKernelGGL((k_ship_encode_generic<SP_DT_F16>), grid, block, 0, s, P, order, src, so, si, dst, dout, n_outer, n_inner);
+    else
+        hipLaunchKernelGGL((k_ship_encode_generic<SP_DT_F32>), grid, block, 0, s, P, order, src, so, si, dst, dout, n_outer, n_inner);
+    return hipGetLastError();
+}
+
+hipError_t sp_launch_ship_decode_generic(const SpPlan &P, const int *order, const unsigned char *src,
+                                         long long so, void *dst, int dtype, long long dout,
+                                         long long din, int n_outer, int n_inner, hipStream_t s) {
+    if (n_outer <= 0 || n_inner <= 0) return hipSuccess;
+    if (P.hd > SP_GEN_MAX_N || P.total_bytes > SP_GEN_MAX_REC) return hipErrorInvalidValue;
+    const long long nv = (long long)n_outer * n_inner;
+    const dim3 grid((unsigned)((nv + 3) / 4)), block(256);
+    if (dtype == SP_DT_F16)
+        hipLaunchKernelGGL((k_ship_decode_generic<SP_DT_F16>), grid, block, 0, s, P, order, src, so, dst, dout, din, n_outer, n_inner);
+    else
+        hipLaunchKernelGGL((k_ship_decode_generic<SP_DT_F32>), grid, block, 0, s, P, order, src, so, dst, dout, din, n_outer, n_inner);
+    return hipGetLastError();
+}
+
+hipError_t sp_launch_transform(const SpPlan &P, float *data, int n_vecs, hipStream_t s) {
+    if (n_vecs <= 0) return hipSuccess;
+    if (P.hd > SP_GEN_MAX_N) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_transform_only, dim3((n_vecs + 3) / 4), dim3(256), 0, s, P, data, n_vecs);
+    return hipGetLastError();
+}
+
+hipError_t sp_launch_permute(float *data, const int *order, int n, int n_vecs, int inverse,
+                             hipStream_t s) {
+    if (n_vecs <= 0) return hipSuccess;
+    if (n > SP_GEN_MAX_N) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_permute, dim3((n_vecs + 3) / 4), dim3(256), 0, s, data, order, n, n_vecs, inverse);
+    return hipGetLastError();
+}

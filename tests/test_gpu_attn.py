@@ -1,0 +1,101 @@
+"""Fused decompress-attention decode vs the oracle (scores and softmax.V within 1e-3
+relative in fp32), GQA grouping, split boundaries, and the fp16 baseline kernel."""
+import ctypes as C
+import math
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+import oracle_py as O  # noqa: E402
+import sp_hip as S  # noqa: E402
+import workloads as W  # noqa: E402
+from gpu_util import dev, empty_f32, host, p, stream  # noqa: E402
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def rel_close(got, ref, tol=1e-3):
+    err = np.abs(got - ref).max()
+    scale = np.abs(ref).max()
+    assert err <= tol * scale, (err, scale)
+
+
+@pytest.mark.parametrize("n_q,H,n_ctx,hd,mob", [
+    (8, 2, 300, 128, True),      # GQA 4, a partial second split
+    (32, 8, 1024, 128, True),    # Llama-3-8B head layout
+    (4, 4, 256, 128, False),     # MHA, exactly one split, no Mobius
+    (16, 8, 777, 256, True),     # Gemma-3 head_dim
+    (8, 8, 129, 64, True),
+])
+def test_fused_attention_matches_oracle(n_q, H, n_ctx, hd, mob):
+    say(f"attn n_q={n_q} H={H} n_ctx={n_ctx} hd={hd} mob={mob}")
+    k16, v16 = W.cfg2_kv(n_heads=H, n_pos=n_ctx, hd=hd, seed=n_ctx)
+    q = W.cfg2_q(n_q=n_q, hd=hd, pos=n_ctx, seed=n_ctx + 1)
+    cfg = S.config(hd, 2, H, mobius=mob)
+    cc = S.ShipCache(cfg, n_ctx + 5, stream=torch.cuda.current_stream().cuda_stream)
+    layer = 1
+    for h in range(H):
+        kt, vt = dev(k16[h].view(np.uint16)), dev(v16[h].view(np.uint16))
+        S.lib().sp_hip_write_k_batch_f16(cc.ref, layer, h, 0, n_ctx, p(kt))
+        S.lib().sp_hip_write_v_batch_f16(cc.ref, layer, h, 0, n_ctx, p(vt))
+    torch.cuda.synchronize()
+    kbc, vbc = O.band_config(hd, [5, 5, 4, 3]), O.band_config(hd, [3])
+    order = O.mobius_order(hd) if mob else None
+    kref = np.stack([O.ship_compress_f16(k16[h].view(np.uint16), kbc, order) for h in range(H)])
+    vref = np.stack([O.ship_compress_f16(v16[h].view(np.uint16), vbc) for h in range(H)])
+    scale = 1.0 / math.sqrt(hd)
+    s_ref, o_ref = O.attn_decode(q, kref, vref, H, n_ctx, kbc, vbc, order, scale)
+    qt = dev(q)
+    sc, out = empty_f32(n_q * n_ctx), empty_f32(n_q * hd)
+    S.check(S.lib().sp_hip_attn_decode(cc.ref, layer, n_ctx, p(qt), n_q, C.c_float(scale), p(sc), p(out),
+                                       stream()))
+    rel_close(host(sc).reshape(n_q, n_ctx), s_ref)
+    rel_close(host(out).reshape(n_q, hd), o_ref)
+    # scores-only mode (the reference op's output) and output-only mode agree
+    sc2, out2 = empty_f32(n_q * n_ctx), empty_f32(n_q * hd)
+    S.check(S.lib().sp_hip_attn_decode(cc.ref, layer, n_ctx, p(qt), n_q, C.c_float(scale), p(sc2), None, stream()))
+    S.check(S.lib().sp_hip_attn_decode(cc.ref, layer, n_ctx, p(qt), n_q, C.c_float(scale), None, p(out2), stream()))
+    np.testing.assert_array_equal(host(sc2), host(sc))
+    np.testing.assert_array_equal(host(out2), host(out))
+    cc.free()
+
+
+def test_attention_rejects_bad_shapes():
+    cfg = S.config(128, 1, 2)
+    cc = S.ShipCache(cfg, 64)
+    q = empty_f32(8 * 128)
+    o = empty_f32(8 * 128)
+    L = S.lib()
+    assert L.sp_hip_attn_decode(cc.ref, 0, 65, p(q), 8, C.c_float(1.0), None, p(o), stream()) == -1  # n_kv > max_seq
+    assert L.sp_hip_attn_decode(cc.ref, 1, 10, p(q), 8, C.c_float(1.0), None, p(o), stream()) == -1  # layer
+    assert L.sp_hip_attn_decode(cc.ref, 0, 10, p(q), 3, C.c_float(1.0), None, p(o), stream()) == -1  # n_q % H
+    assert L.sp_hip_attn_decode(cc.ref, 0, 10, p(q), 0, C.c_float(1.0), None, p(o), stream()) == -1
+    cc.free()
+
+
+def test_fp16_baseline_attention_matches_dense():
+    n_q, H, n_ctx, hd = 8, 2, 600, 128
+    rng = np.random.default_rng(3)
+    k = rng.standard_normal((1, H, n_ctx, hd)).astype(np.float16)
+    v = rng.standard_normal((1, H, n_ctx, hd)).astype(np.float16)
+    q = rng.standard_normal((n_q, hd)).astype(np.float32)
+    scale = 1.0 / math.sqrt(hd)
+    kt, vt, qt = dev(k.view(np.uint16)), dev(v.view(np.uint16)), dev(q)
+    sc, out = empty_f32(n_q * n_ctx), empty_f32(n_q * hd)
+    S.check(S.lib().sp_hip_attn_decode_f16(p(kt), p(vt), H, n_ctx, hd, 0, n_ctx, p(qt), n_q, C.c_float(scale),
+                                           p(sc), p(out), stream()))
+    kk = k[0].astype(np.float64)
+    vv = v[0].astype(np.float64)
+    s_ref = np.stack([kk[h // 4] @ q[h] for h in range(n_q)]) * scale
+    pr = np.exp(s_ref - s_ref.max(1, keepdims=True))
+    pr /= pr.sum(1, keepdims=True)
+    o_ref = np.stack([pr[h] @ vv[h // 4] for h in range(n_q)])
+    rel_close(host(sc).reshape(n_q, n_ctx), s_ref)
+    rel_close(host(out).reshape(n_q, hd), o_ref)

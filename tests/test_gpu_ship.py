@@ -1,0 +1,170 @@
+"""Ship codec on the GPU vs the CPU oracle: packed codes bit-exact, reconstructions
+bit-exact (same fp32 operation order), across kernel families, dtypes, band
+geometries, normalisation conventions, partial reads and edge cases."""
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+import oracle_py as O  # noqa: E402
+import sp_hip as S  # noqa: E402
+import workloads as W  # noqa: E402
+from gpu_util import d2h, decode, dev, empty_f16, empty_f32, empty_u8, encode, host, order_dev, p, stream  # noqa: E402
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+CASES = [
+    # hd, bits, mobius, norm, ternary   (fast path when hd pow2 and bands on multiples of 8)
+    (128, [5, 5, 4, 3], True, S.NORM_FINAL, 0),
+    (128, [3], False, S.NORM_FINAL, 0),
+    (128, [5, 5, 4, 3], True, S.NORM_STAGE, 0),
+    (64, [5, 5, 4, 3], True, S.NORM_FINAL, 0),
+    (256, [5, 5, 4, 3], True, S.NORM_FINAL, 0),
+    (128, [5, 5, 4, 3], True, S.NORM_FINAL, 1 << 3),
+    (64, [5, 4, 4], True, S.NORM_FINAL, 0),        # bands 21/21/22 -> generic kernels
+    (96, [5, 4, 4], True, S.NORM_FINAL, 0),        # Vilenkin 2^5*3
+    (96, [5], False, S.NORM_FINAL, 0),
+    (128, [5] * 10, True, S.NORM_FINAL, 0),        # last band absorbs remainder
+    (128, [8, 8, 8, 8], True, S.NORM_FINAL, 0),
+    (128, [2, 1], True, S.NORM_FINAL, 0),          # draft "aggressive" preset
+]
+
+
+@pytest.mark.parametrize("hd,bits,mob,norm,tmask", CASES)
+def test_encode_decode_bit_exact(hd, bits, mob, norm, tmask):
+    say(f"case hd={hd} bits={bits} mob={mob} norm={norm} tmask={tmask}")
+    n = 1000
+    k16, _ = W.cfg1_kv(n_heads=1, n_pos=n, hd=hd, seed=hd + len(bits))
+    x16 = k16.reshape(n, hd).view(np.uint16)
+    obc = O.band_config(hd, bits, tmask)
+    sbc = S.band_config(hd, bits, tmask)
+    order = O.mobius_order(hd) if mob else None
+    ref = O.ship_compress_f16(x16, obc, order, norm)
+    ot = order_dev(hd) if mob else None
+    xt = dev(x16)
+    for generic in (False, True):
+        got = host(encode(sbc, ot, xt, S.DTYPE_F16, n, hd, norm, generic)).reshape(n, -1)
+        np.testing.assert_array_equal(got, ref, err_msg=f"codes generic={generic}")
+    # fp32 entry point gives the same codes
+    got32 = host(encode(sbc, ot, dev(k16.reshape(n, hd).astype(np.float32)), S.DTYPE_F32, n, hd, norm)).reshape(n, -1)
+    np.testing.assert_array_equal(got32, ref)
+    # decode: fp32 bit-exact, fp16 bit-exact
+    rec = dev(ref.reshape(-1))
+    r32 = O.ship_decompress_f32(ref, obc, order, norm)
+    r16 = O.ship_decompress_f16(ref, obc, order, norm)
+    for generic in (False, True):
+        g32 = host(decode(sbc, ot, rec, S.DTYPE_F32, n, hd, norm, -1, generic)).reshape(n, hd)
+        np.testing.assert_array_equal(g32.view(np.uint32), r32.view(np.uint32), err_msg=f"f32 generic={generic}")
+        g16 = host(decode(sbc, ot, rec, S.DTYPE_F16, n, hd, norm, -1, generic), np.uint16).reshape(n, hd)
+        np.testing.assert_array_equal(g16, r16, err_msg=f"f16 generic={generic}")
+
+
+@pytest.mark.parametrize("max_bands", [0, 1, 2, 3, 4, 7, -1])
+def test_partial_reads(max_bands):
+    hd, bits, n = 128, [5, 5, 4, 3], 300
+    k16, _ = W.cfg1_kv(n_heads=1, n_pos=n, seed=9)
+    x16 = k16.reshape(n, hd).view(np.uint16)
+    obc, sbc = O.band_config(hd, bits), S.band_config(hd, bits)
+    order = O.mobius_order(hd)
+    ref = O.ship_compress_f16(x16, obc, order)
+    want = O.ship_decompress_f32(ref, obc, order, O.NORM_FINAL, max_bands)
+    for generic in (False, True):
+        got = host(decode(sbc, order_dev(hd), dev(ref.reshape(-1)), S.DTYPE_F32, n, hd, S.NORM_FINAL,
+                          max_bands, generic)).reshape(n, hd)
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_edge_inputs():
+    """zeros, fp16 extremes, huge fp32 values (scale overflow -> zeroed band), subnormals."""
+    hd, bits = 128, [5, 5, 4, 3]
+    rng = np.random.default_rng(4)
+    rows = [np.zeros(hd, np.float32), np.full(hd, 65504.0, np.float32), np.full(hd, -65504.0, np.float32),
+            (rng.standard_normal(hd) * 1e-6).astype(np.float32), (rng.standard_normal(hd) * 6e-8).astype(np.float32)]
+    big = rng.standard_normal(hd).astype(np.float32)
+    big[3] = 1e30
+    rows.append(big)
+    one = np.zeros(hd, np.float32)
+    one[17] = 1.0
+    rows.append(one)
+    x = np.stack(rows * 10).astype(np.float32)
+    n = x.shape[0]
+    obc, sbc = O.band_config(hd, bits), S.band_config(hd, bits)
+    order = O.mobius_order(hd)
+    ref = O.ship_compress_f32(x, obc, order)
+    for generic in (False, True):
+        got = host(encode(sbc, order_dev(hd), dev(x), S.DTYPE_F32, n, hd, S.NORM_FINAL, generic)).reshape(n, -1)
+        np.testing.assert_array_equal(got, ref)
+        rec = O.ship_decompress_f32(ref, obc, order)
+        g = host(decode(sbc, order_dev(hd), dev(ref.reshape(-1)), S.DTYPE_F32, n, hd, S.NORM_FINAL, -1, generic))
+        np.testing.assert_array_equal(g.reshape(n, hd).view(np.uint32), rec.view(np.uint32))
+
+
+def test_empty_and_single():
+    hd, bc = 128, S.band_config(128, [3])
+    x = dev(np.zeros((1, hd), np.float32))
+    out = empty_u8(64)
+    S.check(S.lib().sp_hip_ship_encode(C.byref(bc), None, 0, p(x), S.DTYPE_F32, 0, hd, p(out), 0, 1, 0, stream()))
+    torch.cuda.synchronize()
+    assert int(out.sum()) == 0
+    got = host(encode(bc, None, x, S.DTYPE_F32, 1, hd))
+    np.testing.assert_array_equal(got[:50], O.ship_compress_f32(np.zeros((1, hd), np.float32), O.band_config(128, [3]))[0])
+
+
+def test_cache_slots_layer_and_all_layouts():
+    """sp_hip_write_layer / read_layer (llama cache rows) and write_all / read_all agree with
+    the oracle for every slot, including odd start positions (unaligned V records)."""
+    L, H, hd, max_seq = 3, 4, 128, 96
+    cfg = S.config(hd, L, H)
+    cc = S.ShipCache(cfg, max_seq, stream=torch.cuda.current_stream().cuda_stream)
+    order = O.mobius_order(hd)
+    kbc, vbc = O.band_config(hd, [5, 5, 4, 3]), O.band_config(hd, [3])
+    rng = np.random.default_rng(12)
+    start, n_tok = 13, 41
+    k = rng.standard_normal((L, n_tok, H, hd)).astype(np.float16)
+    v = rng.standard_normal((L, n_tok, H, hd)).astype(np.float16)
+    for layer in range(L):
+        kt, vt = dev(k[layer].view(np.uint16)), dev(v[layer].view(np.uint16))
+        S.check(S.lib().sp_hip_write_layer(cc.ref, layer, start, n_tok, p(kt), p(vt), H * hd, S.DTYPE_F16))
+    torch.cuda.synchronize()
+    kB, vB = kbc.total_bytes, vbc.total_bytes
+    kc = d2h(cc.c.d_k_cache, L * H * max_seq * kB).reshape(L, H, max_seq, kB)
+    vc = d2h(cc.c.d_v_cache, L * H * max_seq * vB).reshape(L, H, max_seq, vB)
+    for layer in range(L):
+        for h in range(H):
+            kref = O.ship_compress_f16(k[layer, :, h].view(np.uint16), kbc, order)
+            vref = O.ship_compress_f16(v[layer, :, h].view(np.uint16), vbc)
+            np.testing.assert_array_equal(kc[layer, h, start:start + n_tok], kref)
+            np.testing.assert_array_equal(vc[layer, h, start:start + n_tok], vref)
+            assert not kc[layer, h, :start].any() and not kc[layer, h, start + n_tok:].any()
+            assert not vc[layer, h, :start].any() and not vc[layer, h, start + n_tok:].any()
+    # read_layer back (fp32 rows)
+    for layer in range(L):
+        ko, vo = empty_f32(n_tok * H * hd), empty_f32(n_tok * H * hd)
+        S.check(S.lib().sp_hip_read_layer(cc.ref, layer, start, n_tok, p(ko), p(vo), H * hd, S.DTYPE_F32, -1))
+        ko = host(ko).reshape(n_tok, H, hd)
+        vo = host(vo).reshape(n_tok, H, hd)
+        for h in range(H):
+            np.testing.assert_array_equal(ko[:, h], O.ship_decompress_f32(kc[layer, h, start:start + n_tok], kbc, order))
+            np.testing.assert_array_equal(vo[:, h], O.ship_decompress_f32(vc[layer, h, start:start + n_tok], vbc))
+    # read_all over every slot (fp16)
+    ka, va = empty_f16(L * H * n_tok * hd), empty_f16(L * H * n_tok * hd)
+    S.check(S.lib().sp_hip_read_all(cc.ref, start, n_tok, p(ka), p(va), S.DTYPE_F16, -1))
+    ka = host(ka, np.uint16).reshape(L, H, n_tok, hd)
+    for layer in range(L):
+        for h in range(H):
+            np.testing.assert_array_equal(ka[layer, h], O.ship_decompress_f16(kc[layer, h, start:start + n_tok], kbc, order))
+    # out-of-range requests are rejected without launching
+    kt = dev(k[0].view(np.uint16))
+    assert S.lib().sp_hip_write_layer(cc.ref, L, 0, 1, p(kt), p(kt), H * hd, S.DTYPE_F16) == -1
+    assert S.lib().sp_hip_write_layer(cc.ref, 0, max_seq - 1, 2, p(kt), p(kt), H * hd, S.DTYPE_F16) == -1
+    assert S.lib().sp_hip_write_layer(cc.ref, 0, 0, 2, p(kt), p(kt), H * hd - 1, S.DTYPE_F16) == -1
+    cc.free()
+

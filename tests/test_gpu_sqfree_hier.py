@@ -1,0 +1,115 @@
+"""Sqfree+spinor and hierarchical Vilenkin codecs on the GPU vs the CPU oracle:
+records bit-exact, reconstructions bit-exact."""
+import ctypes as C
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+import oracle_py as O  # noqa: E402
+import sp_hip as S  # noqa: E402
+import workloads as W  # noqa: E402
+from gpu_util import d2h, dev, empty_f32, host, p  # noqa: E402
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.parametrize("hd,bits,rbits,spinor,sk_frac", [
+    (128, [5, 4, 4, 4, 5], 3, True, 0.0),    # reference CUDA geometry: sk_k = pad/2 = 77
+    (128, [5, 4, 4, 4, 5], 3, True, 0.75),   # cfg 4: SK_FRAC 0.75 -> sk_k = 115
+    (128, [3, 3, 3, 3, 3], 3, True, 0.0),    # SPINOR 3/3/3/3/3 (shannon_prime_llama_sqfree.c:27)
+    (128, [5, 4, 4, 4, 5], 2, False, 0.0),
+    (64, [5, 4, 4, 4, 5], 4, True, 0.0),
+    (256, [5, 4, 4, 4, 5], 3, True, 0.0),
+])
+def test_sqfree_bit_exact(hd, bits, rbits, spinor, sk_frac):
+    say(f"sqfree hd={hd} bits={bits} rbits={rbits} spinor={spinor} sk_frac={sk_frac}")
+    n = 300
+    k16, _ = W.cfg4_kv(n_heads=1, n_pos=n, hd=hd, seed=hd + rbits)
+    x16 = k16.reshape(n, hd).view(np.uint16)
+    pad = O.sqfree_pad_dim(hd)
+    sk = int(pad * sk_frac) if sk_frac else pad // 2
+    km = O.Knight(pad, sk)
+    skel_bc = O.band_config(sk, bits)
+    ref = O.sqfree_compress_f16(x16, hd, km, skel_bc, rbits, spinor)
+    rec = O.sqfree_decompress_f32(ref, hd, km, skel_bc, rbits, spinor)
+    cfg = S.config(hd, 1, 1, k_bits=bits, v_bits=bits)
+    cc = S.SqfreeCache(cfg, n, rbits=rbits, spinor=spinor, sk_k=sk,
+                       stream=torch.cuda.current_stream().cuda_stream)
+    assert (cc.c.pad_dim, cc.c.sk_k, cc.c.n_res) == (pad, sk, pad - sk)
+    # device Knight tables equal the oracle's
+    sk_idx = np.zeros(sk, np.int32)
+    res_idx = np.zeros(max(pad - sk, 1), np.int32)
+    off = np.zeros(pad - sk + 1, np.int32)
+    slot = np.zeros(max(cc.c.n_terms, 1), np.int32)
+    mu = np.zeros(max(cc.c.n_terms, 1), np.int32)
+    S.check(S.lib().sp_hip_sqfree_get_tables(cc.ref, C.c_void_p(sk_idx.ctypes.data),
+                                             C.c_void_p(res_idx.ctypes.data), C.c_void_p(off.ctypes.data),
+                                             C.c_void_p(slot.ctypes.data), C.c_void_p(mu.ctypes.data)))
+    np.testing.assert_array_equal(sk_idx, km.skeleton_idx)
+    np.testing.assert_array_equal(off, km.csr_offsets)
+    assert cc.c.n_terms == km.n_terms
+    np.testing.assert_array_equal(slot[:km.n_terms], km.csr_skel_slot)
+    np.testing.assert_array_equal(mu[:km.n_terms], km.csr_mu_sign.astype(np.int32))
+    assert cc.c.bytes_per_pos_k == ref.shape[1]
+    xt = dev(x16)
+    S.check(S.lib().sp_hip_sqfree_write_batch(cc.ref, 0, 0, 0, 0, n, p(xt), S.DTYPE_F16))
+    got = d2h(cc.c.d_k_cache, n * ref.shape[1]).reshape(n, -1)
+    np.testing.assert_array_equal(got, ref)
+    out = empty_f32(n * hd)
+    S.check(S.lib().sp_hip_sqfree_read_batch(cc.ref, 0, 0, 0, 0, n, p(out), S.DTYPE_F32))
+    g = host(out).reshape(n, hd)
+    np.testing.assert_array_equal(g.view(np.uint32), rec.view(np.uint32))
+    corr = np.mean([O.correlation(a, b) for a, b in zip(k16.reshape(n, hd).astype(np.float32), g)])
+    assert corr > 0.9, corr
+    cc.free()
+
+
+def test_sqfree_record_size_cfg4():
+    """98 B at pad 154, sk_k 77, 5/4/4/4/5, rb 3, spinor (shannon_prime_sqfree.cu:683-686)."""
+    cfg = S.config(128, 1, 1, k_bits=[5, 4, 4, 4, 5], v_bits=[5, 4, 4, 4, 5])
+    cc = S.SqfreeCache(cfg, 4, rbits=3, spinor=True)
+    assert cc.c.bytes_per_pos_k == 98
+    cc.free()
+
+
+@pytest.mark.parametrize("hd,rbits,skel_bits", [(256, 2, [5, 5]), (128, 2, [5, 5]), (128, 3, [5, 4, 4])])
+def test_hier_bit_exact(hd, rbits, skel_bits):
+    say(f"hier hd={hd} rbits={rbits} skel_bits={skel_bits}")
+    n, n_slots = 200, 2
+    pad = O.sqfree_pad_dim(hd)
+    skel_idx, tgt_idx = O.hier_geometry(pad)
+    skel_bc = O.band_config(len(skel_idx), skel_bits)
+    Wm = W.hier_W(n_slots, len(tgt_idx), len(skel_idx), seed=hd)
+    k16, _ = W.cfg5_kv(n_heads=n_slots, n_pos=n, hd=hd, seed=hd + 1)
+    cfg = S.config(hd, 1, n_slots)
+    hc = S.HierCache(cfg, pad, skel_idx, tgt_idx, S.band_config(len(skel_idx), skel_bits), rbits, n,
+                     n_slots, stream=torch.cuda.current_stream().cuda_stream)
+    hc.upload_W(Wm)
+    B = O.hier_bytes(skel_bc, len(tgt_idx), rbits)
+    assert hc.c.bytes_per_pos_k == B
+    for slot in range(n_slots):
+        x16 = k16[slot].view(np.uint16)
+        ref = O.hier_compress_f16(x16, hd, pad, skel_idx, tgt_idx, skel_bc, Wm[slot], rbits)
+        rec = O.hier_decompress_f32(ref, hd, pad, skel_idx, tgt_idx, skel_bc, Wm[slot], rbits)
+        xt = dev(x16)
+        S.check(S.lib().sp_hip_hier_write_batch(hc.ref, 1, 0, slot, 0, n, p(xt), S.DTYPE_F16))
+        allv = d2h(hc.c.d_v_cache, n_slots * n * B).reshape(n_slots, n, B)
+        np.testing.assert_array_equal(allv[slot], ref)
+        out = empty_f32(n * hd)
+        S.check(S.lib().sp_hip_hier_read_batch(hc.ref, 1, 0, slot, 0, n, p(out), S.DTYPE_F32))
+        np.testing.assert_array_equal(host(out).reshape(n, hd).view(np.uint32), rec.view(np.uint32))
+    hc.free()
+
+
+def test_hier_record_size_cfg5():
+    pad = O.sqfree_pad_dim(256)
+    skel_idx, tgt_idx = O.hier_geometry(pad)
+    assert (pad, len(skel_idx), len(tgt_idx)) == (330, 30, 300)
+    assert O.hier_bytes(O.band_config(30, [5, 5]), 300, 2) == 103
