@@ -34,6 +34,7 @@ struct SpPlan {
     int n_factors;    // Vilenkin stage primes (non power-of-2 transforms)
     int chunk_ok;     // 1 when every band boundary is a multiple of 8 coefficients
     int skip_transform; // 1: identity transform (quantize/dequantize-only launchers)
+    int order_default;  // 1: the Mobius table passed with this plan is the default squarefree-first order
     unsigned char factors[16];
     unsigned char band_bits[SP_MAX_BANDS_DEV];
     short band_off[SP_MAX_BANDS_DEV];

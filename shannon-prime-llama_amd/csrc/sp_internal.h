@@ -167,6 +167,14 @@ hipError_t sp_launch_ship_decode_generic(const SpPlan &P, const int *order,
                                          int dtype, long long dout, long long din, int n_outer,
                                          int n_inner, hipStream_t s);
 hipError_t sp_launch_transform(const SpPlan &P, float *data, int n_vecs, hipStream_t s);
+// one-vector-per-lane kernels for the shipping layouts; hipErrorNotSupported when
+// no specialization fits (nothing launched)
+hipError_t sp_launch_ship_encode_lane(const SpPlan &P, bool default_order, const void *src, int dtype,
+                                      long long so, long long si, unsigned char *dst, long long dout,
+                                      int n_outer, int n_inner, hipStream_t s);
+hipError_t sp_launch_ship_decode_lane(const SpPlan &P, bool default_order, const unsigned char *src,
+                                      long long so, void *dst, int dtype, long long dout, long long din,
+                                      int n_outer, int n_inner, hipStream_t s);
 hipError_t sp_launch_permute(float *data, const int *order, int n, int n_vecs, int inverse,
                              hipStream_t s);
 

@@ -436,6 +436,7 @@ extern "C" int sp_hip_cache_init(sp_hip_cache_t *cc, const sp_config_t *cfg, int
         set_err("cache_init: head_dim %d needs the generic kernels (max %d)", hd, SP_GEN_MAX_N);
         return -1;
     }
+    pv->kplan.order_default = 1;  // d_mobius_order below is the default table
     cc->priv = pv;
     const size_t n_slots = (size_t)cfg->n_layers * cfg->n_heads_kv;
     const size_t kb = n_slots * max_seq_len * cc->k_bands.total_bytes;
@@ -1084,6 +1085,7 @@ extern "C" int sp_shadow_cache_init(sp_shadow_cache_t *sc, const sp_config_t *cf
         set_err("shadow_init: head_dim %d unsupported", hd);
         return -1;
     }
+    dv->kplan.order_default = 1;
     const int rec = sc->k_bands.total_bytes > sc->v_bands.total_bytes ? sc->k_bands.total_bytes : sc->v_bands.total_bytes;
     dv->st = stage_create(hd, rec, 4096, cfg->use_mobius_mask ? sc->mobius_mask.order : nullptr);
     if (!dv->st) {

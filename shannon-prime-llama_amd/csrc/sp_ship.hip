@@ -22,6 +22,8 @@
 #include "sp_device.h"
 #include "sp_internal.h"
 
+#include <stdlib.h>
+
 #define SP_TILE 64
 
 // ---------------------------------------------------------------------------
@@ -482,6 +484,17 @@ bool fast_eligible(const SpPlan &P, long long src_or_dst_inner, int dtype) {
     return true;
 }
 
+// SP_HIP_NO_LANE_KERNELS=1 routes the shipping layouts through the 8-coefficient-
+// per-lane kernels instead (used by tests to cross-check kernel families).
+bool getenv_lane_off() {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("SP_HIP_NO_LANE_KERNELS");
+        v = (e && e[0] == '1') ? 1 : 0;
+    }
+    return v == 1;
+}
+
 bool aligned16(const void *p, long long outer_elems, long long inner_elems, int esize) {
     return ((uintptr_t)p % 16 == 0) && ((outer_elems * esize) % 16 == 0) &&
            ((inner_elems * esize) % 16 == 0);
@@ -494,6 +507,11 @@ hipError_t sp_launch_ship_encode(const SpPlan &P, const int *order, const void *
                                  int n_outer, int n_inner, hipStream_t s) {
     if (n_outer <= 0 || n_inner <= 0) return hipSuccess;
     const int esize = dtype == SP_DT_F16 ? 2 : 4;
+    if (!P.skip_transform && (order == nullptr || P.order_default) && !getenv_lane_off()) {
+        const hipError_t e = sp_launch_ship_encode_lane(P, order != nullptr, src, dtype, so, si, dst, dout,
+                                                        n_outer, n_inner, s);
+        if (e != hipErrorNotSupported) return e;
+    }
     if (fast_eligible(P, si, dtype) && aligned16(src, so, si, esize)) {
         if (dtype == SP_DT_F16)
             return launch_encode_fast<SP_DT_F16>(P, order, src, so, si, dst, dout, n_outer, n_inner, s);
@@ -514,6 +532,11 @@ hipError_t sp_launch_ship_decode(const SpPlan &P, const int *order, const unsign
                                  int n_outer, int n_inner, hipStream_t s) {
     if (n_outer <= 0 || n_inner <= 0) return hipSuccess;
     const int esize = dtype == SP_DT_F16 ? 2 : 4;
+    if (!P.skip_transform && (order == nullptr || P.order_default) && !getenv_lane_off()) {
+        const hipError_t e = sp_launch_ship_decode_lane(P, order != nullptr, src, so, dst, dtype, dout, din,
+                                                        n_outer, n_inner, s);
+        if (e != hipErrorNotSupported) return e;
+    }
     if (fast_eligible(P, din, dtype) && aligned16(dst, dout, din, esize)) {
         if (dtype == SP_DT_F16)
             return launch_decode_fast<SP_DT_F16>(P, order, src, so, dst, dout, din, n_outer, n_inner, s);
