@@ -22,6 +22,7 @@
 #define ATT_CHUNK 256
 #define ATT_MAX_G 8
 #define ATT_MAX_HD 256
+#define ATT_MAX_SPLITS 4096  // combine weights in LDS: n_kv <= 1M positions
 
 __global__ void __launch_bounds__(64)
 k_attn_prep(const SpPlan KP, const int *__restrict__ order, const float *__restrict__ q, int hd,
@@ -150,28 +151,80 @@ k_attn_split(const SpPlan KP, const SpPlan VP, const SpAttnArgs A, const float *
     }
 }
 
-__global__ void __launch_bounds__(64)
+// Merge the split partials of one query head: M = max_s m_s, e_s = exp(m_s - M),
+// L = sum_s l_s e_s, o~ = sum_s e_s o~_s / L, then one inverse VHT2.
+// 1024 threads: thread (i, g) sums element i over splits g, g + ng, ...; its
+// first 16 partial values are loaded before the weights are formed, so a
+// typical combine costs one round trip to memory. n_splits <= ATT_MAX_SPLITS.
+#define COMB_THREADS 1024
+#define COMB_PRE 16
+__device__ __forceinline__ float comb_block_reduce(float v, float *red, bool is_max) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const float o = __shfl_xor(v, m, 64);
+        v = is_max ? fmaxf(v, o) : v + o;
+    }
+    __syncthreads();  // red may still be read by a previous reduction
+    if (lane == 0) red[w] = v;
+    __syncthreads();
+    float r = red[0];
+    for (int k = 1; k < COMB_THREADS / 64; k++) r = is_max ? fmaxf(r, red[k]) : r + red[k];
+    return r;
+}
+
+__global__ void __launch_bounds__(COMB_THREADS)
 k_attn_combine(const SpPlan VP, const float *__restrict__ ws, int n_splits, int hd,
                float *__restrict__ out) {
+    __shared__ float e_s[ATT_MAX_SPLITS];
+    __shared__ float red[COMB_THREADS];
     __shared__ float c[ATT_MAX_HD];
-    const int h = blockIdx.x, lane = threadIdx.x;
-    const float *base = ws + (long long)h * n_splits * (hd + 2);
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const long long row = hd + 2;
+    const float *base = ws + (long long)h * n_splits * row;
+    const int ng = COMB_THREADS / hd;  // element groups (>= 4 for hd <= 256)
+    const int i = tid % hd, g = tid / hd;
+    const bool active = g < ng;
+    float pre[COMB_PRE];
+#pragma unroll
+    for (int r = 0; r < COMB_PRE; r++) {
+        const int sp = g + ng * r;
+        pre[r] = (active && sp < n_splits) ? base[sp * row + 2 + i] : 0.0f;
+    }
     float M = -INFINITY;
-    for (int s = 0; s < n_splits; s++) M = fmaxf(M, base[(long long)s * (hd + 2)]);
+    for (int sp = tid; sp < n_splits; sp += COMB_THREADS) M = fmaxf(M, base[sp * row]);
+    M = comb_block_reduce(M, red, true);
     float L = 0.0f;
-    for (int s = 0; s < n_splits; s++) L += base[(long long)s * (hd + 2) + 1] * __expf(base[(long long)s * (hd + 2)] - M);
+    for (int sp = tid; sp < n_splits; sp += COMB_THREADS) {
+        const float e = __expf(base[sp * row] - M);
+        e_s[sp] = e;
+        L += base[sp * row + 1] * e;
+    }
+    L = comb_block_reduce(L, red, false);  // its barriers also publish e_s
     const float invL = 1.0f / L;
-    for (int i = lane; i < hd; i += SP_WAVE) {
-        float acc = 0.0f;
-        for (int s = 0; s < n_splits; s++) {
-            const float *p = base + (long long)s * (hd + 2);
-            acc = fmaf(p[2 + i], __expf(p[0] - M), acc);
+    float acc = 0.0f;
+    if (active) {
+#pragma unroll
+        for (int r = 0; r < COMB_PRE; r++) {
+            const int sp = g + ng * r;
+            if (sp < n_splits) acc = fmaf(pre[r], e_s[sp], acc);
         }
-        c[i] = acc * invL;
+#pragma unroll 8
+        for (int sp = g + ng * COMB_PRE; sp < n_splits; sp += ng) acc = fmaf(base[sp * row + 2 + i], e_s[sp], acc);
     }
     __syncthreads();
-    sp_transform_lds(c, hd, VP, lane);
-    for (int i = lane; i < hd; i += SP_WAVE) out[(long long)h * hd + i] = c[i];
+    red[tid] = acc;
+    __syncthreads();
+    if (tid < hd) {
+        float t = 0.0f;
+        for (int k = 0; k < ng; k++) t += red[k * hd + tid];
+        c[tid] = t * invL;
+    }
+    __syncthreads();
+    // every thread reaches the transform's barriers; only wave 0 does its work
+    sp_transform_lds(c, hd, VP, tid < SP_WAVE ? tid : hd);
+    if (tid < SP_WAVE)
+        for (int k = tid; k < hd; k += SP_WAVE) out[(long long)h * hd + k] = c[k];
 }
 
 size_t sp_attn_workspace_floats(int n_q, int hd, int max_kv) {
@@ -186,15 +239,23 @@ hipError_t sp_launch_attn_decode(const SpPlan &KP, const SpPlan &VP, const int *
     if (A.n_q / A.n_kvh > ATT_MAX_G || A.hd > ATT_MAX_HD) return hipErrorInvalidValue;
     if (sp_attn_workspace_floats(A.n_q, A.hd, A.n_kv) > ws_floats) return hipErrorInvalidValue;
     const int n_splits = (A.n_kv + ATT_CHUNK - 1) / ATT_CHUNK;
+    if (n_splits > ATT_MAX_SPLITS) return hipErrorInvalidValue;
     float *qt = workspace;
     float *part = workspace + (size_t)A.n_q * A.hd;
+    const int want_out = A.out != nullptr;
+    const hipError_t me = sp_launch_attn_mfma_split(KP, VP, order, A, part, n_splits, s);
+    if (me == hipSuccess) {
+        if (want_out)
+            hipLaunchKernelGGL(k_attn_combine, dim3(A.n_q), dim3(COMB_THREADS), 0, s, VP, part, n_splits, A.hd, A.out);
+        return hipGetLastError();
+    }
+    if (me != hipErrorNotSupported) return me;
     hipLaunchKernelGGL(k_attn_prep, dim3(A.n_q), dim3(64), 0, s, KP, order, A.q, A.hd, A.kq_scale, qt);
     const size_t lds = (size_t)((ATT_CHUNK * A.kB + 8 + 15) & ~15) + (size_t)ATT_CHUNK * A.vB + 8;
-    const int want_out = A.out != nullptr;
     hipLaunchKernelGGL(k_attn_split, dim3(A.n_kvh, n_splits), dim3(256), lds, s, KP, VP, A, qt, part,
                        n_splits, want_out);
     if (want_out)
-        hipLaunchKernelGGL(k_attn_combine, dim3(A.n_q), dim3(64), 0, s, VP, part, n_splits, A.hd, A.out);
+        hipLaunchKernelGGL(k_attn_combine, dim3(A.n_q), dim3(COMB_THREADS), 0, s, VP, part, n_splits, A.hd, A.out);
     return hipGetLastError();
 }
 

@@ -204,6 +204,8 @@ hipError_t sp_launch_hier_decode(const SpPlan &P, const SpHierGeo &G, const unsi
                                  int n_outer, int n_inner, hipStream_t s);
 
 // Fused decode attention (sp_attn.hip).
+#define SP_CACHE_SLACK 256  // bytes allocated past the last record of a packed ship cache
+
 struct SpAttnArgs {
     const unsigned char *kpack;  // layer base: [n_kvh][max_seq][kB]
     const unsigned char *vpack;
@@ -219,6 +221,10 @@ hipError_t sp_launch_attn_decode(const SpPlan &KP, const SpPlan &VP, const int *
                                  const SpAttnArgs &A, float *workspace, size_t ws_floats,
                                  hipStream_t s);
 size_t sp_attn_workspace_floats(int n_q, int hd, int max_kv);
+// Split kernel on the matrix cores for head_dim 128 with K 5/5/4/3 and V 3-bit;
+// hipErrorNotSupported for any other layout.
+hipError_t sp_launch_attn_mfma_split(const SpPlan &KP, const SpPlan &VP, const int *order,
+                                     const SpAttnArgs &A, float *part, int n_splits, hipStream_t s);
 hipError_t sp_launch_attn_f16(const unsigned short *k, const unsigned short *v,
                               long long head_stride, int n_kv, int n_q, int n_kvh, int hd,
                               float kq_scale, const float *q, float *scores, float *out,

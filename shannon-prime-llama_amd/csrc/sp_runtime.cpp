@@ -441,10 +441,12 @@ extern "C" int sp_hip_cache_init(sp_hip_cache_t *cc, const sp_config_t *cfg, int
     const size_t n_slots = (size_t)cfg->n_layers * cfg->n_heads_kv;
     const size_t kb = n_slots * max_seq_len * cc->k_bands.total_bytes;
     const size_t vb = n_slots * max_seq_len * cc->v_bands.total_bytes;
-    bool ok = hip_ok(hipMalloc(&cc->d_k_cache, kb), "hipMalloc K cache") &&
-              hip_ok(hipMalloc(&cc->d_v_cache, vb), "hipMalloc V cache") &&
-              hip_ok(hipMemsetAsync(cc->d_k_cache, 0, kb, (hipStream_t)stream), "memset K") &&
-              hip_ok(hipMemsetAsync(cc->d_v_cache, 0, vb, (hipStream_t)stream), "memset V");
+    // SP_CACHE_SLACK bytes after the last record let tile loaders read whole
+    // dwords past a record boundary without leaving the allocation.
+    bool ok = hip_ok(hipMalloc(&cc->d_k_cache, kb + SP_CACHE_SLACK), "hipMalloc K cache") &&
+              hip_ok(hipMalloc(&cc->d_v_cache, vb + SP_CACHE_SLACK), "hipMalloc V cache") &&
+              hip_ok(hipMemsetAsync(cc->d_k_cache, 0, kb + SP_CACHE_SLACK, (hipStream_t)stream), "memset K") &&
+              hip_ok(hipMemsetAsync(cc->d_v_cache, 0, vb + SP_CACHE_SLACK, (hipStream_t)stream), "memset V");
     if (ok && cfg->use_mobius_mask) {
         std::vector<int> order(hd), inv(hd);
         build_mobius_order(hd, order.data());

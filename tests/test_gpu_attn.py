@@ -27,15 +27,27 @@ def rel_close(got, ref, tol=1e-3):
     assert err <= tol * scale, (err, scale)
 
 
-@pytest.mark.parametrize("n_q,H,n_ctx,hd,mob", [
-    (8, 2, 300, 128, True),      # GQA 4, a partial second split
+ATTN_CASES = [
+    (8, 2, 300, 128, True),      # GQA 4, a partial second split, odd max_seq (V tiles 2-byte aligned)
     (32, 8, 1024, 128, True),    # Llama-3-8B head layout
     (4, 4, 256, 128, False),     # MHA, exactly one split, no Mobius
-    (16, 8, 777, 256, True),     # Gemma-3 head_dim
-    (8, 8, 129, 64, True),
-])
-def test_fused_attention_matches_oracle(n_q, H, n_ctx, hd, mob):
-    say(f"attn n_q={n_q} H={H} n_ctx={n_ctx} hd={hd} mob={mob}")
+    (16, 2, 4099, 128, True),    # GQA 8, 17 splits, a 3-position last tile
+    (3, 3, 1, 128, True),        # a single position
+    (16, 8, 777, 256, True),     # Gemma-3 head_dim (general kernel)
+    (8, 8, 129, 64, True),       # general kernel
+]
+
+
+@pytest.mark.parametrize("path", ["mfma", "general"])
+@pytest.mark.parametrize("n_q,H,n_ctx,hd,mob", ATTN_CASES)
+def test_fused_attention_matches_oracle(n_q, H, n_ctx, hd, mob, path, monkeypatch):
+    """hd 128 with K 5/5/4/3 and V 3-bit runs the matrix-core kernel unless
+    SP_HIP_NO_MFMA_ATTN=1 routes it to the general one; both meet 1e-3."""
+    if path == "general":
+        monkeypatch.setenv("SP_HIP_NO_MFMA_ATTN", "1")
+    elif hd != 128:
+        pytest.skip("matrix-core kernel covers head_dim 128 only")
+    say(f"attn path={path} n_q={n_q} H={H} n_ctx={n_ctx} hd={hd} mob={mob}")
     k16, v16 = W.cfg2_kv(n_heads=H, n_pos=n_ctx, hd=hd, seed=n_ctx)
     q = W.cfg2_q(n_q=n_q, hd=hd, pos=n_ctx, seed=n_ctx + 1)
     cfg = S.config(hd, 2, H, mobius=mob)
