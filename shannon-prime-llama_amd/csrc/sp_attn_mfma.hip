@@ -48,25 +48,23 @@ constexpr int KREG = KDW / 256;              // 19
 constexpr int VREG = (VDW + 1 + 255) / 256;  // 13 (one more dword when the V chunk is shifted)
 constexpr int DVT_STRIDE = 128 + 8;          // bytes per element row of the transposed V code tile (128 positions)
 constexpr int SC_STRIDE = CHUNK + 8;         // floats per head row of scores / weights
-constexpr int QS_STRIDE = HD + 4;            // floats per head row of the query transform
 constexpr float INV_SQRT_HD = 0.08838834764831845f;
 
 // LDS layout (bytes). U holds the K records until the scores are done, then the
 // transposed V code tile of one half chunk.
 constexpr int OFF_U = 0;
-constexpr int SZ_U = CHUNK * KB + 16;                  // >= 128 * DVT_STRIDE
-constexpr int OFF_KS = SZ_U;                           // ks[4][CHUNK]: K band scales
-constexpr int OFF_SC = OFF_KS + 4 * CHUNK * 4;         // sc[8][SC_STRIDE]; during set-up qs[8][QS_STRIDE]
-constexpr int OFF_QB = OFF_SC + 8 * SC_STRIDE * 4;     // bop[16][128] fp16 B operand, cb[16][4][4], fh[8]
+constexpr int SZ_U = CHUNK * KB + 16;                  // >= HD * DVT_STRIDE (V code tile of a half chunk)
+constexpr int OFF_KS = SZ_U;                           // ks[CHUNK][4]: K band scales
+constexpr int OFF_SC = OFF_KS + 4 * CHUNK * 4;         // sc[8][SC_STRIDE]
+constexpr int OFF_QB = OFF_SC + 8 * SC_STRIDE * 4;     // qop[16][128] fp16 query operand, cb[4][16], fu[8]
 constexpr int OFF_CB = OFF_QB + 16 * HD * 2;
-constexpr int OFF_FH = OFF_CB + 16 * 4 * 4 * 4;
-constexpr int OFF_VS = OFF_FH + 8 * 4;                 // vs[CHUNK]: V scales
+constexpr int OFF_FH = OFF_CB + 4 * 16 * 4;
+constexpr int OFF_VS = OFF_FH + 16 * 4;                // vs[CHUNK]: V scales
 constexpr int OFF_VREC = OFF_VS + CHUNK * 4;           // V records (+ shift, + one dword)
 constexpr int OFF_ST = OFF_VREC + CHUNK * VB + 16;     // st[8][4]: per head max, sum, 1/w-scale
 constexpr int LDS_FULL = OFF_ST + 8 * 4 * 4;
 constexpr int LDS_KQ = OFF_VS;
-static_assert(SZ_U >= 128 * DVT_STRIDE, "V code tile must fit the K record area");
-static_assert(8 * QS_STRIDE <= 8 * SC_STRIDE, "query staging must fit the score area");
+static_assert(SZ_U >= HD * DVT_STRIDE, "V code tile must fit the K record area");
 static_assert(OFF_KS % 16 == 0 && OFF_SC % 16 == 0 && OFF_QB % 16 == 0 && OFF_CB % 16 == 0 && OFF_VS % 16 == 0 &&
                   OFF_VREC % 16 == 0 && OFF_ST % 16 == 0,
               "LDS regions 16-byte aligned");
@@ -117,8 +115,9 @@ __device__ __forceinline__ int code_slot(int b, int c) {
     return b == 2 ? ((((c & 3) >> 1) << 2) | ((c & 1) << 1) | (c >> 2)) : c;
 }
 
-// Eight 3-bit V codes (one per byte) -> fp16 (u - 3): bytes are spread into
-// 16-bit lanes under a 0x64 high byte (1024 + u), then 1027 is subtracted.
+// Eight 3-bit V codes (one per byte) -> fp16 (u - 3): a byte permute spreads a
+// pair under a 0x64 high byte (1024 + u, exact) and a packed subtract of 1027
+// centres it (exact).
 __device__ __forceinline__ half8_t vcodes8(uint32_t c0, uint32_t c1) {
     const _Float16 k = (_Float16)1027.0f;
     const half2_t b = {k, k};
@@ -157,213 +156,185 @@ __device__ __forceinline__ float add_xor1(float v) {
     return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));
 }
 
-// radix-2 Sylvester butterflies over every index bit of x (natural order)
-template <int N>
-__device__ __forceinline__ void hadamard_regs(float (&x)[N]) {
-#pragma unroll
-    for (int len = 1; len < N; len <<= 1)
-#pragma unroll
-        for (int i = 0; i < N; i++)
-            if ((i & len) == 0) {
-                const float u = x[i], v = x[i + len];
-                x[i] = u + v;
-                x[i + len] = u - v;
-            }
+// Value of lane (lane ^ M) for M a power of two below 64: quad permutes and a
+// row rotate via DPP, the others via swizzle / permute (no LDS memory traffic).
+template <int M>
+__device__ __forceinline__ float lane_xor(float v) {
+    const int x = __float_as_int(v);
+    int r;
+    if (M == 1) r = __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, true);        // quad_perm [1,0,3,2]
+    else if (M == 2) r = __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, true);   // quad_perm [2,3,0,1]
+    else if (M == 4) r = __builtin_amdgcn_ds_swizzle(x, 0x101F);              // xor 4 within 32 lanes
+    else if (M == 8) r = __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, true);  // row_ror:8 (xor 8 in a row of 16)
+    else if (M == 16) r = __builtin_amdgcn_ds_swizzle(x, 0x401F);             // xor 16 within 32 lanes
+    else r = __builtin_amdgcn_ds_bpermute(((int)(__lane_id() ^ 32)) << 2, x);
+    return __int_as_float(r);
 }
+
+// One Sylvester stage across lane bit M: x' = x + p (bit clear) or p - x (bit set).
+template <int M>
+__device__ __forceinline__ float lane_butterfly(float x, int lane) {
+    const float p = lane_xor<M>(x);
+    return fmaf(x, (lane & M) ? -1.0f : 1.0f, p);
+}
+
+template <int M>
+__device__ __forceinline__ float wave_max_step(float v) { return fmaxf(v, lane_xor<M>(v)); }
+template <int M>
+__device__ __forceinline__ float wave_sum_step(float v) { return v + lane_xor<M>(v); }
 
 }  // namespace
 
-// One 256-thread block per (KV head, 256-position split).
+// Records of one 256-position split into registers: dword buffer loads, out-of-
+// range dwords read as 0. A V split may start 2 bytes past a dword boundary
+// (odd max_seq): its dwords are read from 2 bytes before it and the staged
+// records start at vshift; the last dword may run 2 bytes past the last record,
+// which the packed caches' slack bytes after their last record cover.
+template <bool WANT_V>
+__device__ __forceinline__ void load_split(const SpAttnArgs &A, int kvh, int split, int vshift, int tid,
+                                           uint32_t (&kr)[KREG], uint32_t (&vr)[WANT_V ? VREG : 1]) {
+    const int c0 = split * CHUNK, n_chunk = min(CHUNK, A.n_kv - c0);
+    const unsigned char *kg = A.kpack + (long long)kvh * A.k_head_stride + (long long)c0 * KB;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void *)kg, (short)0, n_chunk * KB, BUF_WORD3);
+#pragma unroll
+    for (int i = 0; i < KREG; i++) kr[i] = __builtin_amdgcn_raw_buffer_load_b32(rk, 4 * tid, 1024 * i, BUF_NT);
+    if (WANT_V) {
+        const unsigned char *vg = A.vpack + (long long)kvh * A.v_head_stride + (long long)c0 * VB - vshift;
+        const int nbytes = (n_chunk * VB + vshift + 3) & ~3;
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void *)vg, (short)0, nbytes, BUF_WORD3);
+#pragma unroll
+        for (int i = 0; i < (WANT_V ? VREG : 1); i++)
+            vr[i] = __builtin_amdgcn_raw_buffer_load_b32(rv, 4 * tid, 1024 * i, BUF_NT);
+    }
+}
+
+// One 256-thread block per (KV head, run of `rounds` consecutive 256-position
+// splits). The query operand is prepared once per block; each round stages one
+// split's records from registers into LDS and prefetches the next split's
+// while it computes. Every split writes its own partial.
 template <bool WANT_OUT>
 __global__ void __launch_bounds__(256, WANT_OUT ? 3 : 4)
-k_attn_mfma_split(const SpAttnArgs A, const int *__restrict__ order, float *__restrict__ ws, int n_splits) {
+k_attn_mfma_split(const SpAttnArgs A, const int *__restrict__ order, float *__restrict__ ws, int n_splits,
+                  int rounds) {
     __shared__ __attribute__((aligned(16))) unsigned char smem[WANT_OUT ? LDS_FULL : LDS_KQ];
     unsigned char *krec = smem + OFF_U;
     unsigned char *dvt = smem + OFF_U;
     float *ks = reinterpret_cast<float *>(smem + OFF_KS);
     float *sc = reinterpret_cast<float *>(smem + OFF_SC);
-    float *qs = sc;  // natural-order query transform [8][QS_STRIDE] during set-up
-    unsigned short *bop = reinterpret_cast<unsigned short *>(smem + OFF_QB);  // [16 columns][128 slots] fp16
-    float *cb = reinterpret_cast<float *>(smem + OFF_CB);                       // [16 columns][4 bands][4 copies]
-    float *fh = reinterpret_cast<float *>(smem + OFF_FH);                       // [8] power-of-two query scale
+    unsigned short *bop = reinterpret_cast<unsigned short *>(smem + OFF_QB);  // [16 rows][128 slots] fp16
+    float *cb = reinterpret_cast<float *>(smem + OFF_CB);                       // [4 bands][16 rows]
+    float *fu = reinterpret_cast<float *>(smem + OFF_FH);                       // [8] inverse query scale
 
-    const int kvh = blockIdx.x, split = blockIdx.y, tid = threadIdx.x;
+    const int kvh = blockIdx.x, tid = threadIdx.x;
+    const int split0 = blockIdx.y * rounds;
     const int w = tid >> 6, lane = tid & 63, q4 = lane >> 4, c16 = lane & 15;
     const int G = A.n_q / A.n_kvh, h0 = kvh * G;
-    const int c0 = split * CHUNK;
-    const int n_chunk = min(CHUNK, A.n_kv - c0);
 
-    // ---- 1. the query (4 elements per thread) and the order entry, loaded first ----
-    float qv[4];
+    // ---- 1. wave w prepares heads w and w + 4: their query rows and the order
+    // entries of record coefficients lane and lane + 64 are loaded first ----
+    float qx[2][2];
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int idx = tid + 256 * r, h = idx >> 7;
-        qv[r] = A.q[(long long)(h0 + min(h, G - 1)) * HD + (idx & (HD - 1))];
+    for (int r = 0; r < 2; r++) {
+        const float *qg = A.q + (long long)(h0 + min(w + 4 * r, G - 1)) * HD;
+        qx[r][0] = qg[lane];
+        qx[r][1] = qg[lane + 64];
     }
-    // Without an order table, read (and ignore) an in-bounds word of q: both
-    // candidates are kernel-argument pointers, so this stays a global load (a
+    // Without an order table, read (and ignore) in-bounds words of q: both
+    // candidates are kernel-argument pointers, so these stay global loads (a
     // flat load here would make every later wait drain all loads).
     const int *op = order ? order : reinterpret_cast<const int *>(A.q);
-    const int ordv = op[tid & (HD - 1)];
-    const int ord = order ? ordv : (tid & (HD - 1));
+    const int ov0 = op[lane], ov1 = op[lane + 64];
+    const int ord0 = order ? ov0 : lane, ord1 = order ? ov1 : lane + 64;
     __asm__ volatile("" ::: "memory");  // keep the query loads ahead of the record loads
 
-    // ---- 2. the chunk's records: dword buffer loads (out-of-range dwords read as 0) ----
+    // ---- 2. the first split's records ----
+    const int vshift = WANT_OUT ? (int)((uintptr_t)(A.vpack + (long long)kvh * A.v_head_stride) & 3) : 0;
     uint32_t kr[KREG];
-    {
-        const unsigned char *kg = A.kpack + (long long)kvh * A.k_head_stride + (long long)c0 * KB;
-        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)kg, (short)0, n_chunk * KB, BUF_WORD3);
-#pragma unroll
-        for (int i = 0; i < KREG; i++) kr[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, 4 * tid, 1024 * i, BUF_NT);
-    }
-    // A V chunk may start 2 bytes past a dword boundary (odd max_seq): its dwords
-    // are read from 2 bytes before it and the staged records start at vshift. The
-    // last dword may run 2 bytes past the last record; the packed caches carry
-    // slack bytes after their last record for this.
     uint32_t vr[WANT_OUT ? VREG : 1];
-    int vshift = 0;
-    if (WANT_OUT) {
-        const unsigned char *vg = A.vpack + (long long)kvh * A.v_head_stride + (long long)c0 * VB;
-        vshift = (int)((uintptr_t)vg & 3);
-        const int nbytes = (n_chunk * VB + vshift + 3) & ~3;
-        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)(vg - vshift), (short)0, nbytes, BUF_WORD3);
-#pragma unroll
-        for (int i = 0; i < VREG; i++) vr[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, 4 * tid, 1024 * i, BUF_NT);
-    }
+    load_split<WANT_OUT>(A, kvh, split0, vshift, tid, kr, vr);
 
-    // ---- 3. q~ = kq_scale * reorder(VHT2(q)) while the records are in flight ----
+    // ---- 3. while the records are in flight: q~ = kq_scale * reorder(VHT2(q)) per
+    // head, in registers (lane holds elements lane and lane + 64), scaled by a power
+    // of two fh so its largest entry lies in [2^11, 2^12) and split into fp16 hi + lo:
+    // the query operand rows 2h (hi) and 2h + 1 (lo) in LDS, laid out so lane
+    // (c16, q4) of the score MFMA reads the 8 slots of band b as one 16-byte word
+    // at (4b + q4) * 8 (record coefficient k = 32b + 8*q4 + c). Also per (row,
+    // band) -(1024 + m_b) * sum of the row's slots: the MFMA accumulator start. ----
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int idx = tid + 256 * r, h = idx >> 7;
-        if (h < G) qs[h * QS_STRIDE + (idx & (HD - 1))] = qv[r];
+    for (int r = 0; r < 2; r++) {
+        const int h = w + 4 * r;
+        if (h >= G) break;
+        float x0 = qx[r][0], x1 = qx[r][1];
+        x0 = lane_butterfly<1>(x0, lane);   x1 = lane_butterfly<1>(x1, lane);
+        x0 = lane_butterfly<2>(x0, lane);   x1 = lane_butterfly<2>(x1, lane);
+        x0 = lane_butterfly<4>(x0, lane);   x1 = lane_butterfly<4>(x1, lane);
+        x0 = lane_butterfly<8>(x0, lane);   x1 = lane_butterfly<8>(x1, lane);
+        x0 = lane_butterfly<16>(x0, lane);  x1 = lane_butterfly<16>(x1, lane);
+        x0 = lane_butterfly<32>(x0, lane);  x1 = lane_butterfly<32>(x1, lane);
+        const float sq = A.kq_scale * INV_SQRT_HD;
+        const float y0 = (x0 + x1) * sq, y1 = (x0 - x1) * sq;  // elements lane, lane + 64
+        float amax = fmaxf(fabsf(y0), fabsf(y1));
+        amax = wave_max_step<1>(amax);
+        amax = wave_max_step<2>(amax);
+        amax = wave_max_step<4>(amax);
+        amax = wave_max_step<8>(amax);
+        amax = wave_max_step<16>(amax);
+        amax = wave_max_step<32>(amax);
+        const float f = pow2_norm(amax);
+        // record coefficients lane (bands 0, 1) and lane + 64 (bands 2, 3)
+        float va, vb;
+        {
+            const float a0 = __int_as_float(__builtin_amdgcn_ds_bpermute((ord0 & 63) << 2, __float_as_int(y0)));
+            const float a1 = __int_as_float(__builtin_amdgcn_ds_bpermute((ord0 & 63) << 2, __float_as_int(y1)));
+            const float b0 = __int_as_float(__builtin_amdgcn_ds_bpermute((ord1 & 63) << 2, __float_as_int(y0)));
+            const float b1 = __int_as_float(__builtin_amdgcn_ds_bpermute((ord1 & 63) << 2, __float_as_int(y1)));
+            va = ((ord0 & 64) ? a1 : a0) * f;
+            vb = ((ord1 & 64) ? b1 : b0) * f;
+        }
+        uint32_t ha, la, hb, lb;
+        split_hl(va, ha, la);
+        split_hl(vb, hb, lb);
+        const int ka = lane, kb = lane + 64;
+        const int ia = (4 * (ka >> 5) + ((ka >> 3) & 3)) * 8 + code_slot(ka >> 5, ka & 7);
+        const int ib = (4 * (kb >> 5) + ((kb >> 3) & 3)) * 8 + code_slot(kb >> 5, kb & 7);
+        bop[(2 * h) * HD + ia] = (unsigned short)ha;
+        bop[(2 * h + 1) * HD + ia] = (unsigned short)la;
+        bop[(2 * h) * HD + ib] = (unsigned short)hb;
+        bop[(2 * h + 1) * HD + ib] = (unsigned short)lb;
+        // band sums over each 32-lane half (band of ka: lane >> 5; of kb: 2 + (lane >> 5))
+        float sha = (float)__builtin_bit_cast(_Float16, (unsigned short)ha);
+        float sla = (float)__builtin_bit_cast(_Float16, (unsigned short)la);
+        float shb = (float)__builtin_bit_cast(_Float16, (unsigned short)hb);
+        float slb = (float)__builtin_bit_cast(_Float16, (unsigned short)lb);
+        sha = wave_sum_step<1>(sha); sla = wave_sum_step<1>(sla); shb = wave_sum_step<1>(shb); slb = wave_sum_step<1>(slb);
+        sha = wave_sum_step<2>(sha); sla = wave_sum_step<2>(sla); shb = wave_sum_step<2>(shb); slb = wave_sum_step<2>(slb);
+        sha = wave_sum_step<4>(sha); sla = wave_sum_step<4>(sla); shb = wave_sum_step<4>(shb); slb = wave_sum_step<4>(slb);
+        sha = wave_sum_step<8>(sha); sla = wave_sum_step<8>(sla); shb = wave_sum_step<8>(shb); slb = wave_sum_step<8>(slb);
+        sha = wave_sum_step<16>(sha); sla = wave_sum_step<16>(sla); shb = wave_sum_step<16>(shb); slb = wave_sum_step<16>(slb);
+        if ((lane & 31) == 0) {
+            const int ba = lane >> 5, bb = 2 + (lane >> 5);
+            const float ca = -(1024.0f + (float)((1 << (kbits(ba) - 1)) - 1));  // bands 0, 1: 5 bits
+            const float cbb = -(1024.0f + (float)((1 << (kbits(bb) - 1)) - 1));
+            cb[ba * 16 + 2 * h] = ca * sha;
+            cb[ba * 16 + 2 * h + 1] = ca * sla;
+            cb[bb * 16 + 2 * h] = cbb * shb;
+            cb[bb * 16 + 2 * h + 1] = cbb * slb;
+        }
+        if (lane == 0) fu[h] = 1.0f / f;  // exact: a power of two
     }
     __syncthreads();
-    if (tid < G * 16) {  // butterflies over element bits 4..6
-        const int h = tid >> 4, k = tid & 15;
-        float x[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) x[i] = qs[h * QS_STRIDE + k + 16 * i];
-        hadamard_regs(x);
-#pragma unroll
-        for (int i = 0; i < 8; i++) qs[h * QS_STRIDE + k + 16 * i] = x[i];
-    }
-    __syncthreads();
-    if (tid < G * 8) {  // butterflies over element bits 0..3, then the scale
-        const int h = tid >> 3, m = tid & 7;
-        float4 *row = reinterpret_cast<float4 *>(qs + h * QS_STRIDE + 16 * m);
-        float x[16];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float4 v = row[i];
-            x[4 * i] = v.x;
-            x[4 * i + 1] = v.y;
-            x[4 * i + 2] = v.z;
-            x[4 * i + 3] = v.w;
-        }
-        hadamard_regs(x);
-        const float s = A.kq_scale * INV_SQRT_HD;
-        float amax = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            x[i] *= s;
-            amax = fmaxf(amax, fabsf(x[i]));
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) row[i] = make_float4(x[4 * i], x[4 * i + 1], x[4 * i + 2], x[4 * i + 3]);
-        // the 8 threads of a head are 8 aligned lanes of one wave
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
-        if (m == 0) fh[h] = pow2_norm(amax);
-    }
-    __syncthreads();
-    // B operand in LDS: column 2h + part (0: hi, 1: lo) of q~ * fh[h] in record
-    // order, laid out so lane (c16, q4) reads the 8 slots of band b as one
-    // 16-byte word at (4b + q4) * 8. Record coefficient kr = 32b + 8*q4 + c.
-    {
-        const int kr = tid & (HD - 1), b = kr >> 5, lq = (kr >> 3) & 3;
-        const int idx = (4 * b + lq) * 8 + code_slot(b, kr & 7);
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int h = (tid >> 7) + 2 * r;
-            if (h < G) {
-                uint32_t hi, lo;
-                split_hl(qs[h * QS_STRIDE + ord] * fh[h], hi, lo);
-                bop[(2 * h) * HD + idx] = (unsigned short)hi;
-                bop[(2 * h + 1) * HD + idx] = (unsigned short)lo;
-            }
-        }
-    }
-    // records -> LDS
-#pragma unroll
-    for (int i = 0; i < KREG; i++) reinterpret_cast<uint32_t *>(krec)[tid + 256 * i] = kr[i];
-    if (WANT_OUT) {
-        unsigned char *vrec = smem + OFF_VREC;
-#pragma unroll
-        for (int i = 0; i < VREG; i++) {
-            const int k = tid + 256 * i;
-            if (k <= VDW) reinterpret_cast<uint32_t *>(vrec)[k] = vr[i];
-        }
-    }
-    __syncthreads();
-
-    // ---- 4. per (column, band): (1024 + m_b) * sum of the column's slots; per-position scales ----
-    if (tid < 64) {
-        const int col = tid >> 2, b = tid & 3;
-        if ((col >> 1) < G) {
-            float tp[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const half8_t v = __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4 *>(bop + col * HD + 32 * b + 8 * i));
-#pragma unroll
-                for (int e = 0; e < 8; e++) tp[e & 3] += (float)v[e];
-            }
-            const float t = (tp[0] + tp[1]) + (tp[2] + tp[3]);
-            // minus, four copies: read back as an MFMA accumulator start
-            const float c = -(1024.0f + (float)((1 << (kbits(b) - 1)) - 1)) * t;
-            *reinterpret_cast<float4 *>(cb + (col * 4 + b) * 4) = make_float4(c, c, c, c);
-        }
-    }
-    {
-        const unsigned char *r = krec + tid * KB;
-        const bool live = tid < n_chunk;
-#pragma unroll
-        for (int b = 0; b < 4; b++)
-            ks[b * CHUNK + tid] = live ? scale_of(*reinterpret_cast<const unsigned short *>(r + kbyte(b))) : 0.0f;
-        if (WANT_OUT) {
-            const unsigned char *v = smem + OFF_VREC + vshift + tid * VB;
-            reinterpret_cast<float *>(smem + OFF_VS)[tid] = live ? scale_of(*reinterpret_cast<const unsigned short *>(v)) : 0.0f;
-            if (tid < 8) {
-                float *st = reinterpret_cast<float *>(smem + OFF_ST);
-                st[4 * tid] = -INFINITY;
-                st[4 * tid + 1] = 0.0f;
-                st[4 * tid + 2] = 1.0f;
-            }
-        }
-    }
-    __syncthreads();
-
-    // ---- 5. B operand, accumulator start and unscale of this lane's column c16 = 2h + part ----
-    half8_t bq[4];
+    // query operand of row c16 = 2h + part; accumulator start of rows 4*q4 + j
+    // (rows of heads >= G hold whatever the LDS holds and are never stored)
+    half8_t qop[4];
     float4_t cinit[4];
-    float q_unscale = 1.0f;
-    {
-        const int h = c16 >> 1;
-        const bool live = h < G;
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
-            const u32x4 v = live ? *reinterpret_cast<const u32x4 *>(bop + c16 * HD + (4 * b + q4) * 8) : u32x4{0u, 0u, 0u, 0u};
-            bq[b] = __builtin_bit_cast(half8_t, v);
-        }
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-            const float4 c4 = live ? *reinterpret_cast<const float4 *>(cb + (c16 * 4 + b) * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-            cinit[b] = float4_t{c4.x, c4.y, c4.z, c4.w};
-        }
-        if (live) q_unscale = 1.0f / fh[h];  // exact: a power of two
+    for (int b = 0; b < 4; b++) {
+        qop[b] = __builtin_bit_cast(half8_t, *reinterpret_cast<const u32x4 *>(bop + c16 * HD + (4 * b + q4) * 8));
+        const float4 c4 = *reinterpret_cast<const float4 *>(cb + b * 16 + 4 * q4);
+        cinit[b] = float4_t{c4.x, c4.y, c4.z, c4.w};
     }
-
-    // ---- 6. scores: wave w owns positions [64w, 64w + 64) as four 16-row tiles ----
+    const int hq0 = 2 * q4, hq1 = 2 * q4 + 1;  // heads of this lane's D rows (j = 0,1 and 2,3)
+    const float un0 = fu[hq0], un1 = fu[hq1];
     int wofs[4], wsh[4];
 #pragma unroll
     for (int b = 0; b < 4; b++) {
@@ -371,167 +342,214 @@ k_attn_mfma_split(const SpAttnArgs A, const int *__restrict__ order, float *__re
         wofs[b] = 4 * (p >> 5);
         wsh[b] = p & 31;
     }
-    const bool vec_store = A.scores && ((A.n_kv & 3) == 0);
     // code-slot masks and the fp16 1024 bits, kept in registers for bitop3
     const uint32_t kbias = __builtin_amdgcn_readfirstlane(0x64006400u);
     uint32_t kmask5 = 0x001f001fu, kmask4 = 0x000f000fu, kmask3 = 0x00070007u;
     __asm__("" : "+v"(kmask5), "+v"(kmask4), "+v"(kmask3));
+
+    for (int round = 0; round < rounds; round++) {
+        const int split = split0 + round;
+        if (split >= n_splits) break;
+        const int c0 = split * CHUNK;
+        const int n_chunk = min(CHUNK, A.n_kv - c0);
+        if (round > 0) __syncthreads();  // the previous round is done with the LDS
+        // ---- stage this split's records; prefetch the next split's ----
 #pragma unroll
-    for (int sub = 0; sub < 4; sub++) {
-        const int tb = 64 * w + 16 * sub;
-        const unsigned char *rec = krec + (tb + c16) * KB;  // A row = position tb + c16
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < KREG; i++) reinterpret_cast<uint32_t *>(krec)[tid + 256 * i] = kr[i];
+        if (WANT_OUT) {
+            unsigned char *vrec = smem + OFF_VREC;
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
-            const uint32_t d0 = *reinterpret_cast<const uint32_t *>(rec + wofs[b]);
-            const uint32_t d1 = *reinterpret_cast<const uint32_t *>(rec + wofs[b] + 4);
-            half8_t a;
-            if (b < 2) a = band_codes<5>(d0, d1, wsh[b], kmask5, kbias);
-            else if (b == 2) a = band_codes<4>(d0, d1, wsh[b], kmask4, kbias);
-            else a = band_codes<3>(d0, d1, wsh[b], kmask3, kbias);
-            const float4_t d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[b], cinit[b], 0, 0, 0);
-            // D rows 4*q4 + j (positions), column c16
-            const float4 s4 = *reinterpret_cast<const float4 *>(ks + b * CHUNK + tb + 4 * q4);
-            acc[0] = fmaf(s4.x, d[0], acc[0]);
-            acc[1] = fmaf(s4.y, d[1], acc[1]);
-            acc[2] = fmaf(s4.z, d[2], acc[2]);
-            acc[3] = fmaf(s4.w, d[3], acc[3]);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[j] = add_xor1(acc[j]) * q_unscale;  // hi + lo columns
-        const int h = c16 >> 1;
-        if ((c16 & 1) == 0 && h < G) {
-            const int t = tb + 4 * q4;
-            if (WANT_OUT) *reinterpret_cast<float4 *>(sc + h * SC_STRIDE + t) = make_float4(acc[0], acc[1], acc[2], acc[3]);
-            if (A.scores) {
-                float *dst = A.scores + (long long)(h0 + h) * A.n_kv + c0 + t;
-                if (vec_store && t + 3 < n_chunk) {
-                    *reinterpret_cast<float4 *>(dst) = make_float4(acc[0], acc[1], acc[2], acc[3]);
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        if (t + j < n_chunk) dst[j] = acc[j];
-                }
+            for (int i = 0; i < (WANT_OUT ? VREG : 1); i++) {
+                const int k = tid + 256 * i;
+                if (k <= VDW) reinterpret_cast<uint32_t *>(vrec)[k] = vr[i];
             }
         }
-    }
-    if (!WANT_OUT) return;
-    __syncthreads();
-
-    float *vs = reinterpret_cast<float *>(smem + OFF_VS);
-    float *st = reinterpret_cast<float *>(smem + OFF_ST);
-    // ---- 7. softmax over the chunk (wave w: heads w, w + 4); sc <- scaled w = p * scale_v ----
-    for (int h = w; h < G; h += 4) {
-        float sv[4];
-        float m = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int t = lane + 64 * i;
-            sv[i] = t < n_chunk ? sc[h * SC_STRIDE + t] : -INFINITY;
-            m = fmaxf(m, sv[i]);
-        }
-        m = sp_wave_max(m);
-        float l = 0.0f, wm = 0.0f, wv[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int t = lane + 64 * i;
-            const float p = t < n_chunk ? __expf(sv[i] - m) : 0.0f;
-            wv[i] = p * vs[t];
-            l += p;
-            wm = fmaxf(wm, wv[i]);
-        }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            l += __shfl_xor(l, o, 64);
-            wm = fmaxf(wm, __shfl_xor(wm, o, 64));
-        }
-        const float f = pow2_norm(wm);
-#pragma unroll
-        for (int i = 0; i < 4; i++) sc[h * SC_STRIDE + lane + 64 * i] = wv[i] * f;
-        if (lane == 0) {
-            st[4 * h] = m;
-            st[4 * h + 1] = l;
-            st[4 * h + 2] = 1.0f / f;
-        }
-    }
-
-    // ---- 8. values, in two halves of 128 positions:
-    // D[(h, part)][i] = sum_t w_part[h][t] * (u[t][i] - 3) ----
-    float4_t d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
-    const unsigned char *vrecs = smem + OFF_VREC + vshift;
-    const int hrow = c16 >> 1, part = c16 & 1;  // A row = c16
-    const bool live = hrow < G;
-    const int n0 = 32 * w + c16;
-#pragma unroll
-    for (int half = 0; half < 2; half++) {
-        __syncthreads();  // K records (first half) or the previous V tile are no longer read
+        if (round + 1 < rounds && split + 1 < n_splits) load_split<WANT_OUT>(A, kvh, split + 1, vshift, tid, kr, vr);
+        __syncthreads();
+        // ---- per-position scales ----
         {
-            // thread: elements 16g .. 16g+15 (48 bits at byte 2 + 6g) of positions 4pq .. 4pq+3
-            const int g = tid & 7, pq = tid >> 3;
-            unsigned long long bits[4];
+            const unsigned char *r = krec + tid * KB;
+            const bool live = tid < n_chunk;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const unsigned short *p = reinterpret_cast<const unsigned short *>(
-                    vrecs + (128 * half + 4 * pq + i) * VB + 2 + 6 * g);
-                bits[i] = (unsigned long long)p[0] | ((unsigned long long)p[1] << 16) | ((unsigned long long)p[2] << 32);
-            }
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const uint32_t u0 = (uint32_t)(bits[0] >> (3 * e)) & 7u, u1 = (uint32_t)(bits[1] >> (3 * e)) & 7u;
-                const uint32_t u2 = (uint32_t)(bits[2] >> (3 * e)) & 7u, u3 = (uint32_t)(bits[3] >> (3 * e)) & 7u;
-                *reinterpret_cast<uint32_t *>(dvt + (16 * g + e) * DVT_STRIDE + 4 * pq) =
-                    u0 | (u1 << 8) | (u2 << 16) | (u3 << 24);
+            for (int b = 0; b < 4; b++)
+                ks[tid * 4 + b] = live ? scale_of(*reinterpret_cast<const unsigned short *>(r + kbyte(b))) : 0.0f;
+            if (WANT_OUT) {
+                const unsigned char *v = smem + OFF_VREC + vshift + tid * VB;
+                reinterpret_cast<float *>(smem + OFF_VS)[tid] = live ? scale_of(*reinterpret_cast<const unsigned short *>(v)) : 0.0f;
             }
         }
         __syncthreads();
+
+        // ---- scores: wave w owns positions [64w, 64w + 64) as four 16-column tiles;
+        // D[row (h, part)][position]: lane (c16, q4) holds position tb + c16, rows 4*q4 + j ----
 #pragma unroll
-        for (int kk = 0; kk < 4; kk++) {
-            const int tb = 32 * kk + 8 * q4;  // A row c16, k-slots 8*q4 + e: positions tb + e
-            uint32_t wd[4];
-            {
-                float wv[8];
-                if (live) {
-                    const float4 x = *reinterpret_cast<const float4 *>(sc + hrow * SC_STRIDE + 128 * half + tb);
-                    const float4 y = *reinterpret_cast<const float4 *>(sc + hrow * SC_STRIDE + 128 * half + tb + 4);
-                    wv[0] = x.x; wv[1] = x.y; wv[2] = x.z; wv[3] = x.w;
-                    wv[4] = y.x; wv[5] = y.y; wv[6] = y.z; wv[7] = y.w;
-                } else {
+        for (int sub = 0; sub < 4; sub++) {
+            const int t = 64 * w + 16 * sub + c16;  // this lane's position (column)
+            const unsigned char *rec = krec + t * KB;
+            const float4 s4 = *reinterpret_cast<const float4 *>(ks + 4 * t);
+            const float sb[4] = {s4.x, s4.y, s4.z, s4.w};
+            float acc0 = 0.0f, acc1 = 0.0f;
 #pragma unroll
-                    for (int e = 0; e < 8; e++) wv[e] = 0.0f;
-                }
-                uint32_t h16[8];
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    uint32_t hi, lo;
-                    split_hl(wv[e], hi, lo);
-                    h16[e] = part ? lo : hi;
-                }
-#pragma unroll
-                for (int e = 0; e < 4; e++) wd[e] = h16[2 * e] | (h16[2 * e + 1] << 16);
+            for (int b = 0; b < 4; b++) {
+                const uint32_t d0 = *reinterpret_cast<const uint32_t *>(rec + wofs[b]);
+                const uint32_t d1 = *reinterpret_cast<const uint32_t *>(rec + wofs[b] + 4);
+                half8_t code;
+                if (b < 2) code = band_codes<5>(d0, d1, wsh[b], kmask5, kbias);
+                else if (b == 2) code = band_codes<4>(d0, d1, wsh[b], kmask4, kbias);
+                else code = band_codes<3>(d0, d1, wsh[b], kmask3, kbias);
+                const float4_t d = __builtin_amdgcn_mfma_f32_16x16x32_f16(qop[b], code, cinit[b], 0, 0, 0);
+                acc0 = fmaf(sb[b], d[0] + d[1], acc0);  // hi + lo rows of head hq0
+                acc1 = fmaf(sb[b], d[2] + d[3], acc1);
             }
-            const half8_t a = as_half8(wd[0], wd[1], wd[2], wd[3]);
-            const u32x2 v0 = *reinterpret_cast<const u32x2 *>(dvt + n0 * DVT_STRIDE + tb);
-            const u32x2 v1 = *reinterpret_cast<const u32x2 *>(dvt + (n0 + 16) * DVT_STRIDE + tb);
-            d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, vcodes8(v0[0], v0[1]), d0, 0, 0, 0);
-            d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, vcodes8(v1[0], v1[1]), d1, 0, 0, 0);
+            acc0 *= un0;
+            acc1 *= un1;
+            if (t < n_chunk) {
+                if (hq0 < G) {
+                    if (WANT_OUT) sc[hq0 * SC_STRIDE + t] = acc0;
+                    if (A.scores) A.scores[(long long)(h0 + hq0) * A.n_kv + c0 + t] = acc0;
+                }
+                if (hq1 < G) {
+                    if (WANT_OUT) sc[hq1 * SC_STRIDE + t] = acc1;
+                    if (A.scores) A.scores[(long long)(h0 + hq1) * A.n_kv + c0 + t] = acc1;
+                }
+            }
         }
-    }
-    // ---- 9. partials: D rows 4*q4 + j are head 2*q4 + (j >> 1), part j & 1 ----
+        if (!WANT_OUT) continue;
+        __syncthreads();
+
+        float *vs = reinterpret_cast<float *>(smem + OFF_VS);
+        float *st = reinterpret_cast<float *>(smem + OFF_ST);
+        // ---- softmax over the split (wave w: heads w, w + 4); sc <- scaled w = p * scale_v ----
+        for (int h = w; h < G; h += 4) {
+            float sv[4];
+            float m = -INFINITY;
 #pragma unroll
-    for (int hh = 0; hh < 2; hh++) {
-        const int h = 2 * q4 + hh;
-        if (h < G) {
-            const float un = st[4 * h + 2];
-            float *dst = ws + ((long long)(h0 + h) * n_splits + split) * (HD + 2) + 2;
-            dst[32 * w + c16] = (d0[2 * hh] + d0[2 * hh + 1]) * un;
-            dst[32 * w + 16 + c16] = (d1[2 * hh] + d1[2 * hh + 1]) * un;
+            for (int i = 0; i < 4; i++) {
+                const int t = lane + 64 * i;
+                sv[i] = t < n_chunk ? sc[h * SC_STRIDE + t] : -INFINITY;
+                m = fmaxf(m, sv[i]);
+            }
+            m = sp_wave_max(m);
+            float l = 0.0f, wm = 0.0f, wv[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int t = lane + 64 * i;
+                const float p = t < n_chunk ? __expf(sv[i] - m) : 0.0f;
+                wv[i] = p * vs[t];
+                l += p;
+                wm = fmaxf(wm, wv[i]);
+            }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) {
+                l += __shfl_xor(l, o, 64);
+                wm = fmaxf(wm, __shfl_xor(wm, o, 64));
+            }
+            const float f = pow2_norm(wm);
+            // the value MFMA's A operand rows 2h (hi) and 2h + 1 (lo), fp16, written over
+            // this head's score row (all of which this wave has already read)
+            unsigned short *wrow = reinterpret_cast<unsigned short *>(sc + h * SC_STRIDE);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                // lo part scaled by 2^11 (exact) so it stays a normal fp16 value
+                const float v = wv[i] * f;
+                const _Float16 hh = (_Float16)v;
+                const uint32_t hi = (uint32_t)__builtin_bit_cast(unsigned short, hh);
+                const uint32_t lo = (uint32_t)__builtin_bit_cast(unsigned short, (_Float16)((v - (float)hh) * 2048.0f));
+                wrow[lane + 64 * i] = (unsigned short)hi;
+                wrow[CHUNK + lane + 64 * i] = (unsigned short)lo;
+            }
+            if (lane == 0) {
+                st[4 * h] = m;
+                st[4 * h + 1] = l;
+                st[4 * h + 2] = 1.0f / f;
+            }
+        }
+
+        // ---- values, in two halves of 128 positions:
+        // D[(h, part)][i] = sum_t w_part[h][t] * (u[t][i] - 3) ----
+        __syncthreads();  // st complete; K records no longer read
+        float4_t d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
+        const unsigned char *vrecs = smem + OFF_VREC + vshift;
+        const int hrow = c16 >> 1, part = c16 & 1;  // A row = c16 (rows of heads >= G are never stored)
+        const int n0 = 32 * w + c16;
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+            if (half) __syncthreads();  // the previous V tile is no longer read
+            {
+                // thread: elements 16g .. 16g+15 (48 bits at byte 2 + 6g) of positions
+                // 4pq .. 4pq+3 (a, b, c, d) -> dvt[element][position] bytes. Per group of
+                // four elements, two positions' 12-bit chunks share a dword (16 bits
+                // apart), so one shift and mask yields both positions' codes of an
+                // element and a byte permute lines up all four positions.
+                const int g = tid & 7, pq = tid >> 3;
+                uint32_t lo[4], hi[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const unsigned short *p = reinterpret_cast<const unsigned short *>(
+                        vrecs + (128 * half + 4 * pq + i) * VB + 2 + 6 * g);
+                    lo[i] = (uint32_t)p[0] | ((uint32_t)p[1] << 16);
+                    hi[i] = p[2];
+                }
+#pragma unroll
+                for (int sg = 0; sg < 4; sg++) {
+                    uint32_t c[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        c[i] = sg < 2 ? __builtin_amdgcn_ubfe(lo[i], 12 * sg, 12)
+                                      : (sg == 2 ? (__builtin_amdgcn_alignbit(hi[i], lo[i], 24) & 0xfffu)
+                                                 : __builtin_amdgcn_ubfe(hi[i], 4, 12));
+                    const uint32_t wab = c[0] | (c[1] << 16), wcd = c[2] | (c[3] << 16);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const uint32_t x = (wab >> (3 * e)) & 0x00070007u, y = (wcd >> (3 * e)) & 0x00070007u;
+                        *reinterpret_cast<uint32_t *>(dvt + (16 * g + 4 * sg + e) * DVT_STRIDE + 4 * pq) =
+                            __builtin_amdgcn_perm(y, x, 0x06040200u);
+                    }
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                const int tb = 32 * kk + 8 * q4;  // A row c16, k-slots 8*q4 + e: positions tb + e
+                const half8_t a = __builtin_bit_cast(
+                    half8_t, *reinterpret_cast<const u32x4 *>(reinterpret_cast<const unsigned short *>(sc + hrow * SC_STRIDE) +
+                                                              part * CHUNK + 128 * half + tb));
+                const u32x2 v0 = *reinterpret_cast<const u32x2 *>(dvt + n0 * DVT_STRIDE + tb);
+                const u32x2 v1 = *reinterpret_cast<const u32x2 *>(dvt + (n0 + 16) * DVT_STRIDE + tb);
+                d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, vcodes8(v0[0], v0[1]), d0, 0, 0, 0);
+                d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, vcodes8(v1[0], v1[1]), d1, 0, 0, 0);
+            }
+        }
+        // ---- partial of this split: D rows 4*q4 + j are head 2*q4 + (j >> 1), part j & 1 ----
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const int h = 2 * q4 + hh;
+            if (h < G) {
+                const float un = st[4 * h + 2];  // 1/w-scale
+                float *dst = ws + ((long long)(h0 + h) * n_splits + split) * (HD + 2) + 2;
+                dst[32 * w + c16] = fmaf(d0[2 * hh + 1], 1.0f / 2048.0f, d0[2 * hh]) * un;
+                dst[32 * w + 16 + c16] = fmaf(d1[2 * hh + 1], 1.0f / 2048.0f, d1[2 * hh]) * un;
+            }
+        }
+        if (tid < G) {
+            float *dst = ws + ((long long)(h0 + tid) * n_splits + split) * (HD + 2);
+            dst[0] = st[4 * tid];
+            dst[1] = st[4 * tid + 1];
         }
     }
-    if (tid < G) {
-        float *dst = ws + ((long long)(h0 + tid) * n_splits + split) * (HD + 2);
-        dst[0] = st[4 * tid];
-        dst[1] = st[4 * tid + 1];
+}
+
+// Compute units of the current device (cached per device).
+static int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] <= 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
     }
+    return cus[dev];
 }
 
 // SP_HIP_NO_MFMA_ATTN=1 sends every layout to the general kernel (read at each
@@ -551,9 +569,15 @@ hipError_t sp_launch_attn_mfma_split(const SpPlan &KP, const SpPlan &VP, const i
     if (A.n_q % A.n_kvh || A.n_q / A.n_kvh > 8 || (long long)n_splits * CHUNK < A.n_kv) return hipErrorNotSupported;
     if (((uintptr_t)A.kpack % 4) || ((uintptr_t)A.vpack % 2) || (A.k_head_stride % 4) || (A.v_head_stride % 2))
         return hipErrorNotSupported;
+    // Runs of consecutive splits per block: aim for ~2 blocks per CU so each
+    // block prefetches its next split while computing the current one.
+    const int total = A.n_kvh * n_splits;
+    const int target = 2 * device_cus();
+    const int rounds = total > target ? (total + target - 1) / target : 1;
+    const int nb = (n_splits + rounds - 1) / rounds;
     if (A.out)
-        hipLaunchKernelGGL(k_attn_mfma_split<true>, dim3(A.n_kvh, n_splits), dim3(256), 0, s, A, order, part, n_splits);
+        hipLaunchKernelGGL(k_attn_mfma_split<true>, dim3(A.n_kvh, nb), dim3(256), 0, s, A, order, part, n_splits, rounds);
     else
-        hipLaunchKernelGGL(k_attn_mfma_split<false>, dim3(A.n_kvh, n_splits), dim3(256), 0, s, A, order, part, n_splits);
+        hipLaunchKernelGGL(k_attn_mfma_split<false>, dim3(A.n_kvh, nb), dim3(256), 0, s, A, order, part, n_splits, rounds);
     return hipGetLastError();
 }
