@@ -227,6 +227,52 @@ k_attn_combine(const SpPlan VP, const float *__restrict__ ws, int n_splits, int 
         for (int k = tid; k < hd; k += SP_WAVE) out[(long long)h * hd + k] = c[k];
 }
 
+// Merge natural-domain partials [m, l, o[hd]] of query head blockIdx.x:
+// out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s. Block (h, y) produces
+// elements 32y .. 32y+31; thread (element, group g of 8) sums partials g, g+8, ...
+__global__ void __launch_bounds__(256)
+k_attn_merge(const float *__restrict__ ws, int n_parts, int hd, float *__restrict__ out) {
+    __shared__ float e_s[ATT_MAX_SPLITS];
+    __shared__ float red[256];
+    __shared__ float wred[4];
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const long long row = hd + 2;
+    const float *base = ws + (long long)h * n_parts * row;
+    float M = -INFINITY;
+    for (int sp = tid; sp < n_parts; sp += 256) M = fmaxf(M, base[sp * row]);
+    M = sp_wave_max(M);
+    if (lane == 0) wred[wv] = M;
+    __syncthreads();
+    M = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
+    __syncthreads();
+    float L = 0.0f;
+    for (int sp = tid; sp < n_parts; sp += 256) {
+        const float e = __expf(base[sp * row] - M);
+        e_s[sp] = e;
+        L += base[sp * row + 1] * e;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o, 64);
+    if (lane == 0) wred[wv] = L;
+    __syncthreads();
+    L = (wred[0] + wred[1]) + (wred[2] + wred[3]);
+    const int el = tid & 31, g = tid >> 5, i = 32 * blockIdx.y + el;
+    float acc = 0.0f;
+    if (i < hd) {
+        const float *p = base + 2 + i;
+#pragma unroll 8
+        for (int sp = g; sp < n_parts; sp += 8) acc = fmaf(p[sp * row], e_s[sp], acc);
+    }
+    red[tid] = acc;
+    __syncthreads();
+    if (tid < 32 && i < hd) {
+        float t = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) t += red[32 * k + tid];
+        out[(long long)h * hd + i] = t / L;
+    }
+}
+
 size_t sp_attn_workspace_floats(int n_q, int hd, int max_kv) {
     const int n_splits = (max_kv + ATT_CHUNK - 1) / ATT_CHUNK;
     return (size_t)n_q * hd + (size_t)n_q * n_splits * (hd + 2);
@@ -243,10 +289,11 @@ hipError_t sp_launch_attn_decode(const SpPlan &KP, const SpPlan &VP, const int *
     float *qt = workspace;
     float *part = workspace + (size_t)A.n_q * A.hd;
     const int want_out = A.out != nullptr;
-    const hipError_t me = sp_launch_attn_mfma_split(KP, VP, order, A, part, n_splits, s);
+    int n_parts = 0;
+    const hipError_t me = sp_launch_attn_mfma_split(KP, VP, order, A, part, n_splits, &n_parts, s);
     if (me == hipSuccess) {
         if (want_out)
-            hipLaunchKernelGGL(k_attn_combine, dim3(A.n_q), dim3(COMB_THREADS), 0, s, VP, part, n_splits, A.hd, A.out);
+            hipLaunchKernelGGL(k_attn_merge, dim3(A.n_q, (A.hd + 31) / 32), dim3(256), 0, s, part, n_parts, A.hd, A.out);
         return hipGetLastError();
     }
     if (me != hipErrorNotSupported) return me;

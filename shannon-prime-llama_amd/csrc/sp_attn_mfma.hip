@@ -347,6 +347,9 @@ k_attn_mfma_split(const SpAttnArgs A, const int *__restrict__ order, float *__re
     uint32_t kmask5 = 0x001f001fu, kmask4 = 0x000f000fu, kmask3 = 0x00070007u;
     __asm__("" : "+v"(kmask5), "+v"(kmask4), "+v"(kmask3));
 
+    // running softmax state of this lane's heads 2*q4 + hh over the block's rounds
+    float om[2] = {-INFINITY, -INFINITY}, ol[2] = {0.0f, 0.0f}, orun[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+
     for (int round = 0; round < rounds; round++) {
         const int split = split0 + round;
         if (split >= n_splits) break;
@@ -520,21 +523,59 @@ k_attn_mfma_split(const SpAttnArgs A, const int *__restrict__ order, float *__re
                 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, vcodes8(v1[0], v1[1]), d1, 0, 0, 0);
             }
         }
-        // ---- partial of this split: D rows 4*q4 + j are head 2*q4 + (j >> 1), part j & 1 ----
+        // ---- fold this split into the running state: D rows 4*q4 + j are head
+        // 2*q4 + (j >> 1), part j & 1 (rows of heads >= G carry junk, never stored) ----
 #pragma unroll
         for (int hh = 0; hh < 2; hh++) {
             const int h = 2 * q4 + hh;
-            if (h < G) {
-                const float un = st[4 * h + 2];  // 1/w-scale
-                float *dst = ws + ((long long)(h0 + h) * n_splits + split) * (HD + 2) + 2;
-                dst[32 * w + c16] = fmaf(d0[2 * hh + 1], 1.0f / 2048.0f, d0[2 * hh]) * un;
-                dst[32 * w + 16 + c16] = fmaf(d1[2 * hh + 1], 1.0f / 2048.0f, d1[2 * hh]) * un;
+            const float mr = st[4 * h], lr = st[4 * h + 1], un = st[4 * h + 2];  // un: 1/w-scale
+            const float o0 = fmaf(d0[2 * hh + 1], 1.0f / 2048.0f, d0[2 * hh]) * un;
+            const float o1 = fmaf(d1[2 * hh + 1], 1.0f / 2048.0f, d1[2 * hh]) * un;
+            const float mx = fmaxf(om[hh], mr);
+            const float a = __expf(om[hh] - mx), b = __expf(mr - mx);
+            orun[hh][0] = fmaf(orun[hh][0], a, o0 * b);
+            orun[hh][1] = fmaf(orun[hh][1], a, o1 * b);
+            ol[hh] = fmaf(ol[hh], a, lr * b);
+            om[hh] = mx;
+        }
+    }
+    if (!WANT_OUT) return;
+
+    // ---- the block's partial [m, l, o[128]] per head, o in the natural domain
+    // (inverse VHT2 in registers: wave w transforms heads w and w + 4) ----
+    __syncthreads();  // the last round is done with the LDS
+    float *st = reinterpret_cast<float *>(smem + OFF_ST);
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+        const int h = 2 * q4 + hh;
+        if (h < G) {
+            sc[h * SC_STRIDE + 32 * w + c16] = orun[hh][0];
+            sc[h * SC_STRIDE + 32 * w + 16 + c16] = orun[hh][1];
+            if (w == 0 && c16 == 0) {
+                st[4 * h] = om[hh];
+                st[4 * h + 1] = ol[hh];
             }
         }
-        if (tid < G) {
-            float *dst = ws + ((long long)(h0 + tid) * n_splits + split) * (HD + 2);
-            dst[0] = st[4 * tid];
-            dst[1] = st[4 * tid + 1];
+    }
+    __syncthreads();
+    const int n_parts = gridDim.y;
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int h = w + 4 * r;
+        if (h >= G) break;
+        float x0 = sc[h * SC_STRIDE + lane], x1 = sc[h * SC_STRIDE + lane + 64];
+        x0 = lane_butterfly<1>(x0, lane);   x1 = lane_butterfly<1>(x1, lane);
+        x0 = lane_butterfly<2>(x0, lane);   x1 = lane_butterfly<2>(x1, lane);
+        x0 = lane_butterfly<4>(x0, lane);   x1 = lane_butterfly<4>(x1, lane);
+        x0 = lane_butterfly<8>(x0, lane);   x1 = lane_butterfly<8>(x1, lane);
+        x0 = lane_butterfly<16>(x0, lane);  x1 = lane_butterfly<16>(x1, lane);
+        x0 = lane_butterfly<32>(x0, lane);  x1 = lane_butterfly<32>(x1, lane);
+        float *dst = ws + ((long long)(h0 + h) * n_parts + blockIdx.y) * (HD + 2);
+        dst[2 + lane] = (x0 + x1) * INV_SQRT_HD;
+        dst[2 + lane + 64] = (x0 - x1) * INV_SQRT_HD;
+        if (lane == 0) {
+            dst[0] = st[4 * h];
+            dst[1] = st[4 * h + 1];
         }
     }
 }
@@ -555,7 +596,7 @@ static int device_cus() {
 // SP_HIP_NO_MFMA_ATTN=1 sends every layout to the general kernel (read at each
 // call so tests can cross-check both paths in one process).
 hipError_t sp_launch_attn_mfma_split(const SpPlan &KP, const SpPlan &VP, const int *order, const SpAttnArgs &A,
-                                     float *part, int n_splits, hipStream_t s) {
+                                     float *part, int n_splits, int *n_parts, hipStream_t s) {
     static const int kb[4] = {5, 5, 4, 3};
     const char *off = getenv("SP_HIP_NO_MFMA_ATTN");
     if (off && off[0] == '1') return hipErrorNotSupported;
@@ -575,6 +616,7 @@ hipError_t sp_launch_attn_mfma_split(const SpPlan &KP, const SpPlan &VP, const i
     const int target = 2 * device_cus();
     const int rounds = total > target ? (total + target - 1) / target : 1;
     const int nb = (n_splits + rounds - 1) / rounds;
+    *n_parts = nb;
     if (A.out)
         hipLaunchKernelGGL(k_attn_mfma_split<true>, dim3(A.n_kvh, nb), dim3(256), 0, s, A, order, part, n_splits, rounds);
     else

@@ -222,9 +222,11 @@ hipError_t sp_launch_attn_decode(const SpPlan &KP, const SpPlan &VP, const int *
                                  hipStream_t s);
 size_t sp_attn_workspace_floats(int n_q, int hd, int max_kv);
 // Split kernel on the matrix cores for head_dim 128 with K 5/5/4/3 and V 3-bit;
-// hipErrorNotSupported for any other layout.
+// hipErrorNotSupported for any other layout. With an output it writes *n_parts
+// natural-domain partials [m, l, o[hd]] per query head (merged by k_attn_merge).
 hipError_t sp_launch_attn_mfma_split(const SpPlan &KP, const SpPlan &VP, const int *order,
-                                     const SpAttnArgs &A, float *part, int n_splits, hipStream_t s);
+                                     const SpAttnArgs &A, float *part, int n_splits, int *n_parts,
+                                     hipStream_t s);
 hipError_t sp_launch_attn_f16(const unsigned short *k, const unsigned short *v,
                               long long head_stride, int n_kv, int n_q, int n_kvh, int hd,
                               float kq_scale, const float *q, float *scores, float *out,
