@@ -28,6 +28,11 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 HBM_PEAK_GBS = 8000.0
 LAYERS, KVH, HD, POS, NQ = 32, 8, 128, 32768, 32
 K_BITS, V_BITS = (5, 5, 4, 3), (3,)
+# kernels behind each codec step on gfx950 (one launch per step over all 256 slots)
+KERNEL_NAMES = {"k_enc": "k_ship_encode_lane<Layout<128,5,5,4,3>, fp16, Mobius>",
+                "v_enc": "k_ship_encode_lane<Layout<128,3>, fp16>",
+                "k_dec": "k_ship_decode_lane<Layout<128,5,5,4,3>, fp16, Mobius>",
+                "v_dec": "k_ship_decode_lane<Layout<128,3>, fp16>"}
 
 
 def log(*a):
@@ -58,38 +63,59 @@ def make_inputs(torch, n_slots, pos, hd, seed=2, theta=500000.0):
     return k, v
 
 
-def cpu_baseline(kB, vB, target_s=10.0):
-    """Oracle (scalar C port, one thread) round trip of K and V vectors on this host."""
+def cpu_threads():
+    """Host threads for the all-core leg: the box's CPU share (OMP_NUM_THREADS there)."""
+    n = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS")
+    return max(1, min(n, int(env))) if env and env.isdigit() else n
+
+
+def cpu_baseline(target_s=8.0):
+    """The oracle (scalar C restatement of the reference codec, -O2) round-tripping
+    K and V vectors on this host: one thread (the reference's per-vector structure
+    on the decode thread), then OpenMP over the host's cores. Bounded sample: the
+    same seeded cfg2 vectors, repeated, about target_s seconds per leg."""
     import numpy as np
     import oracle_py as O
     import workloads as W
     kbc, vbc = O.band_config(HD, list(K_BITS)), O.band_config(HD, list(V_BITS))
     order = O.mobius_order(HD)
-    k16, v16 = W.cfg2_kv(n_heads=1, n_pos=4096, hd=HD, seed=5)
-    k = k16.reshape(-1, HD).view(np.uint16)
-    v = v16.reshape(-1, HD).view(np.uint16)
+    k16, v16 = W.cfg2_kv(n_heads=8, n_pos=4096, hd=HD, seed=5)
+    k = np.ascontiguousarray(k16.reshape(-1, HD).view(np.uint16))
+    v = np.ascontiguousarray(v16.reshape(-1, HD).view(np.uint16))
 
-    def run(n):
+    def leg(threads, n_rep):
         t0 = time.perf_counter()
-        done = 0
-        while done < n:
-            m = min(n - done, k.shape[0])
-            pk = O.ship_compress_f16(k[:m], kbc, order)
-            O.ship_decompress_f16(pk, kbc, order)
-            pv = O.ship_compress_f16(v[:m], vbc)
-            O.ship_decompress_f16(pv, vbc)
-            done += m
+        for _ in range(n_rep):
+            O.ship_roundtrip_f16_omp(k, kbc, order, threads=threads)
+            O.ship_roundtrip_f16_omp(v, vbc, None, threads=threads)
         return time.perf_counter() - t0
 
-    t = run(2048)
-    n = max(2048, int(2048 * target_s / max(t, 1e-6)))
-    n = min(n, 4096 * 64)
-    t = run(n)
-    vecs = 2 * n
-    return {"value": round(vecs / t, 1), "unit": "KV vecs/s", "cores": 1, "kind": "port",
-            "sample": f"{n} K + {n} V hd=128 vectors (cfg2 distribution) compress+decompress "
-                      f"through the scalar C oracle, single thread, {t:.1f} s; "
+    out = {}
+    for name, threads in (("single", 1), ("all", cpu_threads())):
+        t1 = leg(threads, 1)
+        reps = max(1, int(target_s / max(t1, 1e-6)))
+        t = leg(threads, reps)
+        out[name] = (threads, reps, t, 2 * k.shape[0] * reps / t)
+    th, reps, t, vps = out["all"]
+    return {"value": round(vps, 1), "unit": "KV vecs/s", "cores": th, "kind": "port",
+            "single_thread_value": round(out["single"][3], 1),
+            "sample": f"{k.shape[0]} K + {v.shape[0]} V hd=128 fp16 vectors (cfg2 distribution) compress+"
+                      f"decompress through the C oracle (-O2), repeated {reps}x on {th} OpenMP threads "
+                      f"({t:.1f} s); single thread {out['single'][3]:.0f} vecs/s over {out['single'][2]:.1f} s; "
                       f"host nproc={os.cpu_count()}"}
+
+
+def traffic_from_profile(kernel_key):
+    """HBM bytes per launch of a codec kernel from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy of known size), or None."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_ship_codec_cfg1.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)["per_launch_bytes"]
+        return t.get(kernel_key)
+    except (OSError, ValueError, KeyError):
+        return None
 
 
 def main():
@@ -100,6 +126,8 @@ def main():
     ap.add_argument("--attn-iters", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", choices=["codec", "attn", "all"], default="all")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="also run one plain device copy of the K inputs (known bytes) for PMC scaling")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
@@ -136,6 +164,13 @@ def main():
         "v_dec": lambda: L.sp_hip_read_all(cc.ref, 0, POS, None, P(vr), S.DTYPE_F16, -1),
     }
     result = {}
+    if args.copy_calib:
+        # one plain copy of n_slots * POS * HD fp16 (reads and writes that many bytes)
+        kc = torch.empty_like(k)
+        kc.copy_(k)
+        torch.cuda.synchronize()
+        log(f"[bench] copy calibration: {k.numel() * 2} bytes read and written")
+        del kc
     if args.only in ("codec", "all"):
         for _ in range(args.warmup):
             for f in steps.values():
@@ -187,10 +222,10 @@ def main():
             "hbm_frac": round(step_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "kernel_ms": {n: round(t, 4) for n, t in kern_ms.items()},
             "kernel_gbs": {n: round(n_vec * per[n] / (t * 1e-3) / 1e9, 1) for n, t in kern_ms.items()},
-            "roofline": {"kernel": {"k_enc": "k_ship_encode_fast (K)", "v_enc": "k_ship_encode_fast (V)",
-                                    "k_dec": "k_ship_decode_fast (K)", "v_dec": "k_ship_decode_fast (V)"}[dom],
+            "roofline": {"kernel": KERNEL_NAMES[dom],
                          "bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(dom_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                         "unit": "GB/s", "frac": round(dom_gbs / HBM_PEAK_GBS, 4),
+                         "traffic": traffic_from_profile(dom),
                          "bytes_per_launch": n_vec * per[dom], "avg_ms": round(kern_ms[dom], 4)},
             "parity_sample_mismatches": bad,
         })
@@ -245,8 +280,8 @@ def main():
                    "mobius": True, "vectors_per_step": 2 * n_vec, "io": "fp16 in, fp16 out, records in HBM"},
     })
     if not args.no_cpu:
-        log("[bench] timing CPU baseline (oracle, one thread)")
-        result["cpu_baseline"] = cpu_baseline(kB, vB)
+        log("[bench] timing CPU baseline (oracle, one thread and all cores)")
+        result["cpu_baseline"] = cpu_baseline()
     cc.free()
     print(json.dumps(result), flush=True)
 

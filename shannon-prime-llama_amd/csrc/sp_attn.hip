@@ -230,6 +230,9 @@ k_attn_combine(const SpPlan VP, const float *__restrict__ ws, int n_splits, int 
 // Merge natural-domain partials [m, l, o[hd]] of query head blockIdx.x:
 // out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s. Block (h, y) produces
 // elements 32y .. 32y+31; thread (element, group g of 8) sums partials g, g+8, ...
+// Its first MERGE_PRE partial values and the first 256 (m, l) pairs are loaded
+// together up front, so a typical merge waits on memory once.
+#define MERGE_PRE 8
 __global__ void __launch_bounds__(256)
 k_attn_merge(const float *__restrict__ ws, int n_parts, int hd, float *__restrict__ out) {
     __shared__ float e_s[ATT_MAX_SPLITS];
@@ -238,15 +241,31 @@ k_attn_merge(const float *__restrict__ ws, int n_parts, int hd, float *__restric
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const long long row = hd + 2;
     const float *base = ws + (long long)h * n_parts * row;
-    float M = -INFINITY;
-    for (int sp = tid; sp < n_parts; sp += 256) M = fmaxf(M, base[sp * row]);
+    const int el = tid & 31, g = tid >> 5, i = 32 * blockIdx.y + el;
+    const bool live = i < hd;
+    const float *p = base + 2 + (live ? i : 0);
+    float pre[MERGE_PRE];
+#pragma unroll
+    for (int r = 0; r < MERGE_PRE; r++) {
+        const int sp = g + 8 * r;
+        pre[r] = (live && sp < n_parts) ? p[sp * row] : 0.0f;
+    }
+    const float m0 = tid < n_parts ? base[tid * row] : -INFINITY;
+    const float l0 = tid < n_parts ? base[tid * row + 1] : 0.0f;
+    float M = m0;
+    for (int sp = tid + 256; sp < n_parts; sp += 256) M = fmaxf(M, base[sp * row]);
     M = sp_wave_max(M);
     if (lane == 0) wred[wv] = M;
     __syncthreads();
     M = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
     __syncthreads();
     float L = 0.0f;
-    for (int sp = tid; sp < n_parts; sp += 256) {
+    if (tid < n_parts) {
+        const float e = __expf(m0 - M);
+        e_s[tid] = e;
+        L = l0 * e;
+    }
+    for (int sp = tid + 256; sp < n_parts; sp += 256) {
         const float e = __expf(base[sp * row] - M);
         e_s[sp] = e;
         L += base[sp * row + 1] * e;
@@ -256,16 +275,17 @@ k_attn_merge(const float *__restrict__ ws, int n_parts, int hd, float *__restric
     if (lane == 0) wred[wv] = L;
     __syncthreads();
     L = (wred[0] + wred[1]) + (wred[2] + wred[3]);
-    const int el = tid & 31, g = tid >> 5, i = 32 * blockIdx.y + el;
     float acc = 0.0f;
-    if (i < hd) {
-        const float *p = base + 2 + i;
-#pragma unroll 8
-        for (int sp = g; sp < n_parts; sp += 8) acc = fmaf(p[sp * row], e_s[sp], acc);
+#pragma unroll
+    for (int r = 0; r < MERGE_PRE; r++) {
+        const int sp = g + 8 * r;
+        if (sp < n_parts) acc = fmaf(pre[r], e_s[sp], acc);
     }
+    if (live)
+        for (int sp = g + 8 * MERGE_PRE; sp < n_parts; sp += 8) acc = fmaf(p[sp * row], e_s[sp], acc);
     red[tid] = acc;
     __syncthreads();
-    if (tid < 32 && i < hd) {
+    if (tid < 32 && live) {
         float t = 0.0f;
 #pragma unroll
         for (int k = 0; k < 8; k++) t += red[32 * k + tid];

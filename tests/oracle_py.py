@@ -108,6 +108,19 @@ def ship_compress_f16(x16, bc, order=None, norm=NORM_FINAL):
     return out
 
 
+def ship_roundtrip_f16_omp(x16, bc, order=None, norm=NORM_FINAL, threads=1):
+    """Compress + decompress every vector, split over `threads` OpenMP threads
+    (the all-core CPU baseline); returns the reconstructed fp16 bits."""
+    x16 = np.ascontiguousarray(x16, dtype=np.uint16)
+    n = x16.shape[0]
+    packed = np.empty((n, bc.total_bytes), np.uint8)
+    out = np.empty_like(x16)
+    o = None if order is None else np.ascontiguousarray(order, dtype=np.int32)
+    lib().spo_ship_roundtrip_batch_f16_omp(ptr(x16), ptr(packed), ptr(out), n, x16.shape[1], C.byref(bc), ptr(o),
+                                           norm, int(threads))
+    return out
+
+
 def ship_compress_f32(x, bc, order=None, norm=NORM_FINAL):
     x = np.ascontiguousarray(x, dtype=np.float32)
     n, hd = x.shape
