@@ -403,7 +403,33 @@ struct ShipPriv {
     float *ws = nullptr;
     size_t ws_floats = 0;
     int max_q = 0;
+    // host-pointer calls: persistent device staging and pinned host staging,
+    // grown on demand (one caller at a time)
+    std::mutex stage_mu;
+    float *stage_d = nullptr;
+    float *stage_h = nullptr;
+    size_t stage_n = 0;  // floats in each
 };
+
+// Grow the host-call staging of `pv` to at least n floats (stage_mu held).
+static bool stage_reserve(ShipPriv *pv, size_t n) {
+    if (n <= pv->stage_n) return true;
+    if (pv->stage_d) (void)hipFree(pv->stage_d);
+    if (pv->stage_h) (void)hipHostFree(pv->stage_h);
+    pv->stage_d = nullptr;
+    pv->stage_h = nullptr;
+    pv->stage_n = 0;
+    const size_t want = n < 4096 * 128 ? (size_t)4096 * 128 : n;
+    if (!hip_ok(hipMalloc((void **)&pv->stage_d, want * sizeof(float)), "hipMalloc host-call staging") ||
+        !hip_ok(hipHostMalloc((void **)&pv->stage_h, want * sizeof(float), hipHostMallocDefault),
+                "hipHostMalloc host-call staging")) {
+        if (pv->stage_d) (void)hipFree(pv->stage_d);
+        pv->stage_d = nullptr;
+        return false;
+    }
+    pv->stage_n = want;
+    return true;
+}
 
 static bool check_cfg(const sp_config_t *cfg) {
     if (!cfg || cfg->head_dim <= 0 || cfg->head_dim > SP_MAX_HEAD_DIM || cfg->n_layers <= 0 ||
@@ -478,6 +504,8 @@ extern "C" void sp_hip_cache_free(sp_hip_cache_t *cc) {
     ShipPriv *pv = (ShipPriv *)cc->priv;
     if (pv) {
         if (pv->ws) (void)hipFree(pv->ws);
+        if (pv->stage_d) (void)hipFree(pv->stage_d);
+        if (pv->stage_h) (void)hipHostFree(pv->stage_h);
         delete pv;
     }
     memset(cc, 0, sizeof(*cc));
@@ -1181,27 +1209,33 @@ extern "C" void sp_shadow_read_v_batch(const sp_shadow_cache_t *sc, int l, int h
 extern "C" int sp_hip_write_host(sp_hip_cache_t *cc, int is_v, int layer, int head, int start_pos,
                                  int n_pos, const float *h_vecs) {
     if (!slot_ok(cc, layer, head, start_pos, n_pos) || !h_vecs) { set_err("write_host: bad args"); return -1; }
-    const int hd = cc->config.head_dim;
-    const size_t bytes = sizeof(float) * (size_t)n_pos * hd;
-    float *d = nullptr;
-    if (!hip_ok(hipMalloc((void **)&d, bytes), "write_host staging")) return -1;
-    bool ok = hip_ok(hipMemcpyAsync(d, h_vecs, bytes, hipMemcpyHostToDevice, (hipStream_t)cc->stream), "H2D") &&
-              ship_write(cc, is_v, layer, head, start_pos, n_pos, d, SP_DT_F32) == 0 &&
-              hip_ok(hipStreamSynchronize((hipStream_t)cc->stream), "sync");
-    (void)hipFree(d);
+    if (n_pos == 0) return 0;
+    ShipPriv *pv = (ShipPriv *)cc->priv;
+    const size_t n = (size_t)n_pos * cc->config.head_dim;
+    std::lock_guard<std::mutex> lk(pv->stage_mu);
+    if (!stage_reserve(pv, n)) return -1;
+    memcpy(pv->stage_h, h_vecs, n * sizeof(float));
+    const bool ok =
+        hip_ok(hipMemcpyAsync(pv->stage_d, pv->stage_h, n * sizeof(float), hipMemcpyHostToDevice, (hipStream_t)cc->stream),
+               "H2D") &&
+        ship_write(cc, is_v, layer, head, start_pos, n_pos, pv->stage_d, SP_DT_F32) == 0 &&
+        hip_ok(hipStreamSynchronize((hipStream_t)cc->stream), "sync");
     return ok ? 0 : -1;
 }
 
 extern "C" int sp_hip_read_host(const sp_hip_cache_t *cc, int is_v, int layer, int head, int start_pos,
                                 int n_pos, float *h_out, int max_bands) {
     if (!slot_ok(cc, layer, head, start_pos, n_pos) || !h_out) { set_err("read_host: bad args"); return -1; }
-    const int hd = cc->config.head_dim;
-    const size_t bytes = sizeof(float) * (size_t)n_pos * hd;
-    float *d = nullptr;
-    if (!hip_ok(hipMalloc((void **)&d, bytes), "read_host staging")) return -1;
-    bool ok = ship_read(cc, is_v, layer, head, start_pos, n_pos, d, SP_DT_F32, max_bands) == 0 &&
-              hip_ok(hipMemcpyAsync(h_out, d, bytes, hipMemcpyDeviceToHost, (hipStream_t)cc->stream), "D2H") &&
-              hip_ok(hipStreamSynchronize((hipStream_t)cc->stream), "sync");
-    (void)hipFree(d);
+    if (n_pos == 0) return 0;
+    ShipPriv *pv = (ShipPriv *)cc->priv;
+    const size_t n = (size_t)n_pos * cc->config.head_dim;
+    std::lock_guard<std::mutex> lk(pv->stage_mu);
+    if (!stage_reserve(pv, n)) return -1;
+    const bool ok =
+        ship_read(cc, is_v, layer, head, start_pos, n_pos, pv->stage_d, SP_DT_F32, max_bands) == 0 &&
+        hip_ok(hipMemcpyAsync(pv->stage_h, pv->stage_d, n * sizeof(float), hipMemcpyDeviceToHost, (hipStream_t)cc->stream),
+               "D2H") &&
+        hip_ok(hipStreamSynchronize((hipStream_t)cc->stream), "sync");
+    if (ok) memcpy(h_out, pv->stage_h, n * sizeof(float));
     return ok ? 0 : -1;
 }
