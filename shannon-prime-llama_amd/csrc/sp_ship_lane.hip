@@ -34,6 +34,15 @@ __device__ __forceinline__ void nt_store16(void *p, uint4 v) {
     __builtin_nontemporal_store(w, reinterpret_cast<u32x4 *>(p));
 }
 
+constexpr uint32_t BUF_WORD3 = 0x00020000u;  // raw buffer resource, dword data (gfx9 family)
+constexpr int BUF_NT = 2;                    // non-temporal load policy
+
+// Raw buffer over [p, p + nbytes): loads past nbytes return 0 (the range check
+// covers the vector, scalar and immediate offsets alike).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, int nbytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, nbytes, BUF_WORD3);
+}
+
 constexpr bool c_squarefree(int n) {
     for (int p = 2; p * p <= n; p++)
         if (n % (p * p) == 0) return false;
@@ -86,6 +95,34 @@ __device__ __forceinline__ void rec_insert(uint32_t (&rec)[DW], int pos, int w, 
     const int d = pos / 32, sh = pos % 32;
     rec[d] |= val << sh;
     if (sh + w > 32) rec[d + 1] |= val >> (32 - sh);
+}
+
+// Overwrite the w-bit field at bit position pos with val (val < 2^w).
+template <int DW>
+__device__ __forceinline__ void rec_replace(uint32_t (&rec)[DW], int pos, int w, uint32_t val) {
+    const int d = pos / 32, sh = pos % 32;
+    const uint32_t mask = (1u << w) - 1u;
+    rec[d] = (rec[d] & ~(mask << sh)) | (val << sh);
+    if (sh + w > 32) rec[d + 1] = (rec[d + 1] & ~(mask >> (32 - sh))) | (val >> (32 - sh));
+}
+
+// Insert the low w bits of v (higher bits are ignored) at bit position pos:
+// one shift and one three-input bit operation (v << sh) & mask | rec.
+template <int DW>
+__device__ __forceinline__ void rec_insert_low(uint32_t (&rec)[DW], int pos, int w, uint32_t v) {
+    const int d = pos / 32, sh = pos % 32;
+    const uint32_t mask = (1u << w) - 1u;
+    rec[d] = __builtin_amdgcn_bitop3_b32(v << sh, mask << sh, rec[d], 0xEA);
+    if (sh + w > 32) rec[d + 1] = __builtin_amdgcn_bitop3_b32(v >> (32 - sh), mask >> (32 - sh), rec[d + 1], 0xEA);
+}
+
+// fp16 pair (lo, hi) of w -> (lo + hi, lo - hi) in fp32: v_fma_mix widens each
+// half exactly and rounds once, the same result as convert-then-add.
+__device__ __forceinline__ void bfly_f16_pair(uint32_t w, float &s, float &d) {
+    __asm__("v_fma_mix_f32 %0, %2, 1.0, %2 op_sel:[0,0,1] op_sel_hi:[1,0,1]\n\t"
+            "v_fma_mix_f32 %1, %2, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[1,0,1]"
+            : "=&v"(s), "=v"(d)
+            : "v"(w));
 }
 
 template <int DW>
@@ -178,15 +215,14 @@ __device__ __forceinline__ void enc_tile(const uint4 (&in)[row_bytes<DT>(LY::hd)
 #pragma unroll
             for (int k = 0; k < 4; k++) {
                 const int i = c * 8 + k * 2;
-                const float a = sp_f16_bits_to_f32(w[k] & 0xffffu);
-                const float b = sp_f16_bits_to_f32(w[k] >> 16);
                 if (NORM == 1) {
+                    const float a = sp_f16_bits_to_f32(w[k] & 0xffffu);
+                    const float b = sp_f16_bits_to_f32(w[k] >> 16);
                     const float s2 = 0.70710678118654752440f;
                     x[i] = (a + b) * s2;
                     x[i + 1] = (a - b) * s2;
                 } else {
-                    x[i] = a + b;
-                    x[i + 1] = a - b;
+                    bfly_f16_pair(w[k], x[i], x[i + 1]);
                 }
             }
         }
@@ -219,22 +255,35 @@ __device__ __forceinline__ void enc_tile(const uint4 (&in)[row_bytes<DT>(LY::hd)
 #pragma unroll
         for (int e = 0; e < sz; e++) amax = fmaxf(amax, fabsf(x[src_idx<HD, MOB>(off + e)]));
         const float scale = (amax > 0.0f) ? sp_div(amax, (float)maxv) : 0.0f;
-        const uint32_t h = sp_f32_to_f16_bits(scale);
-        const float ss = sp_f16_bits_to_f32(h);
-        const float inv = (ss > 0.0f) ? sp_div(1.0f, ss) : 0.0f;
-        rec_insert(rec, 8 * bo, 16, h);
-        if (fastv && f16_normal(h)) {
+        // Fast path for every lane: the hardware conversion is IEEE round-to-nearest-even
+        // for finite scales, and for a normal fp16 scale |x*inv| < maxv + 1/2, so
+        // t = x*inv + 1.5*2^23 rounds x*inv to the nearest integer q with ties to even (the
+        // added constant is even) and bits(t) = 0x4B400000 + q: the low bits of
+        // bits(t) + maxv are the code q + maxv. Lanes outside those conditions redo the
+        // band below (a rare, divergent branch that only overwrites fields, so both
+        // sides define every record word).
+        float sc = scale;
+        __asm__ volatile("" : "+v"(sc));  // keep the division and the conversion apart
+        const uint32_t hf = (uint32_t)__builtin_bit_cast(unsigned short, (_Float16)sc);
+        {
+            const float ss = sp_f16_bits_to_f32(hf);
+            const float inv = (ss > 0.0f) ? sp_div(1.0f, ss) : 0.0f;
+            rec_insert_low(rec, 8 * bo, 16, hf);
 #pragma unroll
             for (int e = 0; e < sz; e++) {
                 const float t = x[src_idx<HD, MOB>(off + e)] * inv + 12582912.0f;
-                const uint32_t u = __float_as_uint(t) + (uint32_t)(maxv - 0x4B400000);
-                rec_insert(rec, 8 * (bo + 2) + e * bits, bits, u);
+                rec_insert_low(rec, 8 * (bo + 2) + e * bits, bits, __float_as_uint(t) + (uint32_t)maxv);
             }
-        } else {
+        }
+        if (!(fastv && f16_normal(hf))) {
+            const uint32_t h = sp_f32_to_f16_bits(scale);
+            const float ss = sp_f16_bits_to_f32(h);
+            const float inv = (ss > 0.0f) ? sp_div(1.0f, ss) : 0.0f;
+            rec_replace(rec, 8 * bo, 16, h);
 #pragma unroll
             for (int e = 0; e < sz; e++) {
                 const int q = sp_q_rint_clamp(x[src_idx<HD, MOB>(off + e)] * inv, maxv);
-                rec_insert(rec, 8 * (bo + 2) + e * bits, bits, (uint32_t)(q + maxv));
+                rec_replace(rec, 8 * (bo + 2) + e * bits, bits, (uint32_t)(q + maxv));
             }
         }
     }
@@ -261,36 +310,51 @@ __device__ __forceinline__ void enc_prefetch_coalesced(uint4 (&buf)[row_bytes<DT
     }
 }
 
+// Each single-wave block loads its tile with coalesced 16-byte loads and
+// transposes it through LDS; with no prefetch registers held across the
+// arithmetic, two waves fit per SIMD and one's loads overlap the other's work.
 template <class LY, int DT, int NORM, bool MOB>
-__global__ void __launch_bounds__(64)
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2)))
 k_ship_encode_lane(const void *__restrict__ src, long long so, long long si,
                    unsigned char *__restrict__ dst, long long dout, int n_inner, int tiles_per_outer,
                    int n_tiles, float inv_sqrt_n) {
     constexpr int RB = row_bytes<DT>(LY::hd), RP = RB + 16, CPR = RB / 16, B = LY::total, DW = LY::dwords;
+    // the record stage reuses the row buffer once the rows are in registers:
+    // 17 KB per single-wave block lets two waves share each SIMD
     __shared__ __attribute__((aligned(16))) unsigned char rows[64 * RP];
-    __shared__ __attribute__((aligned(16))) unsigned char stage[64 * B + 16];
+    static_assert(64 * B + 16 <= 64 * RP, "record stage must fit in the row buffer");
+    unsigned char *const stage = rows;
     const int lane = threadIdx.x;
     const TileMap M{tiles_per_outer, n_inner};
-    uint4 nxt[CPR];
-    int t = blockIdx.x;
-    if (t < n_tiles) enc_prefetch_coalesced<LY, DT>(nxt, src, so, si, M, t, lane);
-    for (; t < n_tiles; t += gridDim.x) {
-        // transpose the prefetched tile through LDS, then start the next prefetch
+    constexpr int esz = DT == SP_DT_F16 ? 2 : 4, RPL = 64 / CPR;  // rows per wave-wide load
+    static_assert(64 % CPR == 0, "a wave-wide 16-byte load must cover whole rows");
+    const int rowb = (int)(si * esz);  // the launcher keeps 64 rows of offsets in 32 bits
+    const int voff = (lane / CPR) * rowb + (lane % CPR) * 16;
+    unsigned char *lrow = rows + (lane / CPR) * RP + (lane % CPR) * 16;
+    for (int t = blockIdx.x; t < n_tiles; t += gridDim.x) {
+        {
+            // load k of lane j reads chunk 64k+j of the tile: row (64k+j)/CPR, column
+            // (64k+j)%CPR; rows past the tile's valid ones read as 0
+            int o, i0, nv;
+            M.at(t, o, i0, nv);
+            const unsigned char *g =
+                reinterpret_cast<const unsigned char *>(src) + ((long long)o * so + (long long)i0 * si) * esz;
+            const __amdgpu_buffer_rsrc_t rs = buf_rsrc(g, (nv - 1) * rowb + RB);
+            u32x4 v[CPR];
 #pragma unroll
-        for (int k = 0; k < CPR; k++) {
-            const int c = k * 64 + lane;
-            *reinterpret_cast<uint4 *>(rows + (c / CPR) * RP + (c % CPR) * 16) = nxt[k];
+            for (int k = 0; k < CPR; k++) v[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, k * RPL * rowb, BUF_NT);
+#pragma unroll
+            for (int k = 0; k < CPR; k++) *reinterpret_cast<u32x4 *>(lrow + k * RPL * RP) = v[k];
         }
         __syncthreads();
         uint4 in[CPR];
 #pragma unroll
         for (int c = 0; c < CPR; c++) in[c] = *reinterpret_cast<const uint4 *>(rows + lane * RP + c * 16);
-        if (t + (int)gridDim.x < n_tiles) enc_prefetch_coalesced<LY, DT>(nxt, src, so, si, M, t + gridDim.x, lane);
         uint32_t rec[DW];
         enc_tile<LY, DT, NORM, MOB>(in, inv_sqrt_n, rec);
         int o, i0, nvalid;
         M.at(t, o, i0, nvalid);
-        __syncthreads();  // rows consumed; previous tile's records copied out
+        __syncthreads();  // every lane holds its row before the stage overwrites the buffer
         if (lane < nvalid) {
             unsigned char *p = stage + lane * B;
             if (B % 4 == 0) {
@@ -447,6 +511,9 @@ hipError_t enc_launch(const SpPlan &P, bool mob, const void *src, long long so, 
     const int tpo = (n_inner + 63) / 64;
     const long long n_tiles = (long long)n_outer * tpo;
     if (n_tiles > 0x7fffffffLL) return hipErrorNotSupported;
+    // a tile's 64 rows are addressed by 32-bit buffer offsets
+    constexpr long long esz = DT == SP_DT_F16 ? 2 : 4;
+    if (si < 0 || 64 * si * esz + row_bytes<DT>(LY::hd) > 0x7fffffffLL) return hipErrorNotSupported;
     const dim3 grid((unsigned)std::min<long long>(n_tiles, persistent_blocks())), block(64);
     hipLaunchKernelGGL((k_ship_encode_lane<LY, DT, 0, MOB>), grid, block, 0, s, src, so, si, dst, dout, n_inner, tpo,
                        (int)n_tiles, P.inv_sqrt_n);

@@ -89,8 +89,12 @@ def mobius_order(n):
 
 
 def vht2(x, norm=NORM_FINAL):
+    """Forward VHT2 of one vector, or of every row of a 2-D array."""
     x = np.ascontiguousarray(x, dtype=np.float32).copy()
-    lib().spo_vht2_forward(ptr(x), x.shape[-1], norm)
+    n = x.shape[-1]
+    rows = x.reshape(-1, n)
+    for r in range(rows.shape[0]):
+        lib().spo_vht2_forward(C.c_void_p(rows.ctypes.data + r * n * 4), n, norm)
     return x
 
 

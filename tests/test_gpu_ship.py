@@ -118,6 +118,36 @@ def test_empty_and_single():
     np.testing.assert_array_equal(got[:50], O.ship_compress_f32(np.zeros((1, hd), np.float32), O.band_config(128, [3]))[0])
 
 
+def test_codes_at_rounding_ties():
+    """Quantizer inputs that sit exactly on a half-integer round half to even
+    (__float2int_rn, shannon_prime_cuda.cu:186). Such inputs are rare (a few rows in
+    65536 of Llama-like K/V), so the test writes a whole 8-head, 8192-position layer
+    through the cache, checks with the oracle that it holds tied rows for both K and
+    V, and compares every code."""
+    H, hd, n = 8, 128, 8192
+    k16, v16 = W.cfg1_kv(n_heads=H, n_pos=n, hd=hd, seed=3)
+    order = O.mobius_order(hd)
+    kbc, vbc = O.band_config(hd, [5, 5, 4, 3]), O.band_config(hd, [3])
+    kt_rows = W.tie_rows(k16.reshape(-1, hd).view(np.uint16), kbc, order, O.NORM_FINAL, O.vht2)
+    vt_rows = W.tie_rows(v16.reshape(-1, hd).view(np.uint16), vbc, None, O.NORM_FINAL, O.vht2)
+    say(f"tie rows: K {kt_rows.tolist()} V {vt_rows.tolist()}")
+    assert len(kt_rows) and len(vt_rows)
+    cc = S.ShipCache(S.config(hd, 1, H), n, stream=torch.cuda.current_stream().cuda_stream)
+    kt = dev(np.ascontiguousarray(k16.transpose(1, 0, 2)).view(np.uint16))  # llama rows [pos][head][hd]
+    vt = dev(np.ascontiguousarray(v16.transpose(1, 0, 2)).view(np.uint16))
+    S.check(S.lib().sp_hip_write_layer(cc.ref, 0, 0, n, p(kt), p(vt), H * hd, S.DTYPE_F16))
+    torch.cuda.synchronize()
+    kc = d2h(cc.c.d_k_cache, H * n * kbc.total_bytes).reshape(H * n, -1)
+    vc = d2h(cc.c.d_v_cache, H * n * vbc.total_bytes).reshape(H * n, -1)
+    kref = O.ship_compress_f16(k16.reshape(-1, hd).view(np.uint16), kbc, order)
+    vref = O.ship_compress_f16(v16.reshape(-1, hd).view(np.uint16), vbc)
+    np.testing.assert_array_equal(kc[kt_rows], kref[kt_rows])
+    np.testing.assert_array_equal(vc[vt_rows], vref[vt_rows])
+    np.testing.assert_array_equal(kc, kref)
+    np.testing.assert_array_equal(vc, vref)
+    cc.free()
+
+
 def test_cache_slots_layer_and_all_layouts():
     """sp_hip_write_layer / read_layer (llama cache rows) and write_all / read_all agree with
     the oracle for every slot, including odd start positions (unaligned V records)."""

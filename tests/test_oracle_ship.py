@@ -179,6 +179,25 @@ def test_quantizer_brute_force_nearest_code():
                 assert q == best
 
 
+def test_quantizer_ties_round_half_even():
+    """x*inv exactly on a half-integer: __float2int_rn (shannon_prime_cuda.cu:186)
+    rounds half to even. A power-of-two scale makes inv exact, so the products are
+    the chosen half-integers themselves."""
+    for bits in (5, 4, 3, 2):
+        m = (1 << (bits - 1)) - 1
+        bc = O.band_config(8, [bits])
+        s = np.float32(0.25)
+        halves = [k + 0.5 for k in range(-m, m)]
+        for i in range(0, len(halves), 7):
+            chunk = halves[i:i + 7]
+            x = np.array([m] + chunk + [0.0] * (7 - len(chunk)), np.float64) * float(s)
+            (h, codes), = unpack_band_codes(O.band_quantize(x.astype(np.float32), bc), bc)
+            assert h == np.float16(s).view(np.uint16)
+            for t, u in zip(chunk, codes[1:]):
+                assert u - m == int(np.rint(t)), (bits, t, u - m)
+                assert (u - m) % 2 == 0
+
+
 def test_quantizer_special_cases():
     bc = O.band_config(128, [5, 5, 4, 3])
     z = np.zeros(128, np.float32)

@@ -83,3 +83,29 @@ def hier_W(n_slots, n_target, n_skel, seed=7, scale=0.05):
     rng = np.random.default_rng(seed)
     W = (rng.standard_normal((n_slots, n_target, n_skel)) * scale).astype(np.float16)
     return W.view(np.uint16)
+
+
+def tie_rows(x16, bc, order=None, norm=1, vht2=None):
+    """Indices of the rows of x16 (fp16 bits [n, hd]) for which some quantizer input
+    x*inv is exactly a half-integer, so that the codes depend on round-half-to-even
+    (__float2int_rn at shannon_prime_cuda.cu:186). The spectral values come from the
+    oracle's VHT2 (passed in as `vht2`); scale, fp16 scale, inverse and product follow
+    the quantizer's fp32 steps (shannon_prime_cuda.cu:160-186) in numpy float32."""
+    x = vht2(np.ascontiguousarray(x16, dtype=np.uint16).view(np.float16).astype(np.float32), norm)
+    if order is not None:
+        x = x[:, np.asarray(order)]
+    hits = np.zeros(x.shape[0], bool)
+    for b in range(bc.n_bands):
+        off, sz, bits = bc.band_off[b], bc.band_sz[b], bc.band_bits[b]
+        maxv = (1 << (bits - 1)) - 1
+        if maxv == 0:
+            continue
+        band = x[:, off:off + sz]
+        amax = np.abs(band).max(1)
+        scale = np.where(amax > 0, amax / np.float32(maxv), np.float32(0)).astype(np.float32)
+        ss = scale.astype(np.float16).astype(np.float32)
+        with np.errstate(divide="ignore"):
+            inv = np.where(ss > 0, np.float32(1) / ss, np.float32(0)).astype(np.float32)
+        prod = (band * inv[:, None]).astype(np.float32)
+        hits |= (prod - np.floor(prod) == np.float32(0.5)).any(1)
+    return np.nonzero(hits)[0]
