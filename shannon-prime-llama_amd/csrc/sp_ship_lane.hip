@@ -34,6 +34,9 @@ __device__ __forceinline__ void nt_store16(void *p, uint4 v) {
     __builtin_nontemporal_store(w, reinterpret_cast<u32x4 *>(p));
 }
 
+typedef float float2v __attribute__((ext_vector_type(2)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
 constexpr uint32_t BUF_WORD3 = 0x00020000u;  // raw buffer resource, dword data (gfx9 family)
 constexpr int BUF_NT = 2;                    // non-temporal load policy
 
@@ -314,7 +317,7 @@ __device__ __forceinline__ void enc_prefetch_coalesced(uint4 (&buf)[row_bytes<DT
 // transposes it through LDS; with no prefetch registers held across the
 // arithmetic, two waves fit per SIMD and one's loads overlap the other's work.
 template <class LY, int DT, int NORM, bool MOB>
-__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(DT == SP_DT_F16 ? 2 : 1)))
 k_ship_encode_lane(const void *__restrict__ src, long long so, long long si,
                    unsigned char *__restrict__ dst, long long dout, int n_inner, int tiles_per_outer,
                    int n_tiles, float inv_sqrt_n) {
@@ -379,94 +382,135 @@ k_ship_encode_lane(const void *__restrict__ src, long long so, long long si,
 // ---------------------------------------------------------------------------
 // decode
 // ---------------------------------------------------------------------------
-template <class LY>
-__device__ __forceinline__ void dec_prefetch(uint32_t (&buf)[LY::dwords], const unsigned char *src, long long so,
-                                             const TileMap &M, int t, int lane) {
-    constexpr int B = LY::total;
-    int o, i0, nv;
-    M.at(t, o, i0, nv);
-    if (lane < nv) {
-        const unsigned char *p = src + (long long)o * so + (long long)(i0 + lane) * B;
-        if (B % 4 == 0) {
+// Decode one tile whose records are in registers and write its rows: through
+// LDS, then as wave-wide 16-byte buffer stores whose range check drops rows
+// past the tile's valid ones (no lane-dependent branch anywhere, so the
+// compiler can count outstanding memory operations exactly).
+template <class LY, int DT, int NORM, bool MOB, bool FULL>
+__device__ __forceinline__ void dec_tile(const uint32_t (&rec)[LY::dwords], unsigned char *stage, void *dst,
+                                         long long dout, long long din, const TileMap &M, int t, int lane,
+                                         float inv_sqrt_n, int max_bands) {
+    constexpr int HD = LY::hd, RB = row_bytes<DT>(HD), RP = RB + 16, CPR = RB / 16;
+    constexpr int esz = DT == SP_DT_F16 ? 2 : 4, RPL = 64 / CPR;  // rows per wave-wide store
+    static_assert(64 % CPR == 0, "a wave-wide 16-byte store must cover whole rows");
+    float x[HD];
 #pragma unroll
-            for (int d = 0; d < B / 4; d++) buf[d] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p) + d);
-        } else {
+    for (int b = 0; b < LY::nb; b++) {
+        const int off = LY::off(b), sz = LY::sz(b), bits = LY::bits[b];
+        const int maxv = (1 << (bits - 1)) - 1, bo = LY::byte_off(b);
+        const bool live = FULL || b < max_bands;  // FULL: every band is read
+        const float scale = live ? sp_scale_from_bits(rec_extract(rec, 8 * bo, 16)) : 0.0f;
+        const float bias = 12582912.0f + (float)maxv;
 #pragma unroll
-            for (int d = 0; d < LY::dwords; d++) buf[d] = 0u;
-#pragma unroll
-            for (int hw = 0; hw < B / 2; hw++)
-                buf[hw / 2] |= (uint32_t)__builtin_nontemporal_load(reinterpret_cast<const unsigned short *>(p) + hw)
-                               << (16 * (hw % 2));
+        for (int e = 0; e < sz; e++) {
+            const uint32_t u = rec_extract(rec, 8 * (bo + 2) + e * bits, bits);
+            const float d = __uint_as_float(u | 0x4B400000u) - bias;  // (float)(u - maxv), exact
+            x[src_idx<HD, MOB>(off + e)] = live ? d * scale : 0.0f;
         }
+    }
+    vht2_reg<HD, NORM>(x, inv_sqrt_n, false);
+    int o, i0, nvalid;
+    M.at(t, o, i0, nvalid);
+    __syncthreads();  // previous tile's rows have been read out of LDS
+    if (DT == SP_DT_F16) {
+#pragma unroll
+        for (int c = 0; c < HD / 8; c++) {
+            uint32_t w[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                float2v ab = {x[c * 8 + 2 * k], x[c * 8 + 2 * k + 1]};
+                __asm__ volatile("" : "+v"(ab));  // no multiply-into-convert fusion
+                // one packed IEEE round-to-nearest-even conversion per pair
+                w[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(ab, half2v));
+            }
+            *reinterpret_cast<uint4 *>(stage + lane * RP + c * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < HD / 4; c++)
+            *reinterpret_cast<float4 *>(stage + lane * RP + c * 16) =
+                make_float4(x[c * 4], x[c * 4 + 1], x[c * 4 + 2], x[c * 4 + 3]);
+    }
+    __syncthreads();
+    // store k of lane j writes chunk 64k+j of the tile: row (64k+j)/CPR, column (64k+j)%CPR
+    const int rowb = (int)(din * esz);  // the launcher keeps 64 rows of offsets in 32 bits
+    unsigned char *gdst = reinterpret_cast<unsigned char *>(dst) + ((long long)o * dout + (long long)i0 * din) * esz;
+    const __amdgpu_buffer_rsrc_t ws = buf_rsrc(gdst, (nvalid - 1) * rowb + RB);
+    const int voff = (lane / CPR) * rowb + (lane % CPR) * 16;
+    const unsigned char *lrow = stage + (lane / CPR) * RP + (lane % CPR) * 16;
+#pragma unroll
+    for (int k = 0; k < CPR; k++) {
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(lrow + k * RPL * RP);
+        __builtin_amdgcn_raw_buffer_store_b128(v, ws, voff, k * RPL * rowb, BUF_NT);
     }
 }
 
-template <class LY, int DT, int NORM, bool MOB>
+// A tile's records (64 contiguous records of B bytes) with coalesced 16-byte
+// loads: load k of lane j reads bytes [16(64k+j), 16(64k+j)+16). The raw
+// buffer covers the valid records only; a tile index past the last tile gives
+// an empty range, so the prefetch is issued unconditionally and reads nothing.
+template <class LY>
+__device__ __forceinline__ void rec_tile_load(u32x4 (&pre)[(64 * LY::total / 16 + 63) / 64], const unsigned char *src,
+                                              long long so, const TileMap &M, int t, int n_tiles, int lane) {
+    constexpr int B = LY::total, NCK = (64 * B / 16 + 63) / 64;
+    int o, i0, nv;
+    M.at(t, o, i0, nv);
+    if (t >= n_tiles) o = 0, i0 = 0, nv = 0;
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(src + (long long)o * so + (long long)i0 * B, nv * B);
+#pragma unroll
+    for (int k = 0; k < NCK; k++) pre[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16, k * 1024, BUF_NT);
+}
+
+// The lane's own record out of the tile staged in LDS: dword reads at a stride
+// of B bytes (B/4 odd for the 76-byte K records: no bank conflicts).
+template <class LY>
+__device__ __forceinline__ void rec_from_lds(uint32_t (&rec)[LY::dwords], const unsigned char *stage, int lane) {
+    constexpr int B = LY::total, DW = LY::dwords;
+    if (B % 4 == 0) {
+        const uint32_t *p = reinterpret_cast<const uint32_t *>(stage + lane * B);
+#pragma unroll
+        for (int d = 0; d < DW; d++) rec[d] = p[d];
+    } else {
+        // 2-byte aligned records: read the covering dwords and funnel-shift odd lanes by 16 bits
+        const int a = lane * B;
+        const uint32_t *p = reinterpret_cast<const uint32_t *>(stage + (a & ~3));
+        const uint32_t sh = (a & 2) * 8;
+        uint32_t w[DW + 1];
+#pragma unroll
+        for (int d = 0; d <= DW; d++) w[d] = p[d];
+#pragma unroll
+        for (int d = 0; d < DW; d++) rec[d] = __builtin_amdgcn_alignbit(w[d + 1], w[d], sh);
+        if (B % 4 != 0) rec[DW - 1] &= 0xffffu;
+    }
+}
+
+// Persistent single-wave blocks walk tiles t, t + G, t + 2G, ... (G = grid size).
+// Each tile's records arrive as coalesced 16-byte loads, issued one tile ahead
+// into registers, and are transposed through the LDS row stage (the records
+// are in registers before the stage is overwritten with output rows).
+template <class LY, int DT, int NORM, bool MOB, bool FULL>
 __global__ void __launch_bounds__(64)
 k_ship_decode_lane(const unsigned char *__restrict__ src, long long so, void *__restrict__ dst,
                    long long dout, long long din, int n_inner, int tiles_per_outer, int n_tiles,
                    float inv_sqrt_n, int max_bands) {
-    constexpr int HD = LY::hd, RB = row_bytes<DT>(HD), RP = RB + 16, CPR = RB / 16, DW = LY::dwords;
+    constexpr int RP = row_bytes<DT>(LY::hd) + 16, DW = LY::dwords, B = LY::total;
+    constexpr int NCK = (64 * B / 16 + 63) / 64;
+    static_assert(NCK * 1024 + 16 <= 64 * RP, "record tile must fit in the row stage");
     __shared__ __attribute__((aligned(16))) unsigned char stage[64 * RP];
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x, G = gridDim.x;
     const TileMap M{tiles_per_outer, n_inner};
-    uint32_t nxt[DW];
+    u32x4 pre[NCK];
     int t = blockIdx.x;
-    if (t < n_tiles) dec_prefetch<LY>(nxt, src, so, M, t, lane);
-    for (; t < n_tiles; t += gridDim.x) {
-        uint32_t rec[DW];
+    if (t >= n_tiles) return;
+    rec_tile_load<LY>(pre, src, so, M, t, n_tiles, lane);
+    for (; t < n_tiles; t += G) {
 #pragma unroll
-        for (int d = 0; d < DW; d++) rec[d] = nxt[d];
-        if (t + (int)gridDim.x < n_tiles) dec_prefetch<LY>(nxt, src, so, M, t + gridDim.x, lane);
-        float x[HD];
-#pragma unroll
-        for (int b = 0; b < LY::nb; b++) {
-            const int off = LY::off(b), sz = LY::sz(b), bits = LY::bits[b];
-            const int maxv = (1 << (bits - 1)) - 1, bo = LY::byte_off(b);
-            const bool live = b < max_bands;
-            const float scale = live ? sp_scale_from_bits(rec_extract(rec, 8 * bo, 16)) : 0.0f;
-            const float bias = 12582912.0f + (float)maxv;
-#pragma unroll
-            for (int e = 0; e < sz; e++) {
-                const uint32_t u = rec_extract(rec, 8 * (bo + 2) + e * bits, bits);
-                const float d = __uint_as_float(u | 0x4B400000u) - bias;  // (float)(u - maxv), exact
-                x[src_idx<HD, MOB>(off + e)] = live ? d * scale : 0.0f;
-            }
-        }
-        vht2_reg<HD, NORM>(x, inv_sqrt_n, false);
-        int o, i0, nvalid;
-        M.at(t, o, i0, nvalid);
-        __syncthreads();  // previous tile's rows have been copied out
-        if (DT == SP_DT_F16) {
-#pragma unroll
-            for (int c = 0; c < HD / 8; c++) {
-                uint32_t w[4];
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    float a = x[c * 8 + 2 * k], bb = x[c * 8 + 2 * k + 1];
-                    __asm__ volatile("" : "+v"(a), "+v"(bb));  // no multiply-into-convert fusion
-                    const _Float16 ha = (_Float16)a, hb = (_Float16)bb;
-                    w[k] = (uint32_t)__builtin_bit_cast(unsigned short, ha) |
-                           ((uint32_t)__builtin_bit_cast(unsigned short, hb) << 16);
-                }
-                *reinterpret_cast<uint4 *>(stage + lane * RP + c * 16) = make_uint4(w[0], w[1], w[2], w[3]);
-            }
-        } else {
-#pragma unroll
-            for (int c = 0; c < HD / 4; c++)
-                *reinterpret_cast<float4 *>(stage + lane * RP + c * 16) =
-                    make_float4(x[c * 4], x[c * 4 + 1], x[c * 4 + 2], x[c * 4 + 3]);
-        }
+        for (int k = 0; k < NCK; k++) *reinterpret_cast<u32x4 *>(stage + k * 1024 + lane * 16) = pre[k];
         __syncthreads();
-        constexpr int esz = DT == SP_DT_F16 ? 2 : 4;
-        unsigned char *gdst = reinterpret_cast<unsigned char *>(dst) + ((long long)o * dout) * esz;
-#pragma unroll 4
-        for (int tt = 0; tt < CPR; tt++) {
-            const int c = tt * 64 + lane, row = c / CPR, col = c % CPR;
-            if (row < nvalid)
-                nt_store16(gdst + ((long long)(i0 + row) * din) * esz + col * 16,
-                           *reinterpret_cast<const uint4 *>(stage + row * RP + col * 16));
-        }
+        rec_tile_load<LY>(pre, src, so, M, t + G, n_tiles, lane);
+        uint32_t rec[DW];
+        rec_from_lds<LY>(rec, stage, lane);
+        dec_tile<LY, DT, NORM, MOB, FULL>(rec, stage, dst, dout, din, M, t, lane, inv_sqrt_n, max_bands);
     }
 }
 
@@ -527,9 +571,16 @@ hipError_t dec_launch(const SpPlan &P, bool mob, const unsigned char *src, long 
     const int tpo = (n_inner + 63) / 64;
     const long long n_tiles = (long long)n_outer * tpo;
     if (n_tiles > 0x7fffffffLL) return hipErrorNotSupported;
+    // a tile's 64 output rows are addressed by 32-bit buffer offsets, rows never overlap
+    constexpr long long esz = DT == SP_DT_F16 ? 2 : 4;
+    if (din < LY::hd || 64 * din * esz + row_bytes<DT>(LY::hd) > 0x7fffffffLL) return hipErrorNotSupported;
     const dim3 grid((unsigned)std::min<long long>(n_tiles, persistent_blocks())), block(64);
-    hipLaunchKernelGGL((k_ship_decode_lane<LY, DT, 0, MOB>), grid, block, 0, s, src, so, dst, dout, din, n_inner, tpo,
-                       (int)n_tiles, P.inv_sqrt_n, P.max_bands);
+    if (P.max_bands < 0 || P.max_bands >= LY::nb)
+        hipLaunchKernelGGL((k_ship_decode_lane<LY, DT, 0, MOB, true>), grid, block, 0, s, src, so, dst, dout, din,
+                           n_inner, tpo, (int)n_tiles, P.inv_sqrt_n, P.max_bands);
+    else
+        hipLaunchKernelGGL((k_ship_decode_lane<LY, DT, 0, MOB, false>), grid, block, 0, s, src, so, dst, dout, din,
+                           n_inner, tpo, (int)n_tiles, P.inv_sqrt_n, P.max_bands);
     return hipGetLastError();
 }
 
