@@ -10,11 +10,11 @@
 // Quantization fast path: for a band whose stored fp16 scale is a normal
 // number and a vector whose inputs are finite, |x*inv| <= max_val*(1+2^-10)
 // < max_val + 0.5 for max_val <= 127, so rint never needs the clamp, and
-// rint(v) is obtained exactly as fl(v + 1.5*2^23) - 1.5*2^23 (ties-to-even,
-// since 1.5*2^23 is even and the ulp there is 1). Bands that fail the
-// condition (subnormal/zero/inf scale, non-finite input) take the exact
-// clamp path, so codes are bit-identical to kernel_band_quantize_simple
-// (shannon_prime_cuda.cu:131-204) in every case.
+// rint(v) is exact in the low bits of fl(v + 1.5*2^23) (ties-to-even, since
+// 1.5*2^23 is even and the ulp there is 1); adding max_val as an integer
+// gives the code. Bands that fail the condition (subnormal/zero/inf scale,
+// non-finite input) take the exact clamp path, so codes are bit-identical to
+// kernel_band_quantize_simple (shannon_prime_cuda.cu:131-204) in every case.
 #include <algorithm>
 #include <type_traits>
 
@@ -23,16 +23,6 @@
 namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ uint4 nt_load16(const void *p) {
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-
-__device__ __forceinline__ void nt_store16(void *p, uint4 v) {
-    u32x4 w = {v.x, v.y, v.z, v.w};
-    __builtin_nontemporal_store(w, reinterpret_cast<u32x4 *>(p));
-}
 
 typedef float float2v __attribute__((ext_vector_type(2)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
@@ -189,21 +179,6 @@ struct TileMap {
     }
 };
 
-template <class LY, int DT>
-__device__ __forceinline__ void enc_prefetch(uint4 (&buf)[row_bytes<DT>(LY::hd) / 16], const void *src,
-                                             long long so, long long si, const TileMap &M, int t, int lane) {
-    constexpr int CPR = row_bytes<DT>(LY::hd) / 16;
-    constexpr int esz = DT == SP_DT_F16 ? 2 : 4;
-    int o, i0, nv;
-    M.at(t, o, i0, nv);
-    if (lane < nv) {
-        const uint4 *p = reinterpret_cast<const uint4 *>(reinterpret_cast<const unsigned char *>(src) +
-                                                         ((long long)o * so + (long long)(i0 + lane) * si) * esz);
-#pragma unroll
-        for (int c = 0; c < CPR; c++) buf[c] = nt_load16(p + c);
-    }
-}
-
 template <class LY, int DT, int NORM, bool MOB>
 __device__ __forceinline__ void enc_tile(const uint4 (&in)[row_bytes<DT>(LY::hd) / 16], float inv_sqrt_n,
                                          uint32_t (&rec)[LY::dwords]) {
@@ -292,27 +267,6 @@ __device__ __forceinline__ void enc_tile(const uint4 (&in)[row_bytes<DT>(LY::hd)
     }
 }
 
-// Input tiles are prefetched one tile ahead into registers with coalesced
-// 16-byte loads (load k of lane j reads chunk 64k+j of the tile: row
-// (64k+j)/CPR, column (64k+j)%CPR), then transposed through LDS rows padded to
-// RB+16 bytes so that both the row writes and each lane's read of its own row
-// are bank-conflict free.
-template <class LY, int DT>
-__device__ __forceinline__ void enc_prefetch_coalesced(uint4 (&buf)[row_bytes<DT>(LY::hd) / 16], const void *src,
-                                                       long long so, long long si, const TileMap &M, int t,
-                                                       int lane) {
-    constexpr int CPR = row_bytes<DT>(LY::hd) / 16;
-    constexpr int esz = DT == SP_DT_F16 ? 2 : 4;
-    int o, i0, nv;
-    M.at(t, o, i0, nv);
-    const unsigned char *g = reinterpret_cast<const unsigned char *>(src) + ((long long)o * so) * esz;
-#pragma unroll
-    for (int k = 0; k < CPR; k++) {
-        const int c = k * 64 + lane, row = c / CPR, col = c % CPR;
-        if (row < nv) buf[k] = nt_load16(g + ((long long)(i0 + row) * si) * esz + col * 16);
-    }
-}
-
 // Each single-wave block loads its tile with coalesced 16-byte loads and
 // transposes it through LDS; with no prefetch registers held across the
 // arithmetic, two waves fit per SIMD and one's loads overlap the other's work.
@@ -371,11 +325,25 @@ k_ship_encode_lane(const void *__restrict__ src, long long so, long long si,
             }
         }
         __syncthreads();
+        // the tile's nvalid*B record bytes leave as wave-wide 16-byte stores over
+        // the whole 16-byte chunks, then one 2-byte store per lane over the rest;
+        // each raw buffer's range drops the stores past its end, so the store
+        // count is the same for every tile
         unsigned char *gdst = dst + (long long)o * dout + (long long)i0 * B;
-        const int nbytes = nvalid * B, nq = nbytes >> 4;
-        for (int k = lane; k < nq; k += 64)
-            nt_store16(reinterpret_cast<uint4 *>(gdst) + k, reinterpret_cast<const uint4 *>(stage)[k]);
-        for (int k = 16 * nq + lane; k < nbytes; k += 64) gdst[k] = stage[k];
+        const int nbytes = nvalid * B, nfull = nbytes & ~15;
+        {
+            constexpr int NCK = (64 * B / 16 + 63) / 64;
+            static_assert(NCK * 1024 <= 64 * RP && 64 * B + 128 <= 64 * RP, "stage reads stay in the row buffer");
+            const __amdgpu_buffer_rsrc_t ws = buf_rsrc(gdst, nfull);
+#pragma unroll
+            for (int k = 0; k < NCK; k++) {
+                const u32x4 v = *reinterpret_cast<const u32x4 *>(stage + k * 1024 + lane * 16);
+                __builtin_amdgcn_raw_buffer_store_b128(v, ws, lane * 16, k * 1024, BUF_NT);
+            }
+            const __amdgpu_buffer_rsrc_t wt = buf_rsrc(gdst + nfull, nbytes - nfull);
+            const unsigned short h = *reinterpret_cast<const unsigned short *>(stage + nfull + 2 * lane);
+            __builtin_amdgcn_raw_buffer_store_b16(h, wt, lane * 2, 0, BUF_NT);
+        }
     }
 }
 
