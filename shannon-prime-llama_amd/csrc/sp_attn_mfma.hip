@@ -47,6 +47,7 @@ constexpr int VDW = CHUNK * VB / 4;          // 3200 dwords of V records
 constexpr int KREG = KDW / 256;              // 19
 constexpr int VREG = (VDW + 1 + 255) / 256;  // 13 (one more dword when the V chunk is shifted)
 constexpr int DVT_STRIDE = 128 + 8;          // bytes per element row of the transposed V code tile (128 positions)
+constexpr int W_LO = CHUNK + 8;              // fp16 offset of a weight row's lo part (bank-shifted from the hi part)
 constexpr int SC_STRIDE = CHUNK + 8;         // floats per head row of scores / weights
 constexpr float INV_SQRT_HD = 0.08838834764831845f;
 
@@ -65,6 +66,7 @@ constexpr int OFF_ST = OFF_VREC + CHUNK * VB + 16;     // st[8][4]: per head max
 constexpr int LDS_FULL = OFF_ST + 8 * 4 * 4;
 constexpr int LDS_KQ = OFF_VS;
 static_assert(SZ_U >= HD * DVT_STRIDE, "V code tile must fit the K record area");
+static_assert(W_LO + CHUNK <= 2 * SC_STRIDE, "a head's hi and lo weight parts must fit its score row");
 static_assert(OFF_KS % 16 == 0 && OFF_SC % 16 == 0 && OFF_QB % 16 == 0 && OFF_CB % 16 == 0 && OFF_VS % 16 == 0 &&
                   OFF_VREC % 16 == 0 && OFF_ST % 16 == 0,
               "LDS regions 16-byte aligned");
@@ -459,7 +461,7 @@ k_attn_mfma_split(const SpAttnArgs A, const int *__restrict__ order, float *__re
                 const uint32_t hi = (uint32_t)__builtin_bit_cast(unsigned short, hh);
                 const uint32_t lo = (uint32_t)__builtin_bit_cast(unsigned short, (_Float16)((v - (float)hh) * 2048.0f));
                 wrow[lane + 64 * i] = (unsigned short)hi;
-                wrow[CHUNK + lane + 64 * i] = (unsigned short)lo;
+                wrow[W_LO + lane + 64 * i] = (unsigned short)lo;
             }
             if (lane == 0) {
                 st[4 * h] = m;
@@ -483,7 +485,9 @@ k_attn_mfma_split(const SpAttnArgs A, const int *__restrict__ order, float *__re
                 // 4pq .. 4pq+3 (a, b, c, d) -> dvt[element][position] bytes. Per group of
                 // four elements, two positions' 12-bit chunks share a dword (16 bits
                 // apart), so one shift and mask yields both positions' codes of an
-                // element and a byte permute lines up all four positions.
+                // element and a byte permute lines up all four positions. Element rows
+                // 32s .. 32s + 31 store their 32-byte position blocks XOR-swizzled by s,
+                // so each wave's tile writes fall in 64 distinct banks.
                 const int g = tid & 7, pq = tid >> 3;
                 uint32_t lo[4], hi[4];
 #pragma unroll
@@ -505,7 +509,7 @@ k_attn_mfma_split(const SpAttnArgs A, const int *__restrict__ order, float *__re
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
                         const uint32_t x = (wab >> (3 * e)) & 0x00070007u, y = (wcd >> (3 * e)) & 0x00070007u;
-                        *reinterpret_cast<uint32_t *>(dvt + (16 * g + 4 * sg + e) * DVT_STRIDE + 4 * pq) =
+                        *reinterpret_cast<uint32_t *>(dvt + (16 * g + 4 * sg + e) * DVT_STRIDE + ((4 * pq) ^ (32 * (g >> 1)))) =
                             __builtin_amdgcn_perm(y, x, 0x06040200u);
                     }
                 }
@@ -516,9 +520,9 @@ k_attn_mfma_split(const SpAttnArgs A, const int *__restrict__ order, float *__re
                 const int tb = 32 * kk + 8 * q4;  // A row c16, k-slots 8*q4 + e: positions tb + e
                 const half8_t a = __builtin_bit_cast(
                     half8_t, *reinterpret_cast<const u32x4 *>(reinterpret_cast<const unsigned short *>(sc + hrow * SC_STRIDE) +
-                                                              part * CHUNK + 128 * half + tb));
-                const u32x2 v0 = *reinterpret_cast<const u32x2 *>(dvt + n0 * DVT_STRIDE + tb);
-                const u32x2 v1 = *reinterpret_cast<const u32x2 *>(dvt + (n0 + 16) * DVT_STRIDE + tb);
+                                                              part * W_LO + 128 * half + tb));
+                const u32x2 v0 = *reinterpret_cast<const u32x2 *>(dvt + n0 * DVT_STRIDE + (tb ^ (32 * w)));
+                const u32x2 v1 = *reinterpret_cast<const u32x2 *>(dvt + (n0 + 16) * DVT_STRIDE + (tb ^ (32 * w)));
                 d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, vcodes8(v0[0], v0[1]), d0, 0, 0, 0);
                 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, vcodes8(v1[0], v1[1]), d1, 0, 0, 0);
             }
