@@ -10,8 +10,11 @@ Mobius, V flat 3-bit) and decompress every record back to fp16:
 Printed JSON line: metric/value (K+V vectors per second through compress +
 decompress), HBM GB/s of algorithmic bytes, the dominant kernel's roofline
 (HIP events on the launch stream), fused decompress-attention decode at 32K in
-us/token (32 layers) beside the fp16 baseline kernel, and the CPU baseline
-(the oracle, single thread, on a bounded sample).
+us/token (32 layers) beside uncompressed fp16 attention (torch batched GEMMs and
+this library's fp16 kernel), the other configs' codec paths (hd 96 Vilenkin,
+sqfree+spinor, hier) at their per-GPU shapes, and the CPU baseline (the oracle on
+a bounded sample, one thread and all cores). With the CPU leg, a sample of the
+full-size run is also checked against the oracle.
 """
 import argparse
 import ctypes as C
@@ -118,6 +121,133 @@ def traffic_from_profile(kernel_key):
         return None
 
 
+def parity_sample(S, cc, k, v, kr, kB, vB, n_slots):
+    """The checker, run with the CPU leg: three slots' records and K reconstructions
+    from the full-size run against the oracle (codes and fp16 bits exact)."""
+    import numpy as np
+    import oracle_py as O
+    kbc, vbc = O.band_config(HD, list(K_BITS)), O.band_config(HD, list(V_BITS))
+    order = O.mobius_order(HD)
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    bad = 0
+    for slot in (0, 131, n_slots - 1):
+        p0, m = 1000, 256
+        xk = k[slot, p0:p0 + m].cpu().numpy().view(np.uint16)
+        rec = np.empty(m * kB, np.uint8)
+        hip.hipMemcpy(rec.ctypes.data, cc.c.d_k_cache + (slot * POS + p0) * kB, rec.size, 2)
+        bad += int((rec.reshape(m, kB) != O.ship_compress_f16(xk, kbc, order)).any())
+        xv = v[slot, p0:p0 + m].cpu().numpy().view(np.uint16)
+        recv = np.empty(m * vB, np.uint8)
+        hip.hipMemcpy(recv.ctypes.data, cc.c.d_v_cache + (slot * POS + p0) * vB, recv.size, 2)
+        bad += int((recv.reshape(m, vB) != O.ship_compress_f16(xv, vbc)).any())
+        bad += int((kr[slot, p0:p0 + m].cpu().numpy().view(np.uint16) !=
+                    O.ship_decompress_f16(rec.reshape(m, kB), kbc, order)).any())
+    return bad
+
+
+def bench_variants(torch, S, L, stream, reps=3):
+    """Throughput of the other configs' codec paths at their per-GPU shapes (extra
+    fields of the JSON line, not the headline): configs[2] ship codec at hd 96
+    (Vilenkin 2^5*3, bridge default K 5/4/4, V 5), configs[3] sqfree+spinor
+    (pad 154, skeleton 0.75, K/V 5/4/4/4/5, residual 3 bits), configs[4] hier (pad 330,
+    30-coefficient skeleton at 5/5 bits, 2-bit residual). Rates count algorithmic
+    bytes (2*hd fp16 in or out plus the record)."""
+    sp = C.c_void_p(stream.cuda_stream)
+    P = lambda t: C.c_void_p(t.data_ptr())
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+
+    def timed(f):
+        f()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            f()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps * 1e-3  # s
+
+    def rate(n_vec, hd, B, t):
+        return {"ms": round(t * 1e3, 4), "vecs_per_s": round(n_vec / t, 1),
+                "gbs": round(n_vec * (2 * hd + B) / t / 1e9, 1)}
+
+    out = {}
+    # configs[2]: one layer of 32 heads x 65536 cells (16 sequences x 4096), hd 96
+    H3, N3, hd3 = 32, 65536, 96
+    cfg = S.config(hd3, 1, H3, k_bits=(5, 4, 4), v_bits=(5,))
+    c3 = S.ShipCache(cfg, N3, stream.cuda_stream)
+    x = (torch.randn((H3, N3, hd3), generator=g, device="cuda") *
+         torch.exp(0.5 * torch.randn((H3, 1, hd3), generator=g, device="cuda"))).half()
+    y = torch.empty_like(x)
+    kB3, vB3 = c3.c.k_bands.total_bytes, c3.c.v_bands.total_bytes
+    n3 = H3 * N3
+    out["cfg3_hd96_ship"] = {
+        "k_enc": rate(n3, hd3, kB3, timed(lambda: S.check(L.sp_hip_write_all(c3.ref, 0, N3, P(x), None, S.DTYPE_F16)))),
+        "v_enc": rate(n3, hd3, vB3, timed(lambda: S.check(L.sp_hip_write_all(c3.ref, 0, N3, None, P(x), S.DTYPE_F16)))),
+        "k_dec": rate(n3, hd3, kB3, timed(lambda: S.check(L.sp_hip_read_all(c3.ref, 0, N3, P(y), None, S.DTYPE_F16, -1)))),
+        "v_dec": rate(n3, hd3, vB3, timed(lambda: S.check(L.sp_hip_read_all(c3.ref, 0, N3, None, P(y), S.DTYPE_F16, -1)))),
+        "record_bytes": [kB3, vB3]}
+    c3.free()
+    del x, y
+    # configs[3]: sqfree+spinor, 12 layers x 4 KV heads x 65536 cells (4 x 16384), hd 128 -> pad 154
+    L4, H4, N4 = 12, 4, 65536
+    bits4 = (5, 4, 4, 4, 5)
+    cfg = S.config(128, L4, H4, k_bits=bits4, v_bits=bits4)
+    pad4 = L.sp_sqfree_pad_dim(128)
+    c4 = S.SqfreeCache(cfg, N4, rbits=3, spinor=True, sk_k=int(pad4 * 0.75), stream=stream.cuda_stream)
+    x = (torch.randn((L4 * H4, N4, 128), generator=g, device="cuda")).half()
+    y = torch.empty_like(x)
+    B4 = c4.c.bytes_per_pos_k
+
+    def sq_write():
+        for s in range(L4 * H4):
+            S.check(L.sp_hip_sqfree_write_batch(c4.ref, 0, s // H4, s % H4, 0, N4, P(x[s]), S.DTYPE_F16))
+
+    def sq_read():
+        for s in range(L4 * H4):
+            S.check(L.sp_hip_sqfree_read_batch(c4.ref, 0, s // H4, s % H4, 0, N4, P(y[s]), S.DTYPE_F16))
+
+    out["cfg4_sqfree_spinor"] = {"enc": rate(L4 * H4 * N4, 128, B4, timed(sq_write)),
+                                 "dec": rate(L4 * H4 * N4, 128, B4, timed(sq_read)),
+                                 "record_bytes": B4, "pad_dim": pad4, "skeleton": c4.c.sk_k,
+                                 "calls": f"{L4 * H4} slots x {N4} positions, one call per slot"}
+    c4.free()
+    del x, y
+    # configs[4]: hier, hd 256 -> pad 330, 8 KV heads x (8 x 131072) cells per layer; 2 slots timed
+    H5, N5, hd5 = 8, 8 * 131072, 256
+    pad5 = L.sp_sqfree_pad_dim(hd5)
+    n_sk = L.sp_hier_default_geometry(pad5, None, None)
+    import numpy as np
+    sk = np.zeros(n_sk, np.int32)
+    tg = np.zeros(pad5 - n_sk, np.int32)
+    L.sp_hier_default_geometry(pad5, C.c_void_p(sk.ctypes.data), C.c_void_p(tg.ctypes.data))
+    c5 = S.HierCache(S.config(hd5, 1, H5), pad5, sk, tg, S.band_config(n_sk, [5, 5]), 2, N5, H5,
+                     stream=stream.cuda_stream)
+    Wh = (np.random.default_rng(5).standard_normal((H5, pad5 - n_sk, n_sk)) * 0.05).astype(np.float16)
+    c5.upload_W(Wh.view(np.uint16))
+    n_t = 2
+    x = (torch.randn((n_t, N5, hd5), generator=g, device="cuda")).half()
+    y = torch.empty_like(x)
+    B5 = c5.c.bytes_per_pos_k
+
+    def hi_write():
+        for s in range(n_t):
+            S.check(L.sp_hip_hier_write_batch(c5.ref, 0, 0, s, 0, N5, P(x[s]), S.DTYPE_F16))
+
+    def hi_read():
+        for s in range(n_t):
+            S.check(L.sp_hip_hier_read_batch(c5.ref, 0, 0, s, 0, N5, P(y[s]), S.DTYPE_F16))
+
+    out["cfg5_hier"] = {"enc": rate(n_t * N5, hd5, B5, timed(hi_write)),
+                        "dec": rate(n_t * N5, hd5, B5, timed(hi_read)),
+                        "record_bytes": B5, "pad_dim": pad5, "skeleton": n_sk,
+                        "calls": f"{n_t} slots x {N5} positions, one call per slot"}
+    c5.free()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -125,7 +255,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--attn-iters", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["codec", "attn", "all"], default="all")
+    ap.add_argument("--only", choices=["codec", "attn", "variants", "all"], default="all")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run one plain device copy of the K inputs (known bytes) for PMC scaling")
     args = ap.parse_args()
@@ -193,26 +323,6 @@ def main():
         dom = max(kern_ms, key=kern_ms.get)
         dom_gbs = n_vec * per[dom] / (kern_ms[dom] * 1e-3) / 1e9
         log("[bench] kernel ms: " + ", ".join(f"{n}={t:.3f}" for n, t in kern_ms.items()))
-        # parity spot check on the full-size run: a sample of slots against the oracle
-        import numpy as np
-        import oracle_py as O
-        kbc, vbc = O.band_config(HD, list(K_BITS)), O.band_config(HD, list(V_BITS))
-        order = O.mobius_order(HD)
-        hip = C.CDLL("libamdhip64.so")
-        hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
-        bad = 0
-        for slot in (0, 131, n_slots - 1):
-            p0, m = 1000, 256
-            xk = k[slot, p0:p0 + m].cpu().numpy().view(np.uint16)
-            rec = np.empty(m * kB, np.uint8)
-            hip.hipMemcpy(rec.ctypes.data, cc.c.d_k_cache + (slot * POS + p0) * kB, rec.size, 2)
-            bad += int((rec.reshape(m, kB) != O.ship_compress_f16(xk, kbc, order)).any())
-            xv = v[slot, p0:p0 + m].cpu().numpy().view(np.uint16)
-            recv = np.empty(m * vB, np.uint8)
-            hip.hipMemcpy(recv.ctypes.data, cc.c.d_v_cache + (slot * POS + p0) * vB, recv.size, 2)
-            bad += int((recv.reshape(m, vB) != O.ship_compress_f16(xv, vbc)).any())
-            bad += int((kr[slot, p0:p0 + m].cpu().numpy().view(np.uint16) !=
-                        O.ship_decompress_f16(rec.reshape(m, kB), kbc, order)).any())
         result.update({
             "metric": "KV vecs/s compress+decompress (HBM GB/s, %roofline); fused dqKQ us/tok @32K",
             "value": round(2 * n_vec / (ms_step * 1e-3), 1),
@@ -227,7 +337,6 @@ def main():
                          "unit": "GB/s", "frac": round(dom_gbs / HBM_PEAK_GBS, 4),
                          "traffic": traffic_from_profile(dom),
                          "bytes_per_launch": n_vec * per[dom], "avg_ms": round(kern_ms[dom], 4)},
-            "parity_sample_mismatches": bad,
         })
     if args.only in ("attn", "all"):
         # fused decode attention over the compressed 32K cache, all 32 layers per token
@@ -261,17 +370,41 @@ def main():
             torch.cuda.synchronize()
             return a.elapsed_time(b) / args.attn_iters * 1e3  # us per token
 
+        # uncompressed fp16 attention through torch's batched GEMMs (rocBLAS / hipBLASLt):
+        # per layer scores = K . q (KV head-major, contiguous operands), softmax, . V
+        kl = k.view(LAYERS, KVH, POS, HD)
+        vl = v.view(LAYERS, KVH, POS, HD)
+        qh = q.view(LAYERS, KVH, NQ // KVH, HD).transpose(2, 3).contiguous().half()  # [L][KVH][HD][G]
+
+        def torch_kq():
+            for layer in range(LAYERS):
+                torch.bmm(kl[layer], qh[layer])
+
+        def torch_attn():
+            for layer in range(LAYERS):
+                s = torch.bmm(kl[layer], qh[layer]).float() * scale.value
+                p = torch.softmax(s, dim=1).transpose(1, 2).contiguous().half()
+                torch.bmm(p, vl[layer])
+
         us_fused, us_kq, us_f16 = timeit(fused), timeit(fused_kq), timeit(fp16)
+        us_tkq, us_tattn = timeit(torch_kq), timeit(torch_attn)
         kv_bytes = LAYERS * KVH * POS * (kB + vB)
         result.update({
             "fused_dqkq_us_per_tok": round(us_fused, 1),
             "fused_kq_only_us_per_tok": round(us_kq, 1),
+            "fp16_torch_kq_us_per_tok": round(us_tkq, 1),
+            "fp16_torch_attn_us_per_tok": round(us_tattn, 1),
             "fp16_attn_us_per_tok": round(us_f16, 1),
+            "fp16_kq_floor_us_per_tok": round(LAYERS * KVH * POS * 2 * HD / (HBM_PEAK_GBS * 1e3), 1),
             "fp16_attn_floor_us_per_tok": round(LAYERS * KVH * POS * 4 * HD / (HBM_PEAK_GBS * 1e3), 1),
             "fused_attn_gbs": round(kv_bytes / (us_fused * 1e-6) / 1e9, 1),
             "fused_attn_floor_us_per_tok": round(kv_bytes / (HBM_PEAK_GBS * 1e3), 1),
         })
-        log(f"[bench] fused attn {us_fused:.1f} us/tok, KQ-only {us_kq:.1f}, fp16 {us_f16:.1f}")
+        log(f"[bench] fused attn {us_fused:.1f} us/tok, KQ-only {us_kq:.1f}; fp16 torch attn {us_tattn:.1f}, "
+            f"torch KQ {us_tkq:.1f}, fp16 lane kernel {us_f16:.1f}")
+    if args.only in ("variants", "all"):
+        result["variants"] = bench_variants(torch, S, L, stream)
+        log("[bench] variants: " + json.dumps(result["variants"]))
     result.update({
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
@@ -280,6 +413,9 @@ def main():
                    "mobius": True, "vectors_per_step": 2 * n_vec, "io": "fp16 in, fp16 out, records in HBM"},
     })
     if not args.no_cpu:
+        if args.only in ("codec", "all"):
+            log("[bench] checking a sample of the full-size run against the oracle")
+            result["parity_sample_mismatches"] = parity_sample(S, cc, k, v, kr, kB, vB, n_slots)
         log("[bench] timing CPU baseline (oracle, one thread and all cores)")
         result["cpu_baseline"] = cpu_baseline()
     cc.free()

@@ -128,6 +128,14 @@ uint16_t sp_f32_to_f16(float f);
 /* ---- sqfree geometry (sp_sqfree_pad_dim: shannon_prime_sqfree.cu:600) ---- */
 int sp_sqfree_pad_dim(int head_dim);
 
+/* ---- hier geometry. The reference's core chooses it inside sp_hier_cache_init
+ * (called at kv_cache.cpp:326-329; "n_target typically ~130" at
+ * shannon_prime_hier.cu:114); its rule is not recoverable. This build's default:
+ * skeleton = the first ceil(0.09 * pad_dim) entries of the squarefree-first order
+ * over [0, pad_dim), targets = the rest in that order. Returns n_skeleton (or -1);
+ * skeleton_idx [n_skeleton] and target_idx [pad_dim - n_skeleton] may be NULL. */
+int sp_hier_default_geometry(int pad_dim, int *skeleton_idx, int *target_idx);
+
 #ifdef __cplusplus
 }
 #endif

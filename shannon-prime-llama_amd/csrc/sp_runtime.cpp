@@ -9,6 +9,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <vector>
 
@@ -154,6 +155,20 @@ extern "C" int sp_sqfree_pad_dim(int head_dim) {
     for (int n = head_dim; n < 16 * head_dim + 64; n++)
         if (is_squarefree(n) && is_11_smooth(n)) return n;
     return -1;
+}
+
+extern "C" int sp_hier_default_geometry(int pad_dim, int *skeleton_idx, int *target_idx) {
+    if (pad_dim <= 0) return -1;
+    const int n_skel = std::max(1, (pad_dim * 9 + 99) / 100);
+    if (skeleton_idx || target_idx) {
+        std::vector<int> order((size_t)pad_dim);
+        build_mobius_order(pad_dim, order.data());
+        for (int i = 0; i < pad_dim; i++) {
+            if (i < n_skel) { if (skeleton_idx) skeleton_idx[i] = order[i]; }
+            else if (target_idx) target_idx[i - n_skel] = order[i];
+        }
+    }
+    return n_skel;
 }
 
 static int factor_small(int n, unsigned char *f, int maxf) {

@@ -60,6 +60,19 @@ def test_sqfree_pad_dims():
     assert [S.lib().sp_sqfree_pad_dim(h) for h in (64, 128, 256, 96)] == [66, 154, 330, 105]
 
 
+def test_hier_default_geometry_matches_oracle():
+    for pad in (66, 154, 330, 105):
+        n_skel = S.lib().sp_hier_default_geometry(pad, None, None)
+        sk = np.zeros(n_skel, np.int32)
+        tg = np.zeros(pad - n_skel, np.int32)
+        assert S.lib().sp_hier_default_geometry(pad, C.c_void_p(sk.ctypes.data), C.c_void_p(tg.ctypes.data)) == n_skel
+        osk, otg = O.hier_geometry(pad)
+        np.testing.assert_array_equal(sk, osk)
+        np.testing.assert_array_equal(tg, otg)
+    assert S.lib().sp_hier_default_geometry(330, None, None) == 30  # cfg 5: 30 skeleton, 300 targets
+    assert S.lib().sp_hier_default_geometry(0, None, None) == -1
+
+
 def test_host_fp16_helpers_match_oracle():
     rng = np.random.default_rng(1)
     vals = rng.standard_normal(2000).astype(np.float32) * 10.0 ** rng.integers(-8, 6, 2000)
