@@ -153,6 +153,94 @@ __device__ __forceinline__ void vht2_reg(float (&x)[HD], float inv_sqrt_n, bool 
     }
 }
 
+// ---- staged Vilenkin-Hartley transform for non-power-of-two lengths ----
+// Constants of the transforms, passed by value (they land in scalar registers):
+// cas[pi][m] = (float)(cos(2*pi*m/p) + sin(2*pi*m/p)) and isp[pi] = 1.0f/sqrtf(p)
+// for p = 2, 3, 5, 7, 11 (pi = 0..4), exactly the values of the host plan.
+struct XfConst {
+    float inv_sqrt_n;
+    float isp[5];
+    float cas[5][11];
+};
+
+constexpr int c_prime(int i) { return i == 0 ? 2 : i == 1 ? 3 : i == 2 ? 5 : i == 3 ? 7 : 11; }
+constexpr int c_prime_idx(int p) { return p == 2 ? 0 : p == 3 ? 1 : p == 5 ? 2 : p == 7 ? 3 : 4; }
+constexpr bool c_pow2(int n) { return n > 0 && (n & (n - 1)) == 0; }
+
+// prime factors of N among {2, 3, 5, 7, 11}, ascending with multiplicity
+template <int N>
+struct Factors {
+    int p[16];
+    int n;
+    int rest;
+    constexpr Factors() : p(), n(0), rest(N) {
+        for (int i = 0; i < 5; i++)
+            while (rest % c_prime(i) == 0 && n < 16) {
+                p[n++] = c_prime(i);
+                rest /= c_prime(i);
+            }
+    }
+};
+
+// One stage with prime P at stride S (kernel_vilenkin_inplace order,
+// shannon_prime_sqfree.cu:66-106): each group {base + k*S} becomes
+// r[k] = (sum_j C[k][j] * g[j]) * (1/sqrt(P)), the sum running from 0.0f over j
+// ascending with separately rounded products and adds. C[k][0] = C[0][j] = 1
+// exactly and C = -1 exactly for P = 2 (the host checks), so those products are
+// the value itself; 0.0f + g[0] is kept (it maps -0 to +0 as the reference does).
+template <int N, int P, int S>
+__device__ __forceinline__ void vil_stage(float (&x)[N], const XfConst &K) {
+    constexpr int PI = c_prime_idx(P), BLOCK = S * P;
+    const float isp = K.isp[PI];
+#pragma unroll
+    for (int blk = 0; blk < N / BLOCK; blk++) {
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            const int base = blk * BLOCK + s;
+            float g[P];
+#pragma unroll
+            for (int k = 0; k < P; k++) g[k] = x[base + k * S];
+            const float z = 0.0f + g[0];
+#pragma unroll
+            for (int k = 0; k < P; k++) {
+                float sum = z;
+#pragma unroll
+                for (int j = 1; j < P; j++) {
+                    const int m = (k * j) % P;
+                    if (m == 0) sum = sum + g[j];
+                    else if (P == 2) sum = sum - g[j];
+                    else sum = sum + K.cas[PI][m] * g[j];
+                }
+                x[base + k * S] = sum * isp;
+            }
+        }
+    }
+}
+
+template <int N, int FI, int S>
+__device__ __forceinline__ void vil_stages(float (&x)[N], const XfConst &K) {
+    constexpr Factors<N> F{};
+    if constexpr (FI < F.n) {
+        constexpr int P = F.p[FI];
+        vil_stage<N, P, S>(x, K);
+        vil_stages<N, FI + 1, S * P>(x, K);
+    }
+}
+
+// First stage (P = 2, stride 1) straight from fp16 pairs: v_fma_mix widens
+// exactly and rounds once, so z = lo + 0.0f, r0 = z + hi, r1 = z - hi match
+// the fp32 stage bit for bit.
+__device__ __forceinline__ void vil_first_f16_pair(uint32_t w, float isp, float &r0, float &r1) {
+    float z, a, b;
+    __asm__("v_fma_mix_f32 %0, %1, 1.0, 0 op_sel_hi:[1,0,0]" : "=v"(z) : "v"(w));
+    __asm__("v_fma_mix_f32 %0, %2, 1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+            "v_fma_mix_f32 %1, -%2, 1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+            : "=&v"(a), "=v"(b)
+            : "v"(w), "v"(z));
+    r0 = a * isp;
+    r1 = b * isp;
+}
+
 __device__ __forceinline__ uint32_t f16_normal(uint32_t h) {
     const uint32_t e = h & 0x7c00u;
     return e != 0u && e != 0x7c00u;
@@ -169,6 +257,27 @@ constexpr int row_bytes(int hd) { return hd * (DT == SP_DT_F16 ? 2 : 4); }
 // before computing the current tile, so HBM latency overlaps with the
 // arithmetic even at one wave per SIMD.
 // ---------------------------------------------------------------------------
+// Chunk k of lane j of a 64-row tile moved with wave-wide 16-byte accesses:
+// chunk 64k + j is row (64k + j) / CPR, column (64k + j) % CPR. When CPR
+// divides 64 the row offset splits into a lane part (vector offset) and a
+// uniform part k * (64 / CPR) rows (scalar offset); otherwise the whole
+// offset is per lane.
+template <int CPR>
+struct TileChunk {
+    int row, col, krow;
+    __device__ __forceinline__ TileChunk(int k, int lane) {
+        if (64 % CPR == 0) {
+            row = lane / CPR, col = lane % CPR, krow = k * (64 / CPR);
+        } else {
+            const int c = 64 * k + lane;
+            row = c / CPR, col = c % CPR, krow = 0;
+        }
+    }
+    __device__ __forceinline__ int vofs(int rowb) const { return row * rowb + col * 16; }
+    __device__ __forceinline__ int sofs(int rowb) const { return krow * rowb; }
+    __device__ __forceinline__ int lds(int rp) const { return (row + krow) * rp + col * 16; }
+};
+
 struct TileMap {
     int tpo;      // tiles per outer row
     int n_inner;
@@ -180,12 +289,39 @@ struct TileMap {
 };
 
 template <class LY, int DT, int NORM, bool MOB>
-__device__ __forceinline__ void enc_tile(const uint4 (&in)[row_bytes<DT>(LY::hd) / 16], float inv_sqrt_n,
+__device__ __forceinline__ void enc_tile(const uint4 (&in)[row_bytes<DT>(LY::hd) / 16], const XfConst &K,
                                          uint32_t (&rec)[LY::dwords]) {
     constexpr int HD = LY::hd, DW = LY::dwords;
+    const float inv_sqrt_n = K.inv_sqrt_n;
     float x[HD];
     bool fastv;
-    if (DT == SP_DT_F16) {
+    if constexpr (!c_pow2(HD)) {
+        // Vilenkin lengths: the stage growth is at most sqrt(2p) per stage, so fp16
+        // inputs stay finite and inf/NaN inputs reach the DC coefficient x[0]
+        float mx = 0.0f;
+        if (DT == SP_DT_F16) {
+            static_assert(Factors<HD>{}.p[0] == 2, "the fused fp16 stage needs an even length");
+#pragma unroll
+            for (int c = 0; c < HD / 8; c++) {
+                const uint32_t w[4] = {in[c].x, in[c].y, in[c].z, in[c].w};
+#pragma unroll
+                for (int k = 0; k < 4; k++) vil_first_f16_pair(w[k], K.isp[0], x[c * 8 + k * 2], x[c * 8 + k * 2 + 1]);
+            }
+            vil_stages<HD, 1, 2>(x, K);
+        } else {
+#pragma unroll
+            for (int c = 0; c < HD / 4; c++) {
+                x[c * 4 + 0] = __uint_as_float(in[c].x);
+                x[c * 4 + 1] = __uint_as_float(in[c].y);
+                x[c * 4 + 2] = __uint_as_float(in[c].z);
+                x[c * 4 + 3] = __uint_as_float(in[c].w);
+            }
+#pragma unroll
+            for (int i = 0; i < HD; i++) mx = fmaxf(mx, fabsf(x[i]));
+            vil_stages<HD, 0, 1>(x, K);
+        }
+        fastv = (DT == SP_DT_F16 || mx < 1.2676506e30f) && __builtin_isfinite(x[0]);
+    } else if (DT == SP_DT_F16) {
         // first butterfly stage fused with the exact f16 -> f32 widening
 #pragma unroll
         for (int c = 0; c < HD / 8; c++) {
@@ -274,7 +410,7 @@ template <class LY, int DT, int NORM, bool MOB>
 __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(DT == SP_DT_F16 ? 2 : 1)))
 k_ship_encode_lane(const void *__restrict__ src, long long so, long long si,
                    unsigned char *__restrict__ dst, long long dout, int n_inner, int tiles_per_outer,
-                   int n_tiles, float inv_sqrt_n) {
+                   int n_tiles, const XfConst K) {
     constexpr int RB = row_bytes<DT>(LY::hd), RP = RB + 16, CPR = RB / 16, B = LY::total, DW = LY::dwords;
     // the record stage reuses the row buffer once the rows are in registers:
     // 17 KB per single-wave block lets two waves share each SIMD
@@ -283,11 +419,8 @@ k_ship_encode_lane(const void *__restrict__ src, long long so, long long si,
     unsigned char *const stage = rows;
     const int lane = threadIdx.x;
     const TileMap M{tiles_per_outer, n_inner};
-    constexpr int esz = DT == SP_DT_F16 ? 2 : 4, RPL = 64 / CPR;  // rows per wave-wide load
-    static_assert(64 % CPR == 0, "a wave-wide 16-byte load must cover whole rows");
+    constexpr int esz = DT == SP_DT_F16 ? 2 : 4;
     const int rowb = (int)(si * esz);  // the launcher keeps 64 rows of offsets in 32 bits
-    const int voff = (lane / CPR) * rowb + (lane % CPR) * 16;
-    unsigned char *lrow = rows + (lane / CPR) * RP + (lane % CPR) * 16;
     for (int t = blockIdx.x; t < n_tiles; t += gridDim.x) {
         {
             // load k of lane j reads chunk 64k+j of the tile: row (64k+j)/CPR, column
@@ -299,16 +432,22 @@ k_ship_encode_lane(const void *__restrict__ src, long long so, long long si,
             const __amdgpu_buffer_rsrc_t rs = buf_rsrc(g, (nv - 1) * rowb + RB);
             u32x4 v[CPR];
 #pragma unroll
-            for (int k = 0; k < CPR; k++) v[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, k * RPL * rowb, BUF_NT);
+            for (int k = 0; k < CPR; k++) {
+                const TileChunk<CPR> ch(k, lane);
+                v[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, ch.vofs(rowb), ch.sofs(rowb), BUF_NT);
+            }
 #pragma unroll
-            for (int k = 0; k < CPR; k++) *reinterpret_cast<u32x4 *>(lrow + k * RPL * RP) = v[k];
+            for (int k = 0; k < CPR; k++) {
+                const TileChunk<CPR> ch(k, lane);
+                *reinterpret_cast<u32x4 *>(rows + ch.lds(RP)) = v[k];
+            }
         }
         __syncthreads();
         uint4 in[CPR];
 #pragma unroll
         for (int c = 0; c < CPR; c++) in[c] = *reinterpret_cast<const uint4 *>(rows + lane * RP + c * 16);
         uint32_t rec[DW];
-        enc_tile<LY, DT, NORM, MOB>(in, inv_sqrt_n, rec);
+        enc_tile<LY, DT, NORM, MOB>(in, K, rec);
         int o, i0, nvalid;
         M.at(t, o, i0, nvalid);
         __syncthreads();  // every lane holds its row before the stage overwrites the buffer
@@ -357,10 +496,9 @@ k_ship_encode_lane(const void *__restrict__ src, long long so, long long si,
 template <class LY, int DT, int NORM, bool MOB, bool FULL>
 __device__ __forceinline__ void dec_tile(const uint32_t (&rec)[LY::dwords], unsigned char *stage, void *dst,
                                          long long dout, long long din, const TileMap &M, int t, int lane,
-                                         float inv_sqrt_n, int max_bands) {
+                                         const XfConst &K, int max_bands) {
     constexpr int HD = LY::hd, RB = row_bytes<DT>(HD), RP = RB + 16, CPR = RB / 16;
-    constexpr int esz = DT == SP_DT_F16 ? 2 : 4, RPL = 64 / CPR;  // rows per wave-wide store
-    static_assert(64 % CPR == 0, "a wave-wide 16-byte store must cover whole rows");
+    constexpr int esz = DT == SP_DT_F16 ? 2 : 4;
     float x[HD];
 #pragma unroll
     for (int b = 0; b < LY::nb; b++) {
@@ -376,7 +514,8 @@ __device__ __forceinline__ void dec_tile(const uint32_t (&rec)[LY::dwords], unsi
             x[src_idx<HD, MOB>(off + e)] = live ? d * scale : 0.0f;
         }
     }
-    vht2_reg<HD, NORM>(x, inv_sqrt_n, false);
+    if constexpr (c_pow2(HD)) vht2_reg<HD, NORM>(x, K.inv_sqrt_n, false);
+    else vil_stages<HD, 0, 1>(x, K);
     int o, i0, nvalid;
     M.at(t, o, i0, nvalid);
     __syncthreads();  // previous tile's rows have been read out of LDS
@@ -404,12 +543,11 @@ __device__ __forceinline__ void dec_tile(const uint32_t (&rec)[LY::dwords], unsi
     const int rowb = (int)(din * esz);  // the launcher keeps 64 rows of offsets in 32 bits
     unsigned char *gdst = reinterpret_cast<unsigned char *>(dst) + ((long long)o * dout + (long long)i0 * din) * esz;
     const __amdgpu_buffer_rsrc_t ws = buf_rsrc(gdst, (nvalid - 1) * rowb + RB);
-    const int voff = (lane / CPR) * rowb + (lane % CPR) * 16;
-    const unsigned char *lrow = stage + (lane / CPR) * RP + (lane % CPR) * 16;
 #pragma unroll
     for (int k = 0; k < CPR; k++) {
-        const u32x4 v = *reinterpret_cast<const u32x4 *>(lrow + k * RPL * RP);
-        __builtin_amdgcn_raw_buffer_store_b128(v, ws, voff, k * RPL * rowb, BUF_NT);
+        const TileChunk<CPR> ch(k, lane);
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(stage + ch.lds(RP));
+        __builtin_amdgcn_raw_buffer_store_b128(v, ws, ch.vofs(rowb), ch.sofs(rowb), BUF_NT);
     }
 }
 
@@ -417,16 +555,43 @@ __device__ __forceinline__ void dec_tile(const uint32_t (&rec)[LY::dwords], unsi
 // loads: load k of lane j reads bytes [16(64k+j), 16(64k+j)+16). The raw
 // buffer covers the valid records only; a tile index past the last tile gives
 // an empty range, so the prefetch is issued unconditionally and reads nothing.
+// The range check drops every dword that does not end inside the range, so
+// when the valid bytes end 2 bytes into a dword (B = 2 mod 4 and an odd count
+// of records) those 2 bytes come from an exactly range-checked 2-byte load,
+// `tail`, which the caller writes into LDS after the chunks.
 template <class LY>
-__device__ __forceinline__ void rec_tile_load(u32x4 (&pre)[(64 * LY::total / 16 + 63) / 64], const unsigned char *src,
-                                              long long so, const TileMap &M, int t, int n_tiles, int lane) {
-    constexpr int B = LY::total, NCK = (64 * B / 16 + 63) / 64;
+struct RecTile {
+    static constexpr int NCK = (64 * LY::total / 16 + 63) / 64;
+    u32x4 pre[NCK];
+    uint32_t tail;
+};
+
+template <class LY>
+__device__ __forceinline__ void rec_tile_load(RecTile<LY> &R, const unsigned char *src, long long so,
+                                              const TileMap &M, int t, int n_tiles, int lane) {
+    constexpr int B = LY::total;
     int o, i0, nv;
     M.at(t, o, i0, nv);
     if (t >= n_tiles) o = 0, i0 = 0, nv = 0;
     const __amdgpu_buffer_rsrc_t rs = buf_rsrc(src + (long long)o * so + (long long)i0 * B, nv * B);
 #pragma unroll
-    for (int k = 0; k < NCK; k++) pre[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16, k * 1024, BUF_NT);
+    for (int k = 0; k < RecTile<LY>::NCK; k++)
+        R.pre[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16, k * 1024, BUF_NT);
+    if (B % 4 != 0) R.tail = __builtin_amdgcn_raw_buffer_load_b16(rs, nv > 0 ? nv * B - 2 : 0, 0, BUF_NT);
+}
+
+// Stage tile t's records into LDS (chunks, then the 2-byte tail).
+template <class LY>
+__device__ __forceinline__ void rec_tile_stage(const RecTile<LY> &R, unsigned char *stage, const TileMap &M, int t,
+                                               int lane) {
+    constexpr int B = LY::total;
+#pragma unroll
+    for (int k = 0; k < RecTile<LY>::NCK; k++) *reinterpret_cast<u32x4 *>(stage + k * 1024 + lane * 16) = R.pre[k];
+    if (B % 4 != 0) {
+        int o, i0, nv;
+        M.at(t, o, i0, nv);
+        if (lane == 0) *reinterpret_cast<unsigned short *>(stage + nv * B - 2) = (unsigned short)R.tail;
+    }
 }
 
 // The lane's own record out of the tile staged in LDS: dword reads at a stride
@@ -460,25 +625,24 @@ template <class LY, int DT, int NORM, bool MOB, bool FULL>
 __global__ void __launch_bounds__(64)
 k_ship_decode_lane(const unsigned char *__restrict__ src, long long so, void *__restrict__ dst,
                    long long dout, long long din, int n_inner, int tiles_per_outer, int n_tiles,
-                   float inv_sqrt_n, int max_bands) {
+                   const XfConst K, int max_bands) {
     constexpr int RP = row_bytes<DT>(LY::hd) + 16, DW = LY::dwords, B = LY::total;
     constexpr int NCK = (64 * B / 16 + 63) / 64;
     static_assert(NCK * 1024 + 16 <= 64 * RP, "record tile must fit in the row stage");
     __shared__ __attribute__((aligned(16))) unsigned char stage[64 * RP];
     const int lane = threadIdx.x, G = gridDim.x;
     const TileMap M{tiles_per_outer, n_inner};
-    u32x4 pre[NCK];
+    RecTile<LY> R;
     int t = blockIdx.x;
     if (t >= n_tiles) return;
-    rec_tile_load<LY>(pre, src, so, M, t, n_tiles, lane);
+    rec_tile_load<LY>(R, src, so, M, t, n_tiles, lane);
     for (; t < n_tiles; t += G) {
-#pragma unroll
-        for (int k = 0; k < NCK; k++) *reinterpret_cast<u32x4 *>(stage + k * 1024 + lane * 16) = pre[k];
+        rec_tile_stage<LY>(R, stage, M, t, lane);
         __syncthreads();
-        rec_tile_load<LY>(pre, src, so, M, t + G, n_tiles, lane);
+        rec_tile_load<LY>(R, src, so, M, t + G, n_tiles, lane);
         uint32_t rec[DW];
         rec_from_lds<LY>(rec, stage, lane);
-        dec_tile<LY, DT, NORM, MOB, FULL>(rec, stage, dst, dout, din, M, t, lane, inv_sqrt_n, max_bands);
+        dec_tile<LY, DT, NORM, MOB, FULL>(rec, stage, dst, dout, din, M, t, lane, K, max_bands);
     }
 }
 
@@ -491,6 +655,10 @@ using K128 = Layout<128, 5, 5, 4, 3>;
 using V128 = Layout<128, 3>;
 using K64 = Layout<64, 5, 5, 4, 3>;
 using V64 = Layout<64, 5>;
+// Phi-3-mini-shaped hd 96 (Vilenkin 2^5 * 3) with the bridge's defaults, K 5/4/4 and V 5
+// (shannon_prime_llama.c:240-248)
+using K96 = Layout<96, 5, 4, 4>;
+using V96 = Layout<96, 5>;
 
 // Persistent grid size: enough single-wave blocks for several resident waves
 // per SIMD on every CU (queried once per process).
@@ -508,9 +676,39 @@ int persistent_blocks() {
     return n;
 }
 
+// Kernel constants from the host plan: cas[pi][m] is row 1 of the plan's p x p
+// table (C[1][m] = cas(2*pi*m/p)), which holds every value C[k][j] takes.
+XfConst xf_const(const SpPlan &P) {
+    static const int primes[5] = {2, 3, 5, 7, 11};
+    static const int offs[5] = {SP_CAS_OFF2, SP_CAS_OFF3, SP_CAS_OFF5, SP_CAS_OFF7, SP_CAS_OFF11};
+    XfConst K{};
+    K.inv_sqrt_n = P.inv_sqrt_n;
+    for (int pi = 0; pi < 5; pi++) {
+        K.isp[pi] = P.isp[pi];
+        for (int m = 0; m < primes[pi]; m++) K.cas[pi][m] = P.cas[offs[pi] + primes[pi] + m];
+    }
+    return K;
+}
+
+// The register Vilenkin stages take C = 1 for k*j = 0 (mod p) and C = -1 for
+// p = 2, k*j = 1 as exact; the host plan's values must be exactly those.
+bool vil_consts_exact(const SpPlan &P) {
+    static const int primes[5] = {2, 3, 5, 7, 11};
+    static const int offs[5] = {SP_CAS_OFF2, SP_CAS_OFF3, SP_CAS_OFF5, SP_CAS_OFF7, SP_CAS_OFF11};
+    for (int pi = 0; pi < 5; pi++) {
+        const int p = primes[pi];
+        for (int k = 0; k < p; k++)
+            for (int j = 0; j < p; j++)
+                if ((k * j) % p == 0 && P.cas[offs[pi] + k * p + j] != 1.0f) return false;
+    }
+    return P.cas[SP_CAS_OFF2 + 3] == -1.0f;
+}
+
 template <class LY>
 bool layout_matches(const SpPlan &P) {
     if (P.hd != LY::hd || P.n_bands != LY::nb || P.total_bytes != LY::total) return false;
+    if (P.skip_transform) return false;
+    if (!c_pow2(LY::hd) && !vil_consts_exact(P)) return false;
     for (int b = 0; b < LY::nb; b++)
         if (P.band_bits[b] != LY::bits[b]) return false;
     return true;
@@ -528,7 +726,7 @@ hipError_t enc_launch(const SpPlan &P, bool mob, const void *src, long long so, 
     if (si < 0 || 64 * si * esz + row_bytes<DT>(LY::hd) > 0x7fffffffLL) return hipErrorNotSupported;
     const dim3 grid((unsigned)std::min<long long>(n_tiles, persistent_blocks())), block(64);
     hipLaunchKernelGGL((k_ship_encode_lane<LY, DT, 0, MOB>), grid, block, 0, s, src, so, si, dst, dout, n_inner, tpo,
-                       (int)n_tiles, P.inv_sqrt_n);
+                       (int)n_tiles, xf_const(P));
     return hipGetLastError();
 }
 
@@ -545,10 +743,10 @@ hipError_t dec_launch(const SpPlan &P, bool mob, const unsigned char *src, long 
     const dim3 grid((unsigned)std::min<long long>(n_tiles, persistent_blocks())), block(64);
     if (P.max_bands < 0 || P.max_bands >= LY::nb)
         hipLaunchKernelGGL((k_ship_decode_lane<LY, DT, 0, MOB, true>), grid, block, 0, s, src, so, dst, dout, din,
-                           n_inner, tpo, (int)n_tiles, P.inv_sqrt_n, P.max_bands);
+                           n_inner, tpo, (int)n_tiles, xf_const(P), P.max_bands);
     else
         hipLaunchKernelGGL((k_ship_decode_lane<LY, DT, 0, MOB, false>), grid, block, 0, s, src, so, dst, dout, din,
-                           n_inner, tpo, (int)n_tiles, P.inv_sqrt_n, P.max_bands);
+                           n_inner, tpo, (int)n_tiles, xf_const(P), P.max_bands);
     return hipGetLastError();
 }
 
@@ -557,7 +755,7 @@ hipError_t enc_dispatch(const SpPlan &P, bool mob, const void *src, long long so
                         unsigned char *dst, long long dout, int n_outer, int n_inner, hipStream_t s) {
 #define SP_TRY(LY, MOB) \
     if (layout_matches<LY>(P)) return enc_launch<LY, DT, MOB>(P, mob, src, so, si, dst, dout, n_outer, n_inner, s);
-    SP_TRY(K128, true) SP_TRY(V128, false) SP_TRY(K64, true) SP_TRY(V64, false)
+    SP_TRY(K128, true) SP_TRY(V128, false) SP_TRY(K64, true) SP_TRY(V64, false) SP_TRY(K96, true) SP_TRY(V96, false)
 #undef SP_TRY
     return hipErrorNotSupported;
 }
@@ -567,7 +765,7 @@ hipError_t dec_dispatch(const SpPlan &P, bool mob, const unsigned char *src, lon
                         long long dout, long long din, int n_outer, int n_inner, hipStream_t s) {
 #define SP_TRY(LY, MOB) \
     if (layout_matches<LY>(P)) return dec_launch<LY, DT, MOB>(P, mob, src, so, dst, dout, din, n_outer, n_inner, s);
-    SP_TRY(K128, true) SP_TRY(V128, false) SP_TRY(K64, true) SP_TRY(V64, false)
+    SP_TRY(K128, true) SP_TRY(V128, false) SP_TRY(K64, true) SP_TRY(V64, false) SP_TRY(K96, true) SP_TRY(V96, false)
 #undef SP_TRY
     return hipErrorNotSupported;
 }

@@ -148,6 +148,67 @@ def test_codes_at_rounding_ties():
     cc.free()
 
 
+@pytest.mark.parametrize("strided", [False, True])
+def test_cache_hd96_vilenkin(strided):
+    """hd 96 (Vilenkin 2^5*3) with the bridge defaults K 5/4/4 + Mobius and V 5 through
+    the cache: contiguous [slot][pos][hd] rows (write_all/read_all) or llama cache rows
+    with a head stride (write_layer/read_layer); codes and fp16/fp32 reconstructions
+    bit-exact, including a partial last tile."""
+    L_, H, hd, max_seq, n = 2, 4, 96, 200, 131
+    say(f"cache hd96 strided={strided}")
+    cfg = S.config(hd, L_, H, k_bits=(5, 4, 4), v_bits=(5,))
+    cc = S.ShipCache(cfg, max_seq, stream=torch.cuda.current_stream().cuda_stream)
+    order = O.mobius_order(hd)
+    kbc, vbc = O.band_config(hd, [5, 4, 4]), O.band_config(hd, [5])
+    assert (kbc.total_bytes, vbc.total_bytes) == (58, 62)
+    k16, v16 = W.cfg3_kv(n_heads=L_ * H, n_pos=n, hd=hd, seed=96)  # [slot][pos][hd]
+    if strided:
+        for layer in range(L_):
+            kt = dev(np.ascontiguousarray(k16[layer * H:(layer + 1) * H].transpose(1, 0, 2)).view(np.uint16))
+            vt = dev(np.ascontiguousarray(v16[layer * H:(layer + 1) * H].transpose(1, 0, 2)).view(np.uint16))
+            S.check(S.lib().sp_hip_write_layer(cc.ref, layer, 0, n, p(kt), p(vt), H * hd, S.DTYPE_F16))
+    else:
+        kt, vt = dev(k16.view(np.uint16)), dev(v16.view(np.uint16))  # both alive through the launch
+        S.check(S.lib().sp_hip_write_all(cc.ref, 0, n, p(kt), p(vt), S.DTYPE_F16))
+    torch.cuda.synchronize()
+    kc = d2h(cc.c.d_k_cache, L_ * H * max_seq * 58).reshape(L_ * H, max_seq, 58)
+    vc = d2h(cc.c.d_v_cache, L_ * H * max_seq * 62).reshape(L_ * H, max_seq, 62)
+    for slot in range(L_ * H):
+        kref = O.ship_compress_f16(k16[slot].view(np.uint16), kbc, order)
+        vref = O.ship_compress_f16(v16[slot].view(np.uint16), vbc)
+        np.testing.assert_array_equal(kc[slot, :n], kref, err_msg=f"K codes slot {slot}")
+        np.testing.assert_array_equal(vc[slot, :n], vref, err_msg=f"V codes slot {slot}")
+    for dtype in (S.DTYPE_F16, S.DTYPE_F32):
+        mk = empty_f16 if dtype == S.DTYPE_F16 else empty_f32
+        hdt = np.uint16 if dtype == S.DTYPE_F16 else np.uint32
+        if strided:
+            for layer in range(L_):
+                kl, vl = mk(n * H * hd), mk(n * H * hd)
+                S.check(S.lib().sp_hip_read_layer(cc.ref, layer, 0, n, p(kl), p(vl), H * hd, dtype, -1))
+                ka = host(kl, hdt).reshape(n, H, hd).transpose(1, 0, 2)
+                va = host(vl, hdt).reshape(n, H, hd).transpose(1, 0, 2)
+                if layer == 0:
+                    kall, vall = [ka], [va]
+                else:
+                    kall.append(ka)
+                    vall.append(va)
+            kg, vg = np.concatenate(kall), np.concatenate(vall)
+        else:
+            ko, vo = mk(L_ * H * n * hd), mk(L_ * H * n * hd)
+            S.check(S.lib().sp_hip_read_all(cc.ref, 0, n, p(ko), p(vo), dtype, -1))
+            kg, vg = host(ko, hdt).reshape(L_ * H, n, hd), host(vo, hdt).reshape(L_ * H, n, hd)
+        for slot in range(L_ * H):
+            if dtype == S.DTYPE_F16:
+                kr = O.ship_decompress_f16(kc[slot, :n], kbc, order)
+                vr = O.ship_decompress_f16(vc[slot, :n], vbc)
+            else:
+                kr = O.ship_decompress_f32(kc[slot, :n], kbc, order).view(np.uint32)
+                vr = O.ship_decompress_f32(vc[slot, :n], vbc).view(np.uint32)
+            np.testing.assert_array_equal(kg[slot], kr, err_msg=f"K recon slot {slot} dtype {dtype}")
+            np.testing.assert_array_equal(vg[slot], vr, err_msg=f"V recon slot {slot} dtype {dtype}")
+    cc.free()
+
+
 def test_cache_slots_layer_and_all_layouts():
     """sp_hip_write_layer / read_layer (llama cache rows) and write_all / read_all agree with
     the oracle for every slot, including odd start positions (unaligned V records)."""
