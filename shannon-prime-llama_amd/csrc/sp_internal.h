@@ -190,6 +190,14 @@ struct SpHierGeo {
     long long w_outer;       // elements between consecutive outer slots' W
 };
 
+// one-vector-per-lane sqfree kernels for the shipping geometry; hipErrorNotSupported
+// (nothing launched) when no specialization fits
+hipError_t sp_launch_sqfree_encode_lane(const SpPlan &P, const SpSqGeo &G, const void *src, int dtype, long long so,
+                                        long long si, unsigned char *dst, long long dout, int n_outer, int n_inner,
+                                        hipStream_t s);
+hipError_t sp_launch_sqfree_decode_lane(const SpPlan &P, const SpSqGeo &G, const unsigned char *src, long long so,
+                                        void *dst, int dtype, long long dout, long long din, int n_outer,
+                                        int n_inner, hipStream_t s);
 hipError_t sp_launch_sqfree_encode(const SpPlan &P, const SpSqGeo &G, const void *src, int dtype,
                                    long long so, long long si, unsigned char *dst, long long dout,
                                    int n_outer, int n_inner, hipStream_t s);

@@ -1,0 +1,582 @@
+// sp_lane.h -- device building blocks of the one-vector-per-lane codec kernels:
+// compile-time band layouts and the Mobius order, register transforms (p = 2
+// VHT2 and the staged Vilenkin-Hartley transform), record bit fields, band
+// quantize/dequantize, 64-row tiles moved through LDS with coalesced buffer
+// loads and stores, and the host-side launch helpers they share.
+#pragma once
+#include <algorithm>
+
+#include "sp_internal.h"
+
+namespace {
+
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+typedef float float2v __attribute__((ext_vector_type(2)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+constexpr uint32_t BUF_WORD3 = 0x00020000u;  // raw buffer resource, dword data (gfx9 family)
+constexpr int BUF_NT = 2;                    // non-temporal load policy
+
+// Raw buffer over [p, p + nbytes): loads past nbytes return 0 (the range check
+// covers the vector, scalar and immediate offsets alike).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, int nbytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, nbytes, BUF_WORD3);
+}
+
+constexpr bool c_squarefree(int n) {
+    for (int p = 2; p * p <= n; p++)
+        if (n % (p * p) == 0) return false;
+    return true;
+}
+
+// Squarefree-first order (i+1 squarefree ascending, then the rest ascending):
+// the same table the host builds for d_mobius_order.
+template <int N>
+struct MobOrder {
+    int v[N];
+    constexpr MobOrder() : v() {
+        int r = 0;
+        for (int i = 0; i < N; i++)
+            if (c_squarefree(i + 1)) v[r++] = i;
+        for (int i = 0; i < N; i++)
+            if (!c_squarefree(i + 1)) v[r++] = i;
+    }
+};
+template <int N>
+__device__ constexpr MobOrder<N> kMob{};
+
+// coefficient feeding reordered position r (identity without Mobius)
+template <int HD, bool MOB>
+__device__ __forceinline__ constexpr int src_idx(int r) { return MOB ? kMob<HD>.v[r] : r; }
+
+template <int HD, int... BITS>
+struct Layout {
+    static constexpr int hd = HD;
+    static constexpr int nb = sizeof...(BITS);
+    static constexpr int bits[nb] = {BITS...};
+    static constexpr int bsz = HD / nb;
+    static constexpr int off(int b) { return b * bsz; }
+    static constexpr int sz(int b) { return b == nb - 1 ? HD - b * bsz : bsz; }
+    static constexpr int byte_off(int b) {
+        int o = 0;
+        for (int i = 0; i < b; i++) o += 2 + (sz(i) * bits[i] + 7) / 8;
+        return o;
+    }
+    static constexpr int total = byte_off(nb);
+    static constexpr int dwords = (total + 3) / 4;
+};
+
+constexpr int c_log2(int n) { return n <= 1 ? 0 : 1 + c_log2(n / 2); }
+
+// Insert / extract a field of width w at bit position pos of the record
+// dwords. Called from fully unrolled loops, so pos and w fold to constants.
+template <int DW>
+__device__ __forceinline__ void rec_insert(uint32_t (&rec)[DW], int pos, int w, uint32_t val) {
+    const int d = pos / 32, sh = pos % 32;
+    rec[d] |= val << sh;
+    if (sh + w > 32) rec[d + 1] |= val >> (32 - sh);
+}
+
+// Overwrite the w-bit field at bit position pos with val (val < 2^w).
+template <int DW>
+__device__ __forceinline__ void rec_replace(uint32_t (&rec)[DW], int pos, int w, uint32_t val) {
+    const int d = pos / 32, sh = pos % 32;
+    const uint32_t mask = (1u << w) - 1u;
+    rec[d] = (rec[d] & ~(mask << sh)) | (val << sh);
+    if (sh + w > 32) rec[d + 1] = (rec[d + 1] & ~(mask >> (32 - sh))) | (val >> (32 - sh));
+}
+
+// Insert the low w bits of v (higher bits are ignored) at bit position pos:
+// one shift and one three-input bit operation (v << sh) & mask | rec.
+template <int DW>
+__device__ __forceinline__ void rec_insert_low(uint32_t (&rec)[DW], int pos, int w, uint32_t v) {
+    const int d = pos / 32, sh = pos % 32;
+    const uint32_t mask = (1u << w) - 1u;
+    rec[d] = __builtin_amdgcn_bitop3_b32(v << sh, mask << sh, rec[d], 0xEA);
+    if (sh + w > 32) rec[d + 1] = __builtin_amdgcn_bitop3_b32(v >> (32 - sh), mask >> (32 - sh), rec[d + 1], 0xEA);
+}
+
+// fp16 pair (lo, hi) of w -> (lo + hi, lo - hi) in fp32: v_fma_mix widens each
+// half exactly and rounds once, the same result as convert-then-add.
+__device__ __forceinline__ void bfly_f16_pair(uint32_t w, float &s, float &d) {
+    __asm__("v_fma_mix_f32 %0, %2, 1.0, %2 op_sel:[0,0,1] op_sel_hi:[1,0,1]\n\t"
+            "v_fma_mix_f32 %1, %2, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[1,0,1]"
+            : "=&v"(s), "=v"(d)
+            : "v"(w));
+}
+
+template <int DW>
+__device__ __forceinline__ uint32_t rec_extract(const uint32_t (&rec)[DW], int pos, int w) {
+    const int d = pos / 32, sh = pos % 32;
+    const uint32_t mask = (1u << w) - 1u;
+    if (sh + w <= 32) return (rec[d] >> sh) & mask;
+    return __builtin_amdgcn_alignbit(rec[d + 1], rec[d], sh) & mask;
+}
+
+// p=2 VHT2 over a register-resident vector: stages len = 1, 2, ..., HD/2 in
+// order (the stage order fixes the fp32 rounding), then the final 1/sqrt(n)
+// multiply (NORM 0) or per-stage 1/sqrt(2) (NORM 1).
+template <int HD, int NORM>
+__device__ __forceinline__ void vht2_reg(float (&x)[HD], float inv_sqrt_n, bool first_done) {
+    const float s2 = 0.70710678118654752440f;
+#pragma unroll
+    for (int len = first_done ? 2 : 1; len < HD; len <<= 1) {
+#pragma unroll
+        for (int k = 0; k < HD / 2; k++) {
+            const int i = (k / len) * 2 * len + (k % len);
+            const float u = x[i], v = x[i + len];
+            if (NORM == 1) {
+                x[i] = (u + v) * s2;
+                x[i + len] = (u - v) * s2;
+            } else {
+                x[i] = u + v;
+                x[i + len] = u - v;
+            }
+        }
+    }
+    if (NORM == 0) {
+#pragma unroll
+        for (int i = 0; i < HD; i++) x[i] *= inv_sqrt_n;
+    }
+}
+
+// ---- staged Vilenkin-Hartley transform for non-power-of-two lengths ----
+// Constants of the transforms, passed by value (they land in scalar registers):
+// cas[pi][m] = (float)(cos(2*pi*m/p) + sin(2*pi*m/p)) and isp[pi] = 1.0f/sqrtf(p)
+// for p = 2, 3, 5, 7, 11 (pi = 0..4), exactly the values of the host plan.
+struct XfConst {
+    float inv_sqrt_n;
+    float isp[5];
+    float cas[5][11];
+};
+
+constexpr int c_prime(int i) { return i == 0 ? 2 : i == 1 ? 3 : i == 2 ? 5 : i == 3 ? 7 : 11; }
+constexpr int c_prime_idx(int p) { return p == 2 ? 0 : p == 3 ? 1 : p == 5 ? 2 : p == 7 ? 3 : 4; }
+constexpr bool c_pow2(int n) { return n > 0 && (n & (n - 1)) == 0; }
+
+// prime factors of N among {2, 3, 5, 7, 11}, ascending with multiplicity
+template <int N>
+struct Factors {
+    int p[16];
+    int n;
+    int rest;
+    constexpr Factors() : p(), n(0), rest(N) {
+        for (int i = 0; i < 5; i++)
+            while (rest % c_prime(i) == 0 && n < 16) {
+                p[n++] = c_prime(i);
+                rest /= c_prime(i);
+            }
+    }
+};
+
+// One stage with prime P at stride S (kernel_vilenkin_inplace order,
+// shannon_prime_sqfree.cu:66-106): each group {base + k*S} becomes
+// r[k] = (sum_j C[k][j] * g[j]) * (1/sqrt(P)), the sum running from 0.0f over j
+// ascending with separately rounded products and adds. C[k][0] = C[0][j] = 1
+// exactly and C = -1 exactly for P = 2 (the host checks), so those products are
+// the value itself; 0.0f + g[0] is kept (it maps -0 to +0 as the reference does).
+template <int N, int P, int S>
+__device__ __forceinline__ void vil_stage(float (&x)[N], const XfConst &K) {
+    constexpr int PI = c_prime_idx(P), BLOCK = S * P;
+    const float isp = K.isp[PI];
+#pragma unroll
+    for (int blk = 0; blk < N / BLOCK; blk++) {
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            const int base = blk * BLOCK + s;
+            float g[P];
+#pragma unroll
+            for (int k = 0; k < P; k++) g[k] = x[base + k * S];
+            const float z = 0.0f + g[0];
+#pragma unroll
+            for (int k = 0; k < P; k++) {
+                float sum = z;
+#pragma unroll
+                for (int j = 1; j < P; j++) {
+                    const int m = (k * j) % P;
+                    if (m == 0) sum = sum + g[j];
+                    else if (P == 2) sum = sum - g[j];
+                    else sum = sum + K.cas[PI][m] * g[j];
+                }
+                x[base + k * S] = sum * isp;
+            }
+        }
+    }
+}
+
+template <int N, int FI, int S>
+__device__ __forceinline__ void vil_stages(float (&x)[N], const XfConst &K) {
+    constexpr Factors<N> F{};
+    if constexpr (FI < F.n) {
+        constexpr int P = F.p[FI];
+        vil_stage<N, P, S>(x, K);
+        vil_stages<N, FI + 1, S * P>(x, K);
+    }
+}
+
+// First stage (P = 2, stride 1) straight from fp16 pairs: v_fma_mix widens
+// exactly and rounds once, so z = lo + 0.0f, r0 = z + hi, r1 = z - hi match
+// the fp32 stage bit for bit.
+__device__ __forceinline__ void vil_first_f16_pair(uint32_t w, float isp, float &r0, float &r1) {
+    float z, a, b;
+    __asm__("v_fma_mix_f32 %0, %1, 1.0, 0 op_sel_hi:[1,0,0]" : "=v"(z) : "v"(w));
+    __asm__("v_fma_mix_f32 %0, %2, 1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+            "v_fma_mix_f32 %1, -%2, 1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+            : "=&v"(a), "=v"(b)
+            : "v"(w), "v"(z));
+    r0 = a * isp;
+    r1 = b * isp;
+}
+
+__device__ __forceinline__ uint32_t f16_normal(uint32_t h) {
+    const uint32_t e = h & 0x7c00u;
+    return e != 0u && e != 0x7c00u;
+}
+
+template <int DT>
+constexpr int row_bytes(int hd) { return hd * (DT == SP_DT_F16 ? 2 : 4); }
+
+
+// Chunk k of lane j of a 64-row tile moved with wave-wide 16-byte accesses:
+// chunk 64k + j is row (64k + j) / CPR, column (64k + j) % CPR. When CPR
+// divides 64 the row offset splits into a lane part (vector offset) and a
+// uniform part k * (64 / CPR) rows (scalar offset); otherwise the whole
+// offset is per lane.
+template <int CPR>
+struct TileChunk {
+    int row, col, krow;
+    __device__ __forceinline__ TileChunk(int k, int lane) {
+        if (64 % CPR == 0) {
+            row = lane / CPR, col = lane % CPR, krow = k * (64 / CPR);
+        } else {
+            const int c = 64 * k + lane;
+            row = c / CPR, col = c % CPR, krow = 0;
+        }
+    }
+    __device__ __forceinline__ int vofs(int rowb) const { return row * rowb + col * 16; }
+    __device__ __forceinline__ int sofs(int rowb) const { return krow * rowb; }
+    __device__ __forceinline__ int lds(int rp) const { return (row + krow) * rp + col * 16; }
+};
+
+struct TileMap {
+    int tpo;      // tiles per outer row
+    int n_inner;
+    __device__ __forceinline__ void at(int t, int &o, int &i0, int &nvalid) const {
+        o = t / tpo;
+        i0 = (t - o * tpo) * 64;
+        nvalid = min(64, n_inner - i0);
+    }
+};
+
+
+// Band-quantize coefficients x[src_idx(r)], r in [0, LY::hd), into the record
+// bits [0, 8 * LY::total) of rec (which must start zeroed there):
+// kernel_band_quantize_simple (shannon_prime_cuda.cu:131-204). fastv: every
+// coefficient is finite (the fast path's precondition).
+template <class LY, bool MOB, int N, int DWR>
+__device__ __forceinline__ void quant_bands(const float (&x)[N], bool fastv, uint32_t (&rec)[DWR]) {
+    constexpr int HD = LY::hd;
+    static_assert(DWR >= LY::dwords && N >= HD, "record and vector must hold the layout");
+#pragma unroll
+    for (int b = 0; b < LY::nb; b++) {
+        const int off = LY::off(b), sz = LY::sz(b), bits = LY::bits[b];
+        const int maxv = (1 << (bits - 1)) - 1, bo = LY::byte_off(b);
+        float amax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < sz; e++) amax = fmaxf(amax, fabsf(x[src_idx<HD, MOB>(off + e)]));
+        const float scale = (amax > 0.0f) ? sp_div(amax, (float)maxv) : 0.0f;
+        // Fast path for every lane: the hardware conversion is IEEE round-to-nearest-even
+        // for finite scales, and for a normal fp16 scale |x*inv| < maxv + 1/2, so
+        // t = x*inv + 1.5*2^23 rounds x*inv to the nearest integer q with ties to even (the
+        // added constant is even) and bits(t) = 0x4B400000 + q: the low bits of
+        // bits(t) + maxv are the code q + maxv. Lanes outside those conditions redo the
+        // band below (a rare, divergent branch that only overwrites fields, so both
+        // sides define every record word).
+        float sc = scale;
+        __asm__ volatile("" : "+v"(sc));  // keep the division and the conversion apart
+        const uint32_t hf = (uint32_t)__builtin_bit_cast(unsigned short, (_Float16)sc);
+        {
+            const float ss = sp_f16_bits_to_f32(hf);
+            const float inv = (ss > 0.0f) ? sp_div(1.0f, ss) : 0.0f;
+            rec_insert_low(rec, 8 * bo, 16, hf);
+#pragma unroll
+            for (int e = 0; e < sz; e++) {
+                const float t = x[src_idx<HD, MOB>(off + e)] * inv + 12582912.0f;
+                rec_insert_low(rec, 8 * (bo + 2) + e * bits, bits, __float_as_uint(t) + (uint32_t)maxv);
+            }
+        }
+        if (!(fastv && f16_normal(hf))) {
+            const uint32_t h = sp_f32_to_f16_bits(scale);
+            const float ss = sp_f16_bits_to_f32(h);
+            const float inv = (ss > 0.0f) ? sp_div(1.0f, ss) : 0.0f;
+            rec_replace(rec, 8 * bo, 16, h);
+#pragma unroll
+            for (int e = 0; e < sz; e++) {
+                const int q = sp_q_rint_clamp(x[src_idx<HD, MOB>(off + e)] * inv, maxv);
+                rec_replace(rec, 8 * (bo + 2) + e * bits, bits, (uint32_t)(q + maxv));
+            }
+        }
+    }
+}
+
+// Dequantize the record's bands into x[src_idx(r)] (bands >= max_bands read as
+// 0 unless FULL): kernel_band_dequantize_simple (shannon_prime_cuda.cu:210-270)
+// with the partial-read rule of shannon_prime_llama.h:240-255.
+template <class LY, bool MOB, bool FULL, int N, int DWR>
+__device__ __forceinline__ void dequant_bands(const uint32_t (&rec)[DWR], int max_bands, float (&x)[N]) {
+    constexpr int HD = LY::hd;
+    static_assert(DWR >= LY::dwords && N >= HD, "record and vector must hold the layout");
+#pragma unroll
+    for (int b = 0; b < LY::nb; b++) {
+        const int off = LY::off(b), sz = LY::sz(b), bits = LY::bits[b];
+        const int maxv = (1 << (bits - 1)) - 1, bo = LY::byte_off(b);
+        const bool live = FULL || b < max_bands;  // FULL: every band is read
+        const float scale = live ? sp_scale_from_bits(rec_extract(rec, 8 * bo, 16)) : 0.0f;
+        const float bias = 12582912.0f + (float)maxv;
+#pragma unroll
+        for (int e = 0; e < sz; e++) {
+            const uint32_t u = rec_extract(rec, 8 * (bo + 2) + e * bits, bits);
+            const float d = __uint_as_float(u | 0x4B400000u) - bias;  // (float)(u - maxv), exact
+            x[src_idx<HD, MOB>(off + e)] = live ? d * scale : 0.0f;
+        }
+    }
+}
+
+// A tile's records (64 contiguous records of B bytes) with coalesced 16-byte
+// loads: load k of lane j reads bytes [16(64k+j), 16(64k+j)+16). The raw
+// buffer covers the valid records only; a tile index past the last tile gives
+// an empty range, so the prefetch is issued unconditionally and reads nothing.
+// The range check drops every dword that does not end inside the range, so
+// when the valid bytes end 2 bytes into a dword (B = 2 mod 4 and an odd count
+// of records) those 2 bytes come from an exactly range-checked 2-byte load,
+// `tail`, which the caller writes into LDS after the chunks.
+template <class LY>
+struct RecTile {
+    static constexpr int NCK = (64 * LY::total / 16 + 63) / 64;
+    u32x4 pre[NCK];
+    uint32_t tail;
+};
+
+template <class LY>
+__device__ __forceinline__ void rec_tile_load(RecTile<LY> &R, const unsigned char *src, long long so,
+                                              const TileMap &M, int t, int n_tiles, int lane) {
+    constexpr int B = LY::total;
+    int o, i0, nv;
+    M.at(t, o, i0, nv);
+    if (t >= n_tiles) o = 0, i0 = 0, nv = 0;
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(src + (long long)o * so + (long long)i0 * B, nv * B);
+#pragma unroll
+    for (int k = 0; k < RecTile<LY>::NCK; k++)
+        R.pre[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16, k * 1024, BUF_NT);
+    if (B % 4 != 0) R.tail = __builtin_amdgcn_raw_buffer_load_b16(rs, nv > 0 ? nv * B - 2 : 0, 0, BUF_NT);
+}
+
+// Stage tile t's records into LDS (chunks, then the 2-byte tail).
+template <class LY>
+__device__ __forceinline__ void rec_tile_stage(const RecTile<LY> &R, unsigned char *stage, const TileMap &M, int t,
+                                               int lane) {
+    constexpr int B = LY::total;
+#pragma unroll
+    for (int k = 0; k < RecTile<LY>::NCK; k++) *reinterpret_cast<u32x4 *>(stage + k * 1024 + lane * 16) = R.pre[k];
+    if (B % 4 != 0) {
+        int o, i0, nv;
+        M.at(t, o, i0, nv);
+        if (lane == 0) *reinterpret_cast<unsigned short *>(stage + nv * B - 2) = (unsigned short)R.tail;
+    }
+}
+
+// The lane's own record out of the tile staged in LDS: dword reads at a stride
+// of B bytes (B/4 odd for the 76-byte K records: no bank conflicts).
+template <class LY>
+__device__ __forceinline__ void rec_from_lds(uint32_t (&rec)[LY::dwords], const unsigned char *stage, int lane) {
+    constexpr int B = LY::total, DW = LY::dwords;
+    if (B % 4 == 0) {
+        const uint32_t *p = reinterpret_cast<const uint32_t *>(stage + lane * B);
+#pragma unroll
+        for (int d = 0; d < DW; d++) rec[d] = p[d];
+    } else {
+        // 2-byte aligned records: read the covering dwords and funnel-shift odd lanes by 16 bits
+        const int a = lane * B;
+        const uint32_t *p = reinterpret_cast<const uint32_t *>(stage + (a & ~3));
+        const uint32_t sh = (a & 2) * 8;
+        uint32_t w[DW + 1];
+#pragma unroll
+        for (int d = 0; d <= DW; d++) w[d] = p[d];
+#pragma unroll
+        for (int d = 0; d < DW; d++) rec[d] = __builtin_amdgcn_alignbit(w[d + 1], w[d], sh);
+        if (B % 4 != 0) rec[DW - 1] &= 0xffffu;
+    }
+}
+
+// Tile t's input rows (64 rows of HD values, row i0 + j at (o*so + (i0+j)*si)
+// elements from src) into LDS rows padded to RB + 16 bytes, then lane j's row
+// into in[]: wave-wide 16-byte buffer loads (rows past the tile's valid ones
+// read as 0) and bank-conflict-free LDS row reads.
+template <int DT, int HD>
+__device__ __forceinline__ void tile_rows_in(const void *src, long long so, long long si, const TileMap &M, int t,
+                                             int lane, unsigned char *rows, uint4 (&in)[row_bytes<DT>(HD) / 16]) {
+    constexpr int RB = row_bytes<DT>(HD), RP = RB + 16, CPR = RB / 16, esz = DT == SP_DT_F16 ? 2 : 4;
+    const int rowb = (int)(si * esz);  // launchers keep 64 rows of offsets in 32 bits
+    int o, i0, nv;
+    M.at(t, o, i0, nv);
+    const unsigned char *g = reinterpret_cast<const unsigned char *>(src) + ((long long)o * so + (long long)i0 * si) * esz;
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(g, (nv - 1) * rowb + RB);
+    u32x4 v[CPR];
+#pragma unroll
+    for (int k = 0; k < CPR; k++) {
+        const TileChunk<CPR> ch(k, lane);
+        v[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, ch.vofs(rowb), ch.sofs(rowb), BUF_NT);
+    }
+#pragma unroll
+    for (int k = 0; k < CPR; k++) {
+        const TileChunk<CPR> ch(k, lane);
+        *reinterpret_cast<u32x4 *>(rows + ch.lds(RP)) = v[k];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < CPR; c++) in[c] = *reinterpret_cast<const uint4 *>(rows + lane * RP + c * 16);
+}
+
+// Tile t's records (lane j's record of B bytes in rec) out to dst: staged in
+// LDS (stage holds LDSB bytes and may alias the input rows: the first barrier
+// orders every lane's row reads before the stage writes), then wave-wide
+// 16-byte stores over the whole 16-byte chunks and one 2-byte store per lane
+// over the rest. Each raw buffer's range drops the stores past its end, so the
+// store count is the same for every tile.
+template <int B, int LDSB, int DWR>
+__device__ __forceinline__ void tile_records_out(const uint32_t (&rec)[DWR], unsigned char *stage, unsigned char *dst,
+                                                 long long dout, const TileMap &M, int t, int lane) {
+    constexpr int NCK = (64 * B / 16 + 63) / 64;
+    static_assert(B % 2 == 0, "record bytes must be even");
+    static_assert(DWR * 4 >= B, "record registers must hold the record");
+    static_assert(NCK * 1024 <= LDSB && 64 * B + 128 <= LDSB, "stage reads stay in the stage");
+    int o, i0, nvalid;
+    M.at(t, o, i0, nvalid);
+    __syncthreads();
+    if (lane < nvalid) {
+        unsigned char *p = stage + lane * B;
+        if (B % 4 == 0) {
+#pragma unroll
+            for (int d = 0; d < B / 4; d++) *reinterpret_cast<uint32_t *>(p + 4 * d) = rec[d];
+        } else {
+#pragma unroll
+            for (int hw = 0; hw < B / 2; hw++)
+                *reinterpret_cast<unsigned short *>(p + 2 * hw) = (unsigned short)(rec[hw / 2] >> (16 * (hw % 2)));
+        }
+    }
+    __syncthreads();
+    unsigned char *gdst = dst + (long long)o * dout + (long long)i0 * B;
+    const int nbytes = nvalid * B, nfull = nbytes & ~15;
+    const __amdgpu_buffer_rsrc_t ws = buf_rsrc(gdst, nfull);
+#pragma unroll
+    for (int k = 0; k < NCK; k++) {
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(stage + k * 1024 + lane * 16);
+        __builtin_amdgcn_raw_buffer_store_b128(v, ws, lane * 16, k * 1024, BUF_NT);
+    }
+    const __amdgpu_buffer_rsrc_t wt = buf_rsrc(gdst + nfull, nbytes - nfull);
+    const unsigned short h = *reinterpret_cast<const unsigned short *>(stage + nfull + 2 * lane);
+    __builtin_amdgcn_raw_buffer_store_b16(h, wt, lane * 2, 0, BUF_NT);
+}
+
+// Tile t's output rows (lane j's vector x[0, HD)) out to dst (row i0 + j at
+// (o*dout + (i0+j)*din) elements): converted (fp16: one packed IEEE
+// round-to-nearest-even conversion per pair) into LDS rows padded to RB + 16
+// bytes, then wave-wide 16-byte buffer stores whose range check drops rows past
+// the tile's valid ones. The first barrier orders the previous tile's stage
+// reads before these writes.
+template <int DT, int HD, int N>
+__device__ __forceinline__ void tile_rows_out(const float (&x)[N], unsigned char *stage, void *dst, long long dout,
+                                              long long din, const TileMap &M, int t, int lane) {
+    constexpr int RB = row_bytes<DT>(HD), RP = RB + 16, CPR = RB / 16, esz = DT == SP_DT_F16 ? 2 : 4;
+    static_assert(N >= HD, "vector must hold the row");
+    int o, i0, nvalid;
+    M.at(t, o, i0, nvalid);
+    __syncthreads();
+    if (DT == SP_DT_F16) {
+#pragma unroll
+        for (int c = 0; c < HD / 8; c++) {
+            uint32_t w[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                float2v ab = {x[c * 8 + 2 * k], x[c * 8 + 2 * k + 1]};
+                __asm__ volatile("" : "+v"(ab));  // no multiply-into-convert fusion
+                w[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(ab, half2v));
+            }
+            *reinterpret_cast<uint4 *>(stage + lane * RP + c * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < HD / 4; c++)
+            *reinterpret_cast<float4 *>(stage + lane * RP + c * 16) =
+                make_float4(x[c * 4], x[c * 4 + 1], x[c * 4 + 2], x[c * 4 + 3]);
+    }
+    __syncthreads();
+    const int rowb = (int)(din * esz);  // launchers keep 64 rows of offsets in 32 bits
+    unsigned char *gdst = reinterpret_cast<unsigned char *>(dst) + ((long long)o * dout + (long long)i0 * din) * esz;
+    const __amdgpu_buffer_rsrc_t ws = buf_rsrc(gdst, (nvalid - 1) * rowb + RB);
+#pragma unroll
+    for (int k = 0; k < CPR; k++) {
+        const TileChunk<CPR> ch(k, lane);
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(stage + ch.lds(RP));
+        __builtin_amdgcn_raw_buffer_store_b128(v, ws, ch.vofs(rowb), ch.sofs(rowb), BUF_NT);
+    }
+}
+
+// ---- host side ----
+// Persistent grid size: enough single-wave blocks for several resident waves
+// per SIMD on every CU (queried once per process).
+int persistent_blocks() {
+    static int n = 0;
+    if (n == 0) {
+        int dev = 0, cus = 256;
+        if (hipGetDevice(&dev) == hipSuccess) {
+            hipDeviceProp_t prop;
+            if (hipGetDeviceProperties(&prop, dev) == hipSuccess && prop.multiProcessorCount > 0)
+                cus = prop.multiProcessorCount;
+        }
+        n = cus * 16;
+    }
+    return n;
+}
+
+// Kernel constants from the host plan: cas[pi][m] is row 1 of the plan's p x p
+// table (C[1][m] = cas(2*pi*m/p)), which holds every value C[k][j] takes.
+XfConst xf_const(const SpPlan &P) {
+    static const int primes[5] = {2, 3, 5, 7, 11};
+    static const int offs[5] = {SP_CAS_OFF2, SP_CAS_OFF3, SP_CAS_OFF5, SP_CAS_OFF7, SP_CAS_OFF11};
+    XfConst K{};
+    K.inv_sqrt_n = P.inv_sqrt_n;
+    for (int pi = 0; pi < 5; pi++) {
+        K.isp[pi] = P.isp[pi];
+        for (int m = 0; m < primes[pi]; m++) K.cas[pi][m] = P.cas[offs[pi] + primes[pi] + m];
+    }
+    return K;
+}
+
+// The register Vilenkin stages take C = 1 for k*j = 0 (mod p) and C = -1 for
+// p = 2, k*j = 1 as exact; the host plan's values must be exactly those.
+bool vil_consts_exact(const SpPlan &P) {
+    static const int primes[5] = {2, 3, 5, 7, 11};
+    static const int offs[5] = {SP_CAS_OFF2, SP_CAS_OFF3, SP_CAS_OFF5, SP_CAS_OFF7, SP_CAS_OFF11};
+    for (int pi = 0; pi < 5; pi++) {
+        const int p = primes[pi];
+        for (int k = 0; k < p; k++)
+            for (int j = 0; j < p; j++)
+                if ((k * j) % p == 0 && P.cas[offs[pi] + k * p + j] != 1.0f) return false;
+    }
+    return P.cas[SP_CAS_OFF2 + 3] == -1.0f;
+}
+
+template <class LY>
+bool layout_matches(const SpPlan &P) {
+    if (P.hd != LY::hd || P.n_bands != LY::nb || P.total_bytes != LY::total) return false;
+    if (P.skip_transform) return false;
+    if (!c_pow2(LY::hd) && !vil_consts_exact(P)) return false;
+    for (int b = 0; b < LY::nb; b++)
+        if (P.band_bits[b] != LY::bits[b]) return false;
+    return true;
+}
+
+}  // namespace

@@ -11,6 +11,8 @@
 // Hier write: pad -> Vilenkin -> skeleton gather -> band quantize -> fp16 W
 // GEMV prediction -> deviation -> mag -> rint levels -> pack. Record:
 // [skeleton bands][mag f32 LE][residual bits] (shannon_prime_hier.cu:331-335).
+#include <stdlib.h>
+
 #include "sp_internal.h"
 
 __device__ __forceinline__ void sp_pad_mean(float *c, int hd, int pad, int lane) {
@@ -263,11 +265,26 @@ static bool sq_fits(const SpPlan &P, int pad, int bytes) {
     return pad <= SP_GEN_MAX_N && P.hd <= SP_GEN_MAX_N && bytes + 8 <= SP_GEN_MAX_REC;
 }
 
+// SP_HIP_NO_LANE_KERNELS=1 routes the sqfree geometry with a lane specialization
+// through the one-vector-per-wave kernels (used by tests to cross-check them).
+static bool getenv_lane_off_sq() {
+    static int v = -1;
+    if (v < 0) {
+        const char *e = getenv("SP_HIP_NO_LANE_KERNELS");
+        v = (e && e[0] == '1') ? 1 : 0;
+    }
+    return v == 1;
+}
+
 hipError_t sp_launch_sqfree_encode(const SpPlan &P, const SpSqGeo &G, const void *src, int dtype,
                                    long long so, long long si, unsigned char *dst, long long dout,
                                    int n_outer, int n_inner, hipStream_t s) {
     if (n_outer <= 0 || n_inner <= 0) return hipSuccess;
     if (!sq_fits(P, G.pad, G.bytes)) return hipErrorInvalidValue;
+    if (!getenv_lane_off_sq()) {
+        const hipError_t e = sp_launch_sqfree_encode_lane(P, G, src, dtype, so, si, dst, dout, n_outer, n_inner, s);
+        if (e != hipErrorNotSupported) return e;
+    }
     const long long nv = (long long)n_outer * n_inner;
     const dim3 grid((unsigned)((nv + 3) / 4)), block(256);
     if (dtype == SP_DT_F16)
@@ -282,6 +299,10 @@ hipError_t sp_launch_sqfree_decode(const SpPlan &P, const SpSqGeo &G, const unsi
                                    long long din, int n_outer, int n_inner, hipStream_t s) {
     if (n_outer <= 0 || n_inner <= 0) return hipSuccess;
     if (!sq_fits(P, G.pad, G.bytes)) return hipErrorInvalidValue;
+    if (!getenv_lane_off_sq()) {
+        const hipError_t e = sp_launch_sqfree_decode_lane(P, G, src, so, dst, dtype, dout, din, n_outer, n_inner, s);
+        if (e != hipErrorNotSupported) return e;
+    }
     const long long nv = (long long)n_outer * n_inner;
     const dim3 grid((unsigned)((nv + 3) / 4)), block(256);
     if (dtype == SP_DT_F16)

@@ -66,6 +66,10 @@ def test_sqfree_bit_exact(hd, bits, rbits, spinor, sk_frac):
     S.check(S.lib().sp_hip_sqfree_read_batch(cc.ref, 0, 0, 0, 0, n, p(out), S.DTYPE_F32))
     g = host(out).reshape(n, hd)
     np.testing.assert_array_equal(g.view(np.uint32), rec.view(np.uint32))
+    # fp16 reads: the fp32 reconstruction rounded to nearest even
+    out16 = torch.empty(n * hd, dtype=torch.float16, device="cuda")
+    S.check(S.lib().sp_hip_sqfree_read_batch(cc.ref, 0, 0, 0, 0, n, p(out16), S.DTYPE_F16))
+    np.testing.assert_array_equal(host(out16).reshape(n, hd).view(np.uint16), rec.astype(np.float16).view(np.uint16))
     corr = np.mean([O.correlation(a, b) for a, b in zip(k16.reshape(n, hd).astype(np.float32), g)])
     assert corr > 0.9, corr
     cc.free()
