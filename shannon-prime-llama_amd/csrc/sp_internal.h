@@ -188,7 +188,17 @@ struct SpHierGeo {
     const int *skel_idx, *target_idx;
     const uint16_t *W;       // slot 0 predictor
     long long w_outer;       // elements between consecutive outer slots' W
+    int default_geo;         // skeleton/targets are sp_hier_default_geometry's
 };
+
+// one-vector-per-lane hier kernels for the default geometry at head_dim 256;
+// hipErrorNotSupported (nothing launched) when no specialization fits
+hipError_t sp_launch_hier_encode_lane(const SpPlan &P, const SpHierGeo &G, const void *src, int dtype, long long so,
+                                      long long si, unsigned char *dst, long long dout, int n_outer, int n_inner,
+                                      hipStream_t s);
+hipError_t sp_launch_hier_decode_lane(const SpPlan &P, const SpHierGeo &G, const unsigned char *src, long long so,
+                                      void *dst, int dtype, long long dout, long long din, int n_outer, int n_inner,
+                                      hipStream_t s);
 
 // one-vector-per-lane sqfree kernels for the shipping geometry; hipErrorNotSupported
 // (nothing launched) when no specialization fits

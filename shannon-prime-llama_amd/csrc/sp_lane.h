@@ -115,6 +115,47 @@ __device__ __forceinline__ uint32_t rec_extract(const uint32_t (&rec)[DW], int p
     return __builtin_amdgcn_alignbit(rec[d + 1], rec[d], sh) & mask;
 }
 
+// 32-bit field at a byte offset of the record dwords (the f32 magnitude).
+template <int DW>
+__device__ __forceinline__ void rec_put32(uint32_t (&rec)[DW], int byte, uint32_t v) {
+    const int d = byte / 4, sh = 8 * (byte % 4);
+    rec[d] |= v << sh;
+    if (sh) rec[d + 1] |= v >> (32 - sh);
+}
+
+template <int DW>
+__device__ __forceinline__ uint32_t rec_get32(const uint32_t (&rec)[DW], int byte) {
+    const int d = byte / 4, sh = 8 * (byte % 4);
+    return sh ? __builtin_amdgcn_alignbit(rec[d + 1], rec[d], sh) : rec[d];
+}
+
+// Sum in the order of the reference's 256-slot block reductions over n values
+// (slot t accumulates v[t], v[t + 256] from 0.0f, then slot[t] += slot[t + s]
+// for s = 128..1); slots at or past n hold +0.0f, so adding them is skipped.
+// ABS: |v| terms (never -0, so the 0.0f start drops out). For signed terms the
+// result is the plain tree sum plus 0.0f: every difference the 0.0f starts can
+// make is the sign of a zero sum, which the final + 0.0f maps to the
+// reference's +0.
+template <int N, bool ABS>
+__device__ __forceinline__ float tree256_sum(const float *v) {
+    static_assert(N <= 512, "at most two values per slot");
+    constexpr int NS = N < 256 ? N : 256;
+    float sl[NS];
+#pragma unroll
+    for (int t = 0; t < NS; t++) sl[t] = ABS ? fabsf(v[t]) : v[t];
+#pragma unroll
+    for (int t = 0; t + 256 < N; t++) sl[t] = sl[t] + (ABS ? fabsf(v[t + 256]) : v[t + 256]);
+    int n = NS;
+#pragma unroll
+    for (int s = 128; s > 0; s >>= 1) {
+#pragma unroll
+        for (int t = 0; t < s; t++)
+            if (t + s < n) sl[t] = sl[t] + sl[t + s];
+        n = n < s ? n : s;
+    }
+    return ABS ? sl[0] : sl[0] + 0.0f;
+}
+
 // p=2 VHT2 over a register-resident vector: stages len = 1, 2, ..., HD/2 in
 // order (the stage order fixes the fp32 rounding), then the final 1/sqrt(n)
 // multiply (NORM 0) or per-stage 1/sqrt(2) (NORM 1).
@@ -349,20 +390,22 @@ __device__ __forceinline__ void dequant_bands(const uint32_t (&rec)[DWR], int ma
 // buffer covers the valid records only; a tile index past the last tile gives
 // an empty range, so the prefetch is issued unconditionally and reads nothing.
 // The range check drops every dword that does not end inside the range, so
-// when the valid bytes end 2 bytes into a dword (B = 2 mod 4 and an odd count
-// of records) those 2 bytes come from an exactly range-checked 2-byte load,
-// `tail`, which the caller writes into LDS after the chunks.
+// when the valid bytes end inside a dword (B not a multiple of 4) the last
+// bytes come from exactly range-checked narrow loads, `tail` (one 2-byte load
+// for even B, three 1-byte loads for odd B), which the caller writes into LDS
+// after the chunks.
 template <class LY>
 struct RecTile {
     static constexpr int NCK = (64 * LY::total / 16 + 63) / 64;
+    static constexpr int NT = LY::total % 4 == 0 ? 0 : (LY::total % 2 == 0 ? 1 : 3);
     u32x4 pre[NCK];
-    uint32_t tail;
+    uint32_t tail[NT > 0 ? NT : 1];
 };
 
 template <class LY>
 __device__ __forceinline__ void rec_tile_load(RecTile<LY> &R, const unsigned char *src, long long so,
                                               const TileMap &M, int t, int n_tiles, int lane) {
-    constexpr int B = LY::total;
+    constexpr int B = LY::total, NT = RecTile<LY>::NT;
     int o, i0, nv;
     M.at(t, o, i0, nv);
     if (t >= n_tiles) o = 0, i0 = 0, nv = 0;
@@ -370,20 +413,29 @@ __device__ __forceinline__ void rec_tile_load(RecTile<LY> &R, const unsigned cha
 #pragma unroll
     for (int k = 0; k < RecTile<LY>::NCK; k++)
         R.pre[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16, k * 1024, BUF_NT);
-    if (B % 4 != 0) R.tail = __builtin_amdgcn_raw_buffer_load_b16(rs, nv > 0 ? nv * B - 2 : 0, 0, BUF_NT);
+    if (NT == 1) R.tail[0] = __builtin_amdgcn_raw_buffer_load_b16(rs, nv > 0 ? nv * B - 2 : 0, 0, BUF_NT);
+    if (NT == 3) {
+#pragma unroll
+        for (int k = 0; k < 3; k++)
+            R.tail[k] = __builtin_amdgcn_raw_buffer_load_b8(rs, nv > 0 ? nv * B - 3 + k : 0, 0, BUF_NT);
+    }
 }
 
-// Stage tile t's records into LDS (chunks, then the 2-byte tail).
+// Stage tile t's records into LDS (chunks, then the tail bytes).
 template <class LY>
 __device__ __forceinline__ void rec_tile_stage(const RecTile<LY> &R, unsigned char *stage, const TileMap &M, int t,
                                                int lane) {
-    constexpr int B = LY::total;
+    constexpr int B = LY::total, NT = RecTile<LY>::NT;
 #pragma unroll
     for (int k = 0; k < RecTile<LY>::NCK; k++) *reinterpret_cast<u32x4 *>(stage + k * 1024 + lane * 16) = R.pre[k];
-    if (B % 4 != 0) {
+    if (NT > 0) {
         int o, i0, nv;
         M.at(t, o, i0, nv);
-        if (lane == 0) *reinterpret_cast<unsigned short *>(stage + nv * B - 2) = (unsigned short)R.tail;
+        if (lane == 0) {
+            if (NT == 1) *reinterpret_cast<unsigned short *>(stage + nv * B - 2) = (unsigned short)R.tail[0];
+#pragma unroll
+            for (int k = 0; k < (NT == 3 ? 3 : 0); k++) stage[nv * B - 3 + k] = (unsigned char)R.tail[k];
+        }
     }
 }
 
@@ -397,26 +449,27 @@ __device__ __forceinline__ void rec_from_lds(uint32_t (&rec)[LY::dwords], const 
 #pragma unroll
         for (int d = 0; d < DW; d++) rec[d] = p[d];
     } else {
-        // 2-byte aligned records: read the covering dwords and funnel-shift odd lanes by 16 bits
+        // unaligned records: read the covering dwords and funnel-shift by the byte offset
         const int a = lane * B;
         const uint32_t *p = reinterpret_cast<const uint32_t *>(stage + (a & ~3));
-        const uint32_t sh = (a & 2) * 8;
+        const uint32_t sh = (a & 3) * 8;
         uint32_t w[DW + 1];
 #pragma unroll
         for (int d = 0; d <= DW; d++) w[d] = p[d];
 #pragma unroll
         for (int d = 0; d < DW; d++) rec[d] = __builtin_amdgcn_alignbit(w[d + 1], w[d], sh);
-        if (B % 4 != 0) rec[DW - 1] &= 0xffffu;
+        if (B % 4 != 0) rec[DW - 1] &= (1u << (8 * (B % 4))) - 1u;
     }
 }
 
 // Tile t's input rows (64 rows of HD values, row i0 + j at (o*so + (i0+j)*si)
-// elements from src) into LDS rows padded to RB + 16 bytes, then lane j's row
-// into in[]: wave-wide 16-byte buffer loads (rows past the tile's valid ones
-// read as 0) and bank-conflict-free LDS row reads.
+// elements from src) into LDS rows padded to RB + 16 bytes (tile_rows_stage),
+// then lane j's row into in[] (tile_rows_in): wave-wide 16-byte buffer loads
+// (rows past the tile's valid ones read as 0) and bank-conflict-free LDS row
+// reads.
 template <int DT, int HD>
-__device__ __forceinline__ void tile_rows_in(const void *src, long long so, long long si, const TileMap &M, int t,
-                                             int lane, unsigned char *rows, uint4 (&in)[row_bytes<DT>(HD) / 16]) {
+__device__ __forceinline__ void tile_rows_stage(const void *src, long long so, long long si, const TileMap &M, int t,
+                                                int lane, unsigned char *rows) {
     constexpr int RB = row_bytes<DT>(HD), RP = RB + 16, CPR = RB / 16, esz = DT == SP_DT_F16 ? 2 : 4;
     const int rowb = (int)(si * esz);  // launchers keep 64 rows of offsets in 32 bits
     int o, i0, nv;
@@ -435,6 +488,13 @@ __device__ __forceinline__ void tile_rows_in(const void *src, long long so, long
         *reinterpret_cast<u32x4 *>(rows + ch.lds(RP)) = v[k];
     }
     __syncthreads();
+}
+
+template <int DT, int HD>
+__device__ __forceinline__ void tile_rows_in(const void *src, long long so, long long si, const TileMap &M, int t,
+                                             int lane, unsigned char *rows, uint4 (&in)[row_bytes<DT>(HD) / 16]) {
+    constexpr int RP = row_bytes<DT>(HD) + 16, CPR = row_bytes<DT>(HD) / 16;
+    tile_rows_stage<DT, HD>(src, so, si, M, t, lane, rows);
 #pragma unroll
     for (int c = 0; c < CPR; c++) in[c] = *reinterpret_cast<const uint4 *>(rows + lane * RP + c * 16);
 }
@@ -442,14 +502,13 @@ __device__ __forceinline__ void tile_rows_in(const void *src, long long so, long
 // Tile t's records (lane j's record of B bytes in rec) out to dst: staged in
 // LDS (stage holds LDSB bytes and may alias the input rows: the first barrier
 // orders every lane's row reads before the stage writes), then wave-wide
-// 16-byte stores over the whole 16-byte chunks and one 2-byte store per lane
-// over the rest. Each raw buffer's range drops the stores past its end, so the
-// store count is the same for every tile.
+// 16-byte stores over the whole 16-byte chunks and one 2-byte (odd B: 1-byte)
+// store per lane over the rest. Each raw buffer's range drops the stores past
+// its end, so the store count is the same for every tile.
 template <int B, int LDSB, int DWR>
 __device__ __forceinline__ void tile_records_out(const uint32_t (&rec)[DWR], unsigned char *stage, unsigned char *dst,
                                                  long long dout, const TileMap &M, int t, int lane) {
     constexpr int NCK = (64 * B / 16 + 63) / 64;
-    static_assert(B % 2 == 0, "record bytes must be even");
     static_assert(DWR * 4 >= B, "record registers must hold the record");
     static_assert(NCK * 1024 <= LDSB && 64 * B + 128 <= LDSB, "stage reads stay in the stage");
     int o, i0, nvalid;
@@ -460,10 +519,13 @@ __device__ __forceinline__ void tile_records_out(const uint32_t (&rec)[DWR], uns
         if (B % 4 == 0) {
 #pragma unroll
             for (int d = 0; d < B / 4; d++) *reinterpret_cast<uint32_t *>(p + 4 * d) = rec[d];
-        } else {
+        } else if (B % 2 == 0) {
 #pragma unroll
             for (int hw = 0; hw < B / 2; hw++)
                 *reinterpret_cast<unsigned short *>(p + 2 * hw) = (unsigned short)(rec[hw / 2] >> (16 * (hw % 2)));
+        } else {
+#pragma unroll
+            for (int by = 0; by < B; by++) p[by] = (unsigned char)(rec[by / 4] >> (8 * (by % 4)));
         }
     }
     __syncthreads();
@@ -476,8 +538,12 @@ __device__ __forceinline__ void tile_records_out(const uint32_t (&rec)[DWR], uns
         __builtin_amdgcn_raw_buffer_store_b128(v, ws, lane * 16, k * 1024, BUF_NT);
     }
     const __amdgpu_buffer_rsrc_t wt = buf_rsrc(gdst + nfull, nbytes - nfull);
-    const unsigned short h = *reinterpret_cast<const unsigned short *>(stage + nfull + 2 * lane);
-    __builtin_amdgcn_raw_buffer_store_b16(h, wt, lane * 2, 0, BUF_NT);
+    if (B % 2 == 0) {
+        const unsigned short h = *reinterpret_cast<const unsigned short *>(stage + nfull + 2 * lane);
+        __builtin_amdgcn_raw_buffer_store_b16(h, wt, lane * 2, 0, BUF_NT);
+    } else {
+        __builtin_amdgcn_raw_buffer_store_b8(stage[nfull + lane], wt, lane, 0, BUF_NT);
+    }
 }
 
 // Tile t's output rows (lane j's vector x[0, HD)) out to dst (row i0 + j at

@@ -913,6 +913,7 @@ extern "C" int sp_hip_sqfree_get_tables(const sp_hip_sqfree_cache_t *cc, int *sk
 // ===========================================================================
 struct HierPriv {
     SpPlan plan;
+    bool default_geo;  // skeleton/targets equal sp_hier_default_geometry(pad_dim)
 };
 
 extern "C" int sp_hip_hier_cache_init(sp_hip_hier_cache_t *hc, const sp_config_t *cfg, int pad_dim,
@@ -941,6 +942,13 @@ extern "C" int sp_hip_hier_cache_init(sp_hip_hier_cache_t *hc, const sp_config_t
     HierPriv *pv = new HierPriv();
     hc->priv = pv;
     if (sp_build_plan(skel_bands, pad_dim, 0, -1, &pv->plan)) { set_err("hier_init: plan"); sp_hip_hier_cache_free(hc); return -1; }
+    {
+        std::vector<int> ds((size_t)pad_dim), dt((size_t)pad_dim);
+        const int ns = sp_hier_default_geometry(pad_dim, ds.data(), dt.data());
+        pv->default_geo = ns == n_skeleton && n_target == pad_dim - ns &&
+                          std::equal(skeleton_idx, skeleton_idx + n_skeleton, ds.begin()) &&
+                          std::equal(target_idx, target_idx + n_target, dt.begin());
+    }
     const int res_bytes = (n_target * target_res_bits + 7) / 8;
     hc->bytes_per_pos_k = hc->bytes_per_pos_v = skel_bands->total_bytes + 4 + res_bytes;
     if (hc->bytes_per_pos_k + 8 > SP_GEN_MAX_REC) { set_err("hier_init: record too large"); sp_hip_hier_cache_free(hc); return -1; }
@@ -989,6 +997,7 @@ static SpHierGeo hier_geo(const sp_hip_hier_cache_t *hc, int slot) {
     G.target_idx = hc->d_target_idx;
     G.W = hc->d_W + (size_t)slot * hc->n_target * hc->n_skeleton;
     G.w_outer = (long long)hc->n_target * hc->n_skeleton;
+    G.default_geo = ((const HierPriv *)hc->priv)->default_geo ? 1 : 0;
     return G;
 }
 

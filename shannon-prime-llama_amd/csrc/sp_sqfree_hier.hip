@@ -265,8 +265,9 @@ static bool sq_fits(const SpPlan &P, int pad, int bytes) {
     return pad <= SP_GEN_MAX_N && P.hd <= SP_GEN_MAX_N && bytes + 8 <= SP_GEN_MAX_REC;
 }
 
-// SP_HIP_NO_LANE_KERNELS=1 routes the sqfree geometry with a lane specialization
-// through the one-vector-per-wave kernels (used by tests to cross-check them).
+// SP_HIP_NO_LANE_KERNELS=1 routes the sqfree and hier geometries with a lane
+// specialization through the one-vector-per-wave kernels (used by tests to
+// cross-check them).
 static bool getenv_lane_off_sq() {
     static int v = -1;
     if (v < 0) {
@@ -317,6 +318,10 @@ hipError_t sp_launch_hier_encode(const SpPlan &P, const SpHierGeo &G, const void
                                  int n_outer, int n_inner, hipStream_t s) {
     if (n_outer <= 0 || n_inner <= 0) return hipSuccess;
     if (!sq_fits(P, G.pad, G.bytes)) return hipErrorInvalidValue;
+    if (!getenv_lane_off_sq()) {
+        const hipError_t e = sp_launch_hier_encode_lane(P, G, src, dtype, so, si, dst, dout, n_outer, n_inner, s);
+        if (e != hipErrorNotSupported) return e;
+    }
     const long long nv = (long long)n_outer * n_inner;
     const dim3 grid((unsigned)((nv + 3) / 4)), block(256);
     if (dtype == SP_DT_F16)
@@ -331,6 +336,10 @@ hipError_t sp_launch_hier_decode(const SpPlan &P, const SpHierGeo &G, const unsi
                                  int n_outer, int n_inner, hipStream_t s) {
     if (n_outer <= 0 || n_inner <= 0) return hipSuccess;
     if (!sq_fits(P, G.pad, G.bytes)) return hipErrorInvalidValue;
+    if (!getenv_lane_off_sq()) {
+        const hipError_t e = sp_launch_hier_decode_lane(P, G, src, so, dst, dtype, dout, din, n_outer, n_inner, s);
+        if (e != hipErrorNotSupported) return e;
+    }
     const long long nv = (long long)n_outer * n_inner;
     const dim3 grid((unsigned)((nv + 3) / 4)), block(256);
     if (dtype == SP_DT_F16)

@@ -81,19 +81,6 @@ struct SqRec {
     static constexpr int dwords = (total + 3) / 4;
 };
 
-template <int DW>
-__device__ __forceinline__ void rec_put32(uint32_t (&rec)[DW], int byte, uint32_t v) {
-    const int d = byte / 4, sh = 8 * (byte % 4);
-    rec[d] |= v << sh;
-    if (sh) rec[d + 1] |= v >> (32 - sh);
-}
-
-template <int DW>
-__device__ __forceinline__ uint32_t rec_get32(const uint32_t (&rec)[DW], int byte) {
-    const int d = byte / 4, sh = 8 * (byte % 4);
-    return sh ? __builtin_amdgcn_alignbit(rec[d + 1], rec[d], sh) : rec[d];
-}
-
 // pred[r] = sum over the CSR row of mu * skel[slot], from 0.0f in CSR order
 // (kernel_mobius_predict, shannon_prime_sqfree.cu:179-203); mu = +-1, so each
 // term is +-skel exactly and p + (-s) is p - s.
@@ -104,28 +91,6 @@ __device__ __forceinline__ float csr_predict(const float (&sk)[SK], int r) {
 #pragma unroll
     for (int j = KN.off[r]; j < KN.off[r + 1]; j++) p = KN.mu[j] > 0 ? p + sk[KN.slot[j]] : p - sk[KN.slot[j]];
     return p;
-}
-
-// Sum in the order of the reference's 256-slot block reduction over n values
-// (slot t = 0.0f + v[t] for t < n, then slot[t] += slot[t + s] for s = 128..1);
-// slots at or past n hold +0.0f, so adding them is skipped. ABS: |v| terms.
-// For signed terms the result is the plain tree sum plus 0.0f, which maps the
-// only possible difference (an all -0 tree giving -0) to the reference's +0.
-template <int N, bool ABS>
-__device__ __forceinline__ float tree256_sum(const float *v) {
-    static_assert(N <= 256, "at most one value per slot");
-    float sl[N];
-#pragma unroll
-    for (int t = 0; t < N; t++) sl[t] = ABS ? fabsf(v[t]) : v[t];
-    int n = N;
-#pragma unroll
-    for (int s = 128; s > 0; s >>= 1) {
-#pragma unroll
-        for (int t = 0; t < s; t++)
-            if (t + s < n) sl[t] = sl[t] + sl[t + s];
-        n = n < s ? n : s;
-    }
-    return ABS ? sl[0] : sl[0] + 0.0f;
 }
 
 template <int DT, int HD, int PAD, int SK, int RBITS, bool SPIN, class SL>

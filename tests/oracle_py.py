@@ -244,6 +244,19 @@ def hier_compress_f16(x16, hd, pad, skel_idx, tgt_idx, skel_bc, W, rbits):
     return out
 
 
+def hier_compress_f32(x32, hd, pad, skel_idx, tgt_idx, skel_bc, W, rbits):
+    """fp32 vectors [n][hd] -> records [n][B] (spo_hier_compress per vector)."""
+    x32 = np.ascontiguousarray(x32, dtype=np.float32)
+    n = x32.shape[0]
+    B = hier_bytes(skel_bc, len(tgt_idx), rbits)
+    out = np.zeros((n, B), dtype=np.uint8)
+    W = np.ascontiguousarray(W, dtype=np.uint16)
+    for i in range(n):
+        lib().spo_hier_compress(ptr(x32[i]), ptr(out[i]), hd, pad, len(skel_idx), ptr(skel_idx), len(tgt_idx),
+                                ptr(tgt_idx), C.byref(skel_bc), ptr(W), rbits)
+    return out
+
+
 def hier_decompress_f32(packed, hd, pad, skel_idx, tgt_idx, skel_bc, W, rbits):
     packed = np.ascontiguousarray(packed, dtype=np.uint8)
     n = packed.shape[0]

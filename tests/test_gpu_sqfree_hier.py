@@ -112,6 +112,54 @@ def test_hier_bit_exact(hd, rbits, skel_bits):
     hc.free()
 
 
+@pytest.mark.parametrize("dtype", ["f16", "f32", "f32_tiny"])
+def test_hier_default_geometry_lanes(dtype):
+    """configs[4] geometry (hd 256 -> pad 330, 30 skeleton at 5/5, 300 targets at
+    2 bits): the one-vector-per-lane kernels. 229 positions from position 4 (a
+    partial last tile whose 103-byte records end 3 bytes into a dword), two slots,
+    fp16 and fp32 inputs and outputs; f32_tiny scales the inputs to ~1e-37 so the
+    predictor products are fp32 subnormals."""
+    say(f"hier lanes dtype={dtype}")
+    hd, rbits, n, start, n_slots = 256, 2, 229, 4, 2
+    max_seq = start + n + 3
+    pad = O.sqfree_pad_dim(hd)
+    skel_idx, tgt_idx = O.hier_geometry(pad)
+    skel_bc = O.band_config(len(skel_idx), [5, 5])
+    B = O.hier_bytes(skel_bc, len(tgt_idx), rbits)
+    assert (pad, B, (max_seq * B) % 4, (start * B) % 4, (n * B) % 4) == (330, 103, 0, 0, 3)
+    Wm = W.hier_W(n_slots, len(tgt_idx), len(skel_idx), seed=21)
+    k16, _ = W.cfg5_kv(n_heads=n_slots, n_pos=n, hd=hd, seed=22)
+    cfg = S.config(hd, 1, n_slots)
+    hc = S.HierCache(cfg, pad, skel_idx, tgt_idx, S.band_config(len(skel_idx), [5, 5]), rbits, max_seq,
+                     n_slots, stream=torch.cuda.current_stream().cuda_stream)
+    hc.upload_W(Wm)
+    for slot in range(n_slots):
+        if dtype == "f16":
+            x16 = k16[slot].view(np.uint16)
+            ref = O.hier_compress_f16(x16, hd, pad, skel_idx, tgt_idx, skel_bc, Wm[slot], rbits)
+            xt = dev(x16)
+            S.check(S.lib().sp_hip_hier_write_batch(hc.ref, 0, 0, slot, start, n, p(xt), S.DTYPE_F16))
+        else:
+            x32 = k16[slot].astype(np.float32) * np.float32(1.0 + 2.0 ** -12)
+            if dtype == "f32_tiny":
+                x32 = x32 * np.float32(1e-37)
+            ref = O.hier_compress_f32(x32, hd, pad, skel_idx, tgt_idx, skel_bc, Wm[slot], rbits)
+            xt = dev(x32)
+            S.check(S.lib().sp_hip_hier_write_batch(hc.ref, 0, 0, slot, start, n, p(xt), S.DTYPE_F32))
+        rec = O.hier_decompress_f32(ref, hd, pad, skel_idx, tgt_idx, skel_bc, Wm[slot], rbits)
+        allk = d2h(hc.c.d_k_cache, n_slots * max_seq * B).reshape(n_slots, max_seq, B)
+        np.testing.assert_array_equal(allk[slot, start:start + n], ref)
+        assert not allk[slot, start + n:].any() and not allk[slot, :start].any(), "writes outside the batch"
+        out = empty_f32(n * hd)
+        S.check(S.lib().sp_hip_hier_read_batch(hc.ref, 0, 0, slot, start, n, p(out), S.DTYPE_F32))
+        np.testing.assert_array_equal(host(out).reshape(n, hd).view(np.uint32), rec.view(np.uint32))
+        out16 = torch.empty(n * hd, dtype=torch.float16, device="cuda")
+        S.check(S.lib().sp_hip_hier_read_batch(hc.ref, 0, 0, slot, start, n, p(out16), S.DTYPE_F16))
+        np.testing.assert_array_equal(host(out16).reshape(n, hd).view(np.uint16),
+                                      rec.astype(np.float16).view(np.uint16))
+    hc.free()
+
+
 def test_hier_record_size_cfg5():
     pad = O.sqfree_pad_dim(256)
     skel_idx, tgt_idx = O.hier_geometry(pad)
