@@ -41,40 +41,45 @@ struct HierRec {
     static constexpr int dwords = (total + 3) / 4;
 };
 
-// acc + w0*x0 + w1*x1 for the fp16 pair (w0, w1) of a scalar register, each
-// step rounded once: v_fma_mix widens the weight exactly and rounds w*x + 0
-// (the + 0 turns a -0 product into +0, which a running sum started at +0.0f
-// cannot tell apart: such a sum is never -0), then v_add_f32. One asm block per
-// pair keeps every product next to its add, so a prediction stays one serial
-// chain in registers.
-__device__ __forceinline__ void wmac2(float &acc, uint32_t w2, float x0, float x1) {
-    float p;
-    __asm__("v_fma_mix_f32 %1, %2, %3, 0 op_sel_hi:[1,0,0]\n\t"
-            "v_add_f32 %0, %0, %1\n\t"
-            "v_fma_mix_f32 %1, %2, %4, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
-            "v_add_f32 %0, %0, %1"
-            : "+v"(acc), "=&v"(p)
-            : "s"(w2), "v"(x0), "v"(x1));
+// Two predictions at once: a0 += w0.lo*x0, a1 += w1.lo*x0, a0 += w0.hi*x1,
+// a1 += w1.hi*x1, each step rounded once. v_fma_mix widens the fp16 weight (from
+// a scalar register) exactly and rounds w*x + 0 (the + 0 turns a -0 product into
+// +0, which a running sum started at +0.0f cannot tell apart: such a sum is
+// never -0), then v_add_f32. The two independent chains give each add a free
+// slot after its product; one asm block keeps products next to their adds, so
+// the predictions stay serial chains in registers.
+__device__ __forceinline__ void wmac2x2(float &a0, float &a1, uint32_t w0, uint32_t w1, float x0, float x1) {
+    float p0, p1;
+    __asm__("v_fma_mix_f32 %2, %4, %6, 0 op_sel_hi:[1,0,0]\n\t"
+            "v_fma_mix_f32 %3, %5, %6, 0 op_sel_hi:[1,0,0]\n\t"
+            "v_add_f32 %0, %0, %2\n\t"
+            "v_add_f32 %1, %1, %3\n\t"
+            "v_fma_mix_f32 %2, %4, %7, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+            "v_fma_mix_f32 %3, %5, %7, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+            "v_add_f32 %0, %0, %2\n\t"
+            "v_add_f32 %1, %1, %3"
+            : "+v"(a0), "+v"(a1), "=&v"(p0), "=&v"(p1)
+            : "s"(w0), "s"(w1), "v"(x0), "v"(x1));
 }
 
-// pred = sum_s (float)W[t][s] * sk[s] from 0.0f, s ascending, separately
-// rounded products and adds (kernel_hier_predict, shannon_prime_hier.cu:74-92).
-// wrow: the target's row as fp16 pairs.
 // W is read through the constant address space: the tile-uniform row address
 // then always becomes scalar loads (the scalar cache), whatever the compiler
 // can prove about the kernel's other stores.
 typedef const __attribute__((address_space(4))) uint32_t *wptr_t;
 
-// after: a value the chain is ordered behind (its +0.0f start is produced by an
-// asm that takes it as an operand), so consecutive predictions run in order.
+// pred = sum_s (float)W[t][s] * sk[s] from 0.0f, s ascending, separately
+// rounded products and adds (kernel_hier_predict, shannon_prime_hier.cu:74-92),
+// for targets t and t+1 (rows w0, w1 as fp16 pairs). after: a value the pair is
+// ordered behind (the +0.0f starts come from an asm that takes it as an operand).
 template <int NS>
-__device__ __forceinline__ float hier_predict(wptr_t wrow, const float (&sk)[NS], float after) {
+__device__ __forceinline__ void hier_predict2(wptr_t w0, wptr_t w1, const float (&sk)[NS], float after, float &r0,
+                                              float &r1) {
     static_assert(NS % 2 == 0, "rows of fp16 pairs");
-    float acc;
-    __asm__("v_mov_b32 %0, 0" : "=v"(acc) : "v"(after));
+    float a0, a1;
+    __asm__("v_mov_b32 %0, 0\n\tv_mov_b32 %1, 0" : "=v"(a0), "=v"(a1) : "v"(after));
 #pragma unroll
-    for (int s = 0; s < NS; s += 2) wmac2(acc, wrow[s / 2], sk[s], sk[s + 1]);
-    return acc;
+    for (int s = 0; s < NS; s += 2) wmac2x2(a0, a1, w0[s / 2], w1[s / 2], sk[s], sk[s + 1]);
+    r0 = a0, r1 = a1;
 }
 
 // fp16 halves H of a and b: a + b rounded once (exact widening).
@@ -99,7 +104,7 @@ k_hier_encode_lane(const void *__restrict__ src, long long so, long long si, uns
     using G = HierRec<NT, RBITS, SL>;
     constexpr int RP = row_bytes<DT>(HD) + 16, DWR = G::dwords;
     constexpr auto &HG = kHier<PAD, NS>;
-    static_assert(SL::hd == NS && (PAD - HD) % 2 == 0, "geometry");
+    static_assert(SL::hd == NS && (PAD - HD) % 2 == 0 && NT % 2 == 0, "geometry");
     __shared__ __attribute__((aligned(16))) unsigned char rows[64 * RP];  // input rows, then the record stage
     const int lane = threadIdx.x;
     const TileMap M{tiles_per_outer, n_inner};
@@ -189,13 +194,17 @@ k_hier_encode_lane(const void *__restrict__ src, long long so, long long si, uns
         int o, i0, nv;
         M.at(t, o, i0, nv);
         const wptr_t w32 = (wptr_t)(W + (long long)__builtin_amdgcn_readfirstlane(o) * w_outer);
-        // target r's prediction starts after deviation r-1 exists, so each target
-        // coefficient is consumed before the next chain: without the ordering
+        // the predictions of targets r, r+1 start after deviation r-1 exists, so
+        // the target coefficients are consumed pair by pair: without the ordering
         // the subtractions sink to the tree sum and everything spills
         float dv[NT];
 #pragma unroll
-        for (int r = 0; r < NT; r++)
-            dv[r] = c[HG.tgt[r]] - hier_predict<NS>(w32 + r * (NS / 2), sk, r > 0 ? dv[r - 1] : sk[0]);
+        for (int r = 0; r < NT; r += 2) {
+            float p0, p1;
+            hier_predict2<NS>(w32 + r * (NS / 2), w32 + (r + 1) * (NS / 2), sk, r > 0 ? dv[r - 1] : sk[0], p0, p1);
+            dv[r] = c[HG.tgt[r]] - p0;
+            dv[r + 1] = c[HG.tgt[r + 1]] - p1;
+        }
         float mag = sp_div(tree256_sum<NT, true>(dv), (float)NT);
         mag = mag < 1e-12f ? 1e-12f : mag;
         rec_put32(rec, G::mag_byte, __float_as_uint(mag));
@@ -225,7 +234,7 @@ k_hier_decode_lane(const unsigned char *__restrict__ src, long long so, void *__
     using G = HierRec<NT, RBITS, SL>;
     constexpr int RP = row_bytes<DT>(HD) + 16, DWR = G::dwords;
     constexpr auto &HG = kHier<PAD, NS>;
-    static_assert(RecTile<G>::NCK * 1024 + 16 <= 64 * RP && 64 * G::total + 4 * DWR + 8 <= 64 * RP,
+    static_assert(RecTile<G>::NCK * 1024 + 16 <= 64 * RP && 64 * G::total + 4 * DWR + 8 <= 64 * RP && NT % 2 == 0,
                   "record tile must fit in the row stage");
     __shared__ __attribute__((aligned(16))) unsigned char stage[64 * RP];
     const int lane = threadIdx.x, Gs = gridDim.x;
@@ -254,9 +263,11 @@ k_hier_decode_lane(const unsigned char *__restrict__ src, long long so, void *__
         M.at(t, o, i0, nv);
         const wptr_t w32 = (wptr_t)(W + (long long)__builtin_amdgcn_readfirstlane(o) * w_outer);
 #pragma unroll
-        for (int r = 0; r < NT; r++) {
-            const float p = hier_predict<NS>(w32 + r * (NS / 2), sk, sk[0]);
-            c[HG.tgt[r]] = p + ((float)rec_extract(rec, G::res_bit + r * RBITS, RBITS) - center) * step;
+        for (int r = 0; r < NT; r += 2) {
+            float p0, p1;
+            hier_predict2<NS>(w32 + r * (NS / 2), w32 + (r + 1) * (NS / 2), sk, sk[0], p0, p1);
+            c[HG.tgt[r]] = p0 + ((float)rec_extract(rec, G::res_bit + r * RBITS, RBITS) - center) * step;
+            c[HG.tgt[r + 1]] = p1 + ((float)rec_extract(rec, G::res_bit + (r + 1) * RBITS, RBITS) - center) * step;
         }
         vil_stages<PAD, 0, 1>(c, K);
         tile_rows_out<DT, HD>(c, stage, dst, dout, din, M, t, lane);
