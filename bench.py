@@ -197,25 +197,26 @@ def bench_variants(torch, S, L, stream, reps=3):
     cfg = S.config(128, L4, H4, k_bits=bits4, v_bits=bits4)
     pad4 = L.sp_sqfree_pad_dim(128)
     c4 = S.SqfreeCache(cfg, N4, rbits=3, spinor=True, sk_k=int(pad4 * 0.75), stream=stream.cuda_stream)
-    x = (torch.randn((L4 * H4, N4, 128), generator=g, device="cuda")).half()
+    # rows in llama.cpp's cache layout: [layer][cell][head * hd + d]; one launch per layer and side
+    x = (torch.randn((L4, N4, H4 * 128), generator=g, device="cuda")).half()
     y = torch.empty_like(x)
     B4 = c4.c.bytes_per_pos_k
 
     def sq_write():
-        for s in range(L4 * H4):
-            S.check(L.sp_hip_sqfree_write_batch(c4.ref, 0, s // H4, s % H4, 0, N4, P(x[s]), S.DTYPE_F16))
+        for layer in range(L4):
+            S.check(L.sp_hip_sqfree_write_layer(c4.ref, layer, 0, N4, P(x[layer]), None, H4 * 128, S.DTYPE_F16))
 
     def sq_read():
-        for s in range(L4 * H4):
-            S.check(L.sp_hip_sqfree_read_batch(c4.ref, 0, s // H4, s % H4, 0, N4, P(y[s]), S.DTYPE_F16))
+        for layer in range(L4):
+            S.check(L.sp_hip_sqfree_read_layer(c4.ref, layer, 0, N4, P(y[layer]), None, H4 * 128, S.DTYPE_F16))
 
     out["cfg4_sqfree_spinor"] = {"enc": rate(L4 * H4 * N4, 128, B4, timed(sq_write)),
                                  "dec": rate(L4 * H4 * N4, 128, B4, timed(sq_read)),
                                  "record_bytes": B4, "pad_dim": pad4, "skeleton": c4.c.sk_k,
-                                 "calls": f"{L4 * H4} slots x {N4} positions, one call per slot"}
+                                 "calls": f"{L4} layers x {H4} heads x {N4} positions, one call per layer (K)"}
     c4.free()
     del x, y
-    # hier, hd 256 -> pad 330, 8 KV heads x (8 x 131072) cells per layer; 2 slots timed
+    # hier, hd 256 -> pad 330, 8 KV heads x (8 x 131072) cells of one layer in one launch per side
     H5, N5, hd5 = 8, 8 * 131072, 256
     pad5 = L.sp_sqfree_pad_dim(hd5)
     n_sk = L.sp_hier_default_geometry(pad5, None, None)
@@ -227,23 +228,22 @@ def bench_variants(torch, S, L, stream, reps=3):
                      stream=stream.cuda_stream)
     Wh = (np.random.default_rng(5).standard_normal((H5, pad5 - n_sk, n_sk)) * 0.05).astype(np.float16)
     c5.upload_W(Wh.view(np.uint16))
-    n_t = 2
-    x = (torch.randn((n_t, N5, hd5), generator=g, device="cuda")).half()
+    x = torch.empty((N5, H5 * hd5), dtype=torch.float16, device="cuda")
+    for r0 in range(0, N5, 1 << 18):  # bounded fp32 temporaries
+        x[r0:r0 + (1 << 18)] = torch.randn((min(1 << 18, N5 - r0), H5 * hd5), generator=g, device="cuda").half()
     y = torch.empty_like(x)
     B5 = c5.c.bytes_per_pos_k
 
     def hi_write():
-        for s in range(n_t):
-            S.check(L.sp_hip_hier_write_batch(c5.ref, 0, 0, s, 0, N5, P(x[s]), S.DTYPE_F16))
+        S.check(L.sp_hip_hier_write_layer(c5.ref, 0, 0, N5, P(x), None, H5 * hd5, S.DTYPE_F16))
 
     def hi_read():
-        for s in range(n_t):
-            S.check(L.sp_hip_hier_read_batch(c5.ref, 0, 0, s, 0, N5, P(y[s]), S.DTYPE_F16))
+        S.check(L.sp_hip_hier_read_layer(c5.ref, 0, 0, N5, P(y), None, H5 * hd5, S.DTYPE_F16))
 
-    out["cfg5_hier"] = {"enc": rate(n_t * N5, hd5, B5, timed(hi_write)),
-                        "dec": rate(n_t * N5, hd5, B5, timed(hi_read)),
+    out["cfg5_hier"] = {"enc": rate(H5 * N5, hd5, B5, timed(hi_write)),
+                        "dec": rate(H5 * N5, hd5, B5, timed(hi_read)),
                         "record_bytes": B5, "pad_dim": pad5, "skeleton": n_sk,
-                        "calls": f"{n_t} slots x {N5} positions, one call per slot"}
+                        "calls": f"1 layer x {H5} heads x {N5} positions, one call (K)"}
     c5.free()
     return out
 

@@ -210,6 +210,14 @@ int  sp_hip_sqfree_write_batch(sp_hip_sqfree_cache_t *cc, int is_v, int layer, i
                                int start_pos, int n_pos, const void *d_src, int dtype);
 int  sp_hip_sqfree_read_batch(const sp_hip_sqfree_cache_t *cc, int is_v, int layer, int head,
                               int start_pos, int n_pos, void *d_dst, int dtype);
+/* Extension: every head of one layer in one launch per K/V (the sqfree branch of
+ * KvCache::write_gpu/read_gpu, kv_cache.cpp:1069-1080 and :1139-1197), rows in
+ * llama.cpp's cache layout as for sp_hip_write_layer: element (t, h, d) at
+ * t*row_stride + h*head_dim + d. NULL d_k or d_v skips that side. */
+int  sp_hip_sqfree_write_layer(sp_hip_sqfree_cache_t *cc, int layer, int start_pos, int n_tok,
+                               const void *d_k, const void *d_v, long long row_stride, int dtype);
+int  sp_hip_sqfree_read_layer(const sp_hip_sqfree_cache_t *cc, int layer, int start_pos, int n_tok,
+                              void *d_k, void *d_v, long long row_stride, int dtype);
 /* Host copies of the Knight tables (for tests and calibration tools). */
 int  sp_hip_sqfree_get_tables(const sp_hip_sqfree_cache_t *cc, int *skeleton_idx,
                               int *residual_idx, int *csr_offsets, int *csr_skel_slot,
@@ -256,6 +264,13 @@ int  sp_hip_hier_write_batch(sp_hip_hier_cache_t *hc, int is_v, int layer, int h
                              int start_pos, int n_pos, const void *d_src, int dtype);
 int  sp_hip_hier_read_batch(const sp_hip_hier_cache_t *hc, int is_v, int layer, int head,
                             int start_pos, int n_pos, void *d_dst, int dtype);
+/* Extension: every head of one layer in one launch per K/V (the hier branch of
+ * KvCache::write_gpu/read_gpu, kv_cache.cpp:1056-1068 and :1114-1128), rows as for
+ * sp_hip_write_layer. NULL d_k or d_v skips that side. */
+int  sp_hip_hier_write_layer(sp_hip_hier_cache_t *hc, int layer, int start_pos, int n_tok,
+                             const void *d_k, const void *d_v, long long row_stride, int dtype);
+int  sp_hip_hier_read_layer(const sp_hip_hier_cache_t *hc, int layer, int start_pos, int n_tok,
+                            void *d_k, void *d_v, long long row_stride, int dtype);
 
 /* ======================================================================== */
 /* Runtime                                                                  */

@@ -889,6 +889,44 @@ extern "C" int sp_hip_sqfree_read_batch(const sp_hip_sqfree_cache_t *cc, int is_
                   "sqfree decode") ? 0 : -1;
 }
 
+extern "C" int sp_hip_sqfree_write_layer(sp_hip_sqfree_cache_t *cc, int layer, int start_pos, int n_tok,
+                                         const void *d_k, const void *d_v, long long row_stride, int dtype) {
+    if (!sq_slot_ok(cc, layer, 0, start_pos, n_tok)) { set_err("sqfree write_layer: bad layer/pos"); return -1; }
+    const int H = cc->config.n_heads_kv, hd = cc->config.head_dim;
+    if (row_stride < (long long)H * hd) { set_err("sqfree write_layer: row_stride"); return -1; }
+    SqPriv *pv = (SqPriv *)cc->priv;
+    for (int is_v = 0; is_v < 2; is_v++) {
+        const void *src = is_v ? d_v : d_k;
+        if (!src) continue;
+        const SpSqGeo G = sq_geo(cc, is_v);
+        unsigned char *dst = (is_v ? cc->d_v_cache : cc->d_k_cache) +
+                             ((long long)layer * H * cc->max_seq_len + start_pos) * G.bytes;
+        if (!hip_ok(sp_launch_sqfree_encode(is_v ? pv->vplan : pv->kplan, G, src, dtype, hd, row_stride, dst,
+                                            (long long)cc->max_seq_len * G.bytes, H, n_tok, (hipStream_t)cc->stream),
+                    "sqfree write_layer")) return -1;
+    }
+    return 0;
+}
+
+extern "C" int sp_hip_sqfree_read_layer(const sp_hip_sqfree_cache_t *cc, int layer, int start_pos, int n_tok,
+                                        void *d_k, void *d_v, long long row_stride, int dtype) {
+    if (!sq_slot_ok(cc, layer, 0, start_pos, n_tok)) { set_err("sqfree read_layer: bad layer/pos"); return -1; }
+    const int H = cc->config.n_heads_kv, hd = cc->config.head_dim;
+    if (row_stride < (long long)H * hd) { set_err("sqfree read_layer: row_stride"); return -1; }
+    SqPriv *pv = (SqPriv *)cc->priv;
+    for (int is_v = 0; is_v < 2; is_v++) {
+        void *dst = is_v ? d_v : d_k;
+        if (!dst) continue;
+        const SpSqGeo G = sq_geo(cc, is_v);
+        const unsigned char *src = (is_v ? cc->d_v_cache : cc->d_k_cache) +
+                                   ((long long)layer * H * cc->max_seq_len + start_pos) * G.bytes;
+        if (!hip_ok(sp_launch_sqfree_decode(is_v ? pv->vplan : pv->kplan, G, src, (long long)cc->max_seq_len * G.bytes,
+                                            dst, dtype, hd, row_stride, H, n_tok, (hipStream_t)cc->stream),
+                    "sqfree read_layer")) return -1;
+    }
+    return 0;
+}
+
 extern "C" void sp_hip_sqfree_write_k(sp_hip_sqfree_cache_t *cc, int l, int h, int p, const float *d) { sp_hip_sqfree_write_batch(cc, 0, l, h, p, 1, d, SP_DT_F32); }
 extern "C" void sp_hip_sqfree_write_v(sp_hip_sqfree_cache_t *cc, int l, int h, int p, const float *d) { sp_hip_sqfree_write_batch(cc, 1, l, h, p, 1, d, SP_DT_F32); }
 extern "C" void sp_hip_sqfree_read_k(const sp_hip_sqfree_cache_t *cc, int l, int h, int p, float *d) { sp_hip_sqfree_read_batch(cc, 0, l, h, p, 1, d, SP_DT_F32); }
@@ -1029,6 +1067,44 @@ extern "C" int sp_hip_hier_read_batch(const sp_hip_hier_cache_t *hc, int is_v, i
     return hip_ok(sp_launch_hier_decode(((HierPriv *)hc->priv)->plan, G, src, 0, d_dst, dtype, 0,
                                         hc->config.head_dim, 1, n_pos, (hipStream_t)hc->stream),
                   "hier decode") ? 0 : -1;
+}
+
+extern "C" int sp_hip_hier_write_layer(sp_hip_hier_cache_t *hc, int layer, int start_pos, int n_tok,
+                                       const void *d_k, const void *d_v, long long row_stride, int dtype) {
+    if (!hier_slot_ok(hc, layer, 0, start_pos, n_tok) ||
+        (long long)(layer + 1) * hc->config.n_heads_kv > hc->n_slots) { set_err("hier write_layer: bad layer/pos"); return -1; }
+    const int H = hc->config.n_heads_kv, hd = hc->config.head_dim;
+    if (row_stride < (long long)H * hd) { set_err("hier write_layer: row_stride"); return -1; }
+    const SpHierGeo G = hier_geo(hc, layer * H);
+    for (int is_v = 0; is_v < 2; is_v++) {
+        const void *src = is_v ? d_v : d_k;
+        if (!src) continue;
+        unsigned char *dst = (is_v ? hc->d_v_cache : hc->d_k_cache) +
+                             ((long long)layer * H * hc->max_seq_len + start_pos) * G.bytes;
+        if (!hip_ok(sp_launch_hier_encode(((HierPriv *)hc->priv)->plan, G, src, dtype, hd, row_stride, dst,
+                                          (long long)hc->max_seq_len * G.bytes, H, n_tok, (hipStream_t)hc->stream),
+                    "hier write_layer")) return -1;
+    }
+    return 0;
+}
+
+extern "C" int sp_hip_hier_read_layer(const sp_hip_hier_cache_t *hc, int layer, int start_pos, int n_tok,
+                                      void *d_k, void *d_v, long long row_stride, int dtype) {
+    if (!hier_slot_ok(hc, layer, 0, start_pos, n_tok) ||
+        (long long)(layer + 1) * hc->config.n_heads_kv > hc->n_slots) { set_err("hier read_layer: bad layer/pos"); return -1; }
+    const int H = hc->config.n_heads_kv, hd = hc->config.head_dim;
+    if (row_stride < (long long)H * hd) { set_err("hier read_layer: row_stride"); return -1; }
+    const SpHierGeo G = hier_geo(hc, layer * H);
+    for (int is_v = 0; is_v < 2; is_v++) {
+        void *dst = is_v ? d_v : d_k;
+        if (!dst) continue;
+        const unsigned char *src = (is_v ? hc->d_v_cache : hc->d_k_cache) +
+                                   ((long long)layer * H * hc->max_seq_len + start_pos) * G.bytes;
+        if (!hip_ok(sp_launch_hier_decode(((HierPriv *)hc->priv)->plan, G, src, (long long)hc->max_seq_len * G.bytes,
+                                          dst, dtype, hd, row_stride, H, n_tok, (hipStream_t)hc->stream),
+                    "hier read_layer")) return -1;
+    }
+    return 0;
 }
 
 extern "C" void sp_hip_hier_write_k(sp_hip_hier_cache_t *hc, int l, int h, int p, const float *d) { sp_hip_hier_write_batch(hc, 0, l, h, p, 1, d, SP_DT_F32); }

@@ -128,6 +128,10 @@ def lib():
         L.sp_hip_sqfree_read_batch.argtypes = [vp, i, i, i, i, i, vp, i]
         L.sp_hip_hier_write_batch.argtypes = [vp, i, i, i, i, i, vp, i]
         L.sp_hip_hier_read_batch.argtypes = [vp, i, i, i, i, i, vp, i]
+        L.sp_hip_sqfree_write_layer.argtypes = [vp, i, i, i, vp, vp, ll, i]
+        L.sp_hip_sqfree_read_layer.argtypes = [vp, i, i, i, vp, vp, ll, i]
+        L.sp_hip_hier_write_layer.argtypes = [vp, i, i, i, vp, vp, ll, i]
+        L.sp_hip_hier_read_layer.argtypes = [vp, i, i, i, vp, vp, ll, i]
         L.sp_hip_vht2_forward.argtypes = [vp, i, i, i, vp]
         L.sp_hip_band_quantize.argtypes = [vp, vp, vp, i, vp]
         L.sp_hip_band_dequantize.argtypes = [vp, vp, vp, i, vp]

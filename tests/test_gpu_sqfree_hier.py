@@ -160,6 +160,89 @@ def test_hier_default_geometry_lanes(dtype):
     hc.free()
 
 
+def _rows(x16, row_pad):
+    """[H][n][hd] fp16 -> llama.cpp cache rows [n][H*hd + row_pad] (padding = 0x7e00 NaN sentinel)."""
+    H, n, hd = x16.shape
+    rows = np.full((n, H * hd + row_pad), 0x7e00, np.uint16)
+    for h in range(H):
+        rows[:, h * hd:(h + 1) * hd] = x16[h].view(np.uint16)
+    return rows
+
+
+@pytest.mark.parametrize("sk_frac", [0.75, 0.0])
+def test_sqfree_layer_wide(sk_frac):
+    """sp_hip_sqfree_write_layer / read_layer: every head of layer 1 in one launch
+    from llama.cpp cache rows (row stride H*hd + 8), 150 tokens from position 3;
+    records and fp32 reconstructions bit-exact against the oracle per head, row
+    padding untouched."""
+    say(f"sqfree layer-wide sk_frac={sk_frac}")
+    hd, H, n, start, pad_row = 128, 4, 150, 3, 8
+    k16, v16 = W.cfg4_kv(n_heads=H, n_pos=n, hd=hd, seed=31)
+    pad = O.sqfree_pad_dim(hd)
+    sk = int(pad * sk_frac) if sk_frac else pad // 2
+    km = O.Knight(pad, sk)
+    bits = [5, 4, 4, 4, 5]
+    skel_bc = O.band_config(sk, bits)
+    cfg = S.config(hd, 2, H, k_bits=bits, v_bits=bits)
+    cc = S.SqfreeCache(cfg, start + n + 5, rbits=3, spinor=True, sk_k=sk,
+                       stream=torch.cuda.current_stream().cuda_stream)
+    B = cc.c.bytes_per_pos_k
+    stride = H * hd + pad_row
+    kt, vt = dev(_rows(k16, pad_row)), dev(_rows(v16, pad_row))
+    S.check(S.lib().sp_hip_sqfree_write_layer(cc.ref, 1, start, n, p(kt), p(vt), stride, S.DTYPE_F16))
+    ko = torch.full((n * stride,), float("nan"), dtype=torch.float32, device="cuda")
+    vo = torch.full((n * stride,), float("nan"), dtype=torch.float32, device="cuda")
+    S.check(S.lib().sp_hip_sqfree_read_layer(cc.ref, 1, start, n, p(ko), p(vo), stride, S.DTYPE_F32))
+    ms = cc.c.max_seq_len
+    for name, x16, cache, out in (("K", k16, cc.c.d_k_cache, ko), ("V", v16, cc.c.d_v_cache, vo)):
+        allr = d2h(cache, 2 * H * ms * B).reshape(2 * H, ms, B)
+        g = host(out).reshape(n, stride)
+        assert np.isnan(g[:, H * hd:]).all(), "row padding written"
+        for h in range(H):
+            ref = O.sqfree_compress_f16(x16[h].view(np.uint16), hd, km, skel_bc, 3, True)
+            rec = O.sqfree_decompress_f32(ref, hd, km, skel_bc, 3, True)
+            np.testing.assert_array_equal(allr[H + h, start:start + n], ref, err_msg=f"{name} head {h}")
+            assert not allr[h].any(), "layer 0 written"
+            np.testing.assert_array_equal(g[:, h * hd:(h + 1) * hd].view(np.uint32), rec.view(np.uint32))
+    cc.free()
+
+
+def test_hier_layer_wide():
+    """sp_hip_hier_write_layer / read_layer at the configs[4] geometry: both heads of
+    layer 1 (slots 2, 3, each with its own W) in one launch from cache rows, 200
+    tokens from position 4; bit-exact against the oracle per head."""
+    say("hier layer-wide")
+    hd, H, n, start, pad_row, rbits = 256, 2, 200, 4, 16, 2
+    k16, v16 = W.cfg5_kv(n_heads=H, n_pos=n, hd=hd, seed=41)
+    pad = O.sqfree_pad_dim(hd)
+    skel_idx, tgt_idx = O.hier_geometry(pad)
+    skel_bc = O.band_config(len(skel_idx), [5, 5])
+    Wm = W.hier_W(2 * H, len(tgt_idx), len(skel_idx), seed=42)
+    cfg = S.config(hd, 2, H)
+    ms = start + n + 4
+    hc = S.HierCache(cfg, pad, skel_idx, tgt_idx, S.band_config(len(skel_idx), [5, 5]), rbits, ms, 2 * H,
+                     stream=torch.cuda.current_stream().cuda_stream)
+    hc.upload_W(Wm)
+    B = hc.c.bytes_per_pos_k
+    stride = H * hd + pad_row
+    kt, vt = dev(_rows(k16, pad_row)), dev(_rows(v16, pad_row))
+    S.check(S.lib().sp_hip_hier_write_layer(hc.ref, 1, start, n, p(kt), p(vt), stride, S.DTYPE_F16))
+    ko = torch.full((n * stride,), float("nan"), dtype=torch.float32, device="cuda")
+    vo = torch.full((n * stride,), float("nan"), dtype=torch.float32, device="cuda")
+    S.check(S.lib().sp_hip_hier_read_layer(hc.ref, 1, start, n, p(ko), p(vo), stride, S.DTYPE_F32))
+    for name, x16, cache, out in (("K", k16, hc.c.d_k_cache, ko), ("V", v16, hc.c.d_v_cache, vo)):
+        allr = d2h(cache, 2 * H * ms * B).reshape(2 * H, ms, B)
+        g = host(out).reshape(n, stride)
+        assert np.isnan(g[:, H * hd:]).all(), "row padding written"
+        for h in range(H):
+            slot = H + h
+            ref = O.hier_compress_f16(x16[h].view(np.uint16), hd, pad, skel_idx, tgt_idx, skel_bc, Wm[slot], rbits)
+            rec = O.hier_decompress_f32(ref, hd, pad, skel_idx, tgt_idx, skel_bc, Wm[slot], rbits)
+            np.testing.assert_array_equal(allr[slot, start:start + n], ref, err_msg=f"{name} head {h}")
+            np.testing.assert_array_equal(g[:, h * hd:(h + 1) * hd].view(np.uint32), rec.view(np.uint32))
+    hc.free()
+
+
 def test_hier_record_size_cfg5():
     pad = O.sqfree_pad_dim(256)
     skel_idx, tgt_idx = O.hier_geometry(pad)
