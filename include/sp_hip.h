@@ -88,6 +88,26 @@ int sp_hip_write_layer(sp_hip_cache_t *cc, int layer, int start_pos, int n_tok,
 int sp_hip_read_layer(const sp_hip_cache_t *cc, int layer, int start_pos, int n_tok,
                       void *d_k, void *d_v, long long row_stride, int dtype, int max_bands);
 
+/* Device form of the patch's post-decode hook (llama_sp_post_compute,
+ * llama-cpp-b8861-full-engine.patch:997-1360, which gathers each new cell's
+ * vector to the host, calls sp_llama_write_k/v and sp_llama_read_k/v_partial per
+ * vector and scatters the reconstruction back): for every head and each of the
+ * n_cells cache cells listed in d_cells (device int32, any order), compress the
+ * vector held in the llama.cpp cache tensor into the records at that cell and
+ * overwrite the vector with its reconstruction (bands >= max_bands read as 0;
+ * max_bands < 0 reads every band). One launch per K/V for the whole layer.
+ * K: element (cell, h, d) at cell*k_cell_stride + h*head_dim + d.
+ * V: element (cell, h, d) at cell*v_cell_stride + (h*head_dim + d)*v_elem_stride:
+ *    rows (v_elem_stride 1, v_cell_stride >= n_heads_kv*head_dim) or llama.cpp's
+ *    transposed V (v_trans: v_cell_stride 1, v_elem_stride = kv_size >= max_seq).
+ * NULL d_k or d_v skips that side; cells outside [0, max_seq) are skipped.
+ * Needs a band layout with a lane specialization (hd 128 K 5/5/4/3 + V 3, hd 64
+ * K 5/5/4/3 + V 5, hd 96 K 5/4/4 + V 5) and the default Mobius order; returns -1
+ * otherwise. */
+int sp_hip_roundtrip_cells(sp_hip_cache_t *cc, int layer, const int *d_cells, int n_cells,
+                           void *d_k, long long k_cell_stride, void *d_v, long long v_cell_stride,
+                           long long v_elem_stride, int dtype, int max_bands, void *stream);
+
 /* Every slot at once: src/dst [n_layers*n_heads_kv][n_pos][head_dim] for positions
  * [start_pos, start_pos+n_pos) of each slot (bulk prefill / bulk reconstruct). */
 int sp_hip_write_all(sp_hip_cache_t *cc, int start_pos, int n_pos,

@@ -175,6 +175,13 @@ hipError_t sp_launch_ship_encode_lane(const SpPlan &P, bool default_order, const
 hipError_t sp_launch_ship_decode_lane(const SpPlan &P, bool default_order, const unsigned char *src,
                                       long long so, void *dst, int dtype, long long dout, long long din,
                                       int n_outer, int n_inner, hipStream_t s);
+// in-place compress + decompress of every head's vectors at n_cells cache cells
+// (element (c, h, d) at c*cs + (h*hd + d)*es of x; records at rec_base +
+// h*rec_head_stride + c*B); hipErrorNotSupported when no specialization fits
+hipError_t sp_launch_ship_roundtrip_lane(const SpPlan &P, bool default_order, void *x, int dtype, long long cs,
+                                         long long es, const int *cells, int n_cells, int max_seq,
+                                         unsigned char *rec_base, long long rec_head_stride, int n_heads,
+                                         int max_bands, hipStream_t s);
 hipError_t sp_launch_permute(float *data, const int *order, int n, int n_vecs, int inverse,
                              hipStream_t s);
 

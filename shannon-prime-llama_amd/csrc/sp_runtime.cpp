@@ -615,6 +615,39 @@ extern "C" int sp_hip_read_layer(const sp_hip_cache_t *cc, int layer, int start_
     return 0;
 }
 
+extern "C" int sp_hip_roundtrip_cells(sp_hip_cache_t *cc, int layer, const int *d_cells, int n_cells,
+                                      void *d_k, long long k_cell_stride, void *d_v, long long v_cell_stride,
+                                      long long v_elem_stride, int dtype, int max_bands, void *stream) {
+    if (!slot_ok(cc, layer, 0, 0, 0) || n_cells < 0 || (n_cells > 0 && !d_cells) ||
+        (dtype != SP_DT_F16 && dtype != SP_DT_F32)) { set_err("roundtrip_cells: bad args"); return -1; }
+    const int H = cc->config.n_heads_kv, hd = cc->config.head_dim;
+    const long long row = (long long)H * hd;
+    if (d_k && k_cell_stride < row) { set_err("roundtrip_cells: k_cell_stride"); return -1; }
+    if (d_v && !((v_elem_stride == 1 && v_cell_stride >= row) ||
+                 (v_cell_stride == 1 && v_elem_stride >= cc->max_seq_len))) {
+        set_err("roundtrip_cells: V strides must be rows or the transposed layout"); return -1;
+    }
+    if (n_cells == 0) return 0;
+    ShipPriv *pv = (ShipPriv *)cc->priv;
+    hipStream_t s = (hipStream_t)(stream ? stream : cc->stream);
+    for (int is_v = 0; is_v < 2; is_v++) {
+        void *x = is_v ? d_v : d_k;
+        if (!x) continue;
+        const SpPlan &P = is_v ? pv->vplan : pv->kplan;
+        const int *order = is_v ? nullptr : cc->d_mobius_order;
+        if (P.skip_transform || !(order == nullptr || P.order_default)) {
+            set_err("roundtrip_cells: needs the default Mobius order"); return -1;
+        }
+        const long long B = is_v ? cc->v_bands.total_bytes : cc->k_bands.total_bytes;
+        const hipError_t e = sp_launch_ship_roundtrip_lane(
+            P, order != nullptr, x, dtype, is_v ? v_cell_stride : k_cell_stride, is_v ? v_elem_stride : 1, d_cells,
+            n_cells, cc->max_seq_len, slot_ptr(cc, is_v, layer, 0, 0), (long long)cc->max_seq_len * B, H, max_bands, s);
+        if (e == hipErrorNotSupported) { set_err("roundtrip_cells: no lane kernel for this band layout"); return -1; }
+        if (!hip_ok(e, "roundtrip_cells")) return -1;
+    }
+    return 0;
+}
+
 extern "C" int sp_hip_write_all(sp_hip_cache_t *cc, int start_pos, int n_pos, const void *d_k,
                                 const void *d_v, int dtype) {
     if (!slot_ok(cc, 0, 0, start_pos, n_pos)) { set_err("write_all: bad pos"); return -1; }

@@ -135,16 +135,24 @@ k_ship_encode_lane(const void *__restrict__ src, long long so, long long si,
 // LDS, then as wave-wide 16-byte buffer stores whose range check drops rows
 // past the tile's valid ones (no lane-dependent branch anywhere, so the
 // compiler can count outstanding memory operations exactly).
+// A record in registers -> the lane's reconstructed vector (dequantize, then the
+// inverse transform, which is the same orthonormal self-inverse transform).
+template <class LY, int NORM, bool MOB, bool FULL>
+__device__ __forceinline__ void dec_vec(const uint32_t (&rec)[LY::dwords], const XfConst &K, int max_bands,
+                                        float (&x)[LY::hd]) {
+    constexpr int HD = LY::hd;
+    dequant_bands<LY, MOB, FULL>(rec, max_bands, x);
+    if constexpr (c_pow2(HD)) vht2_reg<HD, NORM>(x, K.inv_sqrt_n, false);
+    else vil_stages<HD, 0, 1>(x, K);
+}
+
 template <class LY, int DT, int NORM, bool MOB, bool FULL>
 __device__ __forceinline__ void dec_tile(const uint32_t (&rec)[LY::dwords], unsigned char *stage, void *dst,
                                          long long dout, long long din, const TileMap &M, int t, int lane,
                                          const XfConst &K, int max_bands) {
-    constexpr int HD = LY::hd;
-    float x[HD];
-    dequant_bands<LY, MOB, FULL>(rec, max_bands, x);
-    if constexpr (c_pow2(HD)) vht2_reg<HD, NORM>(x, K.inv_sqrt_n, false);
-    else vil_stages<HD, 0, 1>(x, K);
-    tile_rows_out<DT, HD>(x, stage, dst, dout, din, M, t, lane);
+    float x[LY::hd];
+    dec_vec<LY, NORM, MOB, FULL>(rec, K, max_bands, x);
+    tile_rows_out<DT, LY::hd>(x, stage, dst, dout, din, M, t, lane);
 }
 
 // Persistent single-wave blocks walk tiles t, t + G, t + 2G, ... (G = grid size).
@@ -173,6 +181,95 @@ k_ship_decode_lane(const unsigned char *__restrict__ src, long long so, void *__
         uint32_t rec[DW];
         rec_from_lds<LY>(rec, stage, lane);
         dec_tile<LY, DT, NORM, MOB, FULL>(rec, stage, dst, dout, din, M, t, lane, K, max_bands);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// in-place round trip over cache cells
+// ---------------------------------------------------------------------------
+// The device form of llama_sp_post_compute's per-layer loop
+// (llama-cpp-b8861-full-engine.patch:997-1360): lane j of tile (h, g) takes cell
+// c = cells[64g + j] of head h, whose element d sits at c*cs + (h*HD + d)*es in
+// the llama.cpp cache tensor x (es = 1: rows; cs = 1, es = kv_size: the
+// transposed V layout). It compresses the vector into the record at position c
+// of head h, then decompresses that record (bands < max_bands unless FULL) and
+// writes the reconstruction back over the vector. Cells outside [0, max_seq)
+// and lanes past n_cells load cell cells[0]'s data and store nothing. CONTIG
+// (es = 1 and 16-byte aligned rows) moves whole rows as 16-byte pieces;
+// otherwise element by element (coalesced across lanes when the cells are
+// consecutive and cs = 1).
+template <class LY, int DT, bool MOB, bool FULL, bool CONTIG>
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+k_ship_roundtrip_lane(void *__restrict__ x, long long cs, long long es, const int *__restrict__ cells, int n_cells,
+                      int max_seq, unsigned char *__restrict__ rec_base, long long rec_head_stride, int n_tiles,
+                      const XfConst K, int max_bands) {
+    constexpr int HD = LY::hd, CPR = row_bytes<DT>(HD) / 16, B = LY::total, DW = LY::dwords;
+    constexpr long long esz = DT == SP_DT_F16 ? 2 : 4;
+    const int lane = threadIdx.x, tpg = (n_cells + 63) / 64;
+    for (int t = blockIdx.x; t < n_tiles; t += gridDim.x) {
+        const int h = t / tpg, i = (t - h * tpg) * 64 + lane;
+        const int c0 = cells[i < n_cells ? i : 0];
+        const bool live = i < n_cells && c0 >= 0 && c0 < max_seq;
+        const long long c = live ? c0 : (long long)((cells[0] >= 0 && cells[0] < max_seq) ? cells[0] : 0);
+        unsigned char *v = reinterpret_cast<unsigned char *>(x) + (c * cs + (long long)h * HD * es) * esz;
+        uint4 in[CPR];
+        if (CONTIG) {
+#pragma unroll
+            for (int q = 0; q < CPR; q++) in[q] = *reinterpret_cast<const uint4 *>(v + 16 * q);
+        } else {
+            uint32_t w[CPR * 4];
+#pragma unroll
+            for (int k = 0; k < CPR * 4; k++) {
+                if (DT == SP_DT_F16)
+                    w[k] = (uint32_t)*reinterpret_cast<const unsigned short *>(v + (2 * k) * es * 2) |
+                           ((uint32_t)*reinterpret_cast<const unsigned short *>(v + (2 * k + 1) * es * 2) << 16);
+                else
+                    w[k] = *reinterpret_cast<const uint32_t *>(v + k * es * 4);
+            }
+#pragma unroll
+            for (int q = 0; q < CPR; q++) in[q] = make_uint4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
+        }
+        uint32_t rec[DW];
+        enc_tile<LY, DT, 0, MOB>(in, K, rec);
+        float y[HD];
+        dec_vec<LY, 0, MOB, FULL>(rec, K, max_bands, y);
+        if (live) {
+            unsigned char *r = rec_base + (long long)h * rec_head_stride + c * B;
+            if (B % 4 == 0) {
+#pragma unroll
+                for (int d = 0; d < B / 4; d++) reinterpret_cast<uint32_t *>(r)[d] = rec[d];
+            } else {
+#pragma unroll
+                for (int hw = 0; hw < B / 2; hw++)
+                    reinterpret_cast<unsigned short *>(r)[hw] = (unsigned short)(rec[hw / 2] >> (16 * (hw % 2)));
+            }
+            uint32_t o[CPR * 4];
+#pragma unroll
+            for (int k = 0; k < CPR * 4; k++) {
+                if (DT == SP_DT_F16) {
+                    float2v ab = {y[2 * k], y[2 * k + 1]};
+                    __asm__ volatile("" : "+v"(ab));  // no multiply-into-convert fusion
+                    o[k] = __builtin_bit_cast(uint32_t, __builtin_convertvector(ab, half2v));
+                } else {
+                    o[k] = __float_as_uint(y[k]);
+                }
+            }
+            if (CONTIG) {
+#pragma unroll
+                for (int q = 0; q < CPR; q++)
+                    *reinterpret_cast<uint4 *>(v + 16 * q) = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+            } else {
+#pragma unroll
+                for (int k = 0; k < CPR * 4; k++) {
+                    if (DT == SP_DT_F16) {
+                        *reinterpret_cast<unsigned short *>(v + (2 * k) * es * 2) = (unsigned short)o[k];
+                        *reinterpret_cast<unsigned short *>(v + (2 * k + 1) * es * 2) = (unsigned short)(o[k] >> 16);
+                    } else {
+                        *reinterpret_cast<uint32_t *>(v + k * es * 4) = o[k];
+                    }
+                }
+            }
+        }
     }
 }
 
@@ -227,6 +324,44 @@ hipError_t dec_launch(const SpPlan &P, bool mob, const unsigned char *src, long 
     return hipGetLastError();
 }
 
+template <class LY, int DT, bool MOB>
+hipError_t rt_launch(const SpPlan &P, bool mob, void *x, long long cs, long long es, const int *cells, int n_cells,
+                     int max_seq, unsigned char *rec_base, long long rec_head_stride, int n_heads, int max_bands,
+                     hipStream_t s) {
+    if (mob != MOB || P.norm != 0) return hipErrorNotSupported;
+    const long long n_tiles = (long long)n_heads * ((n_cells + 63) / 64);
+    if (n_tiles > 0x7fffffffLL) return hipErrorNotSupported;
+    constexpr long long esz = DT == SP_DT_F16 ? 2 : 4;
+    const bool contig = es == 1 && ((uintptr_t)x % 16) == 0 && (cs * esz) % 16 == 0 && (LY::hd * esz) % 16 == 0;
+    const bool full = max_bands < 0 || max_bands >= LY::nb;
+    const dim3 grid((unsigned)std::min<long long>(n_tiles, persistent_blocks())), block(64);
+#define SP_RT(FULLV, CONTIGV)                                                                                      \
+    hipLaunchKernelGGL((k_ship_roundtrip_lane<LY, DT, MOB, FULLV, CONTIGV>), grid, block, 0, s, x, cs, es, cells, \
+                       n_cells, max_seq, rec_base, rec_head_stride, (int)n_tiles, xf_const(P), max_bands)
+    if (full) {
+        if (contig) SP_RT(true, true);
+        else SP_RT(true, false);
+    } else {
+        if (contig) SP_RT(false, true);
+        else SP_RT(false, false);
+    }
+#undef SP_RT
+    return hipGetLastError();
+}
+
+template <int DT>
+hipError_t rt_dispatch(const SpPlan &P, bool mob, void *x, long long cs, long long es, const int *cells, int n_cells,
+                       int max_seq, unsigned char *rec_base, long long rec_head_stride, int n_heads, int max_bands,
+                       hipStream_t s) {
+#define SP_TRY(LY, MOB)                                                                                          \
+    if (layout_matches<LY>(P))                                                                                   \
+        return rt_launch<LY, DT, MOB>(P, mob, x, cs, es, cells, n_cells, max_seq, rec_base, rec_head_stride, n_heads, \
+                                      max_bands, s);
+    SP_TRY(K128, true) SP_TRY(V128, false) SP_TRY(K64, true) SP_TRY(V64, false) SP_TRY(K96, true) SP_TRY(V96, false)
+#undef SP_TRY
+    return hipErrorNotSupported;
+}
+
 template <int DT>
 hipError_t enc_dispatch(const SpPlan &P, bool mob, const void *src, long long so, long long si,
                         unsigned char *dst, long long dout, int n_outer, int n_inner, hipStream_t s) {
@@ -269,4 +404,20 @@ hipError_t sp_launch_ship_decode_lane(const SpPlan &P, bool default_order, const
     if (((uintptr_t)src % 4) || (so % 4)) return hipErrorNotSupported;
     if (dtype == SP_DT_F16) return dec_dispatch<SP_DT_F16>(P, default_order, src, so, dst, dout, din, n_outer, n_inner, s);
     return dec_dispatch<SP_DT_F32>(P, default_order, src, so, dst, dout, din, n_outer, n_inner, s);
+}
+
+// In-place round trip of every head's vectors at n_cells cache cells (see
+// k_ship_roundtrip_lane). hipErrorNotSupported when the layout has no lane
+// specialization.
+hipError_t sp_launch_ship_roundtrip_lane(const SpPlan &P, bool default_order, void *x, int dtype, long long cs,
+                                         long long es, const int *cells, int n_cells, int max_seq,
+                                         unsigned char *rec_base, long long rec_head_stride, int n_heads,
+                                         int max_bands, hipStream_t s) {
+    if (n_cells <= 0 || n_heads <= 0) return hipSuccess;
+    if (((uintptr_t)rec_base % 4) || (rec_head_stride % 4)) return hipErrorNotSupported;
+    if (dtype == SP_DT_F16)
+        return rt_dispatch<SP_DT_F16>(P, default_order, x, cs, es, cells, n_cells, max_seq, rec_base, rec_head_stride,
+                                      n_heads, max_bands, s);
+    return rt_dispatch<SP_DT_F32>(P, default_order, x, cs, es, cells, n_cells, max_seq, rec_base, rec_head_stride,
+                                  n_heads, max_bands, s);
 }

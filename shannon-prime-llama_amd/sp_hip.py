@@ -120,6 +120,7 @@ def lib():
         L.sp_hip_write_layer.argtypes = [vp, i, i, i, vp, vp, ll, i]
         L.sp_hip_read_layer.argtypes = [vp, i, i, i, vp, vp, ll, i, i]
         L.sp_hip_write_all.argtypes = [vp, i, i, vp, vp, i]
+        L.sp_hip_roundtrip_cells.argtypes = [vp, i, vp, i, vp, ll, vp, ll, ll, i, i, vp]
         L.sp_hip_read_all.argtypes = [vp, i, i, vp, vp, i, i]
         L.sp_hip_attn_decode.argtypes = [vp, i, i, vp, i, f, vp, vp, vp]
         L.sp_hip_attn_decode_all_layers.argtypes = [vp, i, vp, i, f, vp, vp]

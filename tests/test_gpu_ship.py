@@ -259,3 +259,64 @@ def test_cache_slots_layer_and_all_layouts():
     assert S.lib().sp_hip_write_layer(cc.ref, 0, 0, 2, p(kt), p(kt), H * hd - 1, S.DTYPE_F16) == -1
     cc.free()
 
+
+@pytest.mark.parametrize("dtype,k_pad,max_bands", [("f16", 0, -1), ("f16", 4, 2), ("f32", 0, 3), ("f32", 3, -1)])
+def test_roundtrip_cells(dtype, k_pad, max_bands):
+    """sp_hip_roundtrip_cells (the device post-decode hook): K as llama.cpp cache rows
+    (row stride H*hd + k_pad: 16-byte pieces, or element by element when the rows
+    are not 16-byte aligned), V in the transposed v_trans layout, 77 scattered cells
+    plus one past max_seq. Records at the listed cells equal the oracle's records of
+    the original vectors; the tensor at those cells holds the oracle's reconstruction
+    (bands >= max_bands zero); every other cell and the row padding are untouched."""
+    say(f"roundtrip cells dtype={dtype} k_pad={k_pad} max_bands={max_bands}")
+    L, H, hd, max_seq, kv_size, layer = 2, 4, 128, 300, 320, 1
+    cfg = S.config(hd, L, H)
+    cc = S.ShipCache(cfg, max_seq, stream=torch.cuda.current_stream().cuda_stream)
+    order = O.mobius_order(hd)
+    kbc, vbc = O.band_config(hd, [5, 5, 4, 3]), O.band_config(hd, [3])
+    rng = np.random.default_rng(50 + k_pad)
+    kcs = H * hd + k_pad
+    npdt = np.float16 if dtype == "f16" else np.float32
+    k = rng.standard_normal((kv_size, kcs)).astype(npdt)
+    v = rng.standard_normal((H * hd, kv_size)).astype(npdt)  # v_trans: [h*hd + d][cell]
+    cells = np.concatenate([rng.choice(max_seq, 77, replace=False), [max_seq + 5]]).astype(np.int32)
+    rng.shuffle(cells)
+    kt, vt, ct = dev(k), dev(v), dev(cells)
+    dt = S.DTYPE_F16 if dtype == "f16" else S.DTYPE_F32
+    S.check(S.lib().sp_hip_roundtrip_cells(cc.ref, layer, p(ct), len(cells), p(kt), kcs, p(vt), 1, kv_size, dt,
+                                           max_bands, None))
+    kg, vg = host(kt), host(vt)
+    kB, vB = kbc.total_bytes, vbc.total_bytes
+    kc = d2h(cc.c.d_k_cache, L * H * max_seq * kB).reshape(L, H, max_seq, kB)
+    vc = d2h(cc.c.d_v_cache, L * H * max_seq * vB).reshape(L, H, max_seq, vB)
+    live = np.sort(cells[cells < max_seq])
+    dead = np.setdiff1d(np.arange(kv_size), live)
+    np.testing.assert_array_equal(kg[dead], k[dead])
+    np.testing.assert_array_equal(vg[:, dead], v[:, dead])
+    np.testing.assert_array_equal(kg[:, H * hd:], k[:, H * hd:])
+    assert not kc[0].any() and not vc[0].any(), "other layer written"
+    mask = np.zeros(max_seq, bool)
+    mask[live] = True
+    for h in range(H):
+        xk, xv = k[live, h * hd:(h + 1) * hd], v[h * hd:(h + 1) * hd, live].T
+        if dtype == "f16":
+            kref = O.ship_compress_f16(xk.view(np.uint16), kbc, order)
+            vref = O.ship_compress_f16(np.ascontiguousarray(xv).view(np.uint16), vbc)
+            krec = O.ship_decompress_f16(kref, kbc, order, max_bands=max_bands).view(np.float16)
+            vrec = O.ship_decompress_f16(vref, vbc, max_bands=max_bands).view(np.float16)
+        else:
+            kref = O.ship_compress_f32(xk, kbc, order)
+            vref = O.ship_compress_f32(np.ascontiguousarray(xv), vbc)
+            krec = O.ship_decompress_f32(kref, kbc, order, max_bands=max_bands)
+            vrec = O.ship_decompress_f32(vref, vbc, max_bands=max_bands)
+        np.testing.assert_array_equal(kc[layer, h, live], kref)
+        np.testing.assert_array_equal(vc[layer, h, live], vref)
+        assert not kc[layer, h, ~mask].any() and not vc[layer, h, ~mask].any()
+        np.testing.assert_array_equal(kg[live, h * hd:(h + 1) * hd].view(np.uint8), krec.view(np.uint8))
+        np.testing.assert_array_equal(vg[h * hd:(h + 1) * hd, live].T.copy().view(np.uint8), vrec.view(np.uint8))
+    # layouts the entry point rejects
+    assert S.lib().sp_hip_roundtrip_cells(cc.ref, layer, p(ct), len(cells), p(kt), H * hd - 1, None, 0, 0, dt, -1,
+                                          None) == -1
+    assert S.lib().sp_hip_roundtrip_cells(cc.ref, layer, p(ct), len(cells), None, 0, p(vt), 2, 2, dt, -1, None) == -1
+    cc.free()
+
