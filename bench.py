@@ -148,7 +148,9 @@ def parity_sample(S, cc, k, v, kr, kB, vB, n_slots):
 
 def bench_variants(torch, S, L, stream, reps=3):
     """Throughput of the other configs' codec paths at their per-GPU shapes (extra
-    fields of the JSON line, not the headline): configs[2] ship codec at hd 96
+    fields of the JSON line, not the headline): the configs[1] post-decode round
+    trip over cache cells (one decode token, a 2048-cell prefill chunk; bytes count
+    the fp16 vector read and written back plus the record), configs[2] ship codec at hd 96
     (Vilenkin 2^5*3, bridge default K 5/4/4, V 5), configs[3] sqfree+spinor
     (pad 154, skeleton 0.75, K/V 5/4/4/4/5, residual 3 bits), configs[4] hier (pad 330,
     30-coefficient skeleton at 5/5 bits, 2-bit residual). Rates count algorithmic
@@ -191,6 +193,27 @@ def bench_variants(torch, S, L, stream, reps=3):
         "record_bytes": [kB3, vB3]}
     c3.free()
     del x, y
+    # configs[1] post-decode hook on the device: sp_hip_roundtrip_cells over one layer's 8 heads,
+    # K as cache rows and V transposed (v_trans), for a 1-token decode step and a 2048-cell prefill chunk
+    H1, KV1, hd1 = 8, 32768, 128
+    cfg = S.config(hd1, 1, H1)
+    c1 = S.ShipCache(cfg, KV1, stream.cuda_stream)
+    kt = torch.randn((KV1, H1 * hd1), generator=g, device="cuda").half()
+    vt = torch.randn((H1 * hd1, KV1), generator=g, device="cuda").half()
+    rt = {}
+    for n_cells, c0 in ((1, 4097), (2048, 8192)):
+        cells = torch.arange(c0, c0 + n_cells, dtype=torch.int32, device="cuda")
+
+        def rt_call():
+            S.check(L.sp_hip_roundtrip_cells(c1.ref, 0, P(cells), n_cells, P(kt), H1 * hd1, P(vt), 1, KV1,
+                                             S.DTYPE_F16, -1, sp))
+        t = timed(rt_call)
+        nv = 2 * H1 * n_cells  # K and V vectors
+        rt[f"cells_{n_cells}"] = {"us": round(t * 1e6, 2), "vecs_per_s": round(nv / t, 1),
+                                  "gbs": round(nv * (2 * 2 * hd1) / t / 1e9 + H1 * n_cells * (76 + 50) / t / 1e9, 1)}
+    out["cfg1_roundtrip_cells"] = dict(rt, layout="K cache rows, V transposed (v_trans), one layer x 8 heads, fp16")
+    c1.free()
+    del kt, vt
     # sqfree+spinor, 12 layers x 4 KV heads x 65536 cells (4 x 16384), hd 128 -> pad 154
     L4, H4, N4 = 12, 4, 65536
     bits4 = (5, 4, 4, 4, 5)
