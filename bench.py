@@ -101,8 +101,14 @@ def cpu_baseline(target_s=8.0):
         t = leg(threads, reps)
         out[name] = (threads, reps, t, 2 * k.shape[0] * reps / t)
     th, reps, t, vps = out["all"]
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), model)
+    except OSError:
+        pass
     return {"value": round(vps, 1), "unit": "KV vecs/s", "cores": th, "kind": "port",
-            "single_thread_value": round(out["single"][3], 1),
+            "single_thread_value": round(out["single"][3], 1), "cpu_model": model,
             "sample": f"{k.shape[0]} K + {v.shape[0]} V hd=128 fp16 vectors (cfg2 distribution) compress+"
                       f"decompress through the C oracle (-O2), repeated {reps}x on {th} OpenMP threads "
                       f"({t:.1f} s); single thread {out['single'][3]:.0f} vecs/s over {out['single'][2]:.1f} s; "
