@@ -78,6 +78,15 @@ typedef struct {
     sp_mobius_mask_t mobius_mask;
     uint8_t        **k_cache;
     uint8_t        **v_cache;
+    /* calibration (fields the engine reads and writes, kv_cache.cpp:553-585, 633-641):
+     * per-coefficient sums of the forward transform of the fed K vectors, the count,
+     * and after sp_shadow_calibrate_end the coefficients ranked by descending variance */
+    int              calibrating;
+    double          *calib_sum;    /* [head_dim] */
+    double          *calib_sum2;   /* [head_dim] */
+    long long        calib_n;
+    int             *var_order;    /* [head_dim] */
+    int              use_var_reorder;
     void            *dev;   /* device-side state owned by the library */
 } sp_shadow_cache_t;
 
@@ -118,6 +127,16 @@ void sp_shadow_read_k_batch(const sp_shadow_cache_t *sc, int layer, int head,
                             int start_pos, int n_pos, float *k_out);
 void sp_shadow_read_v_batch(const sp_shadow_cache_t *sc, int layer, int head,
                             int start_pos, int n_pos, float *v_out);
+
+/* ---- calibration (sp_shadow_calibrate_begin/feed/end, called at kv_cache.cpp:525,
+ * 587, 610). begin clears the sums; feed adds one host fp32 K vector's transform
+ * (computed on the device by the cache's own transform); end ranks the coefficients
+ * by descending variance sum2/n - (sum/n)^2 (ties: lower index first) into var_order,
+ * sets use_var_reorder and makes var_order the K coefficient order of every later
+ * write and read. 0 on success, -1 without data. ---- */
+int  sp_shadow_calibrate_begin(sp_shadow_cache_t *sc);
+void sp_shadow_calibrate_feed(sp_shadow_cache_t *sc, const float *vec);
+int  sp_shadow_calibrate_end(sp_shadow_cache_t *sc);
 
 /* ---- utilities (shannon_prime_llama.c:919, 932; shannon_prime_hexagon.c:234-242) ---- */
 float    sp_correlation_f32(const float *a, const float *b, int n);

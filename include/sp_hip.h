@@ -108,6 +108,17 @@ int sp_hip_roundtrip_cells(sp_hip_cache_t *cc, int layer, const int *d_cells, in
                            void *d_k, long long k_cell_stride, void *d_v, long long v_cell_stride,
                            long long v_elem_stride, int dtype, int max_bands, void *stream);
 
+/* Calibration of the K coefficient order (the CUDA branch of KvCache::calibrate_feed,
+ * kv_cache.cpp:553-585, and the order sync of calibrate_end, :626-652), for device
+ * vectors: feed accumulates per-coefficient sums and sums of squares of the cache's
+ * forward transform of n_vecs K vectors (row i at d_vecs + i*row_stride elements)
+ * in fp64; end ranks the coefficients by descending variance (ties: lower index
+ * first) into var_order_out [head_dim] (may be NULL) and, with apply != 0, makes that
+ * ranking the K coefficient order of later writes, reads and attention. */
+int sp_hip_calibrate_begin(sp_hip_cache_t *cc);
+int sp_hip_calibrate_feed(sp_hip_cache_t *cc, const void *d_vecs, long long row_stride, int n_vecs, int dtype);
+int sp_hip_calibrate_end(sp_hip_cache_t *cc, int *var_order_out, int apply);
+
 /* Every slot at once: src/dst [n_layers*n_heads_kv][n_pos][head_dim] for positions
  * [start_pos, start_pos+n_pos) of each slot (bulk prefill / bulk reconstruct). */
 int sp_hip_write_all(sp_hip_cache_t *cc, int start_pos, int n_pos,
@@ -274,6 +285,17 @@ int  sp_hip_hier_cache_init(sp_hip_hier_cache_t *hc, const sp_config_t *cfg,
                             void *stream);
 void sp_hip_hier_cache_free(sp_hip_hier_cache_t *hc);
 int  sp_hip_hier_cache_upload_W(sp_hip_hier_cache_t *hc, const uint16_t *W_all);
+/* Predictor fit (sp_hier_cache_calibrate_begin/feed/end, kv_cache.cpp:519-521,
+ * 590-597, 606-607, with the W upload of :724-751): feed accumulates, on the device
+ * in fp64, the Gram matrices G_ss = sum s s^T and G_ts = sum t s^T of the slot's
+ * padded, transformed vectors (s = skeleton, t = target coefficients, unquantized);
+ * end solves W = G_ts (G_ss + lambda I)^-1 per fed slot (Cholesky in double,
+ * lambda = ridge * trace(G_ss) / n_skeleton), rounds it to fp16 (via fp32) and
+ * uploads it; slots without data keep their W. */
+int  sp_hip_hier_calibrate_begin(sp_hip_hier_cache_t *hc);
+int  sp_hip_hier_calibrate_feed(sp_hip_hier_cache_t *hc, int slot, const void *d_vecs, long long row_stride,
+                                int n_vecs, int dtype);
+int  sp_hip_hier_calibrate_end(sp_hip_hier_cache_t *hc, double ridge);
 
 void sp_hip_hier_write_k(sp_hip_hier_cache_t *hc, int layer, int head, int pos, const float *d_k_vec);
 void sp_hip_hier_write_v(sp_hip_hier_cache_t *hc, int layer, int head, int pos, const float *d_v_vec);

@@ -256,3 +256,11 @@ hipError_t sp_launch_attn_f16(const unsigned short *k, const unsigned short *v,
                               long long head_stride, int n_kv, int n_q, int n_kvh, int hd,
                               float kq_scale, const float *q, float *scores, float *out,
                               float *workspace, size_t ws_floats, hipStream_t s);
+
+// calibration passes (sp_calib.hip)
+int sp_calib_moment_blocks(int n);
+hipError_t sp_launch_calib_moments(const SpPlan &P, const void *src, int dtype, long long si, int n, double *partials,
+                                   int n_blocks, hipStream_t s);
+int sp_calib_gram_entries(int n_skel, int n_target);
+hipError_t sp_launch_calib_hier_gram(const SpPlan &P, const SpHierGeo &G, const void *src, int dtype, long long si,
+                                     int n, double *partials, int n_blocks, double *acc, hipStream_t s);

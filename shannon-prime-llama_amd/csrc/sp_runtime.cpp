@@ -10,6 +10,8 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
+#include <numeric>
 #include <mutex>
 #include <vector>
 
@@ -418,6 +420,10 @@ struct ShipPriv {
     float *ws = nullptr;
     size_t ws_floats = 0;
     int max_q = 0;
+    // K coefficient-order calibration: fp64 sums of the fed vectors' transforms
+    bool calibrating = false;
+    std::vector<double> csum, csum2;
+    long long cn = 0;
     // host-pointer calls: persistent device staging and pinned host staging,
     // grown on demand (one caller at a time)
     std::mutex stage_mu;
@@ -645,6 +651,105 @@ extern "C" int sp_hip_roundtrip_cells(sp_hip_cache_t *cc, int layer, const int *
         if (e == hipErrorNotSupported) { set_err("roundtrip_cells: no lane kernel for this band layout"); return -1; }
         if (!hip_ok(e, "roundtrip_cells")) return -1;
     }
+    return 0;
+}
+
+// ---- calibration --------------------------------------------------------
+// Per-coefficient sums of the plan's forward transform of n device vectors: the
+// kernel's per-wave fp64 partials are added here in launch order.
+static bool calib_accumulate(const SpPlan &P, const void *d_src, int dtype, long long si, int n, double *sum,
+                             double *sum2, hipStream_t s) {
+    const int hd = P.hd, nb = sp_calib_moment_blocks(n);
+    const size_t cnt = (size_t)nb * 4 * 2 * hd;
+    double *d_part = nullptr;
+    if (!hip_ok(hipMalloc((void **)&d_part, cnt * sizeof(double)), "calib alloc")) return false;
+    std::vector<double> h(cnt);
+    const bool ok = hip_ok(sp_launch_calib_moments(P, d_src, dtype, si, n, d_part, nb, s), "calib moments") &&
+                    hip_ok(hipMemcpyAsync(h.data(), d_part, cnt * sizeof(double), hipMemcpyDeviceToHost, s),
+                           "calib D2H") &&
+                    hip_ok(hipStreamSynchronize(s), "calib sync");
+    (void)hipFree(d_part);
+    if (!ok) return false;
+    for (size_t w = 0; w < (size_t)nb * 4; w++)
+        for (int k = 0; k < hd; k++) {
+            sum[k] += h[w * 2 * hd + k];
+            sum2[k] += h[w * 2 * hd + hd + k];
+        }
+    return true;
+}
+
+// Coefficients by descending variance sum2/n - (sum/n)^2, ties (and NaN, ranked
+// last) by ascending index.
+static void rank_by_variance(const double *sum, const double *sum2, long long n, int hd, int *order) {
+    std::vector<double> var((size_t)hd);
+    for (int k = 0; k < hd; k++) {
+        const double m = sum[k] / (double)n, v = sum2[k] / (double)n - m * m;
+        var[(size_t)k] = std::isnan(v) ? -INFINITY : v;
+    }
+    std::vector<int> idx((size_t)hd);
+    std::iota(idx.begin(), idx.end(), 0);
+    std::stable_sort(idx.begin(), idx.end(), [&](int a, int b) { return var[(size_t)a] > var[(size_t)b]; });
+    std::copy(idx.begin(), idx.end(), order);
+}
+
+static bool is_default_order(const int *order, int hd) {
+    std::vector<int> d((size_t)hd);
+    build_mobius_order(hd, d.data());
+    return std::equal(d.begin(), d.end(), order);
+}
+
+extern "C" int sp_hip_calibrate_begin(sp_hip_cache_t *cc) {
+    if (!cc || !cc->priv) { set_err("calibrate_begin: bad cache"); return -1; }
+    ShipPriv *pv = (ShipPriv *)cc->priv;
+    pv->csum.assign((size_t)cc->config.head_dim, 0.0);
+    pv->csum2.assign((size_t)cc->config.head_dim, 0.0);
+    pv->cn = 0;
+    pv->calibrating = true;
+    return 0;
+}
+
+extern "C" int sp_hip_calibrate_feed(sp_hip_cache_t *cc, const void *d_vecs, long long row_stride, int n_vecs,
+                                     int dtype) {
+    if (!cc || !cc->priv || n_vecs < 0 || (n_vecs > 0 && !d_vecs) || row_stride < cc->config.head_dim ||
+        (dtype != SP_DT_F16 && dtype != SP_DT_F32)) { set_err("calibrate_feed: bad args"); return -1; }
+    ShipPriv *pv = (ShipPriv *)cc->priv;
+    if (!pv->calibrating) { set_err("calibrate_feed: no calibrate_begin"); return -1; }
+    if (n_vecs == 0) return 0;
+    if (!calib_accumulate(pv->kplan, d_vecs, dtype, row_stride, n_vecs, pv->csum.data(), pv->csum2.data(),
+                          (hipStream_t)cc->stream)) return -1;
+    pv->cn += n_vecs;
+    return 0;
+}
+
+// Make `order` the K coefficient order of the cache (and its inverse table).
+static bool install_k_order(sp_hip_cache_t *cc, const int *order) {
+    const int hd = cc->config.head_dim;
+    std::vector<int> inv((size_t)hd);
+    for (int i = 0; i < hd; i++) inv[(size_t)order[i]] = i;
+    if (!cc->d_mobius_order &&
+        !(hip_ok(hipMalloc((void **)&cc->d_mobius_order, sizeof(int) * hd), "hipMalloc order") &&
+          hip_ok(hipMalloc((void **)&cc->d_mobius_inv, sizeof(int) * hd), "hipMalloc inv"))) return false;
+    hipStream_t s = (hipStream_t)cc->stream;
+    if (!(hip_ok(hipStreamSynchronize(s), "order sync") &&
+          hip_ok(hipMemcpy(cc->d_mobius_order, order, sizeof(int) * hd, hipMemcpyHostToDevice), "order H2D") &&
+          hip_ok(hipMemcpy(cc->d_mobius_inv, inv.data(), sizeof(int) * hd, hipMemcpyHostToDevice), "inv H2D")))
+        return false;
+    ShipPriv *pv = (ShipPriv *)cc->priv;
+    pv->kplan.order_default = is_default_order(order, hd) ? 1 : 0;
+    cc->config.use_mobius_mask = 1;
+    return true;
+}
+
+extern "C" int sp_hip_calibrate_end(sp_hip_cache_t *cc, int *var_order_out, int apply) {
+    if (!cc || !cc->priv) { set_err("calibrate_end: bad cache"); return -1; }
+    ShipPriv *pv = (ShipPriv *)cc->priv;
+    if (!pv->calibrating || pv->cn <= 0) { set_err("calibrate_end: no data fed"); return -1; }
+    const int hd = cc->config.head_dim;
+    std::vector<int> order((size_t)hd);
+    rank_by_variance(pv->csum.data(), pv->csum2.data(), pv->cn, hd, order.data());
+    if (var_order_out) std::copy(order.begin(), order.end(), var_order_out);
+    if (apply && !install_k_order(cc, order.data())) return -1;
+    pv->calibrating = false;
     return 0;
 }
 
@@ -985,7 +1090,20 @@ extern "C" int sp_hip_sqfree_get_tables(const sp_hip_sqfree_cache_t *cc, int *sk
 struct HierPriv {
     SpPlan plan;
     bool default_geo;  // skeleton/targets equal sp_hier_default_geometry(pad_dim)
+    // predictor fit: per-slot fp64 Gram accumulators on the device
+    bool calibrating = false;
+    double *d_acc = nullptr;   // [n_slots][n_ent]
+    double *d_part = nullptr;  // [256][n_ent] block partials of one feed
+    std::vector<long long> n_fed;
 };
+
+static void hier_calib_release(HierPriv *pv) {
+    if (pv->d_acc) (void)hipFree(pv->d_acc);
+    if (pv->d_part) (void)hipFree(pv->d_part);
+    pv->d_acc = pv->d_part = nullptr;
+    pv->n_fed.clear();
+    pv->calibrating = false;
+}
 
 extern "C" int sp_hip_hier_cache_init(sp_hip_hier_cache_t *hc, const sp_config_t *cfg, int pad_dim,
                                       int n_skeleton, int n_target, int target_res_bits,
@@ -1046,6 +1164,7 @@ extern "C" void sp_hip_hier_cache_free(sp_hip_hier_cache_t *hc) {
     void *ptrs[] = {hc->d_W, hc->d_skeleton_idx, hc->d_target_idx, hc->d_k_cache, hc->d_v_cache};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
+    if (hc->priv) hier_calib_release((HierPriv *)hc->priv);
     delete (HierPriv *)hc->priv;
     memset(hc, 0, sizeof(*hc));
 }
@@ -1138,6 +1257,111 @@ extern "C" int sp_hip_hier_read_layer(const sp_hip_hier_cache_t *hc, int layer, 
                     "hier read_layer")) return -1;
     }
     return 0;
+}
+
+extern "C" int sp_hip_hier_calibrate_begin(sp_hip_hier_cache_t *hc) {
+    if (!hc || !hc->priv) { set_err("hier calibrate_begin: bad cache"); return -1; }
+    HierPriv *pv = (HierPriv *)hc->priv;
+    hier_calib_release(pv);
+    const size_t n_ent = (size_t)sp_calib_gram_entries(hc->n_skeleton, hc->n_target);
+    const size_t acc_b = (size_t)hc->n_slots * n_ent * sizeof(double);
+    if (!(hip_ok(hipMalloc((void **)&pv->d_acc, acc_b), "hipMalloc gram") &&
+          hip_ok(hipMalloc((void **)&pv->d_part, 256 * n_ent * sizeof(double)), "hipMalloc gram partials") &&
+          hip_ok(hipMemsetAsync(pv->d_acc, 0, acc_b, (hipStream_t)hc->stream), "memset gram"))) {
+        hier_calib_release(pv);
+        return -1;
+    }
+    pv->n_fed.assign((size_t)hc->n_slots, 0);
+    pv->calibrating = true;
+    return 0;
+}
+
+extern "C" int sp_hip_hier_calibrate_feed(sp_hip_hier_cache_t *hc, int slot, const void *d_vecs, long long row_stride,
+                                          int n_vecs, int dtype) {
+    if (!hc || !hc->priv || slot < 0 || slot >= hc->n_slots || n_vecs < 0 || (n_vecs > 0 && !d_vecs) ||
+        row_stride < hc->config.head_dim || (dtype != SP_DT_F16 && dtype != SP_DT_F32)) {
+        set_err("hier calibrate_feed: bad args"); return -1;
+    }
+    HierPriv *pv = (HierPriv *)hc->priv;
+    if (!pv->calibrating) { set_err("hier calibrate_feed: no calibrate_begin"); return -1; }
+    if (n_vecs == 0) return 0;
+    const SpHierGeo G = hier_geo(hc, slot);
+    const int n_ent = sp_calib_gram_entries(hc->n_skeleton, hc->n_target);
+    const int nb = sp_calib_moment_blocks(n_vecs);
+    if (!hip_ok(sp_launch_calib_hier_gram(pv->plan, G, d_vecs, dtype, row_stride, n_vecs, pv->d_part, nb,
+                                          pv->d_acc + (size_t)slot * n_ent, (hipStream_t)hc->stream),
+                "hier gram")) return -1;
+    pv->n_fed[(size_t)slot] += n_vecs;
+    return 0;
+}
+
+// W = G_ts (G_ss + lambda I)^-1 for one slot: Cholesky of the ns x ns system,
+// then one forward / back substitution per target row. False when the system
+// is not positive definite.
+static bool hier_solve(const double *acc, int ns, int nt, double ridge, std::vector<double> &W) {
+    const double *Gts = acc, *Gss = acc + (size_t)nt * ns;
+    double tr = 0.0;
+    for (int i = 0; i < ns; i++) tr += Gss[(size_t)i * ns + i];
+    const double lam = ridge * (tr > 0.0 ? tr / ns : 1.0);
+    std::vector<double> Lm((size_t)ns * ns, 0.0);
+    for (int i = 0; i < ns; i++)
+        for (int j = 0; j <= i; j++) {
+            double v = 0.5 * (Gss[(size_t)i * ns + j] + Gss[(size_t)j * ns + i]) + (i == j ? lam : 0.0);
+            for (int k = 0; k < j; k++) v -= Lm[(size_t)i * ns + k] * Lm[(size_t)j * ns + k];
+            if (i == j) {
+                if (!(v > 0.0)) return false;
+                Lm[(size_t)i * ns + i] = std::sqrt(v);
+            } else {
+                Lm[(size_t)i * ns + j] = v / Lm[(size_t)j * ns + j];
+            }
+        }
+    W.assign((size_t)nt * ns, 0.0);
+    std::vector<double> y((size_t)ns);
+    for (int t = 0; t < nt; t++) {
+        for (int i = 0; i < ns; i++) {
+            double v = Gts[(size_t)t * ns + i];
+            for (int k = 0; k < i; k++) v -= Lm[(size_t)i * ns + k] * y[(size_t)k];
+            y[(size_t)i] = v / Lm[(size_t)i * ns + i];
+        }
+        for (int i = ns - 1; i >= 0; i--) {
+            double v = y[(size_t)i];
+            for (int k = i + 1; k < ns; k++) v -= Lm[(size_t)k * ns + i] * W[(size_t)t * ns + k];
+            W[(size_t)t * ns + i] = v / Lm[(size_t)i * ns + i];
+        }
+    }
+    return true;
+}
+
+extern "C" int sp_hip_hier_calibrate_end(sp_hip_hier_cache_t *hc, double ridge) {
+    if (!hc || !hc->priv || !(ridge >= 0.0)) { set_err("hier calibrate_end: bad args"); return -1; }
+    HierPriv *pv = (HierPriv *)hc->priv;
+    if (!pv->calibrating) { set_err("hier calibrate_end: no calibrate_begin"); return -1; }
+    const int ns = hc->n_skeleton, nt = hc->n_target;
+    const size_t n_ent = (size_t)sp_calib_gram_entries(ns, nt), w_slot = (size_t)nt * ns;
+    std::vector<double> acc((size_t)hc->n_slots * n_ent);
+    std::vector<uint16_t> W_all((size_t)hc->n_slots * w_slot);
+    hipStream_t s = (hipStream_t)hc->stream;
+    bool ok = hip_ok(hipMemcpyAsync(acc.data(), pv->d_acc, acc.size() * sizeof(double), hipMemcpyDeviceToHost, s),
+                     "gram D2H") &&
+              hip_ok(hipMemcpyAsync(W_all.data(), hc->d_W, W_all.size() * sizeof(uint16_t), hipMemcpyDeviceToHost,
+                                    s), "W D2H") &&
+              hip_ok(hipStreamSynchronize(s), "gram sync");
+    if (ok) {
+        std::vector<double> W;
+        for (int slot = 0; slot < hc->n_slots; slot++) {
+            if (pv->n_fed[(size_t)slot] <= 0) continue;
+            uint16_t *dst = W_all.data() + (size_t)slot * w_slot;
+            if (hier_solve(acc.data() + (size_t)slot * n_ent, ns, nt, ridge, W)) {
+                for (size_t e = 0; e < w_slot; e++) dst[e] = sp_f32_to_f16((float)W[e]);
+            } else {
+                std::fill(dst, dst + w_slot, (uint16_t)0);  // degenerate data: no prediction
+            }
+        }
+        ok = hip_ok(hipMemcpy(hc->d_W, W_all.data(), W_all.size() * sizeof(uint16_t), hipMemcpyHostToDevice),
+                    "W upload");
+    }
+    hier_calib_release(pv);
+    return ok ? 0 : -1;
 }
 
 extern "C" void sp_hip_hier_write_k(sp_hip_hier_cache_t *hc, int l, int h, int p, const float *d) { sp_hip_hier_write_batch(hc, 0, l, h, p, 1, d, SP_DT_F32); }
@@ -1268,7 +1492,59 @@ extern "C" void sp_shadow_cache_free(sp_shadow_cache_t *sc) {
         delete dv;
     }
     sp_mobius_mask_free(&sc->mobius_mask);
+    free(sc->calib_sum);
+    free(sc->calib_sum2);
+    free(sc->var_order);
+    sc->calib_sum = sc->calib_sum2 = nullptr;
+    sc->var_order = nullptr;
+    sc->calibrating = sc->use_var_reorder = 0;
     sc->dev = nullptr;
+}
+
+extern "C" int sp_shadow_calibrate_begin(sp_shadow_cache_t *sc) {
+    if (!sc || !sc->dev) return -1;
+    const size_t hd = (size_t)sc->config.head_dim;
+    if (!sc->calib_sum) sc->calib_sum = (double *)malloc(hd * sizeof(double));
+    if (!sc->calib_sum2) sc->calib_sum2 = (double *)malloc(hd * sizeof(double));
+    if (!sc->calib_sum || !sc->calib_sum2) { set_err("calibrate_begin: out of memory"); return -1; }
+    memset(sc->calib_sum, 0, hd * sizeof(double));
+    memset(sc->calib_sum2, 0, hd * sizeof(double));
+    sc->calib_n = 0;
+    sc->calibrating = 1;
+    return 0;
+}
+
+extern "C" void sp_shadow_calibrate_feed(sp_shadow_cache_t *sc, const float *vec) {
+    if (!sc || !sc->dev || !sc->calibrating || !vec || !sc->calib_sum || !sc->calib_sum2) return;
+    ShadowDev *dv = (ShadowDev *)sc->dev;
+    HostStage *st = dv->st;
+    const int hd = sc->config.head_dim;
+    if (!hip_ok(hipMemcpyAsync(st->d_vec, vec, sizeof(float) * hd, hipMemcpyHostToDevice, st->stream), "calib H2D"))
+        return;
+    if (calib_accumulate(dv->kplan, st->d_vec, SP_DT_F32, hd, 1, sc->calib_sum, sc->calib_sum2, st->stream))
+        sc->calib_n++;
+}
+
+extern "C" int sp_shadow_calibrate_end(sp_shadow_cache_t *sc) {
+    if (!sc || !sc->dev || !sc->calib_sum || !sc->calib_sum2 || sc->calib_n <= 0) return -1;
+    const int hd = sc->config.head_dim;
+    if (!sc->var_order) sc->var_order = (int *)malloc(sizeof(int) * (size_t)hd);
+    if (!sc->var_order) { set_err("calibrate_end: out of memory"); return -1; }
+    rank_by_variance(sc->calib_sum, sc->calib_sum2, sc->calib_n, hd, sc->var_order);
+    // var_order becomes the K coefficient order of later writes and reads
+    ShadowDev *dv = (ShadowDev *)sc->dev;
+    HostStage *st = dv->st;
+    if (!st->d_order) {
+        if (!hip_ok(hipMalloc((void **)&st->d_order, sizeof(int) * hd), "hipMalloc order")) return -1;
+        st->order_n = hd;
+    }
+    if (!hip_ok(hipStreamSynchronize(st->stream), "order sync") ||
+        !hip_ok(hipMemcpy(st->d_order, sc->var_order, sizeof(int) * hd, hipMemcpyHostToDevice), "order H2D"))
+        return -1;
+    dv->kplan.order_default = is_default_order(sc->var_order, hd) ? 1 : 0;
+    sc->use_var_reorder = 1;
+    sc->calibrating = 0;
+    return 0;
 }
 
 static uint8_t *shadow_rec(const sp_shadow_cache_t *sc, int is_v, int layer, int head, int pos) {

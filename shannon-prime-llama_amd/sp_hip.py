@@ -43,7 +43,10 @@ class SpShadowCache(C.Structure):
     _fields_ = [
         ("config", SpConfig), ("k_bands", SpBandConfig), ("v_bands", SpBandConfig),
         ("mobius_mask", SpMobiusMask), ("k_cache", C.POINTER(C.POINTER(C.c_uint8))),
-        ("v_cache", C.POINTER(C.POINTER(C.c_uint8))), ("dev", C.c_void_p),
+        ("v_cache", C.POINTER(C.POINTER(C.c_uint8))), ("calibrating", C.c_int),
+        ("calib_sum", C.POINTER(C.c_double)), ("calib_sum2", C.POINTER(C.c_double)),
+        ("calib_n", C.c_longlong), ("var_order", C.POINTER(C.c_int)), ("use_var_reorder", C.c_int),
+        ("dev", C.c_void_p),
     ]
 
 
@@ -121,6 +124,17 @@ def lib():
         L.sp_hip_read_layer.argtypes = [vp, i, i, i, vp, vp, ll, i, i]
         L.sp_hip_write_all.argtypes = [vp, i, i, vp, vp, i]
         L.sp_hip_roundtrip_cells.argtypes = [vp, i, vp, i, vp, ll, vp, ll, ll, i, i, vp]
+        L.sp_hip_calibrate_begin.argtypes = [vp]
+        L.sp_hip_calibrate_feed.argtypes = [vp, vp, ll, i, i]
+        L.sp_hip_calibrate_end.argtypes = [vp, vp, i]
+        L.sp_hip_hier_calibrate_begin.argtypes = [vp]
+        L.sp_hip_hier_calibrate_feed.argtypes = [vp, i, vp, ll, i, i]
+        L.sp_hip_hier_calibrate_end.argtypes = [vp, C.c_double]
+        L.sp_shadow_calibrate_begin.argtypes = [vp]
+        L.sp_shadow_calibrate_feed.argtypes = [vp, vp]
+        L.sp_shadow_calibrate_end.argtypes = [vp]
+        L.sp_shadow_write_k_batch.argtypes = [vp, i, i, i, i, vp]
+        L.sp_shadow_read_k_batch.argtypes = [vp, i, i, i, i, vp]
         L.sp_hip_read_all.argtypes = [vp, i, i, vp, vp, i, i]
         L.sp_hip_attn_decode.argtypes = [vp, i, i, vp, i, f, vp, vp, vp]
         L.sp_hip_attn_decode_all_layers.argtypes = [vp, i, vp, i, f, vp, vp]

@@ -244,6 +244,17 @@ def hier_compress_f16(x16, hd, pad, skel_idx, tgt_idx, skel_bc, W, rbits):
     return out
 
 
+def pad_transform(x32, hd, pad):
+    """fp32 vectors [n][hd] -> padded (true-mean fill, tree-256 order) and
+    transformed [n][pad] (the sqfree / hier coefficients before any quantizing)."""
+    x32 = np.ascontiguousarray(x32, dtype=np.float32)
+    out = np.zeros((x32.shape[0], pad), np.float32)
+    for i in range(x32.shape[0]):
+        lib().spo_sqfree_pad(ptr(x32[i]), ptr(out[i]), hd, pad)
+        lib().spo_vht2_forward(ptr(out[i]), pad, NORM_FINAL)
+    return out
+
+
 def hier_compress_f32(x32, hd, pad, skel_idx, tgt_idx, skel_bc, W, rbits):
     """fp32 vectors [n][hd] -> records [n][B] (spo_hier_compress per vector)."""
     x32 = np.ascontiguousarray(x32, dtype=np.float32)
