@@ -249,6 +249,17 @@ int  sp_hip_sqfree_write_layer(sp_hip_sqfree_cache_t *cc, int layer, int start_p
                                const void *d_k, const void *d_v, long long row_stride, int dtype);
 int  sp_hip_sqfree_read_layer(const sp_hip_sqfree_cache_t *cc, int layer, int start_pos, int n_tok,
                               void *d_k, void *d_v, long long row_stride, int dtype);
+/* Knight-mask recalibration (sp_sqfree_calibrate_begin/feed/end, kv_cache.cpp:523,
+ * 546-548, 608, and the mask sync of :654-722): feed accumulates per-coefficient fp64
+ * sums and sums of squares of the padded transforms of n_vecs device vectors; end
+ * ranks the pad_dim coefficients by descending variance (ties: lower index first)
+ * into ranking_out [pad_dim] (may be NULL) and, with apply != 0, rebuilds the Knight
+ * tables with that ranking in place of the squarefree-first order (skeleton = its
+ * first sk_k entries; the CSR rule is unchanged) for later writes and reads. */
+int sp_hip_sqfree_calibrate_begin(sp_hip_sqfree_cache_t *cc);
+int sp_hip_sqfree_calibrate_feed(sp_hip_sqfree_cache_t *cc, const void *d_vecs, long long row_stride, int n_vecs,
+                                 int dtype);
+int sp_hip_sqfree_calibrate_end(sp_hip_sqfree_cache_t *cc, int *ranking_out, int apply);
 /* Host copies of the Knight tables (for tests and calibration tools). */
 int  sp_hip_sqfree_get_tables(const sp_hip_sqfree_cache_t *cc, int *skeleton_idx,
                               int *residual_idx, int *csr_offsets, int *csr_skel_slot,

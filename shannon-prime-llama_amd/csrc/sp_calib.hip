@@ -1,9 +1,10 @@
 // sp_calib.hip -- calibration passes that feed the codec's tables (the
 // reference's calibrate_begin / feed / end, kv_cache.cpp:515-751):
 //   * per-coefficient first and second moments of the forward transform of a
-//     batch of vectors, for the variance-ranked coefficient order (the CUDA
-//     branch of KvCache::calibrate_feed transforms on the device and
-//     accumulates sum and sum of squares per coefficient, :553-585);
+//     batch of vectors (sqfree: of the padded vector), for the variance-ranked
+//     coefficient order and Knight skeleton (the CUDA branch of
+//     KvCache::calibrate_feed transforms on the device and accumulates sum and
+//     sum of squares per coefficient, :553-585);
 //   * per-slot Gram matrices of the hierarchical skeleton and targets, for the
 //     least-squares predictor W (sp_hier_cache_calibrate_feed / _end, :590-607,
 //     uploaded at :724-751).
@@ -21,10 +22,11 @@ constexpr int CAL_WAVES = 4;  // one vector per wave, four per block
 // runs every round (the transform has block barriers), idle ones on zeros.
 template <int DT>
 __global__ void __launch_bounds__(256)
-k_calib_moments(const SpPlan P, const void *__restrict__ src, long long si, int n, double *__restrict__ partials) {
+k_calib_moments(const SpPlan P, int hd, int tlen, const void *__restrict__ src, long long si, int n,
+                double *__restrict__ partials) {
     __shared__ float c_s[CAL_WAVES][SP_GEN_MAX_N];
     constexpr int MAXK = SP_GEN_MAX_N / SP_WAVE;
-    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, hd = P.hd;
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     float *c = c_s[w];
     double s1[MAXK], s2[MAXK];
 #pragma unroll
@@ -36,12 +38,17 @@ k_calib_moments(const SpPlan P, const void *__restrict__ src, long long si, int 
         const bool valid = v < n;
         for (int k = lane; k < hd; k += SP_WAVE) c[k] = valid ? sp_load1<DT>(src, v * si + k) : 0.0f;
         __syncthreads();
-        sp_transform_lds(c, hd, P, lane);
+        if (tlen > hd) {  // sqfree pad: the true mean, summed in the tree-256 order
+            const float mean = sp_div(sp_wave_tree256_sum(c, hd, 0, lane), (float)hd);
+            for (int k = hd + lane; k < tlen; k += SP_WAVE) c[k] = mean;
+            __syncthreads();
+        }
+        sp_transform_lds(c, tlen, P, lane);
         if (valid) {
 #pragma unroll
             for (int m = 0; m < MAXK; m++) {
                 const int k = lane + SP_WAVE * m;
-                if (k < hd) {
+                if (k < tlen) {
                     const double x = (double)c[k];
                     s1[m] += x;
                     s2[m] += x * x;
@@ -50,13 +57,13 @@ k_calib_moments(const SpPlan P, const void *__restrict__ src, long long si, int 
         }
         __syncthreads();
     }
-    double *out = partials + ((long long)blockIdx.x * CAL_WAVES + w) * 2 * hd;
+    double *out = partials + ((long long)blockIdx.x * CAL_WAVES + w) * 2 * tlen;
 #pragma unroll
     for (int m = 0; m < MAXK; m++) {
         const int k = lane + SP_WAVE * m;
-        if (k < hd) {
+        if (k < tlen) {
             out[k] = s1[m];
-            out[hd + k] = s2[m];
+            out[tlen + k] = s2[m];
         }
     }
 }
@@ -137,13 +144,13 @@ int sp_calib_moment_blocks(int n) {
     return b < 1 ? 1 : (b > 256 ? 256 : b);
 }
 
-hipError_t sp_launch_calib_moments(const SpPlan &P, const void *src, int dtype, long long si, int n, double *partials,
-                                   int n_blocks, hipStream_t s) {
-    if (P.hd > SP_GEN_MAX_N || n <= 0) return hipErrorInvalidValue;
+hipError_t sp_launch_calib_moments(const SpPlan &P, int hd, int tlen, const void *src, int dtype, long long si, int n,
+                                   double *partials, int n_blocks, hipStream_t s) {
+    if (tlen > SP_GEN_MAX_N || hd > tlen || n <= 0) return hipErrorInvalidValue;
     if (dtype == SP_DT_F16)
-        hipLaunchKernelGGL(k_calib_moments<SP_DT_F16>, dim3(n_blocks), dim3(256), 0, s, P, src, si, n, partials);
+        hipLaunchKernelGGL(k_calib_moments<SP_DT_F16>, dim3(n_blocks), dim3(256), 0, s, P, hd, tlen, src, si, n, partials);
     else
-        hipLaunchKernelGGL(k_calib_moments<SP_DT_F32>, dim3(n_blocks), dim3(256), 0, s, P, src, si, n, partials);
+        hipLaunchKernelGGL(k_calib_moments<SP_DT_F32>, dim3(n_blocks), dim3(256), 0, s, P, hd, tlen, src, si, n, partials);
     return hipGetLastError();
 }
 

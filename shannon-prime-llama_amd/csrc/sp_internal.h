@@ -189,6 +189,7 @@ hipError_t sp_launch_permute(float *data, const int *order, int n, int n_vecs, i
 struct SpSqGeo {
     int hd, pad, sk_k, n_res, rbits, spinor, bytes;
     const int *skel_idx, *res_idx, *csr_off, *csr_slot, *csr_mu;
+    int default_tables;  // the Knight tables are the squarefree-first ones (not recalibrated)
 };
 struct SpHierGeo {
     int hd, pad, n_skel, n_target, rbits, bytes;
@@ -259,8 +260,9 @@ hipError_t sp_launch_attn_f16(const unsigned short *k, const unsigned short *v,
 
 // calibration passes (sp_calib.hip)
 int sp_calib_moment_blocks(int n);
-hipError_t sp_launch_calib_moments(const SpPlan &P, const void *src, int dtype, long long si, int n, double *partials,
-                                   int n_blocks, hipStream_t s);
+// moments of the transform over tlen coefficients of hd-element inputs (tlen > hd: mean padded)
+hipError_t sp_launch_calib_moments(const SpPlan &P, int hd, int tlen, const void *src, int dtype, long long si, int n,
+                                   double *partials, int n_blocks, hipStream_t s);
 int sp_calib_gram_entries(int n_skel, int n_target);
 hipError_t sp_launch_calib_hier_gram(const SpPlan &P, const SpHierGeo &G, const void *src, int dtype, long long si,
                                      int n, double *partials, int n_blocks, double *acc, hipStream_t s);

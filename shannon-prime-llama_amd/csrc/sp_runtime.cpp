@@ -655,16 +655,17 @@ extern "C" int sp_hip_roundtrip_cells(sp_hip_cache_t *cc, int layer, const int *
 }
 
 // ---- calibration --------------------------------------------------------
-// Per-coefficient sums of the plan's forward transform of n device vectors: the
-// kernel's per-wave fp64 partials are added here in launch order.
-static bool calib_accumulate(const SpPlan &P, const void *d_src, int dtype, long long si, int n, double *sum,
-                             double *sum2, hipStream_t s) {
-    const int hd = P.hd, nb = sp_calib_moment_blocks(n);
+// Per-coefficient sums of the plan's forward transform (length hd; inputs of
+// in_len < hd elements are mean padded) of n device vectors: the kernel's
+// per-wave fp64 partials are added here in launch order.
+static bool calib_accumulate(const SpPlan &P, int in_len, int hd, const void *d_src, int dtype, long long si, int n,
+                             double *sum, double *sum2, hipStream_t s) {
+    const int nb = sp_calib_moment_blocks(n);
     const size_t cnt = (size_t)nb * 4 * 2 * hd;
     double *d_part = nullptr;
     if (!hip_ok(hipMalloc((void **)&d_part, cnt * sizeof(double)), "calib alloc")) return false;
     std::vector<double> h(cnt);
-    const bool ok = hip_ok(sp_launch_calib_moments(P, d_src, dtype, si, n, d_part, nb, s), "calib moments") &&
+    const bool ok = hip_ok(sp_launch_calib_moments(P, in_len, hd, d_src, dtype, si, n, d_part, nb, s), "calib moments") &&
                     hip_ok(hipMemcpyAsync(h.data(), d_part, cnt * sizeof(double), hipMemcpyDeviceToHost, s),
                            "calib D2H") &&
                     hip_ok(hipStreamSynchronize(s), "calib sync");
@@ -715,7 +716,8 @@ extern "C" int sp_hip_calibrate_feed(sp_hip_cache_t *cc, const void *d_vecs, lon
     ShipPriv *pv = (ShipPriv *)cc->priv;
     if (!pv->calibrating) { set_err("calibrate_feed: no calibrate_begin"); return -1; }
     if (n_vecs == 0) return 0;
-    if (!calib_accumulate(pv->kplan, d_vecs, dtype, row_stride, n_vecs, pv->csum.data(), pv->csum2.data(),
+    const int hd = cc->config.head_dim;
+    if (!calib_accumulate(pv->kplan, hd, hd, d_vecs, dtype, row_stride, n_vecs, pv->csum.data(), pv->csum2.data(),
                           (hipStream_t)cc->stream)) return -1;
     pv->cn += n_vecs;
     return 0;
@@ -860,6 +862,11 @@ extern "C" int sp_hip_attn_decode_f16(const void *d_k, const void *d_v, int n_he
 // ===========================================================================
 struct SqPriv {
     SpPlan kplan, vplan;   // bands over sk_k, transform over pad_dim
+    bool default_tables = true;  // Knight tables not recalibrated
+    // Knight recalibration: fp64 sums of the fed vectors' padded transforms
+    bool calibrating = false;
+    std::vector<double> csum, csum2;
+    long long cn = 0;
 };
 
 static SpSqGeo sq_geo(const sp_hip_sqfree_cache_t *cc, int is_v) {
@@ -876,18 +883,23 @@ static SpSqGeo sq_geo(const sp_hip_sqfree_cache_t *cc, int is_v) {
     G.csr_off = cc->d_csr_offsets;
     G.csr_slot = cc->d_csr_skel_slot;
     G.csr_mu = cc->d_csr_mu_sign;
+    G.default_tables = ((const SqPriv *)cc->priv)->default_tables ? 1 : 0;
     return G;
 }
 
-// Knight mask: skeleton = first sk_k entries of the squarefree-first order over
-// [0, pad); residuals = the rest; CSR terms of residual c (n = c+1): proper
+// Knight mask: skeleton = first sk_k entries of the squarefree-first order (or of
+// a calibrated ranking) over [0, pad); residuals = the rest; CSR terms of residual c (n = c+1): proper
 // divisors d of n whose coefficient d-1 is in the skeleton with mu(n/d) != 0,
 // sign mu(n/d). The reference builder (sp_knight_mask_init, called at
 // shannon_prime_sqfree.cu:606) is absent; this is the build's documented rule.
 static void build_knight(int pad, int sk_k, std::vector<int> &skel, std::vector<int> &res,
-                         std::vector<int> &off, std::vector<int> &slot, std::vector<int> &mu) {
+                         std::vector<int> &off, std::vector<int> &slot, std::vector<int> &mu,
+                         const int *ranking = nullptr) {
+    // ranking: a permutation of [0, pad) (calibration's variance ranking); NULL:
+    // the squarefree-first order
     std::vector<int> order(pad), slot_of(pad, -1);
-    build_mobius_order(pad, order.data());
+    if (ranking) std::copy(ranking, ranking + pad, order.begin());
+    else build_mobius_order(pad, order.data());
     skel.assign(order.begin(), order.begin() + sk_k);
     res.assign(order.begin() + sk_k, order.end());
     for (int s = 0; s < sk_k; s++) slot_of[skel[s]] = s;
@@ -1071,6 +1083,68 @@ extern "C" void sp_hip_sqfree_read_k(const sp_hip_sqfree_cache_t *cc, int l, int
 extern "C" void sp_hip_sqfree_read_v(const sp_hip_sqfree_cache_t *cc, int l, int h, int p, float *d) { sp_hip_sqfree_read_batch(cc, 1, l, h, p, 1, d, SP_DT_F32); }
 extern "C" void sp_hip_sqfree_read_k_batch(const sp_hip_sqfree_cache_t *cc, int l, int h, int s, int n, float *d) { sp_hip_sqfree_read_batch(cc, 0, l, h, s, n, d, SP_DT_F32); }
 extern "C" void sp_hip_sqfree_read_v_batch(const sp_hip_sqfree_cache_t *cc, int l, int h, int s, int n, float *d) { sp_hip_sqfree_read_batch(cc, 1, l, h, s, n, d, SP_DT_F32); }
+
+extern "C" int sp_hip_sqfree_calibrate_begin(sp_hip_sqfree_cache_t *cc) {
+    if (!cc || !cc->priv) { set_err("sqfree calibrate_begin: bad cache"); return -1; }
+    SqPriv *pv = (SqPriv *)cc->priv;
+    pv->csum.assign((size_t)cc->pad_dim, 0.0);
+    pv->csum2.assign((size_t)cc->pad_dim, 0.0);
+    pv->cn = 0;
+    pv->calibrating = true;
+    return 0;
+}
+
+extern "C" int sp_hip_sqfree_calibrate_feed(sp_hip_sqfree_cache_t *cc, const void *d_vecs, long long row_stride,
+                                            int n_vecs, int dtype) {
+    if (!cc || !cc->priv || n_vecs < 0 || (n_vecs > 0 && !d_vecs) || row_stride < cc->config.head_dim ||
+        (dtype != SP_DT_F16 && dtype != SP_DT_F32)) { set_err("sqfree calibrate_feed: bad args"); return -1; }
+    SqPriv *pv = (SqPriv *)cc->priv;
+    if (!pv->calibrating) { set_err("sqfree calibrate_feed: no calibrate_begin"); return -1; }
+    if (n_vecs == 0) return 0;
+    if (!calib_accumulate(pv->kplan, cc->config.head_dim, cc->pad_dim, d_vecs, dtype, row_stride, n_vecs,
+                          pv->csum.data(), pv->csum2.data(), (hipStream_t)cc->stream)) return -1;
+    pv->cn += n_vecs;
+    return 0;
+}
+
+extern "C" int sp_hip_sqfree_calibrate_end(sp_hip_sqfree_cache_t *cc, int *ranking_out, int apply) {
+    if (!cc || !cc->priv) { set_err("sqfree calibrate_end: bad cache"); return -1; }
+    SqPriv *pv = (SqPriv *)cc->priv;
+    if (!pv->calibrating || pv->cn <= 0) { set_err("sqfree calibrate_end: no data fed"); return -1; }
+    const int pad = cc->pad_dim;
+    std::vector<int> rank((size_t)pad);
+    rank_by_variance(pv->csum.data(), pv->csum2.data(), pv->cn, pad, rank.data());
+    if (ranking_out) std::copy(rank.begin(), rank.end(), ranking_out);
+    if (apply) {
+        std::vector<int> skel, res, off, slot, mu;
+        build_knight(pad, cc->sk_k, skel, res, off, slot, mu, rank.data());
+        int *old[5] = {cc->d_skeleton_idx, cc->d_residual_idx, cc->d_csr_offsets, cc->d_csr_skel_slot,
+                       cc->d_csr_mu_sign};
+        cc->d_skeleton_idx = cc->d_residual_idx = cc->d_csr_offsets = cc->d_csr_skel_slot = cc->d_csr_mu_sign = nullptr;
+        const bool ok = hip_ok(hipStreamSynchronize((hipStream_t)cc->stream), "sqfree calib sync") &&
+                        upload(&cc->d_skeleton_idx, skel) && upload(&cc->d_residual_idx, res) &&
+                        upload(&cc->d_csr_offsets, off) && upload(&cc->d_csr_skel_slot, slot) &&
+                        upload(&cc->d_csr_mu_sign, mu);
+        if (!ok) {
+            int *now[5] = {cc->d_skeleton_idx, cc->d_residual_idx, cc->d_csr_offsets, cc->d_csr_skel_slot,
+                           cc->d_csr_mu_sign};
+            for (int *q : now)
+                if (q) (void)hipFree(q);
+            cc->d_skeleton_idx = old[0], cc->d_residual_idx = old[1], cc->d_csr_offsets = old[2];
+            cc->d_csr_skel_slot = old[3], cc->d_csr_mu_sign = old[4];
+            return -1;
+        }
+        for (int *q : old)
+            if (q) (void)hipFree(q);
+        cc->n_terms = (int)slot.size();
+        std::vector<int> dflt((size_t)pad);
+        build_mobius_order(pad, dflt.data());
+        pv->default_tables = std::equal(dflt.begin(), dflt.begin() + cc->sk_k, rank.begin()) &&
+                             std::equal(dflt.begin() + cc->sk_k, dflt.end(), rank.begin() + cc->sk_k);
+    }
+    pv->calibrating = false;
+    return 0;
+}
 
 extern "C" int sp_hip_sqfree_get_tables(const sp_hip_sqfree_cache_t *cc, int *skeleton_idx, int *residual_idx,
                                         int *csr_offsets, int *csr_skel_slot, int *csr_mu_sign) {
@@ -1521,7 +1595,7 @@ extern "C" void sp_shadow_calibrate_feed(sp_shadow_cache_t *sc, const float *vec
     const int hd = sc->config.head_dim;
     if (!hip_ok(hipMemcpyAsync(st->d_vec, vec, sizeof(float) * hd, hipMemcpyHostToDevice, st->stream), "calib H2D"))
         return;
-    if (calib_accumulate(dv->kplan, st->d_vec, SP_DT_F32, hd, 1, sc->calib_sum, sc->calib_sum2, st->stream))
+    if (calib_accumulate(dv->kplan, hd, hd, st->d_vec, SP_DT_F32, hd, 1, sc->calib_sum, sc->calib_sum2, st->stream))
         sc->calib_n++;
 }
 

@@ -235,7 +235,8 @@ using SkelL115 = Layout<115, 5, 4, 4, 4, 5>;
 template <int SK, class SL>
 bool sq_geometry_matches(const SpPlan &P, const SpSqGeo &G) {
     using R = SqRec<154, SK, 3, true, SL>;
-    return G.hd == 128 && G.pad == 154 && G.sk_k == SK && G.n_res == 154 - SK && G.rbits == 3 && G.spinor &&
+    return G.default_tables && G.hd == 128 && G.pad == 154 && G.sk_k == SK && G.n_res == 154 - SK && G.rbits == 3 &&
+           G.spinor &&
            G.bytes == R::total && layout_matches<SL>(P) && vil_consts_exact(P);
 }
 

@@ -127,6 +127,9 @@ def lib():
         L.sp_hip_calibrate_begin.argtypes = [vp]
         L.sp_hip_calibrate_feed.argtypes = [vp, vp, ll, i, i]
         L.sp_hip_calibrate_end.argtypes = [vp, vp, i]
+        L.sp_hip_sqfree_calibrate_begin.argtypes = [vp]
+        L.sp_hip_sqfree_calibrate_feed.argtypes = [vp, vp, ll, i, i]
+        L.sp_hip_sqfree_calibrate_end.argtypes = [vp, vp, i]
         L.sp_hip_hier_calibrate_begin.argtypes = [vp]
         L.sp_hip_hier_calibrate_feed.argtypes = [vp, i, vp, ll, i, i]
         L.sp_hip_hier_calibrate_end.argtypes = [vp, C.c_double]

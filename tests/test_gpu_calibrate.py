@@ -1,6 +1,7 @@
 """Calibration passes on the GPU (the reference's calibrate_begin / feed / end,
 kv_cache.cpp:515-751): the variance-ranked K coefficient order of the ship and
-shadow caches, and the hierarchical predictor fit. The reference's calibrate_end
+shadow caches, the sqfree Knight-mask recalibration, and the hierarchical predictor
+fit. The reference's calibrate_end
 algorithms live in its absent core, so the rules here are this build's (stated in
 the headers); each test recomputes them in numpy (float64) from the oracle's
 bit-exact transforms of the same vectors."""
@@ -188,3 +189,88 @@ def test_hier_calibrate_fit():
     assert res_fit < 0.2 * res_zero, (res_fit, res_zero)
     assert L.sp_hip_hier_calibrate_end(hc.ref, C.c_double(ridge)) == -1  # needs a new begin
     hc.free()
+
+
+def mobius_mu(n):
+    mu, d = 1, 2
+    while d * d <= n:
+        if n % d == 0:
+            n //= d
+            if n % d == 0:
+                return 0
+            mu = -mu
+        d += 1
+    return -mu if n > 1 else mu
+
+
+def knight_tables(ranking, sk):
+    """The Knight rule over a ranking: skeleton = its first sk entries, residuals =
+    the rest; residual c (n = c+1) takes the proper divisors d of n whose
+    coefficient d-1 is in the skeleton and mu(n/d) != 0, with sign mu(n/d)."""
+    skel, res = list(ranking[:sk]), list(ranking[sk:])
+    slot_of = {c: s for s, c in enumerate(skel)}
+    off, slot, mu = [0], [], []
+    for c in res:
+        n = c + 1
+        for d in range(1, n):
+            if n % d == 0 and mobius_mu(n // d) != 0 and (d - 1) in slot_of:
+                slot.append(slot_of[d - 1])
+                mu.append(mobius_mu(n // d))
+        off.append(len(slot))
+    return [np.array(a, np.int32) for a in (skel, res, off, slot, mu)]
+
+
+class CustomKnight:
+    """An oracle Knight mask over given tables."""
+
+    def __init__(self, pad, skel, res, off, slot, mu):
+        self.keep = [np.ascontiguousarray(skel, np.int32), np.ascontiguousarray(res, np.int32),
+                     np.ascontiguousarray(off, np.int32), np.ascontiguousarray(slot, np.int32),
+                     np.ascontiguousarray(mu, np.int8)]
+        P = lambda a, t: a.ctypes.data_as(C.POINTER(t))
+        k = self.keep
+        self.m = O.KnightMask(pad, len(skel), len(res), len(slot), P(k[0], C.c_int), P(k[1], C.c_int),
+                              P(k[2], C.c_int), P(k[3], C.c_int), P(k[4], C.c_int8))
+        self.n_res = len(res)
+
+
+def test_sqfree_knight_recalibration():
+    """Two feeds of K vectors into an hd 128 sqfree cache (pad 154, sk 77); the
+    ranking equals numpy's over the oracle's padded transforms; applied, the device
+    Knight tables follow the rule over that ranking, and records and
+    reconstructions equal the oracle run with those tables."""
+    hd, sk, n = 128, 77, 120
+    pad = O.sqfree_pad_dim(hd)
+    bits = [5, 4, 4, 4, 5]
+    cfg = S.config(hd, 1, 1, k_bits=bits, v_bits=bits)
+    cc = S.SqfreeCache(cfg, n, rbits=3, spinor=True, sk_k=sk, stream=torch.cuda.current_stream().cuda_stream)
+    L = S.lib()
+    x = calib_vectors(1500, hd, seed=70)
+    S.check(L.sp_hip_sqfree_calibrate_begin(cc.ref))
+    a = dev(x[:900].view(np.uint16))
+    b = dev(x[900:].astype(np.float32))
+    S.check(L.sp_hip_sqfree_calibrate_feed(cc.ref, p(a), hd, 900, S.DTYPE_F16))
+    S.check(L.sp_hip_sqfree_calibrate_feed(cc.ref, p(b), hd, 600, S.DTYPE_F32))
+    ranking = np.zeros(pad, np.int32)
+    S.check(L.sp_hip_sqfree_calibrate_end(cc.ref, C.c_void_p(ranking.ctypes.data), 1))
+    np.testing.assert_array_equal(ranking, variance_order(O.pad_transform(x.astype(np.float32), hd, pad)))
+    skel, res, off, slot, mu = knight_tables(ranking, sk)
+    assert cc.c.n_terms == len(slot)
+    got = [np.zeros(len(skel), np.int32), np.zeros(len(res), np.int32), np.zeros(len(off), np.int32),
+           np.zeros(max(len(slot), 1), np.int32), np.zeros(max(len(slot), 1), np.int32)]
+    S.check(L.sp_hip_sqfree_get_tables(cc.ref, *[C.c_void_p(g.ctypes.data) for g in got]))
+    for g, w in zip(got, (skel, res, off, slot, mu)):
+        np.testing.assert_array_equal(g[:len(w)], w)
+    km = CustomKnight(pad, skel, res, off, slot, mu)
+    skel_bc = O.band_config(sk, bits)
+    k16 = W.cfg4_kv(n_heads=1, n_pos=n, hd=hd, seed=71)[0].reshape(n, hd)
+    ref = O.sqfree_compress_f16(k16.view(np.uint16), hd, km, skel_bc, 3, True)
+    rec = O.sqfree_decompress_f32(ref, hd, km, skel_bc, 3, True)
+    kt = dev(k16.view(np.uint16))
+    S.check(L.sp_hip_sqfree_write_batch(cc.ref, 0, 0, 0, 0, n, p(kt), S.DTYPE_F16))
+    np.testing.assert_array_equal(d2h(cc.c.d_k_cache, n * ref.shape[1]).reshape(n, -1), ref)
+    out = empty_f32(n * hd)
+    S.check(L.sp_hip_sqfree_read_batch(cc.ref, 0, 0, 0, 0, n, p(out), S.DTYPE_F32))
+    np.testing.assert_array_equal(host(out).reshape(n, hd).view(np.uint32), rec.view(np.uint32))
+    cc.free()
+
