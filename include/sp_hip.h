@@ -307,6 +307,10 @@ int  sp_hip_hier_calibrate_begin(sp_hip_hier_cache_t *hc);
 int  sp_hip_hier_calibrate_feed(sp_hip_hier_cache_t *hc, int slot, const void *d_vecs, long long row_stride,
                                 int n_vecs, int dtype);
 int  sp_hip_hier_calibrate_end(sp_hip_hier_cache_t *hc, double ridge);
+/* Sticky-EMA end (KvCache::calibrate_end_ema, kv_cache.h:103-107, kv_cache.cpp:758-797):
+ * each fed slot gets W = keep_frac * W_old + (1 - keep_frac) * W_fit (in double, then
+ * fp16 via fp32); keep_frac in [0, 1], 0 is calibrate_end. */
+int  sp_hip_hier_calibrate_end_ema(sp_hip_hier_cache_t *hc, double ridge, float keep_frac);
 
 void sp_hip_hier_write_k(sp_hip_hier_cache_t *hc, int layer, int head, int pos, const float *d_k_vec);
 void sp_hip_hier_write_v(sp_hip_hier_cache_t *hc, int layer, int head, int pos, const float *d_v_vec);

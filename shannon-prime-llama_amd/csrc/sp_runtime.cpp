@@ -1406,8 +1406,13 @@ static bool hier_solve(const double *acc, int ns, int nt, double ridge, std::vec
     return true;
 }
 
-extern "C" int sp_hip_hier_calibrate_end(sp_hip_hier_cache_t *hc, double ridge) {
-    if (!hc || !hc->priv || !(ridge >= 0.0)) { set_err("hier calibrate_end: bad args"); return -1; }
+// Solves every fed slot and uploads W = keep * W_old + (1 - keep) * W_fit (keep = 0:
+// plain replacement), rounded to fp16 via fp32; a slot whose system is not
+// positive definite fits W_fit = 0.
+static int hier_calib_finish(sp_hip_hier_cache_t *hc, double ridge, double keep) {
+    if (!hc || !hc->priv || !(ridge >= 0.0) || !(keep >= 0.0 && keep <= 1.0)) {
+        set_err("hier calibrate_end: bad args"); return -1;
+    }
     HierPriv *pv = (HierPriv *)hc->priv;
     if (!pv->calibrating) { set_err("hier calibrate_end: no calibrate_begin"); return -1; }
     const int ns = hc->n_skeleton, nt = hc->n_target;
@@ -1425,10 +1430,11 @@ extern "C" int sp_hip_hier_calibrate_end(sp_hip_hier_cache_t *hc, double ridge) 
         for (int slot = 0; slot < hc->n_slots; slot++) {
             if (pv->n_fed[(size_t)slot] <= 0) continue;
             uint16_t *dst = W_all.data() + (size_t)slot * w_slot;
-            if (hier_solve(acc.data() + (size_t)slot * n_ent, ns, nt, ridge, W)) {
-                for (size_t e = 0; e < w_slot; e++) dst[e] = sp_f32_to_f16((float)W[e]);
-            } else {
-                std::fill(dst, dst + w_slot, (uint16_t)0);  // degenerate data: no prediction
+            if (!hier_solve(acc.data() + (size_t)slot * n_ent, ns, nt, ridge, W))
+                W.assign(w_slot, 0.0);  // degenerate data: no prediction
+            for (size_t e = 0; e < w_slot; e++) {
+                const double w = keep > 0.0 ? keep * (double)sp_f16_to_f32(dst[e]) + (1.0 - keep) * W[e] : W[e];
+                dst[e] = sp_f32_to_f16((float)w);
             }
         }
         ok = hip_ok(hipMemcpy(hc->d_W, W_all.data(), W_all.size() * sizeof(uint16_t), hipMemcpyHostToDevice),
@@ -1436,6 +1442,14 @@ extern "C" int sp_hip_hier_calibrate_end(sp_hip_hier_cache_t *hc, double ridge) 
     }
     hier_calib_release(pv);
     return ok ? 0 : -1;
+}
+
+extern "C" int sp_hip_hier_calibrate_end(sp_hip_hier_cache_t *hc, double ridge) {
+    return hier_calib_finish(hc, ridge, 0.0);
+}
+
+extern "C" int sp_hip_hier_calibrate_end_ema(sp_hip_hier_cache_t *hc, double ridge, float keep_frac) {
+    return hier_calib_finish(hc, ridge, (double)keep_frac);
 }
 
 extern "C" void sp_hip_hier_write_k(sp_hip_hier_cache_t *hc, int l, int h, int p, const float *d) { sp_hip_hier_write_batch(hc, 0, l, h, p, 1, d, SP_DT_F32); }

@@ -133,6 +133,7 @@ def lib():
         L.sp_hip_hier_calibrate_begin.argtypes = [vp]
         L.sp_hip_hier_calibrate_feed.argtypes = [vp, i, vp, ll, i, i]
         L.sp_hip_hier_calibrate_end.argtypes = [vp, C.c_double]
+        L.sp_hip_hier_calibrate_end_ema.argtypes = [vp, C.c_double, C.c_float]
         L.sp_shadow_calibrate_begin.argtypes = [vp]
         L.sp_shadow_calibrate_feed.argtypes = [vp, vp]
         L.sp_shadow_calibrate_end.argtypes = [vp]

@@ -188,6 +188,24 @@ def test_hier_calibrate_fit():
     res_zero = (T_ ** 2).sum()
     assert res_fit < 0.2 * res_zero, (res_fit, res_zero)
     assert L.sp_hip_hier_calibrate_end(hc.ref, C.c_double(ridge)) == -1  # needs a new begin
+
+    # sticky EMA: refit slots 0 and 2 on the same vectors, keep a quarter of the old W
+    keep = 0.25
+    S.check(L.sp_hip_hier_calibrate_begin(hc.ref))
+    for s in (0, 2):
+        S.check(L.sp_hip_hier_calibrate_feed(hc.ref, s, p(a), hd, 1500, S.DTYPE_F16))
+        S.check(L.sp_hip_hier_calibrate_feed(hc.ref, s, p(b), hd + 4, 1000, S.DTYPE_F32))
+    assert L.sp_hip_hier_calibrate_end_ema(hc.ref, C.c_double(ridge), C.c_float(1.5)) == -1
+    S.check(L.sp_hip_hier_calibrate_end_ema(hc.ref, C.c_double(ridge), C.c_float(keep)))
+    We = d2h(hc.c.d_W, n_slots * nt * ns * 2).view(np.uint16).reshape(n_slots, nt, ns)
+    for s in (1, 3):
+        np.testing.assert_array_equal(We[s], W0[s])
+    for s, old in ((0, W0[0]), (2, Wg[2])):
+        blend = keep * old.view(np.float16).astype(np.float64) + (1 - keep) * Wref
+        want = blend.astype(np.float32).astype(np.float16).view(np.uint16).astype(np.int32)
+        diff = np.abs(We[s].astype(np.int32) - want)
+        assert diff.max() <= 1, (s, diff.max())
+        assert (diff == 0).mean() > 0.999
     hc.free()
 
 
