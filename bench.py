@@ -207,16 +207,24 @@ def bench_variants(torch, S, L, stream, reps=3):
     kt = torch.randn((KV1, H1 * hd1), generator=g, device="cuda").half()
     vt = torch.randn((H1 * hd1, KV1), generator=g, device="cuda").half()
     rt = {}
-    for n_cells, c0 in ((1, 4097), (2048, 8192)):
+    for n_cells, c0 in ((1, 4097), (16, 5000), (256, 6000), (2048, 8192)):
         cells = torch.arange(c0, c0 + n_cells, dtype=torch.int32, device="cuda")
 
         def rt_call():
             S.check(L.sp_hip_roundtrip_cells(c1.ref, 0, P(cells), n_cells, P(kt), H1 * hd1, P(vt), 1, KV1,
                                              S.DTYPE_F16, -1, sp))
-        t = timed(rt_call)
         nv = 2 * H1 * n_cells  # K and V vectors
-        rt[f"cells_{n_cells}"] = {"us": round(t * 1e6, 2), "vecs_per_s": round(nv / t, 1),
-                                  "gbs": round(nv * (2 * 2 * hd1) / t / 1e9 + H1 * n_cells * (76 + 50) / t / 1e9, 1)}
+        for kern in ("default", "narrow", "lane"):
+            # the entry point reads SP_HIP_RT_KERNEL at each call
+            if kern == "default":
+                os.environ.pop("SP_HIP_RT_KERNEL", None)
+            else:
+                os.environ["SP_HIP_RT_KERNEL"] = kern
+            t = timed(rt_call)
+            key = f"cells_{n_cells}" + ("" if kern == "default" else f"_{kern}")
+            rt[key] = {"us": round(t * 1e6, 2), "vecs_per_s": round(nv / t, 1),
+                       "gbs": round(nv * (2 * 2 * hd1) / t / 1e9 + H1 * n_cells * (76 + 50) / t / 1e9, 1)}
+        os.environ.pop("SP_HIP_RT_KERNEL", None)
     out["cfg1_roundtrip_cells"] = dict(rt, layout="K cache rows, V transposed (v_trans), one layer x 8 heads, fp16")
     c1.free()
     del kt, vt
@@ -383,6 +391,15 @@ def main():
             for layer in range(LAYERS):
                 S.check(L.sp_hip_attn_decode(cc.ref, layer, POS, P(q[layer]), NQ, scale, P(sc), None, sptr), "kq")
 
+        def fused_bands(want_out, mb=2):
+            # band-limited decode (K bands >= mb read as 0; the single V band stays)
+            def f():
+                for layer in range(LAYERS):
+                    S.check(L.sp_hip_attn_decode_bands(cc.ref, layer, POS, P(q[layer]), NQ, scale,
+                                                       None if want_out else P(sc),
+                                                       P(out[layer]) if want_out else None, mb, sptr), "bands")
+            return f
+
         def fp16():
             for layer in range(LAYERS):
                 S.check(L.sp_hip_attn_decode_f16(P(k), P(v), KVH, POS, HD, layer, POS, P(q[layer]), NQ, scale,
@@ -417,10 +434,13 @@ def main():
 
         us_fused, us_kq, us_f16 = timeit(fused), timeit(fused_kq), timeit(fp16)
         us_tkq, us_tattn = timeit(torch_kq), timeit(torch_attn)
+        us_kq_b2, us_attn_b2 = timeit(fused_bands(False)), timeit(fused_bands(True))
         kv_bytes = LAYERS * KVH * POS * (kB + vB)
         result.update({
             "fused_dqkq_us_per_tok": round(us_fused, 1),
             "fused_kq_only_us_per_tok": round(us_kq, 1),
+            "fused_kq_only_2bands_us_per_tok": round(us_kq_b2, 1),
+            "fused_dqkq_2bands_us_per_tok": round(us_attn_b2, 1),
             "fp16_torch_kq_us_per_tok": round(us_tkq, 1),
             "fp16_torch_attn_us_per_tok": round(us_tattn, 1),
             "fp16_attn_us_per_tok": round(us_f16, 1),
@@ -430,7 +450,8 @@ def main():
             "fused_attn_floor_us_per_tok": round(kv_bytes / (HBM_PEAK_GBS * 1e3), 1),
         })
         log(f"[bench] fused attn {us_fused:.1f} us/tok, KQ-only {us_kq:.1f}; fp16 torch attn {us_tattn:.1f}, "
-            f"torch KQ {us_tkq:.1f}, fp16 lane kernel {us_f16:.1f}")
+            f"torch KQ {us_tkq:.1f}, fp16 lane kernel {us_f16:.1f}; 2 K bands: KQ {us_kq_b2:.1f}, "
+            f"attn {us_attn_b2:.1f}")
     if args.only in ("variants", "all"):
         result["variants"] = bench_variants(torch, S, L, stream)
         log("[bench] variants: " + json.dumps(result["variants"]))

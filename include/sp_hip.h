@@ -95,15 +95,18 @@ int sp_hip_read_layer(const sp_hip_cache_t *cc, int layer, int start_pos, int n_
  * n_cells cache cells listed in d_cells (device int32, any order), compress the
  * vector held in the llama.cpp cache tensor into the records at that cell and
  * overwrite the vector with its reconstruction (bands >= max_bands read as 0;
- * max_bands < 0 reads every band). One launch per K/V for the whole layer.
+ * max_bands < 0 reads every band). One launch for the whole layer.
  * K: element (cell, h, d) at cell*k_cell_stride + h*head_dim + d.
  * V: element (cell, h, d) at cell*v_cell_stride + (h*head_dim + d)*v_elem_stride:
  *    rows (v_elem_stride 1, v_cell_stride >= n_heads_kv*head_dim) or llama.cpp's
  *    transposed V (v_trans: v_cell_stride 1, v_elem_stride = kv_size >= max_seq).
  * NULL d_k or d_v skips that side; cells outside [0, max_seq) are skipped.
- * Needs a band layout with a lane specialization (hd 128 K 5/5/4/3 + V 3, hd 64
- * K 5/5/4/3 + V 5, hd 96 K 5/4/4 + V 5) and the default Mobius order; returns -1
- * otherwise. */
+ * Head_dim 64, 128 or 256 with band boundaries on multiples of 8 coefficients
+ * takes any coefficient order (default Mobius or calibrated); hd 96 needs K 5/4/4 +
+ * V 5 and the default order. Returns -1 for any other layout. The power-of-two
+ * widths run head_dim/8 lanes per vector with K and V in one launch; hd 96 runs one
+ * vector per lane, one launch per side (SP_HIP_RT_KERNEL=narrow|lane forces either
+ * kernel where its layout allows). */
 int sp_hip_roundtrip_cells(sp_hip_cache_t *cc, int layer, const int *d_cells, int n_cells,
                            void *d_k, long long k_cell_stride, void *d_v, long long v_cell_stride,
                            long long v_elem_stride, int dtype, int max_bands, void *stream);
@@ -175,6 +178,16 @@ int sp_hip_ship_decode(const sp_band_config_t *bc, const int *d_order, int vht2_
 int sp_hip_attn_decode(const sp_hip_cache_t *cc, int layer, int n_kv,
                        const float *d_q, int n_q, float kq_scale,
                        float *d_scores, float *d_out, void *stream);
+
+/* Band-limited attention, the phase-3 attention short-circuit
+ * (llama-cpp-b8861-full-engine.patch:1442-1452 and :347-359, SHANNON_PRIME_DEFAULT_BANDS):
+ * K and V bands >= max_bands read as 0, as in sp_llama_read_k/v_partial
+ * (shannon_prime_llama.h:240-255), so the result equals attention over the
+ * partial reconstructions; the skipped bands cost no matrix-core work.
+ * max_bands < 0 (or >= n_bands) is sp_hip_attn_decode. */
+int sp_hip_attn_decode_bands(const sp_hip_cache_t *cc, int layer, int n_kv,
+                             const float *d_q, int n_q, float kq_scale,
+                             float *d_scores, float *d_out, int max_bands, void *stream);
 
 /* Every layer of one decode step in one launch sequence: q [n_layers][n_q][hd],
  * out [n_layers][n_q][hd] (benchmark helper; per-layer semantics above). */

@@ -807,6 +807,18 @@ void spo_attn_decode(const float *q, const uint8_t *kpack, const uint8_t *vpack,
                      const spo_band_config_t *kbc, const spo_band_config_t *vbc,
                      const int *order, int norm_mode, float kq_scale,
                      float *scores, float *out) {
+    spo_attn_decode_bands(q, kpack, vpack, n_q, n_kvh, n_ctx, hd, kbc, vbc, order, norm_mode, kq_scale,
+                          scores, out, -1);
+}
+
+/* Attention over the partial reconstructions (bands >= max_bands read as 0, the
+ * read_k/v_partial semantics of shannon_prime_llama.h:240-255, applied to K and V
+ * as the post-decode hook does, llama-cpp-b8861-full-engine.patch:1336-1337). */
+void spo_attn_decode_bands(const float *q, const uint8_t *kpack, const uint8_t *vpack,
+                           int n_q, int n_kvh, int n_ctx, int hd,
+                           const spo_band_config_t *kbc, const spo_band_config_t *vbc,
+                           const int *order, int norm_mode, float kq_scale,
+                           float *scores, float *out, int max_bands) {
     int grp = n_q / n_kvh;
     float *kt = (float *)malloc(sizeof(float) * (size_t)hd);
     double *s = (double *)malloc(sizeof(double) * (size_t)n_ctx);
@@ -816,7 +828,7 @@ void spo_attn_decode(const float *q, const uint8_t *kpack, const uint8_t *vpack,
         double mx = -INFINITY;
         for (int t = 0; t < n_ctx; t++) {
             spo_ship_decompress(kpack + ((size_t)kh * n_ctx + t) * kbc->total_bytes, kt, kbc,
-                                order, norm_mode, -1);
+                                order, norm_mode, max_bands);
             double acc = 0.0;
             for (int d = 0; d < hd; d++) acc += (double)q[(size_t)h * hd + d] * (double)kt[d];
             s[t] = acc * (double)kq_scale;
@@ -830,7 +842,7 @@ void spo_attn_decode(const float *q, const uint8_t *kpack, const uint8_t *vpack,
             double p = exp(s[t] - mx);
             l += p;
             spo_ship_decompress(vpack + ((size_t)kh * n_ctx + t) * vbc->total_bytes, kt, vbc,
-                                NULL, norm_mode, -1);
+                                NULL, norm_mode, max_bands);
             for (int d = 0; d < hd; d++) o[d] += p * (double)kt[d];
         }
         for (int d = 0; d < hd; d++) out[(size_t)h * hd + d] = (float)(o[d] / l);

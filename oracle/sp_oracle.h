@@ -170,6 +170,13 @@ void spo_attn_decode(const float *q, const uint8_t *kpack, const uint8_t *vpack,
                      const spo_band_config_t *kbc, const spo_band_config_t *vbc,
                      const int *order, int norm_mode, float kq_scale,
                      float *scores, float *out);
+/* The same over the partial reconstructions: K and V bands >= max_bands read as 0
+ * (max_bands < 0: every band). */
+void spo_attn_decode_bands(const float *q, const uint8_t *kpack, const uint8_t *vpack,
+                           int n_q, int n_kvh, int n_ctx, int hd,
+                           const spo_band_config_t *kbc, const spo_band_config_t *vbc,
+                           const int *order, int norm_mode, float kq_scale,
+                           float *scores, float *out, int max_bands);
 
 /* ---- metrics ---- */
 float spo_correlation_f32(const float *a, const float *b, int n);

@@ -79,7 +79,7 @@ k_attn_split(const SpPlan KP, const SpPlan VP, const SpAttnArgs A, const float *
         float acc[ATT_MAX_G];
 #pragma unroll
         for (int h = 0; h < ATT_MAX_G; h++) acc[h] = 0.0f;
-        for (int b = 0; b < KP.n_bands; b++) {
+        for (int b = 0; b < KP.max_bands; b++) {  // bands past the limit read as 0
             const int off = KP.band_off[b], sz = KP.band_sz[b], bits = KP.band_bits[b];
             const int maxv = (1 << (bits - 1)) - 1;
             const int bo = KP.band_byte_off[b];
@@ -133,7 +133,8 @@ k_attn_split(const SpPlan KP, const SpPlan VP, const SpAttnArgs A, const float *
         float o[ATT_MAX_G];
 #pragma unroll
         for (int h = 0; h < ATT_MAX_G; h++) o[h] = 0.0f;
-        for (int t = 0; t < nt; t++) {
+        const int nt_v = b < VP.max_bands ? nt : 0;  // a band past the limit reads as 0
+        for (int t = 0; t < nt_v; t++) {
             const unsigned char *rec = vrec + t * A.vB;
             const float scale = sp_scale_from_bits((uint32_t)rec[bo] | ((uint32_t)rec[bo + 1] << 8));
             const float d = (float)((int)sp_unpack_bits_lds(rec + bo + 2, k, bits) - maxv) * scale;

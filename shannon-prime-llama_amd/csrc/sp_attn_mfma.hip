@@ -214,10 +214,10 @@ __device__ __forceinline__ void load_split(const SpAttnArgs &A, int kvh, int spl
 // splits). The query operand is prepared once per block; each round stages one
 // split's records from registers into LDS and prefetches the next split's
 // while it computes. Every split writes its own partial.
-template <bool WANT_OUT>
+template <bool WANT_OUT, bool ALL_BANDS>
 __global__ void __launch_bounds__(256, WANT_OUT ? 3 : 4)
 k_attn_mfma_split(const SpAttnArgs A, const int *__restrict__ order, float *__restrict__ ws, int n_splits,
-                  int rounds) {
+                  int rounds, int kbands, int vbands) {
     __shared__ __attribute__((aligned(16))) unsigned char smem[WANT_OUT ? LDS_FULL : LDS_KQ];
     unsigned char *krec = smem + OFF_U;
     unsigned char *dvt = smem + OFF_U;
@@ -377,10 +377,10 @@ k_attn_mfma_split(const SpAttnArgs A, const int *__restrict__ order, float *__re
             const bool live = tid < n_chunk;
 #pragma unroll
             for (int b = 0; b < 4; b++)
-                ks[tid * 4 + b] = live ? scale_of(*reinterpret_cast<const unsigned short *>(r + kbyte(b))) : 0.0f;
+                ks[tid * 4 + b] = live && (ALL_BANDS || b < kbands) ? scale_of(*reinterpret_cast<const unsigned short *>(r + kbyte(b))) : 0.0f;
             if (WANT_OUT) {
                 const unsigned char *v = smem + OFF_VREC + vshift + tid * VB;
-                reinterpret_cast<float *>(smem + OFF_VS)[tid] = live ? scale_of(*reinterpret_cast<const unsigned short *>(v)) : 0.0f;
+                reinterpret_cast<float *>(smem + OFF_VS)[tid] = live && (ALL_BANDS || vbands > 0) ? scale_of(*reinterpret_cast<const unsigned short *>(v)) : 0.0f;
             }
         }
         __syncthreads();
@@ -396,6 +396,7 @@ k_attn_mfma_split(const SpAttnArgs A, const int *__restrict__ order, float *__re
             float acc0 = 0.0f, acc1 = 0.0f;
 #pragma unroll
             for (int b = 0; b < 4; b++) {
+                if (!ALL_BANDS && b >= kbands) break;  // bands past the limit read as 0 (kernel-uniform)
                 const uint32_t d0 = *reinterpret_cast<const uint32_t *>(rec + wofs[b]);
                 const uint32_t d1 = *reinterpret_cast<const uint32_t *>(rec + wofs[b] + 4);
                 half8_t code;
@@ -621,9 +622,16 @@ hipError_t sp_launch_attn_mfma_split(const SpPlan &KP, const SpPlan &VP, const i
     const int rounds = total > target ? (total + target - 1) / target : 1;
     const int nb = (n_splits + rounds - 1) / rounds;
     *n_parts = nb;
-    if (A.out)
-        hipLaunchKernelGGL(k_attn_mfma_split<true>, dim3(A.n_kvh, nb), dim3(256), 0, s, A, order, part, n_splits, rounds);
-    else
-        hipLaunchKernelGGL(k_attn_mfma_split<false>, dim3(A.n_kvh, nb), dim3(256), 0, s, A, order, part, n_splits, rounds);
+    // every band: a branch-free score loop (the band-limited one schedules worse)
+    const bool all = KP.max_bands >= 4 && VP.max_bands >= 1;
+    const dim3 grid(A.n_kvh, nb);
+    const int kb_lim = KP.max_bands, vb_lim = VP.max_bands;
+    if (A.out) {
+        if (all) hipLaunchKernelGGL((k_attn_mfma_split<true, true>), grid, dim3(256), 0, s, A, order, part, n_splits, rounds, kb_lim, vb_lim);
+        else hipLaunchKernelGGL((k_attn_mfma_split<true, false>), grid, dim3(256), 0, s, A, order, part, n_splits, rounds, kb_lim, vb_lim);
+    } else {
+        if (all) hipLaunchKernelGGL((k_attn_mfma_split<false, true>), grid, dim3(256), 0, s, A, order, part, n_splits, rounds, kb_lim, vb_lim);
+        else hipLaunchKernelGGL((k_attn_mfma_split<false, false>), grid, dim3(256), 0, s, A, order, part, n_splits, rounds, kb_lim, vb_lim);
+    }
     return hipGetLastError();
 }

@@ -182,6 +182,15 @@ hipError_t sp_launch_ship_roundtrip_lane(const SpPlan &P, bool default_order, vo
                                          long long es, const int *cells, int n_cells, int max_seq,
                                          unsigned char *rec_base, long long rec_head_stride, int n_heads,
                                          int max_bands, hipStream_t s);
+// the same round trip with head_dim/8 lanes per vector and K and V in one launch
+// (a null k or v skips that side; V element (c, h, d) at c*vcs + (h*hd + d)*ves, K
+// at c*kcs + h*hd + d); any coefficient order; head_dim 64, 128 or 256 with band
+// boundaries on multiples of 8, else hipErrorNotSupported
+hipError_t sp_launch_ship_roundtrip_narrow(const SpPlan &KP, const int *korder, void *k, long long kcs,
+                                           unsigned char *krec, long long krhs, const SpPlan &VP, void *v,
+                                           long long vcs, long long ves, unsigned char *vrec, long long vrhs,
+                                           int dtype, const int *cells, int n_cells, int max_seq, int n_heads,
+                                           int max_bands, hipStream_t s);
 hipError_t sp_launch_permute(float *data, const int *order, int n, int n_vecs, int inverse,
                              hipStream_t s);
 

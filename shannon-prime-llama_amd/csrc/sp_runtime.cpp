@@ -636,6 +636,23 @@ extern "C" int sp_hip_roundtrip_cells(sp_hip_cache_t *cc, int layer, const int *
     if (n_cells == 0) return 0;
     ShipPriv *pv = (ShipPriv *)cc->priv;
     hipStream_t s = (hipStream_t)(stream ? stream : cc->stream);
+    // The narrow kernel (head_dim/8 lanes per vector, K and V in one launch) wherever
+    // its layouts allow: measured faster than the one-vector-per-lane kernel from a
+    // single decode cell (7.3 vs 31.6 us per layer, 8 heads) to 2048-cell prefill
+    // chunks (20.9 vs 32.7 us). The lane kernel covers hd 96. SP_HIP_RT_KERNEL=narrow|lane
+    // forces either.
+    const char *force = getenv("SP_HIP_RT_KERNEL");
+    const bool f_lane = force && !strcmp(force, "lane"), f_narrow = force && !strcmp(force, "narrow");
+    if (!f_lane) {
+        const long long kB = cc->k_bands.total_bytes, vB = cc->v_bands.total_bytes;
+        const hipError_t e = sp_launch_ship_roundtrip_narrow(
+            pv->kplan, cc->d_mobius_order, d_k, k_cell_stride, slot_ptr(cc, 0, layer, 0, 0),
+            (long long)cc->max_seq_len * kB, pv->vplan, d_v, v_cell_stride, v_elem_stride,
+            slot_ptr(cc, 1, layer, 0, 0), (long long)cc->max_seq_len * vB, dtype, d_cells, n_cells,
+            cc->max_seq_len, H, max_bands, s);
+        if (e != hipErrorNotSupported) return hip_ok(e, "roundtrip_cells") ? 0 : -1;
+        if (f_narrow) { set_err("roundtrip_cells: no narrow kernel for this band layout"); return -1; }
+    }
     for (int is_v = 0; is_v < 2; is_v++) {
         void *x = is_v ? d_v : d_k;
         if (!x) continue;
@@ -795,8 +812,8 @@ extern "C" int sp_hip_read_all(const sp_hip_cache_t *cc, int start_pos, int n_po
 // ===========================================================================
 // fused attention
 // ===========================================================================
-extern "C" int sp_hip_attn_decode(const sp_hip_cache_t *cc, int layer, int n_kv, const float *d_q,
-                                  int n_q, float kq_scale, float *d_scores, float *d_out, void *stream) {
+extern "C" int sp_hip_attn_decode_bands(const sp_hip_cache_t *cc, int layer, int n_kv, const float *d_q, int n_q,
+                                        float kq_scale, float *d_scores, float *d_out, int max_bands, void *stream) {
     if (!cc || !cc->priv || layer < 0 || layer >= cc->config.n_layers || n_kv <= 0 ||
         n_kv > cc->max_seq_len || !d_q || n_q <= 0) { set_err("attn: bad args"); return -1; }
     ShipPriv *pv = (ShipPriv *)cc->priv;
@@ -817,9 +834,19 @@ extern "C" int sp_hip_attn_decode(const sp_hip_cache_t *cc, int layer, int n_kv,
     A.q = d_q;
     A.scores = d_scores;
     A.out = d_out;
-    return hip_ok(sp_launch_attn_decode(pv->kplan, pv->vplan, cc->d_mobius_order, A, pv->ws,
-                                        pv->ws_floats, (hipStream_t)(stream ? stream : cc->stream)),
+    SpPlan kp = pv->kplan, vp = pv->vplan;
+    if (max_bands >= 0) {
+        if (max_bands < kp.n_bands) kp.max_bands = max_bands;
+        if (max_bands < vp.n_bands) vp.max_bands = max_bands;
+    }
+    return hip_ok(sp_launch_attn_decode(kp, vp, cc->d_mobius_order, A, pv->ws, pv->ws_floats,
+                                        (hipStream_t)(stream ? stream : cc->stream)),
                   "attn launch") ? 0 : -1;
+}
+
+extern "C" int sp_hip_attn_decode(const sp_hip_cache_t *cc, int layer, int n_kv, const float *d_q,
+                                  int n_q, float kq_scale, float *d_scores, float *d_out, void *stream) {
+    return sp_hip_attn_decode_bands(cc, layer, n_kv, d_q, n_q, kq_scale, d_scores, d_out, -1, stream);
 }
 
 extern "C" int sp_hip_attn_decode_all_layers(const sp_hip_cache_t *cc, int n_kv, const float *d_q, int n_q,

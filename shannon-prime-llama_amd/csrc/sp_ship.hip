@@ -23,8 +23,10 @@
 #include "sp_internal.h"
 
 #include <stdlib.h>
+#include <string.h>
 
 #define SP_TILE 64
+#define SP_RT_MAX_CHUNKS 32   // narrow round trip: head_dim / 8 for head_dim <= 256
 
 // ---------------------------------------------------------------------------
 // register-resident p=2 VHT2 over 8 coefficients/lane, head_dim/8 lanes/vector
@@ -304,6 +306,139 @@ k_ship_decode_fast(const SpPlan P, const int *__restrict__ order,
         sp_vht2_regs<HD, NORM>(x, j, P.inv_sqrt_n);
         if (valid)
             sp_store8<DT>(dst, (long long)o * dst_outer + (long long)(i0 + lv) * dst_inner + j * 8, x);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// narrow cell round trip: head_dim/8 lanes per vector, K and V in one launch
+// ---------------------------------------------------------------------------
+// The post-decode hook's compress + partial decompress of the new cells (the
+// same contract as k_ship_roundtrip_lane), built for a handful of cells: a
+// decode step has one cell per KV head, so the latency of one vector sets the
+// cost. Spreading a vector over head_dim/8 lanes cuts the serial work per lane
+// eightfold against the one-vector-per-lane kernel, and both sides (blockIdx.y:
+// K, V) share one launch. The codes stay in registers between the encode and
+// the decode, so the reconstruction is bit-identical to decoding the stored
+// record. Any coefficient order (default or calibrated) is taken from memory.
+struct RtSide {
+    unsigned char *x;      // cache tensor: element (cell, h, d) at cell*cs + (h*hd + d)*es
+    long long cs, es;
+    unsigned char *rec;    // record of (h, cell) at rec + h*rhs + cell*B
+    long long rhs;
+    const int *order;      // coefficient order; null: none
+    int B, max_bands, contig;
+    float inv_sqrt_n;
+    unsigned char chunk_band[SP_RT_MAX_CHUNKS];
+    short chunk_byte_off[SP_RT_MAX_CHUNKS];
+    unsigned char band_first[SP_MAX_BANDS_DEV], band_last[SP_MAX_BANDS_DEV], band_bits[SP_MAX_BANDS_DEV];
+    short band_byte_off[SP_MAX_BANDS_DEV];
+};
+struct RtArgs {
+    RtSide side[2];
+};
+
+template <int HD, int DT, int NORM>
+__global__ void __launch_bounds__(256)
+k_ship_roundtrip_narrow(const RtArgs A, const int *__restrict__ cells, int n_cells, int max_seq, int n_vec) {
+    constexpr int LPV = HD / 8, VPW = 64 / LPV;
+    __shared__ float coef[4][VPW][HD];
+    const RtSide &S = A.side[blockIdx.y];
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int g = lane / LPV, j = lane % LPV;
+    const int v = (blockIdx.x * 4 + w) * VPW + g;  // head-major: v = h * n_cells + i
+    const bool in_range = v < n_vec;
+    const int h = in_range ? v / n_cells : 0, i = in_range ? v - h * n_cells : 0;
+    const int c = in_range ? cells[i] : -1;
+    const bool live = in_range && c >= 0 && c < max_seq;
+    const long long base = (long long)(live ? c : 0) * S.cs + (long long)h * HD * S.es;
+    const int b = S.chunk_band[j], bits = S.band_bits[b], maxv = (1 << (bits - 1)) - 1;
+    const int cf = S.band_first[b], cl = S.band_last[b];
+    const bool mob = S.order != nullptr;  // uniform over the block (one side per block)
+    int ord[8];
+    if (mob) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) ord[e] = S.order[j * 8 + e];
+    }
+    float x[8];
+    if (live && S.contig) {
+        sp_load8<DT>(S.x, base + j * 8, x);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) x[e] = live ? sp_load1<DT>(S.x, base + (long long)(j * 8 + e) * S.es) : 0.0f;
+    }
+    sp_vht2_regs<HD, NORM>(x, j, S.inv_sqrt_n);
+    if (mob) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) coef[w][g][j * 8 + e] = x[e];
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < 8; e++) x[e] = coef[w][g][ord[e]];
+        __syncthreads();
+    }
+    // band absmax over the band's lanes (segmented scans both ways)
+    float m = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) m = fmaxf(m, fabsf(x[e]));
+    float mf = m, mb = m;
+#pragma unroll
+    for (int d = 1; d < LPV; d <<= 1) {
+        const float t = __shfl_up(mf, d, LPV);
+        if (j - d >= cf) mf = fmaxf(mf, t);
+    }
+#pragma unroll
+    for (int d = 1; d < LPV; d <<= 1) {
+        const float t = __shfl_down(mb, d, LPV);
+        if (j + d <= cl) mb = fmaxf(mb, t);
+    }
+    const float amax = fmaxf(mf, mb);
+    const float scale = (amax > 0.0f) ? sp_div(amax, (float)maxv) : 0.0f;
+    const uint32_t hb = sp_f32_to_f16_bits(scale);
+    const float ss = sp_f16_bits_to_f32(hb);
+    const float inv = (ss > 0.0f) ? sp_div(1.0f, ss) : 0.0f;
+    int q[8];
+    uint64_t acc = 0;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        q[e] = sp_q_rint_clamp(x[e] * inv, maxv);
+        acc |= (uint64_t)(uint32_t)(q[e] + maxv) << (e * bits);
+    }
+    if (live) {
+        unsigned char *pr = S.rec + (long long)h * S.rhs + (long long)c * S.B;
+        const int off = S.chunk_byte_off[j];
+        for (int k = 0; k < bits; k++) pr[off + k] = (unsigned char)(acc >> (8 * k));
+        if (j == cf) {
+            pr[S.band_byte_off[b]] = (unsigned char)(hb & 0xffu);
+            pr[S.band_byte_off[b] + 1] = (unsigned char)(hb >> 8);
+        }
+    }
+    // decode from the codes just formed (bands >= max_bands read as 0)
+    const float ds = b < S.max_bands ? sp_scale_from_bits(hb) : 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) x[e] = b < S.max_bands ? (float)q[e] * ds : 0.0f;
+    if (mob) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) coef[w][g][ord[e]] = x[e];
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < 8; e++) x[e] = coef[w][g][j * 8 + e];
+        __syncthreads();
+    }
+    sp_vht2_regs<HD, NORM>(x, j, S.inv_sqrt_n);
+    if (!live) return;
+    if (S.contig) {
+        sp_store8<DT>(S.x, base + j * 8, x);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const long long off = base + (long long)(j * 8 + e) * S.es;
+            if (DT == SP_DT_F16) {
+                float t = x[e];
+                __asm__ volatile("" : "+v"(t));  // round once, fp32 -> fp16
+                reinterpret_cast<_Float16 *>(S.x)[off] = (_Float16)t;
+            } else {
+                reinterpret_cast<float *>(S.x)[off] = x[e];
+            }
+        }
     }
 }
 
@@ -593,5 +728,68 @@ hipError_t sp_launch_permute(float *data, const int *order, int n, int n_vecs, i
     if (n_vecs <= 0) return hipSuccess;
     if (n > SP_GEN_MAX_N) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_permute, dim3((n_vecs + 3) / 4), dim3(256), 0, s, data, order, n, n_vecs, inverse);
+    return hipGetLastError();
+}
+
+// In-place round trip of n_cells cells of every head, K (ks.x != null) and V
+// (vs.x != null) in one launch, through k_ship_roundtrip_narrow.
+// hipErrorNotSupported when a side's layout does not fit it (head_dim not 64, 128
+// or 256, or a band boundary off a multiple of 8, or no transform).
+hipError_t sp_launch_ship_roundtrip_narrow(const SpPlan &KP, const int *korder, void *k, long long kcs,
+                                           unsigned char *krec, long long krhs, const SpPlan &VP, void *v,
+                                           long long vcs, long long ves, unsigned char *vrec, long long vrhs,
+                                           int dtype, const int *cells, int n_cells, int max_seq, int n_heads,
+                                           int max_bands, hipStream_t s) {
+    if (n_cells <= 0 || n_heads <= 0 || (!k && !v)) return hipSuccess;
+    const int hd = k ? KP.hd : VP.hd;
+    if (!(hd == 64 || hd == 128 || hd == 256)) return hipErrorNotSupported;
+    const int esz = dtype == SP_DT_F16 ? 2 : 4;
+    RtArgs A;
+    int ns = 0;
+    for (int is_v = 0; is_v < 2; is_v++) {
+        void *x = is_v ? v : k;
+        if (!x) continue;
+        const SpPlan &P = is_v ? VP : KP;
+        if (P.hd != hd || !P.chunk_ok || P.skip_transform || P.n_bands > SP_MAX_BANDS_DEV || P.norm != KP.norm)
+            return hipErrorNotSupported;
+        RtSide &S = A.side[ns++];
+        memset(&S, 0, sizeof(S));
+        S.x = (unsigned char *)x;
+        S.cs = is_v ? vcs : kcs;
+        S.es = is_v ? ves : 1;
+        S.rec = is_v ? vrec : krec;
+        S.rhs = is_v ? vrhs : krhs;
+        S.order = is_v ? nullptr : korder;
+        S.B = P.total_bytes;
+        S.max_bands = (max_bands < 0 || max_bands > P.n_bands) ? P.n_bands : max_bands;
+        S.contig = S.es == 1 && (uintptr_t)x % 16 == 0 && (S.cs * esz) % 16 == 0;
+        S.inv_sqrt_n = P.inv_sqrt_n;
+        for (int c = 0; c < hd / 8; c++) {
+            S.chunk_band[c] = P.chunk_band[c];
+            S.chunk_byte_off[c] = P.chunk_byte_off[c];
+        }
+        for (int b = 0; b < P.n_bands; b++) {
+            S.band_first[b] = P.chunk_first[b];
+            S.band_last[b] = P.chunk_last[b];
+            S.band_bits[b] = P.band_bits[b];
+            S.band_byte_off[b] = P.band_byte_off[b];
+        }
+    }
+    const int n_vec = n_heads * n_cells;
+    const int vpb = 4 * (64 / (hd / 8));
+    const dim3 grid((unsigned)((n_vec + vpb - 1) / vpb), (unsigned)ns), block(256);
+#define SP_RTN(HDV, DTV, NV) \
+    hipLaunchKernelGGL((k_ship_roundtrip_narrow<HDV, DTV, NV>), grid, block, 0, s, A, cells, n_cells, max_seq, n_vec)
+#define SP_RTN_DT(HDV)                                                  \
+    if (dtype == SP_DT_F16) {                                           \
+        if (KP.norm == 1) SP_RTN(HDV, SP_DT_F16, 1); else SP_RTN(HDV, SP_DT_F16, 0); \
+    } else {                                                            \
+        if (KP.norm == 1) SP_RTN(HDV, SP_DT_F32, 1); else SP_RTN(HDV, SP_DT_F32, 0); \
+    }
+    if (hd == 64) { SP_RTN_DT(64) }
+    else if (hd == 128) { SP_RTN_DT(128) }
+    else { SP_RTN_DT(256) }
+#undef SP_RTN_DT
+#undef SP_RTN
     return hipGetLastError();
 }

@@ -141,6 +141,7 @@ def lib():
         L.sp_shadow_read_k_batch.argtypes = [vp, i, i, i, i, vp]
         L.sp_hip_read_all.argtypes = [vp, i, i, vp, vp, i, i]
         L.sp_hip_attn_decode.argtypes = [vp, i, i, vp, i, f, vp, vp, vp]
+        L.sp_hip_attn_decode_bands.argtypes = [vp, i, i, vp, i, f, vp, vp, i, vp]
         L.sp_hip_attn_decode_all_layers.argtypes = [vp, i, vp, i, f, vp, vp]
         L.sp_hip_attn_decode_f16.argtypes = [vp, vp, i, i, i, i, i, vp, i, f, vp, vp, vp]
         L.sp_hip_sqfree_write_batch.argtypes = [vp, i, i, i, i, i, vp, i]

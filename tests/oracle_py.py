@@ -68,6 +68,8 @@ def lib():
         _lib.spo_correlation_f32.restype = C.c_float
         _lib.spo_attn_decode.argtypes = [C.c_void_p] * 3 + [C.c_int] * 4 + [C.c_void_p] * 3 + \
             [C.c_int, C.c_float, C.c_void_p, C.c_void_p]
+        _lib.spo_attn_decode_bands.argtypes = [C.c_void_p] * 3 + [C.c_int] * 4 + [C.c_void_p] * 3 + \
+            [C.c_int, C.c_float, C.c_void_p, C.c_void_p, C.c_int]
     return _lib
 
 
@@ -280,15 +282,15 @@ def hier_decompress_f32(packed, hd, pad, skel_idx, tgt_idx, skel_bc, W, rbits):
 
 
 def attn_decode(q, kpack, vpack, n_kvh, n_ctx, kbc, vbc, order, kq_scale, norm=NORM_FINAL,
-                want_scores=True, want_out=True):
+                want_scores=True, want_out=True, max_bands=-1):
     q = np.ascontiguousarray(q, dtype=np.float32)
     n_q, hd = q.shape
     scores = np.zeros((n_q, n_ctx), np.float32) if want_scores else None
     out = np.zeros((n_q, hd), np.float32) if want_out else None
     o = None if order is None else np.ascontiguousarray(order, dtype=np.int32)
-    lib().spo_attn_decode(ptr(q), ptr(np.ascontiguousarray(kpack)), ptr(np.ascontiguousarray(vpack)),
-                          n_q, n_kvh, n_ctx, hd, C.byref(kbc), C.byref(vbc), ptr(o), norm,
-                          C.c_float(kq_scale), ptr(scores), ptr(out))
+    lib().spo_attn_decode_bands(ptr(q), ptr(np.ascontiguousarray(kpack)), ptr(np.ascontiguousarray(vpack)),
+                                n_q, n_kvh, n_ctx, hd, C.byref(kbc), C.byref(vbc), ptr(o), norm,
+                                C.c_float(kq_scale), ptr(scores), ptr(out), max_bands)
     return scores, out
 
 

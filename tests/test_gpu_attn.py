@@ -79,6 +79,48 @@ def test_fused_attention_matches_oracle(n_q, H, n_ctx, hd, mob, path, monkeypatc
     cc.free()
 
 
+@pytest.mark.parametrize("path", ["mfma", "general"])
+@pytest.mark.parametrize("n_q,H,n_ctx", [(8, 2, 300), (32, 8, 1100)])
+def test_band_limited_attention_matches_oracle(n_q, H, n_ctx, path, monkeypatch):
+    """sp_hip_attn_decode_bands for every band limit 0..4 and -1 against the oracle
+    over the partial reconstructions (1e-3); a limit of 4 or -1 equals the full call
+    bit for bit."""
+    if path == "general":
+        monkeypatch.setenv("SP_HIP_NO_MFMA_ATTN", "1")
+    hd = 128
+    k16, v16 = W.cfg2_kv(n_heads=H, n_pos=n_ctx, hd=hd, seed=n_ctx + 3)
+    q = W.cfg2_q(n_q=n_q, hd=hd, pos=n_ctx, seed=n_ctx + 4)
+    cfg = S.config(hd, 1, H)
+    cc = S.ShipCache(cfg, n_ctx, stream=torch.cuda.current_stream().cuda_stream)
+    L = S.lib()
+    for h in range(H):
+        kt, vt = dev(k16[h].view(np.uint16)), dev(v16[h].view(np.uint16))
+        L.sp_hip_write_k_batch_f16(cc.ref, 0, h, 0, n_ctx, p(kt))
+        L.sp_hip_write_v_batch_f16(cc.ref, 0, h, 0, n_ctx, p(vt))
+    torch.cuda.synchronize()
+    kbc, vbc = O.band_config(hd, [5, 5, 4, 3]), O.band_config(hd, [3])
+    order = O.mobius_order(hd)
+    kref = np.stack([O.ship_compress_f16(k16[h].view(np.uint16), kbc, order) for h in range(H)])
+    vref = np.stack([O.ship_compress_f16(v16[h].view(np.uint16), vbc) for h in range(H)])
+    scale = 1.0 / math.sqrt(hd)
+    qt = dev(q)
+    sc_full, out_full = empty_f32(n_q * n_ctx), empty_f32(n_q * hd)
+    S.check(L.sp_hip_attn_decode(cc.ref, 0, n_ctx, p(qt), n_q, C.c_float(scale), p(sc_full), p(out_full), stream()))
+    for mb in (0, 1, 2, 3, 4, -1):
+        say(f"attn bands path={path} n_q={n_q} H={H} n_ctx={n_ctx} max_bands={mb}")
+        sc, out = empty_f32(n_q * n_ctx), empty_f32(n_q * hd)
+        S.check(L.sp_hip_attn_decode_bands(cc.ref, 0, n_ctx, p(qt), n_q, C.c_float(scale), p(sc), p(out), mb,
+                                           stream()))
+        if mb in (4, -1):
+            np.testing.assert_array_equal(host(sc), host(sc_full))
+            np.testing.assert_array_equal(host(out), host(out_full))
+            continue
+        s_ref, o_ref = O.attn_decode(q, kref, vref, H, n_ctx, kbc, vbc, order, scale, max_bands=mb)
+        rel_close(host(sc).reshape(n_q, n_ctx), s_ref)
+        rel_close(host(out).reshape(n_q, hd), o_ref)
+    cc.free()
+
+
 def test_attention_rejects_bad_shapes():
     cfg = S.config(128, 1, 2)
     cc = S.ShipCache(cfg, 64)

@@ -260,15 +260,19 @@ def test_cache_slots_layer_and_all_layouts():
     cc.free()
 
 
+@pytest.mark.parametrize("kernel", ["narrow", "lane"])
 @pytest.mark.parametrize("dtype,k_pad,max_bands", [("f16", 0, -1), ("f16", 4, 2), ("f32", 0, 3), ("f32", 3, -1)])
-def test_roundtrip_cells(dtype, k_pad, max_bands):
+def test_roundtrip_cells(dtype, k_pad, max_bands, kernel, monkeypatch):
     """sp_hip_roundtrip_cells (the device post-decode hook): K as llama.cpp cache rows
     (row stride H*hd + k_pad: 16-byte pieces, or element by element when the rows
     are not 16-byte aligned), V in the transposed v_trans layout, 77 scattered cells
     plus one past max_seq. Records at the listed cells equal the oracle's records of
     the original vectors; the tensor at those cells holds the oracle's reconstruction
-    (bands >= max_bands zero); every other cell and the row padding are untouched."""
-    say(f"roundtrip cells dtype={dtype} k_pad={k_pad} max_bands={max_bands}")
+    (bands >= max_bands zero); every other cell and the row padding are untouched.
+    Both kernels: head_dim/8 lanes per vector with K and V in one launch, and one
+    vector per lane, one launch per side."""
+    monkeypatch.setenv("SP_HIP_RT_KERNEL", kernel)
+    say(f"roundtrip cells kernel={kernel} dtype={dtype} k_pad={k_pad} max_bands={max_bands}")
     L, H, hd, max_seq, kv_size, layer = 2, 4, 128, 300, 320, 1
     cfg = S.config(hd, L, H)
     cc = S.ShipCache(cfg, max_seq, stream=torch.cuda.current_stream().cuda_stream)
@@ -320,3 +324,54 @@ def test_roundtrip_cells(dtype, k_pad, max_bands):
     assert S.lib().sp_hip_roundtrip_cells(cc.ref, layer, p(ct), len(cells), None, 0, p(vt), 2, 2, dt, -1, None) == -1
     cc.free()
 
+
+
+@pytest.mark.parametrize("hd,n_cells,calibrated,v_trans", [(64, 1, False, True), (128, 1, True, True),
+                                                         (256, 5, False, False), (128, 300, True, False)])
+def test_roundtrip_cells_any_order_and_width(hd, n_cells, calibrated, v_trans):
+    """The narrow round trip at head_dim 64 / 128 / 256, a single decode cell, and a
+    calibrated (variance-ranked) K order, which the one-vector-per-lane kernel does
+    not take: records and reconstructions equal the oracle's with that order."""
+    say(f"roundtrip narrow hd={hd} n_cells={n_cells} calibrated={calibrated} v_trans={v_trans}")
+    L, H, max_seq, layer = 1, 4, 400, 0
+    cfg = S.config(hd, L, H)
+    cc = S.ShipCache(cfg, max_seq, stream=torch.cuda.current_stream().cuda_stream)
+    Lb = S.lib()
+    rng = np.random.default_rng(hd + n_cells)
+    order = O.mobius_order(hd)
+    if calibrated:
+        calib = (rng.standard_normal((512, hd)) * np.linspace(0.1, 3.0, hd)).astype(np.float16)
+        ct0 = dev(calib.view(np.uint16))
+        S.check(Lb.sp_hip_calibrate_begin(cc.ref))
+        S.check(Lb.sp_hip_calibrate_feed(cc.ref, p(ct0), hd, 512, S.DTYPE_F16))
+        got = np.zeros(hd, np.int32)
+        S.check(Lb.sp_hip_calibrate_end(cc.ref, got.ctypes.data_as(C.c_void_p), 1))
+        order = got
+        assert not np.array_equal(order, O.mobius_order(hd))
+    kbc = O.band_config(hd, list(cfg.k_band_bits[:cfg.k_n_bands]))
+    vbc = O.band_config(hd, list(cfg.v_band_bits[:cfg.v_n_bands]))
+    row = H * hd
+    k = rng.standard_normal((max_seq, row)).astype(np.float16)
+    v = rng.standard_normal((row, max_seq) if v_trans else (max_seq, row)).astype(np.float16)
+    cells = rng.choice(max_seq, n_cells, replace=False).astype(np.int32)
+    kt, vt, ct = dev(k.view(np.uint16)), dev(v.view(np.uint16)), dev(cells)
+    vcs, ves = (1, max_seq) if v_trans else (row, 1)
+    S.check(Lb.sp_hip_roundtrip_cells(cc.ref, layer, p(ct), n_cells, p(kt), row, p(vt), vcs, ves, S.DTYPE_F16, -1,
+                                      None))
+    kg, vg = host(kt).view(np.float16).reshape(k.shape), host(vt).view(np.float16).reshape(v.shape)
+    kB, vB = kbc.total_bytes, vbc.total_bytes
+    kc = d2h(cc.c.d_k_cache, H * max_seq * kB).reshape(H, max_seq, kB)
+    vc = d2h(cc.c.d_v_cache, H * max_seq * vB).reshape(H, max_seq, vB)
+    for h in range(H):
+        xk = np.ascontiguousarray(k[cells, h * hd:(h + 1) * hd])
+        xv = np.ascontiguousarray(v[h * hd:(h + 1) * hd, cells].T if v_trans else v[cells, h * hd:(h + 1) * hd])
+        kref = O.ship_compress_f16(xk.view(np.uint16), kbc, order)
+        vref = O.ship_compress_f16(xv.view(np.uint16), vbc)
+        np.testing.assert_array_equal(kc[h, cells], kref)
+        np.testing.assert_array_equal(vc[h, cells], vref)
+        krec = O.ship_decompress_f16(kref, kbc, order).view(np.float16)
+        vrec = O.ship_decompress_f16(vref, vbc).view(np.float16)
+        np.testing.assert_array_equal(kg[cells, h * hd:(h + 1) * hd].view(np.uint16), krec.view(np.uint16))
+        vgot = vg[h * hd:(h + 1) * hd, cells].T if v_trans else vg[cells, h * hd:(h + 1) * hd]
+        np.testing.assert_array_equal(np.ascontiguousarray(vgot).view(np.uint16), vrec.view(np.uint16))
+    cc.free()

@@ -298,3 +298,31 @@ def test_attention_oracle_matches_dense_softmax():
         p = np.exp(ref_s - ref_s.max())
         p /= p.sum()
         np.testing.assert_allclose(out[h], p @ vr[h // 2], rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("mb", [0, 1, 2, 3])
+def test_band_limited_attention_oracle_matches_dense_softmax(mb):
+    """Band-limited attention equals a dense softmax over the partial
+    reconstructions (K and V bands >= mb read as 0); every band is the full one."""
+    k16, v16 = W.cfg2_kv(n_heads=2, n_pos=48, seed=mb + 7)
+    q = W.cfg2_q(n_q=4, pos=48, seed=mb + 8)
+    kbc, vbc = O.band_config(128, [5, 5, 4, 3]), O.band_config(128, [3])
+    order = O.mobius_order(128)
+    kp = np.stack([O.ship_compress_f16(k16[h].view(np.uint16), kbc, order) for h in range(2)])
+    vp = np.stack([O.ship_compress_f16(v16[h].view(np.uint16), vbc) for h in range(2)])
+    scale = 1 / math.sqrt(128)
+    s, out = O.attn_decode(q, kp, vp, 2, 48, kbc, vbc, order, scale, max_bands=mb)
+    kr = np.stack([O.ship_decompress_f32(kp[h], kbc, order, max_bands=mb) for h in range(2)]).astype(np.float64)
+    vr = np.stack([O.ship_decompress_f32(vp[h], vbc, max_bands=mb) for h in range(2)]).astype(np.float64)
+    if mb == 0:
+        assert not kr.any() and not vr.any()
+    for h in range(4):
+        ref_s = kr[h // 2] @ q[h].astype(np.float64) * scale
+        np.testing.assert_allclose(s[h], ref_s, rtol=1e-5, atol=1e-5)
+        p = np.exp(ref_s - ref_s.max())
+        p /= p.sum()
+        np.testing.assert_allclose(out[h], p @ vr[h // 2], rtol=1e-5, atol=1e-6)
+    s4, o4 = O.attn_decode(q, kp, vp, 2, 48, kbc, vbc, order, scale, max_bands=4)
+    s_all, o_all = O.attn_decode(q, kp, vp, 2, 48, kbc, vbc, order, scale)
+    np.testing.assert_array_equal(s4, s_all)
+    np.testing.assert_array_equal(o4, o_all)
