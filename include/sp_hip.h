@@ -343,6 +343,51 @@ int  sp_hip_hier_read_layer(const sp_hip_hier_cache_t *hc, int layer, int start_
                             void *d_k, void *d_v, long long row_stride, int dtype);
 
 /* ======================================================================== */
+/* System 1/2 dual cache (DualKvCache, kv_cache.h:238-310,                  */
+/* kv_cache.cpp:1641-1877)                                                  */
+/* ======================================================================== */
+/* System 1 is a ship cache; System 2 a sqfree or hier cache of the same
+ * n_layers, n_heads_kv, head_dim and max_seq_len on the same stream. Both are
+ * initialised and freed by the caller; the dual cache holds the per-position
+ * route table (all positions start in System 1). */
+#define SP_DUAL_SQFREE 1
+#define SP_DUAL_HIER   2
+typedef struct {
+    sp_hip_cache_t  *sys1;
+    void            *sys2;            /* sp_hip_sqfree_cache_t* or sp_hip_hier_cache_t* */
+    int              sys2_kind;       /* SP_DUAL_SQFREE or SP_DUAL_HIER */
+    float            entropy_threshold;
+    int              max_seq_len;
+    void            *priv;            /* route table, device list of System 2 positions */
+} sp_hip_dual_cache_t;
+
+/* DualKvCache::create_gpu (:1641-1690) over caches the caller built; -1 when the
+ * shapes or streams differ. */
+int  sp_hip_dual_init(sp_hip_dual_cache_t *dc, sp_hip_cache_t *sys1, int sys2_kind, void *sys2,
+                      float entropy_threshold);
+void sp_hip_dual_free(sp_hip_dual_cache_t *dc);
+/* DualKvCache::route_position (:1692-1697): System 2 when entropy >= the threshold;
+ * returns 1 for System 2, 0 for System 1 (and for pos outside [0, max_seq)). */
+int  sp_hip_dual_route_position(sp_hip_dual_cache_t *dc, int pos, float entropy);
+/* DualKvCache::owner_of (:1699-1702): 1 or 2; 1 outside [0, max_seq). */
+int  sp_hip_dual_owner_of(const sp_hip_dual_cache_t *dc, int pos);
+/* DualKvCache::sys1_count / sys2_count (:1862-1876): over all max_seq positions. */
+int  sp_hip_dual_sys1_count(const sp_hip_dual_cache_t *dc);
+int  sp_hip_dual_sys2_count(const sp_hip_dual_cache_t *dc);
+/* DualKvCache::write_gpu (:1733-1751): each of positions [start_pos, start_pos +
+ * n_tok) goes to its owner only, one layer-wide write per run of positions with
+ * the same owner; rows as for sp_hip_write_layer. */
+int  sp_hip_dual_write_layer(sp_hip_dual_cache_t *dc, int layer, int start_pos, int n_tok,
+                             const void *d_k, const void *d_v, long long row_stride, int dtype);
+/* DualKvCache::read_merged_gpu (:1832-1860), with the per-position merge its
+ * comment leaves for later: positions [0, kv_len) of `layer`, each from its owner,
+ * into rows (t, h, d) at t*row_stride + h*head_dim + d. System 1 is decoded over
+ * the whole range, then System 2 over its own positions only, overwriting those
+ * rows on the shared stream. NULL d_k or d_v skips that side. */
+int  sp_hip_dual_read_merged(sp_hip_dual_cache_t *dc, int layer, int kv_len, void *d_k, void *d_v,
+                             long long row_stride, int dtype);
+
+/* ======================================================================== */
 /* Runtime                                                                  */
 /* ======================================================================== */
 

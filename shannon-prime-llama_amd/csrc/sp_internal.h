@@ -228,15 +228,18 @@ hipError_t sp_launch_sqfree_decode_lane(const SpPlan &P, const SpSqGeo &G, const
 hipError_t sp_launch_sqfree_encode(const SpPlan &P, const SpSqGeo &G, const void *src, int dtype,
                                    long long so, long long si, unsigned char *dst, long long dout,
                                    int n_outer, int n_inner, hipStream_t s);
+// cells (optional, device int32 [n_inner]): decode the records at positions
+// cells[i] into rows cells[i] instead of positions 0..n_inner-1
 hipError_t sp_launch_sqfree_decode(const SpPlan &P, const SpSqGeo &G, const unsigned char *src,
                                    long long so, void *dst, int dtype, long long dout,
-                                   long long din, int n_outer, int n_inner, hipStream_t s);
+                                   long long din, int n_outer, int n_inner, hipStream_t s,
+                                   const int *cells = nullptr);
 hipError_t sp_launch_hier_encode(const SpPlan &P, const SpHierGeo &G, const void *src, int dtype,
                                  long long so, long long si, unsigned char *dst, long long dout,
                                  int n_outer, int n_inner, hipStream_t s);
 hipError_t sp_launch_hier_decode(const SpPlan &P, const SpHierGeo &G, const unsigned char *src,
                                  long long so, void *dst, int dtype, long long dout, long long din,
-                                 int n_outer, int n_inner, hipStream_t s);
+                                 int n_outer, int n_inner, hipStream_t s, const int *cells = nullptr);
 
 // Fused decode attention (sp_attn.hip).
 #define SP_CACHE_SLACK 256  // bytes allocated past the last record of a packed ship cache

@@ -1763,3 +1763,183 @@ extern "C" int sp_hip_read_host(const sp_hip_cache_t *cc, int is_v, int layer, i
     if (ok) memcpy(h_out, pv->stage_h, n * sizeof(float));
     return ok ? 0 : -1;
 }
+
+// ===========================================================================
+// System 1/2 dual cache (DualKvCache, kv_cache.cpp:1593-1877)
+// ===========================================================================
+// A per-position route table chooses the owner of each position: System 1 (the
+// ship cache) or System 2 (a sqfree or hier cache). Writes go to the owner only;
+// the merged read decodes System 1 over the whole range and then System 2 over
+// the sorted list of its positions only (the general kernels' listed-position
+// form), writing those rows over System 1's output on the same stream.
+struct DualPriv {
+    std::vector<unsigned char> route;  // 1: System 2
+    int n2 = 0;                        // positions routed to System 2
+    bool dirty = true;                 // device list out of date
+    int *d_list = nullptr;             // System 2 positions, ascending
+    int *h_list = nullptr;             // pinned staging for the list upload
+    int n_list = 0;
+};
+
+static bool dual_dims(const sp_hip_dual_cache_t *dc, int *L, int *H, int *hd, int *ms) {
+    if (!dc || !dc->priv || !dc->sys1 || !dc->sys2) return false;
+    *L = dc->sys1->config.n_layers, *H = dc->sys1->config.n_heads_kv, *hd = dc->sys1->config.head_dim;
+    *ms = dc->max_seq_len;
+    return true;
+}
+
+extern "C" int sp_hip_dual_init(sp_hip_dual_cache_t *dc, sp_hip_cache_t *sys1, int sys2_kind, void *sys2,
+                                float entropy_threshold) {
+    if (!dc || !sys1 || !sys1->priv || !sys2 || (sys2_kind != SP_DUAL_SQFREE && sys2_kind != SP_DUAL_HIER)) {
+        set_err("dual_init: bad args"); return -1;
+    }
+    memset(dc, 0, sizeof(*dc));
+    const sp_config_t *c2;
+    int ms2;
+    void *st2;
+    if (sys2_kind == SP_DUAL_SQFREE) {
+        const sp_hip_sqfree_cache_t *q = (const sp_hip_sqfree_cache_t *)sys2;
+        c2 = &q->config, ms2 = q->max_seq_len, st2 = q->stream;
+    } else {
+        const sp_hip_hier_cache_t *q = (const sp_hip_hier_cache_t *)sys2;
+        c2 = &q->config, ms2 = q->max_seq_len, st2 = q->stream;
+        if (q->n_slots < q->config.n_layers * q->config.n_heads_kv) { set_err("dual_init: hier slots"); return -1; }
+    }
+    const sp_config_t &c1 = sys1->config;
+    if (c1.head_dim != c2->head_dim || c1.n_layers != c2->n_layers || c1.n_heads_kv != c2->n_heads_kv ||
+        sys1->max_seq_len != ms2) {
+        set_err("dual_init: System 1 and 2 shapes differ"); return -1;
+    }
+    if (sys1->stream != st2) { set_err("dual_init: System 1 and 2 must share a stream"); return -1; }
+    DualPriv *pv = new DualPriv();
+    pv->route.assign((size_t)ms2, 0);
+    if (!(hip_ok(hipMalloc((void **)&pv->d_list, (size_t)ms2 * sizeof(int)), "dual list") &&
+          hip_ok(hipHostMalloc((void **)&pv->h_list, (size_t)ms2 * sizeof(int), hipHostMallocDefault),
+                 "dual list staging"))) {
+        if (pv->d_list) (void)hipFree(pv->d_list);
+        delete pv;
+        return -1;
+    }
+    dc->sys1 = sys1;
+    dc->sys2 = sys2;
+    dc->sys2_kind = sys2_kind;
+    dc->entropy_threshold = entropy_threshold;
+    dc->max_seq_len = ms2;
+    dc->priv = pv;
+    return 0;
+}
+
+extern "C" void sp_hip_dual_free(sp_hip_dual_cache_t *dc) {
+    if (!dc || !dc->priv) return;
+    DualPriv *pv = (DualPriv *)dc->priv;
+    (void)hipStreamSynchronize((hipStream_t)dc->sys1->stream);  // a list upload may be in flight
+    (void)hipFree(pv->d_list);
+    (void)hipHostFree(pv->h_list);
+    delete pv;
+    dc->priv = nullptr;
+}
+
+extern "C" int sp_hip_dual_route_position(sp_hip_dual_cache_t *dc, int pos, float entropy) {
+    if (!dc || !dc->priv || pos < 0 || pos >= dc->max_seq_len) return 0;
+    DualPriv *pv = (DualPriv *)dc->priv;
+    const unsigned char r = entropy >= dc->entropy_threshold ? 1 : 0;
+    if (pv->route[(size_t)pos] != r) {
+        pv->n2 += r ? 1 : -1;
+        pv->route[(size_t)pos] = r;
+        pv->dirty = true;
+    }
+    return r;
+}
+
+extern "C" int sp_hip_dual_owner_of(const sp_hip_dual_cache_t *dc, int pos) {
+    if (!dc || !dc->priv || pos < 0 || pos >= dc->max_seq_len) return 1;
+    return ((const DualPriv *)dc->priv)->route[(size_t)pos] ? 2 : 1;
+}
+
+extern "C" int sp_hip_dual_sys1_count(const sp_hip_dual_cache_t *dc) {
+    return (dc && dc->priv) ? dc->max_seq_len - ((const DualPriv *)dc->priv)->n2 : 0;
+}
+
+extern "C" int sp_hip_dual_sys2_count(const sp_hip_dual_cache_t *dc) {
+    return (dc && dc->priv) ? ((const DualPriv *)dc->priv)->n2 : 0;
+}
+
+extern "C" int sp_hip_dual_write_layer(sp_hip_dual_cache_t *dc, int layer, int start_pos, int n_tok, const void *d_k,
+                                       const void *d_v, long long row_stride, int dtype) {
+    int L, H, hd, ms;
+    if (!dual_dims(dc, &L, &H, &hd, &ms) || layer < 0 || layer >= L || start_pos < 0 || n_tok < 0 ||
+        (long long)start_pos + n_tok > ms || row_stride < (long long)H * hd || (dtype != SP_DT_F16 && dtype != SP_DT_F32)) {
+        set_err("dual write_layer: bad args"); return -1;
+    }
+    const DualPriv *pv = (const DualPriv *)dc->priv;
+    const long long esz = dtype == SP_DT_F16 ? 2 : 4;
+    // one layer-wide write per run of positions with the same owner
+    for (int t = 0; t < n_tok;) {
+        const unsigned char r = pv->route[(size_t)(start_pos + t)];
+        int e = t + 1;
+        while (e < n_tok && pv->route[(size_t)(start_pos + e)] == r) e++;
+        const long long off = (long long)t * row_stride * esz;
+        const void *k = d_k ? (const unsigned char *)d_k + off : nullptr;
+        const void *v = d_v ? (const unsigned char *)d_v + off : nullptr;
+        int rc;
+        if (!r)
+            rc = sp_hip_write_layer(dc->sys1, layer, start_pos + t, e - t, k, v, row_stride, dtype);
+        else if (dc->sys2_kind == SP_DUAL_SQFREE)
+            rc = sp_hip_sqfree_write_layer((sp_hip_sqfree_cache_t *)dc->sys2, layer, start_pos + t, e - t, k, v,
+                                           row_stride, dtype);
+        else
+            rc = sp_hip_hier_write_layer((sp_hip_hier_cache_t *)dc->sys2, layer, start_pos + t, e - t, k, v,
+                                         row_stride, dtype);
+        if (rc) return -1;
+        t = e;
+    }
+    return 0;
+}
+
+extern "C" int sp_hip_dual_read_merged(sp_hip_dual_cache_t *dc, int layer, int kv_len, void *d_k, void *d_v,
+                                       long long row_stride, int dtype) {
+    int L, H, hd, ms;
+    if (!dual_dims(dc, &L, &H, &hd, &ms) || layer < 0 || layer >= L || kv_len <= 0 || kv_len > ms ||
+        row_stride < (long long)H * hd || (dtype != SP_DT_F16 && dtype != SP_DT_F32)) {
+        set_err("dual read_merged: bad args"); return -1;
+    }
+    DualPriv *pv = (DualPriv *)dc->priv;
+    hipStream_t s = (hipStream_t)dc->sys1->stream;
+    if (sp_hip_read_layer(dc->sys1, layer, 0, kv_len, d_k, d_v, row_stride, dtype, -1)) return -1;
+    if (pv->n2 == 0) return 0;
+    if (pv->dirty) {
+        // the previous upload may still be reading the staging buffer
+        if (!hip_ok(hipStreamSynchronize(s), "dual list sync")) return -1;
+        int n = 0;
+        for (int p = 0; p < ms; p++)
+            if (pv->route[(size_t)p]) pv->h_list[n++] = p;
+        if (n && !hip_ok(hipMemcpyAsync(pv->d_list, pv->h_list, (size_t)n * sizeof(int), hipMemcpyHostToDevice, s),
+                         "dual list upload")) return -1;
+        pv->n_list = n;
+        pv->dirty = false;
+    }
+    // System 2 positions below kv_len: a prefix of the ascending list
+    const int n2 = (int)(std::lower_bound(pv->h_list, pv->h_list + pv->n_list, kv_len) - pv->h_list);
+    if (n2 == 0) return 0;
+    for (int is_v = 0; is_v < 2; is_v++) {
+        void *dst = is_v ? d_v : d_k;
+        if (!dst) continue;
+        hipError_t e;
+        if (dc->sys2_kind == SP_DUAL_SQFREE) {
+            const sp_hip_sqfree_cache_t *q = (const sp_hip_sqfree_cache_t *)dc->sys2;
+            const SqPriv *qp = (const SqPriv *)q->priv;
+            const SpSqGeo G = sq_geo(q, is_v);
+            const unsigned char *src = (is_v ? q->d_v_cache : q->d_k_cache) + (long long)layer * H * ms * G.bytes;
+            e = sp_launch_sqfree_decode(is_v ? qp->vplan : qp->kplan, G, src, (long long)ms * G.bytes, dst, dtype, hd,
+                                        row_stride, H, n2, s, pv->d_list);
+        } else {
+            const sp_hip_hier_cache_t *q = (const sp_hip_hier_cache_t *)dc->sys2;
+            const SpHierGeo G = hier_geo(q, layer * H);
+            const unsigned char *src = (is_v ? q->d_v_cache : q->d_k_cache) + (long long)layer * H * ms * G.bytes;
+            e = sp_launch_hier_decode(((const HierPriv *)q->priv)->plan, G, src, (long long)ms * G.bytes, dst, dtype,
+                                      hd, row_stride, H, n2, s, pv->d_list);
+        }
+        if (!hip_ok(e, "dual read_merged System 2")) return -1;
+    }
+    return 0;
+}

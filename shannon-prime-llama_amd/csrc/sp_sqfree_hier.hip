@@ -125,14 +125,15 @@ template <int DT>
 __global__ void __launch_bounds__(256)
 k_sqfree_decode(const SpPlan P, const SpSqGeo G, const unsigned char *__restrict__ src,
                 long long so, void *__restrict__ dst, long long dout, long long din, int n_outer,
-                int n_inner) {
+                int n_inner, const int *__restrict__ cells) {
     __shared__ float c_s[4][SP_GEN_MAX_N];
     __shared__ float sk_s[4][SP_GEN_MAX_N];
     __shared__ __attribute__((aligned(16))) unsigned char rec_s[4][SP_GEN_MAX_REC];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const long long v = (long long)blockIdx.x * 4 + w;
     const bool valid = v < (long long)n_outer * n_inner;
-    const int o = valid ? (int)(v / n_inner) : 0, i = valid ? (int)(v % n_inner) : 0;
+    const int o = valid ? (int)(v / n_inner) : 0, i0 = valid ? (int)(v % n_inner) : 0;
+    const int i = cells ? (valid ? cells[i0] : 0) : i0;  // listed positions: record and row at cells[i0]
     float *c = c_s[w], *sk = sk_s[w];
     unsigned char *rec = rec_s[w];
     const unsigned char *g = src + (long long)o * so + (long long)i * G.bytes;
@@ -224,14 +225,15 @@ template <int DT>
 __global__ void __launch_bounds__(256)
 k_hier_decode(const SpPlan P, const SpHierGeo G, const unsigned char *__restrict__ src,
               long long so, void *__restrict__ dst, long long dout, long long din, int n_outer,
-              int n_inner) {
+              int n_inner, const int *__restrict__ cells) {
     __shared__ float c_s[4][SP_GEN_MAX_N];
     __shared__ float sk_s[4][SP_GEN_MAX_N];
     __shared__ __attribute__((aligned(16))) unsigned char rec_s[4][SP_GEN_MAX_REC];
     const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const long long v = (long long)blockIdx.x * 4 + w;
     const bool valid = v < (long long)n_outer * n_inner;
-    const int o = valid ? (int)(v / n_inner) : 0, i = valid ? (int)(v % n_inner) : 0;
+    const int o = valid ? (int)(v / n_inner) : 0, i0 = valid ? (int)(v % n_inner) : 0;
+    const int i = cells ? (valid ? cells[i0] : 0) : i0;  // listed positions: record and row at cells[i0]
     float *c = c_s[w], *sk = sk_s[w];
     unsigned char *rec = rec_s[w];
     const uint16_t *Wslot = G.W + (long long)o * G.w_outer;
@@ -297,19 +299,19 @@ hipError_t sp_launch_sqfree_encode(const SpPlan &P, const SpSqGeo &G, const void
 
 hipError_t sp_launch_sqfree_decode(const SpPlan &P, const SpSqGeo &G, const unsigned char *src,
                                    long long so, void *dst, int dtype, long long dout,
-                                   long long din, int n_outer, int n_inner, hipStream_t s) {
+                                   long long din, int n_outer, int n_inner, hipStream_t s, const int *cells) {
     if (n_outer <= 0 || n_inner <= 0) return hipSuccess;
     if (!sq_fits(P, G.pad, G.bytes)) return hipErrorInvalidValue;
-    if (!getenv_lane_off_sq()) {
+    if (!cells && !getenv_lane_off_sq()) {  // listed positions: general kernels only
         const hipError_t e = sp_launch_sqfree_decode_lane(P, G, src, so, dst, dtype, dout, din, n_outer, n_inner, s);
         if (e != hipErrorNotSupported) return e;
     }
     const long long nv = (long long)n_outer * n_inner;
     const dim3 grid((unsigned)((nv + 3) / 4)), block(256);
     if (dtype == SP_DT_F16)
-        hipLaunchKernelGGL((k_sqfree_decode<SP_DT_F16>), grid, block, 0, s, P, G, src, so, dst, dout, din, n_outer, n_inner);
+        hipLaunchKernelGGL((k_sqfree_decode<SP_DT_F16>), grid, block, 0, s, P, G, src, so, dst, dout, din, n_outer, n_inner, cells);
     else
-        hipLaunchKernelGGL((k_sqfree_decode<SP_DT_F32>), grid, block, 0, s, P, G, src, so, dst, dout, din, n_outer, n_inner);
+        hipLaunchKernelGGL((k_sqfree_decode<SP_DT_F32>), grid, block, 0, s, P, G, src, so, dst, dout, din, n_outer, n_inner, cells);
     return hipGetLastError();
 }
 
@@ -333,18 +335,18 @@ hipError_t sp_launch_hier_encode(const SpPlan &P, const SpHierGeo &G, const void
 
 hipError_t sp_launch_hier_decode(const SpPlan &P, const SpHierGeo &G, const unsigned char *src,
                                  long long so, void *dst, int dtype, long long dout, long long din,
-                                 int n_outer, int n_inner, hipStream_t s) {
+                                 int n_outer, int n_inner, hipStream_t s, const int *cells) {
     if (n_outer <= 0 || n_inner <= 0) return hipSuccess;
     if (!sq_fits(P, G.pad, G.bytes)) return hipErrorInvalidValue;
-    if (!getenv_lane_off_sq()) {
+    if (!cells && !getenv_lane_off_sq()) {  // listed positions: general kernels only
         const hipError_t e = sp_launch_hier_decode_lane(P, G, src, so, dst, dtype, dout, din, n_outer, n_inner, s);
         if (e != hipErrorNotSupported) return e;
     }
     const long long nv = (long long)n_outer * n_inner;
     const dim3 grid((unsigned)((nv + 3) / 4)), block(256);
     if (dtype == SP_DT_F16)
-        hipLaunchKernelGGL((k_hier_decode<SP_DT_F16>), grid, block, 0, s, P, G, src, so, dst, dout, din, n_outer, n_inner);
+        hipLaunchKernelGGL((k_hier_decode<SP_DT_F16>), grid, block, 0, s, P, G, src, so, dst, dout, din, n_outer, n_inner, cells);
     else
-        hipLaunchKernelGGL((k_hier_decode<SP_DT_F32>), grid, block, 0, s, P, G, src, so, dst, dout, din, n_outer, n_inner);
+        hipLaunchKernelGGL((k_hier_decode<SP_DT_F32>), grid, block, 0, s, P, G, src, so, dst, dout, din, n_outer, n_inner, cells);
     return hipGetLastError();
 }

@@ -83,6 +83,14 @@ class SpHipHierCache(C.Structure):
     ]
 
 
+class SpHipDualCache(C.Structure):
+    _fields_ = [("sys1", C.c_void_p), ("sys2", C.c_void_p), ("sys2_kind", C.c_int),
+                ("entropy_threshold", C.c_float), ("max_seq_len", C.c_int), ("priv", C.c_void_p)]
+
+
+DUAL_SQFREE, DUAL_HIER = 1, 2
+
+
 class SpLlamaParams(C.Structure):
     _fields_ = [
         ("head_dim", C.c_int), ("n_layers", C.c_int), ("n_heads_kv", C.c_int),
@@ -142,6 +150,14 @@ def lib():
         L.sp_hip_read_all.argtypes = [vp, i, i, vp, vp, i, i]
         L.sp_hip_attn_decode.argtypes = [vp, i, i, vp, i, f, vp, vp, vp]
         L.sp_hip_attn_decode_bands.argtypes = [vp, i, i, vp, i, f, vp, vp, i, vp]
+        L.sp_hip_dual_init.argtypes = [vp, vp, i, vp, f]
+        L.sp_hip_dual_free.argtypes = [vp]
+        L.sp_hip_dual_route_position.argtypes = [vp, i, f]
+        L.sp_hip_dual_owner_of.argtypes = [vp, i]
+        L.sp_hip_dual_sys1_count.argtypes = [vp]
+        L.sp_hip_dual_sys2_count.argtypes = [vp]
+        L.sp_hip_dual_write_layer.argtypes = [vp, i, i, i, vp, vp, ll, i]
+        L.sp_hip_dual_read_merged.argtypes = [vp, i, i, vp, vp, ll, i]
         L.sp_hip_attn_decode_all_layers.argtypes = [vp, i, vp, i, f, vp, vp]
         L.sp_hip_attn_decode_f16.argtypes = [vp, vp, i, i, i, i, i, vp, i, f, vp, vp, vp]
         L.sp_hip_sqfree_write_batch.argtypes = [vp, i, i, i, i, i, vp, i]
@@ -288,6 +304,28 @@ class HierCache:
     def free(self):
         if self.c.priv:
             lib().sp_hip_hier_cache_free(self.ref)
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class DualCache:
+    """sp_hip_dual_cache_t over a ship cache and a sqfree or hier cache (both stay
+    owned by the caller)."""
+
+    def __init__(self, sys1, sys2, kind, threshold):
+        self.c = SpHipDualCache()
+        self.sys1, self.sys2 = sys1, sys2  # keep the caches alive
+        check(lib().sp_hip_dual_init(C.byref(self.c), sys1.ref, kind, sys2.ref, C.c_float(threshold)),
+              "sp_hip_dual_init")
+        self.ref = C.byref(self.c)
+
+    def free(self):
+        if self.c.priv:
+            lib().sp_hip_dual_free(self.ref)
 
     def __del__(self):
         try:
