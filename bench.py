@@ -226,8 +226,33 @@ def bench_variants(torch, S, L, stream, reps=3):
                        "gbs": round(nv * (2 * 2 * hd1) / t / 1e9 + H1 * n_cells * (76 + 50) / t / 1e9, 1)}
         os.environ.pop("SP_HIP_RT_KERNEL", None)
     out["cfg1_roundtrip_cells"] = dict(rt, layout="K cache rows, V transposed (v_trans), one layer x 8 heads, fp16")
+    # System 1/2 dual cache at the configs[1] layer shape (8 heads x 32768 positions, hd 128): System 1 the
+    # ship cache above, System 2 a sqfree cache (pad 154, skeleton 77, 5/4/4/4/5, 3-bit residual, spinor)
+    # owning a random 20% of the positions; one layer's merged K+V read into fp16 rows
+    bits = [5, 4, 4, 4, 5]
+    sq1 = S.SqfreeCache(S.config(hd1, 1, H1, k_bits=bits, v_bits=bits), KV1, rbits=3, spinor=True, sk_k=77,
+                        stream=stream.cuda_stream)
+    dc = S.DualCache(c1, sq1, S.DUAL_SQFREE, 1.0)
+    own2 = torch.rand(KV1, generator=g, device="cuda").cpu().numpy() < 0.2
+    for t in range(KV1):
+        L.sp_hip_dual_route_position(dc.ref, t, 2.0 if own2[t] else 0.0)
+    krow = torch.randn((KV1, H1 * hd1), generator=g, device="cuda").half()
+    vrow = torch.randn((KV1, H1 * hd1), generator=g, device="cuda").half()
+    S.check(L.sp_hip_dual_write_layer(dc.ref, 0, 0, KV1, P(krow), P(vrow), H1 * hd1, S.DTYPE_F16), "dual write")
+    ko, vo = torch.empty_like(krow), torch.empty_like(vrow)
+    t_m = timed(lambda: S.check(L.sp_hip_dual_read_merged(dc.ref, 0, KV1, P(ko), P(vo), H1 * hd1, S.DTYPE_F16),
+                                "dual read"))
+    t_1 = timed(lambda: S.check(L.sp_hip_read_layer(c1.ref, 0, 0, KV1, P(ko), P(vo), H1 * hd1, S.DTYPE_F16, -1),
+                                "ship read"))
+    n2 = int(own2.sum())
+    out["cfg1_dual_merged_read"] = {
+        "us": round(t_m * 1e6, 1), "ship_only_read_us": round(t_1 * 1e6, 1), "sys2_positions": n2,
+        "vecs_per_s": round(2 * H1 * KV1 / t_m, 1),
+        "layout": "one layer x 8 heads x 32768 positions, K+V, fp16 rows; System 2 = sqfree on 20% of positions"}
+    dc.free()
+    sq1.free()
     c1.free()
-    del kt, vt
+    del kt, vt, krow, vrow, ko, vo
     # sqfree+spinor, 12 layers x 4 KV heads x 65536 cells (4 x 16384), hd 128 -> pad 154
     L4, H4, N4 = 12, 4, 65536
     bits4 = (5, 4, 4, 4, 5)
