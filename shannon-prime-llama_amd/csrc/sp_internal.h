@@ -225,6 +225,10 @@ hipError_t sp_launch_sqfree_encode_lane(const SpPlan &P, const SpSqGeo &G, const
 hipError_t sp_launch_sqfree_decode_lane(const SpPlan &P, const SpSqGeo &G, const unsigned char *src, long long so,
                                         void *dst, int dtype, long long dout, long long din, int n_outer,
                                         int n_inner, hipStream_t s);
+// listed positions: record and row at cells[i] for i < n_inner (slack after the cache)
+hipError_t sp_launch_sqfree_decode_lane_cells(const SpPlan &P, const SpSqGeo &G, const unsigned char *src,
+                                              long long so, void *dst, int dtype, long long dout, long long din,
+                                              int n_outer, int n_inner, const int *cells, hipStream_t s);
 hipError_t sp_launch_sqfree_encode(const SpPlan &P, const SpSqGeo &G, const void *src, int dtype,
                                    long long so, long long si, unsigned char *dst, long long dout,
                                    int n_outer, int n_inner, hipStream_t s);

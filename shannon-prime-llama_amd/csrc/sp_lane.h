@@ -553,13 +553,9 @@ __device__ __forceinline__ void tile_records_out(const uint32_t (&rec)[DWR], uns
 // the tile's valid ones. The first barrier orders the previous tile's stage
 // reads before these writes.
 template <int DT, int HD, int N>
-__device__ __forceinline__ void tile_rows_out(const float (&x)[N], unsigned char *stage, void *dst, long long dout,
-                                              long long din, const TileMap &M, int t, int lane) {
-    constexpr int RB = row_bytes<DT>(HD), RP = RB + 16, CPR = RB / 16, esz = DT == SP_DT_F16 ? 2 : 4;
+__device__ __forceinline__ void rows_to_stage(const float (&x)[N], unsigned char *stage, int lane) {
+    constexpr int RB = row_bytes<DT>(HD), RP = RB + 16;
     static_assert(N >= HD, "vector must hold the row");
-    int o, i0, nvalid;
-    M.at(t, o, i0, nvalid);
-    __syncthreads();
     if (DT == SP_DT_F16) {
 #pragma unroll
         for (int c = 0; c < HD / 8; c++) {
@@ -578,6 +574,16 @@ __device__ __forceinline__ void tile_rows_out(const float (&x)[N], unsigned char
             *reinterpret_cast<float4 *>(stage + lane * RP + c * 16) =
                 make_float4(x[c * 4], x[c * 4 + 1], x[c * 4 + 2], x[c * 4 + 3]);
     }
+}
+
+template <int DT, int HD, int N>
+__device__ __forceinline__ void tile_rows_out(const float (&x)[N], unsigned char *stage, void *dst, long long dout,
+                                              long long din, const TileMap &M, int t, int lane) {
+    constexpr int RB = row_bytes<DT>(HD), RP = RB + 16, CPR = RB / 16, esz = DT == SP_DT_F16 ? 2 : 4;
+    int o, i0, nvalid;
+    M.at(t, o, i0, nvalid);
+    __syncthreads();
+    rows_to_stage<DT, HD>(x, stage, lane);
     __syncthreads();
     const int rowb = (int)(din * esz);  // launchers keep 64 rows of offsets in 32 bits
     unsigned char *gdst = reinterpret_cast<unsigned char *>(dst) + ((long long)o * dout + (long long)i0 * din) * esz;

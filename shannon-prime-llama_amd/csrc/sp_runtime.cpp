@@ -1003,8 +1003,10 @@ extern "C" int sp_hip_sqfree_cache_init_ex(sp_hip_sqfree_cache_t *cc, const sp_c
         sp_hip_sqfree_cache_free(cc);
         return -1;
     }
-    const size_t kbytes = (size_t)cc->n_slots * max_seq_len * cc->bytes_per_pos_k;
-    const size_t vbytes = (size_t)cc->n_slots * max_seq_len * cc->bytes_per_pos_v;
+    // SP_CACHE_SLACK bytes past the last record: per-lane record loaders read the
+    // dwords covering a record
+    const size_t kbytes = (size_t)cc->n_slots * max_seq_len * cc->bytes_per_pos_k + SP_CACHE_SLACK;
+    const size_t vbytes = (size_t)cc->n_slots * max_seq_len * cc->bytes_per_pos_v + SP_CACHE_SLACK;
     bool ok = upload(&cc->d_skeleton_idx, skel) && upload(&cc->d_residual_idx, res) &&
               upload(&cc->d_csr_offsets, off) && upload(&cc->d_csr_skel_slot, slot) &&
               upload(&cc->d_csr_mu_sign, mu) &&
@@ -1242,7 +1244,7 @@ extern "C" int sp_hip_hier_cache_init(sp_hip_hier_cache_t *hc, const sp_config_t
     const int res_bytes = (n_target * target_res_bits + 7) / 8;
     hc->bytes_per_pos_k = hc->bytes_per_pos_v = skel_bands->total_bytes + 4 + res_bytes;
     if (hc->bytes_per_pos_k + 8 > SP_GEN_MAX_REC) { set_err("hier_init: record too large"); sp_hip_hier_cache_free(hc); return -1; }
-    const size_t cb = (size_t)n_slots * max_seq_len * hc->bytes_per_pos_k;
+    const size_t cb = (size_t)n_slots * max_seq_len * hc->bytes_per_pos_k + SP_CACHE_SLACK;
     const size_t wb = (size_t)n_slots * n_target * n_skeleton * sizeof(uint16_t);
     std::vector<int> sk(skeleton_idx, skeleton_idx + n_skeleton), tg(target_idx, target_idx + n_target);
     bool ok = upload(&hc->d_skeleton_idx, sk) && upload(&hc->d_target_idx, tg) &&

@@ -226,6 +226,73 @@ k_sqfree_decode_lane(const unsigned char *__restrict__ src, long long so, void *
     }
 }
 
+// Listed positions (the dual cache's System 2 rows): lane j of tile t decodes the
+// record at position cells[i0 + j] of outer row o into row cells[i0 + j] of dst.
+// Each lane reads its own record as the covering dwords, funnel-shifted to the
+// record's byte offset (the cache keeps slack bytes past its last record); the
+// rows leave through the padded LDS stage, CPR lanes per row, so every row is
+// written as whole 16-byte pieces in one contiguous run.
+template <int DT, int HD, int PAD, int SK, int RBITS, bool SPIN, class SL>
+__global__ void __launch_bounds__(64)
+k_sqfree_decode_lane_cells(const unsigned char *__restrict__ src, long long so, void *__restrict__ dst,
+                           long long dout, long long din, const int *__restrict__ cells, int n_inner,
+                           int tiles_per_outer, int n_tiles, const XfConst K) {
+    using G = SqRec<PAD, SK, RBITS, SPIN, SL>;
+    constexpr int RB = row_bytes<DT>(HD), RP = RB + 16, CPR = RB / 16, NR = PAD - SK, DWR = G::dwords, B = G::total;
+    constexpr long long esz = DT == SP_DT_F16 ? 2 : 4;
+    constexpr auto &KN = kKnight<PAD, SK>;
+    __shared__ __attribute__((aligned(16))) unsigned char stage[64 * RP];
+    const int lane = threadIdx.x;
+    const TileMap M{tiles_per_outer, n_inner};
+    for (int t = blockIdx.x; t < n_tiles; t += gridDim.x) {
+        int o, i0, nvalid;
+        M.at(t, o, i0, nvalid);
+        const int pos = cells[lane < nvalid ? i0 + lane : i0];
+        const uintptr_t a = (uintptr_t)(src + (long long)o * so + (long long)pos * B);
+        const uint32_t *p = reinterpret_cast<const uint32_t *>(a & ~(uintptr_t)3);
+        const uint32_t sh = (uint32_t)(a & 3) * 8;
+        uint32_t w[DWR + 1], rec[DWR];
+#pragma unroll
+        for (int d = 0; d <= DWR; d++) w[d] = p[d];
+#pragma unroll
+        for (int d = 0; d < DWR; d++) rec[d] = __builtin_amdgcn_alignbit(w[d + 1], w[d], sh);
+        if (B % 4 != 0) rec[DWR - 1] &= (1u << (8 * (B % 4))) - 1u;
+        float sk[SK];
+        dequant_bands<SL, false, true>(rec, SL::nb, sk);
+        float c[PAD];
+#pragma unroll
+        for (int s = 0; s < SK; s++) c[KN.skel[s]] = sk[s];
+        if constexpr (NR > 0) {
+            const float mag = __uint_as_float(rec_get32(rec, G::mag_byte));
+            constexpr int L = 1 << RBITS;
+            const float center = 0.5f * (float)(L - 1);
+            const float sat = mag * (float)RBITS;
+            const float step = (L > 1) ? sp_div(2.0f * sat, (float)(L - 1)) : 0.0f;
+#pragma unroll
+            for (int r = 0; r < NR; r++) {
+                float pr = csr_predict<PAD, SK>(sk, r);
+                if (SPIN && rec_extract(rec, G::sheet_bit + r, 1)) pr = -pr;
+                const float d = ((float)rec_extract(rec, G::res_bit + r * RBITS, RBITS) - center) * step;
+                c[KN.res[r]] = pr + d;
+            }
+        }
+        vil_stages<PAD, 0, 1>(c, K);
+        __syncthreads();  // the previous tile's stage reads are done
+        rows_to_stage<DT, HD>(c, stage, lane);
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < CPR; q++) {
+            const int idx = q * 64 + lane, r = idx / CPR, piece = idx - r * CPR;
+            const int prow = __shfl(pos, r, 64);
+            if (r < nvalid) {
+                const u32x4 v = *reinterpret_cast<const u32x4 *>(stage + r * RP + piece * 16);
+                *reinterpret_cast<u32x4 *>(reinterpret_cast<unsigned char *>(dst) +
+                                           ((long long)o * dout + (long long)prow * din) * esz + piece * 16) = v;
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // dispatch
 // ---------------------------------------------------------------------------
@@ -266,7 +333,38 @@ hipError_t sq_dec_launch(const SpPlan &P, const unsigned char *src, long long so
     return hipGetLastError();
 }
 
+template <int DT, int SK, class SL>
+hipError_t sq_dec_cells_launch(const SpPlan &P, const unsigned char *src, long long so, void *dst, long long dout,
+                               long long din, const int *cells, int n_outer, int n_inner, hipStream_t s) {
+    const int tpo = (n_inner + 63) / 64;
+    const long long n_tiles = (long long)n_outer * tpo;
+    if (n_tiles > 0x7fffffffLL || din < 128) return hipErrorNotSupported;
+    const dim3 grid((unsigned)std::min<long long>(n_tiles, persistent_blocks())), block(64);
+    hipLaunchKernelGGL((k_sqfree_decode_lane_cells<DT, 128, 154, SK, 3, true, SL>), grid, block, 0, s, src, so, dst,
+                       dout, din, cells, n_inner, tpo, (int)n_tiles, xf_const(P));
+    return hipGetLastError();
+}
+
 }  // namespace
+
+// Listed positions (see k_sqfree_decode_lane_cells); hipErrorNotSupported
+// (nothing launched) when the geometry or the row alignment has no lane
+// specialization. The cache must carry slack bytes past its last record.
+hipError_t sp_launch_sqfree_decode_lane_cells(const SpPlan &P, const SpSqGeo &G, const unsigned char *src,
+                                              long long so, void *dst, int dtype, long long dout, long long din,
+                                              int n_outer, int n_inner, const int *cells, hipStream_t s) {
+    const int esz = dtype == SP_DT_F16 ? 2 : 4;
+    if (((uintptr_t)dst % 16) || ((dout * esz) % 16) || ((din * esz) % 16)) return hipErrorNotSupported;
+    if (sq_geometry_matches<77, SkelL77>(P, G))
+        return dtype == SP_DT_F16
+                   ? sq_dec_cells_launch<SP_DT_F16, 77, SkelL77>(P, src, so, dst, dout, din, cells, n_outer, n_inner, s)
+                   : sq_dec_cells_launch<SP_DT_F32, 77, SkelL77>(P, src, so, dst, dout, din, cells, n_outer, n_inner, s);
+    if (sq_geometry_matches<115, SkelL115>(P, G))
+        return dtype == SP_DT_F16
+                   ? sq_dec_cells_launch<SP_DT_F16, 115, SkelL115>(P, src, so, dst, dout, din, cells, n_outer, n_inner, s)
+                   : sq_dec_cells_launch<SP_DT_F32, 115, SkelL115>(P, src, so, dst, dout, din, cells, n_outer, n_inner, s);
+    return hipErrorNotSupported;
+}
 
 // Returns hipErrorNotSupported (nothing launched) when the geometry or the
 // operand alignment has no lane specialization: the caller then uses the
