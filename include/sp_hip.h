@@ -388,6 +388,32 @@ int  sp_hip_dual_read_merged(sp_hip_dual_cache_t *dc, int layer, int kv_len, voi
                              long long row_stride, int dtype);
 
 /* ======================================================================== */
+/* Disk serialisation, format v3 (KvCache::save_to_disk / load_from_disk,   */
+/* kv_cache.h:132-146, kv_cache.cpp:1533-1585; band-major partial load of   */
+/* the disk-tier notes, CHANGELOG.md)                                       */
+/* ======================================================================== */
+/* One file per layer, {prefix}.L{layer}.bin: a 64-byte header ("VHT2", version 3,
+ * model hash, n_pos, layer, n_heads, head_dim, cache kind, record bytes and
+ * segment counts of K and V, a check of the K coefficient order, FNV-1a of the
+ * first 56 bytes), then K and V band-major: for each band (sqfree/hier: each
+ * skeleton band, then the residual tail) the bytes of every head's positions
+ * [0, n_pos). Saves return 0, loads the n_pos stored (-1 on any error). A model
+ * hash mismatch fails the load unless SP_DISK_HASH_STRICT=0, which only warns
+ * (the reference's strict hash guard and its opt-out). */
+uint64_t sp_fnv1a64(const void *data, size_t n);   /* the model_hash of a path string */
+int sp_hip_cache_save(const sp_hip_cache_t *cc, const char *prefix, int n_pos, uint64_t model_hash);
+int sp_hip_cache_load(sp_hip_cache_t *cc, const char *prefix, uint64_t expected_hash);
+/* sp_shadow_cache_load_partial / KvCache::load_from_disk_partial: reads only the
+ * first max_bands bands of K and of V from each file and clears the others'
+ * bytes, so they decode as 0 (max_bands >= 0). */
+int sp_hip_cache_load_partial(sp_hip_cache_t *cc, const char *prefix, uint64_t expected_hash, int max_bands);
+int sp_hip_sqfree_cache_save(const sp_hip_sqfree_cache_t *cc, const char *prefix, int n_pos, uint64_t model_hash);
+int sp_hip_sqfree_cache_load(sp_hip_sqfree_cache_t *cc, const char *prefix, uint64_t expected_hash);
+/* The hier cache also writes and reads {prefix}.hier_w.bin (every slot's fp16 W). */
+int sp_hip_hier_cache_save(const sp_hip_hier_cache_t *hc, const char *prefix, int n_pos, uint64_t model_hash);
+int sp_hip_hier_cache_load(sp_hip_hier_cache_t *hc, const char *prefix, uint64_t expected_hash);
+
+/* ======================================================================== */
 /* Runtime                                                                  */
 /* ======================================================================== */
 

@@ -245,6 +245,19 @@ hipError_t sp_launch_hier_decode(const SpPlan &P, const SpHierGeo &G, const unsi
                                  long long so, void *dst, int dtype, long long dout, long long din,
                                  int n_outer, int n_inner, hipStream_t s, const int *cells = nullptr);
 
+// Disk layout v3 (sp_disk.hip): a record's segments (bands, then any residual
+// tail); segment s of record (slot, pos) lives at base[s] + (slot*n_pos + pos)*len[s]
+struct SpDiskSegs {
+    int n;
+    short off[SP_MAX_BANDS_DEV + 1];
+    short len[SP_MAX_BANDS_DEV + 1];
+    long long base[SP_MAX_BANDS_DEV + 1];
+};
+hipError_t sp_launch_disk_pack(const unsigned char *rec, long long slot_stride, int B, int n_slots, int n_pos,
+                               const SpDiskSegs &S, unsigned char *out, hipStream_t s);
+hipError_t sp_launch_disk_unpack(const unsigned char *in, long long slot_stride, int B, int n_slots, int n_pos,
+                                 const SpDiskSegs &S, int n_load, unsigned char *rec, hipStream_t s);
+
 // Fused decode attention (sp_attn.hip).
 #define SP_CACHE_SLACK 256  // bytes allocated past the last record of a packed ship cache
 

@@ -6,6 +6,8 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+
+#include <string>
 #include <stdlib.h>
 #include <string.h>
 
@@ -1944,4 +1946,309 @@ extern "C" int sp_hip_dual_read_merged(sp_hip_dual_cache_t *dc, int layer, int k
         if (!hip_ok(e, "dual read_merged System 2")) return -1;
     }
     return 0;
+}
+
+// ===========================================================================
+// disk serialisation, format v3 (KvCache::save_to_disk / load_from_disk,
+// kv_cache.h:132-146, kv_cache.cpp:1533-1585; band-major layout and partial
+// load: the disk-tier notes of CHANGELOG.md)
+// ===========================================================================
+// One file per layer, {prefix}.L{layer}.bin: a 64-byte header, then the K
+// segments and the V segments, each [n_heads][n_pos][segment bytes] (sp_disk.hip).
+
+extern "C" uint64_t sp_fnv1a64(const void *data, size_t n) {
+    const unsigned char *p = (const unsigned char *)data;
+    uint64_t h = 0xcbf29ce484222325ULL;  // FNV-1a 64: offset basis, prime 2^40 + 2^8 + 0xb3
+    for (size_t i = 0; i < n; i++) {
+        h ^= p[i];
+        h *= 0x100000001b3ULL;
+    }
+    return h;
+}
+
+namespace {
+
+constexpr uint32_t SP_DISK_VERSION = 3;
+enum { DISK_SHIP = 0, DISK_SQFREE = 1, DISK_HIER = 2, DISK_HIER_W = 3 };
+
+struct DiskHeader {  // 64 bytes, little-endian
+    char magic[4];        // "VHT2"
+    uint32_t version;     // 3
+    uint64_t model_hash;  // FNV-1a of the model path (the caller's)
+    int32_t n_pos, layer, n_heads, head_dim, kind, k_bytes, v_bytes, k_segs, v_segs;
+    uint32_t order_check; // low 32 bits of FNV-1a of the K coefficient order (ship), else 0
+    uint64_t check;       // FNV-1a of bytes [0, 56)
+};
+static_assert(sizeof(DiskHeader) == 64, "the disk header is 64 bytes");
+
+// A record's segments: each band's [fp16 scale][codes], then the bytes after the
+// last band (sqfree/hier: magnitude, residual codes, spinor sheet) as one more.
+SpDiskSegs disk_segs(const sp_band_config_t *bc, int B, long long n_rec) {
+    SpDiskSegs S{};
+    int byte = 0, n = 0;
+    for (int b = 0; b < bc->n_bands; b++) {
+        int off, sz;
+        sp_band_span(bc, b, &off, &sz);
+        S.off[n] = (short)byte;
+        S.len[n] = (short)(2 + (sz * bc->band_bits[b] + 7) / 8);
+        byte += S.len[n++];
+    }
+    if (byte < B) {
+        S.off[n] = (short)byte;
+        S.len[n++] = (short)(B - byte);
+    }
+    S.n = n;
+    long long base = 0;
+    for (int s = 0; s < n; s++) {
+        S.base[s] = base;
+        base += n_rec * S.len[s];
+    }
+    return S;
+}
+
+long long segs_bytes(const SpDiskSegs &S, int n_seg, long long n_rec) {
+    long long b = 0;
+    for (int s = 0; s < n_seg && s < S.n; s++) b += n_rec * S.len[s];
+    return b;
+}
+
+struct DiskCache {  // what save/load need of any of the three cache kinds
+    int kind, n_layers, H, hd, max_seq, kB, vB;
+    unsigned char *kc, *vc;
+    const sp_band_config_t *kbc, *vbc;
+    uint32_t order_check;
+    hipStream_t s;
+};
+
+std::string layer_path(const char *prefix, int l) { return std::string(prefix) + ".L" + std::to_string(l) + ".bin"; }
+
+void header_seal(DiskHeader &h) { h.check = sp_fnv1a64(&h, 56); }
+
+bool hash_ok(uint64_t got, uint64_t want, const char *what) {
+    if (got == want) return true;
+    const char *e = getenv("SP_DISK_HASH_STRICT");
+    if (e && e[0] == '0') {
+        fprintf(stderr, "[sp-hip] %s: model hash mismatch (file %016llx, expected %016llx); loading anyway "
+                        "(SP_DISK_HASH_STRICT=0)\n", what, (unsigned long long)got, (unsigned long long)want);
+        return true;
+    }
+    set_err("%s: model hash mismatch (file %016llx, expected %016llx)", what, (unsigned long long)got,
+            (unsigned long long)want);
+    return false;
+}
+
+int disk_save(const DiskCache &D, const char *prefix, int n_pos, uint64_t model_hash) {
+    if (!prefix || n_pos <= 0 || n_pos > D.max_seq) { set_err("save: bad n_pos %d", n_pos); return -1; }
+    const long long n_rec = (long long)D.H * n_pos;
+    const SpDiskSegs Sk = disk_segs(D.kbc, D.kB, n_rec), Sv = disk_segs(D.vbc, D.vB, n_rec);
+    const size_t kbytes = (size_t)n_rec * D.kB, body = kbytes + (size_t)n_rec * D.vB;
+    unsigned char *d_stage = nullptr, *h_stage = nullptr;
+    if (!(hip_ok(hipMalloc((void **)&d_stage, body), "save staging") &&
+          hip_ok(hipHostMalloc((void **)&h_stage, body, hipHostMallocDefault), "save host staging"))) {
+        if (d_stage) (void)hipFree(d_stage);
+        return -1;
+    }
+    int rc = 0;
+    for (int l = 0; l < D.n_layers && rc == 0; l++) {
+        const long long ks = (long long)D.max_seq * D.kB, vs = (long long)D.max_seq * D.vB;
+        if (!(hip_ok(sp_launch_disk_pack(D.kc + (long long)l * D.H * ks, ks, D.kB, D.H, n_pos, Sk, d_stage, D.s),
+                     "save pack K") &&
+              hip_ok(sp_launch_disk_pack(D.vc + (long long)l * D.H * vs, vs, D.vB, D.H, n_pos, Sv, d_stage + kbytes, D.s),
+                     "save pack V") &&
+              hip_ok(hipMemcpyAsync(h_stage, d_stage, body, hipMemcpyDeviceToHost, D.s), "save D2H") &&
+              hip_ok(hipStreamSynchronize(D.s), "save sync"))) { rc = -1; break; }
+        DiskHeader h{};
+        memcpy(h.magic, "VHT2", 4);
+        h.version = SP_DISK_VERSION;
+        h.model_hash = model_hash;
+        h.n_pos = n_pos, h.layer = l, h.n_heads = D.H, h.head_dim = D.hd, h.kind = D.kind;
+        h.k_bytes = D.kB, h.v_bytes = D.vB, h.k_segs = Sk.n, h.v_segs = Sv.n, h.order_check = D.order_check;
+        header_seal(h);
+        const std::string path = layer_path(prefix, l);
+        FILE *f = fopen(path.c_str(), "wb");
+        if (!f) { set_err("save: cannot open %s", path.c_str()); rc = -1; break; }
+        const bool ok = fwrite(&h, sizeof(h), 1, f) == 1 && fwrite(h_stage, 1, body, f) == body;
+        if (fclose(f) != 0 || !ok) { set_err("save: write failed for %s", path.c_str()); rc = -1; }
+    }
+    (void)hipFree(d_stage);
+    (void)hipHostFree(h_stage);
+    return rc;
+}
+
+// Loads positions [0, n_pos) of every layer; segments past max_segs (< 0: all)
+// are cleared instead of read. Returns n_pos.
+int disk_load(const DiskCache &D, const char *prefix, uint64_t expected_hash, int max_segs) {
+    if (!prefix) { set_err("load: no prefix"); return -1; }
+    unsigned char *d_stage = nullptr, *h_stage = nullptr;
+    size_t cap = 0;
+    int n_pos_all = -1, rc = 0;
+    for (int l = 0; l < D.n_layers && rc == 0; l++) {
+        const std::string path = layer_path(prefix, l);
+        FILE *f = fopen(path.c_str(), "rb");
+        if (!f) { set_err("load: cannot open %s", path.c_str()); rc = -1; break; }
+        DiskHeader h{};
+        bool ok = fread(&h, sizeof(h), 1, f) == 1;
+        if (!ok || memcmp(h.magic, "VHT2", 4) != 0 || h.check != sp_fnv1a64(&h, 56)) {
+            set_err("load: %s is not a VHT2 cache file", path.c_str());
+            ok = false;
+        } else if (h.version != SP_DISK_VERSION) {
+            set_err("load: %s has format version %u (this build reads %u)", path.c_str(), h.version, SP_DISK_VERSION);
+            ok = false;
+        } else if (h.kind != D.kind || h.layer != l || h.n_heads != D.H || h.head_dim != D.hd || h.k_bytes != D.kB ||
+                   h.v_bytes != D.vB || h.n_pos <= 0 || h.n_pos > D.max_seq || (n_pos_all >= 0 && h.n_pos != n_pos_all)) {
+            set_err("load: %s does not match this cache's shape", path.c_str());
+            ok = false;
+        } else if (h.order_check != D.order_check) {
+            set_err("load: %s was written with another coefficient order", path.c_str());
+            ok = false;
+        } else {
+            ok = hash_ok(h.model_hash, expected_hash, "load");
+        }
+        const long long n_rec = ok ? (long long)D.H * h.n_pos : 0;
+        const SpDiskSegs Sk = disk_segs(D.kbc, D.kB, n_rec), Sv = disk_segs(D.vbc, D.vB, n_rec);
+        if (ok && (Sk.n != h.k_segs || Sv.n != h.v_segs)) { set_err("load: %s band layout differs", path.c_str()); ok = false; }
+        if (!ok) { fclose(f); rc = -1; break; }
+        n_pos_all = h.n_pos;
+        const int nk = max_segs < 0 ? Sk.n : std::min(max_segs, Sk.n), nv = max_segs < 0 ? Sv.n : std::min(max_segs, Sv.n);
+        const size_t kfull = (size_t)n_rec * D.kB, body = kfull + (size_t)n_rec * D.vB;
+        const size_t kread = (size_t)segs_bytes(Sk, nk, n_rec), vread = (size_t)segs_bytes(Sv, nv, n_rec);
+        if (body > cap) {
+            if (d_stage) (void)hipFree(d_stage);
+            if (h_stage) (void)hipHostFree(h_stage);
+            d_stage = nullptr, h_stage = nullptr, cap = 0;
+            if (!(hip_ok(hipMalloc((void **)&d_stage, body), "load staging") &&
+                  hip_ok(hipHostMalloc((void **)&h_stage, body, hipHostMallocDefault), "load host staging"))) {
+                fclose(f); rc = -1; break;
+            }
+            cap = body;
+        }
+        // the K segments to load, skip the rest of K, the V segments to load
+        ok = fread(h_stage, 1, kread, f) == kread && fseek(f, (long)(kfull - kread), SEEK_CUR) == 0 &&
+             fread(h_stage + kfull, 1, vread, f) == vread;
+        fclose(f);
+        if (!ok) { set_err("load: %s is truncated", path.c_str()); rc = -1; break; }
+        const long long ks = (long long)D.max_seq * D.kB, vs = (long long)D.max_seq * D.vB;
+        if (!(hip_ok(hipMemcpyAsync(d_stage, h_stage, body, hipMemcpyHostToDevice, D.s), "load H2D") &&
+              hip_ok(sp_launch_disk_unpack(d_stage, ks, D.kB, D.H, h.n_pos, Sk, nk, D.kc + (long long)l * D.H * ks, D.s),
+                     "load unpack K") &&
+              hip_ok(sp_launch_disk_unpack(d_stage + kfull, vs, D.vB, D.H, h.n_pos, Sv, nv,
+                                           D.vc + (long long)l * D.H * vs, D.s), "load unpack V") &&
+              hip_ok(hipStreamSynchronize(D.s), "load sync"))) { rc = -1; break; }
+    }
+    if (d_stage) (void)hipFree(d_stage);
+    if (h_stage) (void)hipHostFree(h_stage);
+    return rc == 0 ? n_pos_all : -1;
+}
+
+bool ship_disk(const sp_hip_cache_t *cc, DiskCache &D) {
+    if (!cc || !cc->priv) { set_err("disk: bad cache"); return false; }
+    D.kind = DISK_SHIP, D.n_layers = cc->config.n_layers, D.H = cc->config.n_heads_kv, D.hd = cc->config.head_dim;
+    D.max_seq = cc->max_seq_len, D.kB = cc->k_bands.total_bytes, D.vB = cc->v_bands.total_bytes;
+    D.kc = (unsigned char *)cc->d_k_cache, D.vc = (unsigned char *)cc->d_v_cache;
+    D.kbc = &cc->k_bands, D.vbc = &cc->v_bands, D.s = (hipStream_t)cc->stream;
+    D.order_check = 0;
+    if (cc->d_mobius_order) {
+        std::vector<int> ord((size_t)D.hd);
+        if (!hip_ok(hipMemcpy(ord.data(), cc->d_mobius_order, ord.size() * sizeof(int), hipMemcpyDeviceToHost),
+                    "disk order")) return false;
+        D.order_check = (uint32_t)sp_fnv1a64(ord.data(), ord.size() * sizeof(int));
+    }
+    return true;
+}
+
+bool sqfree_disk(const sp_hip_sqfree_cache_t *cc, DiskCache &D) {
+    if (!cc || !cc->priv) { set_err("disk: bad sqfree cache"); return false; }
+    const int H = cc->config.n_heads_kv;
+    if (cc->n_slots < cc->config.n_layers * H) { set_err("disk: sqfree slots"); return false; }
+    D.kind = DISK_SQFREE, D.n_layers = cc->config.n_layers, D.H = H, D.hd = cc->config.head_dim;
+    D.max_seq = cc->max_seq_len, D.kB = cc->bytes_per_pos_k, D.vB = cc->bytes_per_pos_v;
+    D.kc = cc->d_k_cache, D.vc = cc->d_v_cache, D.kbc = &cc->k_bands, D.vbc = &cc->v_bands;
+    D.s = (hipStream_t)cc->stream, D.order_check = 0;
+    return true;
+}
+
+bool hier_disk(const sp_hip_hier_cache_t *hc, DiskCache &D) {
+    if (!hc || !hc->priv) { set_err("disk: bad hier cache"); return false; }
+    const int H = hc->config.n_heads_kv;
+    if (hc->n_slots < hc->config.n_layers * H) { set_err("disk: hier slots"); return false; }
+    D.kind = DISK_HIER, D.n_layers = hc->config.n_layers, D.H = H, D.hd = hc->config.head_dim;
+    D.max_seq = hc->max_seq_len, D.kB = hc->bytes_per_pos_k, D.vB = hc->bytes_per_pos_v;
+    D.kc = hc->d_k_cache, D.vc = hc->d_v_cache, D.kbc = &hc->skel_bands, D.vbc = &hc->skel_bands;
+    D.s = (hipStream_t)hc->stream, D.order_check = 0;
+    return true;
+}
+
+}  // namespace
+
+extern "C" int sp_hip_cache_save(const sp_hip_cache_t *cc, const char *prefix, int n_pos, uint64_t model_hash) {
+    DiskCache D;
+    return ship_disk(cc, D) ? disk_save(D, prefix, n_pos, model_hash) : -1;
+}
+
+extern "C" int sp_hip_cache_load(sp_hip_cache_t *cc, const char *prefix, uint64_t expected_hash) {
+    DiskCache D;
+    return ship_disk(cc, D) ? disk_load(D, prefix, expected_hash, -1) : -1;
+}
+
+extern "C" int sp_hip_cache_load_partial(sp_hip_cache_t *cc, const char *prefix, uint64_t expected_hash,
+                                         int max_bands) {
+    DiskCache D;
+    if (max_bands < 0) { set_err("load_partial: max_bands < 0"); return -1; }
+    return ship_disk(cc, D) ? disk_load(D, prefix, expected_hash, max_bands) : -1;
+}
+
+extern "C" int sp_hip_sqfree_cache_save(const sp_hip_sqfree_cache_t *cc, const char *prefix, int n_pos,
+                                        uint64_t model_hash) {
+    DiskCache D;
+    return sqfree_disk(cc, D) ? disk_save(D, prefix, n_pos, model_hash) : -1;
+}
+
+extern "C" int sp_hip_sqfree_cache_load(sp_hip_sqfree_cache_t *cc, const char *prefix, uint64_t expected_hash) {
+    DiskCache D;
+    return sqfree_disk(cc, D) ? disk_load(D, prefix, expected_hash, -1) : -1;
+}
+
+// The hier cache also writes {prefix}.hier_w.bin: a header (kind 3, n_heads =
+// n_slots, head_dim = n_target, k_bytes = n_skeleton) and every slot's fp16 W.
+extern "C" int sp_hip_hier_cache_save(const sp_hip_hier_cache_t *hc, const char *prefix, int n_pos,
+                                      uint64_t model_hash) {
+    DiskCache D;
+    if (!hier_disk(hc, D) || disk_save(D, prefix, n_pos, model_hash)) return -1;
+    const size_t nw = (size_t)hc->n_slots * hc->n_target * hc->n_skeleton;
+    std::vector<uint16_t> W(nw);
+    if (!hip_ok(hipMemcpy(W.data(), hc->d_W, nw * sizeof(uint16_t), hipMemcpyDeviceToHost), "save W")) return -1;
+    DiskHeader h{};
+    memcpy(h.magic, "VHT2", 4);
+    h.version = SP_DISK_VERSION;
+    h.model_hash = model_hash;
+    h.n_heads = hc->n_slots, h.head_dim = hc->n_target, h.k_bytes = hc->n_skeleton, h.kind = DISK_HIER_W;
+    header_seal(h);
+    const std::string path = std::string(prefix) + ".hier_w.bin";
+    FILE *f = fopen(path.c_str(), "wb");
+    if (!f) { set_err("save: cannot open %s", path.c_str()); return -1; }
+    const bool ok = fwrite(&h, sizeof(h), 1, f) == 1 && fwrite(W.data(), sizeof(uint16_t), nw, f) == nw;
+    if (fclose(f) != 0 || !ok) { set_err("save: write failed for %s", path.c_str()); return -1; }
+    return 0;
+}
+
+extern "C" int sp_hip_hier_cache_load(sp_hip_hier_cache_t *hc, const char *prefix, uint64_t expected_hash) {
+    DiskCache D;
+    if (!hier_disk(hc, D) || !prefix) { if (!prefix) set_err("load: no prefix"); return -1; }
+    const std::string path = std::string(prefix) + ".hier_w.bin";
+    FILE *f = fopen(path.c_str(), "rb");
+    if (!f) { set_err("load: cannot open %s", path.c_str()); return -1; }
+    DiskHeader h{};
+    const size_t nw = (size_t)hc->n_slots * hc->n_target * hc->n_skeleton;
+    std::vector<uint16_t> W(nw);
+    bool ok = fread(&h, sizeof(h), 1, f) == 1 && memcmp(h.magic, "VHT2", 4) == 0 && h.check == sp_fnv1a64(&h, 56) &&
+              h.version == SP_DISK_VERSION && h.kind == DISK_HIER_W && h.n_heads == hc->n_slots &&
+              h.head_dim == hc->n_target && h.k_bytes == hc->n_skeleton;
+    if (!ok) set_err("load: %s does not match this hier cache", path.c_str());
+    ok = ok && hash_ok(h.model_hash, expected_hash, "load");
+    if (ok && fread(W.data(), sizeof(uint16_t), nw, f) != nw) { set_err("load: %s is truncated", path.c_str()); ok = false; }
+    fclose(f);
+    if (!ok) return -1;
+    const int n = disk_load(D, prefix, expected_hash, -1);
+    if (n < 0) return -1;
+    return sp_hip_hier_cache_upload_W(hc, W.data()) == 0 ? n : -1;
 }

@@ -150,6 +150,14 @@ def lib():
         L.sp_hip_read_all.argtypes = [vp, i, i, vp, vp, i, i]
         L.sp_hip_attn_decode.argtypes = [vp, i, i, vp, i, f, vp, vp, vp]
         L.sp_hip_attn_decode_bands.argtypes = [vp, i, i, vp, i, f, vp, vp, i, vp]
+        u64, cp = C.c_uint64, C.c_char_p
+        L.sp_fnv1a64.argtypes = [vp, C.c_size_t]
+        L.sp_fnv1a64.restype = u64
+        for name in ("sp_hip_cache_save", "sp_hip_sqfree_cache_save", "sp_hip_hier_cache_save"):
+            getattr(L, name).argtypes = [vp, cp, i, u64]
+        for name in ("sp_hip_cache_load", "sp_hip_sqfree_cache_load", "sp_hip_hier_cache_load"):
+            getattr(L, name).argtypes = [vp, cp, u64]
+        L.sp_hip_cache_load_partial.argtypes = [vp, cp, u64, i]
         L.sp_hip_dual_init.argtypes = [vp, vp, i, vp, f]
         L.sp_hip_dual_free.argtypes = [vp]
         L.sp_hip_dual_route_position.argtypes = [vp, i, f]

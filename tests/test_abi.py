@@ -113,3 +113,11 @@ def test_init_fails_loudly_without_gpu():
     assert "gfx950" in S.last_error() or S.last_error()
     sc = S.SpShadowCache()
     assert S.lib().sp_shadow_cache_init(C.byref(sc), C.byref(cfg)) == -1
+
+
+def test_fnv1a64_known_answers():
+    """sp_fnv1a64 (the disk files' model hash and header check) against the published
+    FNV-1a 64-bit test vectors (offset basis 0xcbf29ce484222325, prime 0x100000001b3)."""
+    L = S.lib()
+    for msg, want in ((b"", 0xcbf29ce484222325), (b"a", 0xaf63dc4c8601ec8c), (b"foobar", 0x85944171f73967e8)):
+        assert L.sp_fnv1a64(msg, len(msg)) == want, msg
