@@ -251,6 +251,32 @@ def bench_variants(torch, S, L, stream, reps=3):
         "layout": "one layer x 8 heads x 32768 positions, K+V, fp16 rows; System 2 = sqfree on 20% of positions"}
     dc.free()
     sq1.free()
+    # disk format v3 at the configs[1] layer shape: 4 layers x 8 heads x 32768 positions (33 MB of records
+    # per layer file), save, load, and a partial load of K band 0 (+ the one V band), files under /tmp
+    import tempfile
+    cd = S.ShipCache(S.config(hd1, 4, H1), KV1, stream.cuda_stream)
+    xs = torch.randn((4 * H1 * KV1, hd1), generator=g, device="cuda").half()
+    S.check(L.sp_hip_write_all(cd.ref, 0, KV1, P(xs), P(xs), S.DTYPE_F16), "disk fill")
+    del xs
+    torch.cuda.synchronize()
+    with tempfile.TemporaryDirectory(dir="/tmp") as td:
+        prefix = os.path.join(td, "ctx").encode()
+        file_bytes = 4 * H1 * KV1 * (76 + 50)
+        t0 = time.perf_counter()
+        S.check(L.sp_hip_cache_save(cd.ref, prefix, KV1, 1), "save")
+        t_save = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        n_l = L.sp_hip_cache_load(cd.ref, prefix, 1)
+        t_load = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        n_p = L.sp_hip_cache_load_partial(cd.ref, prefix, 1, 1)
+        t_part = time.perf_counter() - t0
+    assert n_l == KV1 and n_p == KV1
+    out["cfg1_disk_v3"] = {"save_ms": round(t_save * 1e3, 1), "load_ms": round(t_load * 1e3, 1),
+                           "load_partial_1band_ms": round(t_part * 1e3, 1), "file_mb": round(file_bytes / 1e6, 1),
+                           "partial_read_mb": round(4 * H1 * KV1 * (22 + 50) / 1e6, 1),
+                           "layout": "4 layers x 8 heads x 32768 positions, K 76 B + V 50 B records, files in /tmp"}
+    cd.free()
     c1.free()
     del kt, vt, krow, vrow, ko, vo
     # sqfree+spinor, 12 layers x 4 KV heads x 65536 cells (4 x 16384), hd 128 -> pad 154
