@@ -225,11 +225,14 @@ k_hier_encode_lane(const void *__restrict__ src, long long so, long long si, uns
     }
 }
 
-template <int DT, int PAD, int NS, int RBITS, class SL>
+// LISTED: lane j of tile t decodes the record at position cells[i0 + j] into row
+// cells[i0 + j] (the dual cache's System 2 rows): its own record read directly,
+// rows out through rows_out_listed.
+template <int DT, int PAD, int NS, int RBITS, class SL, bool LISTED>
 __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1)))
 k_hier_decode_lane(const unsigned char *__restrict__ src, long long so, void *__restrict__ dst, long long dout,
                    long long din, int n_inner, int tiles_per_outer, int n_tiles, const XfConst K,
-                   const uint16_t *__restrict__ W, long long w_outer) {
+                   const uint16_t *__restrict__ W, long long w_outer, const int *__restrict__ cells) {
     constexpr int HD = HIER_HD, NT = PAD - NS;
     using G = HierRec<NT, RBITS, SL>;
     constexpr int RP = row_bytes<DT>(HD) + 16, DWR = G::dwords;
@@ -242,13 +245,21 @@ k_hier_decode_lane(const unsigned char *__restrict__ src, long long so, void *__
     RecTile<G> R;
     int t = blockIdx.x;
     if (t >= n_tiles) return;
-    rec_tile_load<G>(R, src, so, M, t, n_tiles, lane);
+    if constexpr (!LISTED) rec_tile_load<G>(R, src, so, M, t, n_tiles, lane);
     for (; t < n_tiles; t += Gs) {
-        rec_tile_stage<G>(R, stage, M, t, lane);
-        __syncthreads();
-        rec_tile_load<G>(R, src, so, M, t + Gs, n_tiles, lane);
         uint32_t rec[DWR];
-        rec_from_lds<G>(rec, stage, lane);
+        int pos = 0;
+        if constexpr (LISTED) {
+            int o_, i0_, nv_;
+            M.at(t, o_, i0_, nv_);
+            pos = cells[lane < nv_ ? i0_ + lane : i0_];
+            rec_load_direct<G>(rec, src + (long long)o_ * so + (long long)pos * G::total);
+        } else {
+            rec_tile_stage<G>(R, stage, M, t, lane);
+            __syncthreads();
+            rec_tile_load<G>(R, src, so, M, t + Gs, n_tiles, lane);
+            rec_from_lds<G>(rec, stage, lane);
+        }
         float sk[NS];
         dequant_bands<SL, false, true>(rec, SL::nb, sk);
         float c[PAD];
@@ -270,7 +281,10 @@ k_hier_decode_lane(const unsigned char *__restrict__ src, long long so, void *__
             c[HG.tgt[r + 1]] = p1 + ((float)rec_extract(rec, G::res_bit + (r + 1) * RBITS, RBITS) - center) * step;
         }
         vil_stages<PAD, 0, 1>(c, K);
-        tile_rows_out<DT, HD>(c, stage, dst, dout, din, M, t, lane);
+        if constexpr (LISTED)
+            rows_out_listed<DT, HD>(c, stage, dst, dout, din, o, pos, nv, lane);
+        else
+            tile_rows_out<DT, HD>(c, stage, dst, dout, din, M, t, lane);
     }
 }
 
@@ -302,15 +316,19 @@ hipError_t hier_enc_launch(const SpPlan &P, const SpHierGeo &G, const void *src,
 
 template <int DT>
 hipError_t hier_dec_launch(const SpPlan &P, const SpHierGeo &G, const unsigned char *src, long long so, void *dst,
-                           long long dout, long long din, int n_outer, int n_inner, hipStream_t s) {
+                           long long dout, long long din, int n_outer, int n_inner, hipStream_t s, const int *cells) {
     const int tpo = (n_inner + 63) / 64;
     const long long n_tiles = (long long)n_outer * tpo;
     constexpr long long esz = DT == SP_DT_F16 ? 2 : 4;
     if (n_tiles > 0x7fffffffLL || din < HIER_HD || 64 * din * esz + HIER_HD * esz > 0x7fffffffLL)
         return hipErrorNotSupported;
     const dim3 grid((unsigned)std::min<long long>(n_tiles, persistent_blocks())), block(64);
-    hipLaunchKernelGGL((k_hier_decode_lane<DT, 330, 30, 2, HierSkL>), grid, block, 0, s, src, so, dst, dout, din,
-                       n_inner, tpo, (int)n_tiles, xf_const(P), G.W, G.w_outer);
+    if (cells)
+        hipLaunchKernelGGL((k_hier_decode_lane<DT, 330, 30, 2, HierSkL, true>), grid, block, 0, s, src, so, dst, dout,
+                           din, n_inner, tpo, (int)n_tiles, xf_const(P), G.W, G.w_outer, cells);
+    else
+        hipLaunchKernelGGL((k_hier_decode_lane<DT, 330, 30, 2, HierSkL, false>), grid, block, 0, s, src, so, dst, dout,
+                           din, n_inner, tpo, (int)n_tiles, xf_const(P), G.W, G.w_outer, nullptr);
     return hipGetLastError();
 }
 
@@ -332,11 +350,11 @@ hipError_t sp_launch_hier_encode_lane(const SpPlan &P, const SpHierGeo &G, const
 
 hipError_t sp_launch_hier_decode_lane(const SpPlan &P, const SpHierGeo &G, const unsigned char *src, long long so,
                                       void *dst, int dtype, long long dout, long long din, int n_outer, int n_inner,
-                                      hipStream_t s) {
+                                      hipStream_t s, const int *cells) {
     const int esz = dtype == SP_DT_F16 ? 2 : 4;
     if (((uintptr_t)dst % 16) || ((dout * esz) % 16) || ((din * esz) % 16)) return hipErrorNotSupported;
     if (((uintptr_t)src % 4) || (so % 4)) return hipErrorNotSupported;
     if (!hier_geometry_matches(P, G)) return hipErrorNotSupported;
-    return dtype == SP_DT_F16 ? hier_dec_launch<SP_DT_F16>(P, G, src, so, dst, dout, din, n_outer, n_inner, s)
-                              : hier_dec_launch<SP_DT_F32>(P, G, src, so, dst, dout, din, n_outer, n_inner, s);
+    return dtype == SP_DT_F16 ? hier_dec_launch<SP_DT_F16>(P, G, src, so, dst, dout, din, n_outer, n_inner, s, cells)
+                              : hier_dec_launch<SP_DT_F32>(P, G, src, so, dst, dout, din, n_outer, n_inner, s, cells);
 }

@@ -213,9 +213,10 @@ struct SpHierGeo {
 hipError_t sp_launch_hier_encode_lane(const SpPlan &P, const SpHierGeo &G, const void *src, int dtype, long long so,
                                       long long si, unsigned char *dst, long long dout, int n_outer, int n_inner,
                                       hipStream_t s);
+// cells (optional): listed positions, record and row at cells[i] (slack after the cache)
 hipError_t sp_launch_hier_decode_lane(const SpPlan &P, const SpHierGeo &G, const unsigned char *src, long long so,
                                       void *dst, int dtype, long long dout, long long din, int n_outer, int n_inner,
-                                      hipStream_t s);
+                                      hipStream_t s, const int *cells = nullptr);
 
 // one-vector-per-lane sqfree kernels for the shipping geometry; hipErrorNotSupported
 // (nothing launched) when no specialization fits

@@ -576,6 +576,46 @@ __device__ __forceinline__ void rows_to_stage(const float (&x)[N], unsigned char
     }
 }
 
+// Listed positions: the lane's own record at byte address g, as the dwords that
+// cover it, funnel-shifted to its byte offset (the cache must hold at least 4
+// bytes past its last record).
+template <class LY>
+__device__ __forceinline__ void rec_load_direct(uint32_t (&rec)[LY::dwords], const unsigned char *g) {
+    constexpr int B = LY::total, DW = LY::dwords;
+    const uintptr_t a = (uintptr_t)g;
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(a & ~(uintptr_t)3);
+    const uint32_t sh = (uint32_t)(a & 3) * 8;
+    uint32_t w[DW + 1];
+#pragma unroll
+    for (int d = 0; d <= DW; d++) w[d] = p[d];
+#pragma unroll
+    for (int d = 0; d < DW; d++) rec[d] = __builtin_amdgcn_alignbit(w[d + 1], w[d], sh);
+    if (B % 4 != 0) rec[DW - 1] &= (1u << (8 * (B % 4))) - 1u;
+}
+
+// Listed positions: lane j's row (x) to row `pos` of lane j (dst + (o*dout +
+// pos*din) elements) for j < nvalid, through the padded LDS stage with RB/16
+// lanes per row, so each row leaves as one contiguous run of 16-byte stores.
+template <int DT, int HD, int N>
+__device__ __forceinline__ void rows_out_listed(const float (&x)[N], unsigned char *stage, void *dst, long long dout,
+                                                long long din, int o, int pos, int nvalid, int lane) {
+    constexpr int RB = row_bytes<DT>(HD), RP = RB + 16, CPR = RB / 16;
+    constexpr long long esz = DT == SP_DT_F16 ? 2 : 4;
+    __syncthreads();  // the previous tile's stage reads are done
+    rows_to_stage<DT, HD>(x, stage, lane);
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < CPR; q++) {
+        const int idx = q * 64 + lane, r = idx / CPR, piece = idx - r * CPR;
+        const int prow = __shfl(pos, r, 64);
+        if (r < nvalid) {
+            const u32x4 v = *reinterpret_cast<const u32x4 *>(stage + r * RP + piece * 16);
+            *reinterpret_cast<u32x4 *>(reinterpret_cast<unsigned char *>(dst) +
+                                       ((long long)o * dout + (long long)prow * din) * esz + piece * 16) = v;
+        }
+    }
+}
+
 template <int DT, int HD, int N>
 __device__ __forceinline__ void tile_rows_out(const float (&x)[N], unsigned char *stage, void *dst, long long dout,
                                               long long din, const TileMap &M, int t, int lane) {

@@ -340,8 +340,8 @@ hipError_t sp_launch_hier_decode(const SpPlan &P, const SpHierGeo &G, const unsi
                                  int n_outer, int n_inner, hipStream_t s, const int *cells) {
     if (n_outer <= 0 || n_inner <= 0) return hipSuccess;
     if (!sq_fits(P, G.pad, G.bytes)) return hipErrorInvalidValue;
-    if (!cells && !getenv_lane_off_sq()) {  // listed positions: general kernels only
-        const hipError_t e = sp_launch_hier_decode_lane(P, G, src, so, dst, dtype, dout, din, n_outer, n_inner, s);
+    if (!getenv_lane_off_sq()) {
+        const hipError_t e = sp_launch_hier_decode_lane(P, G, src, so, dst, dtype, dout, din, n_outer, n_inner, s, cells);
         if (e != hipErrorNotSupported) return e;
     }
     const long long nv = (long long)n_outer * n_inner;

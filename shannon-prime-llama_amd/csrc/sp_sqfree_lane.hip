@@ -238,8 +238,7 @@ k_sqfree_decode_lane_cells(const unsigned char *__restrict__ src, long long so, 
                            long long dout, long long din, const int *__restrict__ cells, int n_inner,
                            int tiles_per_outer, int n_tiles, const XfConst K) {
     using G = SqRec<PAD, SK, RBITS, SPIN, SL>;
-    constexpr int RB = row_bytes<DT>(HD), RP = RB + 16, CPR = RB / 16, NR = PAD - SK, DWR = G::dwords, B = G::total;
-    constexpr long long esz = DT == SP_DT_F16 ? 2 : 4;
+    constexpr int RP = row_bytes<DT>(HD) + 16, NR = PAD - SK, DWR = G::dwords, B = G::total;
     constexpr auto &KN = kKnight<PAD, SK>;
     __shared__ __attribute__((aligned(16))) unsigned char stage[64 * RP];
     const int lane = threadIdx.x;
@@ -248,15 +247,8 @@ k_sqfree_decode_lane_cells(const unsigned char *__restrict__ src, long long so, 
         int o, i0, nvalid;
         M.at(t, o, i0, nvalid);
         const int pos = cells[lane < nvalid ? i0 + lane : i0];
-        const uintptr_t a = (uintptr_t)(src + (long long)o * so + (long long)pos * B);
-        const uint32_t *p = reinterpret_cast<const uint32_t *>(a & ~(uintptr_t)3);
-        const uint32_t sh = (uint32_t)(a & 3) * 8;
-        uint32_t w[DWR + 1], rec[DWR];
-#pragma unroll
-        for (int d = 0; d <= DWR; d++) w[d] = p[d];
-#pragma unroll
-        for (int d = 0; d < DWR; d++) rec[d] = __builtin_amdgcn_alignbit(w[d + 1], w[d], sh);
-        if (B % 4 != 0) rec[DWR - 1] &= (1u << (8 * (B % 4))) - 1u;
+        uint32_t rec[DWR];
+        rec_load_direct<G>(rec, src + (long long)o * so + (long long)pos * B);
         float sk[SK];
         dequant_bands<SL, false, true>(rec, SL::nb, sk);
         float c[PAD];
@@ -277,19 +269,7 @@ k_sqfree_decode_lane_cells(const unsigned char *__restrict__ src, long long so, 
             }
         }
         vil_stages<PAD, 0, 1>(c, K);
-        __syncthreads();  // the previous tile's stage reads are done
-        rows_to_stage<DT, HD>(c, stage, lane);
-        __syncthreads();
-#pragma unroll
-        for (int q = 0; q < CPR; q++) {
-            const int idx = q * 64 + lane, r = idx / CPR, piece = idx - r * CPR;
-            const int prow = __shfl(pos, r, 64);
-            if (r < nvalid) {
-                const u32x4 v = *reinterpret_cast<const u32x4 *>(stage + r * RP + piece * 16);
-                *reinterpret_cast<u32x4 *>(reinterpret_cast<unsigned char *>(dst) +
-                                           ((long long)o * dout + (long long)prow * din) * esz + piece * 16) = v;
-            }
-        }
+        rows_out_listed<DT, HD>(c, stage, dst, dout, din, o, pos, nvalid, lane);
     }
 }
 

@@ -36,10 +36,13 @@ def _rows(x16, pad_row):
     return r
 
 
-@pytest.mark.parametrize("kind", ["sqfree", "hier"])
-def test_dual_routed_write_and_merged_read(kind):
-    say(f"dual cache kind={kind}")
-    hd, L, H, ms, pad_row, layer = 128, 2, 2, 200, 8, 1
+@pytest.mark.parametrize("kind,hd", [("sqfree", 128), ("hier", 128), ("hier", 256)])
+def test_dual_routed_write_and_merged_read(kind, hd):
+    """sqfree at hd 128 and hier at hd 256 (the default 30/300 geometry) read their
+    listed positions through the one-vector-per-lane kernels, hier at hd 128 through
+    the one-vector-per-wave kernel."""
+    say(f"dual cache kind={kind} hd={hd}")
+    L, H, ms, pad_row, layer = 2, 2, 200, 8, 1
     stream = torch.cuda.current_stream().cuda_stream
     ship = S.ShipCache(S.config(hd, L, H), ms, stream=stream)
     pad = O.sqfree_pad_dim(hd)
