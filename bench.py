@@ -251,6 +251,34 @@ def bench_variants(torch, S, L, stream, reps=3):
         "layout": "one layer x 8 heads x 32768 positions, K+V, fp16 rows; System 2 = sqfree on 20% of positions"}
     dc.free()
     sq1.free()
+    # the same with System 2 = hier at the configs[4] geometry (hd 256 -> pad 330, 30/300, 2-bit residual;
+    # W random, one per slot) beside an hd 256 ship cache, 8 heads x 32768 positions
+    import numpy as np
+    hd4 = 256
+    sk4, tg4 = np.zeros(30, np.int32), np.zeros(300, np.int32)
+    assert L.sp_hier_default_geometry(330, C.c_void_p(sk4.ctypes.data), C.c_void_p(tg4.ctypes.data)) == 30
+    c4 = S.ShipCache(S.config(hd4, 1, H1), KV1, stream.cuda_stream)
+    hc4 = S.HierCache(S.config(hd4, 1, H1), 330, sk4, tg4, S.band_config(30, [5, 5]), 2, KV1, H1,
+                      stream=stream.cuda_stream)
+    hc4.upload_W((np.random.default_rng(9).standard_normal((H1, 300, 30)) * 0.05).astype(np.float16).view(np.uint16))
+    dc4 = S.DualCache(c4, hc4, S.DUAL_HIER, 1.0)
+    for t in range(KV1):
+        L.sp_hip_dual_route_position(dc4.ref, t, 2.0 if own2[t] else 0.0)
+    krow4 = torch.randn((KV1, H1 * hd4), generator=g, device="cuda").half()
+    S.check(L.sp_hip_dual_write_layer(dc4.ref, 0, 0, KV1, P(krow4), P(krow4), H1 * hd4, S.DTYPE_F16), "dual4 write")
+    ko4 = torch.empty_like(krow4)
+    vo4 = torch.empty_like(krow4)
+    t_m4 = timed(lambda: S.check(L.sp_hip_dual_read_merged(dc4.ref, 0, KV1, P(ko4), P(vo4), H1 * hd4, S.DTYPE_F16),
+                                 "dual4 read"))
+    t_14 = timed(lambda: S.check(L.sp_hip_read_layer(c4.ref, 0, 0, KV1, P(ko4), P(vo4), H1 * hd4, S.DTYPE_F16, -1),
+                                 "ship4 read"))
+    out["cfg4_dual_hier_merged_read"] = {
+        "us": round(t_m4 * 1e6, 1), "ship_only_read_us": round(t_14 * 1e6, 1), "sys2_positions": n2,
+        "layout": "one layer x 8 heads x 32768 positions, hd 256, K+V, fp16 rows; System 2 = hier (pad 330) on 20%"}
+    dc4.free()
+    hc4.free()
+    c4.free()
+    del krow4, ko4, vo4
     # disk format v3 at the configs[1] layer shape: 4 layers x 8 heads x 32768 positions (33 MB of records
     # per layer file), save, load, and a partial load of K band 0 (+ the one V band), files under /tmp
     import tempfile
