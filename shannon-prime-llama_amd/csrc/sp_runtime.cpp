@@ -1781,7 +1781,12 @@ struct DualPriv {
     int n2 = 0;                        // positions routed to System 2
     bool dirty = true;                 // device list out of date
     int *d_list = nullptr;             // System 2 positions, ascending
-    int *h_list = nullptr;             // pinned staging for the list upload
+    // pinned staging for the list upload, double-buffered: a buffer is refilled
+    // only after the copy issued from it last time has run (its event)
+    int *h_list[2] = {nullptr, nullptr};
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    bool ev_used[2] = {false, false};
+    int cur = 0;
     int n_list = 0;
 };
 
@@ -1817,10 +1822,17 @@ extern "C" int sp_hip_dual_init(sp_hip_dual_cache_t *dc, sp_hip_cache_t *sys1, i
     if (sys1->stream != st2) { set_err("dual_init: System 1 and 2 must share a stream"); return -1; }
     DualPriv *pv = new DualPriv();
     pv->route.assign((size_t)ms2, 0);
-    if (!(hip_ok(hipMalloc((void **)&pv->d_list, (size_t)ms2 * sizeof(int)), "dual list") &&
-          hip_ok(hipHostMalloc((void **)&pv->h_list, (size_t)ms2 * sizeof(int), hipHostMallocDefault),
-                 "dual list staging"))) {
+    bool ok = hip_ok(hipMalloc((void **)&pv->d_list, (size_t)ms2 * sizeof(int)), "dual list");
+    for (int b = 0; b < 2 && ok; b++)
+        ok = hip_ok(hipHostMalloc((void **)&pv->h_list[b], (size_t)ms2 * sizeof(int), hipHostMallocDefault),
+                    "dual list staging") &&
+             hip_ok(hipEventCreateWithFlags(&pv->ev[b], hipEventDisableTiming), "dual list event");
+    if (!ok) {
         if (pv->d_list) (void)hipFree(pv->d_list);
+        for (int b = 0; b < 2; b++) {
+            if (pv->h_list[b]) (void)hipHostFree(pv->h_list[b]);
+            if (pv->ev[b]) (void)hipEventDestroy(pv->ev[b]);
+        }
         delete pv;
         return -1;
     }
@@ -1838,7 +1850,10 @@ extern "C" void sp_hip_dual_free(sp_hip_dual_cache_t *dc) {
     DualPriv *pv = (DualPriv *)dc->priv;
     (void)hipStreamSynchronize((hipStream_t)dc->sys1->stream);  // a list upload may be in flight
     (void)hipFree(pv->d_list);
-    (void)hipHostFree(pv->h_list);
+    for (int b = 0; b < 2; b++) {
+        (void)hipHostFree(pv->h_list[b]);
+        (void)hipEventDestroy(pv->ev[b]);
+    }
     delete pv;
     dc->priv = nullptr;
 }
@@ -1912,18 +1927,24 @@ extern "C" int sp_hip_dual_read_merged(sp_hip_dual_cache_t *dc, int layer, int k
     if (sp_hip_read_layer(dc->sys1, layer, 0, kv_len, d_k, d_v, row_stride, dtype, -1)) return -1;
     if (pv->n2 == 0) return 0;
     if (pv->dirty) {
-        // the previous upload may still be reading the staging buffer
-        if (!hip_ok(hipStreamSynchronize(s), "dual list sync")) return -1;
+        // refill the other staging buffer once the copy last issued from it has run
+        // (stream order keeps the device list from changing under earlier kernels)
+        const int b = pv->cur ^ 1;
+        if (pv->ev_used[b] && !hip_ok(hipEventSynchronize(pv->ev[b]), "dual list staging wait")) return -1;
         int n = 0;
         for (int p = 0; p < ms; p++)
-            if (pv->route[(size_t)p]) pv->h_list[n++] = p;
-        if (n && !hip_ok(hipMemcpyAsync(pv->d_list, pv->h_list, (size_t)n * sizeof(int), hipMemcpyHostToDevice, s),
-                         "dual list upload")) return -1;
+            if (pv->route[(size_t)p]) pv->h_list[b][n++] = p;
+        if (n && !(hip_ok(hipMemcpyAsync(pv->d_list, pv->h_list[b], (size_t)n * sizeof(int), hipMemcpyHostToDevice, s),
+                          "dual list upload") &&
+                   hip_ok(hipEventRecord(pv->ev[b], s), "dual list event"))) return -1;
+        pv->ev_used[b] = n > 0;
+        pv->cur = b;
         pv->n_list = n;
         pv->dirty = false;
     }
     // System 2 positions below kv_len: a prefix of the ascending list
-    const int n2 = (int)(std::lower_bound(pv->h_list, pv->h_list + pv->n_list, kv_len) - pv->h_list);
+    const int *hl = pv->h_list[pv->cur];
+    const int n2 = (int)(std::lower_bound(hl, hl + pv->n_list, kv_len) - hl);
     if (n2 == 0) return 0;
     for (int is_v = 0; is_v < 2; is_v++) {
         void *dst = is_v ? d_v : d_k;
