@@ -286,6 +286,11 @@ using V64 = Layout<64, 5>;
 // (shannon_prime_llama.c:240-248)
 using K96 = Layout<96, 5, 4, 4>;
 using V96 = Layout<96, 5>;
+// Gemma-shaped hd 256, K 5/5/4/3 and V 3: decode both, encode V (K's encode with the
+// Mobius gather needs more than the 512 registers of a lane and stays on the
+// 8-coefficients-per-lane kernel)
+using K256 = Layout<256, 5, 5, 4, 3>;
+using V256 = Layout<256, 3>;
 
 
 template <class LY, int DT, bool MOB>
@@ -367,7 +372,7 @@ hipError_t enc_dispatch(const SpPlan &P, bool mob, const void *src, long long so
                         unsigned char *dst, long long dout, int n_outer, int n_inner, hipStream_t s) {
 #define SP_TRY(LY, MOB) \
     if (layout_matches<LY>(P)) return enc_launch<LY, DT, MOB>(P, mob, src, so, si, dst, dout, n_outer, n_inner, s);
-    SP_TRY(K128, true) SP_TRY(V128, false) SP_TRY(K64, true) SP_TRY(V64, false) SP_TRY(K96, true) SP_TRY(V96, false)
+    SP_TRY(K128, true) SP_TRY(V128, false) SP_TRY(K64, true) SP_TRY(V64, false) SP_TRY(K96, true) SP_TRY(V96, false) SP_TRY(V256, false)
 #undef SP_TRY
     return hipErrorNotSupported;
 }
@@ -377,7 +382,7 @@ hipError_t dec_dispatch(const SpPlan &P, bool mob, const unsigned char *src, lon
                         long long dout, long long din, int n_outer, int n_inner, hipStream_t s) {
 #define SP_TRY(LY, MOB) \
     if (layout_matches<LY>(P)) return dec_launch<LY, DT, MOB>(P, mob, src, so, dst, dout, din, n_outer, n_inner, s);
-    SP_TRY(K128, true) SP_TRY(V128, false) SP_TRY(K64, true) SP_TRY(V64, false) SP_TRY(K96, true) SP_TRY(V96, false)
+    SP_TRY(K128, true) SP_TRY(V128, false) SP_TRY(K64, true) SP_TRY(V64, false) SP_TRY(K96, true) SP_TRY(V96, false) SP_TRY(K256, true) SP_TRY(V256, false)
 #undef SP_TRY
     return hipErrorNotSupported;
 }

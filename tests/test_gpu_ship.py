@@ -28,6 +28,7 @@ CASES = [
     (128, [5, 5, 4, 3], True, S.NORM_STAGE, 0),
     (64, [5, 5, 4, 3], True, S.NORM_FINAL, 0),
     (256, [5, 5, 4, 3], True, S.NORM_FINAL, 0),
+    (256, [3], False, S.NORM_FINAL, 0),
     (128, [5, 5, 4, 3], True, S.NORM_FINAL, 1 << 3),
     (64, [5, 4, 4], True, S.NORM_FINAL, 0),        # bands 21/21/22 -> generic kernels
     (96, [5, 4, 4], True, S.NORM_FINAL, 0),        # Vilenkin 2^5*3
@@ -67,10 +68,11 @@ def test_encode_decode_bit_exact(hd, bits, mob, norm, tmask):
         np.testing.assert_array_equal(g16, r16, err_msg=f"f16 generic={generic}")
 
 
+@pytest.mark.parametrize("hd", [128, 256])
 @pytest.mark.parametrize("max_bands", [0, 1, 2, 3, 4, 7, -1])
-def test_partial_reads(max_bands):
-    hd, bits, n = 128, [5, 5, 4, 3], 300
-    k16, _ = W.cfg1_kv(n_heads=1, n_pos=n, seed=9)
+def test_partial_reads(max_bands, hd):
+    bits, n = [5, 5, 4, 3], 300
+    k16, _ = W.cfg1_kv(n_heads=1, n_pos=n, hd=hd, seed=9)
     x16 = k16.reshape(n, hd).view(np.uint16)
     obc, sbc = O.band_config(hd, bits), S.band_config(hd, bits)
     order = O.mobius_order(hd)
