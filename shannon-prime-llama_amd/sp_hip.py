@@ -91,6 +91,13 @@ class SpHipDualCache(C.Structure):
 DUAL_SQFREE, DUAL_HIER = 1, 2
 
 
+class SpHipColdLayer(C.Structure):
+    _fields_ = [("h_pinned", C.c_void_p), ("capacity", C.c_int64), ("packed_stride", C.c_int),
+                ("n_heads", C.c_int), ("max_seq_len", C.c_int), ("cap_pos", C.c_int64), ("write_head", C.c_int64),
+                ("oldest_pos", C.c_int64), ("newest_pos", C.c_int64), ("ring_mode", C.c_int),
+                ("initialized", C.c_int)]
+
+
 class SpLlamaParams(C.Structure):
     _fields_ = [
         ("head_dim", C.c_int), ("n_layers", C.c_int), ("n_heads_kv", C.c_int),
@@ -158,6 +165,13 @@ def lib():
         for name in ("sp_hip_cache_load", "sp_hip_sqfree_cache_load", "sp_hip_hier_cache_load"):
             getattr(L, name).argtypes = [vp, cp, u64]
         L.sp_hip_cache_load_partial.argtypes = [vp, cp, u64, i]
+        L.sp_hip_memset.argtypes = [vp, i, C.c_size_t, vp]
+        L.sp_hip_cold_layer_init.argtypes = [vp, C.c_int64, i, i, i]
+        L.sp_hip_cold_layer_free.argtypes = [vp]
+        L.sp_hip_cold_writeback.argtypes = [vp, vp, i, i, vp]
+        L.sp_hip_cold_restore.argtypes = [vp, vp, i, vp]
+        L.sp_hip_d2h_async.argtypes = [vp, vp, C.c_int64, vp]
+        L.sp_hip_h2d_async.argtypes = [vp, vp, C.c_int64, vp]
         L.sp_hip_dual_init.argtypes = [vp, vp, i, vp, f]
         L.sp_hip_dual_free.argtypes = [vp]
         L.sp_hip_dual_route_position.argtypes = [vp, i, f]
