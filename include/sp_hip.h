@@ -189,6 +189,10 @@ int sp_hip_attn_decode_bands(const sp_hip_cache_t *cc, int layer, int n_kv,
                              const float *d_q, int n_q, float kq_scale,
                              float *d_scores, float *d_out, int max_bands, void *stream);
 
+/* Memory report to stderr (sp_cuda_print_memory, shannon_prime_cuda.h:140-141): the
+ * records' MiB against an fp16 K+V cache of the same shape. */
+void sp_hip_print_memory(const sp_hip_cache_t *cc);
+
 /* Every layer of one decode step in one launch sequence: q [n_layers][n_q][hd],
  * out [n_layers][n_q][hd] (benchmark helper; per-layer semantics above). */
 int sp_hip_attn_decode_all_layers(const sp_hip_cache_t *cc, int n_kv, const float *d_q,

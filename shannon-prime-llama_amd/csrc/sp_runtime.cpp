@@ -2365,3 +2365,14 @@ extern "C" int sp_hip_cold_restore(const sp_hip_cold_layer_t *cl, void *d_packed
     }
     return cold_copy(cl, (unsigned char *)d_packed, 0, n_pos, false, (hipStream_t)stream) ? 0 : -1;
 }
+
+// Memory report of a ship cache (sp_cuda_print_memory, shannon_prime_cuda.cu:663-677):
+// record bytes against an fp16 K+V cache of the same shape.
+extern "C" void sp_hip_print_memory(const sp_hip_cache_t *cc) {
+    if (!cc) return;
+    const double slots = (double)cc->config.n_layers * cc->config.n_heads_kv * cc->max_seq_len;
+    const double k = slots * cc->k_bands.total_bytes, v = slots * cc->v_bands.total_bytes;
+    const double fp16 = slots * cc->config.head_dim * 2.0 * 2.0, mib = 1024.0 * 1024.0;
+    fprintf(stderr, "[sp-hip] cache memory: %.2f MiB of records (K %.2f + V %.2f), fp16 K+V %.2f MiB, %.1fx smaller\n",
+            (k + v) / mib, k / mib, v / mib, fp16 / mib, (k + v) > 0 ? fp16 / (k + v) : 0.0);
+}
