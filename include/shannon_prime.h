@@ -128,6 +128,15 @@ void sp_shadow_read_k_batch(const sp_shadow_cache_t *sc, int layer, int head,
 void sp_shadow_read_v_batch(const sp_shadow_cache_t *sc, int layer, int head,
                             int start_pos, int n_pos, float *v_out);
 
+/* ---- disk (sp_shadow_cache_save / _load, kv_cache.cpp:1549, 1572; the partial load
+ *      of the disk tier, CHANGELOG.md): the v3 files of sp_hip_cache_save (one per
+ *      layer, {prefix}.L{layer}.bin), read and written from the host record buffers;
+ *      the header carries the model hash (strict unless SP_DISK_HASH_STRICT=0).
+ *      save returns 0, the loads the n_pos stored; -1 on any error. ---- */
+int  sp_shadow_cache_save(const sp_shadow_cache_t *sc, const char *prefix, int n_pos, uint64_t model_hash);
+int  sp_shadow_cache_load(sp_shadow_cache_t *sc, const char *prefix, uint64_t expected_hash);
+int  sp_shadow_cache_load_partial(sp_shadow_cache_t *sc, const char *prefix, uint64_t expected_hash, int max_bands);
+
 /* ---- calibration (sp_shadow_calibrate_begin/feed/end, called at kv_cache.cpp:525,
  * 587, 610). begin clears the sums; feed adds one host fp32 K vector's transform
  * (computed on the device by the cache's own transform); end ranks the coefficients

@@ -2376,3 +2376,108 @@ extern "C" void sp_hip_print_memory(const sp_hip_cache_t *cc) {
     fprintf(stderr, "[sp-hip] cache memory: %.2f MiB of records (K %.2f + V %.2f), fp16 K+V %.2f MiB, %.1fx smaller\n",
             (k + v) / mib, k / mib, v / mib, fp16 / mib, (k + v) > 0 ? fp16 / (k + v) : 0.0);
 }
+
+// Shadow cache save / load (sp_shadow_cache_save / _load / _load_partial, called
+// at kv_cache.cpp:1549, 1572): the shadow cache's records are host buffers
+// (k_cache[slot], v_cache[slot], slot = layer * n_heads + head), so the same v3
+// files are written and read here with a host-side band-major repack. Files are
+// interchangeable with sp_hip_cache_save / _load for the same config and order.
+namespace {
+
+uint32_t shadow_order_check(const sp_shadow_cache_t *sc) {
+    const int hd = sc->config.head_dim;
+    const int *ord = sc->use_var_reorder && sc->var_order ? sc->var_order
+                   : sc->config.use_mobius_mask ? sc->mobius_mask.order : nullptr;
+    return ord ? (uint32_t)sp_fnv1a64(ord, (size_t)hd * sizeof(int)) : 0u;
+}
+
+int shadow_disk(sp_shadow_cache_t *sc, const char *prefix, int n_pos, uint64_t hash, int max_segs, bool save) {
+    if (!sc || !sc->k_cache || !sc->v_cache || !prefix) { set_err("shadow disk: bad cache"); return -1; }
+    const int H = sc->config.n_heads_kv, hd = sc->config.head_dim, Lyr = sc->config.n_layers;
+    const int kB = sc->k_bands.total_bytes, vB = sc->v_bands.total_bytes;
+    const uint32_t oc = shadow_order_check(sc);
+    int n_all = -1;
+    std::vector<unsigned char> body;
+    for (int l = 0; l < Lyr; l++) {
+        const std::string path = layer_path(prefix, l);
+        DiskHeader h{};
+        FILE *f = fopen(path.c_str(), save ? "wb" : "rb");
+        if (!f) { set_err("shadow disk: cannot open %s", path.c_str()); return -1; }
+        if (!save) {
+            bool ok = fread(&h, sizeof(h), 1, f) == 1 && memcmp(h.magic, "VHT2", 4) == 0 &&
+                      h.check == sp_fnv1a64(&h, 56) && h.version == SP_DISK_VERSION;
+            if (!ok) set_err("load: %s is not a VHT2 v%u cache file", path.c_str(), SP_DISK_VERSION);
+            else if (h.kind != DISK_SHIP || h.layer != l || h.n_heads != H || h.head_dim != hd || h.k_bytes != kB ||
+                     h.v_bytes != vB || h.n_pos <= 0 || (n_all >= 0 && h.n_pos != n_all)) {
+                set_err("load: %s does not match this cache's shape", path.c_str());
+                ok = false;
+            } else if (h.order_check != oc) {
+                set_err("load: %s was written with another coefficient order", path.c_str());
+                ok = false;
+            } else {
+                ok = hash_ok(h.model_hash, hash, "load");
+            }
+            if (!ok) { fclose(f); return -1; }
+            n_pos = n_all = h.n_pos;
+        }
+        const long long n_rec = (long long)H * n_pos;
+        const SpDiskSegs Sk = disk_segs(&sc->k_bands, kB, n_rec), Sv = disk_segs(&sc->v_bands, vB, n_rec);
+        const size_t kfull = (size_t)n_rec * kB;
+        body.assign(kfull + (size_t)n_rec * vB, 0);
+        bool ok = true;
+        if (!save) {
+            const int nk = max_segs < 0 ? Sk.n : std::min(max_segs, Sk.n), nv = max_segs < 0 ? Sv.n : std::min(max_segs, Sv.n);
+            const size_t kread = (size_t)segs_bytes(Sk, nk, n_rec), vread = (size_t)segs_bytes(Sv, nv, n_rec);
+            ok = fread(body.data(), 1, kread, f) == kread && fseek(f, (long)(kfull - kread), SEEK_CUR) == 0 &&
+                 fread(body.data() + kfull, 1, vread, f) == vread;
+            if (!ok) set_err("load: %s is truncated", path.c_str());
+            // segments past the loaded ones stay zero in `body` and clear the records
+        }
+        for (int side = 0; side < 2 && ok; side++) {
+            const SpDiskSegs &Sg = side ? Sv : Sk;
+            const int B = side ? vB : kB;
+            unsigned char *base = body.data() + (side ? kfull : 0);
+            for (int hh = 0; hh < H; hh++) {
+                uint8_t *rec = (side ? sc->v_cache : sc->k_cache)[l * H + hh];
+                if (!rec) { set_err("shadow disk: slot %d has no buffer", l * H + hh); ok = false; break; }
+                for (int p = 0; p < n_pos; p++)
+                    for (int s = 0; s < Sg.n; s++) {
+                        unsigned char *seg = base + Sg.base[s] + ((long long)hh * n_pos + p) * Sg.len[s];
+                        unsigned char *r = rec + (size_t)p * B + Sg.off[s];
+                        if (save) memcpy(seg, r, (size_t)Sg.len[s]);
+                        else memcpy(r, seg, (size_t)Sg.len[s]);
+                    }
+            }
+        }
+        if (ok && save) {
+            memcpy(h.magic, "VHT2", 4);
+            h.version = SP_DISK_VERSION;
+            h.model_hash = hash;
+            h.n_pos = n_pos, h.layer = l, h.n_heads = H, h.head_dim = hd, h.kind = DISK_SHIP;
+            h.k_bytes = kB, h.v_bytes = vB, h.k_segs = Sk.n, h.v_segs = Sv.n, h.order_check = oc;
+            header_seal(h);
+            ok = fwrite(&h, sizeof(h), 1, f) == 1 && fwrite(body.data(), 1, body.size(), f) == body.size();
+            if (!ok) set_err("save: write failed for %s", path.c_str());
+        }
+        if (fclose(f) != 0 && save) { set_err("save: write failed for %s", path.c_str()); ok = false; }
+        if (!ok) return -1;
+    }
+    return save ? 0 : n_all;
+}
+
+}  // namespace
+
+extern "C" int sp_shadow_cache_save(const sp_shadow_cache_t *sc, const char *prefix, int n_pos, uint64_t model_hash) {
+    if (n_pos <= 0) { set_err("shadow save: bad n_pos"); return -1; }
+    return shadow_disk(const_cast<sp_shadow_cache_t *>(sc), prefix, n_pos, model_hash, -1, true);
+}
+
+extern "C" int sp_shadow_cache_load(sp_shadow_cache_t *sc, const char *prefix, uint64_t expected_hash) {
+    return shadow_disk(sc, prefix, 0, expected_hash, -1, false);
+}
+
+extern "C" int sp_shadow_cache_load_partial(sp_shadow_cache_t *sc, const char *prefix, uint64_t expected_hash,
+                                            int max_bands) {
+    if (max_bands < 0) { set_err("load_partial: max_bands < 0"); return -1; }
+    return shadow_disk(sc, prefix, 0, expected_hash, max_bands, false);
+}

@@ -165,6 +165,9 @@ def lib():
         for name in ("sp_hip_cache_load", "sp_hip_sqfree_cache_load", "sp_hip_hier_cache_load"):
             getattr(L, name).argtypes = [vp, cp, u64]
         L.sp_hip_cache_load_partial.argtypes = [vp, cp, u64, i]
+        L.sp_shadow_cache_save.argtypes = [vp, cp, i, u64]
+        L.sp_shadow_cache_load.argtypes = [vp, cp, u64]
+        L.sp_shadow_cache_load_partial.argtypes = [vp, cp, u64, i]
         L.sp_hip_memset.argtypes = [vp, i, C.c_size_t, vp]
         L.sp_hip_cold_layer_init.argtypes = [vp, C.c_int64, i, i, i]
         L.sp_hip_cold_layer_free.argtypes = [vp]

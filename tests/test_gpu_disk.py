@@ -204,3 +204,61 @@ def test_load_rejects_another_coefficient_order(tmp_path):
     assert b"order" in Lb.sp_hip_last_error()
     a.free()
     b.free()
+
+
+def test_shadow_files_match_the_device_cache(tmp_path):
+    """The shadow cache (host record buffers) writes the same bytes as the device
+    cache for the same vectors, and each loads the other's files; a partial load
+    clears the bands past the limit."""
+    say("disk shadow")
+    L, H, hd, n = 2, 2, 128, 48
+    cfg = S.config(hd, L, H)
+    Lb = S.lib()
+    kB, vB = 76, 50
+    x = np.random.default_rng(8).standard_normal((L, H, n, hd)).astype(np.float32)
+
+    def shadow():
+        sc = S.SpShadowCache()
+        S.check(Lb.sp_shadow_cache_init(C.byref(sc), C.byref(cfg)))
+        bufs = [np.zeros(n * kB, np.uint8) for _ in range(L * H)] + [np.zeros(n * vB, np.uint8) for _ in range(L * H)]
+        kp = (C.POINTER(C.c_uint8) * (L * H))(*[b.ctypes.data_as(C.POINTER(C.c_uint8)) for b in bufs[:L * H]])
+        vp = (C.POINTER(C.c_uint8) * (L * H))(*[b.ctypes.data_as(C.POINTER(C.c_uint8)) for b in bufs[L * H:]])
+        sc.k_cache = C.cast(kp, C.POINTER(C.POINTER(C.c_uint8)))
+        sc.v_cache = C.cast(vp, C.POINTER(C.POINTER(C.c_uint8)))
+        return sc, bufs, (kp, vp)
+
+    sa, ba, keep_a = shadow()
+    for layer in range(L):
+        for h in range(H):
+            Lb.sp_shadow_write_k_batch(C.byref(sa), layer, h, 0, n, C.c_void_p(x[layer, h].ctypes.data))
+            Lb.sp_shadow_write_v_batch(C.byref(sa), layer, h, 0, n, C.c_void_p(x[layer, h].ctypes.data))
+    ps, pd = str(tmp_path / "shadow"), str(tmp_path / "dev")
+    S.check(Lb.sp_shadow_cache_save(C.byref(sa), ps.encode(), n, 11))
+    stream = torch.cuda.current_stream().cuda_stream
+    cc = S.ShipCache(cfg, n, stream=stream)
+    # the device cache takes the same fp32 vectors ([slot][pos][hd])
+    S.check(Lb.sp_hip_write_all(cc.ref, 0, n, p(dev(x.reshape(-1, hd))), p(dev(x.reshape(-1, hd))), S.DTYPE_F32))
+    S.check(Lb.sp_hip_cache_save(cc.ref, pd.encode(), n, 11))
+    for layer in range(L):
+        assert open(f"{ps}.L{layer}.bin", "rb").read() == open(f"{pd}.L{layer}.bin", "rb").read()
+    # shadow loads the device files, device loads the shadow files
+    sb, bb, keep_b = shadow()
+    assert Lb.sp_shadow_cache_load(C.byref(sb), pd.encode(), 11) == n
+    for a_, b_ in zip(ba, bb):
+        np.testing.assert_array_equal(a_, b_)
+    cd = S.ShipCache(cfg, n, stream=stream)
+    assert Lb.sp_hip_cache_load(cd.ref, ps.encode(), 11) == n
+    np.testing.assert_array_equal(d2h(cd.c.d_k_cache, L * H * n * kB), np.concatenate(ba[:L * H]))
+    # partial: K bands 0..1 kept, 2..3 cleared; the single V band kept
+    sp_, bp, keep_p = shadow()
+    assert Lb.sp_shadow_cache_load_partial(C.byref(sp_), ps.encode(), 11, 2) == n
+    for s in range(L * H):
+        k_full, k_part = ba[s].reshape(n, kB), bp[s].reshape(n, kB)
+        np.testing.assert_array_equal(k_part[:, :44], k_full[:, :44])
+        assert not k_part[:, 44:].any()
+        np.testing.assert_array_equal(bp[L * H + s], ba[L * H + s])
+    assert Lb.sp_shadow_cache_load(C.byref(sb), ps.encode(), 12) == -1
+    for sc_ in (sa, sb, sp_):
+        Lb.sp_shadow_cache_free(C.byref(sc_))
+    cc.free()
+    cd.free()
