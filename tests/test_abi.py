@@ -121,3 +121,11 @@ def test_fnv1a64_known_answers():
     L = S.lib()
     for msg, want in ((b"", 0xcbf29ce484222325), (b"a", 0xaf63dc4c8601ec8c), (b"foobar", 0x85944171f73967e8)):
         assert L.sp_fnv1a64(msg, len(msg)) == want, msg
+
+
+def test_cpp_kv_cache_header_compiles():
+    """include/sp_kv_cache.hpp (the C++ KvCache mirror) is self-contained C++17."""
+    inc = os.path.join(os.path.dirname(__file__), "..", "include")
+    r = subprocess.run(["g++", "-std=c++17", "-Wall", "-Wextra", "-Werror", "-fsyntax-only", "-x", "c++", "-I", inc,
+                        "-"], input='#include "sp_kv_cache.hpp"\n', capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
