@@ -128,6 +128,16 @@ void sp_shadow_read_k_batch(const sp_shadow_cache_t *sc, int layer, int head,
 void sp_shadow_read_v_batch(const sp_shadow_cache_t *sc, int layer, int head,
                             int start_pos, int n_pos, float *v_out);
 
+/* ---- per-vector core calls on host pointers (the absent core's sp_vht2_forward_f32,
+ *      used at llama_sp_fused_kq.cpp:33 and kv_cache.cpp:399, and its band codec
+ *      sp_band_quantize / sp_band_dequantize / _partial, semantics at
+ *      shannon_prime_llama.h:240-255): computed on the device by the caches' kernels
+ *      through a staging round trip; VHT2 with the final 1/sqrt(n) normalisation. ---- */
+void sp_vht2_forward_f32(float *data, int n);
+void sp_band_quantize(const float *in, uint8_t *out, const sp_band_config_t *bc);
+void sp_band_dequantize(const uint8_t *in, float *out, const sp_band_config_t *bc);
+void sp_band_dequantize_partial(const uint8_t *in, float *out, const sp_band_config_t *bc, int max_bands);
+
 /* ---- disk (sp_shadow_cache_save / _load, kv_cache.cpp:1549, 1572; the partial load
  *      of the disk tier, CHANGELOG.md): the v3 files of sp_hip_cache_save (one per
  *      layer, {prefix}.L{layer}.bin), read and written from the host record buffers;

@@ -2481,3 +2481,68 @@ extern "C" int sp_shadow_cache_load_partial(sp_shadow_cache_t *sc, const char *p
     if (max_bands < 0) { set_err("load_partial: max_bands < 0"); return -1; }
     return shadow_disk(sc, prefix, 0, expected_hash, max_bands, false);
 }
+
+// ===========================================================================
+// host-pointer forms of the core's per-vector calls: sp_vht2_forward_f32 (called
+// at llama_sp_fused_kq.cpp:33, kv_cache.cpp:399) and sp_band_quantize /
+// sp_band_dequantize(_partial) (the absent core's band codec): one round trip
+// through a device staging buffer, computed by the same kernels as the caches
+// ===========================================================================
+static std::mutex g_core_mu;
+static float *g_core_f = nullptr;
+static unsigned char *g_core_b = nullptr;
+static size_t g_core_nf = 0, g_core_nb = 0;
+
+static bool core_stage(size_t nf, size_t nb) {
+    if (nf > g_core_nf) {
+        if (g_core_f) (void)hipFree(g_core_f);
+        g_core_f = nullptr, g_core_nf = 0;
+        if (!hip_ok(hipMalloc((void **)&g_core_f, nf * sizeof(float)), "core staging")) return false;
+        g_core_nf = nf;
+    }
+    if (nb > g_core_nb) {
+        if (g_core_b) (void)hipFree(g_core_b);
+        g_core_b = nullptr, g_core_nb = 0;
+        if (!hip_ok(hipMalloc((void **)&g_core_b, nb + SP_CACHE_SLACK), "core staging")) return false;
+        g_core_nb = nb;
+    }
+    return true;
+}
+
+extern "C" void sp_vht2_forward_f32(float *data, int n) {
+    if (!data || n <= 0) return;
+    std::lock_guard<std::mutex> lk(g_core_mu);
+    if (!core_stage((size_t)n, 0) ||
+        !hip_ok(hipMemcpy(g_core_f, data, (size_t)n * sizeof(float), hipMemcpyHostToDevice), "vht2 H2D")) return;
+    sp_hip_vht2_forward(g_core_f, n, 1, SP_VHT2_NORM_FINAL, nullptr);
+    (void)hip_ok(hipMemcpy(data, g_core_f, (size_t)n * sizeof(float), hipMemcpyDeviceToHost), "vht2 D2H");
+}
+
+extern "C" void sp_band_quantize(const float *in, uint8_t *out, const sp_band_config_t *bc) {
+    if (!in || !out || !bc) return;
+    std::lock_guard<std::mutex> lk(g_core_mu);
+    const size_t n = (size_t)bc->head_dim, B = (size_t)bc->total_bytes;
+    if (!core_stage(n, B) || !hip_ok(hipMemcpy(g_core_f, in, n * sizeof(float), hipMemcpyHostToDevice), "quantize H2D"))
+        return;
+    sp_hip_band_quantize(g_core_f, g_core_b, bc, 1, nullptr);
+    (void)hip_ok(hipMemcpy(out, g_core_b, B, hipMemcpyDeviceToHost), "quantize D2H");
+}
+
+// bands >= max_bands read as 0; max_bands < 0 (or >= n_bands) reads every band
+extern "C" void sp_band_dequantize_partial(const uint8_t *in, float *out, const sp_band_config_t *bc, int max_bands) {
+    if (!in || !out || !bc) return;
+    std::lock_guard<std::mutex> lk(g_core_mu);
+    const size_t n = (size_t)bc->head_dim, B = (size_t)bc->total_bytes;
+    if (!core_stage(n, B) || !hip_ok(hipMemcpy(g_core_b, in, B, hipMemcpyHostToDevice), "dequantize H2D")) return;
+    sp_hip_band_dequantize(g_core_b, g_core_f, bc, 1, nullptr);
+    if (!hip_ok(hipMemcpy(out, g_core_f, n * sizeof(float), hipMemcpyDeviceToHost), "dequantize D2H")) return;
+    for (int b = (max_bands < 0 ? bc->n_bands : max_bands); b < bc->n_bands; b++) {
+        int off, sz;
+        sp_band_span(bc, b, &off, &sz);
+        for (int k = 0; k < sz; k++) out[off + k] = 0.0f;
+    }
+}
+
+extern "C" void sp_band_dequantize(const uint8_t *in, float *out, const sp_band_config_t *bc) {
+    sp_band_dequantize_partial(in, out, bc, -1);
+}
