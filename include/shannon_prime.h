@@ -128,6 +128,25 @@ void sp_shadow_read_k_batch(const sp_shadow_cache_t *sc, int layer, int head,
 void sp_shadow_read_v_batch(const sp_shadow_cache_t *sc, int layer, int head,
                             int start_pos, int n_pos, float *v_out);
 
+/* ---- Knight mask (sp_knight_mask_init / _free, shannon_prime_sqfree.cu:606-657):
+ *      skeleton = the first sk_k coefficients of `ranking` (NULL: the squarefree-first
+ *      order), residuals = the rest; CSR row r lists the skeleton slots of the proper
+ *      divisors d of n = residual_idx[r] + 1 with coefficient d - 1 in the skeleton
+ *      and mu(n/d) != 0, with sign mu(n/d). Host memory; _free releases it. ---- */
+typedef struct {
+    int     pad_dim;
+    int     sk_k;
+    int     n_res;
+    int     n_terms;
+    int    *skeleton_idx;   /* [sk_k] */
+    int    *residual_idx;   /* [n_res] */
+    int    *csr_offsets;    /* [n_res + 1] */
+    int    *csr_skel_slot;  /* [n_terms] */
+    int8_t *csr_mu_sign;    /* [n_terms] */
+} sp_knight_mask_t;
+int  sp_knight_mask_init(sp_knight_mask_t *m, int pad_dim, int sk_k, const int *ranking);
+void sp_knight_mask_free(sp_knight_mask_t *m);
+
 /* ---- per-vector core calls on host pointers (the absent core's sp_vht2_forward_f32,
  *      used at llama_sp_fused_kq.cpp:33 and kv_cache.cpp:399, and its band codec
  *      sp_band_quantize / sp_band_dequantize / _partial, semantics at

@@ -2546,3 +2546,40 @@ extern "C" void sp_band_dequantize_partial(const uint8_t *in, float *out, const 
 extern "C" void sp_band_dequantize(const uint8_t *in, float *out, const sp_band_config_t *bc) {
     sp_band_dequantize_partial(in, out, bc, -1);
 }
+
+// Knight mask tables on the host (sp_knight_mask_init / _free, called at
+// shannon_prime_sqfree.cu:606-657): the same tables the sqfree caches build.
+extern "C" int sp_knight_mask_init(sp_knight_mask_t *m, int pad_dim, int sk_k, const int *ranking) {
+    if (!m || pad_dim <= 0 || sk_k <= 0 || sk_k > pad_dim) { set_err("knight_mask_init: bad args"); return -1; }
+    memset(m, 0, sizeof(*m));
+    std::vector<int> skel, res, off, slot, mu;
+    build_knight(pad_dim, sk_k, skel, res, off, slot, mu, ranking);
+    const int nr = (int)res.size(), nt = (int)slot.size();
+    m->skeleton_idx = (int *)malloc(sizeof(int) * (size_t)sk_k);
+    m->residual_idx = (int *)malloc(sizeof(int) * (size_t)(nr > 0 ? nr : 1));
+    m->csr_offsets = (int *)malloc(sizeof(int) * (size_t)(nr + 1));
+    m->csr_skel_slot = (int *)malloc(sizeof(int) * (size_t)(nt > 0 ? nt : 1));
+    m->csr_mu_sign = (int8_t *)malloc((size_t)(nt > 0 ? nt : 1));
+    if (!m->skeleton_idx || !m->residual_idx || !m->csr_offsets || !m->csr_skel_slot || !m->csr_mu_sign) {
+        sp_knight_mask_free(m);
+        set_err("knight_mask_init: out of memory");
+        return -1;
+    }
+    std::copy(skel.begin(), skel.end(), m->skeleton_idx);
+    std::copy(res.begin(), res.end(), m->residual_idx);
+    std::copy(off.begin(), off.end(), m->csr_offsets);
+    std::copy(slot.begin(), slot.end(), m->csr_skel_slot);
+    for (int t = 0; t < nt; t++) m->csr_mu_sign[t] = (int8_t)mu[(size_t)t];
+    m->pad_dim = pad_dim, m->sk_k = sk_k, m->n_res = nr, m->n_terms = nt;
+    return 0;
+}
+
+extern "C" void sp_knight_mask_free(sp_knight_mask_t *m) {
+    if (!m) return;
+    free(m->skeleton_idx);
+    free(m->residual_idx);
+    free(m->csr_offsets);
+    free(m->csr_skel_slot);
+    free(m->csr_mu_sign);
+    memset(m, 0, sizeof(*m));
+}

@@ -129,3 +129,28 @@ def test_cpp_kv_cache_header_compiles():
     r = subprocess.run(["g++", "-std=c++17", "-Wall", "-Wextra", "-Werror", "-fsyntax-only", "-x", "c++", "-I", inc,
                         "-"], input='#include "sp_kv_cache.hpp"\n', capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+class _Knight(C.Structure):
+    _fields_ = [("pad_dim", C.c_int), ("sk_k", C.c_int), ("n_res", C.c_int), ("n_terms", C.c_int),
+                ("skeleton_idx", C.POINTER(C.c_int)), ("residual_idx", C.POINTER(C.c_int)),
+                ("csr_offsets", C.POINTER(C.c_int)), ("csr_skel_slot", C.POINTER(C.c_int)),
+                ("csr_mu_sign", C.POINTER(C.c_int8))]
+
+
+@pytest.mark.parametrize("pad,sk", [(154, 77), (154, 115), (330, 165), (66, 1)])
+def test_knight_mask_matches_oracle(pad, sk):
+    """sp_knight_mask_init (host tables, no GPU) equals the oracle's Knight tables."""
+    L = S.lib()
+    m = _Knight()
+    assert L.sp_knight_mask_init(C.byref(m), pad, sk, None) == 0
+    ref = O.Knight(pad, sk)
+    assert (m.pad_dim, m.sk_k, m.n_res, m.n_terms) == (pad, sk, ref.n_res, ref.n_terms)
+    np.testing.assert_array_equal(np.ctypeslib.as_array(m.skeleton_idx, (sk,)), ref.skeleton_idx)
+    np.testing.assert_array_equal(np.ctypeslib.as_array(m.residual_idx, (m.n_res,)), ref.residual_idx)
+    np.testing.assert_array_equal(np.ctypeslib.as_array(m.csr_offsets, (m.n_res + 1,)), ref.csr_offsets)
+    if m.n_terms:
+        np.testing.assert_array_equal(np.ctypeslib.as_array(m.csr_skel_slot, (m.n_terms,)), ref.csr_skel_slot)
+        np.testing.assert_array_equal(np.ctypeslib.as_array(m.csr_mu_sign, (m.n_terms,)), ref.csr_mu_sign)
+    L.sp_knight_mask_free(C.byref(m))
+    assert L.sp_knight_mask_init(C.byref(m), pad, pad + 1, None) == -1
