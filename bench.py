@@ -377,7 +377,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the codec shards by layer or KV head with no exchange; see DESIGN.md)", file=sys.stderr)
+              "(the codec shards by layer or KV head with no exchange between GPUs)", file=sys.stderr)
         sys.exit(2)
 
     import torch
