@@ -3,6 +3,7 @@ oracle (CPU only, no compute calls on a GPU)."""
 import ctypes as C
 import os
 import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -154,3 +155,12 @@ def test_knight_mask_matches_oracle(pad, sk):
         np.testing.assert_array_equal(np.ctypeslib.as_array(m.csr_mu_sign, (m.n_terms,)), ref.csr_mu_sign)
     L.sp_knight_mask_free(C.byref(m))
     assert L.sp_knight_mask_init(C.byref(m), pad, pad + 1, None) == -1
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus 2 exits with status 2 and says so, before any GPU work."""
+    root = os.path.join(os.path.dirname(__file__), "..")
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=300, cwd=root)
+    assert r.returncode == 2, (r.returncode, r.stderr[-500:])
+    assert "one GPU" in r.stderr
