@@ -17,9 +17,11 @@
 //     (2h, 2h+1) of v_mfma_f32_16x16x32_f16 carry head h, ~22 bits together.
 //   * scores: lane (row, q4) of a 16-position tile takes a contiguous run of 8
 //     codes of every band from one 64-bit window of its record (the B operand
-//     uses the matching coefficient permutation); a shift/or/mask makes a code
-//     pair 1024 + u in fp16 and one packed subtract centres it (u - m_b,
-//     exact); per-position band scales are applied to the fp32 MFMA results.
+//     uses the matching coefficient permutation); a shift/multiply/mask puts a
+//     code pair at the top of two fp16 mantissas, 2^BITS + u (exact), and the
+//     MFMA accumulator starts at -(2^BITS + m_b) * sum(q~ over the band), which
+//     centres the codes; per-position band scales are applied to the fp32 MFMA
+//     results.
 //   * softmax over the chunk; w = p * scale_v is scaled per head by a power of
 //     two and split hi + lo the same way.
 //   * values in two halves: V codes are unpacked into a transposed byte tile
@@ -76,16 +78,31 @@ constexpr int BUF_NT = 2;                    // non-temporal load policy
 __device__ __forceinline__ constexpr int kbits(int b) { return b < 2 ? 5 : (b == 2 ? 4 : 3); }
 __device__ __forceinline__ constexpr int kbyte(int b) { return b == 0 ? 0 : b == 1 ? 22 : b == 2 ? 44 : 62; }
 
-// Code pairs as fp16 (1024 + u, exact): the MFMA accumulator starts at
-// -(1024 + m_b) * sum(B column over the band), which centres the codes.
-// Two adjacent BITS-bit codes at bit `off` of x: the 2*BITS-bit field times
-// (1 + 2^(16-BITS)) copies the second code to bit 16, the mask keeps both slots.
-// The mask and the 0x6400 bits arrive in registers (kmask, kbias) so one
-// three-input bit operation, (a & b) | c, finishes the pair.
+// Code pairs as fp16 2^BITS + u (exact): the code sits in the top BITS bits of
+// the mantissa under the exponent of 2^BITS. The MFMA accumulator starts at
+// -(2^BITS + m_b) * sum(B column over the band), which centres the codes. The
+// offset 2^BITS is kept as small as the format allows: the fp32 accumulator
+// holds (2^BITS + m_b) * sum|q~| before the centring cancels it, so each bit of
+// offset costs a bit of score precision.
+// Two adjacent BITS-bit codes y = c0 | c1 << BITS at bit `off` of x: y times
+// 2^(10-BITS) + 2^(26-2*BITS) puts c0 at bits [10-BITS, 10) and c1 at
+// [26-BITS, 26) (the other two copies land in disjoint fields, so nothing
+// carries), and the mask keeps those two. The mask and the exponent bits
+// arrive in registers (kmask, kbias) so one three-input bit operation,
+// (a & b) | c, finishes the pair.
+template <int BITS>
+__device__ __forceinline__ constexpr uint32_t code_mask() {
+    return (((1u << BITS) - 1u) << (10 - BITS)) * 0x10001u;
+}
+template <int BITS>
+__device__ __forceinline__ constexpr uint32_t code_bias() {
+    return ((uint32_t)(15 + BITS) << 10) * 0x10001u;  // fp16 2^BITS in both halves
+}
 template <int BITS>
 __device__ __forceinline__ uint32_t code_pair(uint32_t x, uint32_t off, uint32_t kmask, uint32_t kbias) {
     const uint32_t y = __builtin_amdgcn_ubfe(x, off, 2 * BITS);
-    return __builtin_amdgcn_bitop3_b32(y * (1u + (1u << (16 - BITS))), kmask, kbias, 0xEA);
+    return __builtin_amdgcn_bitop3_b32(y * ((1u << (10 - BITS)) + (1u << (26 - 2 * BITS))),
+                                       kmask, kbias, 0xEA);
 }
 
 __device__ __forceinline__ half8_t as_half8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
@@ -100,11 +117,11 @@ __device__ __forceinline__ half8_t as_half8(uint32_t a, uint32_t b, uint32_t c, 
 template <int BITS>
 __device__ __forceinline__ half8_t band_codes(uint32_t d0, uint32_t d1, uint32_t sh, uint32_t kmask, uint32_t kbias) {
     const uint32_t lo = __builtin_amdgcn_alignbit(d1, d0, sh);  // window bits 0..31
-    if (BITS == 4)
-        return as_half8(__builtin_amdgcn_bitop3_b32(lo, kmask, kbias, 0xEA),
-                        __builtin_amdgcn_bitop3_b32(lo >> 4, kmask, kbias, 0xEA),
-                        __builtin_amdgcn_bitop3_b32(lo >> 8, kmask, kbias, 0xEA),
-                        __builtin_amdgcn_bitop3_b32(lo >> 12, kmask, kbias, 0xEA));
+    if (BITS == 4)  // codes k and k + 4 (bits 4k, 4k + 16) move to bits 6..9 and 22..25
+        return as_half8(__builtin_amdgcn_bitop3_b32(lo << 6, kmask, kbias, 0xEA),
+                        __builtin_amdgcn_bitop3_b32(lo << 2, kmask, kbias, 0xEA),
+                        __builtin_amdgcn_bitop3_b32(lo >> 2, kmask, kbias, 0xEA),
+                        __builtin_amdgcn_bitop3_b32(lo >> 6, kmask, kbias, 0xEA));
     uint32_t p67;
     if (BITS == 5) p67 = code_pair<5>(__builtin_amdgcn_alignbit(d1 >> sh, lo, 30), 0, kmask, kbias);  // bits 30..39
     else p67 = code_pair<BITS>(lo, 6 * BITS, kmask, kbias);
@@ -261,7 +278,7 @@ k_attn_mfma_split(const SpAttnArgs A, const int *__restrict__ order, float *__re
     // the query operand rows 2h (hi) and 2h + 1 (lo) in LDS, laid out so lane
     // (c16, q4) of the score MFMA reads the 8 slots of band b as one 16-byte word
     // at (4b + q4) * 8 (record coefficient k = 32b + 8*q4 + c). Also per (row,
-    // band) -(1024 + m_b) * sum of the row's slots: the MFMA accumulator start. ----
+    // band) -(2^BITS + m_b) * sum of the row's slots: the MFMA accumulator start. ----
 #pragma unroll
     for (int r = 0; r < 2; r++) {
         const int h = w + 4 * r;
@@ -315,8 +332,8 @@ k_attn_mfma_split(const SpAttnArgs A, const int *__restrict__ order, float *__re
         sha = wave_sum_step<16>(sha); sla = wave_sum_step<16>(sla); shb = wave_sum_step<16>(shb); slb = wave_sum_step<16>(slb);
         if ((lane & 31) == 0) {
             const int ba = lane >> 5, bb = 2 + (lane >> 5);
-            const float ca = -(1024.0f + (float)((1 << (kbits(ba) - 1)) - 1));  // bands 0, 1: 5 bits
-            const float cbb = -(1024.0f + (float)((1 << (kbits(bb) - 1)) - 1));
+            const float ca = -(float)((1 << kbits(ba)) + (1 << (kbits(ba) - 1)) - 1);  // -(2^BITS + m_b)
+            const float cbb = -(float)((1 << kbits(bb)) + (1 << (kbits(bb) - 1)) - 1);
             cb[ba * 16 + 2 * h] = ca * sha;
             cb[ba * 16 + 2 * h + 1] = ca * sla;
             cb[bb * 16 + 2 * h] = cbb * shb;
@@ -344,9 +361,11 @@ k_attn_mfma_split(const SpAttnArgs A, const int *__restrict__ order, float *__re
         wofs[b] = 4 * (p >> 5);
         wsh[b] = p & 31;
     }
-    // code-slot masks and the fp16 1024 bits, kept in registers for bitop3
-    const uint32_t kbias = __builtin_amdgcn_readfirstlane(0x64006400u);
-    uint32_t kmask5 = 0x001f001fu, kmask4 = 0x000f000fu, kmask3 = 0x00070007u;
+    // code-slot masks and the fp16 2^BITS exponent bits, kept in registers for bitop3
+    const uint32_t kbias5 = __builtin_amdgcn_readfirstlane(code_bias<5>());
+    const uint32_t kbias4 = __builtin_amdgcn_readfirstlane(code_bias<4>());
+    const uint32_t kbias3 = __builtin_amdgcn_readfirstlane(code_bias<3>());
+    uint32_t kmask5 = code_mask<5>(), kmask4 = code_mask<4>(), kmask3 = code_mask<3>();
     __asm__("" : "+v"(kmask5), "+v"(kmask4), "+v"(kmask3));
 
     // running softmax state of this lane's heads 2*q4 + hh over the block's rounds
@@ -400,9 +419,9 @@ k_attn_mfma_split(const SpAttnArgs A, const int *__restrict__ order, float *__re
                 const uint32_t d0 = *reinterpret_cast<const uint32_t *>(rec + wofs[b]);
                 const uint32_t d1 = *reinterpret_cast<const uint32_t *>(rec + wofs[b] + 4);
                 half8_t code;
-                if (b < 2) code = band_codes<5>(d0, d1, wsh[b], kmask5, kbias);
-                else if (b == 2) code = band_codes<4>(d0, d1, wsh[b], kmask4, kbias);
-                else code = band_codes<3>(d0, d1, wsh[b], kmask3, kbias);
+                if (b < 2) code = band_codes<5>(d0, d1, wsh[b], kmask5, kbias5);
+                else if (b == 2) code = band_codes<4>(d0, d1, wsh[b], kmask4, kbias4);
+                else code = band_codes<3>(d0, d1, wsh[b], kmask3, kbias3);
                 const float4_t d = __builtin_amdgcn_mfma_f32_16x16x32_f16(qop[b], code, cinit[b], 0, 0, 0);
                 acc0 = fmaf(sb[b], d[0] + d[1], acc0);  // hi + lo rows of head hq0
                 acc1 = fmaf(sb[b], d[2] + d[3], acc1);

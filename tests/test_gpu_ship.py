@@ -150,6 +150,42 @@ def test_codes_at_rounding_ties():
     cc.free()
 
 
+@pytest.mark.parametrize("n_pos", [65536, 40001])
+def test_multi_tile_blocks_bit_exact(n_pos):
+    """Layer-wide calls large enough that every persistent block walks more than one
+    64-vector tile (the grid is 16 single-wave blocks per CU, 4096 on MI355X):
+    8 heads x 65536 positions are 8192 tiles, two per block, with the next tile's
+    inputs prefetched across the tile boundary; 40001 positions give 626 tiles per
+    head (the last one a single vector), so blocks walk one or two tiles and some
+    tiles straddle nothing but a one-vector tail. K and V encode through write_all,
+    both decodes through read_all (fp16), every code and every reconstructed value
+    against the oracle."""
+    H, hd = 8, 128
+    say(f"multi-tile codec H={H} n_pos={n_pos}")
+    k16, v16 = W.cfg2_kv(n_heads=H, n_pos=n_pos, hd=hd, seed=n_pos)
+    cc = S.ShipCache(S.config(hd, 1, H), n_pos, stream=torch.cuda.current_stream().cuda_stream)
+    L = S.lib()
+    kt = dev(k16.reshape(H * n_pos, hd).view(np.uint16))
+    vt = dev(v16.reshape(H * n_pos, hd).view(np.uint16))
+    S.check(L.sp_hip_write_all(cc.ref, 0, n_pos, p(kt), p(vt), S.DTYPE_F16), "write_all")
+    del kt, vt
+    order = O.mobius_order(hd)
+    kbc, vbc = O.band_config(hd, [5, 5, 4, 3]), O.band_config(hd, [3])
+    kref = O.ship_compress_f16(k16.reshape(-1, hd).view(np.uint16), kbc, order)
+    vref = O.ship_compress_f16(v16.reshape(-1, hd).view(np.uint16), vbc)
+    kc = d2h(cc.c.d_k_cache, kref.size).reshape(kref.shape)
+    vc = d2h(cc.c.d_v_cache, vref.size).reshape(vref.shape)
+    np.testing.assert_array_equal(kc, kref, err_msg="K codes")
+    np.testing.assert_array_equal(vc, vref, err_msg="V codes")
+    ko, vo = empty_f16(H * n_pos * hd), empty_f16(H * n_pos * hd)
+    S.check(L.sp_hip_read_all(cc.ref, 0, n_pos, p(ko), p(vo), S.DTYPE_F16, -1), "read_all")
+    np.testing.assert_array_equal(host(ko, np.uint16).reshape(-1, hd), O.ship_decompress_f16(kref, kbc, order),
+                                  err_msg="K reconstruction")
+    np.testing.assert_array_equal(host(vo, np.uint16).reshape(-1, hd), O.ship_decompress_f16(vref, vbc),
+                                  err_msg="V reconstruction")
+    cc.free()
+
+
 @pytest.mark.parametrize("strided", [False, True])
 def test_cache_hd96_vilenkin(strided):
     """hd 96 (Vilenkin 2^5*3) with the bridge defaults K 5/4/4 + Mobius and V 5 through
