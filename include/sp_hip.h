@@ -189,6 +189,22 @@ int sp_hip_attn_decode_bands(const sp_hip_cache_t *cc, int layer, int n_kv,
                              const float *d_q, int n_q, float kq_scale,
                              float *d_scores, float *d_out, int max_bands, void *stream);
 
+/* sp_hip_attn_decode_bands with no allocation. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, allocation-free serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, checks and results as sp_hip_attn_decode_bands; the
+ * attention workspace comes from a fixed per-GPU device array of
+ * sp_hip_attn_noalloc_max_floats() floats (16 MiB, held until the process
+ * ends) instead of the cache's workspace, and the call makes no hipMalloc /
+ * hipFree. Returns -1 when the call needs more than that
+ * (n_q*head_dim + n_q*ceil(n_kv/256)*(head_dim + 2) floats: at head_dim 128 and
+ * 32 query heads up to 128K positions) or when `stream` is not on the current
+ * device. Calls that overlap on one GPU share the array and race. */
+int sp_hip_attn_decode_bands_noalloc(const sp_hip_cache_t *cc, int layer, int n_kv,
+                                     const float *d_q, int n_q, float kq_scale,
+                                     float *d_scores, float *d_out, int max_bands, void *stream);
+size_t sp_hip_attn_noalloc_max_floats(void);
+
 /* Memory report to stderr (sp_cuda_print_memory, shannon_prime_cuda.h:140-141): the
  * records' MiB against an fp16 K+V cache of the same shape. */
 void sp_hip_print_memory(const sp_hip_cache_t *cc);

@@ -6,6 +6,7 @@
 
 #include "sp_device.h"
 #include "../../include/shannon_prime.h"
+#include "../../include/sp_hip.h"
 
 #define SP_DT_F32 0
 #define SP_DT_F16 1
@@ -277,6 +278,14 @@ hipError_t sp_launch_attn_decode(const SpPlan &KP, const SpPlan &VP, const int *
                                  const SpAttnArgs &A, float *workspace, size_t ws_floats,
                                  hipStream_t s);
 size_t sp_attn_workspace_floats(int n_q, int hd, int max_kv);
+// Checks the arguments of a decode-attention call on one layer of a ship cache
+// and fills its launch arguments and K/V plans (band limit applied); -1 with the
+// error message set for bad arguments (sp_runtime.cpp).
+int sp_attn_prepare(const sp_hip_cache_t *cc, int layer, int n_kv, const float *d_q, int n_q, float kq_scale,
+                    float *d_scores, float *d_out, int max_bands, SpAttnArgs *out_args, SpPlan *out_kp,
+                    SpPlan *out_vp);
+// Sets the message sp_hip_last_error() returns (sp_runtime.cpp).
+void sp_set_error(const char *fmt, ...);
 // Split kernel on the matrix cores for head_dim 128 with K 5/5/4/3 and V 3-bit;
 // hipErrorNotSupported for any other layout. With an output it writes *n_parts
 // natural-domain partials [m, l, o[hd]] per query head (merged by k_attn_merge).

@@ -26,12 +26,24 @@
 // ===========================================================================
 static thread_local char g_err[512];
 
+static void set_err_v(const char *fmt, va_list ap) {
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    if (getenv("SHANNON_PRIME_VERBOSE")) fprintf(stderr, "[Shannon-Prime HIP] %s\n", g_err);
+}
+
 static void set_err(const char *fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
-    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    set_err_v(fmt, ap);
     va_end(ap);
-    if (getenv("SHANNON_PRIME_VERBOSE")) fprintf(stderr, "[Shannon-Prime HIP] %s\n", g_err);
+}
+
+// The same message slot for the library's other source files.
+void sp_set_error(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    set_err_v(fmt, ap);
+    va_end(ap);
 }
 
 static bool hip_ok(hipError_t e, const char *what) {
@@ -814,12 +826,13 @@ extern "C" int sp_hip_read_all(const sp_hip_cache_t *cc, int start_pos, int n_po
 // ===========================================================================
 // fused attention
 // ===========================================================================
-extern "C" int sp_hip_attn_decode_bands(const sp_hip_cache_t *cc, int layer, int n_kv, const float *d_q, int n_q,
-                                        float kq_scale, float *d_scores, float *d_out, int max_bands, void *stream) {
+// Launch arguments of one layer's decode attention over the cache's records.
+int sp_attn_prepare(const sp_hip_cache_t *cc, int layer, int n_kv, const float *d_q, int n_q, float kq_scale,
+                    float *d_scores, float *d_out, int max_bands, SpAttnArgs *out_args, SpPlan *out_kp,
+                    SpPlan *out_vp) {
     if (!cc || !cc->priv || layer < 0 || layer >= cc->config.n_layers || n_kv <= 0 ||
         n_kv > cc->max_seq_len || !d_q || n_q <= 0) { set_err("attn: bad args"); return -1; }
     ShipPriv *pv = (ShipPriv *)cc->priv;
-    if (n_q > pv->max_q) { set_err("attn: n_q %d > %d", n_q, pv->max_q); return -1; }
     SpAttnArgs A;
     const int H = cc->config.n_heads_kv;
     A.kB = cc->k_bands.total_bytes;
@@ -841,6 +854,19 @@ extern "C" int sp_hip_attn_decode_bands(const sp_hip_cache_t *cc, int layer, int
         if (max_bands < kp.n_bands) kp.max_bands = max_bands;
         if (max_bands < vp.n_bands) vp.max_bands = max_bands;
     }
+    *out_args = A;
+    *out_kp = kp;
+    *out_vp = vp;
+    return 0;
+}
+
+extern "C" int sp_hip_attn_decode_bands(const sp_hip_cache_t *cc, int layer, int n_kv, const float *d_q, int n_q,
+                                        float kq_scale, float *d_scores, float *d_out, int max_bands, void *stream) {
+    SpAttnArgs A;
+    SpPlan kp, vp;
+    if (sp_attn_prepare(cc, layer, n_kv, d_q, n_q, kq_scale, d_scores, d_out, max_bands, &A, &kp, &vp)) return -1;
+    ShipPriv *pv = (ShipPriv *)cc->priv;
+    if (n_q > pv->max_q) { set_err("attn: n_q %d > %d", n_q, pv->max_q); return -1; }
     return hip_ok(sp_launch_attn_decode(kp, vp, cc->d_mobius_order, A, pv->ws, pv->ws_floats,
                                         (hipStream_t)(stream ? stream : cc->stream)),
                   "attn launch") ? 0 : -1;

@@ -125,6 +125,7 @@ def lib():
         L = C.CDLL(LIB_PATH)
         vp, i, f, ll = C.c_void_p, C.c_int, C.c_float, C.c_longlong
         L.sp_hip_last_error.restype = C.c_char_p
+        L.sp_hip_attn_noalloc_max_floats.restype = C.c_size_t
         L.sp_hip_event_create.restype = vp
         L.sp_hip_event_elapsed_ms.restype = f
         L.sp_hip_event_elapsed_ms.argtypes = [vp, vp]
