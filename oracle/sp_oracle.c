@@ -525,7 +525,7 @@ int spo_sqfree_bytes(const spo_band_config_t *skel_bc, int n_res, int rbits, int
 
 /* LSB-first bit packing of small levels (kernel_pack_levels,
  * shannon_prime_sqfree.cu:552-564). */
-static void pack_levels(const uint8_t *lv, int n, int bits, uint8_t *out) {
+void spo_pack_levels(const uint8_t *lv, int n, int bits, uint8_t *out) {
     int nb = (n * bits + 7) / 8;
     memset(out, 0, (size_t)nb);
     for (int i = 0; i < n; i++) {
@@ -535,7 +535,8 @@ static void pack_levels(const uint8_t *lv, int n, int bits, uint8_t *out) {
     }
 }
 
-static void unpack_levels(const uint8_t *in, int n, int bits, uint8_t *lv) {
+/* kernel_unpack_levels, shannon_prime_sqfree.cu:567-579. */
+void spo_unpack_levels(const uint8_t *in, int n, int bits, uint8_t *lv) {
     int nb = (n * bits + 7) / 8;
     uint32_t mask = (1u << bits) - 1u;
     for (int i = 0; i < n; i++) {
@@ -562,13 +563,59 @@ static float mean_abs_floor(const float *dev, int n) {
 
 /* CSR Mobius prediction: pred[r] = sum_j (float)mu[j] * skel[slot[j]], from
  * 0.0f in CSR order (kernel_mobius_predict, shannon_prime_sqfree.cu:179-203). */
-static void mobius_predict(const float *skel, const spo_knight_mask_t *m, float *pred) {
+void spo_mobius_predict(const float *skel, const spo_knight_mask_t *m, float *pred) {
     for (int r = 0; r < m->n_res; r++) {
         float p = 0.0f;
         for (int j = m->csr_offsets[r]; j < m->csr_offsets[r + 1]; j++)
             p += (float)m->csr_mu_sign[j] * skel[m->csr_skel_slot[j]];
         pred[r] = p;
     }
+}
+
+/* Spinor sheet choice (kernel_spinor_extract, shannon_prime_sqfree.cu:212-240):
+ * v+ = a - p, v- = a + p; the sheet bit is 1 iff |v-| < |v+| (strict, so a tie
+ * keeps v+ and bit 0); dev = the winner; bits LSB-first, sheet zeroed first. */
+void spo_spinor_extract(const float *a, const float *p, int n, float *dev, uint8_t *sheet) {
+    memset(sheet, 0, (size_t)((n + 7) / 8));
+    for (int r = 0; r < n; r++) {
+        float vp = a[r] - p[r], vm = a[r] + p[r];
+        int use_minus = fabsf(vm) < fabsf(vp);
+        dev[r] = use_minus ? vm : vp;
+        if (use_minus) sheet[r / 8] |= (uint8_t)(1u << (r % 8));
+    }
+}
+
+/* Sqfree residual quantizer (kernel_mean_abs + kernel_quantize_residual,
+ * shannon_prime_sqfree.cu:493-532): mag = max(tree-256 sum of |dev| / n, 1e-12);
+ * L = 2^bits, center = (L-1)/2, sat = mag*bits (1e-12 when mag is at the floor),
+ * step = 2*sat/(L-1), level = (int)(dev*(1/step) + center + 0.5) (truncation),
+ * clamped to [0, L-1]. Returns the mag the record stores. */
+float spo_sqfree_residual_quantize(const float *dev, int n, int bits, uint8_t *lv) {
+    float mag = mean_abs_floor(dev, n);
+    int L = 1 << bits;
+    float center = 0.5f * (float)(L - 1);
+    float sat = (mag > 1e-12f) ? (mag * (float)bits) : 1e-12f;
+    float step = (2.0f * sat) / (float)(L - 1);
+    float inv_step = 1.0f / step;
+    for (int r = 0; r < n; r++) {
+        float qf = dev[r] * inv_step + center;
+        int level = trunc_sat(qf + 0.5f);
+        if (level < 0) level = 0;
+        if (level >= L) level = L - 1;
+        lv[r] = (uint8_t)level;
+    }
+    return mag;
+}
+
+/* Sqfree residual dequantizer (kernel_dequantize_residual,
+ * shannon_prime_sqfree.cu:535-548): step = 2*mag*bits/(L-1) (no floor test),
+ * dev = (level - center) * step. */
+void spo_sqfree_residual_dequantize(const uint8_t *lv, int n, int bits, float mag, float *dev) {
+    int L = 1 << bits;
+    float center = 0.5f * (float)(L - 1);
+    float sat = mag * (float)bits;
+    float step = (L > 1) ? (2.0f * sat / (float)(L - 1)) : 0.0f;
+    for (int r = 0; r < n; r++) dev[r] = ((float)lv[r] - center) * step;
 }
 
 /* Sqfree write (sp_cuda_sqfree_write_one, shannon_prime_sqfree.cu:750-853):
@@ -589,36 +636,19 @@ void spo_sqfree_compress(const float *vec, uint8_t *out, int hd, const spo_knigh
     for (int s = 0; s < sk; s++) skel[s] = c[m->skeleton_idx[s]];
     spo_band_quantize(skel, out, skel_bc);
     if (nr == 0) return;
-    mobius_predict(skel, m, pred);
+    spo_mobius_predict(skel, m, pred);
     int res_bytes = (nr * rbits + 7) / 8;
     uint8_t *sheet = out + skel_bc->total_bytes + 4 + res_bytes;
-    if (spinor) memset(sheet, 0, (size_t)((nr + 7) / 8));
-    for (int r = 0; r < nr; r++) {
-        float a = c[m->residual_idx[r]], p = pred[r];
-        if (spinor) {
-            float vp = a - p, vm = a + p;
-            int use_minus = fabsf(vm) < fabsf(vp);  /* strict (:231) */
-            dev[r] = use_minus ? vm : vp;
-            if (use_minus) sheet[r / 8] |= (uint8_t)(1u << (r % 8));
-        } else {
-            dev[r] = a - p;
-        }
+    float act[1024];
+    for (int r = 0; r < nr; r++) act[r] = c[m->residual_idx[r]];
+    if (spinor) {
+        spo_spinor_extract(act, pred, nr, dev, sheet);
+    } else {
+        for (int r = 0; r < nr; r++) dev[r] = act[r] - pred[r];
     }
-    float mag = mean_abs_floor(dev, nr);
+    float mag = spo_sqfree_residual_quantize(dev, nr, rbits, lv);
     memcpy(out + skel_bc->total_bytes, &mag, 4);
-    int L = 1 << rbits;
-    float center = 0.5f * (float)(L - 1);
-    float sat = (mag > 1e-12f) ? (mag * (float)rbits) : 1e-12f;
-    float step = (2.0f * sat) / (float)(L - 1);
-    float inv_step = 1.0f / step;
-    for (int r = 0; r < nr; r++) {
-        float qf = dev[r] * inv_step + center;
-        int level = trunc_sat(qf + 0.5f);
-        if (level < 0) level = 0;
-        if (level >= L) level = L - 1;
-        lv[r] = (uint8_t)level;
-    }
-    pack_levels(lv, nr, rbits, out + skel_bc->total_bytes + 4);
+    spo_pack_levels(lv, nr, rbits, out + skel_bc->total_bytes + 4);
 }
 
 /* Sqfree read (sp_cuda_sqfree_read_one, shannon_prime_sqfree.cu:857-950):
@@ -636,21 +666,18 @@ void spo_sqfree_decompress(const uint8_t *in, float *out, int hd, const spo_knig
     for (int i = 0; i < pd; i++) c[i] = 0.0f;
     for (int s = 0; s < sk; s++) c[m->skeleton_idx[s]] = skel[s];
     if (nr > 0) {
-        mobius_predict(skel, m, pred);
+        spo_mobius_predict(skel, m, pred);
         float mag;
         memcpy(&mag, in + skel_bc->total_bytes, 4);
         int res_bytes = (nr * rbits + 7) / 8;
-        unpack_levels(in + skel_bc->total_bytes + 4, nr, rbits, lv);
-        int L = 1 << rbits;
-        float center = 0.5f * (float)(L - 1);
-        float sat = mag * (float)rbits;
-        float step = (L > 1) ? (2.0f * sat / (float)(L - 1)) : 0.0f;
+        spo_unpack_levels(in + skel_bc->total_bytes + 4, nr, rbits, lv);
+        float dv[1024];
+        spo_sqfree_residual_dequantize(lv, nr, rbits, mag, dv);
         const uint8_t *sheet = in + skel_bc->total_bytes + 4 + res_bytes;
         for (int r = 0; r < nr; r++) {
             float p = pred[r];
-            if (spinor && (sheet[r / 8] & (1u << (r % 8)))) p = -p;
-            float d = ((float)lv[r] - center) * step;
-            c[m->residual_idx[r]] = p + d;
+            if (spinor && (sheet[r / 8] & (1u << (r % 8)))) p = -p;  /* kernel_spinor_reconstruct :249-283 */
+            c[m->residual_idx[r]] = p + dv[r];
         }
     }
     spo_vilenkin(c, pd, f, nf);
@@ -706,12 +733,42 @@ int spo_hier_bytes(const spo_band_config_t *skel_bc, int n_target, int rbits) {
 
 /* pred[t] = sum_s (float)W[t][s] * skel[s] from 0.0f (kernel_hier_predict,
  * shannon_prime_hier.cu:74-92). */
-static void hier_predict(const uint16_t *W, const float *skel, float *pred, int nt, int ns) {
+void spo_hier_predict(const uint16_t *W, const float *skel, float *pred, int nt, int ns) {
     for (int t = 0; t < nt; t++) {
         float acc = 0.0f;
         for (int s = 0; s < ns; s++) acc += spo_f16_to_f32(W[(size_t)t * ns + s]) * skel[s];
         pred[t] = acc;
     }
+}
+
+/* Hier residual quantizer (kernel_residual_magnitude + kernel_quantize_residual,
+ * shannon_prime_hier.cu:115-171): m = max(tree-256 sum of |dev| / n, 1e-12);
+ * L = 2^bits, step = 2*m/(L-1), center = (L-1)/2, inv_step = 1/step (0 if step
+ * is 0), level = rint(dev*inv_step + center) (__float2int_rn: half to even),
+ * clamped to [0, L-1]. Returns the stored m. */
+float spo_hier_residual_quantize(const float *dev, int n, int bits, uint8_t *lv) {
+    float mag = mean_abs_floor(dev, n);
+    int L = 1 << bits;
+    float step = 2.0f * mag / (float)(L - 1);
+    float center = (float)(L - 1) / 2.0f;
+    float inv_step = (step > 0.0f) ? 1.0f / step : 0.0f;
+    for (int t = 0; t < n; t++) {
+        float v = rintf(dev[t] * inv_step + center);
+        int q = (v != v) ? 0 : (v >= 2147483647.0f ? 2147483647 : (v <= -2147483648.0f ? (-2147483647 - 1) : (int)v));
+        if (q < 0) q = 0;
+        if (q >= L) q = L - 1;
+        lv[t] = (uint8_t)q;
+    }
+    return mag;
+}
+
+/* Hier residual dequantizer (kernel_dequantize_residual, shannon_prime_hier.cu:177-193):
+ * dev = (level - center) * (2*m/(L-1)). */
+void spo_hier_residual_dequantize(const uint8_t *lv, int n, int bits, float mag, float *dev) {
+    int L = 1 << bits;
+    float step = 2.0f * mag / (float)(L - 1);
+    float center = (float)(L - 1) / 2.0f;
+    for (int t = 0; t < n; t++) dev[t] = ((float)lv[t] - center) * step;
 }
 
 /* Hier write (sp_cuda_hier_write_one, shannon_prime_hier.cu:399-486):
@@ -729,22 +786,11 @@ void spo_hier_compress(const float *vec, uint8_t *out, int hd, int pad,
     spo_vilenkin(c, pad, f, nf);
     for (int s = 0; s < n_skel; s++) skel[s] = c[skel_idx[s]];
     spo_band_quantize(skel, out, skel_bc);
-    hier_predict(W, skel, pred, n_target, n_skel);
+    spo_hier_predict(W, skel, pred, n_target, n_skel);
     for (int t = 0; t < n_target; t++) dev[t] = c[target_idx[t]] - pred[t];
-    float mag = mean_abs_floor(dev, n_target);
+    float mag = spo_hier_residual_quantize(dev, n_target, rbits, lv);
     memcpy(out + skel_bc->total_bytes, &mag, 4);
-    int L = 1 << rbits;
-    float step = 2.0f * mag / (float)(L - 1);
-    float center = (float)(L - 1) / 2.0f;
-    float inv_step = (step > 0.0f) ? 1.0f / step : 0.0f;
-    for (int t = 0; t < n_target; t++) {
-        float v = rintf(dev[t] * inv_step + center);
-        int q = (v != v) ? 0 : (v >= 2147483647.0f ? 2147483647 : (v <= -2147483648.0f ? (-2147483647 - 1) : (int)v));
-        if (q < 0) q = 0;
-        if (q >= L) q = L - 1;
-        lv[t] = (uint8_t)q;
-    }
-    pack_levels(lv, n_target, rbits, out + skel_bc->total_bytes + 4);
+    spo_pack_levels(lv, n_target, rbits, out + skel_bc->total_bytes + 4);
 }
 
 /* Hier read (sp_cuda_hier_read_one, shannon_prime_hier.cu:490-571). */
@@ -756,16 +802,15 @@ void spo_hier_decompress(const uint8_t *in, float *out, int hd, int pad,
     int f[16];
     int nf = spo_factor_small(pad, f, 16);
     spo_band_dequantize(in, skel, skel_bc);
-    hier_predict(W, skel, pred, n_target, n_skel);
+    spo_hier_predict(W, skel, pred, n_target, n_skel);
     float mag;
     memcpy(&mag, in + skel_bc->total_bytes, 4);
-    unpack_levels(in + skel_bc->total_bytes + 4, n_target, rbits, lv);
-    int L = 1 << rbits;
-    float step = 2.0f * mag / (float)(L - 1);
-    float center = (float)(L - 1) / 2.0f;
+    spo_unpack_levels(in + skel_bc->total_bytes + 4, n_target, rbits, lv);
+    float dv[1024];
+    spo_hier_residual_dequantize(lv, n_target, rbits, mag, dv);
     for (int i = 0; i < pad; i++) c[i] = 0.0f;
     for (int s = 0; s < n_skel; s++) c[skel_idx[s]] = skel[s];
-    for (int t = 0; t < n_target; t++) c[target_idx[t]] = pred[t] + ((float)lv[t] - center) * step;
+    for (int t = 0; t < n_target; t++) c[target_idx[t]] = pred[t] + dv[t];
     spo_vilenkin(c, pad, f, nf);
     for (int i = 0; i < hd; i++) out[i] = c[i];
 }

@@ -28,11 +28,20 @@
  *     band, amax=0, LSB-first packing known answers, brute-force minimality
  *     of the code (rint of x/scale).
  *   - fidelity: K corr > 0.985, V corr > 0.95 at hd=128 (test_adreno log).
- *   - Mobius order, Knight skeleton/CSR construction, hier geometry: the
- *     construction rules are NOT pinned by the reference (the builder lives
- *     in the absent core); they are host-side index tables and the kernels'
- *     parity does not depend on how they are built ("parity unpinned" for
- *     the table construction only).
+ *   - sqfree / spinor / hier: every stage (pad mean, residual quantizers and
+ *     dequantizers, spinor choice, level packing, CSR and W.skel predictions)
+ *     and every whole record are compared with an independent numpy
+ *     restatement of the reference's CUDA text (tests/np_restate.py,
+ *     tests/test_oracle_variants.py) on inputs where the plausible misreadings
+ *     differ: round-half-up vs rint, sat = mag*bits vs mag, the 1e-12 floor,
+ *     the strict spinor comparison, the serial predictor order, the 256-slot
+ *     reduction order; mu(n) against known values and the Mertens function;
+ *     the Knight CSR against a brute-force divisor enumeration.
+ *   - Mobius order, Knight skeleton/CSR construction rule, hier geometry: the
+ *     construction rules are NOT fixed by the reference (the builder lives in
+ *     the absent core); they are host-side index tables, the tests pin this
+ *     build's stated rule, and the kernels' parity does not depend on how the
+ *     tables are built ("parity unpinned" for the choice of rule only).
  */
 #ifndef SP_ORACLE_H
 #define SP_ORACLE_H
@@ -130,6 +139,13 @@ typedef struct {
 int  spo_knight_mask_init(spo_knight_mask_t *m, int pad_dim, int sk_k);
 void spo_knight_mask_free(spo_knight_mask_t *m);
 void spo_sqfree_pad(const float *in, float *out, int hd, int pad);
+/* stages of the sqfree write/read, each pinned on its own */
+void  spo_pack_levels(const uint8_t *lv, int n, int bits, uint8_t *out);
+void  spo_unpack_levels(const uint8_t *in, int n, int bits, uint8_t *lv);
+void  spo_mobius_predict(const float *skel, const spo_knight_mask_t *m, float *pred);
+void  spo_spinor_extract(const float *a, const float *p, int n, float *dev, uint8_t *sheet);
+float spo_sqfree_residual_quantize(const float *dev, int n, int bits, uint8_t *lv);
+void  spo_sqfree_residual_dequantize(const uint8_t *lv, int n, int bits, float mag, float *dev);
 int  spo_sqfree_bytes(const spo_band_config_t *skel_bc, int n_res, int rbits, int spinor);
 void spo_sqfree_compress(const float *vec, uint8_t *out, int hd, const spo_knight_mask_t *m,
                          const spo_band_config_t *skel_bc, int rbits, int spinor);
@@ -146,6 +162,10 @@ void spo_sqfree_decompress_batch_f32(const uint8_t *in, float *out, int n, int h
 void spo_hier_default_geometry(int pad, int *n_skel);
 void spo_hier_indices(int pad, int n_skel, int *skel_idx, int *target_idx);
 int  spo_hier_bytes(const spo_band_config_t *skel_bc, int n_target, int rbits);
+/* stages of the hier write/read, each pinned on its own */
+void  spo_hier_predict(const uint16_t *W, const float *skel, float *pred, int nt, int ns);
+float spo_hier_residual_quantize(const float *dev, int n, int bits, uint8_t *lv);
+void  spo_hier_residual_dequantize(const uint8_t *lv, int n, int bits, float mag, float *dev);
 void spo_hier_compress(const float *vec, uint8_t *out, int hd, int pad,
                        int n_skel, const int *skel_idx, int n_target, const int *target_idx,
                        const spo_band_config_t *skel_bc, const uint16_t *W, int rbits);

@@ -66,6 +66,10 @@ def lib():
         _lib.spo_inv_sqrt_n.restype = C.c_float
         _lib.spo_tree256_sum.restype = C.c_float
         _lib.spo_correlation_f32.restype = C.c_float
+        _lib.spo_sqfree_residual_quantize.restype = C.c_float
+        _lib.spo_sqfree_residual_dequantize.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_float, C.c_void_p]
+        _lib.spo_hier_residual_quantize.restype = C.c_float
+        _lib.spo_hier_residual_dequantize.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_float, C.c_void_p]
         _lib.spo_attn_decode.argtypes = [C.c_void_p] * 3 + [C.c_int] * 4 + [C.c_void_p] * 3 + \
             [C.c_int, C.c_float, C.c_void_p, C.c_void_p]
         _lib.spo_attn_decode_bands.argtypes = [C.c_void_p] * 3 + [C.c_int] * 4 + [C.c_void_p] * 3 + \
@@ -303,3 +307,76 @@ def correlation(a, b):
 def tree256_sum(v, take_abs=False):
     v = np.ascontiguousarray(v, dtype=np.float32)
     return lib().spo_tree256_sum(ptr(v), v.size, int(take_abs))
+
+
+# ---- individual stages of the sqfree / hier codecs ----
+
+def spinor_extract(a, p):
+    a = np.ascontiguousarray(a, np.float32)
+    p = np.ascontiguousarray(p, np.float32)
+    dev = np.zeros_like(a)
+    sheet = np.zeros((len(a) + 7) // 8, np.uint8)
+    lib().spo_spinor_extract(ptr(a), ptr(p), len(a), ptr(dev), ptr(sheet))
+    return dev, sheet
+
+
+def sqfree_residual_quantize(dev, bits):
+    dev = np.ascontiguousarray(dev, np.float32)
+    lv = np.zeros(len(dev), np.uint8)
+    mag = lib().spo_sqfree_residual_quantize(ptr(dev), len(dev), bits, ptr(lv))
+    return np.float32(mag), lv
+
+
+def sqfree_residual_dequantize(lv, bits, mag):
+    lv = np.ascontiguousarray(lv, np.uint8)
+    out = np.zeros(len(lv), np.float32)
+    lib().spo_sqfree_residual_dequantize(ptr(lv), len(lv), bits, C.c_float(mag), ptr(out))
+    return out
+
+
+def hier_residual_quantize(dev, bits):
+    dev = np.ascontiguousarray(dev, np.float32)
+    lv = np.zeros(len(dev), np.uint8)
+    mag = lib().spo_hier_residual_quantize(ptr(dev), len(dev), bits, ptr(lv))
+    return np.float32(mag), lv
+
+
+def hier_residual_dequantize(lv, bits, mag):
+    lv = np.ascontiguousarray(lv, np.uint8)
+    out = np.zeros(len(lv), np.float32)
+    lib().spo_hier_residual_dequantize(ptr(lv), len(lv), bits, C.c_float(mag), ptr(out))
+    return out
+
+
+def hier_predict(W16, skel):
+    W16 = np.ascontiguousarray(W16, np.uint16)
+    skel = np.ascontiguousarray(skel, np.float32)
+    out = np.zeros(W16.shape[0], np.float32)
+    lib().spo_hier_predict(ptr(W16), ptr(skel), ptr(out), W16.shape[0], W16.shape[1])
+    return out
+
+
+def mobius_predict(skel, km):
+    skel = np.ascontiguousarray(skel, np.float32)
+    out = np.zeros(max(km.n_res, 1), np.float32)
+    lib().spo_mobius_predict(ptr(skel), C.byref(km.m), ptr(out))
+    return out[:km.n_res]
+
+
+def pack_levels(lv, bits):
+    lv = np.ascontiguousarray(lv, np.uint8)
+    out = np.zeros((len(lv) * bits + 7) // 8, np.uint8)
+    lib().spo_pack_levels(ptr(lv), len(lv), bits, ptr(out))
+    return out
+
+
+def sqfree_pad(x, hd, pad):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros(pad, np.float32)
+    lib().spo_sqfree_pad(ptr(x), ptr(out), hd, pad)
+    return out
+
+
+def vilenkin(x):
+    """Forward Vilenkin / VHT2 of one vector (the oracle's dispatch)."""
+    return vht2(x)
