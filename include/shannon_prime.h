@@ -185,6 +185,101 @@ uint16_t sp_f32_to_f16(float f);
 /* ---- sqfree geometry (sp_sqfree_pad_dim: shannon_prime_sqfree.cu:600) ---- */
 int sp_sqfree_pad_dim(int head_dim);
 
+/* ---- sqfree + spinor cache on host vectors: the absent core's sp_sqfree_cache_t,
+ * as the b8861 hook calls it (llama-cpp-b8861-full-engine.patch:790-791 init,
+ * :851/:866 free, :1206-1207 K and :1274-1275, :1333-1334 V write/read round
+ * trips), the sqfree bridge (shannon_prime_llama_sqfree.c:145-240) and the
+ * engine (kv_cache.cpp:337-346, 523, 549, 608, 1547, 1570). The records live in
+ * HBM in a device cache the library owns (sp_hip_sqfree_cache_t); each call
+ * stages its vector through pinned host memory and runs the device kernels, so
+ * records and reconstructions equal the device cache's bit for bit. A GPU is
+ * required: init returns -1 without one. Skeleton = pad_dim / 2 as in the
+ * reference's sqfree cache (shannon_prime_sqfree.cu:606); K bands over the
+ * skeleton from cfg->k_band_bits (default 5,4,4,4,5), V from cfg->v_band_bits.
+ * Record [skeleton bands][f32 mag][residual][sheet] (shannon_prime_sqfree.cu:683-686). */
+typedef struct {
+    sp_config_t      config;
+    int              pad_dim;
+    sp_knight_mask_t mask;          /* host copy of the tables the device uses */
+    sp_band_config_t k_bands;       /* over mask.sk_k skeleton coefficients */
+    sp_band_config_t v_bands;
+    int              residual_bits;
+    int              use_spinor;
+    int              max_seq_len;
+    int              bytes_per_pos_k;
+    int              bytes_per_pos_v;
+    void            *dev;           /* device cache and staging owned by the library */
+} sp_sqfree_cache_t;
+
+int  sp_sqfree_cache_init(sp_sqfree_cache_t *c, const sp_config_t *cfg, int max_seq_len,
+                          int residual_bits, int use_spinor);
+void sp_sqfree_cache_free(sp_sqfree_cache_t *c);
+/* void calls ignore bad arguments, as the reference's writers and readers do */
+void sp_sqfree_write_k(sp_sqfree_cache_t *c, int layer, int head, int pos, const float *k_vec);
+void sp_sqfree_write_v(sp_sqfree_cache_t *c, int layer, int head, int pos, const float *v_vec);
+void sp_sqfree_read_k(const sp_sqfree_cache_t *c, int layer, int head, int pos, float *k_out);
+void sp_sqfree_read_v(const sp_sqfree_cache_t *c, int layer, int head, int pos, float *v_out);
+/* Knight-mask recalibration (kv_cache.cpp:523, 549, 608): begin clears, feed adds
+ * one host K vector's padded transform, end ranks the coefficients by variance and
+ * rebuilds the Knight tables (device and c->mask) for later writes and reads.
+ * 0 on success, -1 without data. */
+int  sp_sqfree_calibrate_begin(sp_sqfree_cache_t *c);
+void sp_sqfree_calibrate_feed(sp_sqfree_cache_t *c, const float *vec);
+int  sp_sqfree_calibrate_end(sp_sqfree_cache_t *c);
+/* v3 files as sp_hip_sqfree_cache_save/load (kv_cache.cpp:1547, 1570). */
+int  sp_sqfree_cache_save(const sp_sqfree_cache_t *c, const char *prefix, int n_pos, uint64_t model_hash);
+int  sp_sqfree_cache_load(sp_sqfree_cache_t *c, const char *prefix, uint64_t expected_hash);
+
+/* ---- hierarchical cache on host vectors: the absent core's sp_hier_cache_t as the
+ * engine calls it (kv_cache.cpp:326-336 init, 211-212 free, 444-446 / 502-504
+ * write and read, 521, 594, 606, 765 calibration, 1545 / 1568 disk) and reads its
+ * predictors (:270-277, 724-751, 870-876). Records live in HBM in a device cache
+ * the library owns (sp_hip_hier_cache_t), as for the sqfree cache above. Every
+ * slot shares the geometry (sp_hier_default_geometry); predictors[s].W is a host
+ * copy of slot s's fp16 predictor [n_target][n_skeleton], zero until calibrated,
+ * refreshed by calibrate_end(_ema) and load (changes made to it are not used by
+ * the device). */
+typedef struct {
+    int              pad_dim;
+    int              n_skeleton;
+    int              n_target;
+    int             *skeleton_idx;    /* [n_skeleton] */
+    int             *target_idx;      /* [n_target] */
+    sp_band_config_t skel_bands;
+    int              target_res_bits;
+    uint16_t        *W;               /* [n_target][n_skeleton] fp16 */
+} sp_hier_predictor_t;
+
+typedef struct {
+    sp_config_t          config;
+    int                  pad_dim;
+    int                  n_slots;      /* n_layers * n_heads_kv */
+    int                  max_seq_len;
+    int                  level;
+    sp_hier_predictor_t *predictors;   /* [n_slots] */
+    int                  bytes_per_pos;
+    void                *dev;          /* device cache and staging owned by the library */
+} sp_hier_cache_t;
+
+/* level 0 (the engine's default, "auto") selects sp_hier_default_geometry; other
+ * levels are refused (-1): their grouping rule lives in the absent core.
+ * n_skel_bands / skel_bits: skeleton band bits (default 5,5); res_bits 1..4
+ * (default 2). 0 on success, -1 on bad arguments or without a GPU. */
+int  sp_hier_cache_init(sp_hier_cache_t *hc, const sp_config_t *cfg, int max_seq_len, int level,
+                        int n_skel_bands, const int *skel_bits, int res_bits);
+void sp_hier_cache_free(sp_hier_cache_t *hc);
+void sp_hier_cache_write_k(sp_hier_cache_t *hc, int layer, int head, int pos, const float *k_vec);
+void sp_hier_cache_write_v(sp_hier_cache_t *hc, int layer, int head, int pos, const float *v_vec);
+void sp_hier_cache_read_k(const sp_hier_cache_t *hc, int layer, int head, int pos, float *k_out);
+void sp_hier_cache_read_v(const sp_hier_cache_t *hc, int layer, int head, int pos, float *v_out);
+/* Predictor fit per slot (ridge 1e-6 of trace/n_skeleton, as sp_hip_hier_calibrate_end). */
+int  sp_hier_cache_calibrate_begin(sp_hier_cache_t *hc);
+void sp_hier_cache_calibrate_feed(sp_hier_cache_t *hc, int slot, const float *vec);
+int  sp_hier_cache_calibrate_end(sp_hier_cache_t *hc);
+int  sp_hier_cache_calibrate_end_ema(sp_hier_cache_t *hc, float keep_frac);
+int  sp_hier_cache_save(const sp_hier_cache_t *hc, const char *prefix, int n_pos, uint64_t model_hash);
+int  sp_hier_cache_load(sp_hier_cache_t *hc, const char *prefix, uint64_t expected_hash);
+
 /* ---- hier geometry. The reference's core chooses it inside sp_hier_cache_init
  * (called at kv_cache.cpp:326-329; "n_target typically ~130" at
  * shannon_prime_hier.cu:114); its rule is not recoverable. This build's default:

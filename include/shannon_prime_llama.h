@@ -60,6 +60,15 @@ typedef enum {
     SP_LLAMA_ROLE_DRAFT   = 2
 } sp_llama_role_t;
 
+/* The configuration and backend sp_llama_init_with_role would use, from the
+ * environment alone (no caches are created): 1 with *cfg and *backend filled,
+ * 0 when SHANNON_PRIME_ENABLED (or the draft's) is off, -1 for NULL arguments.
+ * Extension: the reference resolves these inline in sp_llama_init_with_role
+ * (shannon_prime_llama.c:209-307); exported so hosts and tests can see the
+ * configuration without a GPU. */
+int sp_llama_resolve_env(const sp_llama_params_t *params, sp_llama_role_t role, sp_config_t *cfg,
+                         int *backend);
+
 /* ---- lifecycle (shannon_prime_llama.h:163-185) ---- */
 sp_llama_ctx_t *sp_llama_init(const sp_llama_params_t *params);
 sp_llama_ctx_t *sp_llama_init_with_role(const sp_llama_params_t *params, sp_llama_role_t role);
@@ -125,6 +134,43 @@ int         sp_llama_get_backend(const sp_llama_ctx_t *ctx);
  * attention launcher in sp_hip.h), else NULL. Returned as void* to keep this
  * header free of the device API. */
 void       *sp_llama_get_hip_cache(const sp_llama_ctx_t *ctx);
+
+/* ======================================================================== */
+/* Sqfree + spinor bridge (src/tools/shannon_prime_llama_sqfree.c:48-240)   */
+/* ======================================================================== */
+/* Environment (shannon_prime_llama_sqfree.c:48-101): SHANNON_PRIME_SQFREE=1
+ * enables the path; SHANNON_PRIME_SPINOR=1 adds the sheet bit and turns SQFREE
+ * on with a message; _RESIDUAL_BITS (1..4, default 3); _SK_FRAC (0.1..1.0,
+ * default 0.75; parsed and kept but, as in the reference, not passed to the
+ * cache: the skeleton is pad_dim / 2); _K_BITS (default 5,4,4,4,5; V mirrors
+ * K); _DUMP_K=<path> with _DUMP_K_LIMIT (default 8192, 0 = no limit) appends
+ * each written K vector as raw fp32. The variables are exactly "1" to enable. */
+typedef struct {
+    int   sqfree_enabled;
+    int   spinor_enabled;
+    int   residual_bits;
+    float sk_frac;
+    int   k_band_bits[SP_MAX_BANDS];
+    int   n_k_bands;
+} sp_llama_sqfree_config_t;
+
+/* Extension: the environment as sp_llama_sqfree_init reads it. */
+void sp_llama_sqfree_config_from_env(sp_llama_sqfree_config_t *out);
+
+typedef struct sp_llama_sqfree_ctx_s sp_llama_sqfree_ctx_t;
+
+/* NULL when SHANNON_PRIME_SQFREE is off or the cache cannot be created
+ * (shannon_prime_llama_sqfree.c:123-190). */
+sp_llama_sqfree_ctx_t *sp_llama_sqfree_init(int head_dim, int n_layers, int n_heads_kv, int max_seq_len);
+void  sp_llama_sqfree_free(sp_llama_sqfree_ctx_t *ctx);
+void  sp_llama_sqfree_write_kv(sp_llama_sqfree_ctx_t *ctx, int layer, int head, int pos,
+                               const float *k_vec, const float *v_vec);
+void  sp_llama_sqfree_read_k(const sp_llama_sqfree_ctx_t *ctx, int layer, int head, int pos, float *k_out);
+void  sp_llama_sqfree_read_v(const sp_llama_sqfree_ctx_t *ctx, int layer, int head, int pos, float *v_out);
+/* Round trip through slot (0, 0, 0) and the correlation with the input (:229-239). */
+float sp_llama_sqfree_validate_k(sp_llama_sqfree_ctx_t *ctx, const float *k_vec, int head_dim);
+/* The context's core cache (for its pad_dim and Knight tables). */
+const sp_sqfree_cache_t *sp_llama_sqfree_get_cache(const sp_llama_sqfree_ctx_t *ctx);
 
 #ifdef __cplusplus
 }

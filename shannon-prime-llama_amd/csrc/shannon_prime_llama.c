@@ -8,6 +8,7 @@
  */
 #include "../../include/shannon_prime_llama.h"
 #include "../../include/sp_hip.h"
+#include "sp_env.h"
 
 #include <stdio.h>
 #include <stdlib.h>
@@ -22,89 +23,85 @@ struct sp_llama_ctx_s {
     sp_hip_cache_t    hip_cache;   /* SP_BACKEND_HIP: device storage */
 };
 
-/* ---- env parsing (shannon_prime_llama.c:73-165) ---- */
+/* ---- configuration from the environment ----
+ * Names, defaults and precedence are the reference bridge's
+ * (shannon_prime_llama.c:73-307); the decoders live in sp_env.c. */
 
-static int parse_env_bool(const char *name, int default_val) {
-    const char *v = getenv(name);
-    if (!v) return default_val;
-    return (v[0] == '1' || v[0] == 'y' || v[0] == 'Y');
-}
+/* Draft presets: band tables a draft context starts from before its explicit
+ * K_BITS / V_BITS (shannon_prime_llama.c:177-199). k_n == 0 keeps the
+ * head-dim defaults. */
+static const struct draft_preset {
+    const char *name;
+    int k_n, k_bits[2];
+    int v_n, v_bits[1];
+} k_presets[] = {
+    {"aggressive", 2, {2, 1}, 1, {1}},
+    {"ternary", 2, {2, 2}, 1, {2}},
+    {"ship", 0, {0, 0}, 0, {0}},
+};
 
-static int parse_env_bits_autocount(const char *name, int *bits, int max_n) {
-    const char *v = getenv(name);
-    if (!v || !*v) return 0;
-    int i = 0;
-    const char *p = v;
-    while (i < max_n && *p) {
-        bits[i++] = atoi(p);
-        while (*p && *p != ',') p++;
-        if (*p == ',') p++;
-    }
-    return i;
-}
-
-static const char *resolve_role_name(const char *base, sp_llama_role_t role, char *out, size_t n) {
-    if (role == SP_LLAMA_ROLE_DRAFT) {
-        snprintf(out, n, "SHANNON_PRIME_DRAFT_%s", base);
-        const char *v = getenv(out);
-        if (v && *v) return out;
-    }
-    snprintf(out, n, "SHANNON_PRIME_%s", base);
-    return out;
-}
-
-static const char *role_getenv(const char *base, sp_llama_role_t role) {
-    char name[160];
-    return getenv(resolve_role_name(base, role, name, sizeof(name)));
-}
-
-static int parse_role_bool(const char *base, sp_llama_role_t role, int def) {
-    char name[160];
-    return parse_env_bool(resolve_role_name(base, role, name, sizeof(name)), def);
-}
-
-static int parse_role_bits(const char *base, sp_llama_role_t role, int *bits, int max_n) {
-    char name[160];
-    return parse_env_bits_autocount(resolve_role_name(base, role, name, sizeof(name)), bits, max_n);
-}
-
-static uint32_t parse_role_ternary_mask(const char *base, sp_llama_role_t role) {
-    const char *v = role_getenv(base, role);
-    if (!v || !*v) return 0u;
-    uint32_t mask = 0u;
-    const char *p = v;
-    while (*p) {
-        while (*p == ',' || *p == ' ' || *p == '\t') p++;
-        if (!*p) break;
-        if (*p < '0' || *p > '9') {
-            while (*p && *p != ',') p++;
-            continue;
+static void apply_preset(const char *name, sp_config_t *cfg) {
+    if (!name || !name[0]) return;
+    for (size_t i = 0; i < sizeof(k_presets) / sizeof(k_presets[0]); i++) {
+        const struct draft_preset *pr = &k_presets[i];
+        if (strcmp(name, pr->name) != 0) continue;
+        if (pr->k_n) {
+            cfg->k_n_bands = pr->k_n;
+            memcpy(cfg->k_band_bits, pr->k_bits, sizeof(pr->k_bits));
+            cfg->v_n_bands = pr->v_n;
+            memcpy(cfg->v_band_bits, pr->v_bits, sizeof(pr->v_bits));
         }
-        int idx = atoi(p);
-        if (idx >= 0 && idx < 32) mask |= (1u << idx);
-        while (*p && *p != ',') p++;
+        return;
     }
-    return mask;
+    fprintf(stderr, "[Shannon-Prime] unknown SHANNON_PRIME_DRAFT_PRESET '%s' "
+                    "(known: aggressive, ternary, ship); ignoring\n", name);
 }
 
-/* Draft presets (shannon_prime_llama.c:177-199). */
-static int apply_draft_preset(int *k_bits, int *k_n, int *v_bits, int *v_n) {
-    const char *preset = getenv("SHANNON_PRIME_DRAFT_PRESET");
-    if (!preset || !*preset) return 0;
-    if (strcmp(preset, "aggressive") == 0) {
-        k_bits[0] = 2; k_bits[1] = 1; *k_n = 2;
-        v_bits[0] = 1; *v_n = 1;
-        return 1;
-    }
-    if (strcmp(preset, "ternary") == 0) {
-        k_bits[0] = 2; k_bits[1] = 2; *k_n = 2;
-        v_bits[0] = 2; *v_n = 1;
-        return 1;
-    }
-    if (strcmp(preset, "ship") == 0) return 1;
-    fprintf(stderr, "[Shannon-Prime] unknown SHANNON_PRIME_DRAFT_PRESET '%s' "
-                    "(known: aggressive, ternary, ship); ignoring\n", preset);
-    return 0;
+/* Backend names: the reference's (cpu, hexagon, adreno) plus this build's. */
+static const struct backend_name {
+    const char *name;
+    int backend;
+} k_backends[] = {
+    {"cpu", SP_BACKEND_CPU},   {"hip", SP_BACKEND_HIP},       {"gpu", SP_BACKEND_HIP},
+    {"rocm", SP_BACKEND_HIP},  {"cuda", SP_BACKEND_HIP},      {"hexagon", SP_BACKEND_HEXAGON},
+    {"adreno", SP_BACKEND_ADRENO}, {"vulkan", SP_BACKEND_VULKAN},
+};
+
+int sp_llama_resolve_env(const sp_llama_params_t *params, sp_llama_role_t role, sp_config_t *cfg,
+                         int *backend) {
+    if (!params || !cfg) return -1;
+    const int draft = role == SP_LLAMA_ROLE_DRAFT;
+    if (!sp_env_flag(sp_env_text("ENABLED", draft), 0)) return 0;
+
+    sp_config_init(cfg, params->head_dim, params->n_layers, params->n_heads_kv);
+    /* head-dim adaptive defaults (shannon_prime_llama.c:235-252): K 5/5/4/3 and
+     * V 3 from head_dim 128 on, K 5/4/4 and V 5 below */
+    const int wide = params->head_dim >= 128;
+    const int kdef[4] = {5, wide ? 5 : 4, 4, wide ? 3 : 4};
+    cfg->k_n_bands = wide ? 4 : 3;
+    memcpy(cfg->k_band_bits, kdef, sizeof(int) * (size_t)cfg->k_n_bands);
+    cfg->v_n_bands = 1;
+    cfg->v_band_bits[0] = wide ? 3 : 5;
+    if (draft) apply_preset(getenv("SHANNON_PRIME_DRAFT_PRESET"), cfg);
+
+    int n = sp_env_int_list(sp_env_text("K_BITS", draft), cfg->k_band_bits, SP_MAX_BANDS);
+    if (n > 0) cfg->k_n_bands = n;
+    n = sp_env_int_list(sp_env_text("V_BITS", draft), cfg->v_band_bits, SP_MAX_BANDS);
+    if (n > 0) cfg->v_n_bands = n;
+    cfg->use_mobius_mask = sp_env_flag(sp_env_text("MOBIUS", draft), 1);
+    cfg->k_ternary_mask = sp_env_index_mask(sp_env_text("K_TERNARY_BANDS", draft));
+    cfg->v_ternary_mask = sp_env_index_mask(sp_env_text("V_TERNARY_BANDS", draft));
+    cfg->use_fp8 = sp_env_flag(sp_env_text("FP8", draft), 0);
+    const char *norm = sp_env_text("VHT2_NORM", draft);
+    if (norm && strcmp(norm, "stage") == 0) cfg->vht2_norm = SP_VHT2_NORM_STAGE;
+
+    int be = params->backend;
+    const char *bname = sp_env_text("BACKEND", draft);
+    if (bname)
+        for (size_t i = 0; i < sizeof(k_backends) / sizeof(k_backends[0]); i++)
+            if (strcmp(bname, k_backends[i].name) == 0) be = k_backends[i].backend;
+    if (backend) *backend = be;
+    return 1;
 }
 
 /* ---- lifecycle ---- */
@@ -114,46 +111,11 @@ sp_llama_ctx_t *sp_llama_init(const sp_llama_params_t *params) {
 }
 
 sp_llama_ctx_t *sp_llama_init_with_role(const sp_llama_params_t *params, sp_llama_role_t role) {
-    if (!params) return NULL;
-    if (!parse_role_bool("ENABLED", role, 0)) return NULL;
-
     sp_config_t cfg;
-    sp_config_init(&cfg, params->head_dim, params->n_layers, params->n_heads_kv);
-    /* head-dim adaptive defaults (shannon_prime_llama.c:235-252) */
-    static const int k128[4] = {5, 5, 4, 3}, k64[4] = {5, 4, 4, 4};
-    if (params->head_dim >= 128) {
-        cfg.k_n_bands = 4;
-        memcpy(cfg.k_band_bits, k128, sizeof(k128));
-        cfg.v_band_bits[0] = 3;
-    } else {
-        cfg.k_n_bands = 3;
-        memcpy(cfg.k_band_bits, k64, sizeof(k64));
-        cfg.v_band_bits[0] = 5;
-    }
-    cfg.v_n_bands = 1;
-    if (role == SP_LLAMA_ROLE_DRAFT)
-        apply_draft_preset(cfg.k_band_bits, &cfg.k_n_bands, cfg.v_band_bits, &cfg.v_n_bands);
-    int kn = parse_role_bits("K_BITS", role, cfg.k_band_bits, SP_MAX_BANDS);
-    if (kn > 0) cfg.k_n_bands = kn;
-    int vn = parse_role_bits("V_BITS", role, cfg.v_band_bits, SP_MAX_BANDS);
-    if (vn > 0) cfg.v_n_bands = vn;
-    cfg.use_mobius_mask = parse_role_bool("MOBIUS", role, 1);
-    cfg.k_ternary_mask = parse_role_ternary_mask("K_TERNARY_BANDS", role);
-    cfg.v_ternary_mask = parse_role_ternary_mask("V_TERNARY_BANDS", role);
-    cfg.use_fp8 = parse_role_bool("FP8", role, 0);
-    const char *norm = role_getenv("VHT2_NORM", role);
-    if (norm && strcmp(norm, "stage") == 0) cfg.vht2_norm = SP_VHT2_NORM_STAGE;
-
+    int backend = 0;
+    if (sp_llama_resolve_env(params, role, &cfg, &backend) != 1) return NULL;
     sp_llama_params_t p = *params;
-    const char *b = role_getenv("BACKEND", role);
-    if (b) {
-        if (strcmp(b, "cpu") == 0) p.backend = SP_BACKEND_CPU;
-        else if (!strcmp(b, "hip") || !strcmp(b, "gpu") || !strcmp(b, "rocm") || !strcmp(b, "cuda"))
-            p.backend = SP_BACKEND_HIP;
-        else if (!strcmp(b, "hexagon")) p.backend = SP_BACKEND_HEXAGON;
-        else if (!strcmp(b, "adreno")) p.backend = SP_BACKEND_ADRENO;
-        else if (!strcmp(b, "vulkan")) p.backend = SP_BACKEND_VULKAN;
-    }
+    p.backend = backend;
     if (cfg.use_fp8)
         fprintf(stderr, "[Shannon-Prime]%s SHANNON_PRIME_FP8=1 requested but this library has "
                         "no fp8 path; using integer band codes.\n",
@@ -202,12 +164,15 @@ sp_llama_ctx_t *sp_llama_init_config(const sp_llama_params_t *params, const sp_c
     }
     if (backend == SP_BACKEND_HIP) {
         if (sp_hip_cache_init(&ctx->hip_cache, cfg, params->max_seq_len, params->gpu_context) != 0) {
+            fprintf(stderr, "[Shannon-Prime] cache init failed: %s; compression stays off\n", sp_hip_last_error());
             free(ctx);
             return NULL;
         }
     } else {
         backend = SP_BACKEND_CPU;
         if (sp_shadow_cache_init(&ctx->cpu_cache, cfg) != 0) {
+            fprintf(stderr, "[Shannon-Prime] cache init failed: %s; compression stays off "
+                            "(the CPU-storage backend runs its codec on the GPU)\n", sp_hip_last_error());
             free(ctx);
             return NULL;
         }
@@ -219,7 +184,7 @@ sp_llama_ctx_t *sp_llama_init_config(const sp_llama_params_t *params, const sp_c
         }
     }
     ctx->active_backend = backend;
-    if (parse_env_bool("SHANNON_PRIME_VERBOSE", 0)) sp_llama_print_config(ctx);
+    if (sp_env_flag(getenv("SHANNON_PRIME_VERBOSE"), 0)) sp_llama_print_config(ctx);
     return ctx;
 }
 

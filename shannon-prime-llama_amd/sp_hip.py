@@ -111,7 +111,41 @@ class SpLlamaMemory(C.Structure):
                 ("compression_ratio", C.c_float), ("n_positions", C.c_int)]
 
 
+class SpKnightMask(C.Structure):
+    _fields_ = [("pad_dim", C.c_int), ("sk_k", C.c_int), ("n_res", C.c_int), ("n_terms", C.c_int),
+                ("skeleton_idx", C.POINTER(C.c_int)), ("residual_idx", C.POINTER(C.c_int)),
+                ("csr_offsets", C.POINTER(C.c_int)), ("csr_skel_slot", C.POINTER(C.c_int)),
+                ("csr_mu_sign", C.POINTER(C.c_int8))]
+
+
+class SpSqfreeCache(C.Structure):
+    """The core's sqfree cache on host vectors (sp_sqfree_cache_t)."""
+    _fields_ = [("config", SpConfig), ("pad_dim", C.c_int), ("mask", SpKnightMask),
+                ("k_bands", SpBandConfig), ("v_bands", SpBandConfig), ("residual_bits", C.c_int),
+                ("use_spinor", C.c_int), ("max_seq_len", C.c_int), ("bytes_per_pos_k", C.c_int),
+                ("bytes_per_pos_v", C.c_int), ("dev", C.c_void_p)]
+
+
+class SpHierPredictor(C.Structure):
+    _fields_ = [("pad_dim", C.c_int), ("n_skeleton", C.c_int), ("n_target", C.c_int),
+                ("skeleton_idx", C.POINTER(C.c_int)), ("target_idx", C.POINTER(C.c_int)),
+                ("skel_bands", SpBandConfig), ("target_res_bits", C.c_int), ("W", C.POINTER(C.c_uint16))]
+
+
+class SpHierCache(C.Structure):
+    """The core's hierarchical cache on host vectors (sp_hier_cache_t)."""
+    _fields_ = [("config", SpConfig), ("pad_dim", C.c_int), ("n_slots", C.c_int), ("max_seq_len", C.c_int),
+                ("level", C.c_int), ("predictors", C.POINTER(SpHierPredictor)), ("bytes_per_pos", C.c_int),
+                ("dev", C.c_void_p)]
+
+
+class SpLlamaSqfreeConfig(C.Structure):
+    _fields_ = [("sqfree_enabled", C.c_int), ("spinor_enabled", C.c_int), ("residual_bits", C.c_int),
+                ("sk_frac", C.c_float), ("k_band_bits", C.c_int * SP_MAX_BANDS), ("n_k_bands", C.c_int)]
+
+
 BACKEND_CPU, BACKEND_CUDA, BACKEND_VULKAN, BACKEND_ADRENO, BACKEND_HEXAGON, BACKEND_HIP = range(6)
+ROLE_DEFAULT, ROLE_TARGET, ROLE_DRAFT = range(3)
 
 _lib = None
 
@@ -126,6 +160,16 @@ def lib():
         vp, i, f, ll = C.c_void_p, C.c_int, C.c_float, C.c_longlong
         L.sp_hip_last_error.restype = C.c_char_p
         L.sp_hip_attn_noalloc_max_floats.restype = C.c_size_t
+        L.sp_llama_sqfree_init.restype = vp
+        L.sp_llama_sqfree_init.argtypes = [i, i, i, i]
+        L.sp_llama_sqfree_free.argtypes = [vp]
+        L.sp_llama_sqfree_write_kv.argtypes = [vp, i, i, i, vp, vp]
+        L.sp_llama_sqfree_read_k.argtypes = [vp, i, i, i, vp]
+        L.sp_llama_sqfree_read_v.argtypes = [vp, i, i, i, vp]
+        L.sp_llama_sqfree_validate_k.argtypes = [vp, vp, i]
+        L.sp_llama_sqfree_validate_k.restype = f
+        L.sp_llama_sqfree_get_cache.argtypes = [vp]
+        L.sp_llama_sqfree_get_cache.restype = C.POINTER(SpSqfreeCache)
         L.sp_hip_event_create.restype = vp
         L.sp_hip_event_elapsed_ms.restype = f
         L.sp_hip_event_elapsed_ms.argtypes = [vp, vp]
