@@ -165,6 +165,11 @@ void sp_band_dequantize_partial(const uint8_t *in, float *out, const sp_band_con
 int  sp_shadow_cache_save(const sp_shadow_cache_t *sc, const char *prefix, int n_pos, uint64_t model_hash);
 int  sp_shadow_cache_load(sp_shadow_cache_t *sc, const char *prefix, uint64_t expected_hash);
 int  sp_shadow_cache_load_partial(sp_shadow_cache_t *sc, const char *prefix, uint64_t expected_hash, int max_bands);
+/* Positions each caller-owned slot buffer (k_cache[s], v_cache[s]) holds. Extension: the
+ * reference's API never tells the core, but save and load need it to stay inside the
+ * buffers: they refuse files (or n_pos) beyond it, and fail until it is set. The loads
+ * check every layer's file before changing any record. 0, or -1 for bad arguments. */
+int  sp_shadow_cache_set_slot_capacity(sp_shadow_cache_t *sc, int n_positions);
 
 /* ---- calibration (sp_shadow_calibrate_begin/feed/end, called at kv_cache.cpp:525,
  * 587, 610). begin clears the sums; feed adds one host fp32 K vector's transform

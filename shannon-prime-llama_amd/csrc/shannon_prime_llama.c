@@ -125,6 +125,7 @@ sp_llama_ctx_t *sp_llama_init_with_role(const sp_llama_params_t *params, sp_llam
 
 static int alloc_host_slots(sp_llama_ctx_t *ctx) {
     const int n_slots = ctx->config.n_layers * ctx->config.n_heads_kv;
+    if (sp_shadow_cache_set_slot_capacity(&ctx->cpu_cache, ctx->params.max_seq_len) != 0) return -1;
     ctx->cpu_cache.k_cache = (uint8_t **)calloc((size_t)n_slots, sizeof(uint8_t *));
     ctx->cpu_cache.v_cache = (uint8_t **)calloc((size_t)n_slots, sizeof(uint8_t *));
     if (!ctx->cpu_cache.k_cache || !ctx->cpu_cache.v_cache) return -1;

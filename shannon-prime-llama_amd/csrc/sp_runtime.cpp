@@ -14,6 +14,7 @@
 #include <algorithm>
 #include <cmath>
 #include <numeric>
+#include <atomic>
 #include <mutex>
 #include <vector>
 
@@ -1597,7 +1598,14 @@ static void stage_destroy(HostStage *st) {
 struct ShadowDev {
     HostStage *st;
     SpPlan kplan, vplan;
+    int slot_capacity = 0;  // positions each caller-owned slot buffer holds (0: not told)
 };
+
+extern "C" int sp_shadow_cache_set_slot_capacity(sp_shadow_cache_t *sc, int n_positions) {
+    if (!sc || !sc->dev || n_positions <= 0) { set_err("set_slot_capacity: bad args"); return -1; }
+    ((ShadowDev *)sc->dev)->slot_capacity = n_positions;
+    return 0;
+}
 
 extern "C" int sp_shadow_cache_init(sp_shadow_cache_t *sc, const sp_config_t *cfg) {
     if (!sc) return -1;
@@ -2122,40 +2130,86 @@ int disk_save(const DiskCache &D, const char *prefix, int n_pos, uint64_t model_
     return rc;
 }
 
+// Opens layer l's file and checks its header against the cache D (shape, n_pos
+// within D.max_seq and equal to n_pos_all when that is >= 0, coefficient order,
+// model hash, segment layout) and the file's length against the body the header
+// announces. Returns the file positioned after the header, or nullptr with the
+// error set.
+FILE *open_layer_file(const DiskCache &D, const char *prefix, int l, uint64_t expected_hash, int n_pos_all,
+                      DiskHeader &h) {
+    const std::string path = layer_path(prefix, l);
+    FILE *f = fopen(path.c_str(), "rb");
+    if (!f) { set_err("load: cannot open %s", path.c_str()); return nullptr; }
+    h = DiskHeader{};
+    bool ok = fread(&h, sizeof(h), 1, f) == 1;
+    if (!ok || memcmp(h.magic, "VHT2", 4) != 0 || h.check != sp_fnv1a64(&h, 56)) {
+        set_err("load: %s is not a VHT2 cache file", path.c_str());
+        ok = false;
+    } else if (h.version != SP_DISK_VERSION) {
+        set_err("load: %s has format version %u (this build reads %u)", path.c_str(), h.version, SP_DISK_VERSION);
+        ok = false;
+    } else if (h.kind != D.kind || h.layer != l || h.n_heads != D.H || h.head_dim != D.hd || h.k_bytes != D.kB ||
+               h.v_bytes != D.vB || h.n_pos <= 0 || (n_pos_all >= 0 && h.n_pos != n_pos_all)) {
+        set_err("load: %s does not match this cache's shape", path.c_str());
+        ok = false;
+    } else if (h.n_pos > D.max_seq) {
+        set_err("load: %s holds %d positions, the cache has room for %d", path.c_str(), h.n_pos, D.max_seq);
+        ok = false;
+    } else if (h.order_check != D.order_check) {
+        set_err("load: %s was written with another coefficient order", path.c_str());
+        ok = false;
+    } else {
+        ok = hash_ok(h.model_hash, expected_hash, "load");
+    }
+    if (ok) {
+        const long long n_rec = (long long)D.H * h.n_pos;
+        const SpDiskSegs Sk = disk_segs(D.kbc, D.kB, n_rec), Sv = disk_segs(D.vbc, D.vB, n_rec);
+        if (Sk.n != h.k_segs || Sv.n != h.v_segs) {
+            set_err("load: %s band layout differs", path.c_str());
+            ok = false;
+        } else {
+            const long long want = (long long)sizeof(h) + n_rec * (D.kB + D.vB);
+            ok = fseek(f, 0, SEEK_END) == 0 && ftell(f) >= want && fseek(f, (long)sizeof(h), SEEK_SET) == 0;
+            if (!ok) set_err("load: %s is truncated", path.c_str());
+        }
+    }
+    if (!ok) {
+        fclose(f);
+        return nullptr;
+    }
+    return f;
+}
+
+// Checks every layer's file before anything is loaded, so a bad file at layer l
+// leaves the records of layers < l untouched. Returns the common n_pos or -1.
+int check_layer_files(const DiskCache &D, const char *prefix, uint64_t expected_hash) {
+    if (!prefix) { set_err("load: no prefix"); return -1; }
+    int n_pos_all = -1;
+    for (int l = 0; l < D.n_layers; l++) {
+        DiskHeader h;
+        FILE *f = open_layer_file(D, prefix, l, expected_hash, n_pos_all, h);
+        if (!f) return -1;
+        fclose(f);
+        n_pos_all = h.n_pos;
+    }
+    return n_pos_all;
+}
+
 // Loads positions [0, n_pos) of every layer; segments past max_segs (< 0: all)
 // are cleared instead of read. Returns n_pos.
 int disk_load(const DiskCache &D, const char *prefix, uint64_t expected_hash, int max_segs) {
-    if (!prefix) { set_err("load: no prefix"); return -1; }
+    int n_pos_all = check_layer_files(D, prefix, expected_hash);
+    if (n_pos_all < 0) return -1;
     unsigned char *d_stage = nullptr, *h_stage = nullptr;
     size_t cap = 0;
-    int n_pos_all = -1, rc = 0;
+    int rc = 0;
     for (int l = 0; l < D.n_layers && rc == 0; l++) {
+        DiskHeader h;
+        FILE *f = open_layer_file(D, prefix, l, expected_hash, n_pos_all, h);
+        if (!f) { rc = -1; break; }
         const std::string path = layer_path(prefix, l);
-        FILE *f = fopen(path.c_str(), "rb");
-        if (!f) { set_err("load: cannot open %s", path.c_str()); rc = -1; break; }
-        DiskHeader h{};
-        bool ok = fread(&h, sizeof(h), 1, f) == 1;
-        if (!ok || memcmp(h.magic, "VHT2", 4) != 0 || h.check != sp_fnv1a64(&h, 56)) {
-            set_err("load: %s is not a VHT2 cache file", path.c_str());
-            ok = false;
-        } else if (h.version != SP_DISK_VERSION) {
-            set_err("load: %s has format version %u (this build reads %u)", path.c_str(), h.version, SP_DISK_VERSION);
-            ok = false;
-        } else if (h.kind != D.kind || h.layer != l || h.n_heads != D.H || h.head_dim != D.hd || h.k_bytes != D.kB ||
-                   h.v_bytes != D.vB || h.n_pos <= 0 || h.n_pos > D.max_seq || (n_pos_all >= 0 && h.n_pos != n_pos_all)) {
-            set_err("load: %s does not match this cache's shape", path.c_str());
-            ok = false;
-        } else if (h.order_check != D.order_check) {
-            set_err("load: %s was written with another coefficient order", path.c_str());
-            ok = false;
-        } else {
-            ok = hash_ok(h.model_hash, expected_hash, "load");
-        }
-        const long long n_rec = ok ? (long long)D.H * h.n_pos : 0;
+        const long long n_rec = (long long)D.H * h.n_pos;
         const SpDiskSegs Sk = disk_segs(D.kbc, D.kB, n_rec), Sv = disk_segs(D.vbc, D.vB, n_rec);
-        if (ok && (Sk.n != h.k_segs || Sv.n != h.v_segs)) { set_err("load: %s band layout differs", path.c_str()); ok = false; }
-        if (!ok) { fclose(f); rc = -1; break; }
-        n_pos_all = h.n_pos;
         const int nk = max_segs < 0 ? Sk.n : std::min(max_segs, Sk.n), nv = max_segs < 0 ? Sv.n : std::min(max_segs, Sv.n);
         const size_t kfull = (size_t)n_rec * D.kB, body = kfull + (size_t)n_rec * D.vB;
         const size_t kread = (size_t)segs_bytes(Sk, nk, n_rec), vread = (size_t)segs_bytes(Sv, nv, n_rec);
@@ -2170,8 +2224,8 @@ int disk_load(const DiskCache &D, const char *prefix, uint64_t expected_hash, in
             cap = body;
         }
         // the K segments to load, skip the rest of K, the V segments to load
-        ok = fread(h_stage, 1, kread, f) == kread && fseek(f, (long)(kfull - kread), SEEK_CUR) == 0 &&
-             fread(h_stage + kfull, 1, vread, f) == vread;
+        const bool ok = fread(h_stage, 1, kread, f) == kread && fseek(f, (long)(kfull - kread), SEEK_CUR) == 0 &&
+                        fread(h_stage + kfull, 1, vread, f) == vread;
         fclose(f);
         if (!ok) { set_err("load: %s is truncated", path.c_str()); rc = -1; break; }
         const long long ks = (long long)D.max_seq * D.kB, vs = (long long)D.max_seq * D.vB;
@@ -2418,33 +2472,36 @@ uint32_t shadow_order_check(const sp_shadow_cache_t *sc) {
 }
 
 int shadow_disk(sp_shadow_cache_t *sc, const char *prefix, int n_pos, uint64_t hash, int max_segs, bool save) {
-    if (!sc || !sc->k_cache || !sc->v_cache || !prefix) { set_err("shadow disk: bad cache"); return -1; }
+    if (!sc || !sc->dev || !sc->k_cache || !sc->v_cache || !prefix) { set_err("shadow disk: bad cache"); return -1; }
+    const int cap = ((ShadowDev *)sc->dev)->slot_capacity;
+    if (cap <= 0) {
+        set_err("shadow disk: slot capacity unknown (sp_shadow_cache_set_slot_capacity)");
+        return -1;
+    }
     const int H = sc->config.n_heads_kv, hd = sc->config.head_dim, Lyr = sc->config.n_layers;
     const int kB = sc->k_bands.total_bytes, vB = sc->v_bands.total_bytes;
-    const uint32_t oc = shadow_order_check(sc);
-    int n_all = -1;
+    DiskCache D{};
+    D.kind = DISK_SHIP, D.n_layers = Lyr, D.H = H, D.hd = hd, D.max_seq = cap, D.kB = kB, D.vB = vB;
+    D.kbc = &sc->k_bands, D.vbc = &sc->v_bands, D.order_check = shadow_order_check(sc);
+    for (int l = 0; l < Lyr; l++)
+        for (int hh = 0; hh < H; hh++)
+            if (!sc->k_cache[l * H + hh] || !sc->v_cache[l * H + hh]) {
+                set_err("shadow disk: slot %d has no buffer", l * H + hh);
+                return -1;
+            }
+    if (save && (n_pos <= 0 || n_pos > cap)) { set_err("shadow save: n_pos %d outside 1..%d", n_pos, cap); return -1; }
+    if (!save) {
+        n_pos = check_layer_files(D, prefix, hash);  // every file checked before any record changes
+        if (n_pos < 0) return -1;
+    }
     std::vector<unsigned char> body;
     for (int l = 0; l < Lyr; l++) {
         const std::string path = layer_path(prefix, l);
         DiskHeader h{};
-        FILE *f = fopen(path.c_str(), save ? "wb" : "rb");
-        if (!f) { set_err("shadow disk: cannot open %s", path.c_str()); return -1; }
-        if (!save) {
-            bool ok = fread(&h, sizeof(h), 1, f) == 1 && memcmp(h.magic, "VHT2", 4) == 0 &&
-                      h.check == sp_fnv1a64(&h, 56) && h.version == SP_DISK_VERSION;
-            if (!ok) set_err("load: %s is not a VHT2 v%u cache file", path.c_str(), SP_DISK_VERSION);
-            else if (h.kind != DISK_SHIP || h.layer != l || h.n_heads != H || h.head_dim != hd || h.k_bytes != kB ||
-                     h.v_bytes != vB || h.n_pos <= 0 || (n_all >= 0 && h.n_pos != n_all)) {
-                set_err("load: %s does not match this cache's shape", path.c_str());
-                ok = false;
-            } else if (h.order_check != oc) {
-                set_err("load: %s was written with another coefficient order", path.c_str());
-                ok = false;
-            } else {
-                ok = hash_ok(h.model_hash, hash, "load");
-            }
-            if (!ok) { fclose(f); return -1; }
-            n_pos = n_all = h.n_pos;
+        FILE *f = save ? fopen(path.c_str(), "wb") : open_layer_file(D, prefix, l, hash, n_pos, h);
+        if (!f) {
+            if (save) set_err("shadow disk: cannot open %s", path.c_str());
+            return -1;
         }
         const long long n_rec = (long long)H * n_pos;
         const SpDiskSegs Sk = disk_segs(&sc->k_bands, kB, n_rec), Sv = disk_segs(&sc->v_bands, vB, n_rec);
@@ -2465,13 +2522,12 @@ int shadow_disk(sp_shadow_cache_t *sc, const char *prefix, int n_pos, uint64_t h
             unsigned char *base = body.data() + (side ? kfull : 0);
             for (int hh = 0; hh < H; hh++) {
                 uint8_t *rec = (side ? sc->v_cache : sc->k_cache)[l * H + hh];
-                if (!rec) { set_err("shadow disk: slot %d has no buffer", l * H + hh); ok = false; break; }
                 for (int p = 0; p < n_pos; p++)
-                    for (int s = 0; s < Sg.n; s++) {
-                        unsigned char *seg = base + Sg.base[s] + ((long long)hh * n_pos + p) * Sg.len[s];
-                        unsigned char *r = rec + (size_t)p * B + Sg.off[s];
-                        if (save) memcpy(seg, r, (size_t)Sg.len[s]);
-                        else memcpy(r, seg, (size_t)Sg.len[s]);
+                    for (int sg = 0; sg < Sg.n; sg++) {
+                        unsigned char *seg = base + Sg.base[sg] + ((long long)hh * n_pos + p) * Sg.len[sg];
+                        unsigned char *r = rec + (size_t)p * B + Sg.off[sg];
+                        if (save) memcpy(seg, r, (size_t)Sg.len[sg]);
+                        else memcpy(r, seg, (size_t)Sg.len[sg]);
                     }
             }
         }
@@ -2480,7 +2536,7 @@ int shadow_disk(sp_shadow_cache_t *sc, const char *prefix, int n_pos, uint64_t h
             h.version = SP_DISK_VERSION;
             h.model_hash = hash;
             h.n_pos = n_pos, h.layer = l, h.n_heads = H, h.head_dim = hd, h.kind = DISK_SHIP;
-            h.k_bytes = kB, h.v_bytes = vB, h.k_segs = Sk.n, h.v_segs = Sv.n, h.order_check = oc;
+            h.k_bytes = kB, h.v_bytes = vB, h.k_segs = Sk.n, h.v_segs = Sv.n, h.order_check = D.order_check;
             header_seal(h);
             ok = fwrite(&h, sizeof(h), 1, f) == 1 && fwrite(body.data(), 1, body.size(), f) == body.size();
             if (!ok) set_err("save: write failed for %s", path.c_str());
@@ -2488,7 +2544,7 @@ int shadow_disk(sp_shadow_cache_t *sc, const char *prefix, int n_pos, uint64_t h
         if (fclose(f) != 0 && save) { set_err("save: write failed for %s", path.c_str()); ok = false; }
         if (!ok) return -1;
     }
-    return save ? 0 : n_all;
+    return save ? 0 : n_pos;
 }
 
 }  // namespace
@@ -2535,38 +2591,71 @@ static bool core_stage(size_t nf, size_t nb) {
     return true;
 }
 
+// A configuration these calls cannot run leaves the caller's output untouched
+// and says so once on stderr (the message stays in sp_hip_last_error()).
+static void core_refuse(const char *what) {
+    static std::atomic<int> said{0};
+    if (!said.exchange(1)) fprintf(stderr, "[Shannon-Prime HIP] %s: %s; output left unchanged\n", what, g_err);
+}
+
 extern "C" void sp_vht2_forward_f32(float *data, int n) {
     if (!data || n <= 0) return;
+    sp_band_config_t bc;
+    int bits = 8;
+    sp_band_config_init(&bc, n, 1, &bits);
+    SpPlan P;
+    if (sp_build_plan(&bc, n, SP_VHT2_NORM_FINAL, -1, &P)) {
+        set_err("sp_vht2_forward_f32: length %d does not factor over 2, 3, 5, 7, 11", n);
+        core_refuse("sp_vht2_forward_f32");
+        return;
+    }
     std::lock_guard<std::mutex> lk(g_core_mu);
     if (!core_stage((size_t)n, 0) ||
-        !hip_ok(hipMemcpy(g_core_f, data, (size_t)n * sizeof(float), hipMemcpyHostToDevice), "vht2 H2D")) return;
-    sp_hip_vht2_forward(g_core_f, n, 1, SP_VHT2_NORM_FINAL, nullptr);
-    (void)hip_ok(hipMemcpy(data, g_core_f, (size_t)n * sizeof(float), hipMemcpyDeviceToHost), "vht2 D2H");
+        !hip_ok(hipMemcpy(g_core_f, data, (size_t)n * sizeof(float), hipMemcpyHostToDevice), "vht2 H2D") ||
+        !hip_ok(sp_launch_transform(P, g_core_f, 1, nullptr), "vht2") ||
+        !hip_ok(hipMemcpy(data, g_core_f, (size_t)n * sizeof(float), hipMemcpyDeviceToHost), "vht2 D2H"))
+        core_refuse("sp_vht2_forward_f32");
+}
+
+// Plan of the band codec with no transform (the core's sp_band_quantize works on
+// coefficients already transformed).
+static bool band_plan(const sp_band_config_t *bc, SpPlan &P, const char *what) {
+    if (sp_build_plan(bc, 1, 0, -1, &P)) {
+        set_err("%s: band configuration rejected", what);
+        core_refuse(what);
+        return false;
+    }
+    P.chunk_ok = 0;
+    P.skip_transform = 1;
+    return true;
 }
 
 extern "C" void sp_band_quantize(const float *in, uint8_t *out, const sp_band_config_t *bc) {
     if (!in || !out || !bc) return;
+    SpPlan P;
+    if (!band_plan(bc, P, "sp_band_quantize")) return;
     std::lock_guard<std::mutex> lk(g_core_mu);
     const size_t n = (size_t)bc->head_dim, B = (size_t)bc->total_bytes;
-    if (!core_stage(n, B) || !hip_ok(hipMemcpy(g_core_f, in, n * sizeof(float), hipMemcpyHostToDevice), "quantize H2D"))
-        return;
-    sp_hip_band_quantize(g_core_f, g_core_b, bc, 1, nullptr);
-    (void)hip_ok(hipMemcpy(out, g_core_b, B, hipMemcpyDeviceToHost), "quantize D2H");
+    if (!core_stage(n, B) || !hip_ok(hipMemcpy(g_core_f, in, n * sizeof(float), hipMemcpyHostToDevice), "quantize H2D") ||
+        !hip_ok(sp_launch_ship_encode_generic(P, nullptr, g_core_f, SP_DT_F32, 0, bc->head_dim, g_core_b, 0, 1, 1,
+                                              nullptr), "band_quantize") ||
+        !hip_ok(hipMemcpy(out, g_core_b, B, hipMemcpyDeviceToHost), "quantize D2H"))
+        core_refuse("sp_band_quantize");
 }
 
 // bands >= max_bands read as 0; max_bands < 0 (or >= n_bands) reads every band
 extern "C" void sp_band_dequantize_partial(const uint8_t *in, float *out, const sp_band_config_t *bc, int max_bands) {
     if (!in || !out || !bc) return;
+    SpPlan P;
+    if (!band_plan(bc, P, "sp_band_dequantize")) return;
+    if (max_bands >= 0 && max_bands < P.n_bands) P.max_bands = max_bands;
     std::lock_guard<std::mutex> lk(g_core_mu);
     const size_t n = (size_t)bc->head_dim, B = (size_t)bc->total_bytes;
-    if (!core_stage(n, B) || !hip_ok(hipMemcpy(g_core_b, in, B, hipMemcpyHostToDevice), "dequantize H2D")) return;
-    sp_hip_band_dequantize(g_core_b, g_core_f, bc, 1, nullptr);
-    if (!hip_ok(hipMemcpy(out, g_core_f, n * sizeof(float), hipMemcpyDeviceToHost), "dequantize D2H")) return;
-    for (int b = (max_bands < 0 ? bc->n_bands : max_bands); b < bc->n_bands; b++) {
-        int off, sz;
-        sp_band_span(bc, b, &off, &sz);
-        for (int k = 0; k < sz; k++) out[off + k] = 0.0f;
-    }
+    if (!core_stage(n, B) || !hip_ok(hipMemcpy(g_core_b, in, B, hipMemcpyHostToDevice), "dequantize H2D") ||
+        !hip_ok(sp_launch_ship_decode_generic(P, nullptr, g_core_b, 0, g_core_f, SP_DT_F32, 0, bc->head_dim, 1, 1,
+                                              nullptr), "band_dequantize") ||
+        !hip_ok(hipMemcpy(out, g_core_f, n * sizeof(float), hipMemcpyDeviceToHost), "dequantize D2H"))
+        core_refuse("sp_band_dequantize");
 }
 
 extern "C" void sp_band_dequantize(const uint8_t *in, float *out, const sp_band_config_t *bc) {

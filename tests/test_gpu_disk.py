@@ -225,6 +225,7 @@ def test_shadow_files_match_the_device_cache(tmp_path):
         vp = (C.POINTER(C.c_uint8) * (L * H))(*[b.ctypes.data_as(C.POINTER(C.c_uint8)) for b in bufs[L * H:]])
         sc.k_cache = C.cast(kp, C.POINTER(C.POINTER(C.c_uint8)))
         sc.v_cache = C.cast(vp, C.POINTER(C.POINTER(C.c_uint8)))
+        S.check(Lb.sp_shadow_cache_set_slot_capacity(C.byref(sc), n))
         return sc, bufs, (kp, vp)
 
     sa, ba, keep_a = shadow()
@@ -258,7 +259,30 @@ def test_shadow_files_match_the_device_cache(tmp_path):
         assert not k_part[:, 44:].any()
         np.testing.assert_array_equal(bp[L * H + s], ba[L * H + s])
     assert Lb.sp_shadow_cache_load(C.byref(sb), ps.encode(), 12) == -1
-    for sc_ in (sa, sb, sp_):
+    # files longer than the slot buffers are refused before any record changes,
+    # and so is a layer set whose last file is bad
+    small, bs, keep_s = shadow()
+    S.check(Lb.sp_shadow_cache_set_slot_capacity(C.byref(small), n - 1))
+    assert Lb.sp_shadow_cache_load(C.byref(small), ps.encode(), 11) == -1
+    assert "room" in S.last_error()
+    assert Lb.sp_shadow_cache_save(C.byref(small), str(tmp_path / "x").encode(), n, 11) == -1
+    assert not any(b_.any() for b_ in bs)
+    bad = str(tmp_path / "bad")
+    for layer in range(L):
+        data = open(f"{ps}.L{layer}.bin", "rb").read()
+        open(f"{bad}.L{layer}.bin", "wb").write(data if layer + 1 < L else data[:-5])
+    fresh, bf, keep_f = shadow()
+    assert Lb.sp_shadow_cache_load(C.byref(fresh), bad.encode(), 11) == -1
+    assert "truncated" in S.last_error()
+    assert not any(b_.any() for b_ in bf)
+    cbad = S.ShipCache(cfg, n, stream=stream)
+    assert Lb.sp_hip_cache_load(cbad.ref, bad.encode(), 11) == -1
+    assert not d2h(cbad.c.d_k_cache, L * H * n * kB).any()
+    cbad.free()
+    cshort = S.ShipCache(cfg, n - 1, stream=stream)
+    assert Lb.sp_hip_cache_load(cshort.ref, ps.encode(), 11) == -1
+    cshort.free()
+    for sc_ in (sa, sb, sp_, small, fresh):
         Lb.sp_shadow_cache_free(C.byref(sc_))
     cc.free()
     cd.free()
