@@ -360,6 +360,28 @@ def bench_variants(torch, S, L, stream, reps=3):
                         "dec": rate(H5 * N5, hd5, B5, timed(hi_read)),
                         "record_bytes": B5, "pad_dim": pad5, "skeleton": n_sk,
                         "calls": f"1 layer x {H5} heads x {N5} positions, one call (K)"}
+    # configs[4] fused decode attention over hier records: one sequence's layer at 131072
+    # positions x 8 KV heads (K and V from the rows above), 16 query heads (GQA 2)
+    NA, NQ5 = 131072, 16
+    c6 = S.HierCache(S.config(hd5, 1, H5), pad5, sk, tg, S.band_config(n_sk, [5, 5]), 2, NA, H5,
+                     stream=stream.cuda_stream)
+    c6.upload_W(Wh.view(np.uint16))
+    S.check(L.sp_hip_hier_write_layer(c6.ref, 0, 0, NA, P(x[:NA]), P(x[NA:2 * NA]), H5 * hd5, S.DTYPE_F16))
+    q5 = torch.randn((NQ5, hd5), generator=g, device="cuda")
+    o5 = torch.empty((NQ5, hd5), device="cuda")
+    s5 = torch.empty((NQ5, NA), device="cuda")
+    sc5 = C.c_float(1.0 / math.sqrt(hd5))
+    t_full = timed(lambda: S.check(L.sp_hip_hier_attn_decode(c6.ref, 0, NA, P(q5), NQ5, sc5, None, P(o5), sp)))
+    t_kq = timed(lambda: S.check(L.sp_hip_hier_attn_decode(c6.ref, 0, NA, P(q5), NQ5, sc5, P(s5), None, sp)))
+    rec_b = 2 * H5 * NA * B5
+    out["cfg5_hier_fused_attn"] = {
+        "layer_us": round(t_full * 1e6, 1), "kq_only_layer_us": round(t_kq * 1e6, 1),
+        "us_per_token_34_layers": round(34 * t_full * 1e6, 1),
+        "record_gbs": round(rec_b / t_full / 1e9, 1),
+        "fp16_layer_floor_us": round(2 * H5 * NA * hd5 * 2 / (HBM_PEAK_GBS * 1e3), 1),
+        "layout": f"1 layer x {H5} KV heads x {NA} positions, {NQ5} query heads, hd {hd5} (pad {pad5}), "
+                  f"K+V hier records of {B5} B; per sequence (a batch of 8 is 8 such calls)"}
+    c6.free()
     c5.free()
     return out
 
@@ -452,6 +474,9 @@ def main():
                          "bound": "hbm", "achieved": round(dom_gbs, 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(dom_gbs / HBM_PEAK_GBS, 4),
                          "traffic": traffic_from_profile(dom),
+                         "traffic_source": "profiles/hbm_traffic_ship_codec_cfg1.json (rocprofv3 --pmc "
+                                           "FETCH_SIZE/WRITE_SIZE of this kernel, copy-calibrated); "
+                                           "read from the committed profile, not measured in this run",
                          "bytes_per_launch": n_vec * per[dom], "avg_ms": round(kern_ms[dom], 4)},
         })
     if args.only in ("attn", "all"):

@@ -361,6 +361,19 @@ int  sp_hip_hier_write_layer(sp_hip_hier_cache_t *hc, int layer, int start_pos, 
                              const void *d_k, const void *d_v, long long row_stride, int dtype);
 int  sp_hip_hier_read_layer(const sp_hip_hier_cache_t *hc, int layer, int start_pos, int n_tok,
                             void *d_k, void *d_v, long long row_stride, int dtype);
+/* Extension: fused decode attention over the hier cache's records of one layer
+ * (positions [0, n_kv) of every KV head), the contract of sp_hip_attn_decode:
+ * d_q [n_q][head_dim] fp32 (GQA: query head h reads KV head h / (n_q / n_heads_kv),
+ * at most 8 per KV head), d_scores [n_q][n_kv] = kq_scale * q . K~ and d_out
+ * [n_q][head_dim] = softmax(scores) . V~, with K~ and V~ what sp_hip_hier_read_*
+ * returns; either output may be NULL (not both). Neither is reconstructed: the
+ * query is moved into the records' coefficient domain (q~ = V(q zero-padded),
+ * u = q~_skel + W^T q~_tgt) once per query head, so a score costs one pass over
+ * the record. The reference's fused op is ship-only (llama_sp_fused_kq.cpp:14-34);
+ * this serves the hier cache the same way. The workspace is allocated on the
+ * first call and grown when a call needs more. 0 or -1. */
+int  sp_hip_hier_attn_decode(const sp_hip_hier_cache_t *hc, int layer, int n_kv, const float *d_q, int n_q,
+                             float kq_scale, float *d_scores, float *d_out, void *stream);
 
 /* ======================================================================== */
 /* System 1/2 dual cache (DualKvCache, kv_cache.h:238-310,                  */

@@ -847,6 +847,52 @@ void spo_hier_decompress_batch_f32(const uint8_t *in, float *out, int n, int hd,
  * packed archive. This oracle decompresses with the full read path (including
  * the Mobius unreorder the reference op omits, :131-139), applies llama.cpp's
  * GQA grouping qh -> qh / (n_q / n_kvh) and kq_scale, then softmax and . V~. */
+/* The same scores / softmax / . V in double as spo_attn_decode_bands, over hier
+ * records: a position's K~ and V~ are spo_hier_decompress of its records with
+ * its KV head's predictor W[kh]. Not a reference op (the reference's fused op is
+ * ship-only, llama_sp_fused_kq.cpp:14-34); it is the attention a caller gets by
+ * reading the hier cache back and attending over it. */
+void spo_hier_attn_decode(const float *q, const uint8_t *kpack, const uint8_t *vpack,
+                          int n_q, int n_kvh, int n_ctx, int hd, int pad,
+                          int n_skel, const int *skel_idx, int n_target, const int *target_idx,
+                          const spo_band_config_t *skel_bc, const uint16_t *W, int rbits,
+                          float kq_scale, float *scores, float *out) {
+    int grp = n_q / n_kvh;
+    int B = spo_hier_bytes(skel_bc, n_target, rbits);
+    size_t wsz = (size_t)n_target * n_skel;
+    float *kt = (float *)malloc(sizeof(float) * (size_t)hd);
+    double *s = (double *)malloc(sizeof(double) * (size_t)(n_ctx > 0 ? n_ctx : 1));
+    double *o = (double *)malloc(sizeof(double) * (size_t)hd);
+    for (int h = 0; h < n_q; h++) {
+        int kh = h / grp;
+        const uint16_t *Wk = W + (size_t)kh * wsz;
+        double mx = -INFINITY;
+        for (int t = 0; t < n_ctx; t++) {
+            spo_hier_decompress(kpack + ((size_t)kh * n_ctx + t) * B, kt, hd, pad, n_skel, skel_idx,
+                                n_target, target_idx, skel_bc, Wk, rbits);
+            double acc = 0.0;
+            for (int d = 0; d < hd; d++) acc += (double)q[(size_t)h * hd + d] * (double)kt[d];
+            s[t] = acc * (double)kq_scale;
+            if (scores) scores[(size_t)h * n_ctx + t] = (float)s[t];
+            if (s[t] > mx) mx = s[t];
+        }
+        if (!out) continue;
+        double l = 0.0;
+        for (int d = 0; d < hd; d++) o[d] = 0.0;
+        for (int t = 0; t < n_ctx; t++) {
+            double p = exp(s[t] - mx);
+            l += p;
+            spo_hier_decompress(vpack + ((size_t)kh * n_ctx + t) * B, kt, hd, pad, n_skel, skel_idx,
+                                n_target, target_idx, skel_bc, Wk, rbits);
+            for (int d = 0; d < hd; d++) o[d] += p * (double)kt[d];
+        }
+        for (int d = 0; d < hd; d++) out[(size_t)h * hd + d] = (float)(o[d] / l);
+    }
+    free(kt);
+    free(s);
+    free(o);
+}
+
 void spo_attn_decode(const float *q, const uint8_t *kpack, const uint8_t *vpack,
                      int n_q, int n_kvh, int n_ctx, int hd,
                      const spo_band_config_t *kbc, const spo_band_config_t *vbc,

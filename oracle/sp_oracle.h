@@ -198,6 +198,15 @@ void spo_attn_decode_bands(const float *q, const uint8_t *kpack, const uint8_t *
                            const int *order, int norm_mode, float kq_scale,
                            float *scores, float *out, int max_bands);
 
+/* Decode attention over hier records (the hier cache's K and V arrays,
+ * [n_kvh][n_ctx][bytes] each, W [n_kvh][n_target][n_skel] fp16 per KV head):
+ * spo_attn_decode's arithmetic with K~ and V~ from spo_hier_decompress. */
+void spo_hier_attn_decode(const float *q, const uint8_t *kpack, const uint8_t *vpack,
+                          int n_q, int n_kvh, int n_ctx, int hd, int pad,
+                          int n_skel, const int *skel_idx, int n_target, const int *target_idx,
+                          const spo_band_config_t *skel_bc, const uint16_t *W, int rbits,
+                          float kq_scale, float *scores, float *out);
+
 /* ---- metrics ---- */
 float spo_correlation_f32(const float *a, const float *b, int n);
 

@@ -1,0 +1,805 @@
+// sp_hier_attn.hip -- fused decode attention over hierarchical-Vilenkin records
+// (the hier cache's K and V arrays), any hier geometry.
+//
+// A hier record holds the skeleton coefficients (band-quantized) and the target
+// coefficients as residual levels about the slot's linear prediction W * skel;
+// the read path rebuilds c (pad coefficients) and returns V(c)[0, hd), V the
+// length-pad Vilenkin transform (shannon_prime_hier.cu:490-571). V is symmetric
+// and its own inverse, so nothing is ever reconstructed:
+//   * with q~ = kq_scale * V(q zero-padded to pad) (once per query head),
+//     q . K~_t = u . skel_t + q~_tgt . dev_t,   u = q~_skel + W^T q~_tgt,
+//     and dev_t = (level_t - centre) * step_t, so a score is one dot product
+//     with the skeleton values plus step_t * (q~_tgt . level_t - centre * sum q~_tgt);
+//   * sum_t p_t V~_t = V(c)[0, hd) with c_skel = sum_t p_t skel_t and
+//     c_tgt = W c_skel + sum_t p_t dev_t: the weighted sums stay in the record's
+//     coefficient domain and one transform per query head finishes them.
+// The 9000-term prediction W * skel is paid once per query head instead of once
+// per position.
+//
+// Three launches per layer:
+//   k_hier_attn_prep   one block per query head: q~ (LDS transform), u, q~_tgt, sum q~_tgt;
+//   k_hier_attn_split  block (KV head, run): 256-position chunks of the run, one
+//                      position per thread for the scores, an online softmax
+//                      across the run's chunks, and the weighted coefficient sums
+//                      of the V records;
+//   k_hier_attn_merge  one block per query head: the runs' partials merged,
+//                      c rebuilt and transformed.
+// Residual levels of 2, 4 or 8 bits (RB) are read as 32-bit windows of the level
+// stream (32 / RB levels per window, compile-time shifts): for the scores a
+// thread walks its record's windows against q~_tgt (zero-padded to whole
+// windows), and for V a thread owns one window of target coefficients for two
+// query heads over a group of positions (the sums of the position groups meet
+// in LDS at the end of the run). Other level widths take a bit-serial path.
+#include "sp_internal.h"
+
+#include <algorithm>
+
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+constexpr int NT = 256;      // threads per block
+constexpr int CH = 256;      // positions per chunk
+constexpr int MAX_G = 8;     // query heads per KV head
+constexpr int MAX_COEF_PER_THREAD = (SP_GEN_MAX_N + NT - 1) / NT;
+
+__host__ __device__ constexpr int r4(int x) { return (x + 3) & ~3; }
+__host__ __device__ constexpr int r32(int x) { return (x + 31) & ~31; }
+
+// Prepared query per head: [u (r4(ns)) | q~_tgt zero-padded to r32(nt) | sum q~_tgt, 0, 0, 0].
+__host__ __device__ constexpr int prep_qt_off(int ns) { return r4(ns); }
+__host__ __device__ constexpr int prep_sum_off(int ns, int nt) { return r4(ns) + r32(nt); }
+
+// dst[i] = src[i] (i < n), 0 (n <= i < total): U loads per thread in flight at once.
+template <typename T, int U>
+__device__ __forceinline__ void copy_to_lds(T *dst, const T *__restrict__ src, int n, int total, int tid) {
+    for (int i0 = tid; i0 < total; i0 += NT * U) {
+        T v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = i0 + u * NT;
+            v[u] = i < n ? src[i] : T(0);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = i0 + u * NT;
+            if (i < total) dst[i] = v[u];
+        }
+    }
+}
+
+// 4 little-endian bytes at LDS byte offset o (any alignment) of a dword-aligned array.
+__device__ __forceinline__ uint32_t lds_u32_at(const unsigned char *base, int o) {
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(base + (o & ~3));
+    return __builtin_amdgcn_alignbit(w[1], w[0], 8u * (uint32_t)(o & 3));
+}
+
+// nbits (<= 8) bits at bit `bit` (0..7) of byte offset o.
+__device__ __forceinline__ uint32_t lds_bits_at(const unsigned char *base, int o, int bit, int nbits) {
+    return __builtin_amdgcn_ubfe(lds_u32_at(base, o), (uint32_t)bit, (uint32_t)nbits);
+}
+
+// LSB-first bit stream starting at byte offset o of a dword-aligned LDS array.
+// The stream is read in 32-bit windows [32j, 32j + 32) through funnel shifts of
+// aligned dwords, so every lane refills at the same code index whatever its start
+// byte (the refill branch stays uniform). Reads up to 12 bytes past the stream.
+struct LdsBits {
+    const uint32_t *dw;
+    uint32_t fs, prev;
+    uint64_t buf;
+    int nbits;
+    __device__ LdsBits(const unsigned char *base, int o) {
+        dw = reinterpret_cast<const uint32_t *>(base + (o & ~3));
+        fs = 8u * (uint32_t)(o & 3);
+        prev = dw[0];
+        buf = win();
+        buf |= (uint64_t)win() << 32;
+        nbits = 64;
+    }
+    __device__ uint32_t win() {
+        const uint32_t cur = dw[1];
+        const uint32_t w = __builtin_amdgcn_alignbit(cur, prev, fs);
+        prev = cur;
+        dw++;
+        return w;
+    }
+    __device__ uint32_t get(int bits) {
+        if (nbits < bits) {
+            buf |= (uint64_t)win() << nbits;
+            nbits += 32;
+        }
+        const uint32_t v = (uint32_t)buf & ((1u << bits) - 1u);
+        buf >>= bits;
+        nbits -= bits;
+        return v;
+    }
+};
+
+// One Vilenkin stage of radix p over c[0, n) (stride `stride`), all NT threads,
+// the p x p cas matrix C (scaled by isp) read from LDS.
+template <int p>
+__device__ __forceinline__ void vil_stage(float *c, int n, int stride, const float *C, float isp, int tid) {
+    const int block = stride * p;
+    for (int wi = tid; wi < n / p; wi += NT) {
+        const int base = (wi / stride) * block + (wi % stride);
+        float gv[p], rv[p];
+#pragma unroll
+        for (int k = 0; k < p; k++) gv[k] = c[base + k * stride];
+#pragma unroll
+        for (int k = 0; k < p; k++) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int jj = 0; jj < p; jj++) sum += C[k * p + jj] * gv[jj];
+            rv[k] = sum * isp;
+        }
+#pragma unroll
+        for (int k = 0; k < p; k++) c[base + k * stride] = rv[k];
+    }
+}
+
+// In-place transform of c[0, n) in LDS by the whole block: the stages of
+// sp_transform_lds (same arithmetic), with every thread of the block taking
+// groups and the cas tables copied to LDS (cas_s, SP_CAS_TOTAL floats) first.
+// Ends with a barrier.
+__device__ __forceinline__ void transform_block(float *c, int n, const SpPlan &P, float *cas_s, int tid) {
+    if ((n & (n - 1)) == 0 || P.skip_transform) {
+        sp_transform_lds(c, n, P, tid < SP_WAVE ? tid : n);
+        __syncthreads();
+        return;
+    }
+    for (int i = tid; i < SP_CAS_TOTAL; i += NT) cas_s[i] = P.cas[i];
+    __syncthreads();
+    int stride = 1;
+    for (int f = 0; f < P.n_factors; f++) {
+        const int p = P.factors[f];
+        const float *C = cas_s + sp_cas_off(p);
+        const float isp = P.isp[sp_prime_idx(p)];
+        switch (p) {
+            case 2: vil_stage<2>(c, n, stride, C, isp, tid); break;
+            case 3: vil_stage<3>(c, n, stride, C, isp, tid); break;
+            case 5: vil_stage<5>(c, n, stride, C, isp, tid); break;
+            case 7: vil_stage<7>(c, n, stride, C, isp, tid); break;
+            default: vil_stage<11>(c, n, stride, C, isp, tid); break;
+        }
+        stride *= p;
+        __syncthreads();
+    }
+}
+
+// Power of two p with amax * p in [2^11, 2^12) (1 when amax is 0 or not finite).
+__device__ __forceinline__ float pow2_norm(float amax) {
+    if (!(amax > 0.0f) || !(amax < INFINITY)) return 1.0f;
+    int e;
+    (void)frexpf(amax, &e);
+    return ldexpf(1.0f, 12 - e);
+}
+
+// v + the value of lane ^ 1 (DPP quad permute [1,0,3,2]).
+__device__ __forceinline__ float add_xor1(float v) {
+    return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));
+}
+
+// Eight 2-bit levels (bits 0..15 of y) -> the A operand slots of v_mfma_f32_16x16x32_f16
+// as fp16 4 + level (exact): level pair m (bits 4m..4m+3) times 2^8 + 2^22 puts the two
+// levels at bits 8-9 and 24-25 (the other copies land outside the mask), and the
+// exponent bits of 4.0 in both halves finish the pair.
+__device__ __forceinline__ half8_t level_pairs2(uint32_t y) {
+    u32x4 v;
+#pragma unroll
+    for (int m = 0; m < 4; m++)
+        v[m] = __builtin_amdgcn_bitop3_b32(__builtin_amdgcn_ubfe(y, 4u * m, 4u) * 0x00400100u, 0x03000300u,
+                                           0x44004400u, 0xEA);
+    return __builtin_bit_cast(half8_t, v);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, SP_WAVE);
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// Query preparation. Dynamic LDS: c[pad], qt[r32(n_target)], part[8][r4(n_skel)]
+// floats, then the KV head's W [n_target][n_skel] fp16.
+__global__ void __launch_bounds__(NT)
+k_hier_attn_prep(const SpPlan P, const SpHierAttnArgs A, float *__restrict__ prep) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char dsm[];
+    __shared__ float wsum[NT / SP_WAVE];
+    __shared__ float cas_s[SP_CAS_TOTAL];
+    const int h = blockIdx.x, tid = threadIdx.x;
+    const int G = A.n_q / A.n_kvh, kvh = h / G;
+    const int ns = A.n_skel, nt = A.n_target, ns4 = r4(ns), nt32 = r32(nt);
+    float *c = reinterpret_cast<float *>(dsm);
+    float *qt = c + r4(A.pad);
+    float *part = qt + nt32;
+    unsigned short *Ws = reinterpret_cast<unsigned short *>(part + 8 * ns4);
+    const unsigned short *Wk = reinterpret_cast<const unsigned short *>(A.W) + (long long)kvh * A.w_outer;
+    copy_to_lds<unsigned short, 16>(Ws, Wk, nt * ns, nt * ns, tid);
+    for (int k = tid; k < A.pad; k += NT) c[k] = k < A.hd ? A.q[(long long)h * A.hd + k] : 0.0f;
+    __syncthreads();
+    transform_block(c, A.pad, P, cas_s, tid);
+    for (int t = tid; t < nt32; t += NT) qt[t] = t < nt ? A.kq_scale * c[A.tgt_idx[t]] : 0.0f;
+    __syncthreads();
+    // W^T q~_tgt in 8 interleaved partial sums per skeleton coefficient
+    for (int i = tid; i < 8 * ns; i += NT) {
+        const int s = i % ns, g = i / ns;
+        float acc = 0.0f;
+#pragma unroll 4
+        for (int t = g; t < nt; t += 8) acc = fmaf(sp_f16_bits_to_f32(Ws[t * ns + s]), qt[t], acc);
+        part[g * ns4 + s] = acc;
+    }
+    __syncthreads();
+    float *pr = prep + (long long)h * A.ps;
+    for (int s = tid; s < ns4; s += NT) {
+        float u = 0.0f;
+        if (s < ns) {
+            u = A.kq_scale * c[A.skel_idx[s]];
+            for (int g = 0; g < 8; g++) u += part[g * ns4 + s];
+        }
+        pr[s] = u;
+    }
+    float qs = 0.0f;
+    for (int t = tid; t < nt32; t += NT) {
+        pr[ns4 + t] = qt[t];
+        qs += qt[t];
+    }
+    qs = wave_sum(qs);
+    if ((tid & 63) == 0) wsum[tid >> 6] = qs;
+    __syncthreads();
+    if (tid < 4) pr[prep_sum_off(ns, nt) + tid] = tid == 0 ? (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]) : 0.0f;
+}
+
+// ---------------------------------------------------------------------------
+// Scores, softmax and the V records' weighted coefficient sums. Block
+// (kvh, run) takes chunks run, run + n_runs, ... of KV head kvh. RB: residual
+// level bits read as 32-bit windows (2, 4, 8), or 0 for the bit-serial path.
+// Dynamic LDS (bytes, 16-aligned pieces):
+//   rec   r16(CH * B + 32)  K, then V records of the chunk (dword-staged from a shift of
+//                           0..3 bytes, then 12 zero bytes for the bit readers' look-ahead)
+//   prep  G * ps floats     the G query heads' prepared queries
+//   sc    G * CH floats     scores, then the softmax weights p
+//   pw    G * CH floats     p * step (V targets)
+//   psb   n_bands * G * CH  p * scale_b (V skeleton bands)
+//   red   8 * MAX_G floats  block reductions
+// (RB > 0: at the end of the run the same memory holds the position groups' sums.)
+// Partial per (query head, run): [m, l, -, -, c_skel sum (n_skel), dev sum (n_target)].
+template <int RB, int GM>
+__global__ void __launch_bounds__(NT, 3)
+k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A, const float *__restrict__ prep, float *__restrict__ part,
+                  int n_runs) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char dsm[];
+    const int kvh = blockIdx.x, run = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int G = A.n_q / A.n_kvh, h0 = kvh * G;
+    const int ns = A.n_skel, nt = A.n_target, B = A.B, nb = P.n_bands;
+    const int qo = prep_qt_off(ns), so = prep_sum_off(ns, nt);
+    const bool want_out = A.out != nullptr;
+    const int rec_bytes = ((CH * B + 32) + 15) & ~15;
+    unsigned char *rec = dsm;
+    uint32_t *rec32 = reinterpret_cast<uint32_t *>(dsm);
+    float *prep_s = reinterpret_cast<float *>(dsm + rec_bytes);
+    float *sc = prep_s + G * A.ps;
+    float *pw = sc + G * CH;
+    float *psb = pw + G * CH;
+    float *red = psb + nb * G * CH;
+    const int skB = P.total_bytes;
+    const int Lv = 1 << A.rbits;
+    const float step_div = (float)(Lv - 1);
+    const float centre = sp_div((float)(Lv - 1), 2.0f);
+
+    copy_to_lds<float, 4>(prep_s, prep + (long long)h0 * A.ps, G * A.ps, G * A.ps, tid);
+
+    // RB == 2: the target dots run on v_mfma_f32_16x16x32_f16 with the levels as the A
+    // operand (rows = positions, fp16 4 + level) and q~_tgt as B: column c16 = (head
+    // c16 >> 1, hi / lo fp16 part c16 & 1) of q~_tgt scaled by a power of two per head.
+    // bq[j][q4][c16]: the 8 B-operand halves of levels 32 j + 8 q4 .. +7; cin[c16]: the
+    // accumulator start -(4 + centre) * (column sum), which centres the levels; unh: the
+    // inverse scale. The skeleton bands stay on the position threads.
+    constexpr bool KM = RB == 2;
+    const int n_kb = r32(nt) / 32;
+    u32x4 *bq = reinterpret_cast<u32x4 *>(red + 8 * MAX_G);
+    float *cin = reinterpret_cast<float *>(bq + n_kb * 64);
+    float *unh = cin + 16;
+    float *fh = unh + 16;
+    float *psum = fh + 8;
+    if (KM) {
+        __syncthreads();
+        for (int h = wv; h < G; h += NT / SP_WAVE) {
+            float am = 0.0f;
+            for (int kk = lane; kk < nt; kk += SP_WAVE) am = fmaxf(am, fabsf(prep_s[h * A.ps + qo + kk]));
+            am = sp_wave_max(am);
+            if (lane == 0) fh[h] = pow2_norm(am);
+        }
+        __syncthreads();
+        unsigned short *bqh = reinterpret_cast<unsigned short *>(bq);
+        const int c16 = tid & 15, hq = c16 >> 1;
+        float colsum = 0.0f;
+        for (int kk = tid >> 4; kk < n_kb * 32; kk += NT / 16) {
+            const float v = hq < G ? prep_s[hq * A.ps + qo + kk] * fh[hq] : 0.0f;
+            const _Float16 hi = (_Float16)v;
+            const _Float16 lo = (_Float16)(v - (float)hi);
+            const _Float16 x = (c16 & 1) ? lo : hi;
+            colsum += (float)x;
+            bqh[(((kk >> 5) * 4 + ((kk >> 3) & 3)) * 16 + c16) * 8 + (kk & 7)] = __builtin_bit_cast(unsigned short, x);
+        }
+        psum[(tid >> 4) * 16 + c16] = colsum;
+        __syncthreads();
+        if (tid < 16) {
+            float sum = 0.0f;
+            for (int g = 0; g < 16; g++) sum += psum[g * 16 + tid];
+            cin[tid] = -(4.0f + centre) * sum;
+            unh[tid] = (tid >> 1) < G ? 1.0f / fh[tid >> 1] : 0.0f;
+        }
+        // the chunk loop's first barrier orders these before their use
+    }
+
+    // running softmax state per head (identical in every thread)
+    float m_run[GM], l_run[GM];
+#pragma unroll
+    for (int h = 0; h < GM; h++) {
+        m_run[h] = -INFINITY;
+        l_run[h] = 0.0f;
+    }
+    // V sums. Bit-serial path: coefficient j = tid + NT * r (skeleton first, then targets)
+    // for every head. Window path: one target window (32 / RB coefficients) and one
+    // skeleton coefficient, each for head pair (2 hp, 2 hp + 1), over a group of positions.
+    constexpr int LPW = RB > 0 ? 32 / RB : 1;
+    constexpr uint32_t LMASK = RB > 0 ? (1u << RB) - 1u : 1u;
+    constexpr int NCOEF = RB > 0 ? 1 : MAX_COEF_PER_THREAD;
+    float acc[NCOEF][GM];
+    float tacc[LPW][2], twsum[2], sacc[2];
+#pragma unroll
+    for (int r = 0; r < NCOEF; r++)
+#pragma unroll
+        for (int h = 0; h < GM; h++) acc[r][h] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        twsum[j] = sacc[j] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < LPW; k++) tacc[k][j] = 0.0f;
+    }
+    const int n_win = RB > 0 ? (nt * RB + 31) / 32 : 1;
+    const int n_hp = (G + 1) / 2;
+    const int t_items = n_win * n_hp, s_items = ns * n_hp;
+    const int npg_t = max(1, NT / t_items), npg_s = max(1, NT / s_items);
+    const bool t_on = tid < t_items * npg_t, s_on = tid < s_items * npg_s;
+    const int t_item = tid % t_items, t_pg = tid / t_items, t_w = t_item % n_win, t_hp = t_item / n_win;
+    const int s_item = tid % s_items, s_pg = tid / s_items, s_s = s_item % ns, s_hp = s_item / ns;
+    const int t_ha = 2 * t_hp, t_hb = min(2 * t_hp + 1, G - 1);
+    const int s_ha = 2 * s_hp, s_hb = min(2 * s_hp + 1, G - 1);
+    int s_b = 0;
+    while (s_b + 1 < nb && s_s >= P.band_off[s_b + 1]) s_b++;
+    const int s_bits = P.band_bits[s_b], s_bo = (s_s - P.band_off[s_b]) * s_bits;
+    const int s_byte = P.band_byte_off[s_b] + 2 + (s_bo >> 3), s_bit = s_bo & 7;
+    const float s_off = (float)((1 << (s_bits - 1)) - 1);
+
+    const int n_chunks = (A.n_kv + CH - 1) / CH;
+    for (int ch = run; ch < n_chunks; ch += n_runs) {
+        const int c0 = ch * CH;
+        const int n_t = min(CH, A.n_kv - c0);
+        // ---- K records of the chunk into LDS (aligned dwords; records from byte `shift`) ----
+        const unsigned char *kg = A.kcache + (long long)kvh * A.slot_bytes + (long long)c0 * B;
+        const int shift = (int)((uintptr_t)kg & 3);
+        const int ndw = (n_t * B + shift + 3) >> 2;
+        __syncthreads();  // the previous chunk is done with rec / sc
+        copy_to_lds<uint32_t, 32>(rec32, reinterpret_cast<const uint32_t *>(kg - shift), ndw, ndw + 3, tid);
+        __syncthreads();
+        if (KM) {
+            // ---- target dots of this wave's 64 positions on the matrix cores -> sc ----
+            const int r = lane & 15, q4 = lane >> 4;
+            const float ci = cin[r], un = unh[r];
+            const bool wr = !(r & 1) && (r >> 1) < G;
+#pragma unroll
+            for (int sub = 0; sub < 4; sub++) {
+                const int pos0 = 64 * wv + 16 * sub;
+                float4_t acc = {ci, ci, ci, ci};
+                const int ob = shift + (pos0 + r) * B + skB + 4 + 2 * q4;
+                for (int j = 0; j < n_kb; j++) {
+                    const half8_t code = level_pairs2(lds_u32_at(rec, ob + 8 * j));
+                    const half8_t bv = __builtin_bit_cast(half8_t, bq[(j * 4 + q4) * 16 + r]);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(code, bv, acc, 0, 0, 0);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float v = add_xor1(acc[i]) * un;  // hi + lo columns
+                    if (wr) sc[(r >> 1) * CH + pos0 + 4 * q4 + i] = v;
+                }
+            }
+            __asm__ volatile("" ::: "memory");  // the wave's position threads read sc next
+        }
+        // ---- scores: thread = position ----
+        if (tid < n_t) {
+            const int rb = shift + tid * B;
+            const float mag = __uint_as_float(lds_u32_at(rec, rb + skB));
+            const float step = sp_div(2.0f * mag, step_div);
+            for (int hp = 0; hp < G; hp += 2) {
+                const int ha = hp, hb = hp + 1 < G ? hp + 1 : hp;
+                const float *ua = prep_s + ha * A.ps, *ub = prep_s + hb * A.ps;
+                float s0 = 0.0f, s1 = 0.0f;
+                for (int b = 0; b < nb; b++) {
+                    const int bits = P.band_bits[b], off = P.band_off[b], sz = P.band_sz[b];
+                    const int maxv = (1 << (bits - 1)) - 1;
+                    const float scale = sp_scale_from_bits(lds_u32_at(rec, rb + P.band_byte_off[b]) & 0xffffu);
+                    LdsBits br(rec, rb + P.band_byte_off[b] + 2);
+                    float a0 = 0.0f, a1 = 0.0f;
+                    for (int i = 0; i < sz; i++) {
+                        const float cv = (float)((int)br.get(bits) - maxv);
+                        a0 = fmaf(ua[off + i], cv, a0);
+                        a1 = fmaf(ub[off + i], cv, a1);
+                    }
+                    s0 = fmaf(scale, a0, s0);
+                    s1 = fmaf(scale, a1, s1);
+                }
+                float d0 = 0.0f, d1 = 0.0f;
+                if (KM) {
+                    d0 = sc[ha * CH + tid] + centre * ua[so];  // centred on the matrix cores
+                    d1 = sc[hb * CH + tid] + centre * ub[so];
+                } else if (RB > 0) {
+                    // window w of the level stream against q~_tgt[w * LPW ..] (zero past n_target)
+                    const int o = rb + skB + 4;
+                    const uint32_t *dw = reinterpret_cast<const uint32_t *>(rec + (o & ~3));
+                    const uint32_t fs = 8u * (uint32_t)(o & 3);
+                    uint32_t prev = dw[0];
+                    for (int w = 0; w < n_win; w++) {
+                        const uint32_t cur = dw[w + 1];
+                        const uint32_t win = __builtin_amdgcn_alignbit(cur, prev, fs);
+                        prev = cur;
+                        const float *qa = ua + qo + w * LPW, *qb = ub + qo + w * LPW;
+#pragma unroll
+                        for (int k = 0; k < LPW; k++) {
+                            const float lv = (float)((win >> (k * RB)) & LMASK);
+                            d0 = fmaf(qa[k], lv, d0);
+                            d1 = fmaf(qb[k], lv, d1);
+                        }
+                    }
+                } else {
+                    LdsBits br(rec, rb + skB + 4);
+                    for (int t = 0; t < nt; t++) {
+                        const float lv = (float)br.get(A.rbits);
+                        d0 = fmaf(ua[qo + t], lv, d0);
+                        d1 = fmaf(ub[qo + t], lv, d1);
+                    }
+                }
+                s0 = fmaf(step, d0 - centre * ua[so], s0);
+                s1 = fmaf(step, d1 - centre * ub[so], s1);
+                sc[ha * CH + tid] = s0;
+                if (hb != ha) sc[hb * CH + tid] = s1;
+                if (A.scores) {
+                    A.scores[(long long)(h0 + ha) * A.n_kv + c0 + tid] = s0;
+                    if (hb != ha) A.scores[(long long)(h0 + hb) * A.n_kv + c0 + tid] = s1;
+                }
+            }
+        }
+        if (!want_out) continue;
+        __syncthreads();
+        // ---- online softmax over the chunk (per head: block max, then block sum) ----
+        float alpha[GM];
+        {
+            float mx[GM];
+#pragma unroll
+            for (int h = 0; h < GM; h++) mx[h] = (h < G && tid < n_t) ? sc[h * CH + tid] : -INFINITY;
+#pragma unroll
+            for (int h = 0; h < GM; h++) {
+                if (h < G) {
+                    const float v = sp_wave_max(mx[h]);
+                    if (lane == 0) red[wv * MAX_G + h] = v;
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int h = 0; h < GM; h++) {
+                if (h < G) {
+                    const float cm = fmaxf(fmaxf(red[h], red[MAX_G + h]), fmaxf(red[2 * MAX_G + h], red[3 * MAX_G + h]));
+                    const float mn = fmaxf(m_run[h], cm);
+                    alpha[h] = __expf(m_run[h] - mn);
+                    m_run[h] = mn;
+                } else {
+                    alpha[h] = 1.0f;
+                }
+            }
+            float pl[GM];
+#pragma unroll
+            for (int h = 0; h < GM; h++) {
+                const float p = (h < G && tid < n_t) ? __expf(sc[h * CH + tid] - m_run[h]) : 0.0f;
+                if (h < G) sc[h * CH + tid] = p;
+                pl[h] = p;
+            }
+#pragma unroll
+            for (int h = 0; h < GM; h++) {
+                if (h < G) {
+                    const float v = wave_sum(pl[h]);
+                    if (lane == 0) red[4 * MAX_G + wv * MAX_G + h] = v;
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int h = 0; h < GM; h++) {
+                if (h < G) {
+                    const float *rs = red + 4 * MAX_G;
+                    l_run[h] = fmaf(l_run[h], alpha[h], (rs[h] + rs[MAX_G + h]) + (rs[2 * MAX_G + h] + rs[3 * MAX_G + h]));
+                }
+            }
+        }
+        // ---- V records of the chunk; per position: p * step and p * scale_b ----
+        const unsigned char *vg = A.vcache + (long long)kvh * A.slot_bytes + (long long)c0 * B;
+        const int vshift = (int)((uintptr_t)vg & 3);
+        const int vdw = (n_t * B + vshift + 3) >> 2;
+        copy_to_lds<uint32_t, 32>(rec32, reinterpret_cast<const uint32_t *>(vg - vshift), vdw, vdw + 3, tid);
+        __syncthreads();
+        {
+            const int rb = vshift + tid * B;
+            const bool live = tid < n_t;
+            const float vstep = live ? sp_div(2.0f * __uint_as_float(lds_u32_at(rec, rb + skB)), step_div) : 0.0f;
+            for (int h = 0; h < G; h++) pw[h * CH + tid] = sc[h * CH + tid] * vstep;
+            for (int b = 0; b < nb; b++) {
+                const float scale =
+                    live ? sp_scale_from_bits(lds_u32_at(rec, rb + P.band_byte_off[b]) & 0xffffu) : 0.0f;
+                for (int h = 0; h < G; h++) psb[(b * G + h) * CH + tid] = sc[h * CH + tid] * scale;
+            }
+        }
+        __syncthreads();
+        if (RB > 0) {
+            // ---- window sums: target window t_w and skeleton coefficient s_s for a head pair ----
+            float fa = 1.0f, fb = 1.0f, ga = 1.0f, gb = 1.0f;
+#pragma unroll
+            for (int h = 0; h < GM; h++) {
+                if (h == t_ha) fa = alpha[h];
+                if (h == t_hb) fb = alpha[h];
+                if (h == s_ha) ga = alpha[h];
+                if (h == s_hb) gb = alpha[h];
+            }
+            twsum[0] *= fa;
+            twsum[1] *= fb;
+#pragma unroll
+            for (int k = 0; k < LPW; k++) {
+                tacc[k][0] *= fa;
+                tacc[k][1] *= fb;
+            }
+            sacc[0] *= ga;
+            sacc[1] *= gb;
+            if (t_on) {
+                const int wo = skB + 4 + 4 * t_w;
+#pragma unroll 2
+                for (int t = t_pg; t < n_t; t += npg_t) {
+                    const uint32_t win = lds_u32_at(rec, vshift + t * B + wo);
+                    const float wa = pw[t_ha * CH + t], wb = pw[t_hb * CH + t];
+                    twsum[0] += wa;
+                    twsum[1] += wb;
+#pragma unroll
+                    for (int k = 0; k < LPW; k++) {
+                        const float lv = (float)((win >> (k * RB)) & LMASK);
+                        tacc[k][0] = fmaf(wa, lv, tacc[k][0]);
+                        tacc[k][1] = fmaf(wb, lv, tacc[k][1]);
+                    }
+                }
+            }
+            if (s_on) {
+                const float *wa_row = psb + (s_b * G + s_ha) * CH, *wb_row = psb + (s_b * G + s_hb) * CH;
+#pragma unroll 4
+                for (int t = s_pg; t < n_t; t += npg_s) {
+                    const float cv = (float)lds_bits_at(rec, vshift + t * B + s_byte, s_bit, s_bits) - s_off;
+                    sacc[0] = fmaf(wa_row[t], cv, sacc[0]);
+                    sacc[1] = fmaf(wb_row[t], cv, sacc[1]);
+                }
+            }
+        } else {
+            // ---- bit-serial path: coefficient j = tid + NT*r, positions of the chunk in order ----
+#pragma unroll
+            for (int r = 0; r < NCOEF; r++) {
+#pragma unroll
+                for (int h = 0; h < GM; h++) acc[r][h] *= alpha[h];
+                const int j = tid + NT * r;
+                if (j >= ns + nt) continue;
+                int byte0, bit0, bits;
+                float offv;
+                const float *wrow;
+                if (j < ns) {
+                    int b = 0;
+                    while (b + 1 < nb && j >= P.band_off[b + 1]) b++;
+                    bits = P.band_bits[b];
+                    const int bo = (j - P.band_off[b]) * bits;
+                    byte0 = P.band_byte_off[b] + 2 + (bo >> 3);
+                    bit0 = bo & 7;
+                    offv = (float)((1 << (bits - 1)) - 1);
+                    wrow = psb + b * G * CH;
+                } else {
+                    bits = A.rbits;
+                    const int bo = (j - ns) * bits;
+                    byte0 = skB + 4 + (bo >> 3);
+                    bit0 = bo & 7;
+                    offv = centre;
+                    wrow = pw;
+                }
+#pragma unroll 4
+                for (int t = 0; t < n_t; t++) {
+                    const float cv = (float)lds_bits_at(rec, vshift + t * B + byte0, bit0, bits) - offv;
+#pragma unroll
+                    for (int h = 0; h < GM; h++)
+                        if (h < G) acc[r][h] = fmaf(wrow[h * CH + t], cv, acc[r][h]);
+                }
+            }
+        }
+    }
+    if (!want_out) return;
+    // ---- the run's partial per query head ----
+    const int pp = A.pp;
+    if (tid == 0) {
+        for (int h = 0; h < G; h++) {
+            float *dst = part + ((long long)(h0 + h) * n_runs + run) * pp;
+            dst[0] = m_run[h];
+            dst[1] = l_run[h];
+        }
+    }
+    if (RB > 0) {
+        // position groups' sums through LDS: T [npg_t][G][n_win * LPW], S [npg_s][G][ns]
+        const int tw = n_win * LPW;
+        float *T = reinterpret_cast<float *>(dsm);
+        float *S = T + npg_t * G * tw;
+        __syncthreads();  // the last chunk is done with the staging memory
+        if (t_on) {
+#pragma unroll
+            for (int k = 0; k < LPW; k++) T[(t_pg * G + t_ha) * tw + t_w * LPW + k] = fmaf(-centre, twsum[0], tacc[k][0]);
+            if (t_hb != t_ha) {
+#pragma unroll
+                for (int k = 0; k < LPW; k++)
+                    T[(t_pg * G + t_hb) * tw + t_w * LPW + k] = fmaf(-centre, twsum[1], tacc[k][1]);
+            }
+        }
+        if (s_on) {
+            S[(s_pg * G + s_ha) * ns + s_s] = sacc[0];
+            if (s_hb != s_ha) S[(s_pg * G + s_hb) * ns + s_s] = sacc[1];
+        }
+        __syncthreads();
+        for (int i = tid; i < G * (ns + nt); i += NT) {
+            const int h = i / (ns + nt), j = i - h * (ns + nt);
+            float v = 0.0f;
+            if (j < ns)
+                for (int g = 0; g < npg_s; g++) v += S[(g * G + h) * ns + j];
+            else
+                for (int g = 0; g < npg_t; g++) v += T[(g * G + h) * tw + (j - ns)];
+            part[((long long)(h0 + h) * n_runs + run) * pp + 4 + j] = v;
+        }
+    } else {
+        for (int h = 0; h < G; h++) {
+            float *dst = part + ((long long)(h0 + h) * n_runs + run) * pp;
+#pragma unroll
+            for (int r = 0; r < NCOEF; r++) {
+                const int j = tid + NT * r;
+                if (j < ns + nt) dst[4 + j] = acc[r][h];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Merge of the runs' partials for query head blockIdx.x, then c and its transform.
+// Dynamic LDS: c[pad], cs[n_skel], e[n_runs] floats, then the KV head's W fp16.
+__global__ void __launch_bounds__(NT)
+k_hier_attn_merge(const SpPlan P, const SpHierAttnArgs A, const float *__restrict__ part, int n_runs) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char dsm[];
+    __shared__ float red[2 * (NT / SP_WAVE)];
+    __shared__ float cas_s[SP_CAS_TOTAL];
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int G = A.n_q / A.n_kvh, kvh = h / G;
+    const int ns = A.n_skel, nt = A.n_target, pp = A.pp;
+    float *c = reinterpret_cast<float *>(dsm);
+    float *cs = c + r4(A.pad);
+    float *e = cs + r4(ns);
+    unsigned short *Ws = reinterpret_cast<unsigned short *>(e + r4(n_runs));
+    const unsigned short *Wk = reinterpret_cast<const unsigned short *>(A.W) + (long long)kvh * A.w_outer;
+    copy_to_lds<unsigned short, 16>(Ws, Wk, nt * ns, nt * ns, tid);
+    const float *ph = part + (long long)h * n_runs * pp;
+    float mx = -INFINITY;
+    for (int r = tid; r < n_runs; r += NT) mx = fmaxf(mx, ph[(long long)r * pp]);
+    mx = sp_wave_max(mx);
+    if (lane == 0) red[wv] = mx;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float l = 0.0f;
+    for (int r = tid; r < n_runs; r += NT) {
+        const float w = __expf(ph[(long long)r * pp] - M);  // 0 for a run without positions (m = -inf)
+        e[r] = w;
+        l = fmaf(ph[(long long)r * pp + 1], w, l);
+    }
+    l = wave_sum(l);
+    if (lane == 0) red[NT / SP_WAVE + wv] = l;
+    __syncthreads();
+    const float inv_l = sp_div(1.0f, (red[4] + red[5]) + (red[6] + red[7]));
+    for (int k = tid; k < A.pad; k += NT) c[k] = 0.0f;
+    __syncthreads();
+    for (int j = tid; j < ns + nt; j += NT) {
+        // 32 runs' values in flight per batch (the last batch re-reads run 0 with weight 0)
+        float s = 0.0f;
+        for (int r0 = 0; r0 < n_runs; r0 += 32) {
+            float v[32];
+#pragma unroll
+            for (int k = 0; k < 32; k++) v[k] = ph[(long long)(r0 + k < n_runs ? r0 + k : 0) * pp + 4 + j];
+#pragma unroll
+            for (int k = 0; k < 32; k++) s = fmaf(v[k], r0 + k < n_runs ? e[r0 + k] : 0.0f, s);
+        }
+        s *= inv_l;
+        if (j < ns) {
+            cs[j] = s;
+            c[A.skel_idx[j]] = s;
+        } else {
+            c[A.tgt_idx[j - ns]] = s;  // the dev part; W c_skel is added below
+        }
+    }
+    __syncthreads();
+    for (int t = tid; t < nt; t += NT) {
+        float pred = 0.0f;
+#pragma unroll 4
+        for (int s = 0; s < ns; s++) pred = fmaf(sp_f16_bits_to_f32(Ws[t * ns + s]), cs[s], pred);
+        c[A.tgt_idx[t]] += pred;
+    }
+    __syncthreads();
+    transform_block(c, A.pad, P, cas_s, tid);
+    for (int k = tid; k < A.hd; k += NT) A.out[(long long)h * A.hd + k] = c[k];
+}
+
+// Level width of the window path for this call (0: bit-serial): the windows and
+// skeleton coefficients of a head pair must each fit the block once.
+int window_bits(const SpHierAttnArgs &A) {
+    const int rb = A.rbits;
+    if (rb != 2 && rb != 4 && rb != 8) return 0;
+    const int n_hp = (A.n_q / A.n_kvh + 1) / 2;
+    if ((A.n_target * rb + 31) / 32 * n_hp > NT || A.n_skel * n_hp > NT) return 0;
+    return rb;
+}
+
+}  // namespace
+
+int sp_hier_attn_prep_floats(int n_skel, int n_target) { return prep_sum_off(n_skel, n_target) + 4; }
+
+size_t sp_hier_attn_workspace_floats(const SpHierAttnArgs &A, int n_runs) {
+    return (size_t)A.n_q * A.ps + (size_t)A.n_q * n_runs * A.pp;
+}
+
+// Runs per KV head: the blocks that are resident at once (three per CU) spread
+// over the KV heads, so the split kernel runs in one round.
+int sp_hier_attn_runs(const SpHierAttnArgs &A, int cus) {
+    const int n_chunks = (A.n_kv + CH - 1) / CH;
+    const int per_head = std::max(1, (3 * cus) / std::max(1, A.n_kvh));
+    return std::max(1, std::min(n_chunks, per_head));
+}
+
+hipError_t sp_launch_hier_attn(const SpPlan &P, const SpHierAttnArgs &A, float *ws, size_t ws_floats, int n_runs,
+                               hipStream_t s) {
+    if (A.n_kv <= 0 || A.n_q <= 0 || A.n_kvh <= 0 || A.n_q % A.n_kvh || A.n_q / A.n_kvh > MAX_G ||
+        A.pad > SP_GEN_MAX_N || A.n_skel + A.n_target > SP_GEN_MAX_N || A.hd > A.pad || n_runs <= 0 ||
+        A.ps != sp_hier_attn_prep_floats(A.n_skel, A.n_target) || A.pp < 4 + A.n_skel + A.n_target)
+        return hipErrorInvalidValue;
+    if (sp_hier_attn_workspace_floats(A, n_runs) > ws_floats) return hipErrorInvalidValue;
+    const int G = A.n_q / A.n_kvh;
+    const int rb = window_bits(A);
+    const size_t lds_prep = 4 * (size_t)(r4(A.pad) + r32(A.n_target) + 8 * r4(A.n_skel)) +
+                            2 * (size_t)A.n_target * A.n_skel;
+    const size_t rec_bytes = (size_t)(((CH * A.B + 32) + 15) & ~15);
+    size_t lds_split = rec_bytes + 4 * ((size_t)G * A.ps + (size_t)(2 + P.n_bands) * G * CH + 8 * MAX_G);
+    if (rb == 2) lds_split += (size_t)r32(A.n_target) / 32 * 1024 + 4 * (16 + 16 + 8 + 256);
+    if (rb > 0) {
+        const int n_win = (A.n_target * rb + 31) / 32, n_hp = (G + 1) / 2;
+        const int npg_t = std::max(1, NT / (n_win * n_hp)), npg_s = std::max(1, NT / (A.n_skel * n_hp));
+        const size_t red_b = 4 * ((size_t)npg_t * G * n_win * (32 / rb) + (size_t)npg_s * G * A.n_skel);
+        lds_split = std::max(lds_split, red_b);
+    }
+    const size_t lds_merge = 4 * (size_t)(r4(A.pad) + r4(A.n_skel) + r4(n_runs)) + 2 * (size_t)A.n_target * A.n_skel;
+    if (lds_prep > 65536 || lds_split > 65536 || lds_merge > 65536) return hipErrorInvalidValue;
+    float *prep = ws;
+    float *part = ws + (size_t)A.n_q * A.ps;
+    hipLaunchKernelGGL(k_hier_attn_prep, dim3(A.n_q), dim3(NT), lds_prep, s, P, A, prep);
+    const dim3 grid(A.n_kvh, n_runs);
+    if (rb == 2 && G <= 2)
+        hipLaunchKernelGGL((k_hier_attn_split<2, 2>), grid, dim3(NT), lds_split, s, P, A, prep, part, n_runs);
+    else if (rb == 2)
+        hipLaunchKernelGGL((k_hier_attn_split<2, MAX_G>), grid, dim3(NT), lds_split, s, P, A, prep, part, n_runs);
+    else if (rb == 4)
+        hipLaunchKernelGGL((k_hier_attn_split<4, MAX_G>), grid, dim3(NT), lds_split, s, P, A, prep, part, n_runs);
+    else if (rb == 8)
+        hipLaunchKernelGGL((k_hier_attn_split<8, MAX_G>), grid, dim3(NT), lds_split, s, P, A, prep, part, n_runs);
+    else
+        hipLaunchKernelGGL((k_hier_attn_split<0, MAX_G>), grid, dim3(NT), lds_split, s, P, A, prep, part, n_runs);
+    if (A.out) hipLaunchKernelGGL(k_hier_attn_merge, dim3(A.n_q), dim3(NT), lds_merge, s, P, A, part, n_runs);
+    return hipGetLastError();
+}

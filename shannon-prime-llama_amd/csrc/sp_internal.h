@@ -209,6 +209,27 @@ struct SpHierGeo {
     int default_geo;         // skeleton/targets are sp_hier_default_geometry's
 };
 
+// Fused decode attention over hier records (sp_hier_attn.hip).
+struct SpHierAttnArgs {
+    const unsigned char *kcache, *vcache;  // records of slot (layer, KV head 0); KV head h at + h * slot_bytes
+    long long slot_bytes;
+    const uint16_t *W;                     // predictor of slot (layer, KV head 0); KV head h at + h * w_outer
+    long long w_outer;
+    const int *skel_idx, *tgt_idx;
+    const float *q;                        // [n_q][hd]
+    float kq_scale;
+    float *scores;                         // [n_q][n_kv] or null
+    float *out;                            // [n_q][hd] or null
+    int n_q, n_kvh, n_kv, hd, pad, n_skel, n_target, rbits, B;
+    int ps;                                // floats per query head of the prepared query
+    int pp;                                // floats per (query head, run) partial
+};
+int sp_hier_attn_prep_floats(int n_skel, int n_target);  // the value SpHierAttnArgs::ps must hold
+size_t sp_hier_attn_workspace_floats(const SpHierAttnArgs &A, int n_runs);
+int sp_hier_attn_runs(const SpHierAttnArgs &A, int cus);
+hipError_t sp_launch_hier_attn(const SpPlan &P, const SpHierAttnArgs &A, float *ws, size_t ws_floats, int n_runs,
+                               hipStream_t s);
+
 // one-vector-per-lane hier kernels for the default geometry at head_dim 256;
 // hipErrorNotSupported (nothing launched) when no specialization fits
 hipError_t sp_launch_hier_encode_lane(const SpPlan &P, const SpHierGeo &G, const void *src, int dtype, long long so,

@@ -1227,6 +1227,9 @@ struct HierPriv {
     double *d_acc = nullptr;   // [n_slots][n_ent]
     double *d_part = nullptr;  // [256][n_ent] block partials of one feed
     std::vector<long long> n_fed;
+    // fused attention: prepared queries and the runs' partials (grown on demand)
+    float *d_attn_ws = nullptr;
+    size_t attn_ws_floats = 0;
 };
 
 static void hier_calib_release(HierPriv *pv) {
@@ -1296,7 +1299,10 @@ extern "C" void sp_hip_hier_cache_free(sp_hip_hier_cache_t *hc) {
     void *ptrs[] = {hc->d_W, hc->d_skeleton_idx, hc->d_target_idx, hc->d_k_cache, hc->d_v_cache};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
-    if (hc->priv) hier_calib_release((HierPriv *)hc->priv);
+    if (hc->priv) {
+        hier_calib_release((HierPriv *)hc->priv);
+        if (((HierPriv *)hc->priv)->d_attn_ws) (void)hipFree(((HierPriv *)hc->priv)->d_attn_ws);
+    }
     delete (HierPriv *)hc->priv;
     memset(hc, 0, sizeof(*hc));
 }
@@ -1389,6 +1395,65 @@ extern "C" int sp_hip_hier_read_layer(const sp_hip_hier_cache_t *hc, int layer, 
                     "hier read_layer")) return -1;
     }
     return 0;
+}
+
+extern "C" int sp_hip_hier_attn_decode(const sp_hip_hier_cache_t *hc, int layer, int n_kv, const float *d_q,
+                                       int n_q, float kq_scale, float *d_scores, float *d_out, void *stream) {
+    if (!hier_slot_ok(hc, layer, 0, 0, n_kv) || n_kv <= 0 || !d_q || n_q <= 0 || (!d_scores && !d_out) ||
+        (long long)(layer + 1) * hc->config.n_heads_kv > hc->n_slots) {
+        set_err("hier attn: bad args");
+        return -1;
+    }
+    const int H = hc->config.n_heads_kv;
+    if (n_q % H || n_q / H > 8) { set_err("hier attn: n_q must be a multiple of n_heads_kv, at most 8 per KV head"); return -1; }
+    HierPriv *pv = (HierPriv *)hc->priv;
+    const SpHierGeo G = hier_geo(hc, layer * H);
+    SpHierAttnArgs A;
+    A.kcache = hc->d_k_cache + (long long)layer * H * hc->max_seq_len * G.bytes;
+    A.vcache = hc->d_v_cache + (long long)layer * H * hc->max_seq_len * G.bytes;
+    A.slot_bytes = (long long)hc->max_seq_len * G.bytes;
+    A.W = G.W;
+    A.w_outer = G.w_outer;
+    A.skel_idx = G.skel_idx;
+    A.tgt_idx = G.target_idx;
+    A.q = d_q;
+    A.kq_scale = kq_scale;
+    A.scores = d_scores;
+    A.out = d_out;
+    A.n_q = n_q;
+    A.n_kvh = H;
+    A.n_kv = n_kv;
+    A.hd = hc->config.head_dim;
+    A.pad = hc->pad_dim;
+    A.n_skel = hc->n_skeleton;
+    A.n_target = hc->n_target;
+    A.rbits = hc->target_res_bits;
+    A.B = G.bytes;
+    A.ps = sp_hier_attn_prep_floats(A.n_skel, A.n_target);
+    A.pp = (4 + A.n_skel + A.n_target + 3) & ~3;
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    int n_runs = sp_hier_attn_runs(A, cus);
+    // SP_HIP_HIER_ATTN_RUNS=n caps the runs per KV head (read at each call; tests use it to
+    // give every run several chunks at small context lengths)
+    if (const char *e = getenv("SP_HIP_HIER_ATTN_RUNS")) {
+        const int r = atoi(e);
+        if (r > 0) n_runs = std::min(n_runs, r);
+    }
+    const size_t need = sp_hier_attn_workspace_floats(A, n_runs);
+    const hipStream_t s = (hipStream_t)(stream ? stream : hc->stream);
+    if (need > pv->attn_ws_floats) {
+        if (pv->d_attn_ws) {
+            if (!hip_ok(hipStreamSynchronize(s), "hier attn: sync before growing the workspace")) return -1;
+            (void)hipFree(pv->d_attn_ws);
+            pv->d_attn_ws = nullptr;
+            pv->attn_ws_floats = 0;
+        }
+        if (!hip_ok(hipMalloc((void **)&pv->d_attn_ws, need * sizeof(float)), "hipMalloc hier attn workspace")) return -1;
+        pv->attn_ws_floats = need;
+    }
+    return hip_ok(sp_launch_hier_attn(pv->plan, A, pv->d_attn_ws, pv->attn_ws_floats, n_runs, s), "hier attn") ? 0 : -1;
 }
 
 extern "C" int sp_hip_hier_calibrate_begin(sp_hip_hier_cache_t *hc) {

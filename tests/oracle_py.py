@@ -298,6 +298,22 @@ def attn_decode(q, kpack, vpack, n_kvh, n_ctx, kbc, vbc, order, kq_scale, norm=N
     return scores, out
 
 
+def hier_attn_decode(q, kpack, vpack, n_kvh, n_ctx, hd, pad, skel_idx, tgt_idx, skel_bc, W, rbits, kq_scale,
+                     want_scores=True, want_out=True):
+    """spo_hier_attn_decode: kpack/vpack [n_kvh][n_ctx][B] uint8, W [n_kvh][n_target][n_skel] fp16 bits."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    n_q = q.shape[0]
+    scores = np.zeros((n_q, n_ctx), np.float32) if want_scores else None
+    out = np.zeros((n_q, hd), np.float32) if want_out else None
+    s = np.ascontiguousarray(skel_idx, dtype=np.int32)
+    t = np.ascontiguousarray(tgt_idx, dtype=np.int32)
+    w = np.ascontiguousarray(W, dtype=np.uint16)
+    lib().spo_hier_attn_decode(ptr(q), ptr(np.ascontiguousarray(kpack)), ptr(np.ascontiguousarray(vpack)),
+                               n_q, n_kvh, n_ctx, hd, pad, len(s), ptr(s), len(t), ptr(t), C.byref(skel_bc),
+                               ptr(w), rbits, C.c_float(kq_scale), ptr(scores), ptr(out))
+    return scores, out
+
+
 def correlation(a, b):
     a = np.ascontiguousarray(a, dtype=np.float32).ravel()
     b = np.ascontiguousarray(b, dtype=np.float32).ravel()
