@@ -89,6 +89,39 @@ def test_fused_attention_matches_oracle(n_q, H, n_ctx, hd, mob, path, monkeypatc
     cc.free()
 
 
+@pytest.mark.parametrize("n_q,H,n_ctx,k_bits,v_bits", [
+    (32, 32, 300, (5, 4, 4), (5,)),      # configs[2] (Phi-3-mini, MHA) at the bridge's hd-96 bands
+    (16, 4, 1037, (5, 5, 4, 3), (3,)),   # the shipping bands at hd 96, GQA 4
+])
+def test_hd96_attention_matches_oracle(n_q, H, n_ctx, k_bits, v_bits):
+    """head_dim 96 (Vilenkin 2^5 * 3) through the general kernel: scores and output
+    within 1e-3 of the oracle, several splits and a ragged last one."""
+    hd = 96
+    say(f"attn hd96 n_q={n_q} H={H} n_ctx={n_ctx} k={k_bits} v={v_bits}")
+    k16, v16 = W.cfg3_kv(n_heads=H, n_pos=n_ctx, hd=hd, seed=n_ctx)
+    q = W.cfg2_q(n_q=n_q, hd=hd, pos=n_ctx, seed=n_ctx + 1)
+    cfg = S.config(hd, 1, H, k_bits=k_bits, v_bits=v_bits)
+    cc = S.ShipCache(cfg, n_ctx, stream=torch.cuda.current_stream().cuda_stream)
+    for h in range(H):
+        kt, vt = dev(k16[h].view(np.uint16)), dev(v16[h].view(np.uint16))
+        S.lib().sp_hip_write_k_batch_f16(cc.ref, 0, h, 0, n_ctx, p(kt))
+        S.lib().sp_hip_write_v_batch_f16(cc.ref, 0, h, 0, n_ctx, p(vt))
+    torch.cuda.synchronize()
+    kbc, vbc = O.band_config(hd, list(k_bits)), O.band_config(hd, list(v_bits))
+    order = O.mobius_order(hd)
+    kref = np.stack([O.ship_compress_f16(k16[h].view(np.uint16), kbc, order) for h in range(H)])
+    vref = np.stack([O.ship_compress_f16(v16[h].view(np.uint16), vbc) for h in range(H)])
+    scale = 1.0 / math.sqrt(hd)
+    s_ref, o_ref = O.attn_decode(q, kref, vref, H, n_ctx, kbc, vbc, order, scale)
+    qt = dev(q)
+    sc, out = empty_f32(n_q * n_ctx), empty_f32(n_q * hd)
+    S.check(S.lib().sp_hip_attn_decode(cc.ref, 0, n_ctx, p(qt), n_q, C.c_float(scale), p(sc), p(out), stream()))
+    torch.cuda.synchronize()
+    rel_close(host(sc).reshape(n_q, n_ctx), s_ref)
+    rel_close(host(out).reshape(n_q, hd), o_ref)
+    cc.free()
+
+
 @pytest.mark.parametrize("path", ["mfma", "general"])
 @pytest.mark.parametrize("n_q,H,n_ctx", [(8, 2, 300), (32, 8, 1100)])
 def test_band_limited_attention_matches_oracle(n_q, H, n_ctx, path, monkeypatch):

@@ -58,6 +58,7 @@ CASES = [
     (64, 3, [5, 4], 2, 2, 517, 1),      # pad 66, 3-bit levels straddling bytes, one run of 3 chunks
     (96, 2, [4], 2, 6, 257, 0),         # pad 105, GQA 3 (odd: a lone last head), 1-position last chunk
     (256, 2, [5, 5], 1, 1, 1, 0),       # a single position
+    (256, 2, [5, 5], 8, 16, 2000, 3),   # configs[4] head layout (8 KV heads, GQA 2), 3 runs of 2-3 chunks
 ]
 
 
