@@ -70,6 +70,28 @@ __device__ __forceinline__ void copy_to_lds(T *dst, const T *__restrict__ src, i
     }
 }
 
+// Up to U * NT elements staged through registers: the loads go out first (load),
+// the LDS stores come later (store), so other work hides the loads' latency.
+template <typename T, int U>
+struct RegStage {
+    T v[U];
+    __device__ void load(const T *__restrict__ src, int n, int tid) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = tid + u * NT;
+            v[u] = i < n ? src[i] : T(0);
+        }
+    }
+    __device__ void store(T *dst, int n, int tid) const {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = tid + u * NT;
+            if (i < n) dst[i] = v[u];
+        }
+    }
+};
+constexpr int W_STAGE = 40;  // W elements per thread staged through registers (n_target * n_skel <= 10240)
+
 // 4 little-endian bytes at LDS byte offset o (any alignment) of a dword-aligned array.
 __device__ __forceinline__ uint32_t lds_u32_at(const unsigned char *base, int o) {
     const uint32_t *w = reinterpret_cast<const uint32_t *>(base + (o & ~3));
@@ -216,11 +238,23 @@ k_hier_attn_prep(const SpPlan P, const SpHierAttnArgs A, float *__restrict__ pre
     float *part = qt + nt32;
     unsigned short *Ws = reinterpret_cast<unsigned short *>(part + 8 * ns4);
     const unsigned short *Wk = reinterpret_cast<const unsigned short *>(A.W) + (long long)kvh * A.w_outer;
-    copy_to_lds<unsigned short, 16>(Ws, Wk, nt * ns, nt * ns, tid);
+    // W and the target indices load while the query is transformed
+    const bool w_reg = nt * ns <= W_STAGE * NT;
+    RegStage<unsigned short, W_STAGE> wst;
+    if (w_reg) wst.load(Wk, nt * ns, tid);
+    else copy_to_lds<unsigned short, 16>(Ws, Wk, nt * ns, nt * ns, tid);
+    int ti[(SP_GEN_MAX_N + NT - 1) / NT];
+#pragma unroll
+    for (int u = 0; u < (SP_GEN_MAX_N + NT - 1) / NT; u++) ti[u] = tid + u * NT < nt ? A.tgt_idx[tid + u * NT] : 0;
     for (int k = tid; k < A.pad; k += NT) c[k] = k < A.hd ? A.q[(long long)h * A.hd + k] : 0.0f;
     __syncthreads();
     transform_block(c, A.pad, P, cas_s, tid);
-    for (int t = tid; t < nt32; t += NT) qt[t] = t < nt ? A.kq_scale * c[A.tgt_idx[t]] : 0.0f;
+    if (w_reg) wst.store(Ws, nt * ns, tid);
+#pragma unroll
+    for (int u = 0; u < (SP_GEN_MAX_N + NT - 1) / NT; u++) {
+        const int t = tid + u * NT;
+        if (t < nt32) qt[t] = t < nt ? A.kq_scale * c[ti[u]] : 0.0f;
+    }
     __syncthreads();
     // W^T q~_tgt in 8 interleaved partial sums per skeleton coefficient
     for (int i = tid; i < 8 * ns; i += NT) {
@@ -688,7 +722,11 @@ k_hier_attn_merge(const SpPlan P, const SpHierAttnArgs A, const float *__restric
     float *e = cs + r4(ns);
     unsigned short *Ws = reinterpret_cast<unsigned short *>(e + r4(n_runs));
     const unsigned short *Wk = reinterpret_cast<const unsigned short *>(A.W) + (long long)kvh * A.w_outer;
-    copy_to_lds<unsigned short, 16>(Ws, Wk, nt * ns, nt * ns, tid);
+    // W loads while the partials are merged
+    const bool w_reg = nt * ns <= W_STAGE * NT;
+    RegStage<unsigned short, W_STAGE> wst;
+    if (w_reg) wst.load(Wk, nt * ns, tid);
+    else copy_to_lds<unsigned short, 16>(Ws, Wk, nt * ns, nt * ns, tid);
     const float *ph = part + (long long)h * n_runs * pp;
     float mx = -INFINITY;
     for (int r = tid; r < n_runs; r += NT) mx = fmaxf(mx, ph[(long long)r * pp]);
@@ -709,14 +747,14 @@ k_hier_attn_merge(const SpPlan P, const SpHierAttnArgs A, const float *__restric
     for (int k = tid; k < A.pad; k += NT) c[k] = 0.0f;
     __syncthreads();
     for (int j = tid; j < ns + nt; j += NT) {
-        // 32 runs' values in flight per batch (the last batch re-reads run 0 with weight 0)
+        // 48 runs' values in flight per batch (the last batch re-reads run 0 with weight 0)
         float s = 0.0f;
-        for (int r0 = 0; r0 < n_runs; r0 += 32) {
-            float v[32];
+        for (int r0 = 0; r0 < n_runs; r0 += 48) {
+            float v[48];
 #pragma unroll
-            for (int k = 0; k < 32; k++) v[k] = ph[(long long)(r0 + k < n_runs ? r0 + k : 0) * pp + 4 + j];
+            for (int k = 0; k < 48; k++) v[k] = ph[(long long)(r0 + k < n_runs ? r0 + k : 0) * pp + 4 + j];
 #pragma unroll
-            for (int k = 0; k < 32; k++) s = fmaf(v[k], r0 + k < n_runs ? e[r0 + k] : 0.0f, s);
+            for (int k = 0; k < 48; k++) s = fmaf(v[k], r0 + k < n_runs ? e[r0 + k] : 0.0f, s);
         }
         s *= inv_l;
         if (j < ns) {
@@ -726,6 +764,7 @@ k_hier_attn_merge(const SpPlan P, const SpHierAttnArgs A, const float *__restric
             c[A.tgt_idx[j - ns]] = s;  // the dev part; W c_skel is added below
         }
     }
+    if (w_reg) wst.store(Ws, nt * ns, tid);
     __syncthreads();
     for (int t = tid; t < nt; t += NT) {
         float pred = 0.0f;
