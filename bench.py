@@ -360,6 +360,45 @@ def bench_variants(torch, S, L, stream, reps=3):
                         "dec": rate(H5 * N5, hd5, B5, timed(hi_read)),
                         "record_bytes": B5, "pad_dim": pad5, "skeleton": n_sk,
                         "calls": f"1 layer x {H5} heads x {N5} positions, one call (K)"}
+    # the reference caller's per-vector hook path through the bridge (host pointers): one
+    # sp_llama_write_k / write_v / read_k / read_v per vector, each an H2D or D2H copy, a launch
+    # and a stream sync (the Python call overhead, ~1 us, is included)
+    saved = {k: os.environ.get(k) for k in ("SHANNON_PRIME_ENABLED", "SHANNON_PRIME_BACKEND")}
+    os.environ["SHANNON_PRIME_ENABLED"] = "1"
+    os.environ["SHANNON_PRIME_BACKEND"] = "hip"
+    try:
+        prm = S.SpLlamaParams(128, 2, 8, 4096, S.BACKEND_HIP, None, None)
+        ctx = L.sp_llama_init(C.byref(prm))
+        if ctx:
+            vec = np.random.default_rng(3).standard_normal((64, 128)).astype(np.float32)
+            outv = np.empty(128, np.float32)
+            fp = lambda a: a.ctypes.data_as(C.POINTER(C.c_float))
+            n_calls = 256
+            times = {}
+            for name, call in (("write_k", lambda i: L.sp_llama_write_k(ctx, 1, i % 8, i, fp(vec[i % 64]))),
+                               ("write_v", lambda i: L.sp_llama_write_v(ctx, 1, i % 8, i, fp(vec[i % 64]))),
+                               ("read_k", lambda i: L.sp_llama_read_k(ctx, 1, i % 8, i, fp(outv))),
+                               ("read_v", lambda i: L.sp_llama_read_v(ctx, 1, i % 8, i, fp(outv)))):
+                # the first calls load each kernel's code object (records at odd positions of a
+                # 50 B V record are not 16 B aligned and take the row kernel): keep them untimed
+                for i in range(8):
+                    call(i)
+                t0 = time.perf_counter()
+                for i in range(n_calls):
+                    call(i)
+                times[name] = (time.perf_counter() - t0) / n_calls * 1e6
+            L.sp_llama_free(ctx)
+            per_tok = 32 * 8 * (times["write_k"] + times["write_v"] + times["read_k"] + times["read_v"])
+            out["cfg1_hook_per_vector"] = {
+                "us_per_call": {k: round(v, 2) for k, v in times.items()},
+                "us_per_token_32x8_write_and_read": round(per_tok, 1),
+                "layout": "bridge backend hip, hd 128, one fp32 vector per call (host pointer), synchronous"}
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
     # configs[4] fused decode attention over hier records: one sequence's layer at 131072
     # positions x 8 KV heads (K and V from the rows above), 16 query heads (GQA 2)
     NA, NQ5 = 131072, 16

@@ -490,6 +490,39 @@ __device__ __forceinline__ void tile_rows_stage(const void *src, long long so, l
     __syncthreads();
 }
 
+// The same in two halves, so a tile's loads can be in flight while the previous
+// tile computes: tile_rows_load issues the wave-wide loads into registers,
+// tile_rows_put stores them to the LDS rows and hands lane j its row.
+template <int DT, int HD>
+__device__ __forceinline__ void tile_rows_load(const void *src, long long so, long long si, const TileMap &M, int t,
+                                               int lane, u32x4 (&v)[row_bytes<DT>(HD) / 16]) {
+    constexpr int RB = row_bytes<DT>(HD), CPR = RB / 16, esz = DT == SP_DT_F16 ? 2 : 4;
+    const int rowb = (int)(si * esz);
+    int o, i0, nv;
+    M.at(t, o, i0, nv);
+    const unsigned char *g = reinterpret_cast<const unsigned char *>(src) + ((long long)o * so + (long long)i0 * si) * esz;
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(g, (nv - 1) * rowb + RB);
+#pragma unroll
+    for (int k = 0; k < CPR; k++) {
+        const TileChunk<CPR> ch(k, lane);
+        v[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, ch.vofs(rowb), ch.sofs(rowb), BUF_NT);
+    }
+}
+template <int DT, int HD>
+__device__ __forceinline__ void tile_rows_put(const u32x4 (&v)[row_bytes<DT>(HD) / 16], int lane, unsigned char *rows,
+                                              uint4 (&in)[row_bytes<DT>(HD) / 16]) {
+    constexpr int RP = row_bytes<DT>(HD) + 16, CPR = row_bytes<DT>(HD) / 16;
+    __syncthreads();  // the previous tile's reads of the rows are done
+#pragma unroll
+    for (int k = 0; k < CPR; k++) {
+        const TileChunk<CPR> ch(k, lane);
+        *reinterpret_cast<u32x4 *>(rows + ch.lds(RP)) = v[k];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < CPR; c++) in[c] = *reinterpret_cast<const uint4 *>(rows + lane * RP + c * 16);
+}
+
 template <int DT, int HD>
 __device__ __forceinline__ void tile_rows_in(const void *src, long long so, long long si, const TileMap &M, int t,
                                              int lane, unsigned char *rows, uint4 (&in)[row_bytes<DT>(HD) / 16]) {
@@ -639,19 +672,24 @@ __device__ __forceinline__ void tile_rows_out(const float (&x)[N], unsigned char
 // ---- host side ----
 // Persistent grid size: enough single-wave blocks for several resident waves
 // per SIMD on every CU (queried once per process).
-int persistent_blocks() {
-    static int n = 0;
-    if (n == 0) {
-        int dev = 0, cus = 256;
+int device_cu_count() {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0, n = 256;
         if (hipGetDevice(&dev) == hipSuccess) {
             hipDeviceProp_t prop;
             if (hipGetDeviceProperties(&prop, dev) == hipSuccess && prop.multiProcessorCount > 0)
-                cus = prop.multiProcessorCount;
+                n = prop.multiProcessorCount;
         }
-        n = cus * 16;
+        cus = n;
     }
-    return n;
+    return cus;
 }
+int persistent_blocks() { return device_cu_count() * 16; }
+// Single-wave blocks that are resident at once for a kernel that fits `waves_per_simd`
+// waves on a SIMD: a grid of that size keeps every block walking several tiles, so a
+// tile's loads overlap the previous tile's compute.
+int resident_blocks(int waves_per_simd) { return device_cu_count() * 4 * waves_per_simd; }
 
 // Kernel constants from the host plan: cas[pi][m] is row 1 of the plan's p x p
 // table (C[1][m] = cas(2*pi*m/p)), which holds every value C[k][j] takes.

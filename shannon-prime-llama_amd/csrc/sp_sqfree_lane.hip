@@ -104,9 +104,13 @@ k_sqfree_encode_lane(const void *__restrict__ src, long long so, long long si, u
     __shared__ __attribute__((aligned(16))) unsigned char rows[64 * RP];  // input rows, then the record stage
     const int lane = threadIdx.x;
     const TileMap M{tiles_per_outer, n_inner};
+    // the next tile's rows are in flight while this one computes
+    u32x4 pre[CPR];
+    if (blockIdx.x < n_tiles) tile_rows_load<DT, HD>(src, so, si, M, blockIdx.x, lane, pre);
     for (int t = blockIdx.x; t < n_tiles; t += gridDim.x) {
         uint4 in[CPR];
-        tile_rows_in<DT, HD>(src, so, si, M, t, lane, rows, in);
+        tile_rows_put<DT, HD>(pre, lane, rows, in);
+        if (t + (int)gridDim.x < n_tiles) tile_rows_load<DT, HD>(src, so, si, M, t + gridDim.x, lane, pre);
         float c[PAD];
         float mx = 0.0f;
 #pragma unroll
@@ -294,7 +298,8 @@ hipError_t sq_enc_launch(const SpPlan &P, const void *src, long long so, long lo
     const long long n_tiles = (long long)n_outer * tpo;
     constexpr long long esz = DT == SP_DT_F16 ? 2 : 4;
     if (n_tiles > 0x7fffffffLL || si < 128 || 64 * si * esz + 128 * esz > 0x7fffffffLL) return hipErrorNotSupported;
-    const dim3 grid((unsigned)std::min<long long>(n_tiles, persistent_blocks())), block(64);
+    // one wave per SIMD fits (~330-460 registers): a resident grid, each block prefetching
+    const dim3 grid((unsigned)std::min<long long>(n_tiles, resident_blocks(1))), block(64);
     hipLaunchKernelGGL((k_sqfree_encode_lane<DT, 128, 154, SK, 3, true, SL>), grid, block, 0, s, src, so, si, dst,
                        dout, n_inner, tpo, (int)n_tiles, xf_const(P));
     return hipGetLastError();
