@@ -79,23 +79,33 @@ __device__ __forceinline__ void rec_insert(uint32_t (&rec)[DW], int pos, int w, 
     if (sh + w > 32) rec[d + 1] |= val >> (32 - sh);
 }
 
-// Overwrite the w-bit field at bit position pos with val (val < 2^w).
+// Add val << pos into the record words (val < 2^w, the field's bits zero before):
+// with disjoint fields, addition is insertion, and a chain of these folds into
+// one shift-and-add per field.
 template <int DW>
-__device__ __forceinline__ void rec_replace(uint32_t (&rec)[DW], int pos, int w, uint32_t val) {
+__device__ __forceinline__ void rec_add(uint32_t (&rec)[DW], int pos, int w, uint32_t val) {
     const int d = pos / 32, sh = pos % 32;
-    const uint32_t mask = (1u << w) - 1u;
-    rec[d] = (rec[d] & ~(mask << sh)) | (val << sh);
-    if (sh + w > 32) rec[d + 1] = (rec[d + 1] & ~(mask >> (32 - sh))) | (val >> (32 - sh));
+    rec[d] += val << sh;
+    if (sh + w > 32) rec[d + 1] += val >> (32 - sh);
 }
 
-// Insert the low w bits of v (higher bits are ignored) at bit position pos:
-// one shift and one three-input bit operation (v << sh) & mask | rec.
+// The code field of one quantized coefficient, from tb = bits(fl(v + 1.5*2^23))
+// with rint(v) = q in [-m, m]: tb = 0x4B400000 + q exactly, so the code q + m
+// is tb + (m - 0x4B400000) in 32-bit arithmetic. A field inside one word adds
+// (tb << sh) and the compile-time constant (m - 0x4B400000) << sh, which the
+// compiler merges across the word's fields into one constant: one shift-and-add
+// per code. A field that crosses into the next word forms the code first.
 template <int DW>
-__device__ __forceinline__ void rec_insert_low(uint32_t (&rec)[DW], int pos, int w, uint32_t v) {
+__device__ __forceinline__ void rec_add_code(uint32_t (&rec)[DW], int pos, int w, uint32_t tb, int m) {
     const int d = pos / 32, sh = pos % 32;
-    const uint32_t mask = (1u << w) - 1u;
-    rec[d] = __builtin_amdgcn_bitop3_b32(v << sh, mask << sh, rec[d], 0xEA);
-    if (sh + w > 32) rec[d + 1] = __builtin_amdgcn_bitop3_b32(v >> (32 - sh), mask >> (32 - sh), rec[d + 1], 0xEA);
+    const uint32_t bias = (uint32_t)m - 0x4B400000u;
+    if (sh + w <= 32) {
+        rec[d] += (tb << sh) + (bias << sh);
+    } else {
+        const uint32_t code = tb + bias;
+        rec[d] += code << sh;
+        rec[d + 1] += code >> (32 - sh);
+    }
 }
 
 // fp16 pair (lo, hi) of w -> (lo + hi, lo - hi) in fp32: v_fma_mix widens each
@@ -312,14 +322,49 @@ struct TileMap {
 };
 
 
+// a / m for a finite a >= 0 and a band's largest level m = 2^(bits-1) - 1: with
+// r = fl(1/m), q0 = fl(a*r), the remainder a - q0*m is exact in one fma and
+// fl(q0 + rem*r) is the correctly rounded quotient. This was checked against
+// IEEE division for every fp32 significand and every m in {1, 3, 7, ..., 127};
+// the steps scale exactly with the exponent while the quotient is a normal
+// number. (Smaller quotients only occur for amax < 2^-119, whose fp16 scale is
+// 0 either way; a 1-bit band, m = 0, gets a non-finite scale and the exact path.)
+__device__ __forceinline__ float div_by_level(float a, int m) {
+    const float fm = (float)m, r = 1.0f / fm;  // compile-time constants
+    const float q0 = a * r;
+    const float rem = __builtin_fmaf(-q0, fm, a);
+    return __builtin_fmaf(rem, r, q0);
+}
+
+// 1/s correctly rounded for s > 0 an fp16 value widened to fp32: one Newton
+// step with fma from v_rcp_f32 (specified to 1 ulp). Checked for all 1024 fp16
+// significands with the starting value anywhere within +-3 ulp of 1/s; s and
+// 1/s stay normal fp32 numbers, so the exponent scales out exactly.
+__device__ __forceinline__ float rcp_f16_scale(float s) {
+    const float r0 = __builtin_amdgcn_rcpf(s);
+    const float e = __builtin_fmaf(-s, r0, 1.0f);
+    return __builtin_fmaf(e, r0, r0);
+}
+
 // Band-quantize coefficients x[src_idx(r)], r in [0, LY::hd), into the record
 // bits [0, 8 * LY::total) of rec (which must start zeroed there):
 // kernel_band_quantize_simple (shannon_prime_cuda.cu:131-204). fastv: every
-// coefficient is finite (the fast path's precondition).
+// coefficient is finite.
+//
+// Fast path, for every lane: when the band's stored fp16 scale is a normal
+// number, |x*inv| <= maxv*(1 + 2^-10) < maxv + 1/2, so rint never needs the
+// clamp, and t = x*inv + 1.5*2^23 rounds x*inv to the nearest integer q with
+// ties to even (the added constant is even): bits(t) = 0x4B400000 + q, and the
+// codes are summed into the record words (rec_add_code). A band whose scale is
+// 0 uses inv = 0, as the reference does, and gets q = 0 everywhere. When any
+// band has a subnormal or non-finite scale, or an input is not finite, the lane
+// clears the record and redoes every band with the exact clamped rounding (a
+// rare, divergent branch that overwrites the whole result).
 template <class LY, bool MOB, int N, int DWR>
 __device__ __forceinline__ void quant_bands(const float (&x)[N], bool fastv, uint32_t (&rec)[DWR]) {
     constexpr int HD = LY::hd;
     static_assert(DWR >= LY::dwords && N >= HD, "record and vector must hold the layout");
+    bool ok = fastv;
 #pragma unroll
     for (int b = 0; b < LY::nb; b++) {
         const int off = LY::off(b), sz = LY::sz(b), bits = LY::bits[b];
@@ -327,36 +372,40 @@ __device__ __forceinline__ void quant_bands(const float (&x)[N], bool fastv, uin
         float amax = 0.0f;
 #pragma unroll
         for (int e = 0; e < sz; e++) amax = fmaxf(amax, fabsf(x[src_idx<HD, MOB>(off + e)]));
-        const float scale = (amax > 0.0f) ? sp_div(amax, (float)maxv) : 0.0f;
-        // Fast path for every lane: the hardware conversion is IEEE round-to-nearest-even
-        // for finite scales, and for a normal fp16 scale |x*inv| < maxv + 1/2, so
-        // t = x*inv + 1.5*2^23 rounds x*inv to the nearest integer q with ties to even (the
-        // added constant is even) and bits(t) = 0x4B400000 + q: the low bits of
-        // bits(t) + maxv are the code q + maxv. Lanes outside those conditions redo the
-        // band below (a rare, divergent branch that only overwrites fields, so both
-        // sides define every record word).
-        float sc = scale;
+        float sc = div_by_level(amax, maxv);
         __asm__ volatile("" : "+v"(sc));  // keep the division and the conversion apart
         const uint32_t hf = (uint32_t)__builtin_bit_cast(unsigned short, (_Float16)sc);
-        {
-            const float ss = sp_f16_bits_to_f32(hf);
-            const float inv = (ss > 0.0f) ? sp_div(1.0f, ss) : 0.0f;
-            rec_insert_low(rec, 8 * bo, 16, hf);
+        const bool zero = hf == 0u;
+        ok = ok && (zero || f16_normal(hf));
+        const float inv = zero ? 0.0f : rcp_f16_scale(sp_f16_bits_to_f32(hf));
+        rec_add(rec, 8 * bo, 16, hf);
 #pragma unroll
-            for (int e = 0; e < sz; e++) {
-                const float t = x[src_idx<HD, MOB>(off + e)] * inv + 12582912.0f;
-                rec_insert_low(rec, 8 * (bo + 2) + e * bits, bits, __float_as_uint(t) + (uint32_t)maxv);
-            }
+        for (int e = 0; e < sz; e++) {
+            const float t = x[src_idx<HD, MOB>(off + e)] * inv + 12582912.0f;
+            rec_add_code(rec, 8 * (bo + 2) + e * bits, bits, __float_as_uint(t), maxv);
         }
-        if (!(fastv && f16_normal(hf))) {
+    }
+    if (!ok) {
+        constexpr int TW = LY::total / 4, TB = LY::total % 4;
+#pragma unroll
+        for (int d = 0; d < TW; d++) rec[d] = 0u;
+        if (TB) rec[TW] &= ~((1u << (8 * TB)) - 1u);
+#pragma unroll
+        for (int b = 0; b < LY::nb; b++) {
+            const int off = LY::off(b), sz = LY::sz(b), bits = LY::bits[b];
+            const int maxv = (1 << (bits - 1)) - 1, bo = LY::byte_off(b);
+            float amax = 0.0f;
+#pragma unroll
+            for (int e = 0; e < sz; e++) amax = fmaxf(amax, fabsf(x[src_idx<HD, MOB>(off + e)]));
+            const float scale = (amax > 0.0f) ? sp_div(amax, (float)maxv) : 0.0f;
             const uint32_t h = sp_f32_to_f16_bits(scale);
             const float ss = sp_f16_bits_to_f32(h);
             const float inv = (ss > 0.0f) ? sp_div(1.0f, ss) : 0.0f;
-            rec_replace(rec, 8 * bo, 16, h);
+            rec_insert(rec, 8 * bo, 16, h);
 #pragma unroll
             for (int e = 0; e < sz; e++) {
                 const int q = sp_q_rint_clamp(x[src_idx<HD, MOB>(off + e)] * inv, maxv);
-                rec_replace(rec, 8 * (bo + 2) + e * bits, bits, (uint32_t)(q + maxv));
+                rec_insert(rec, 8 * (bo + 2) + e * bits, bits, (uint32_t)(q + maxv));
             }
         }
     }
