@@ -150,6 +150,62 @@ def test_codes_at_rounding_ties():
     cc.free()
 
 
+def _v3_records(codes, scales):
+    """Records of the one-band 3-bit layout at hd 128: the fp16 scale, then the 128
+    codes packed 3 bits each from bit 0 (the reference's band packing)."""
+    n = codes.shape[0]
+    bits = ((codes[:, :, None] >> np.arange(3)) & 1).astype(np.uint8).reshape(n, 384)
+    rec = np.zeros((n, 50), np.uint8)
+    rec[:, 0:2] = scales.astype(np.uint16).view(np.uint8).reshape(n, 2)
+    rec[:, 2:] = np.packbits(bits, axis=1, bitorder="little")
+    return rec
+
+
+def _same_bits_or_both_nan(got, ref, ftype):
+    gf, rf = got.view(ftype), ref.view(ftype)
+    both_nan = np.isnan(gf) & np.isnan(rf)
+    return np.all((got == ref) | both_nan)
+
+
+@pytest.mark.parametrize("n", [64 * 9 + 17, 64])
+def test_v_decode_crafted_records(n):
+    """The one-band 3-bit V layout at hd 128 over records the encoder never
+    writes: every code 0..7 (7 decodes to +4), scales across the fp16 range
+    (subnormal, normal, large enough that outputs overflow fp16), and tiles
+    holding a +0, -0, infinite or NaN scale; a partial last tile. fp16 and fp32
+    outputs against the oracle, bit for bit (NaN outputs compared as NaN: the
+    oracle runs on x86, whose default NaN has the sign bit set)."""
+    say(f"v3 crafted-record decode n={n}")
+    hd = 128
+    rng = np.random.default_rng(n)
+    codes = rng.integers(0, 8, (n, hd))
+    scales = rng.integers(0x0400, 0x7bff, n).astype(np.uint16)  # normal fp16
+    scales[rng.random(n) < 0.05] = rng.integers(1, 0x3ff, 1)[0]  # some subnormal
+    scales[3] = 0x7bff  # 65504: outputs overflow fp16
+    if n > 64:
+        scales[64 + 5] = 0x0000   # tile 1: +0
+        scales[128 + 63] = 0x8000  # tile 2: -0
+        scales[256] = 0x7c00      # tile 4: +inf
+        scales[320 + 9] = 0xfe00  # tile 5: NaN
+        codes[448:512] = 3        # tile 7: all-zero coefficients with a zero scale
+        scales[448:512] = 0x0000
+    rec = _v3_records(codes, scales)
+    obc, sbc = O.band_config(hd, [3]), S.band_config(hd, [3])
+    rt = dev(rec.reshape(-1))
+    r16 = O.ship_decompress_f16(rec, obc)
+    r32 = O.ship_decompress_f32(rec, obc)
+    g16 = host(decode(sbc, None, rt, S.DTYPE_F16, n, hd), np.uint16).reshape(n, hd)
+    g32 = host(decode(sbc, None, rt, S.DTYPE_F32, n, hd)).reshape(n, hd)
+    assert _same_bits_or_both_nan(g16, r16, np.float16), np.argwhere(g16 != r16)[:8]
+    assert _same_bits_or_both_nan(g32.view(np.uint32), r32.view(np.uint32), np.float32), \
+        np.argwhere(g32.view(np.uint32) != r32.view(np.uint32))[:8]
+    # tiles without a non-finite scale match bit for bit, NaN aside
+    good = np.ones(n, bool)
+    if n > 64:
+        good[256:384] = False
+    assert np.array_equal(g16[good], r16[good])
+
+
 @pytest.mark.parametrize("n_pos", [65536, 40001])
 def test_multi_tile_blocks_bit_exact(n_pos):
     """Layer-wide calls large enough that every persistent block walks more than one
