@@ -3,7 +3,8 @@
 // "Disk-tier scaffold", kv_cache.h:132-146): a record is cut into segments (its
 // bands, plus for sqfree/hier the residual tail), and segment s of every (slot,
 // position) is stored contiguously, [segment][slot][position][segment bytes], so a
-// partial load reads the first bands' regions only.
+// partial load reads the first bands' regions only. Format v2 is the same with one
+// segment, the whole record.
 // One thread per record: it reads its record's bytes in one contiguous run and
 // writes each segment at its place in the segment's region; consecutive threads
 // handle consecutive positions, so both sides move through memory in order.

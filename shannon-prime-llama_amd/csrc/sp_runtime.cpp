@@ -2069,12 +2069,16 @@ extern "C" int sp_hip_dual_read_merged(sp_hip_dual_cache_t *dc, int layer, int k
 }
 
 // ===========================================================================
-// disk serialisation, format v3 (KvCache::save_to_disk / load_from_disk,
-// kv_cache.h:132-146, kv_cache.cpp:1533-1585; band-major layout and partial
-// load: the disk-tier notes of CHANGELOG.md)
+// disk serialisation, formats v2 and v3 (KvCache::save_to_disk / load_from_disk,
+// kv_cache.h:132-146, kv_cache.cpp:1533-1585; band-major v3, partial load, and
+// v2 files staying readable: the disk-tier notes of CHANGELOG.md)
 // ===========================================================================
 // One file per layer, {prefix}.L{layer}.bin: a 64-byte header, then the K
 // segments and the V segments, each [n_heads][n_pos][segment bytes] (sp_disk.hip).
+// v3 (the ship caches) cuts each record into its bands (+ the sqfree/hier tail);
+// v2 (the sqfree and hier caches, which the reference has not moved to v3) keeps
+// each record whole: one segment of B bytes, i.e. the records in cache order.
+// Every loader reads both; a partial load of a v2 file reads every band.
 
 extern "C" uint64_t sp_fnv1a64(const void *data, size_t n) {
     const unsigned char *p = (const unsigned char *)data;
@@ -2088,7 +2092,7 @@ extern "C" uint64_t sp_fnv1a64(const void *data, size_t n) {
 
 namespace {
 
-constexpr uint32_t SP_DISK_VERSION = 3;
+constexpr uint32_t DISK_V2 = 2, DISK_V3 = 3;
 enum { DISK_SHIP = 0, DISK_SQFREE = 1, DISK_HIER = 2, DISK_HIER_W = 3 };
 
 struct DiskHeader {  // 64 bytes, little-endian
@@ -2126,6 +2130,17 @@ SpDiskSegs disk_segs(const sp_band_config_t *bc, int B, long long n_rec) {
     return S;
 }
 
+// A file's segments: v3 per band (disk_segs), v2 one whole-record segment.
+SpDiskSegs file_segs(uint32_t version, const sp_band_config_t *bc, int B, long long n_rec) {
+    if (version == DISK_V3) return disk_segs(bc, B, n_rec);
+    SpDiskSegs S{};
+    S.n = 1;
+    S.off[0] = 0;
+    S.len[0] = (short)B;
+    S.base[0] = 0;
+    return S;
+}
+
 long long segs_bytes(const SpDiskSegs &S, int n_seg, long long n_rec) {
     long long b = 0;
     for (int s = 0; s < n_seg && s < S.n; s++) b += n_rec * S.len[s];
@@ -2134,6 +2149,7 @@ long long segs_bytes(const SpDiskSegs &S, int n_seg, long long n_rec) {
 
 struct DiskCache {  // what save/load need of any of the three cache kinds
     int kind, n_layers, H, hd, max_seq, kB, vB;
+    uint32_t version;  // the format this kind writes
     unsigned char *kc, *vc;
     const sp_band_config_t *kbc, *vbc;
     uint32_t order_check;
@@ -2160,7 +2176,7 @@ bool hash_ok(uint64_t got, uint64_t want, const char *what) {
 int disk_save(const DiskCache &D, const char *prefix, int n_pos, uint64_t model_hash) {
     if (!prefix || n_pos <= 0 || n_pos > D.max_seq) { set_err("save: bad n_pos %d", n_pos); return -1; }
     const long long n_rec = (long long)D.H * n_pos;
-    const SpDiskSegs Sk = disk_segs(D.kbc, D.kB, n_rec), Sv = disk_segs(D.vbc, D.vB, n_rec);
+    const SpDiskSegs Sk = file_segs(D.version, D.kbc, D.kB, n_rec), Sv = file_segs(D.version, D.vbc, D.vB, n_rec);
     const size_t kbytes = (size_t)n_rec * D.kB, body = kbytes + (size_t)n_rec * D.vB;
     unsigned char *d_stage = nullptr, *h_stage = nullptr;
     if (!(hip_ok(hipMalloc((void **)&d_stage, body), "save staging") &&
@@ -2179,7 +2195,7 @@ int disk_save(const DiskCache &D, const char *prefix, int n_pos, uint64_t model_
               hip_ok(hipStreamSynchronize(D.s), "save sync"))) { rc = -1; break; }
         DiskHeader h{};
         memcpy(h.magic, "VHT2", 4);
-        h.version = SP_DISK_VERSION;
+        h.version = D.version;
         h.model_hash = model_hash;
         h.n_pos = n_pos, h.layer = l, h.n_heads = D.H, h.head_dim = D.hd, h.kind = D.kind;
         h.k_bytes = D.kB, h.v_bytes = D.vB, h.k_segs = Sk.n, h.v_segs = Sv.n, h.order_check = D.order_check;
@@ -2210,8 +2226,8 @@ FILE *open_layer_file(const DiskCache &D, const char *prefix, int l, uint64_t ex
     if (!ok || memcmp(h.magic, "VHT2", 4) != 0 || h.check != sp_fnv1a64(&h, 56)) {
         set_err("load: %s is not a VHT2 cache file", path.c_str());
         ok = false;
-    } else if (h.version != SP_DISK_VERSION) {
-        set_err("load: %s has format version %u (this build reads %u)", path.c_str(), h.version, SP_DISK_VERSION);
+    } else if (h.version != DISK_V2 && h.version != DISK_V3) {
+        set_err("load: %s has format version %u (this build reads 2 and 3)", path.c_str(), h.version);
         ok = false;
     } else if (h.kind != D.kind || h.layer != l || h.n_heads != D.H || h.head_dim != D.hd || h.k_bytes != D.kB ||
                h.v_bytes != D.vB || h.n_pos <= 0 || (n_pos_all >= 0 && h.n_pos != n_pos_all)) {
@@ -2228,7 +2244,7 @@ FILE *open_layer_file(const DiskCache &D, const char *prefix, int l, uint64_t ex
     }
     if (ok) {
         const long long n_rec = (long long)D.H * h.n_pos;
-        const SpDiskSegs Sk = disk_segs(D.kbc, D.kB, n_rec), Sv = disk_segs(D.vbc, D.vB, n_rec);
+        const SpDiskSegs Sk = file_segs(h.version, D.kbc, D.kB, n_rec), Sv = file_segs(h.version, D.vbc, D.vB, n_rec);
         if (Sk.n != h.k_segs || Sv.n != h.v_segs) {
             set_err("load: %s band layout differs", path.c_str());
             ok = false;
@@ -2261,7 +2277,7 @@ int check_layer_files(const DiskCache &D, const char *prefix, uint64_t expected_
 }
 
 // Loads positions [0, n_pos) of every layer; segments past max_segs (< 0: all)
-// are cleared instead of read. Returns n_pos.
+// are cleared instead of read (v3 files; a v2 file is read whole). Returns n_pos.
 int disk_load(const DiskCache &D, const char *prefix, uint64_t expected_hash, int max_segs) {
     int n_pos_all = check_layer_files(D, prefix, expected_hash);
     if (n_pos_all < 0) return -1;
@@ -2274,8 +2290,9 @@ int disk_load(const DiskCache &D, const char *prefix, uint64_t expected_hash, in
         if (!f) { rc = -1; break; }
         const std::string path = layer_path(prefix, l);
         const long long n_rec = (long long)D.H * h.n_pos;
-        const SpDiskSegs Sk = disk_segs(D.kbc, D.kB, n_rec), Sv = disk_segs(D.vbc, D.vB, n_rec);
-        const int nk = max_segs < 0 ? Sk.n : std::min(max_segs, Sk.n), nv = max_segs < 0 ? Sv.n : std::min(max_segs, Sv.n);
+        const SpDiskSegs Sk = file_segs(h.version, D.kbc, D.kB, n_rec), Sv = file_segs(h.version, D.vbc, D.vB, n_rec);
+        const int ms = h.version == DISK_V3 ? max_segs : -1;
+        const int nk = ms < 0 ? Sk.n : std::min(ms, Sk.n), nv = ms < 0 ? Sv.n : std::min(ms, Sv.n);
         const size_t kfull = (size_t)n_rec * D.kB, body = kfull + (size_t)n_rec * D.vB;
         const size_t kread = (size_t)segs_bytes(Sk, nk, n_rec), vread = (size_t)segs_bytes(Sv, nv, n_rec);
         if (body > cap) {
@@ -2308,7 +2325,8 @@ int disk_load(const DiskCache &D, const char *prefix, uint64_t expected_hash, in
 
 bool ship_disk(const sp_hip_cache_t *cc, DiskCache &D) {
     if (!cc || !cc->priv) { set_err("disk: bad cache"); return false; }
-    D.kind = DISK_SHIP, D.n_layers = cc->config.n_layers, D.H = cc->config.n_heads_kv, D.hd = cc->config.head_dim;
+    D.kind = DISK_SHIP, D.version = DISK_V3, D.n_layers = cc->config.n_layers, D.H = cc->config.n_heads_kv,
+    D.hd = cc->config.head_dim;
     D.max_seq = cc->max_seq_len, D.kB = cc->k_bands.total_bytes, D.vB = cc->v_bands.total_bytes;
     D.kc = (unsigned char *)cc->d_k_cache, D.vc = (unsigned char *)cc->d_v_cache;
     D.kbc = &cc->k_bands, D.vbc = &cc->v_bands, D.s = (hipStream_t)cc->stream;
@@ -2326,7 +2344,7 @@ bool sqfree_disk(const sp_hip_sqfree_cache_t *cc, DiskCache &D) {
     if (!cc || !cc->priv) { set_err("disk: bad sqfree cache"); return false; }
     const int H = cc->config.n_heads_kv;
     if (cc->n_slots < cc->config.n_layers * H) { set_err("disk: sqfree slots"); return false; }
-    D.kind = DISK_SQFREE, D.n_layers = cc->config.n_layers, D.H = H, D.hd = cc->config.head_dim;
+    D.kind = DISK_SQFREE, D.version = DISK_V2, D.n_layers = cc->config.n_layers, D.H = H, D.hd = cc->config.head_dim;
     D.max_seq = cc->max_seq_len, D.kB = cc->bytes_per_pos_k, D.vB = cc->bytes_per_pos_v;
     D.kc = cc->d_k_cache, D.vc = cc->d_v_cache, D.kbc = &cc->k_bands, D.vbc = &cc->v_bands;
     D.s = (hipStream_t)cc->stream, D.order_check = 0;
@@ -2337,7 +2355,7 @@ bool hier_disk(const sp_hip_hier_cache_t *hc, DiskCache &D) {
     if (!hc || !hc->priv) { set_err("disk: bad hier cache"); return false; }
     const int H = hc->config.n_heads_kv;
     if (hc->n_slots < hc->config.n_layers * H) { set_err("disk: hier slots"); return false; }
-    D.kind = DISK_HIER, D.n_layers = hc->config.n_layers, D.H = H, D.hd = hc->config.head_dim;
+    D.kind = DISK_HIER, D.version = DISK_V2, D.n_layers = hc->config.n_layers, D.H = H, D.hd = hc->config.head_dim;
     D.max_seq = hc->max_seq_len, D.kB = hc->bytes_per_pos_k, D.vB = hc->bytes_per_pos_v;
     D.kc = hc->d_k_cache, D.vc = hc->d_v_cache, D.kbc = &hc->skel_bands, D.vbc = &hc->skel_bands;
     D.s = (hipStream_t)hc->stream, D.order_check = 0;
@@ -2385,7 +2403,7 @@ extern "C" int sp_hip_hier_cache_save(const sp_hip_hier_cache_t *hc, const char 
     if (!hip_ok(hipMemcpy(W.data(), hc->d_W, nw * sizeof(uint16_t), hipMemcpyDeviceToHost), "save W")) return -1;
     DiskHeader h{};
     memcpy(h.magic, "VHT2", 4);
-    h.version = SP_DISK_VERSION;
+    h.version = D.version;
     h.model_hash = model_hash;
     h.n_heads = hc->n_slots, h.head_dim = hc->n_target, h.k_bytes = hc->n_skeleton, h.kind = DISK_HIER_W;
     header_seal(h);
@@ -2407,7 +2425,7 @@ extern "C" int sp_hip_hier_cache_load(sp_hip_hier_cache_t *hc, const char *prefi
     const size_t nw = (size_t)hc->n_slots * hc->n_target * hc->n_skeleton;
     std::vector<uint16_t> W(nw);
     bool ok = fread(&h, sizeof(h), 1, f) == 1 && memcmp(h.magic, "VHT2", 4) == 0 && h.check == sp_fnv1a64(&h, 56) &&
-              h.version == SP_DISK_VERSION && h.kind == DISK_HIER_W && h.n_heads == hc->n_slots &&
+              (h.version == DISK_V2 || h.version == DISK_V3) && h.kind == DISK_HIER_W && h.n_heads == hc->n_slots &&
               h.head_dim == hc->n_target && h.k_bytes == hc->n_skeleton;
     if (!ok) set_err("load: %s does not match this hier cache", path.c_str());
     ok = ok && hash_ok(h.model_hash, expected_hash, "load");
@@ -2546,7 +2564,7 @@ int shadow_disk(sp_shadow_cache_t *sc, const char *prefix, int n_pos, uint64_t h
     const int H = sc->config.n_heads_kv, hd = sc->config.head_dim, Lyr = sc->config.n_layers;
     const int kB = sc->k_bands.total_bytes, vB = sc->v_bands.total_bytes;
     DiskCache D{};
-    D.kind = DISK_SHIP, D.n_layers = Lyr, D.H = H, D.hd = hd, D.max_seq = cap, D.kB = kB, D.vB = vB;
+    D.kind = DISK_SHIP, D.version = DISK_V3, D.n_layers = Lyr, D.H = H, D.hd = hd, D.max_seq = cap, D.kB = kB, D.vB = vB;
     D.kbc = &sc->k_bands, D.vbc = &sc->v_bands, D.order_check = shadow_order_check(sc);
     for (int l = 0; l < Lyr; l++)
         for (int hh = 0; hh < H; hh++)
@@ -2569,12 +2587,14 @@ int shadow_disk(sp_shadow_cache_t *sc, const char *prefix, int n_pos, uint64_t h
             return -1;
         }
         const long long n_rec = (long long)H * n_pos;
-        const SpDiskSegs Sk = disk_segs(&sc->k_bands, kB, n_rec), Sv = disk_segs(&sc->v_bands, vB, n_rec);
+        const uint32_t ver = save ? DISK_V3 : h.version;
+        const SpDiskSegs Sk = file_segs(ver, &sc->k_bands, kB, n_rec), Sv = file_segs(ver, &sc->v_bands, vB, n_rec);
         const size_t kfull = (size_t)n_rec * kB;
         body.assign(kfull + (size_t)n_rec * vB, 0);
         bool ok = true;
         if (!save) {
-            const int nk = max_segs < 0 ? Sk.n : std::min(max_segs, Sk.n), nv = max_segs < 0 ? Sv.n : std::min(max_segs, Sv.n);
+            const int ms = ver == DISK_V3 ? max_segs : -1;  // a v2 file is read whole
+            const int nk = ms < 0 ? Sk.n : std::min(ms, Sk.n), nv = ms < 0 ? Sv.n : std::min(ms, Sv.n);
             const size_t kread = (size_t)segs_bytes(Sk, nk, n_rec), vread = (size_t)segs_bytes(Sv, nv, n_rec);
             ok = fread(body.data(), 1, kread, f) == kread && fseek(f, (long)(kfull - kread), SEEK_CUR) == 0 &&
                  fread(body.data() + kfull, 1, vread, f) == vread;
@@ -2598,7 +2618,7 @@ int shadow_disk(sp_shadow_cache_t *sc, const char *prefix, int n_pos, uint64_t h
         }
         if (ok && save) {
             memcpy(h.magic, "VHT2", 4);
-            h.version = SP_DISK_VERSION;
+            h.version = DISK_V3;
             h.model_hash = hash;
             h.n_pos = n_pos, h.layer = l, h.n_heads = H, h.head_dim = hd, h.kind = DISK_SHIP;
             h.k_bytes = kB, h.v_bytes = vB, h.k_segs = Sk.n, h.v_segs = Sv.n, h.order_check = D.order_check;

@@ -1,7 +1,8 @@
-"""Disk format v3 (save / load / partial load of the ship, sqfree and hier caches):
-the file layout against a numpy restatement of the band-major order, bit-exact
-round trips, partial loads that equal partial reads, and the header and hash
-guards."""
+"""Disk formats v3 (ship caches: band-major) and v2 (sqfree and hier caches:
+records whole, in cache order): the file layouts against numpy restatements,
+bit-exact round trips, partial loads that equal partial reads, v2 files read by
+every loader (a partial load of a v2 file reads every band), and the header and
+hash guards."""
 import ctypes as C
 import os
 import struct
@@ -152,9 +153,15 @@ def test_sqfree_and_hier_save_load(tmp_path):
     prefix = str(tmp_path / "sq")
     S.check(Lb.sp_hip_sqfree_cache_save(a.ref, prefix.encode(), n, h))
     B = a.c.bytes_per_pos_k
-    raw = open(f"{prefix}.L0.bin", "rb").read()
-    hdr = struct.unpack("<4sIQ10iQ", raw[:64])
-    assert hdr[7] == 1 and hdr[8] == B and hdr[10] == len(bits) + 1  # kind, k_bytes, skeleton bands + residual tail
+    # v2: one whole-record segment per side, the records in cache order
+    for layer in range(L):
+        raw = open(f"{prefix}.L{layer}.bin", "rb").read()
+        hdr = struct.unpack("<4sIQ10iQ", raw[:64])
+        assert hdr[:2] == (b"VHT2", 2) and hdr[7] == 1 and hdr[8] == B and hdr[10:12] == (1, 1), hdr
+        assert hdr[13] == fnv(raw[:56])
+        body = np.concatenate([records(a.c.d_k_cache, L, H, ms, B)[layer, :, :n].reshape(-1),
+                               records(a.c.d_v_cache, L, H, ms, B)[layer, :, :n].reshape(-1)])
+        np.testing.assert_array_equal(np.frombuffer(raw[64:], np.uint8), body)
     b = S.SqfreeCache(cfg, ms, rbits=3, spinor=True, sk_k=77, stream=stream)
     assert Lb.sp_hip_sqfree_cache_load(b.ref, prefix.encode(), h) == n
     for ptr_a, ptr_b in ((a.c.d_k_cache, b.c.d_k_cache), (a.c.d_v_cache, b.c.d_v_cache)):
@@ -173,6 +180,13 @@ def test_sqfree_and_hier_save_load(tmp_path):
     prefix = str(tmp_path / "hier")
     S.check(Lb.sp_hip_hier_cache_save(a.ref, prefix.encode(), n, h))
     assert os.path.getsize(f"{prefix}.hier_w.bin") == 64 + Wm.size * 2
+    raw = open(f"{prefix}.L1.bin", "rb").read()
+    hdr = struct.unpack("<4sIQ10iQ", raw[:64])
+    B = a.c.bytes_per_pos_k
+    assert hdr[:2] == (b"VHT2", 2) and hdr[7] == 2 and hdr[10:12] == (1, 1), hdr
+    body = np.concatenate([records(a.c.d_k_cache, L, H, ms, B)[1, :, :n].reshape(-1),
+                           records(a.c.d_v_cache, L, H, ms, B)[1, :, :n].reshape(-1)])
+    np.testing.assert_array_equal(np.frombuffer(raw[64:], np.uint8), body)
     b = S.HierCache(cfg, pad, skel, tgt, S.band_config(len(skel), [5, 5]), 2, ms, L * H, stream=stream)
     assert Lb.sp_hip_hier_cache_load(b.ref, prefix.encode(), h) == n
     B = a.c.bytes_per_pos_k
@@ -181,6 +195,72 @@ def test_sqfree_and_hier_save_load(tmp_path):
     np.testing.assert_array_equal(d2h(b.c.d_W, Wm.size * 2).view(np.uint16).reshape(Wm.shape), Wm)
     a.free()
     b.free()
+
+
+def write_v2(prefix, recs_k, recs_v, n, h, kind, order_check):
+    """v2 layer files from records [L][H][n_pos][B]: the 64-byte header (version 2,
+    one segment per side) and the records whole, in cache order."""
+    L, H, _, kB = recs_k.shape
+    vB = recs_v.shape[3]
+    hd = 128
+    for layer in range(L):
+        hdr = struct.pack("<4sIQ10i", b"VHT2", 2, h, n, layer, H, hd, kind, kB, vB, 1, 1, order_check)
+        hdr += struct.pack("<Q", fnv(hdr))
+        body = recs_k[layer, :, :n].tobytes() + recs_v[layer, :, :n].tobytes()
+        open(f"{prefix}.L{layer}.bin", "wb").write(hdr + body)
+
+
+def test_v2_files_load_into_ship_caches(tmp_path):
+    """A ship cache and the shadow cache load v2 files (records whole) as well as
+    their own v3 files; a partial load of a v2 file reads every band."""
+    say("disk v2 into ship caches")
+    L, H, hd, ms, n = 2, 2, 128, 96, 80
+    stream = torch.cuda.current_stream().cuda_stream
+    cfg = S.config(hd, L, H)
+    kB, vB = 76, 50
+    a = S.ShipCache(cfg, ms, stream=stream)
+    fill_ship(a, L, H, hd, n, 21)
+    rk, rv = records(a.c.d_k_cache, L, H, ms, kB), records(a.c.d_v_cache, L, H, ms, vB)
+    order = O.mobius_order(hd).astype(np.int32)
+    order_check = fnv(order.tobytes()) & 0xffffffff
+    order_check -= (1 << 32) if order_check >= (1 << 31) else 0  # the header's int32 slot
+    prefix = str(tmp_path / "v2")
+    h = fnv(b"model-v2")
+    write_v2(prefix, rk, rv, n, h, 0, order_check)
+    Lb = S.lib()
+    for partial in (False, True):
+        b = S.ShipCache(cfg, ms, stream=stream)
+        got = (Lb.sp_hip_cache_load_partial(b.ref, prefix.encode(), h, 1) if partial
+               else Lb.sp_hip_cache_load(b.ref, prefix.encode(), h))
+        assert got == n, S.last_error()
+        np.testing.assert_array_equal(records(b.c.d_k_cache, L, H, ms, kB)[:, :, :n], rk[:, :, :n])
+        np.testing.assert_array_equal(records(b.c.d_v_cache, L, H, ms, vB)[:, :, :n], rv[:, :, :n])
+        b.free()
+    # the shadow cache (host record buffers) reads the same files
+    sc = S.SpShadowCache()
+    S.check(Lb.sp_shadow_cache_init(C.byref(sc), C.byref(cfg)))
+    bufs = [np.zeros(n * kB, np.uint8) for _ in range(L * H)] + [np.zeros(n * vB, np.uint8) for _ in range(L * H)]
+    kp = (C.POINTER(C.c_uint8) * (L * H))(*[x.ctypes.data_as(C.POINTER(C.c_uint8)) for x in bufs[:L * H]])
+    vp = (C.POINTER(C.c_uint8) * (L * H))(*[x.ctypes.data_as(C.POINTER(C.c_uint8)) for x in bufs[L * H:]])
+    sc.k_cache = C.cast(kp, C.POINTER(C.POINTER(C.c_uint8)))
+    sc.v_cache = C.cast(vp, C.POINTER(C.POINTER(C.c_uint8)))
+    S.check(Lb.sp_shadow_cache_set_slot_capacity(C.byref(sc), n))
+    assert Lb.sp_shadow_cache_load_partial(C.byref(sc), prefix.encode(), h, 1) == n, S.last_error()
+    for layer in range(L):
+        for hh in range(H):
+            np.testing.assert_array_equal(bufs[layer * H + hh].reshape(n, kB), rk[layer, hh, :n])
+            np.testing.assert_array_equal(bufs[L * H + layer * H + hh].reshape(n, vB), rv[layer, hh, :n])
+    Lb.sp_shadow_cache_free(C.byref(sc))
+    # another version number is refused
+    raw = bytearray(open(f"{prefix}.L0.bin", "rb").read())
+    raw[4] = 4
+    raw[56:64] = struct.pack("<Q", fnv(bytes(raw[:56])))
+    open(f"{prefix}.L0.bin", "wb").write(bytes(raw))
+    b = S.ShipCache(cfg, ms, stream=stream)
+    assert Lb.sp_hip_cache_load(b.ref, prefix.encode(), h) == -1
+    assert "version" in S.last_error()
+    b.free()
+    a.free()
 
 
 def test_load_rejects_another_coefficient_order(tmp_path):
