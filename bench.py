@@ -422,6 +422,43 @@ def bench_variants(torch, S, L, stream, reps=3):
                   f"K+V hier records of {B5} B; per sequence (a batch of 8 is 8 such calls)"}
     c6.free()
     c5.free()
+    # configs[4] sustained: batch-8 decode interleaved with prefill-chunk compression. Eight
+    # sequences are the eight layers of one cache (131072 positions each, K and V from distinct
+    # rows); one step of a layer decodes all eight (fused attention, 16 query heads each) and
+    # compresses one 2048-token chunk of a ninth sequence's new K and V (8 heads) into its
+    # positions [131072, 133120)
+    NB, CHK = 8, 2048
+    c7 = S.HierCache(S.config(hd5, NB + 1, H5), pad5, sk, tg, S.band_config(n_sk, [5, 5]), 2, NA + CHK,
+                     (NB + 1) * H5, stream=stream.cuda_stream)
+    c7.upload_W(np.tile(Wh.view(np.uint16), (NB + 1, 1, 1)))
+    for sq in range(NB):
+        r0 = (sq * NA) % (N5 - NA)
+        S.check(L.sp_hip_hier_write_layer(c7.ref, sq, 0, NA, P(x[r0:r0 + NA]), P(x[r0 + 1:r0 + 1 + NA]), H5 * hd5,
+                                          S.DTYPE_F16))
+    q8 = torch.randn((NB, NQ5, hd5), generator=g, device="cuda")
+    o8 = torch.empty((NB, NQ5, hd5), device="cuda")
+    kc, vc = x[:CHK], x[CHK:2 * CHK]
+
+    def decode8():
+        for sq in range(NB):
+            S.check(L.sp_hip_hier_attn_decode(c7.ref, sq, NA, P(q8[sq]), NQ5, sc5, None, P(o8[sq]), sp))
+
+    def chunk():
+        S.check(L.sp_hip_hier_write_layer(c7.ref, NB, NA, CHK, P(kc), P(vc), H5 * hd5, S.DTYPE_F16))
+
+    def step():
+        decode8()
+        chunk()
+
+    t_dec8, t_chunk, t_step = timed(decode8), timed(chunk), timed(step)
+    out["cfg5_batch8_with_prefill_chunk"] = {
+        "step_layer_us": round(t_step * 1e6, 1), "decode8_layer_us": round(t_dec8 * 1e6, 1),
+        "chunk_layer_us": round(t_chunk * 1e6, 1),
+        "chunk_vecs_per_s": round(2 * H5 * CHK / t_chunk, 1),
+        "decode_tokens_per_s_34_layers": round(NB / (34 * t_step), 1),
+        "layout": f"{NB} sequences x {NA} positions x {H5} KV heads, {NQ5} query heads each, hd {hd5} (pad {pad5}); "
+                  f"per layer and step: {NB} fused attention calls, then one {CHK}-token K+V chunk compressed"}
+    c7.free()
     return out
 
 

@@ -99,7 +99,8 @@ template <int DT, int PAD, int NS, int RBITS, class SL>
 __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1)))
 k_hier_encode_lane(const void *__restrict__ src, long long so, long long si, unsigned char *__restrict__ dst,
                    long long dout, int n_inner, int tiles_per_outer, int n_tiles, const XfConst K,
-                   const uint16_t *__restrict__ W, long long w_outer) {
+                   const uint16_t *__restrict__ W, long long w_outer, const void *__restrict__ src2,
+                   unsigned char *__restrict__ dst2, int n_sides) {
     constexpr int HD = HIER_HD, NT = PAD - NS;
     using G = HierRec<NT, RBITS, SL>;
     constexpr int RP = row_bytes<DT>(HD) + 16, DWR = G::dwords;
@@ -108,8 +109,14 @@ k_hier_encode_lane(const void *__restrict__ src, long long so, long long si, uns
     __shared__ __attribute__((aligned(16))) unsigned char rows[64 * RP];  // input rows, then the record stage
     const int lane = threadIdx.x;
     const TileMap M{tiles_per_outer, n_inner};
-    for (int t = blockIdx.x; t < n_tiles; t += gridDim.x) {
-        tile_rows_stage<DT, HD>(src, so, si, M, t, lane, rows);
+    // n_sides == 2: tiles [n_tiles, 2 n_tiles) encode the second side (src2 -> dst2, the
+    // same slots and W), so a layer's K and V share one launch
+    for (int tt = blockIdx.x; tt < n_sides * n_tiles; tt += gridDim.x) {
+        const bool second = tt >= n_tiles;
+        const int t = second ? tt - n_tiles : tt;
+        const void *const sp = second ? src2 : src;
+        unsigned char *const dp = second ? dst2 : dst;
+        tile_rows_stage<DT, HD>(sp, so, si, M, t, lane, rows);
         const unsigned char *row = rows + lane * RP;
         // pad mean: the first level of the 256-slot tree, x[i] + x[i + 128],
         // straight from the staged row, then the rest of the tree
@@ -221,7 +228,7 @@ k_hier_encode_lane(const void *__restrict__ src, long long so, long long si, uns
             const float cl = fminf(fmaxf(v, 0.0f), (float)(L - 1));
             rec_insert(rec, G::res_bit + r * RBITS, RBITS, (uint32_t)__builtin_rintf(cl));
         }
-        tile_records_out<G::total, 64 * RP>(rec, rows, dst, dout, M, t, lane);
+        tile_records_out<G::total, 64 * RP>(rec, rows, dp, dout, M, t, lane);
     }
 }
 
@@ -302,15 +309,17 @@ bool hier_geometry_matches(const SpPlan &P, const SpHierGeo &G) {
 
 template <int DT>
 hipError_t hier_enc_launch(const SpPlan &P, const SpHierGeo &G, const void *src, long long so, long long si,
-                           unsigned char *dst, long long dout, int n_outer, int n_inner, hipStream_t s) {
+                           unsigned char *dst, long long dout, int n_outer, int n_inner, hipStream_t s,
+                           const void *src2, unsigned char *dst2) {
     const int tpo = (n_inner + 63) / 64;
     const long long n_tiles = (long long)n_outer * tpo;
+    const int sides = src2 ? 2 : 1;
     constexpr long long esz = DT == SP_DT_F16 ? 2 : 4;
-    if (n_tiles > 0x7fffffffLL || si < HIER_HD || 64 * si * esz + HIER_HD * esz > 0x7fffffffLL)
+    if (sides * n_tiles > 0x7fffffffLL || si < HIER_HD || 64 * si * esz + HIER_HD * esz > 0x7fffffffLL)
         return hipErrorNotSupported;
-    const dim3 grid((unsigned)std::min<long long>(n_tiles, persistent_blocks())), block(64);
+    const dim3 grid((unsigned)std::min<long long>(sides * n_tiles, persistent_blocks())), block(64);
     hipLaunchKernelGGL((k_hier_encode_lane<DT, 330, 30, 2, HierSkL>), grid, block, 0, s, src, so, si, dst, dout,
-                       n_inner, tpo, (int)n_tiles, xf_const(P), G.W, G.w_outer);
+                       n_inner, tpo, (int)n_tiles, xf_const(P), G.W, G.w_outer, src2, dst2, sides);
     return hipGetLastError();
 }
 
@@ -337,15 +346,18 @@ hipError_t hier_dec_launch(const SpPlan &P, const SpHierGeo &G, const unsigned c
 // Returns hipErrorNotSupported (nothing launched) when the geometry or the
 // operand alignment has no lane specialization: the caller then uses the
 // one-vector-per-wave kernels.
+// src2/dst2 (optional): a second side (V after K) with the same strides and slots,
+// encoded by the same launch.
 hipError_t sp_launch_hier_encode_lane(const SpPlan &P, const SpHierGeo &G, const void *src, int dtype, long long so,
                                       long long si, unsigned char *dst, long long dout, int n_outer, int n_inner,
-                                      hipStream_t s) {
+                                      hipStream_t s, const void *src2, unsigned char *dst2) {
     const int esz = dtype == SP_DT_F16 ? 2 : 4;
     if (((uintptr_t)src % 16) || ((so * esz) % 16) || ((si * esz) % 16)) return hipErrorNotSupported;
     if (((uintptr_t)dst % 4) || (dout % 4)) return hipErrorNotSupported;
+    if (src2 && (((uintptr_t)src2 % 16) || ((uintptr_t)dst2 % 4) || !dst2)) return hipErrorNotSupported;
     if (!hier_geometry_matches(P, G)) return hipErrorNotSupported;
-    return dtype == SP_DT_F16 ? hier_enc_launch<SP_DT_F16>(P, G, src, so, si, dst, dout, n_outer, n_inner, s)
-                              : hier_enc_launch<SP_DT_F32>(P, G, src, so, si, dst, dout, n_outer, n_inner, s);
+    return dtype == SP_DT_F16 ? hier_enc_launch<SP_DT_F16>(P, G, src, so, si, dst, dout, n_outer, n_inner, s, src2, dst2)
+                              : hier_enc_launch<SP_DT_F32>(P, G, src, so, si, dst, dout, n_outer, n_inner, s, src2, dst2);
 }
 
 hipError_t sp_launch_hier_decode_lane(const SpPlan &P, const SpHierGeo &G, const unsigned char *src, long long so,

@@ -231,10 +231,11 @@ hipError_t sp_launch_hier_attn(const SpPlan &P, const SpHierAttnArgs &A, float *
                                hipStream_t s);
 
 // one-vector-per-lane hier kernels for the default geometry at head_dim 256;
-// hipErrorNotSupported (nothing launched) when no specialization fits
+// hipErrorNotSupported (nothing launched) when no specialization fits. src2/dst2:
+// an optional second side (V with K) encoded by the same launch.
 hipError_t sp_launch_hier_encode_lane(const SpPlan &P, const SpHierGeo &G, const void *src, int dtype, long long so,
                                       long long si, unsigned char *dst, long long dout, int n_outer, int n_inner,
-                                      hipStream_t s);
+                                      hipStream_t s, const void *src2 = nullptr, unsigned char *dst2 = nullptr);
 // cells (optional): listed positions, record and row at cells[i] (slack after the cache)
 hipError_t sp_launch_hier_decode_lane(const SpPlan &P, const SpHierGeo &G, const unsigned char *src, long long so,
                                       void *dst, int dtype, long long dout, long long din, int n_outer, int n_inner,
@@ -264,6 +265,10 @@ hipError_t sp_launch_sqfree_decode(const SpPlan &P, const SpSqGeo &G, const unsi
 hipError_t sp_launch_hier_encode(const SpPlan &P, const SpHierGeo &G, const void *src, int dtype,
                                  long long so, long long si, unsigned char *dst, long long dout,
                                  int n_outer, int n_inner, hipStream_t s);
+// K and V of the same slots in one lane launch when it applies; else two launches
+hipError_t sp_launch_hier_encode_kv(const SpPlan &P, const SpHierGeo &G, const void *src_k, const void *src_v,
+                                    int dtype, long long so, long long si, unsigned char *dst_k,
+                                    unsigned char *dst_v, long long dout, int n_outer, int n_inner, hipStream_t s);
 hipError_t sp_launch_hier_decode(const SpPlan &P, const SpHierGeo &G, const unsigned char *src,
                                  long long so, void *dst, int dtype, long long dout, long long din,
                                  int n_outer, int n_inner, hipStream_t s, const int *cells = nullptr);

@@ -1366,13 +1366,19 @@ extern "C" int sp_hip_hier_write_layer(sp_hip_hier_cache_t *hc, int layer, int s
     const int H = hc->config.n_heads_kv, hd = hc->config.head_dim;
     if (row_stride < (long long)H * hd) { set_err("hier write_layer: row_stride"); return -1; }
     const SpHierGeo G = hier_geo(hc, layer * H);
+    const long long rec0 = ((long long)layer * H * hc->max_seq_len + start_pos) * G.bytes;
+    const long long hs = (long long)hc->max_seq_len * G.bytes;
+    const SpPlan &plan = ((HierPriv *)hc->priv)->plan;
+    if (d_k && d_v)  // one launch for both sides: twice the tiles in flight for short chunks
+        return hip_ok(sp_launch_hier_encode_kv(plan, G, d_k, d_v, dtype, hd, row_stride, hc->d_k_cache + rec0,
+                                               hc->d_v_cache + rec0, hs, H, n_tok, (hipStream_t)hc->stream),
+                      "hier write_layer") ? 0 : -1;
     for (int is_v = 0; is_v < 2; is_v++) {
         const void *src = is_v ? d_v : d_k;
         if (!src) continue;
-        unsigned char *dst = (is_v ? hc->d_v_cache : hc->d_k_cache) +
-                             ((long long)layer * H * hc->max_seq_len + start_pos) * G.bytes;
-        if (!hip_ok(sp_launch_hier_encode(((HierPriv *)hc->priv)->plan, G, src, dtype, hd, row_stride, dst,
-                                          (long long)hc->max_seq_len * G.bytes, H, n_tok, (hipStream_t)hc->stream),
+        unsigned char *dst = (is_v ? hc->d_v_cache : hc->d_k_cache) + rec0;
+        if (!hip_ok(sp_launch_hier_encode(plan, G, src, dtype, hd, row_stride, dst, hs, H, n_tok,
+                                          (hipStream_t)hc->stream),
                     "hier write_layer")) return -1;
     }
     return 0;

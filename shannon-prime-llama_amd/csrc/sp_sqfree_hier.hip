@@ -335,6 +335,21 @@ hipError_t sp_launch_hier_encode(const SpPlan &P, const SpHierGeo &G, const void
     return hipGetLastError();
 }
 
+hipError_t sp_launch_hier_encode_kv(const SpPlan &P, const SpHierGeo &G, const void *src_k, const void *src_v,
+                                    int dtype, long long so, long long si, unsigned char *dst_k,
+                                    unsigned char *dst_v, long long dout, int n_outer, int n_inner, hipStream_t s) {
+    if (n_outer <= 0 || n_inner <= 0) return hipSuccess;
+    if (!sq_fits(P, G.pad, G.bytes)) return hipErrorInvalidValue;
+    if (!getenv_lane_off_sq()) {
+        const hipError_t e = sp_launch_hier_encode_lane(P, G, src_k, dtype, so, si, dst_k, dout, n_outer, n_inner, s,
+                                                        src_v, dst_v);
+        if (e != hipErrorNotSupported) return e;
+    }
+    const hipError_t e = sp_launch_hier_encode(P, G, src_k, dtype, so, si, dst_k, dout, n_outer, n_inner, s);
+    if (e != hipSuccess) return e;
+    return sp_launch_hier_encode(P, G, src_v, dtype, so, si, dst_v, dout, n_outer, n_inner, s);
+}
+
 hipError_t sp_launch_hier_decode(const SpPlan &P, const SpHierGeo &G, const unsigned char *src,
                                  long long so, void *dst, int dtype, long long dout, long long din,
                                  int n_outer, int n_inner, hipStream_t s, const int *cells) {
