@@ -19,6 +19,8 @@
 // No full-precision K or V is materialized anywhere.
 #include "sp_internal.h"
 
+#include <cstdlib>
+
 #define ATT_CHUNK 256
 #define ATT_MAX_G 8
 #define ATT_MAX_HD 256
@@ -296,7 +298,7 @@ k_attn_merge(const float *__restrict__ ws, int n_parts, int hd, float *__restric
 
 size_t sp_attn_workspace_floats(int n_q, int hd, int max_kv) {
     const int n_splits = (max_kv + ATT_CHUNK - 1) / ATT_CHUNK;
-    return (size_t)n_q * hd + (size_t)n_q * n_splits * (hd + 2);
+    return (size_t)n_q * hd + (size_t)n_q * n_splits * (hd + 2) + SP_ATTN_COUNTERS;
 }
 
 hipError_t sp_launch_attn_decode(const SpPlan &KP, const SpPlan &VP, const int *order,
@@ -311,6 +313,14 @@ hipError_t sp_launch_attn_decode(const SpPlan &KP, const SpPlan &VP, const int *
     float *part = workspace + (size_t)A.n_q * A.hd;
     const int want_out = A.out != nullptr;
     int n_parts = 0;
+    const char *old_k = getenv("SP_HIP_ATTN_OLD");
+    if (!(old_k && old_k[0] == '1')) {
+        // the per-KV-head arrival counters sit in the workspace's last SP_ATTN_COUNTERS words
+        int *cnt = reinterpret_cast<int *>(workspace + ws_floats - SP_ATTN_COUNTERS);
+        const hipError_t we = sp_launch_attn_wave(KP, VP, order, A, part,
+                                                  ws_floats - (size_t)A.n_q * A.hd - SP_ATTN_COUNTERS, cnt, s);
+        if (we != hipErrorNotSupported) return we;
+    }
     const hipError_t me = sp_launch_attn_mfma_split(KP, VP, order, A, part, n_splits, &n_parts, s);
     if (me == hipSuccess) {
         if (want_out)

@@ -318,6 +318,16 @@ void sp_set_error(const char *fmt, ...);
 hipError_t sp_launch_attn_mfma_split(const SpPlan &KP, const SpPlan &VP, const int *order,
                                      const SpAttnArgs &A, float *part, int n_splits, int *n_parts,
                                      hipStream_t s);
+// Words at the end of every attention workspace (sp_attn_workspace_floats) that
+// hold the wave kernel's per-KV-head arrival counters: zero when the workspace
+// is created, and back at zero after each call.
+#define SP_ATTN_COUNTERS 256
+// Wave-tiled matrix-core kernel for the same layout (sp_attn_wave.hip): scores
+// and/or the attention output in one launch (each block writes a spectral-domain
+// partial [m, l, o~[hd]] per query head, at most part_floats floats, and the last
+// block of each KV head merges them); hipErrorNotSupported for other layouts.
+hipError_t sp_launch_attn_wave(const SpPlan &KP, const SpPlan &VP, const int *order, const SpAttnArgs &A, float *part,
+                               size_t part_floats, int *counters, hipStream_t s);
 hipError_t sp_launch_attn_f16(const unsigned short *k, const unsigned short *v,
                               long long head_stride, int n_kv, int n_q, int n_kvh, int hd,
                               float kq_scale, const float *q, float *scores, float *out,

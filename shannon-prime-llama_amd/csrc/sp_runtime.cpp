@@ -521,7 +521,9 @@ extern "C" int sp_hip_cache_init(sp_hip_cache_t *cc, const sp_config_t *cfg, int
     if (ok) {
         pv->max_q = cfg->n_heads_kv * 8;
         pv->ws_floats = sp_attn_workspace_floats(pv->max_q, hd, max_seq_len);
-        ok = hip_ok(hipMalloc((void **)&pv->ws, pv->ws_floats * sizeof(float)), "hipMalloc attention workspace");
+        ok = hip_ok(hipMalloc((void **)&pv->ws, pv->ws_floats * sizeof(float)), "hipMalloc attention workspace") &&
+             hip_ok(hipMemsetAsync(pv->ws, 0, pv->ws_floats * sizeof(float), (hipStream_t)stream),
+                    "attention workspace clear");  // the attention kernel's counters start at zero
     }
     if (ok) ok = hip_ok(hipStreamSynchronize((hipStream_t)stream), "init sync");
     if (!ok) {

@@ -45,6 +45,8 @@ ATTN_CASES = [
     (3, 3, 1, 128, True),        # a single position
     (16, 8, 777, 256, True),     # Gemma-3 head_dim (general kernel)
     (8, 8, 129, 64, True),       # general kernel
+    (12, 4, 700, 128, True),     # GQA 3: one unused head column of the score matrix cores
+    (20, 4, 333, 128, True),     # GQA 5: a second column set, three of its heads unused
 ]
 
 
