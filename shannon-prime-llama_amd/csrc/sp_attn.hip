@@ -298,7 +298,7 @@ k_attn_merge(const float *__restrict__ ws, int n_parts, int hd, float *__restric
 
 size_t sp_attn_workspace_floats(int n_q, int hd, int max_kv) {
     const int n_splits = (max_kv + ATT_CHUNK - 1) / ATT_CHUNK;
-    return (size_t)n_q * hd + (size_t)n_q * n_splits * (hd + 2) + SP_ATTN_COUNTERS;
+    return (size_t)n_q * hd + (size_t)n_q * n_splits * (hd + 2) + SP_ATTN_COUNTERS + SP_ATTN_COUNTER_STRIDE;
 }
 
 hipError_t sp_launch_attn_decode(const SpPlan &KP, const SpPlan &VP, const int *order,
@@ -315,10 +315,12 @@ hipError_t sp_launch_attn_decode(const SpPlan &KP, const SpPlan &VP, const int *
     int n_parts = 0;
     const char *old_k = getenv("SP_HIP_ATTN_OLD");
     if (!(old_k && old_k[0] == '1')) {
-        // the per-KV-head arrival counters sit in the workspace's last SP_ATTN_COUNTERS words
-        int *cnt = reinterpret_cast<int *>(workspace + ws_floats - SP_ATTN_COUNTERS);
-        const hipError_t we = sp_launch_attn_wave(KP, VP, order, A, part,
-                                                  ws_floats - (size_t)A.n_q * A.hd - SP_ATTN_COUNTERS, cnt, s);
+        // the per-KV-head arrival counters: the workspace's last SP_ATTN_COUNTERS words
+        // (plus up to one line of slack), starting on a 256-byte boundary
+        const uintptr_t ctail = (uintptr_t)(workspace + ws_floats - SP_ATTN_COUNTERS - SP_ATTN_COUNTER_STRIDE);
+        int *cnt = reinterpret_cast<int *>((ctail + 255) & ~(uintptr_t)255);
+        const hipError_t we = sp_launch_attn_wave(
+            KP, VP, order, A, part, ws_floats - (size_t)A.n_q * A.hd - SP_ATTN_COUNTERS - SP_ATTN_COUNTER_STRIDE, cnt, s);
         if (we != hipErrorNotSupported) return we;
     }
     const hipError_t me = sp_launch_attn_mfma_split(KP, VP, order, A, part, n_splits, &n_parts, s);

@@ -75,8 +75,7 @@ constexpr int MB_STRIDE = 132;          // floats per (wave, head) in the in-blo
 static_assert(R_ST + 8 * 16 <= R_V && R_V >= TILE * KB, "K area holds the records, then the weights and state");
 static_assert(R_SIZE - R_V >= 2 + TILE * VB + 14, "V area with slack for the window reads");
 static_assert(NW * 8 * MB_STRIDE * 4 <= S_QS, "merge records fit the wave regions");
-constexpr int MAX_PARTS = 256;          // partials per KV head the last block can merge (LDS below S_QS)
-static_assert((8 * MAX_PARTS * 2 + 8 * HD) * 4 <= S_QS, "the final merge's (m, l) table and vectors fit");
+constexpr int MAX_PARTS = 256;          // partials per KV head (blocks per KV head)
 static_assert(R_V % 16 == 0 && R_SIZE % 16 == 0 && S_QS % 16 == 0 && S_CB % 16 == 0 && S_FU % 16 == 0,
               "LDS regions 16-byte aligned");
 static_assert(LDS_BYTES <= 160 * 1024, "LDS of one CU");
@@ -90,14 +89,36 @@ constexpr uint32_t VBIAS = 0x48004800u;      // fp16 2^3 in both halves: 8 + u w
 __device__ __forceinline__ constexpr int kbits(int b) { return b < 2 ? 5 : (b == 2 ? 4 : 3); }
 __device__ __forceinline__ constexpr int kbyte(int b) { return b == 0 ? 0 : b == 1 ? 22 : b == 2 ? 44 : 62; }
 
-// K slot (0..31) of code c of band b in the score MFMA: step s = slot / 4 takes
-// slots 4s .. 4s+3. 5- and 3-bit bands: slot = c. 4-bit band: a dword of 8
-// codes 8d + 4a + i yields the pairs (i, i + 4) already 16 bits apart, so the
-// steps 2d, 2d + 1 take codes (8d, 8d+4, 8d+1, 8d+5) and (8d+2, 8d+6, 8d+3, 8d+7).
+// Score MFMA slots. Step s of a band takes slots 4s .. 4s+3, i.e. the band's
+// code pairs 2s and 2s + 1, each pair one dword of two fp16 (pair p: slots
+// 2p, 2p + 1). A pair built with one shift and one masked OR needs its two
+// codes about 16 bits apart:
+//   5-bit band: pairs (6g + i, 6g + i + 3), g < 5, i < 3, are 15 bits apart:
+//     the first code at mantissa bits 5..9 (2^5 + c), the second at bits
+//     4..8 of the high half (2^5 + c/2: half gain, so its query slot holds 2q~);
+//     codes 30 and 31 form an ordinary pair (both 2^5 + c).
+//   3-bit band: likewise pairs (10g + i, 10g + i + 5), g < 3, i < 5 (2^3 + c,
+//     2^3 + c/2), and the ordinary pair (30, 31).
+//   4-bit band: a dword of 8 codes 8d + 4a + i yields pairs (i, i + 4) already
+//     16 bits apart (both 2^4 + c), steps 2d and 2d + 1.
+// slot_of(b, c) = slot of code c; the high bit of the result marks half gain.
 __device__ __forceinline__ int score_slot(int b, int c) {
-    if (b != 2) return c;
-    const int d = c >> 3, a = (c >> 2) & 1, i = c & 3;
-    return 8 * d + 4 * (i >> 1) + 2 * (i & 1) + a;
+    if (b == 2) {
+        const int d = c >> 3, a = (c >> 2) & 1, i = c & 3;
+        return 8 * d + 4 * (i >> 1) + 2 * (i & 1) + a;
+    }
+    const int span = b < 2 ? 6 : 10, half = span / 2;  // codes per group, pairs per group
+    if (c >= 30) return 30 + (c - 30);                 // pair 15, ordinary
+    const int g = c / span, i = c % span;
+    const int pr = half * g + (i < half ? i : i - half);
+    return i < half ? 2 * pr : (2 * pr + 1) | 0x100;
+}
+
+// The 32 record bits starting at bit p (p compile-time after unrolling; bits past
+// the record's 19 dwords read from the zero dword r[19]).
+__device__ __forceinline__ uint32_t rec_window(const uint32_t (&r)[20], int p) {
+    const int d = p >> 5, o = p & 31;
+    return o == 0 ? r[d] : __builtin_amdgcn_alignbit(r[d + 1], r[d], o);
 }
 
 // v -> (hi, lo) fp16 bit patterns with hi + lo ~= v to ~22 bits.
@@ -122,18 +143,28 @@ __device__ __forceinline__ float scale_of(uint32_t h) {
     return ((h & 0x7c00u) == 0x7c00u) ? 0.0f : f;
 }
 
-// Value of lane (lane ^ M) for M a power of two below 64: quad permutes and a
-// row rotate via DPP, the others via swizzle / permute (no LDS memory traffic).
+// Value of lane (lane ^ M) for M a power of two below 64, all on the VALU (no
+// LDS crossbar round trip): quad permutes and row shifts / rotates via DPP,
+// 16 and 32 via the gfx950 row swaps (permlane16/32_swap(x, x) leave lane l
+// with lane l ^ 16 (^ 32) in one result or the other, by that lane bit).
 template <int M>
 __device__ __forceinline__ float lane_xor(float v) {
     const int x = __float_as_int(v);
+    const int lane = (int)__lane_id();
     int r;
     if (M == 1) r = __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, true);        // quad_perm [1,0,3,2]
     else if (M == 2) r = __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, true);   // quad_perm [2,3,0,1]
-    else if (M == 4) r = __builtin_amdgcn_ds_swizzle(x, 0x101F);              // xor 4 within 32 lanes
-    else if (M == 8) r = __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, true);  // row_ror:8 (xor 8 in a row of 16)
-    else if (M == 16) r = __builtin_amdgcn_ds_swizzle(x, 0x401F);             // xor 16 within 32 lanes
-    else r = __builtin_amdgcn_ds_bpermute(((int)(__lane_id() ^ 32)) << 2, x);
+    else if (M == 4) {                                                        // row_shr:4 / row_shl:4
+        const int dn = __builtin_amdgcn_mov_dpp(x, 0x114, 0xF, 0xF, true), up = __builtin_amdgcn_mov_dpp(x, 0x104, 0xF, 0xF, true);
+        r = (lane & 4) ? dn : up;
+    } else if (M == 8) r = __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, true);  // row_ror:8 (xor 8 in a row of 16)
+    else if (M == 16) {
+        const u32x2 t = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
+        r = (int)((lane & 16) ? t[0] : t[1]);
+    } else {
+        const u32x2 t = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
+        r = (int)((lane & 32) ? t[0] : t[1]);
+    }
     return __int_as_float(r);
 }
 
@@ -170,7 +201,7 @@ __device__ __forceinline__ float head_sum(float v) {
 }
 
 // Bits [p, p + w) of a K record held as 19 dwords (p, w compile-time after unrolling).
-__device__ __forceinline__ uint32_t rec_bits(const uint32_t (&r)[19], int p, int w) {
+__device__ __forceinline__ uint32_t rec_bits(const uint32_t (&r)[20], int p, int w) {
     const int d = p >> 5, o = p & 31;
     if (o + w <= 32) return __builtin_amdgcn_ubfe(r[d], o, w);
     return __builtin_amdgcn_ubfe(__builtin_amdgcn_alignbit(r[d + 1], r[d], o), 0, w);
@@ -183,15 +214,27 @@ __device__ __forceinline__ uint32_t pair_fp16(uint32_t y, uint32_t kmask, uint32
     return __builtin_amdgcn_bitop3_b32(y * ((1u << (10 - BITS)) + (1u << (26 - 2 * BITS))), kmask, kbias, 0xEA);
 }
 
+// Pair p (0..15) of a 5- or 3-bit band as one dword of two fp16 (see score_slot).
+template <int BITS>
+__device__ __forceinline__ uint32_t band_pair(const uint32_t (&r)[20], int b0, int p, uint32_t kmask, uint32_t kbias,
+                                              uint32_t kmask15) {
+    constexpr int span = BITS == 5 ? 6 : 10, half = span / 2;
+    if (p == 15) return pair_fp16<BITS>(rec_bits(r, b0 + 30 * BITS, 2 * BITS), kmask, kbias);
+    const int a = span * (p / half) + p % half;  // first code of the pair
+    // the first code lands at mantissa bits 10-BITS .. 9, the second 15 bits above it
+    return __builtin_amdgcn_bitop3_b32(rec_window(r, b0 + BITS * a - (10 - BITS)), kmask15, kbias, 0xEA);
+}
+
 // The score MFMA's A operand for band b, step s: 4 codes of the lane's record
-// as fp16 2^BITS + u in slots 4s .. 4s+3 (see score_slot).
-__device__ __forceinline__ half4_t score_codes(const uint32_t (&r)[19], int b, int s, uint32_t kmask5, uint32_t kbias5,
-                                               uint32_t kmask4, uint32_t kbias4, uint32_t kmask3, uint32_t kbias3) {
+// as fp16 in slots 4s .. 4s+3 (see score_slot).
+__device__ __forceinline__ half4_t score_codes(const uint32_t (&r)[20], int b, int s, uint32_t kmask5, uint32_t kbias5,
+                                               uint32_t kmask4, uint32_t kbias4, uint32_t kmask3, uint32_t kbias3,
+                                               uint32_t kmask5p, uint32_t kmask3p) {
     uint32_t x0, x1;
     if (b < 2) {
-        const int p = 8 * (kbyte(b) + 2) + 20 * s;
-        x0 = pair_fp16<5>(rec_bits(r, p, 10), kmask5, kbias5);
-        x1 = pair_fp16<5>(rec_bits(r, p + 10, 10), kmask5, kbias5);
+        const int b0 = 8 * (kbyte(b) + 2);
+        x0 = band_pair<5>(r, b0, 2 * s, kmask5, kbias5, kmask5p);
+        x1 = band_pair<5>(r, b0, 2 * s + 1, kmask5, kbias5, kmask5p);
     } else if (b == 2) {
         // the dword of codes 8d .. 8d+7 starts at bit 368 + 32d = 32 (11 + d) + 16
         const int d = s >> 1;
@@ -204,9 +247,9 @@ __device__ __forceinline__ half4_t score_codes(const uint32_t (&r)[19], int b, i
             x1 = __builtin_amdgcn_bitop3_b32(x >> 6, kmask4, kbias4, 0xEA);  // codes 3, 7
         }
     } else {
-        const int p = 8 * (kbyte(3) + 2) + 12 * s;
-        x0 = pair_fp16<3>(rec_bits(r, p, 6), kmask3, kbias3);
-        x1 = pair_fp16<3>(rec_bits(r, p + 6, 6), kmask3, kbias3);
+        const int b0 = 8 * (kbyte(3) + 2);
+        x0 = band_pair<3>(r, b0, 2 * s, kmask3, kbias3, kmask3p);
+        x1 = band_pair<3>(r, b0, 2 * s + 1, kmask3, kbias3, kmask3p);
     }
     return __builtin_bit_cast(half4_t, u32x2{x0, x1});
 }
@@ -360,22 +403,30 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
         split_hl(va, ha, la);
         split_hl(vb, hb, lb);
         const int ba = lane >> 5, bb = 2 + (lane >> 5);  // bands of coefficients lane and lane + 64
-        const int ia = 32 * ba + score_slot(ba, lane & 31), ib = 32 * bb + score_slot(bb, lane & 31);
-        qs[(0 * 8 + h) * QS_STRIDE + ia] = (unsigned short)ha;
-        qs[(1 * 8 + h) * QS_STRIDE + ia] = (unsigned short)la;
-        qs[(0 * 8 + h) * QS_STRIDE + ib] = (unsigned short)hb;
-        qs[(1 * 8 + h) * QS_STRIDE + ib] = (unsigned short)lb;
-        // band sums of hi + lo over each 32-lane half
-        float sa = (float)__builtin_bit_cast(_Float16, (unsigned short)ha) + (float)__builtin_bit_cast(_Float16, (unsigned short)la);
-        float sb = (float)__builtin_bit_cast(_Float16, (unsigned short)hb) + (float)__builtin_bit_cast(_Float16, (unsigned short)lb);
+        const int sa_ = score_slot(ba, lane & 31), sb_ = score_slot(bb, lane & 31);
+        const int ia = 32 * ba + (sa_ & 0xff), ib = 32 * bb + (sb_ & 0xff);
+        // a half-gain slot (its code stored as 2^BITS + c/2) holds 2q~: exact in fp16
+        const float ga = (sa_ & 0x100) ? 2.0f : 1.0f, gb = (sb_ & 0x100) ? 2.0f : 1.0f;
+        const float fha = (float)__builtin_bit_cast(_Float16, (unsigned short)ha), fla = (float)__builtin_bit_cast(_Float16, (unsigned short)la);
+        const float fhb = (float)__builtin_bit_cast(_Float16, (unsigned short)hb), flb = (float)__builtin_bit_cast(_Float16, (unsigned short)lb);
+        qs[(0 * 8 + h) * QS_STRIDE + ia] = __builtin_bit_cast(unsigned short, (_Float16)(fha * ga));
+        qs[(1 * 8 + h) * QS_STRIDE + ia] = __builtin_bit_cast(unsigned short, (_Float16)(fla * ga));
+        qs[(0 * 8 + h) * QS_STRIDE + ib] = __builtin_bit_cast(unsigned short, (_Float16)(fhb * gb));
+        qs[(1 * 8 + h) * QS_STRIDE + ib] = __builtin_bit_cast(unsigned short, (_Float16)(flb * gb));
+        // centring: sum over the band of q~ (offset / gain + m_b), the slot's fp16
+        // value being offset + gain * code with offset 2^BITS
+        const float wa = ga * (float)(1 << kbits(ba)) + (float)((1 << (kbits(ba) - 1)) - 1);
+        const float wb = gb * (float)(1 << kbits(bb)) + (float)((1 << (kbits(bb) - 1)) - 1);
+        float sa = (fha + fla) * wa;
+        float sb = (fhb + flb) * wb;
         sa = wave_sum_step<1>(sa); sb = wave_sum_step<1>(sb);
         sa = wave_sum_step<2>(sa); sb = wave_sum_step<2>(sb);
         sa = wave_sum_step<4>(sa); sb = wave_sum_step<4>(sb);
         sa = wave_sum_step<8>(sa); sb = wave_sum_step<8>(sb);
         sa = wave_sum_step<16>(sa); sb = wave_sum_step<16>(sb);
         if ((lane & 31) == 0) {
-            cb[h * 4 + ba] = -(float)((1 << kbits(ba)) + (1 << (kbits(ba) - 1)) - 1) * sa;  // -(2^BITS + m_b)
-            cb[h * 4 + bb] = -(float)((1 << kbits(bb)) + (1 << (kbits(bb) - 1)) - 1) * sb;
+            cb[h * 4 + ba] = -sa;
+            cb[h * 4 + bb] = -sb;
         }
         if (lane == 0) fu[h] = 1.0f / f;  // exact: a power of two
         // publish: this wave's LDS writes are complete before it counts itself
@@ -402,7 +453,8 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
     const uint32_t kbias3 = __builtin_amdgcn_readfirstlane(code_bias<3>());
     const uint32_t vbias = __builtin_amdgcn_readfirstlane(VBIAS);
     uint32_t kmask5 = code_mask<5>(), kmask4 = code_mask<4>(), kmask3 = code_mask<3>(), vmask = VMASK;
-    __asm__("" : "+v"(kmask5), "+v"(kmask4), "+v"(kmask3), "+v"(vmask));
+    uint32_t kmask5p = 0x01F003E0u, kmask3p = 0x01C00380u;  // 15-bit pairs: bits 5..9 + 20..24, 7..9 + 22..24
+    __asm__("" : "+v"(kmask5), "+v"(kmask4), "+v"(kmask3), "+v"(vmask), "+v"(kmask5p), "+v"(kmask3p));
 
     // running state of this lane's value heads 2*q4 + hh over the wave's tiles
     float om[2] = {-INFINITY, -INFINITY}, ol[2] = {0.0f, 0.0f};
@@ -427,11 +479,12 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
         stage_tile<WANT_OUT>(wl, regs, lane);
         __asm__ volatile("" ::: "memory");
         // ---- lane t takes record t of the K tile into registers, and the scale of its V record ----
-        uint32_t r[19];
+        uint32_t r[20];
         {
             const uint32_t *kr = reinterpret_cast<const uint32_t *>(wl + R_K + ln * KB);
 #pragma unroll
             for (int m = 0; m < 19; m++) r[m] = kr[m];
+            r[19] = 0;
         }
         float sv_own = 0.0f;
         if (WANT_OUT)
@@ -461,7 +514,7 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
 #pragma unroll
             for (int b = 0; b < 4; b++) {
                 if (!ALL_BANDS && b >= kbands) break;  // bands past the limit read as 0 (kernel-uniform)
-                a[b] = score_codes(r, b, s, kmask5, kbias5, kmask4, kbias4, kmask3, kbias3);
+                a[b] = score_codes(r, b, s, kmask5, kbias5, kmask4, kbias4, kmask3, kbias3, kmask5p, kmask3p);
             }
 #pragma unroll
             for (int st = 0; st < NH; st++)
@@ -662,33 +715,46 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
     __syncthreads();
     int *flag = reinterpret_cast<int *>(smem + S_FLAG);
     if (tid == 0) {
-        const int arrived = __hip_atomic_fetch_add(counters + kvh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        int *cnt = counters + kvh * SP_ATTN_COUNTER_STRIDE;
+        const int arrived = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const int last = arrived == n_parts - 1;
-        if (last) __hip_atomic_store(counters + kvh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // ready for the next call
+        if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // ready for the next call
         *flag = last;
     }
     __syncthreads();
     if (!*flag) return;
-    float *ml = reinterpret_cast<float *>(smem);  // [G][n_parts][m, l]
-    float *vec = ml + 8 * MAX_PARTS * 2;          // [G][HD] merged o~ / L
-    for (int k = tid; k < G * n_parts; k += NT) {
-        const int h = k / n_parts, pp = k - h * n_parts;
-        const float *src = part + ((long long)(h0 + h) * n_parts + pp) * (HD + 2);
-        ml[2 * k] = __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        ml[2 * k + 1] = __hip_atomic_load(src + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
+    // thread (h, i) loads every partial's m, l and o~[i] at once (one memory round
+    // trip per 32 partials; the m and l addresses are the same across a wave)
+    float *vec = reinterpret_cast<float *>(smem);  // [G][HD] merged o~ / L
     if (tid < G * HD) {
         const int h = tid >> 7, i = tid & (HD - 1);
-        const float *mh = ml + 2 * h * n_parts;
-        float M = -INFINITY;
-        for (int pp = 0; pp < n_parts; pp++) M = fmaxf(M, mh[2 * pp]);
-        float L = 0.0f, O = 0.0f;
-        const float *src = part + (long long)(h0 + h) * n_parts * (HD + 2) + 2 + i;
-        for (int pp = 0; pp < n_parts; pp++) {
-            const float e = __expf(mh[2 * pp] - M);
-            L = fmaf(mh[2 * pp + 1], e, L);
-            O = fmaf(__hip_atomic_load(src + (long long)pp * (HD + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), e, O);
+        const float *src = part + (long long)(h0 + h) * n_parts * (HD + 2);
+        float M = -INFINITY, L = 0.0f, O = 0.0f;
+        for (int p0 = 0; p0 < n_parts; p0 += 32) {
+            float pm[32], pl[32], po[32];
+#pragma unroll
+            for (int k = 0; k < 32; k++) {
+                const int pp = min(p0 + k, n_parts - 1);  // a repeated last partial is skipped below
+                const float *r = src + (long long)pp * (HD + 2);
+                pm[k] = __hip_atomic_load(r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                pl[k] = __hip_atomic_load(r + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                po[k] = __hip_atomic_load(r + 2 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            float cm = M;
+#pragma unroll
+            for (int k = 0; k < 32; k++)
+                if (p0 + k < n_parts) cm = fmaxf(cm, pm[k]);
+            const float a = __expf(M - cm);  // rescale of the running sums (0 on the first chunk)
+            L *= a;
+            O *= a;
+#pragma unroll
+            for (int k = 0; k < 32; k++)
+                if (p0 + k < n_parts) {
+                    const float e = __expf(pm[k] - cm);
+                    L = fmaf(pl[k], e, L);
+                    O = fmaf(po[k], e, O);
+                }
+            M = cm;
         }
         vec[tid] = O / L;
     }
@@ -746,7 +812,7 @@ hipError_t sp_launch_attn_wave(const SpPlan &KP, const SpPlan &VP, const int *or
         if (KP.band_bits[b] != kb[b] || KP.band_off[b] != 32 * b || KP.band_sz[b] != 32 ||
             KP.band_byte_off[b] != (b == 0 ? 0 : b == 1 ? 22 : b == 2 ? 44 : 62))
             return hipErrorNotSupported;
-    if (A.n_q % A.n_kvh || A.n_q / A.n_kvh > 8 || A.n_kvh > SP_ATTN_COUNTERS) return hipErrorNotSupported;
+    if (A.n_q % A.n_kvh || A.n_q / A.n_kvh > 8 || A.n_kvh > SP_ATTN_MAX_KVH) return hipErrorNotSupported;
     if (((uintptr_t)A.kpack % 4) || ((uintptr_t)A.vpack % 2) || (A.k_head_stride % 4) || (A.v_head_stride % 2))
         return hipErrorNotSupported;
     // Tiles per wave: one round of blocks (one per CU) when the context allows.

@@ -319,9 +319,12 @@ hipError_t sp_launch_attn_mfma_split(const SpPlan &KP, const SpPlan &VP, const i
                                      const SpAttnArgs &A, float *part, int n_splits, int *n_parts,
                                      hipStream_t s);
 // Words at the end of every attention workspace (sp_attn_workspace_floats) that
-// hold the wave kernel's per-KV-head arrival counters: zero when the workspace
-// is created, and back at zero after each call.
-#define SP_ATTN_COUNTERS 256
+// hold the wave kernel's per-KV-head arrival counters, one per 256-byte line
+// (SP_ATTN_COUNTER_STRIDE words) so the KV heads' atomics do not queue on one
+// line: zero when the workspace is created, and back at zero after each call.
+#define SP_ATTN_COUNTER_STRIDE 64
+#define SP_ATTN_MAX_KVH 256
+#define SP_ATTN_COUNTERS (SP_ATTN_MAX_KVH * SP_ATTN_COUNTER_STRIDE)
 // Wave-tiled matrix-core kernel for the same layout (sp_attn_wave.hip): scores
 // and/or the attention output in one launch (each block writes a spectral-domain
 // partial [m, l, o~[hd]] per query head, at most part_floats floats, and the last

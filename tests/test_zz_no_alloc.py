@@ -69,9 +69,12 @@ def test_noalloc_refuses_oversized_calls(cache):
     L = S.lib()
     cap = L.sp_hip_attn_noalloc_max_floats()
     assert cap == (16 << 20) // 4
-    n_q = 64  # 64*128 + 64*ceil(n_kv/256)*130 floats: over 16 MiB from 504 splits on
-    n_kv = 504 * 256
-    assert n_q * HD + n_q * ((n_kv + 255) // 256) * (HD + 2) > cap
+    # 64*128 + 64*ceil(n_kv/256)*130 floats + the 256 arrival counters (one per 64-word
+    # line, plus one line of alignment slack): over 16 MiB from 502 splits on
+    n_q = 64
+    counters = 256 * 64 + 64
+    n_kv = 502 * 256
+    assert n_q * HD + n_q * ((n_kv + 255) // 256) * (HD + 2) + counters > cap
     qt = dev(np.ones((n_q, HD), np.float32))
     sc = torch.full((n_q * n_kv,), 7.0, dtype=torch.float32, device="cuda")
     out = torch.full((n_q * HD,), 7.0, dtype=torch.float32, device="cuda")
@@ -81,7 +84,8 @@ def test_noalloc_refuses_oversized_calls(cache):
     assert b"scratch" in S.lib().sp_hip_last_error()
     assert bool((sc == 7.0).all()) and bool((out == 7.0).all())
     # one split fewer fits
-    n_kv = 503 * 256
+    n_kv = 501 * 256
+    assert n_q * HD + n_q * ((n_kv + 255) // 256) * (HD + 2) + counters <= cap
     rc = L.sp_hip_attn_decode_bands_noalloc(cache.ref, 0, n_kv, p(qt), n_q, C.c_float(1.0), None, p(out), -1,
                                             stream())
     assert rc == 0
