@@ -33,8 +33,9 @@
 //     subtract centres it (u - 3, exact).
 //   * the block's waves merge their (m, l, o~) in LDS; each block writes one
 //     spectral-domain partial [m, l, o~[128]] per query head with agent-scope
-//     atomic stores and counts itself on its KV head's counter; the block that
-//     arrives last merges the partials and applies one inverse VHT2 per head.
+//     atomic stores, waits for them to complete and counts itself on its KV
+//     head's counter; the block that arrives last reads the partials back with
+//     agent-scope atomic loads, merges them and applies one inverse VHT2 per head.
 #include "sp_internal.h"
 #include "sp_mfma_codes.h"
 
@@ -129,11 +130,16 @@ __device__ __forceinline__ void split_hl(float v, uint32_t &hi, uint32_t &lo) {
     lo = (uint32_t)__builtin_bit_cast(unsigned short, l);
 }
 
-// Power of two p with amax * p in [2^11, 2^12) (1 when amax is 0 or not finite).
-__device__ __forceinline__ float pow2_norm(float amax) {
-    if (!(amax > 0.0f) || !(amax < INFINITY)) return 1.0f;
+// Power of two p with amax * p in [2^11, 2^12) (1 when amax is 0 or not finite),
+// and its reciprocal (exact).
+__device__ __forceinline__ float pow2_norm(float amax, float &inv) {
+    if (!(amax > 0.0f) || !(amax < INFINITY)) {
+        inv = 1.0f;
+        return 1.0f;
+    }
     int e;
     (void)frexpf(amax, &e);  // amax = f * 2^e, f in [0.5, 1)
+    inv = ldexpf(1.0f, e - 12);
     return ldexpf(1.0f, 12 - e);
 }
 
@@ -181,8 +187,12 @@ __device__ __forceinline__ float lane_butterfly(float x, int lane) {
     return fmaf(x, (lane & M) ? -1.0f : 1.0f, p);
 }
 
+// max(a, b) of finite or infinite values as one v_med3 (fmaxf would first quiet
+// the exchanged operand, an extra instruction per step)
+__device__ __forceinline__ float max_ninf(float a, float b) { return __builtin_amdgcn_fmed3f(a, b, INFINITY); }
+
 template <int M>
-__device__ __forceinline__ float wave_max_step(float v) { return fmaxf(v, lane_xor<M>(v)); }
+__device__ __forceinline__ float wave_max_step(float v) { return max_ninf(v, lane_xor<M>(v)); }
 template <int M>
 __device__ __forceinline__ float wave_sum_step(float v) { return v + lane_xor<M>(v); }
 
@@ -388,7 +398,8 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
         amax = wave_max_step<8>(amax);
         amax = wave_max_step<16>(amax);
         amax = wave_max_step<32>(amax);
-        const float f = pow2_norm(amax);
+        float finv;
+        const float f = pow2_norm(amax, finv);
         // record coefficients lane (bands 0, 1) and lane + 64 (bands 2, 3)
         float va, vb;
         {
@@ -428,7 +439,7 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
             cb[h * 4 + ba] = -sa;
             cb[h * 4 + bb] = -sb;
         }
-        if (lane == 0) fu[h] = 1.0f / f;  // exact: a power of two
+        if (lane == 0) fu[h] = finv;
         // publish: this wave's LDS writes are complete before it counts itself
         __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         if (lane == 0) __hip_atomic_fetch_add(ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -440,6 +451,8 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
     // each wave instead checks `ready` just before its first query read ----
     const int vshift = WANT_OUT ? (int)((uintptr_t)(A.vpack + (long long)kvh * A.v_head_stride) & 3) : 0;
     const int tile0 = (blk * NW + w) * tpw;  // tile index of the wave's first tile within the KV head
+    // score rows 16-byte aligned at every tile: one 16-byte store per lane
+    const bool sc_vec = ((uintptr_t)A.scores & 15) == 0 && (A.n_kv & 3) == 0;
     TileRegs regs;
     {
         const int c0 = tile0 * TILE;
@@ -488,7 +501,8 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
         }
         float sv_own = 0.0f;
         if (WANT_OUT)
-            sv_own = (lane < n_chunk && (ALL_BANDS || vbands > 0))
+            // (a lane past the tile's end takes whatever scale lies there: its weight is p = 0)
+            sv_own = (ALL_BANDS || vbands > 0)
                          ? scale_of(*reinterpret_cast<const unsigned short *>(wl + R_V + vshift + ln * VB))
                          : 0.0f;
         __asm__ volatile("" ::: "memory");  // every lane has read its record before the K area is reused
@@ -529,10 +543,11 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
                     }
         }
         // band scales of the lane's own record; position 4*qd + i's come from quad lane i
+        // (a lane past the tile's end holds a zero record: scale 0)
         float ks[4];
 #pragma unroll
         for (int b = 0; b < 4; b++)
-            ks[b] = (lane < n_chunk && (ALL_BANDS || b < kbands)) ? scale_of(rec_bits(r, 8 * kbyte(b), 16)) : 0.0f;
+            ks[b] = (ALL_BANDS || b < kbands) ? scale_of(rec_bits(r, 8 * kbyte(b), 16)) : 0.0f;
         float sc[NH][4];
 #pragma unroll
         for (int st = 0; st < NH; st++) {
@@ -557,9 +572,13 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
             for (int i = 0; i < 4; i++) sc[st][i] *= un;
             if (A.scores && 4 * st + hj < G) {
                 float *dst = A.scores + (long long)(h0 + 4 * st + hj) * A.n_kv + c0 + 4 * qd;
+                if (n_chunk == TILE && sc_vec) {
+                    *reinterpret_cast<float4 *>(dst) = float4{sc[st][0], sc[st][1], sc[st][2], sc[st][3]};
+                } else {
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-                    if (4 * qd + i < n_chunk) dst[i] = sc[st][i];
+                    for (int i = 0; i < 4; i++)
+                        if (4 * qd + i < n_chunk) dst[i] = sc[st][i];
+                }
             }
         }
         if (!WANT_OUT) continue;
@@ -571,21 +590,24 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
         const float sv[4] = {quad_bcast<0>(sv_own), quad_bcast<1>(sv_own), quad_bcast<2>(sv_own), quad_bcast<3>(sv_own)};
 #pragma unroll
         for (int st = 0; st < NH; st++) {
-            float v[4];
+            float v[4] = {sc[st][0], sc[st][1], sc[st][2], sc[st][3]};
+            if (n_chunk < TILE) {  // positions past the tile's end take no weight
 #pragma unroll
-            for (int i = 0; i < 4; i++) v[i] = 4 * qd + i < n_chunk ? sc[st][i] : -INFINITY;
+                for (int i = 0; i < 4; i++) v[i] = 4 * qd + i < n_chunk ? v[i] : -INFINITY;
+            }
             float m = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
             m = head_max(m);  // finite: the tile holds at least one position
             float l = 0.0f, wm = 0.0f, wv[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const float p = __expf(v[i] - m);
-                l += p;
+                l = i == 0 ? p : l + p;
                 wv[i] = p * sv[i];
                 wm = fmaxf(wm, wv[i]);
             }
             wm = head_max(wm);
-            const float f = pow2_norm(wm);
+            float finv;
+            const float f = pow2_norm(wm, finv);
             uint32_t hi[4], lo[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -599,7 +621,7 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
             *reinterpret_cast<u32x2 *>(wt + row * WT_STRIDE + 4 * qd) = u32x2{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)};
             *reinterpret_cast<u32x2 *>(wt + (row + 1) * WT_STRIDE + 4 * qd) = u32x2{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
             l = head_sum(l);
-            if (qd == 0) *reinterpret_cast<float4 *>(stt + 4 * (4 * st + hj)) = float4{m, l, 1.0f / f, 0.0f};
+            if (qd == 0) *reinterpret_cast<float4 *>(stt + 4 * (4 * st + hj)) = float4{m, l, finv, 0.0f};
         }
         __asm__ volatile("" ::: "memory");
 
@@ -821,7 +843,7 @@ hipError_t sp_launch_attn_wave(const SpPlan &KP, const SpPlan &VP, const int *or
     int tpw = (int)std::max(1LL, ((long long)A.n_kvh * n_tiles + waves - 1) / waves);
     tpw = (int)std::max<long long>(tpw, (n_tiles + (long long)NW * MAX_PARTS - 1) / ((long long)NW * MAX_PARTS));
     const int nb = (int)((n_tiles + (long long)NW * tpw - 1) / ((long long)NW * tpw));
-    if ((size_t)A.n_q * nb * (HD + 2) > part_floats || !counters) return hipErrorInvalidValue;
+    if (!part || !counters || (size_t)A.n_q * nb * (HD + 2) > part_floats) return hipErrorInvalidValue;
     // every band: a branch-free score loop (the band-limited one schedules worse)
     const bool all = KP.max_bands >= 4 && VP.max_bands >= 1;
     const bool multi = tpw > 1;
