@@ -467,7 +467,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--attn-iters", type=int, default=5)
+    ap.add_argument("--attn-iters", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", choices=["codec", "attn", "variants", "all"], default="all")
     ap.add_argument("--copy-calib", action="store_true",
@@ -586,7 +586,8 @@ def main():
                                                  None, P(out[layer]), sptr), "attn_f16")
 
         def timeit(f):
-            f()
+            for _ in range(3):  # warm-up calls: the first ones after a change of work run slower
+                f()
             torch.cuda.synchronize()
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record(stream)

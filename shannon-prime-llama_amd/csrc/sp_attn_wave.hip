@@ -353,8 +353,18 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
     float *cb = reinterpret_cast<float *>(smem + S_CB);                    // [head][band]
     float *fu = reinterpret_cast<float *>(smem + S_FU);                    // [head]
 
-    // ---- 1. wave w < G prepares head w: its query row and the order entries of
-    // record coefficients lane and lane + 64 are loaded first ----
+    // ---- 1. the waves w >= G issue their first tile's record loads at once;
+    // wave w < G prepares head w first: its query row and the order entries of
+    // record coefficients lane and lane + 64 ----
+    int *ready = reinterpret_cast<int *>(smem + S_FLAG + 4);  // query-operand waves done
+    if (tid == 0) *ready = 0;
+    __syncthreads();
+    const int vshift = WANT_OUT ? (int)((uintptr_t)(A.vpack + (long long)kvh * A.v_head_stride) & 3) : 0;
+    const int tile0 = (blk * NW + w) * tpw;  // tile index of the wave's first tile within the KV head
+    const int c00 = tile0 * TILE;
+    const int n_chunk0 = c00 < A.n_kv ? min(TILE, A.n_kv - c00) : 0;
+    TileRegs regs;
+    if (w >= G) load_tile<WANT_OUT>(A, kvh, c00, n_chunk0, vshift, lane, regs);
     float qx0 = 0.0f, qx1 = 0.0f;
     int ord0 = lane, ord1 = lane + 64;
     if (w < G) {
@@ -368,12 +378,6 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
         ord0 = order ? ov0 : lane;
         ord1 = order ? ov1 : lane + 64;
     }
-    // The query rows arrive before any record load is issued: issued next to the
-    // whole grid's record loads they would wait behind them.
-    int *ready = reinterpret_cast<int *>(smem + S_FLAG + 4);  // query-operand waves done
-    if (tid == 0) *ready = 0;
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
 
     // ---- 2. q~ = kq_scale * reorder(VHT2(q)) for head w, in registers (lane
     // holds elements lane and lane + 64), scaled by a power of two fh so its
@@ -445,20 +449,11 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
         if (lane == 0) __hip_atomic_fetch_add(ready, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
 
-    // ---- 3. the wave's first tile. No block barrier here: a wave that issues
-    // its record loads into a saturated memory system stalls at issue, so a
-    // barrier after them would hold every wave until the data is nearly in;
-    // each wave instead checks `ready` just before its first query read ----
-    const int vshift = WANT_OUT ? (int)((uintptr_t)(A.vpack + (long long)kvh * A.v_head_stride) & 3) : 0;
-    const int tile0 = (blk * NW + w) * tpw;  // tile index of the wave's first tile within the KV head
+    // ---- 3. the preparing waves' first tile. No block barrier here: each wave
+    // checks `ready` just before its first query read ----
+    if (w < G) load_tile<WANT_OUT>(A, kvh, c00, n_chunk0, vshift, lane, regs);
     // score rows 16-byte aligned at every tile: one 16-byte store per lane
     const bool sc_vec = ((uintptr_t)A.scores & 15) == 0 && (A.n_kv & 3) == 0;
-    TileRegs regs;
-    {
-        const int c0 = tile0 * TILE;
-        const int n_chunk = c0 < A.n_kv ? min(TILE, A.n_kv - c0) : 0;
-        load_tile<WANT_OUT>(A, kvh, c0, n_chunk, vshift, lane, regs);
-    }
 
     // code-slot masks and the fp16 2^BITS exponent bits, kept in registers for bitop3
     const uint32_t kbias5 = __builtin_amdgcn_readfirstlane(code_bias<5>());
