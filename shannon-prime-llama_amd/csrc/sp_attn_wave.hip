@@ -740,40 +740,67 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
     }
     __syncthreads();
     if (!*flag) return;
-    // thread (h, i) loads every partial's m, l and o~[i] at once (one memory round
-    // trip per 32 partials; the m and l addresses are the same across a wave)
-    float *vec = reinterpret_cast<float *>(smem);  // [G][HD] merged o~ / L
-    if (tid < G * HD) {
-        const int h = tid >> 7, i = tid & (HD - 1);
+    // Two halves of the block (G <= 4) take half the partials each: thread
+    // (half, h, i) loads o~[i] of its partials, and lane k of each 16-lane row
+    // the m and l of partial p0 + k, shared across the row (one m, l load per
+    // partial and lane instead of one per element)
+    float *vec = reinterpret_cast<float *>(smem);   // [G][HD] merged o~ / L
+    float *xo = vec + 8 * HD;                       // second half's o~ [G][HD]
+    float *xml = xo + 8 * HD;                       // second half's (M, L) [G][2]
+    const int GH = G * HD, halves = 2 * GH <= NT ? 2 : 1;
+    const int half = tid >= GH ? 1 : 0, r = tid - half * GH, h = r >> 7, i = r & (HD - 1);
+    const int per = (n_parts + halves - 1) / halves, pb = half * per, pe = min(n_parts, pb + per);
+    float M = -INFINITY, L = 0.0f, O = 0.0f;
+    if (tid < halves * GH) {
         const float *src = part + (long long)(h0 + h) * n_parts * (HD + 2);
-        float M = -INFINITY, L = 0.0f, O = 0.0f;
-        for (int p0 = 0; p0 < n_parts; p0 += 32) {
-            float pm[32], pl[32], po[32];
+        for (int p0 = pb; p0 < pe; p0 += 16) {
+            const int pk = min(p0 + (lane & 15), pe - 1);
+            const float mk0 = __hip_atomic_load(src + (long long)pk * (HD + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const float lk = __hip_atomic_load(src + (long long)pk * (HD + 2) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            float po[16];
 #pragma unroll
-            for (int k = 0; k < 32; k++) {
-                const int pp = min(p0 + k, n_parts - 1);  // a repeated last partial is skipped below
-                const float *r = src + (long long)pp * (HD + 2);
-                pm[k] = __hip_atomic_load(r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                pl[k] = __hip_atomic_load(r + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                po[k] = __hip_atomic_load(r + 2 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            float cm = M;
-#pragma unroll
-            for (int k = 0; k < 32; k++)
-                if (p0 + k < n_parts) cm = fmaxf(cm, pm[k]);
-            const float a = __expf(M - cm);  // rescale of the running sums (0 on the first chunk)
-            L *= a;
+            for (int k = 0; k < 16; k++)
+                po[k] = __hip_atomic_load(src + (long long)min(p0 + k, pe - 1) * (HD + 2) + 2 + i, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+            const float mk = p0 + (lane & 15) < pe ? mk0 : -INFINITY;  // a repeated last partial counts once
+            float cm = mk;
+            cm = wave_max_step<1>(cm);
+            cm = wave_max_step<2>(cm);
+            cm = wave_max_step<4>(cm);
+            cm = wave_max_step<8>(cm);
+            cm = fmaxf(cm, M);
+            const float ek = mk == -INFINITY ? 0.0f : __expf(mk - cm);
+            float ls = lk * ek;
+            ls = wave_sum_step<1>(ls);
+            ls = wave_sum_step<2>(ls);
+            ls = wave_sum_step<4>(ls);
+            ls = wave_sum_step<8>(ls);
+            const float a = M == -INFINITY ? 0.0f : __expf(M - cm);  // rescale of the running sums
+            L = fmaf(L, a, ls);
             O *= a;
 #pragma unroll
-            for (int k = 0; k < 32; k++)
-                if (p0 + k < n_parts) {
-                    const float e = __expf(pm[k] - cm);
-                    L = fmaf(pl[k], e, L);
-                    O = fmaf(po[k], e, O);
-                }
+            for (int k = 0; k < 16; k++)
+                O = fmaf(po[k], __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ek), k)), O);
             M = cm;
         }
-        vec[tid] = O / L;
+    }
+    if (halves == 2 && half == 1) {
+        xo[r] = O;
+        if (i == 0) {
+            xml[2 * h] = M;
+            xml[2 * h + 1] = L;
+        }
+    }
+    __syncthreads();
+    if (tid < GH) {
+        if (halves == 2) {
+            const float m2 = xml[2 * h], l2 = xml[2 * h + 1], o2 = xo[r];
+            const float cm = fmaxf(M, m2);
+            const float a = M == -INFINITY ? 0.0f : __expf(M - cm), b = m2 == -INFINITY ? 0.0f : __expf(m2 - cm);
+            L = fmaf(L, a, l2 * b);
+            O = fmaf(O, a, o2 * b);
+        }
+        vec[r] = O / L;
     }
     __syncthreads();
     // ---- one inverse VHT2 per query head: wave h, lane holds elements lane and lane + 64 ----
