@@ -19,7 +19,6 @@
 // No full-precision K or V is materialized anywhere.
 #include "sp_internal.h"
 
-#include <cstdlib>
 
 #define ATT_CHUNK 256
 #define ATT_MAX_G 8
@@ -230,72 +229,6 @@ k_attn_combine(const SpPlan VP, const float *__restrict__ ws, int n_splits, int 
         for (int k = tid; k < hd; k += SP_WAVE) out[(long long)h * hd + k] = c[k];
 }
 
-// Merge natural-domain partials [m, l, o[hd]] of query head blockIdx.x:
-// out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s. Block (h, y) produces
-// elements 32y .. 32y+31; thread (element, group g of 8) sums partials g, g+8, ...
-// Its first MERGE_PRE partial values and the first 256 (m, l) pairs are loaded
-// together up front, so a typical merge waits on memory once.
-#define MERGE_PRE 8
-__global__ void __launch_bounds__(256)
-k_attn_merge(const float *__restrict__ ws, int n_parts, int hd, float *__restrict__ out) {
-    __shared__ float e_s[ATT_MAX_SPLITS];
-    __shared__ float red[256];
-    __shared__ float wred[4];
-    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const long long row = hd + 2;
-    const float *base = ws + (long long)h * n_parts * row;
-    const int el = tid & 31, g = tid >> 5, i = 32 * blockIdx.y + el;
-    const bool live = i < hd;
-    const float *p = base + 2 + (live ? i : 0);
-    float pre[MERGE_PRE];
-#pragma unroll
-    for (int r = 0; r < MERGE_PRE; r++) {
-        const int sp = g + 8 * r;
-        pre[r] = (live && sp < n_parts) ? p[sp * row] : 0.0f;
-    }
-    const float m0 = tid < n_parts ? base[tid * row] : -INFINITY;
-    const float l0 = tid < n_parts ? base[tid * row + 1] : 0.0f;
-    float M = m0;
-    for (int sp = tid + 256; sp < n_parts; sp += 256) M = fmaxf(M, base[sp * row]);
-    M = sp_wave_max(M);
-    if (lane == 0) wred[wv] = M;
-    __syncthreads();
-    M = fmaxf(fmaxf(wred[0], wred[1]), fmaxf(wred[2], wred[3]));
-    __syncthreads();
-    float L = 0.0f;
-    if (tid < n_parts) {
-        const float e = __expf(m0 - M);
-        e_s[tid] = e;
-        L = l0 * e;
-    }
-    for (int sp = tid + 256; sp < n_parts; sp += 256) {
-        const float e = __expf(base[sp * row] - M);
-        e_s[sp] = e;
-        L += base[sp * row + 1] * e;
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o, 64);
-    if (lane == 0) wred[wv] = L;
-    __syncthreads();
-    L = (wred[0] + wred[1]) + (wred[2] + wred[3]);
-    float acc = 0.0f;
-#pragma unroll
-    for (int r = 0; r < MERGE_PRE; r++) {
-        const int sp = g + 8 * r;
-        if (sp < n_parts) acc = fmaf(pre[r], e_s[sp], acc);
-    }
-    if (live)
-        for (int sp = g + 8 * MERGE_PRE; sp < n_parts; sp += 8) acc = fmaf(p[sp * row], e_s[sp], acc);
-    red[tid] = acc;
-    __syncthreads();
-    if (tid < 32 && live) {
-        float t = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 8; k++) t += red[32 * k + tid];
-        out[(long long)h * hd + i] = t / L;
-    }
-}
-
 size_t sp_attn_workspace_floats(int n_q, int hd, int max_kv) {
     const int n_splits = (max_kv + ATT_CHUNK - 1) / ATT_CHUNK;
     return (size_t)n_q * hd + (size_t)n_q * n_splits * (hd + 2) + SP_ATTN_COUNTERS + SP_ATTN_COUNTER_STRIDE;
@@ -312,9 +245,7 @@ hipError_t sp_launch_attn_decode(const SpPlan &KP, const SpPlan &VP, const int *
     float *qt = workspace;
     float *part = workspace + (size_t)A.n_q * A.hd;
     const int want_out = A.out != nullptr;
-    int n_parts = 0;
-    const char *old_k = getenv("SP_HIP_ATTN_OLD");
-    if (!(old_k && old_k[0] == '1')) {
+    {
         // the per-KV-head arrival counters: the workspace's last SP_ATTN_COUNTERS words
         // (plus up to one line of slack), starting on a 256-byte boundary
         const uintptr_t ctail = (uintptr_t)(workspace + ws_floats - SP_ATTN_COUNTERS - SP_ATTN_COUNTER_STRIDE);
@@ -323,13 +254,6 @@ hipError_t sp_launch_attn_decode(const SpPlan &KP, const SpPlan &VP, const int *
             KP, VP, order, A, part, ws_floats - (size_t)A.n_q * A.hd - SP_ATTN_COUNTERS - SP_ATTN_COUNTER_STRIDE, cnt, s);
         if (we != hipErrorNotSupported) return we;
     }
-    const hipError_t me = sp_launch_attn_mfma_split(KP, VP, order, A, part, n_splits, &n_parts, s);
-    if (me == hipSuccess) {
-        if (want_out)
-            hipLaunchKernelGGL(k_attn_merge, dim3(A.n_q, (A.hd + 31) / 32), dim3(256), 0, s, part, n_parts, A.hd, A.out);
-        return hipGetLastError();
-    }
-    if (me != hipErrorNotSupported) return me;
     hipLaunchKernelGGL(k_attn_prep, dim3(A.n_q), dim3(64), 0, s, KP, order, A.q, A.hd, A.kq_scale, qt);
     const size_t lds = (size_t)((ATT_CHUNK * A.kB + 8 + 15) & ~15) + (size_t)ATT_CHUNK * A.vB + 8;
     hipLaunchKernelGGL(k_attn_split, dim3(A.n_kvh, n_splits), dim3(256), lds, s, KP, VP, A, qt, part,

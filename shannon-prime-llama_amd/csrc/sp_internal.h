@@ -312,12 +312,6 @@ int sp_attn_prepare(const sp_hip_cache_t *cc, int layer, int n_kv, const float *
                     SpPlan *out_vp);
 // Sets the message sp_hip_last_error() returns (sp_runtime.cpp).
 void sp_set_error(const char *fmt, ...);
-// Split kernel on the matrix cores for head_dim 128 with K 5/5/4/3 and V 3-bit;
-// hipErrorNotSupported for any other layout. With an output it writes *n_parts
-// natural-domain partials [m, l, o[hd]] per query head (merged by k_attn_merge).
-hipError_t sp_launch_attn_mfma_split(const SpPlan &KP, const SpPlan &VP, const int *order,
-                                     const SpAttnArgs &A, float *part, int n_splits, int *n_parts,
-                                     hipStream_t s);
 // Words at the end of every attention workspace (sp_attn_workspace_floats) that
 // hold the wave kernel's per-KV-head arrival counters, one per 256-byte line
 // (SP_ATTN_COUNTER_STRIDE words) so the KV heads' atomics do not queue on one
