@@ -172,7 +172,9 @@ def test_band_limited_attention_matches_oracle(n_q, H, n_ctx, path, monkeypatch)
 # split's records while it computes: 32768 gives runs of 2; 16600 (65 splits per
 # head, the last one partial) ends each head with a run of one partial split;
 # 40000 (157 splits per head) gives runs of 3.
-LONG_CASES = [(32, 8, 32768), (32, 8, 16600), (32, 8, 40000)]
+# (4, 1, 40000) and (8, 1, 40000): one KV head, so 40 blocks each write a partial; the last
+# block merges them in runs of 16 (two halves of 20 for GQA 4, one run of 40 for GQA 8)
+LONG_CASES = [(32, 8, 32768), (32, 8, 16600), (32, 8, 40000), (4, 1, 40000), (8, 1, 40000)]
 
 
 @functools.lru_cache(maxsize=1)
