@@ -452,7 +452,7 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
     // ---- 3. the preparing waves' first tile. No block barrier here: each wave
     // checks `ready` just before its first query read ----
     if (w < G) load_tile<WANT_OUT>(A, kvh, c00, n_chunk0, vshift, lane, regs);
-    // score rows 16-byte aligned at every tile: one 16-byte store per lane
+    // score rows 16-byte aligned at every tile: one 16-byte non-temporal store per lane
     const bool sc_vec = ((uintptr_t)A.scores & 15) == 0 && (A.n_kv & 3) == 0;
 
     // code-slot masks and the fp16 2^BITS exponent bits, kept in registers for bitop3
@@ -568,7 +568,7 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
             if (A.scores && 4 * st + hj < G) {
                 float *dst = A.scores + (long long)(h0 + 4 * st + hj) * A.n_kv + c0 + 4 * qd;
                 if (n_chunk == TILE && sc_vec) {
-                    *reinterpret_cast<float4 *>(dst) = float4{sc[st][0], sc[st][1], sc[st][2], sc[st][3]};
+                    __builtin_nontemporal_store(float4_t{sc[st][0], sc[st][1], sc[st][2], sc[st][3]}, reinterpret_cast<float4_t *>(dst));
                 } else {
 #pragma unroll
                     for (int i = 0; i < 4; i++)
