@@ -91,6 +91,7 @@ struct RegStage {
     }
 };
 constexpr int W_STAGE = 40;  // W elements per thread staged through registers (n_target * n_skel <= 10240)
+constexpr int MERGE_RUNS_PER_THREAD = 4;  // runs per merge thread (n_runs <= 4 * NT)
 
 // 4 little-endian bytes at LDS byte offset o (any alignment) of a dword-aligned array.
 __device__ __forceinline__ uint32_t lds_u32_at(const unsigned char *base, int o) {
@@ -139,33 +140,28 @@ struct LdsBits {
     }
 };
 
-// One Vilenkin stage of radix p over c[0, n) (stride `stride`), all NT threads,
-// the p x p cas matrix C (scaled by isp) read from LDS.
+// One Vilenkin stage of radix p from src to dst (stride `stride`), one output
+// element per thread: dst[e] = isp * sum_jj C[k][jj] src[base + jj*stride] for
+// e = base + k*stride (the same sums, in the same order, as a whole group per
+// thread, with p times the parallelism), the p x p cas matrix C read from LDS.
 template <int p>
-__device__ __forceinline__ void vil_stage(float *c, int n, int stride, const float *C, float isp, int tid) {
+__device__ __forceinline__ void vil_stage(const float *src, float *dst, int n, int stride, const float *C, float isp,
+                                          int tid) {
     const int block = stride * p;
-    for (int wi = tid; wi < n / p; wi += NT) {
-        const int base = (wi / stride) * block + (wi % stride);
-        float gv[p], rv[p];
+    for (int e = tid; e < n; e += NT) {
+        const int b0 = (e / block) * block, r = e - b0, k = r / stride, base = b0 + (r - k * stride);
+        float sum = 0.0f;
 #pragma unroll
-        for (int k = 0; k < p; k++) gv[k] = c[base + k * stride];
-#pragma unroll
-        for (int k = 0; k < p; k++) {
-            float sum = 0.0f;
-#pragma unroll
-            for (int jj = 0; jj < p; jj++) sum += C[k * p + jj] * gv[jj];
-            rv[k] = sum * isp;
-        }
-#pragma unroll
-        for (int k = 0; k < p; k++) c[base + k * stride] = rv[k];
+        for (int jj = 0; jj < p; jj++) sum += C[k * p + jj] * src[base + jj * stride];
+        dst[e] = sum * isp;
     }
 }
 
-// In-place transform of c[0, n) in LDS by the whole block: the stages of
-// sp_transform_lds (same arithmetic), with every thread of the block taking
-// groups and the cas tables copied to LDS (cas_s, SP_CAS_TOTAL floats) first.
-// Ends with a barrier.
-__device__ __forceinline__ void transform_block(float *c, int n, const SpPlan &P, float *cas_s, int tid) {
+// Transform of c[0, n) in LDS by the whole block (tmp: n more floats of LDS): the
+// stages of sp_transform_lds (same arithmetic), ping-ponging between c and tmp,
+// with the cas tables copied to LDS (cas_s, SP_CAS_TOTAL floats) first. The
+// result ends in c. Ends with a barrier.
+__device__ __forceinline__ void transform_block(float *c, float *tmp, int n, const SpPlan &P, float *cas_s, int tid) {
     if ((n & (n - 1)) == 0 || P.skip_transform) {
         sp_transform_lds(c, n, P, tid < SP_WAVE ? tid : n);
         __syncthreads();
@@ -173,19 +169,27 @@ __device__ __forceinline__ void transform_block(float *c, int n, const SpPlan &P
     }
     for (int i = tid; i < SP_CAS_TOTAL; i += NT) cas_s[i] = P.cas[i];
     __syncthreads();
+    float *src = c, *dst = tmp;
     int stride = 1;
     for (int f = 0; f < P.n_factors; f++) {
         const int p = P.factors[f];
         const float *C = cas_s + sp_cas_off(p);
         const float isp = P.isp[sp_prime_idx(p)];
         switch (p) {
-            case 2: vil_stage<2>(c, n, stride, C, isp, tid); break;
-            case 3: vil_stage<3>(c, n, stride, C, isp, tid); break;
-            case 5: vil_stage<5>(c, n, stride, C, isp, tid); break;
-            case 7: vil_stage<7>(c, n, stride, C, isp, tid); break;
-            default: vil_stage<11>(c, n, stride, C, isp, tid); break;
+            case 2: vil_stage<2>(src, dst, n, stride, C, isp, tid); break;
+            case 3: vil_stage<3>(src, dst, n, stride, C, isp, tid); break;
+            case 5: vil_stage<5>(src, dst, n, stride, C, isp, tid); break;
+            case 7: vil_stage<7>(src, dst, n, stride, C, isp, tid); break;
+            default: vil_stage<11>(src, dst, n, stride, C, isp, tid); break;
         }
         stride *= p;
+        __syncthreads();
+        float *t = src;
+        src = dst;
+        dst = t;
+    }
+    if (src != c) {  // an odd number of stages
+        for (int i = tid; i < n; i += NT) c[i] = src[i];
         __syncthreads();
     }
 }
@@ -230,6 +234,7 @@ k_hier_attn_prep(const SpPlan P, const SpHierAttnArgs A, float *__restrict__ pre
     extern __shared__ __attribute__((aligned(16))) unsigned char dsm[];
     __shared__ float wsum[NT / SP_WAVE];
     __shared__ float cas_s[SP_CAS_TOTAL];
+    __shared__ float tsm[SP_GEN_MAX_N];
     const int h = blockIdx.x, tid = threadIdx.x;
     const int G = A.n_q / A.n_kvh, kvh = h / G;
     const int ns = A.n_skel, nt = A.n_target, ns4 = r4(ns), nt32 = r32(nt);
@@ -248,7 +253,7 @@ k_hier_attn_prep(const SpPlan P, const SpHierAttnArgs A, float *__restrict__ pre
     for (int u = 0; u < (SP_GEN_MAX_N + NT - 1) / NT; u++) ti[u] = tid + u * NT < nt ? A.tgt_idx[tid + u * NT] : 0;
     for (int k = tid; k < A.pad; k += NT) c[k] = k < A.hd ? A.q[(long long)h * A.hd + k] : 0.0f;
     __syncthreads();
-    transform_block(c, A.pad, P, cas_s, tid);
+    transform_block(c, tsm, A.pad, P, cas_s, tid);
     if (w_reg) wst.store(Ws, nt * ns, tid);
 #pragma unroll
     for (int u = 0; u < (SP_GEN_MAX_N + NT - 1) / NT; u++) {
@@ -714,6 +719,7 @@ k_hier_attn_merge(const SpPlan P, const SpHierAttnArgs A, const float *__restric
     extern __shared__ __attribute__((aligned(16))) unsigned char dsm[];
     __shared__ float red[2 * (NT / SP_WAVE)];
     __shared__ float cas_s[SP_CAS_TOTAL];
+    __shared__ float tsm[SP_GEN_MAX_N];
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int G = A.n_q / A.n_kvh, kvh = h / G;
     const int ns = A.n_skel, nt = A.n_target, pp = A.pp;
@@ -728,17 +734,32 @@ k_hier_attn_merge(const SpPlan P, const SpHierAttnArgs A, const float *__restric
     if (w_reg) wst.load(Wk, nt * ns, tid);
     else copy_to_lds<unsigned short, 16>(Ws, Wk, nt * ns, nt * ns, tid);
     const float *ph = part + (long long)h * n_runs * pp;
+    // range-checked buffer loads (rows past the last run read as 0): unconditional,
+    // so every load of a pass is in flight before the first wait
+    const __amdgpu_buffer_rsrc_t rp =
+        __builtin_amdgcn_make_buffer_rsrc((void *)ph, (short)0, n_runs * pp * 4, 0x00020000);
+    float mr[MERGE_RUNS_PER_THREAD], lr[MERGE_RUNS_PER_THREAD];
+#pragma unroll
+    for (int u = 0; u < MERGE_RUNS_PER_THREAD; u++) {
+        const int r = tid + u * NT;
+        mr[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, r * pp * 4, 0, 0));
+        lr[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, r * pp * 4 + 4, 0, 0));
+        if (r >= n_runs) mr[u] = -INFINITY;
+    }
     float mx = -INFINITY;
-    for (int r = tid; r < n_runs; r += NT) mx = fmaxf(mx, ph[(long long)r * pp]);
+#pragma unroll
+    for (int u = 0; u < MERGE_RUNS_PER_THREAD; u++) mx = fmaxf(mx, mr[u]);
     mx = sp_wave_max(mx);
     if (lane == 0) red[wv] = mx;
     __syncthreads();
     const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     float l = 0.0f;
-    for (int r = tid; r < n_runs; r += NT) {
-        const float w = __expf(ph[(long long)r * pp] - M);  // 0 for a run without positions (m = -inf)
-        e[r] = w;
-        l = fmaf(ph[(long long)r * pp + 1], w, l);
+#pragma unroll
+    for (int u = 0; u < MERGE_RUNS_PER_THREAD; u++) {
+        const int r = tid + u * NT;
+        const float w = __expf(mr[u] - M);  // 0 for a run without positions (m = -inf)
+        if (r < n_runs) e[r] = w;
+        l = fmaf(lr[u], w, l);
     }
     l = wave_sum(l);
     if (lane == 0) red[NT / SP_WAVE + wv] = l;
@@ -746,22 +767,35 @@ k_hier_attn_merge(const SpPlan P, const SpHierAttnArgs A, const float *__restric
     const float inv_l = sp_div(1.0f, (red[4] + red[5]) + (red[6] + red[7]));
     for (int k = tid; k < A.pad; k += NT) c[k] = 0.0f;
     __syncthreads();
-    for (int j = tid; j < ns + nt; j += NT) {
-        // 48 runs' values in flight per batch (the last batch re-reads run 0 with weight 0)
-        float s = 0.0f;
+    // coefficients j0 = tid and j1 = tid + NT together, 48 runs of each in flight
+    for (int j0 = tid; j0 < ns + nt; j0 += 2 * NT) {
+        const int j1 = j0 + NT;
+        float s0 = 0.0f, s1 = 0.0f;
         for (int r0 = 0; r0 < n_runs; r0 += 48) {
-            float v[48];
+            float v0[48], v1[48];
 #pragma unroll
-            for (int k = 0; k < 48; k++) v[k] = ph[(long long)(r0 + k < n_runs ? r0 + k : 0) * pp + 4 + j];
+            for (int k = 0; k < 48; k++) {
+                v0[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, (4 + j0) * 4, (r0 + k) * pp * 4, 0));
+                v1[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, (4 + j1) * 4, (r0 + k) * pp * 4, 0));
+            }
 #pragma unroll
-            for (int k = 0; k < 48; k++) s = fmaf(v[k], r0 + k < n_runs ? e[r0 + k] : 0.0f, s);
+            for (int k = 0; k < 48; k++) {
+                const float w = r0 + k < n_runs ? e[r0 + k] : 0.0f;
+                s0 = fmaf(v0[k], w, s0);
+                s1 = fmaf(v1[k], w, s1);  // (j1 past the coefficients: discarded below)
+            }
         }
-        s *= inv_l;
-        if (j < ns) {
-            cs[j] = s;
-            c[A.skel_idx[j]] = s;
-        } else {
-            c[A.tgt_idx[j - ns]] = s;  // the dev part; W c_skel is added below
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int j = q == 0 ? j0 : j1;
+            if (j >= ns + nt) continue;
+            const float sj = (q == 0 ? s0 : s1) * inv_l;
+            if (j < ns) {
+                cs[j] = sj;
+                c[A.skel_idx[j]] = sj;
+            } else {
+                c[A.tgt_idx[j - ns]] = sj;  // the dev part; W c_skel is added below
+            }
         }
     }
     if (w_reg) wst.store(Ws, nt * ns, tid);
@@ -773,7 +807,7 @@ k_hier_attn_merge(const SpPlan P, const SpHierAttnArgs A, const float *__restric
         c[A.tgt_idx[t]] += pred;
     }
     __syncthreads();
-    transform_block(c, A.pad, P, cas_s, tid);
+    transform_block(c, tsm, A.pad, P, cas_s, tid);
     for (int k = tid; k < A.hd; k += NT) A.out[(long long)h * A.hd + k] = c[k];
 }
 
@@ -800,7 +834,7 @@ size_t sp_hier_attn_workspace_floats(const SpHierAttnArgs &A, int n_runs) {
 int sp_hier_attn_runs(const SpHierAttnArgs &A, int cus) {
     const int n_chunks = (A.n_kv + CH - 1) / CH;
     const int per_head = std::max(1, (3 * cus) / std::max(1, A.n_kvh));
-    return std::max(1, std::min(n_chunks, per_head));
+    return std::max(1, std::min(std::min(n_chunks, per_head), MERGE_RUNS_PER_THREAD * NT));
 }
 
 hipError_t sp_launch_hier_attn(const SpPlan &P, const SpHierAttnArgs &A, float *ws, size_t ws_floats, int n_runs,
@@ -809,7 +843,8 @@ hipError_t sp_launch_hier_attn(const SpPlan &P, const SpHierAttnArgs &A, float *
         A.pad > SP_GEN_MAX_N || A.n_skel + A.n_target > SP_GEN_MAX_N || A.hd > A.pad || n_runs <= 0 ||
         A.ps != sp_hier_attn_prep_floats(A.n_skel, A.n_target) || A.pp < 4 + A.n_skel + A.n_target)
         return hipErrorInvalidValue;
-    if (sp_hier_attn_workspace_floats(A, n_runs) > ws_floats) return hipErrorInvalidValue;
+    if (sp_hier_attn_workspace_floats(A, n_runs) > ws_floats || n_runs > MERGE_RUNS_PER_THREAD * NT)
+        return hipErrorInvalidValue;
     const int G = A.n_q / A.n_kvh;
     const int rb = window_bits(A);
     const size_t lds_prep = 4 * (size_t)(r4(A.pad) + r32(A.n_target) + 8 * r4(A.n_skel)) +
