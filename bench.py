@@ -561,23 +561,27 @@ def main():
             S.check(L.sp_hip_write_all(cc.ref, 0, POS, P(k), P(v), S.DTYPE_F16), "write_all")
         q = torch.randn((LAYERS, NQ, HD), dtype=torch.float32, device="cuda")
         out = torch.empty((LAYERS, NQ, HD), dtype=torch.float32, device="cuda")
-        sc = torch.empty((NQ, POS), dtype=torch.float32, device="cuda")
         scale = C.c_float(1.0 / math.sqrt(HD))
 
         def fused():
             S.check(L.sp_hip_attn_decode_all_layers(cc.ref, POS, P(q), NQ, scale, P(out), sptr), "attn")
 
-        def fused_kq():
-            for layer in range(LAYERS):
-                S.check(L.sp_hip_attn_decode(cc.ref, layer, POS, P(q[layer]), NQ, scale, P(sc), None, sptr), "kq")
+        # scores of every layer, [layer][query head][position]; like the full path, the
+        # per-layer launches come from the library's C loop (a Python loop costs ~5 us per
+        # call, most of a scores-only layer)
+        sc_all = torch.empty((LAYERS, NQ, POS), dtype=torch.float32, device="cuda")
+
+        def fused_kq(mb=-1):
+            S.check(L.sp_hip_attn_scores_all_layers(cc.ref, POS, P(q), NQ, scale, P(sc_all), mb, sptr), "kq")
 
         def fused_bands(want_out, mb=2):
             # band-limited decode (K bands >= mb read as 0; the single V band stays)
             def f():
+                if not want_out:
+                    return fused_kq(mb)
                 for layer in range(LAYERS):
-                    S.check(L.sp_hip_attn_decode_bands(cc.ref, layer, POS, P(q[layer]), NQ, scale,
-                                                       None if want_out else P(sc),
-                                                       P(out[layer]) if want_out else None, mb, sptr), "bands")
+                    S.check(L.sp_hip_attn_decode_bands(cc.ref, layer, POS, P(q[layer]), NQ, scale, None,
+                                                       P(out[layer]), mb, sptr), "bands")
             return f
 
         def fp16():
@@ -613,9 +617,10 @@ def main():
                 p = torch.softmax(s, dim=1).transpose(1, 2).contiguous().half()
                 torch.bmm(p, vl[layer])
 
-        us_fused, us_kq, us_f16 = timeit(fused), timeit(fused_kq), timeit(fp16)
-        us_tkq, us_tattn = timeit(torch_kq), timeit(torch_attn)
+        # the compressed-cache variants first, back to back, then the fp16 baselines
+        us_fused, us_kq = timeit(fused), timeit(fused_kq)
         us_kq_b2, us_attn_b2 = timeit(fused_bands(False)), timeit(fused_bands(True))
+        us_f16, us_tkq, us_tattn = timeit(fp16), timeit(torch_kq), timeit(torch_attn)
         kv_bytes = LAYERS * KVH * POS * (kB + vB)
         result.update({
             "fused_dqkq_us_per_tok": round(us_fused, 1),

@@ -214,6 +214,13 @@ void sp_hip_print_memory(const sp_hip_cache_t *cc);
 int sp_hip_attn_decode_all_layers(const sp_hip_cache_t *cc, int n_kv, const float *d_q,
                                   int n_q, float kq_scale, float *d_out, void *stream);
 
+/* The scores-only form of the same loop, band-limited as sp_hip_attn_decode_bands
+ * (max_bands -1: every band): q [n_layers][n_q][hd], scores [n_layers][n_q][n_kv]
+ * (benchmark helper; per-layer semantics above). */
+int sp_hip_attn_scores_all_layers(const sp_hip_cache_t *cc, int n_kv, const float *d_q,
+                                  int n_q, float kq_scale, float *d_scores, int max_bands,
+                                  void *stream);
+
 /* fp16 reference attention over an uncompressed cache, same layout contract
  * as the compressed one ([slot][pos][head_dim] fp16): the baseline the fused
  * kernel is compared against. */

@@ -339,7 +339,10 @@ __device__ __forceinline__ void stage_tile(unsigned char *wl, const TileRegs &r,
 // part[(query head) * n_parts + blockIdx.y] as [m, l, o~[128]]. NH = 1 serves
 // up to 4 query heads per KV head, NH = 2 up to 8 (a second set of columns).
 // MULTI = false: one tile per wave (tpw = 1), so no running state is carried.
-template <bool WANT_OUT, bool ALL_BANDS, int NH, bool MULTI>
+// Band limits: K bands b >= kbands and the V band when vbands == 0 take a zero
+// scale (a finite sum times 0 adds exactly nothing, so the scores and outputs
+// equal those with the bands read as 0, at the cost of the all-band loop).
+template <bool WANT_OUT, int NH, bool MULTI>
 __global__ void __launch_bounds__(NT, 1)
 k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict__ part, int n_parts, int tpw,
             int kbands, int vbands, int *__restrict__ counters) {
@@ -497,7 +500,7 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
         float sv_own = 0.0f;
         if (WANT_OUT)
             // (a lane past the tile's end takes whatever scale lies there: its weight is p = 0)
-            sv_own = (ALL_BANDS || vbands > 0)
+            sv_own = vbands > 0
                          ? scale_of(*reinterpret_cast<const unsigned short *>(wl + R_V + vshift + ln * VB))
                          : 0.0f;
         __asm__ volatile("" ::: "memory");  // every lane has read its record before the K area is reused
@@ -522,7 +525,6 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
             half4_t a[4];
 #pragma unroll
             for (int b = 0; b < 4; b++) {
-                if (!ALL_BANDS && b >= kbands) break;  // bands past the limit read as 0 (kernel-uniform)
                 a[b] = score_codes(r, b, s, kmask5, kbias5, kmask4, kbias4, kmask3, kbias3, kmask5p, kmask3p);
             }
 #pragma unroll
@@ -531,7 +533,6 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
                 for (int part = 0; part < 2; part++)
 #pragma unroll
                     for (int b = 0; b < 4; b++) {
-                        if (!ALL_BANDS && b >= kbands) break;
                         const half4_t qv = __builtin_bit_cast(
                             half4_t, *reinterpret_cast<const u32x2 *>(qs + (part * 8 + 4 * st + hj) * QS_STRIDE + 32 * b + 4 * s));
                         acc[st][b] = __builtin_amdgcn_mfma_f32_4x4x4f16(a[b], qv, acc[st][b], 0, 0, 0);
@@ -542,7 +543,7 @@ k_attn_wave(const SpAttnArgs A, const int *__restrict__ order, float *__restrict
         float ks[4];
 #pragma unroll
         for (int b = 0; b < 4; b++)
-            ks[b] = (ALL_BANDS || b < kbands) ? scale_of(rec_bits(r, 8 * kbyte(b), 16)) : 0.0f;
+            ks[b] = b < kbands ? scale_of(rec_bits(r, 8 * kbyte(b), 16)) : 0.0f;
         float sc[NH][4];
 #pragma unroll
         for (int st = 0; st < NH; st++) {
@@ -832,16 +833,11 @@ static int wave_device_cus() {
 }
 
 template <int NH, bool MULTI>
-static void launch_wave(const SpAttnArgs &A, const int *order, float *part, int nb, int tpw, bool all, int kb_lim,
-                        int vb_lim, int *cnt, hipStream_t s) {
+static void launch_wave(const SpAttnArgs &A, const int *order, float *part, int nb, int tpw, int kb_lim, int vb_lim,
+                        int *cnt, hipStream_t s) {
     const dim3 grid(A.n_kvh, nb);
-    if (A.out) {
-        if (all) hipLaunchKernelGGL((k_attn_wave<true, true, NH, MULTI>), grid, dim3(NT), 0, s, A, order, part, nb, tpw, kb_lim, vb_lim, cnt);
-        else hipLaunchKernelGGL((k_attn_wave<true, false, NH, MULTI>), grid, dim3(NT), 0, s, A, order, part, nb, tpw, kb_lim, vb_lim, cnt);
-    } else {
-        if (all) hipLaunchKernelGGL((k_attn_wave<false, true, NH, MULTI>), grid, dim3(NT), 0, s, A, order, part, nb, tpw, kb_lim, vb_lim, cnt);
-        else hipLaunchKernelGGL((k_attn_wave<false, false, NH, MULTI>), grid, dim3(NT), 0, s, A, order, part, nb, tpw, kb_lim, vb_lim, cnt);
-    }
+    if (A.out) hipLaunchKernelGGL((k_attn_wave<true, NH, MULTI>), grid, dim3(NT), 0, s, A, order, part, nb, tpw, kb_lim, vb_lim, cnt);
+    else hipLaunchKernelGGL((k_attn_wave<false, NH, MULTI>), grid, dim3(NT), 0, s, A, order, part, nb, tpw, kb_lim, vb_lim, cnt);
 }
 
 hipError_t sp_launch_attn_wave(const SpPlan &KP, const SpPlan &VP, const int *order, const SpAttnArgs &A, float *part,
@@ -866,15 +862,13 @@ hipError_t sp_launch_attn_wave(const SpPlan &KP, const SpPlan &VP, const int *or
     tpw = (int)std::max<long long>(tpw, (n_tiles + (long long)NW * MAX_PARTS - 1) / ((long long)NW * MAX_PARTS));
     const int nb = (int)((n_tiles + (long long)NW * tpw - 1) / ((long long)NW * tpw));
     if (!part || !counters || (size_t)A.n_q * nb * (HD + 2) > part_floats) return hipErrorInvalidValue;
-    // every band: a branch-free score loop (the band-limited one schedules worse)
-    const bool all = KP.max_bands >= 4 && VP.max_bands >= 1;
     const bool multi = tpw > 1;
     if (A.n_q / A.n_kvh <= 4) {
-        if (multi) launch_wave<1, true>(A, order, part, nb, tpw, all, KP.max_bands, VP.max_bands, counters, s);
-        else launch_wave<1, false>(A, order, part, nb, tpw, all, KP.max_bands, VP.max_bands, counters, s);
+        if (multi) launch_wave<1, true>(A, order, part, nb, tpw, KP.max_bands, VP.max_bands, counters, s);
+        else launch_wave<1, false>(A, order, part, nb, tpw, KP.max_bands, VP.max_bands, counters, s);
     } else {
-        if (multi) launch_wave<2, true>(A, order, part, nb, tpw, all, KP.max_bands, VP.max_bands, counters, s);
-        else launch_wave<2, false>(A, order, part, nb, tpw, all, KP.max_bands, VP.max_bands, counters, s);
+        if (multi) launch_wave<2, true>(A, order, part, nb, tpw, KP.max_bands, VP.max_bands, counters, s);
+        else launch_wave<2, false>(A, order, part, nb, tpw, KP.max_bands, VP.max_bands, counters, s);
     }
     return hipGetLastError();
 }

@@ -890,6 +890,16 @@ extern "C" int sp_hip_attn_decode_all_layers(const sp_hip_cache_t *cc, int n_kv,
     return 0;
 }
 
+extern "C" int sp_hip_attn_scores_all_layers(const sp_hip_cache_t *cc, int n_kv, const float *d_q, int n_q,
+                                             float kq_scale, float *d_scores, int max_bands, void *stream) {
+    if (!cc || !d_scores) return -1;
+    const int hd = cc->config.head_dim;
+    for (int l = 0; l < cc->config.n_layers; l++)
+        if (sp_hip_attn_decode_bands(cc, l, n_kv, d_q + (size_t)l * n_q * hd, n_q, kq_scale,
+                                     d_scores + (size_t)l * n_q * n_kv, nullptr, max_bands, stream)) return -1;
+    return 0;
+}
+
 static std::mutex g_f16ws_mu;
 static float *g_f16ws = nullptr;
 static size_t g_f16ws_n = 0;

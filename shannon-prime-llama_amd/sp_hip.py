@@ -229,6 +229,7 @@ def lib():
         L.sp_hip_dual_write_layer.argtypes = [vp, i, i, i, vp, vp, ll, i]
         L.sp_hip_dual_read_merged.argtypes = [vp, i, i, vp, vp, ll, i]
         L.sp_hip_attn_decode_all_layers.argtypes = [vp, i, vp, i, f, vp, vp]
+        L.sp_hip_attn_scores_all_layers.argtypes = [vp, i, vp, i, f, vp, i, vp]
         L.sp_hip_attn_decode_f16.argtypes = [vp, vp, i, i, i, i, i, vp, i, f, vp, vp, vp]
         L.sp_hip_sqfree_write_batch.argtypes = [vp, i, i, i, i, i, vp, i]
         L.sp_hip_sqfree_read_batch.argtypes = [vp, i, i, i, i, i, vp, i]

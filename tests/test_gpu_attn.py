@@ -227,6 +227,40 @@ def test_long_context_attention_matches_oracle(n_q, H, n_ctx, path, monkeypatch)
     cc.free()
 
 
+def test_all_layer_loops_equal_per_layer_calls():
+    """sp_hip_attn_decode_all_layers and sp_hip_attn_scores_all_layers (all bands and
+    two K bands) return, bit for bit, what the per-layer calls return."""
+    L, H, n_q, n_ctx, hd = 3, 2, 8, 700, 128
+    say(f"all-layer loops L={L} H={H} n_q={n_q} n_ctx={n_ctx}")
+    cc = S.ShipCache(S.config(hd, L, H), n_ctx, stream=torch.cuda.current_stream().cuda_stream)
+    lib = S.lib()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+    k = torch.randn((L * H, n_ctx, hd), generator=g, device="cuda").half()
+    v = torch.randn((L * H, n_ctx, hd), generator=g, device="cuda").half()
+    S.check(lib.sp_hip_write_all(cc.ref, 0, n_ctx, C.c_void_p(k.data_ptr()), C.c_void_p(v.data_ptr()), S.DTYPE_F16),
+            "write_all")
+    q = torch.randn((L, n_q, hd), generator=g, device="cuda")
+    scale = C.c_float(1.0 / math.sqrt(hd))
+    qp = C.c_void_p(q.data_ptr())
+    out_all = torch.empty((L, n_q, hd), device="cuda")
+    S.check(lib.sp_hip_attn_decode_all_layers(cc.ref, n_ctx, qp, n_q, scale, C.c_void_p(out_all.data_ptr()), stream()))
+    for mb in (-1, 2):
+        sc_all = torch.empty((L, n_q, n_ctx), device="cuda")
+        S.check(lib.sp_hip_attn_scores_all_layers(cc.ref, n_ctx, qp, n_q, scale, C.c_void_p(sc_all.data_ptr()), mb,
+                                                  stream()))
+        for layer in range(L):
+            sc1, out1 = torch.empty((n_q, n_ctx), device="cuda"), torch.empty((n_q, hd), device="cuda")
+            S.check(lib.sp_hip_attn_decode_bands(cc.ref, layer, n_ctx, C.c_void_p(q[layer].data_ptr()), n_q, scale,
+                                                 C.c_void_p(sc1.data_ptr()), C.c_void_p(out1.data_ptr()), mb,
+                                                 stream()))
+            torch.cuda.synchronize()
+            assert torch.equal(sc_all[layer], sc1), (mb, layer)
+            if mb == -1:
+                assert torch.equal(out_all[layer], out1), layer
+    cc.free()
+
+
 def test_attention_rejects_bad_shapes():
     cfg = S.config(128, 1, 2)
     cc = S.ShipCache(cfg, 64)
