@@ -91,6 +91,7 @@ struct RegStage {
     }
 };
 constexpr int W_STAGE = 40;  // W elements per thread staged through registers (n_target * n_skel <= 10240)
+constexpr int W_DW = 20;     // W dwords (fp16 pairs) per prep thread staged through registers
 constexpr int MERGE_RUNS_PER_THREAD = 4;  // runs per merge thread (n_runs <= 4 * NT)
 
 // 4 little-endian bytes at LDS byte offset o (any alignment) of a dword-aligned array.
@@ -243,18 +244,42 @@ k_hier_attn_prep(const SpPlan P, const SpHierAttnArgs A, float *__restrict__ pre
     float *part = qt + nt32;
     unsigned short *Ws = reinterpret_cast<unsigned short *>(part + 8 * ns4);
     const unsigned short *Wk = reinterpret_cast<const unsigned short *>(A.W) + (long long)kvh * A.w_outer;
-    // W and the target indices load while the query is transformed
-    const bool w_reg = nt * ns <= W_STAGE * NT;
-    RegStage<unsigned short, W_STAGE> wst;
-    if (w_reg) wst.load(Wk, nt * ns, tid);
-    else copy_to_lds<unsigned short, 16>(Ws, Wk, nt * ns, nt * ns, tid);
-    int ti[(SP_GEN_MAX_N + NT - 1) / NT];
+    // the query row, the target indices and W (as dwords of two fp16) all load at once
+    // through range-checked buffer loads (unconditional: reads past a range return 0),
+    // W reaching LDS while the query is transformed
+    constexpr int PU = (SP_GEN_MAX_N + NT - 1) / NT;
+    const int nw = nt * ns, nwd = nw >> 1;  // W dwords (an odd count's last half loads alone)
+    const bool w_reg = nwd <= W_DW * NT && ((uintptr_t)Wk & 3) == 0;
+    const __amdgpu_buffer_rsrc_t rq =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(A.q + (long long)h * A.hd), (short)0, A.hd * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rt = __builtin_amdgcn_make_buffer_rsrc((void *)A.tgt_idx, (short)0, nt * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)Wk, (short)0, nwd * 4, 0x00020000);
+    float qv[PU];
+    int ti[PU];
 #pragma unroll
-    for (int u = 0; u < (SP_GEN_MAX_N + NT - 1) / NT; u++) ti[u] = tid + u * NT < nt ? A.tgt_idx[tid + u * NT] : 0;
-    for (int k = tid; k < A.pad; k += NT) c[k] = k < A.hd ? A.q[(long long)h * A.hd + k] : 0.0f;
+    for (int u = 0; u < PU; u++) {
+        qv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rq, 4 * (tid + u * NT), 0, 0));
+        ti[u] = (int)__builtin_amdgcn_raw_buffer_load_b32(rt, 4 * (tid + u * NT), 0, 0);
+    }
+    uint32_t wd[W_DW];
+    if (w_reg) {
+#pragma unroll
+        for (int u = 0; u < W_DW; u++) wd[u] = __builtin_amdgcn_raw_buffer_load_b32(rw, 4 * (tid + u * NT), 0, 0);
+    } else {
+        copy_to_lds<unsigned short, 16>(Ws, Wk, nw, nw, tid);
+    }
+#pragma unroll
+    for (int u = 0; u < PU; u++)
+        if (tid + u * NT < A.pad) c[tid + u * NT] = qv[u];  // zero past hd (out of range)
     __syncthreads();
     transform_block(c, tsm, A.pad, P, cas_s, tid);
-    if (w_reg) wst.store(Ws, nt * ns, tid);
+    if (w_reg) {
+        uint32_t *Ws32 = reinterpret_cast<uint32_t *>(Ws);
+#pragma unroll
+        for (int u = 0; u < W_DW; u++)
+            if (tid + u * NT < nwd) Ws32[tid + u * NT] = wd[u];
+        if ((nw & 1) && tid == 0) Ws[nw - 1] = Wk[nw - 1];
+    }
 #pragma unroll
     for (int u = 0; u < (SP_GEN_MAX_N + NT - 1) / NT; u++) {
         const int t = tid + u * NT;
