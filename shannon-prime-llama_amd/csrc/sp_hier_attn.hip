@@ -90,6 +90,7 @@ struct RegStage {
         }
     }
 };
+constexpr int K_STAGE = 26;  // K record dwords per thread staged through registers (256 x 103 B chunks)
 constexpr int W_STAGE = 40;  // W elements per thread staged through registers (n_target * n_skel <= 10240)
 constexpr int W_DW = 20;     // W dwords (fp16 pairs) per prep thread staged through registers
 constexpr int MERGE_RUNS_PER_THREAD = 4;  // runs per merge thread (n_runs <= 4 * NT)
@@ -329,7 +330,9 @@ k_hier_attn_prep(const SpPlan P, const SpHierAttnArgs A, float *__restrict__ pre
 //   red   8 * MAX_G floats  block reductions
 // (RB > 0: at the end of the run the same memory holds the position groups' sums.)
 // Partial per (query head, run): [m, l, -, -, c_skel sum (n_skel), dev sum (n_target)].
-template <int RB, int GM>
+// OUT = false: scores only (no V half), with the next chunk's K records prefetched
+// into registers while the current chunk's scores run.
+template <int RB, int GM, bool OUT>
 __global__ void __launch_bounds__(NT, 3)
 k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A, const float *__restrict__ prep, float *__restrict__ part,
                   int n_runs) {
@@ -338,7 +341,7 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A, const float *__restric
     const int G = A.n_q / A.n_kvh, h0 = kvh * G;
     const int ns = A.n_skel, nt = A.n_target, B = A.B, nb = P.n_bands;
     const int qo = prep_qt_off(ns), so = prep_sum_off(ns, nt);
-    const bool want_out = A.out != nullptr;
+    constexpr bool want_out = OUT;
     const int rec_bytes = ((CH * B + 32) + 15) & ~15;
     unsigned char *rec = dsm;
     uint32_t *rec32 = reinterpret_cast<uint32_t *>(dsm);
@@ -439,15 +442,39 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A, const float *__restric
     const float s_off = (float)((1 << (s_bits - 1)) - 1);
 
     const int n_chunks = (A.n_kv + CH - 1) / CH;
+    // scores only: chunk ch's K records wait in registers (kst) from the previous chunk on
+    const bool k_pre = !OUT && (CH * B + 6) / 4 <= K_STAGE * NT;
+    RegStage<uint32_t, K_STAGE> kst;
+    auto k_src = [&](int chn, int &shift_, int &ndw_) {
+        const int c0_ = chn * CH, n_t_ = min(CH, A.n_kv - c0_);
+        const unsigned char *kg_ = A.kcache + (long long)kvh * A.slot_bytes + (long long)c0_ * B;
+        shift_ = (int)((uintptr_t)kg_ & 3);
+        ndw_ = (n_t_ * B + shift_ + 3) >> 2;
+        return reinterpret_cast<const uint32_t *>(kg_ - shift_);
+    };
+    if (k_pre && run < n_chunks) {
+        int sh_, nd_;
+        const uint32_t *src_ = k_src(run, sh_, nd_);
+        kst.load(src_, nd_, tid);
+    }
     for (int ch = run; ch < n_chunks; ch += n_runs) {
         const int c0 = ch * CH;
         const int n_t = min(CH, A.n_kv - c0);
         // ---- K records of the chunk into LDS (aligned dwords; records from byte `shift`) ----
-        const unsigned char *kg = A.kcache + (long long)kvh * A.slot_bytes + (long long)c0 * B;
-        const int shift = (int)((uintptr_t)kg & 3);
-        const int ndw = (n_t * B + shift + 3) >> 2;
+        int shift, ndw;
+        const uint32_t *ksrc = k_src(ch, shift, ndw);
         __syncthreads();  // the previous chunk is done with rec / sc
-        copy_to_lds<uint32_t, 32>(rec32, reinterpret_cast<const uint32_t *>(kg - shift), ndw, ndw + 3, tid);
+        if (k_pre) {
+            kst.store(rec32, ndw, tid);
+            if (tid < 3) rec32[ndw + tid] = 0u;  // the bit readers' look-ahead
+            if (ch + n_runs < n_chunks) {
+                int sh_, nd_;
+                const uint32_t *src_ = k_src(ch + n_runs, sh_, nd_);
+                kst.load(src_, nd_, tid);
+            }
+        } else {
+            copy_to_lds<uint32_t, 32>(rec32, ksrc, ndw, ndw + 3, tid);
+        }
         __syncthreads();
         if (KM) {
             // ---- target dots of this wave's 64 positions on the matrix cores -> sc ----
@@ -846,6 +873,23 @@ int window_bits(const SpHierAttnArgs &A) {
     return rb;
 }
 
+// The split kernel's instance for this call's level width and output mode.
+template <bool OUT>
+void launch_split(const SpPlan &P, const SpHierAttnArgs &A, const float *prep, float *part, int n_runs, int rb, int G,
+                  size_t lds_split, hipStream_t s) {
+    const dim3 grid(A.n_kvh, n_runs);
+    if (rb == 2 && G <= 2)
+        hipLaunchKernelGGL((k_hier_attn_split<2, 2, OUT>), grid, dim3(NT), lds_split, s, P, A, prep, part, n_runs);
+    else if (rb == 2)
+        hipLaunchKernelGGL((k_hier_attn_split<2, MAX_G, OUT>), grid, dim3(NT), lds_split, s, P, A, prep, part, n_runs);
+    else if (rb == 4)
+        hipLaunchKernelGGL((k_hier_attn_split<4, MAX_G, OUT>), grid, dim3(NT), lds_split, s, P, A, prep, part, n_runs);
+    else if (rb == 8)
+        hipLaunchKernelGGL((k_hier_attn_split<8, MAX_G, OUT>), grid, dim3(NT), lds_split, s, P, A, prep, part, n_runs);
+    else
+        hipLaunchKernelGGL((k_hier_attn_split<0, MAX_G, OUT>), grid, dim3(NT), lds_split, s, P, A, prep, part, n_runs);
+}
+
 }  // namespace
 
 int sp_hier_attn_prep_floats(int n_skel, int n_target) { return prep_sum_off(n_skel, n_target) + 4; }
@@ -888,17 +932,8 @@ hipError_t sp_launch_hier_attn(const SpPlan &P, const SpHierAttnArgs &A, float *
     float *prep = ws;
     float *part = ws + (size_t)A.n_q * A.ps;
     hipLaunchKernelGGL(k_hier_attn_prep, dim3(A.n_q), dim3(NT), lds_prep, s, P, A, prep);
-    const dim3 grid(A.n_kvh, n_runs);
-    if (rb == 2 && G <= 2)
-        hipLaunchKernelGGL((k_hier_attn_split<2, 2>), grid, dim3(NT), lds_split, s, P, A, prep, part, n_runs);
-    else if (rb == 2)
-        hipLaunchKernelGGL((k_hier_attn_split<2, MAX_G>), grid, dim3(NT), lds_split, s, P, A, prep, part, n_runs);
-    else if (rb == 4)
-        hipLaunchKernelGGL((k_hier_attn_split<4, MAX_G>), grid, dim3(NT), lds_split, s, P, A, prep, part, n_runs);
-    else if (rb == 8)
-        hipLaunchKernelGGL((k_hier_attn_split<8, MAX_G>), grid, dim3(NT), lds_split, s, P, A, prep, part, n_runs);
-    else
-        hipLaunchKernelGGL((k_hier_attn_split<0, MAX_G>), grid, dim3(NT), lds_split, s, P, A, prep, part, n_runs);
+    if (A.out) launch_split<true>(P, A, prep, part, n_runs, rb, G, lds_split, s);
+    else launch_split<false>(P, A, prep, part, n_runs, rb, G, lds_split, s);
     if (A.out) hipLaunchKernelGGL(k_hier_attn_merge, dim3(A.n_q), dim3(NT), lds_merge, s, P, A, part, n_runs);
     return hipGetLastError();
 }
