@@ -197,9 +197,11 @@ int sp_hip_attn_decode_bands(const sp_hip_cache_t *cc, int layer, int n_kv,
  * sp_hip_attn_noalloc_max_floats() floats (16 MiB, held until the process
  * ends) instead of the cache's workspace, and the call makes no hipMalloc /
  * hipFree. Returns -1 when the call needs more than that
- * (n_q*head_dim + n_q*ceil(n_kv/256)*(head_dim + 2) floats: at head_dim 128 and
- * 32 query heads up to 128K positions) or when `stream` is not on the current
- * device. Calls that overlap on one GPU share the array and race. */
+ * (n_q*head_dim + n_q*ceil(n_kv/256)*(head_dim + 2) floats plus 16448 floats of
+ * arrival counters: at head_dim 128 up to 256768 positions with 32 query heads and
+ * 128256 with 64) or when `stream` is not on the current device. The counters
+ * must start at zero: the array starts zeroed and every completed call leaves
+ * them at zero. Calls that overlap on one GPU share the array and race. */
 int sp_hip_attn_decode_bands_noalloc(const sp_hip_cache_t *cc, int layer, int n_kv,
                                      const float *d_q, int n_q, float kq_scale,
                                      float *d_scores, float *d_out, int max_bands, void *stream);

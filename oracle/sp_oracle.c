@@ -365,8 +365,9 @@ void spo_ship_decompress(const uint8_t *in, float *out, const spo_band_config_t 
 
 void spo_ship_compress_batch_f16(const uint16_t *in, uint8_t *out, int n, int hd,
                                  const spo_band_config_t *bc, const int *order, int norm_mode) {
-    float v[1024];
+#pragma omp parallel for schedule(static)
     for (int t = 0; t < n; t++) {
+        float v[1024];
         for (int i = 0; i < hd; i++) v[i] = spo_f16_to_f32(in[(size_t)t * hd + i]);
         spo_ship_compress(v, out + (size_t)t * bc->total_bytes, bc, order, norm_mode);
     }
@@ -382,6 +383,7 @@ void spo_ship_compress_batch_f32(const float *in, uint8_t *out, int n, int hd,
 void spo_ship_decompress_batch_f32(const uint8_t *in, float *out, int n, int hd,
                                    const spo_band_config_t *bc, const int *order,
                                    int norm_mode, int max_bands) {
+#pragma omp parallel for schedule(static)
     for (int t = 0; t < n; t++)
         spo_ship_decompress(in + (size_t)t * bc->total_bytes, out + (size_t)t * hd, bc, order,
                             norm_mode, max_bands);
@@ -390,8 +392,9 @@ void spo_ship_decompress_batch_f32(const uint8_t *in, float *out, int n, int hd,
 void spo_ship_decompress_batch_f16(const uint8_t *in, uint16_t *out, int n, int hd,
                                    const spo_band_config_t *bc, const int *order,
                                    int norm_mode, int max_bands) {
-    float v[1024];
+#pragma omp parallel for schedule(static)
     for (int t = 0; t < n; t++) {
+        float v[1024];
         spo_ship_decompress(in + (size_t)t * bc->total_bytes, v, bc, order, norm_mode, max_bands);
         for (int i = 0; i < hd; i++) out[(size_t)t * hd + i] = spo_f32_to_f16(v[i]);
     }
@@ -688,8 +691,9 @@ void spo_sqfree_compress_batch_f16(const uint16_t *in, uint8_t *out, int n, int 
                                    const spo_knight_mask_t *m, const spo_band_config_t *skel_bc,
                                    int rbits, int spinor) {
     int B = spo_sqfree_bytes(skel_bc, m->n_res, rbits, spinor);
-    float v[1024];
+#pragma omp parallel for schedule(static)
     for (int t = 0; t < n; t++) {
+        float v[1024];
         for (int i = 0; i < hd; i++) v[i] = spo_f16_to_f32(in[(size_t)t * hd + i]);
         spo_sqfree_compress(v, out + (size_t)t * B, hd, m, skel_bc, rbits, spinor);
     }
@@ -699,6 +703,7 @@ void spo_sqfree_decompress_batch_f32(const uint8_t *in, float *out, int n, int h
                                      const spo_knight_mask_t *m, const spo_band_config_t *skel_bc,
                                      int rbits, int spinor) {
     int B = spo_sqfree_bytes(skel_bc, m->n_res, rbits, spinor);
+#pragma omp parallel for schedule(static)
     for (int t = 0; t < n; t++)
         spo_sqfree_decompress(in + (size_t)t * B, out + (size_t)t * hd, hd, m, skel_bc, rbits,
                               spinor);
@@ -820,8 +825,9 @@ void spo_hier_compress_batch_f16(const uint16_t *in, uint8_t *out, int n, int hd
                                  const int *target_idx, const spo_band_config_t *skel_bc,
                                  const uint16_t *W, int rbits) {
     int B = spo_hier_bytes(skel_bc, n_target, rbits);
-    float v[1024];
+#pragma omp parallel for schedule(static)
     for (int t = 0; t < n; t++) {
+        float v[1024];
         for (int i = 0; i < hd; i++) v[i] = spo_f16_to_f32(in[(size_t)t * hd + i]);
         spo_hier_compress(v, out + (size_t)t * B, hd, pad, n_skel, skel_idx, n_target,
                           target_idx, skel_bc, W, rbits);
@@ -833,6 +839,7 @@ void spo_hier_decompress_batch_f32(const uint8_t *in, float *out, int n, int hd,
                                    const int *target_idx, const spo_band_config_t *skel_bc,
                                    const uint16_t *W, int rbits) {
     int B = spo_hier_bytes(skel_bc, n_target, rbits);
+#pragma omp parallel for schedule(static)
     for (int t = 0; t < n; t++)
         spo_hier_decompress(in + (size_t)t * B, out + (size_t)t * hd, hd, pad, n_skel, skel_idx,
                             n_target, target_idx, skel_bc, W, rbits);
@@ -842,57 +849,117 @@ void spo_hier_decompress_batch_f32(const uint8_t *in, float *out, int n, int hd,
 /* decode attention                                                         */
 /* ------------------------------------------------------------------------ */
 
+/* Decode attention over records, in double: every K~ / V~ row of a KV head is
+ * reconstructed by the codec's own read path (row(), the records' decompress),
+ * then, per query head h of the head's group (llama.cpp's GQA grouping
+ * h -> h / (n_q / n_kvh)), s_t = kq_scale * sum_d q[h][d] K~_t[d] accumulated
+ * over d in order, softmax with the maximum subtracted, and
+ * out[h] = sum_t p_t V~_t / sum_t p_t accumulated over t in order. The rows of
+ * a head are reconstructed in parallel (each row independently, so the result
+ * does not depend on the thread count); the sums are serial. */
+typedef void (*spo_row_fn)(const void *ctx, int is_v, int kvh, int t, float *row);
+
+static void attn_core(const float *q, int n_q, int n_kvh, int n_ctx, int hd, float kq_scale,
+                      spo_row_fn row, const void *ctx, float *scores, float *out) {
+    int grp = n_q / n_kvh;
+    size_t nr = (size_t)(n_ctx > 0 ? n_ctx : 1);
+    float *rows = (float *)malloc(sizeof(float) * nr * (size_t)hd);
+    double *s = (double *)malloc(sizeof(double) * nr * (size_t)grp);
+    double *o = (double *)malloc(sizeof(double) * (size_t)hd);
+    for (int kh = 0; kh < n_kvh; kh++) {
+#pragma omp parallel for schedule(static)
+        for (int t = 0; t < n_ctx; t++) row(ctx, 0, kh, t, rows + (size_t)t * hd);
+        for (int g = 0; g < grp; g++) {
+            int h = kh * grp + g;
+            double *sh = s + (size_t)g * nr;
+            for (int t = 0; t < n_ctx; t++) {
+                const float *kt = rows + (size_t)t * hd;
+                double acc = 0.0;
+                for (int d = 0; d < hd; d++) acc += (double)q[(size_t)h * hd + d] * (double)kt[d];
+                sh[t] = acc * (double)kq_scale;
+                if (scores) scores[(size_t)h * n_ctx + t] = (float)sh[t];
+            }
+        }
+        if (!out) continue;
+#pragma omp parallel for schedule(static)
+        for (int t = 0; t < n_ctx; t++) row(ctx, 1, kh, t, rows + (size_t)t * hd);
+        for (int g = 0; g < grp; g++) {
+            int h = kh * grp + g;
+            const double *sh = s + (size_t)g * nr;
+            double mx = -INFINITY;
+            for (int t = 0; t < n_ctx; t++)
+                if (sh[t] > mx) mx = sh[t];
+            double l = 0.0;
+            for (int d = 0; d < hd; d++) o[d] = 0.0;
+            for (int t = 0; t < n_ctx; t++) {
+                double p = exp(sh[t] - mx);
+                l += p;
+                const float *vt = rows + (size_t)t * hd;
+                for (int d = 0; d < hd; d++) o[d] += p * (double)vt[d];
+            }
+            for (int d = 0; d < hd; d++) out[(size_t)h * hd + d] = (float)(o[d] / l);
+        }
+    }
+    free(rows);
+    free(s);
+    free(o);
+}
+
+/* ship records: the read path with bands >= max_bands read as 0 */
+typedef struct {
+    const uint8_t *kpack, *vpack;
+    int n_ctx;
+    const spo_band_config_t *kbc, *vbc;
+    const int *order;
+    int norm_mode, max_bands;
+} ship_rows_t;
+
+static void ship_row(const void *ctx, int is_v, int kvh, int t, float *row) {
+    const ship_rows_t *c = (const ship_rows_t *)ctx;
+    const spo_band_config_t *bc = is_v ? c->vbc : c->kbc;
+    const uint8_t *pk = is_v ? c->vpack : c->kpack;
+    spo_ship_decompress(pk + ((size_t)kvh * c->n_ctx + t) * bc->total_bytes, row, bc, is_v ? NULL : c->order,
+                        c->norm_mode, c->max_bands);
+}
+
+/* hier records: spo_hier_decompress with the KV head's predictor W[kvh] */
+typedef struct {
+    const uint8_t *kpack, *vpack;
+    int n_ctx, hd, pad, n_skel, n_target, rbits, B;
+    const int *skel_idx, *target_idx;
+    const spo_band_config_t *skel_bc;
+    const uint16_t *W;
+} hier_rows_t;
+
+static void hier_row(const void *ctx, int is_v, int kvh, int t, float *row) {
+    const hier_rows_t *c = (const hier_rows_t *)ctx;
+    const uint8_t *pk = is_v ? c->vpack : c->kpack;
+    spo_hier_decompress(pk + ((size_t)kvh * c->n_ctx + t) * c->B, row, c->hd, c->pad, c->n_skel, c->skel_idx,
+                        c->n_target, c->target_idx, c->skel_bc, c->W + (size_t)kvh * c->n_target * c->n_skel,
+                        c->rbits);
+}
+
+/* sqfree records: spo_sqfree_decompress, K and V each with their skeleton bands */
+typedef struct {
+    const uint8_t *kpack, *vpack;
+    int n_ctx, hd, rbits, spinor;
+    const spo_knight_mask_t *m;
+    const spo_band_config_t *kbc, *vbc;
+} sqfree_rows_t;
+
+static void sqfree_row(const void *ctx, int is_v, int kvh, int t, float *row) {
+    const sqfree_rows_t *c = (const sqfree_rows_t *)ctx;
+    const spo_band_config_t *bc = is_v ? c->vbc : c->kbc;
+    const uint8_t *pk = is_v ? c->vpack : c->kpack;
+    int B = spo_sqfree_bytes(bc, c->m->n_res, c->rbits, c->spinor);
+    spo_sqfree_decompress(pk + ((size_t)kvh * c->n_ctx + t) * B, row, c->hd, c->m, bc, c->rbits, c->spinor);
+}
+
 /* Score semantics of llama_sp_kq_compute (src/engine/llama_sp_fused_kq.cpp:
  * 83-165): dst[qh][kv] = sum_d q[qh][d] * K~[kv][d], K~ decompressed from the
  * packed archive. This oracle decompresses with the full read path (including
  * the Mobius unreorder the reference op omits, :131-139), applies llama.cpp's
  * GQA grouping qh -> qh / (n_q / n_kvh) and kq_scale, then softmax and . V~. */
-/* The same scores / softmax / . V in double as spo_attn_decode_bands, over hier
- * records: a position's K~ and V~ are spo_hier_decompress of its records with
- * its KV head's predictor W[kh]. Not a reference op (the reference's fused op is
- * ship-only, llama_sp_fused_kq.cpp:14-34); it is the attention a caller gets by
- * reading the hier cache back and attending over it. */
-void spo_hier_attn_decode(const float *q, const uint8_t *kpack, const uint8_t *vpack,
-                          int n_q, int n_kvh, int n_ctx, int hd, int pad,
-                          int n_skel, const int *skel_idx, int n_target, const int *target_idx,
-                          const spo_band_config_t *skel_bc, const uint16_t *W, int rbits,
-                          float kq_scale, float *scores, float *out) {
-    int grp = n_q / n_kvh;
-    int B = spo_hier_bytes(skel_bc, n_target, rbits);
-    size_t wsz = (size_t)n_target * n_skel;
-    float *kt = (float *)malloc(sizeof(float) * (size_t)hd);
-    double *s = (double *)malloc(sizeof(double) * (size_t)(n_ctx > 0 ? n_ctx : 1));
-    double *o = (double *)malloc(sizeof(double) * (size_t)hd);
-    for (int h = 0; h < n_q; h++) {
-        int kh = h / grp;
-        const uint16_t *Wk = W + (size_t)kh * wsz;
-        double mx = -INFINITY;
-        for (int t = 0; t < n_ctx; t++) {
-            spo_hier_decompress(kpack + ((size_t)kh * n_ctx + t) * B, kt, hd, pad, n_skel, skel_idx,
-                                n_target, target_idx, skel_bc, Wk, rbits);
-            double acc = 0.0;
-            for (int d = 0; d < hd; d++) acc += (double)q[(size_t)h * hd + d] * (double)kt[d];
-            s[t] = acc * (double)kq_scale;
-            if (scores) scores[(size_t)h * n_ctx + t] = (float)s[t];
-            if (s[t] > mx) mx = s[t];
-        }
-        if (!out) continue;
-        double l = 0.0;
-        for (int d = 0; d < hd; d++) o[d] = 0.0;
-        for (int t = 0; t < n_ctx; t++) {
-            double p = exp(s[t] - mx);
-            l += p;
-            spo_hier_decompress(vpack + ((size_t)kh * n_ctx + t) * B, kt, hd, pad, n_skel, skel_idx,
-                                n_target, target_idx, skel_bc, Wk, rbits);
-            for (int d = 0; d < hd; d++) o[d] += p * (double)kt[d];
-        }
-        for (int d = 0; d < hd; d++) out[(size_t)h * hd + d] = (float)(o[d] / l);
-    }
-    free(kt);
-    free(s);
-    free(o);
-}
-
 void spo_attn_decode(const float *q, const uint8_t *kpack, const uint8_t *vpack,
                      int n_q, int n_kvh, int n_ctx, int hd,
                      const spo_band_config_t *kbc, const spo_band_config_t *vbc,
@@ -910,37 +977,38 @@ void spo_attn_decode_bands(const float *q, const uint8_t *kpack, const uint8_t *
                            const spo_band_config_t *kbc, const spo_band_config_t *vbc,
                            const int *order, int norm_mode, float kq_scale,
                            float *scores, float *out, int max_bands) {
-    int grp = n_q / n_kvh;
-    float *kt = (float *)malloc(sizeof(float) * (size_t)hd);
-    double *s = (double *)malloc(sizeof(double) * (size_t)n_ctx);
-    double *o = (double *)malloc(sizeof(double) * (size_t)hd);
-    for (int h = 0; h < n_q; h++) {
-        int kh = h / grp;
-        double mx = -INFINITY;
-        for (int t = 0; t < n_ctx; t++) {
-            spo_ship_decompress(kpack + ((size_t)kh * n_ctx + t) * kbc->total_bytes, kt, kbc,
-                                order, norm_mode, max_bands);
-            double acc = 0.0;
-            for (int d = 0; d < hd; d++) acc += (double)q[(size_t)h * hd + d] * (double)kt[d];
-            s[t] = acc * (double)kq_scale;
-            if (scores) scores[(size_t)h * n_ctx + t] = (float)s[t];
-            if (s[t] > mx) mx = s[t];
-        }
-        if (!out) continue;
-        double l = 0.0;
-        for (int d = 0; d < hd; d++) o[d] = 0.0;
-        for (int t = 0; t < n_ctx; t++) {
-            double p = exp(s[t] - mx);
-            l += p;
-            spo_ship_decompress(vpack + ((size_t)kh * n_ctx + t) * vbc->total_bytes, kt, vbc,
-                                NULL, norm_mode, max_bands);
-            for (int d = 0; d < hd; d++) o[d] += p * (double)kt[d];
-        }
-        for (int d = 0; d < hd; d++) out[(size_t)h * hd + d] = (float)(o[d] / l);
-    }
-    free(kt);
-    free(s);
-    free(o);
+    ship_rows_t c = {kpack, vpack, n_ctx, kbc, vbc, order, norm_mode, max_bands};
+    attn_core(q, n_q, n_kvh, n_ctx, hd, kq_scale, ship_row, &c, scores, out);
+}
+
+/* The same scores / softmax / . V in double over hier records: a position's K~
+ * and V~ are spo_hier_decompress of its records with its KV head's predictor
+ * W[kh]. Not a reference op (the reference's fused op is ship-only,
+ * llama_sp_fused_kq.cpp:14-34); it is the attention a caller gets by reading the
+ * hier cache back and attending over it. */
+void spo_hier_attn_decode(const float *q, const uint8_t *kpack, const uint8_t *vpack,
+                          int n_q, int n_kvh, int n_ctx, int hd, int pad,
+                          int n_skel, const int *skel_idx, int n_target, const int *target_idx,
+                          const spo_band_config_t *skel_bc, const uint16_t *W, int rbits,
+                          float kq_scale, float *scores, float *out) {
+    hier_rows_t c = {kpack, vpack, n_ctx, hd, pad, n_skel, n_target, rbits,
+                     spo_hier_bytes(skel_bc, n_target, rbits), skel_idx, target_idx, skel_bc, W};
+    attn_core(q, n_q, n_kvh, n_ctx, hd, kq_scale, hier_row, &c, scores, out);
+}
+
+/* The same attention over sqfree(+spinor) records: K~ and V~ are
+ * spo_sqfree_decompress of the records (the read path of sp_cuda_sqfree_read_one,
+ * shannon_prime_sqfree.cu:857-950, which the reference's hook calls per vector
+ * before its attention, llama-cpp-b8861-full-engine.patch:1205-1207), K with the
+ * K skeleton bands and V with the V bands, one Knight mask for both. Not a
+ * reference op (the reference's fused op is ship-only, llama_sp_fused_kq.cpp:
+ * 14-34). */
+void spo_sqfree_attn_decode(const float *q, const uint8_t *kpack, const uint8_t *vpack,
+                            int n_q, int n_kvh, int n_ctx, int hd, const spo_knight_mask_t *m,
+                            const spo_band_config_t *kbc, const spo_band_config_t *vbc, int rbits, int spinor,
+                            float kq_scale, float *scores, float *out) {
+    sqfree_rows_t c = {kpack, vpack, n_ctx, hd, rbits, spinor, m, kbc, vbc};
+    attn_core(q, n_q, n_kvh, n_ctx, hd, kq_scale, sqfree_row, &c, scores, out);
 }
 
 /* Pearson correlation, accumulated in double (the fidelity metric of the

@@ -206,6 +206,12 @@ void spo_hier_attn_decode(const float *q, const uint8_t *kpack, const uint8_t *v
                           int n_skel, const int *skel_idx, int n_target, const int *target_idx,
                           const spo_band_config_t *skel_bc, const uint16_t *W, int rbits,
                           float kq_scale, float *scores, float *out);
+/* spo_attn_decode's arithmetic with K~ and V~ from spo_sqfree_decompress (K with
+ * the K skeleton bands kbc, V with vbc; one Knight mask). */
+void spo_sqfree_attn_decode(const float *q, const uint8_t *kpack, const uint8_t *vpack,
+                            int n_q, int n_kvh, int n_ctx, int hd, const spo_knight_mask_t *m,
+                            const spo_band_config_t *kbc, const spo_band_config_t *vbc, int rbits, int spinor,
+                            float kq_scale, float *scores, float *out);
 
 /* ---- metrics ---- */
 float spo_correlation_f32(const float *a, const float *b, int n);

@@ -4,6 +4,8 @@
 // quantize/dequantize, 64-row tiles moved through LDS with coalesced buffer
 // loads and stores, and the host-side launch helpers they share.
 #pragma once
+#include <stdlib.h>
+
 #include <algorithm>
 
 #include "sp_internal.h"
@@ -734,11 +736,21 @@ int device_cu_count() {
     }
     return cus;
 }
-int persistent_blocks() { return device_cu_count() * 16; }
+// SP_HIP_MAX_BLOCKS=n (read at each launch) caps the persistent and resident grids,
+// so that tests reach the multi-tile loops (cross-tile prefetch, every block walking
+// several tiles) with inputs small enough for the CPU oracle.
+int grid_cap(int blocks) {
+    if (const char *e = getenv("SP_HIP_MAX_BLOCKS")) {
+        const int n = atoi(e);
+        if (n > 0 && n < blocks) return n;
+    }
+    return blocks;
+}
+int persistent_blocks() { return grid_cap(device_cu_count() * 16); }
 // Single-wave blocks that are resident at once for a kernel that fits `waves_per_simd`
 // waves on a SIMD: a grid of that size keeps every block walking several tiles, so a
 // tile's loads overlap the previous tile's compute.
-int resident_blocks(int waves_per_simd) { return device_cu_count() * 4 * waves_per_simd; }
+int resident_blocks(int waves_per_simd) { return grid_cap(device_cu_count() * 4 * waves_per_simd); }
 
 // Kernel constants from the host plan: cas[pi][m] is row 1 of the plan's p x p
 // table (C[1][m] = cas(2*pi*m/p)), which holds every value C[k][j] takes.

@@ -10,10 +10,13 @@
 // The array is a file-scope __device__ variable, so every GPU the library runs
 // on holds its own copy until the process ends. Its device address is looked up
 // once per device with hipGetSymbolAddress and kept per device; host code uses
-// only that address. The kernels write every scratch word they later read in
-// the same call, so nothing has to start at zero, but all calls on one GPU share
-// the array: calls that overlap on one GPU (two streams, or two host threads)
-// race on it.
+// only that address. The array's last lines hold the matrix-core kernel's
+// per-KV-head arrival counters, which must be zero when a call starts: the
+// array is zero-initialised, and every completed call leaves the counters at
+// zero (the last block of each KV head resets its counter). The kernels write
+// every other scratch word before reading it in the same call. All calls on one
+// GPU share the array: calls that overlap on one GPU (two streams, or two host
+// threads) race on it.
 #include <mutex>
 
 #include "sp_internal.h"

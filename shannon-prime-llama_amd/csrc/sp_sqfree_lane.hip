@@ -2,7 +2,7 @@
 // shipping geometry: head_dim 128 padded to 154 = 2*7*11, skeleton bands
 // 5/4/4/4/5 over the first SK squarefree-first coefficients (SK = 77, the
 // reference CUDA default, or 115 = 0.75 of the pad), 3-bit residuals, spinor
-// sheet on.
+// sheet on; at SK = 115 also one 3-bit skeleton band (configs[3]'s V).
 //
 // Each lane owns one vector: the pad, the staged Vilenkin transform, the
 // skeleton gather, the CSR Mobius prediction, the spinor choice and every
@@ -282,6 +282,7 @@ k_sqfree_decode_lane_cells(const unsigned char *__restrict__ src, long long so, 
 // ---------------------------------------------------------------------------
 using SkelL77 = Layout<77, 5, 4, 4, 4, 5>;
 using SkelL115 = Layout<115, 5, 4, 4, 4, 5>;
+using SkelL115V3 = Layout<115, 3>;  // configs[3]'s V: one 3-bit band over the 115-coefficient skeleton
 
 template <int SK, class SL>
 bool sq_geometry_matches(const SpPlan &P, const SpSqGeo &G) {
@@ -348,6 +349,10 @@ hipError_t sp_launch_sqfree_decode_lane_cells(const SpPlan &P, const SpSqGeo &G,
         return dtype == SP_DT_F16
                    ? sq_dec_cells_launch<SP_DT_F16, 115, SkelL115>(P, src, so, dst, dout, din, cells, n_outer, n_inner, s)
                    : sq_dec_cells_launch<SP_DT_F32, 115, SkelL115>(P, src, so, dst, dout, din, cells, n_outer, n_inner, s);
+    if (sq_geometry_matches<115, SkelL115V3>(P, G))
+        return dtype == SP_DT_F16
+                   ? sq_dec_cells_launch<SP_DT_F16, 115, SkelL115V3>(P, src, so, dst, dout, din, cells, n_outer, n_inner, s)
+                   : sq_dec_cells_launch<SP_DT_F32, 115, SkelL115V3>(P, src, so, dst, dout, din, cells, n_outer, n_inner, s);
     return hipErrorNotSupported;
 }
 
@@ -366,6 +371,9 @@ hipError_t sp_launch_sqfree_encode_lane(const SpPlan &P, const SpSqGeo &G, const
     if (sq_geometry_matches<115, SkelL115>(P, G))
         return dtype == SP_DT_F16 ? sq_enc_launch<SP_DT_F16, 115, SkelL115>(P, src, so, si, dst, dout, n_outer, n_inner, s)
                                   : sq_enc_launch<SP_DT_F32, 115, SkelL115>(P, src, so, si, dst, dout, n_outer, n_inner, s);
+    if (sq_geometry_matches<115, SkelL115V3>(P, G))
+        return dtype == SP_DT_F16 ? sq_enc_launch<SP_DT_F16, 115, SkelL115V3>(P, src, so, si, dst, dout, n_outer, n_inner, s)
+                                  : sq_enc_launch<SP_DT_F32, 115, SkelL115V3>(P, src, so, si, dst, dout, n_outer, n_inner, s);
     return hipErrorNotSupported;
 }
 
@@ -381,5 +389,8 @@ hipError_t sp_launch_sqfree_decode_lane(const SpPlan &P, const SpSqGeo &G, const
     if (sq_geometry_matches<115, SkelL115>(P, G))
         return dtype == SP_DT_F16 ? sq_dec_launch<SP_DT_F16, 115, SkelL115>(P, src, so, dst, dout, din, n_outer, n_inner, s)
                                   : sq_dec_launch<SP_DT_F32, 115, SkelL115>(P, src, so, dst, dout, din, n_outer, n_inner, s);
+    if (sq_geometry_matches<115, SkelL115V3>(P, G))
+        return dtype == SP_DT_F16 ? sq_dec_launch<SP_DT_F16, 115, SkelL115V3>(P, src, so, dst, dout, din, n_outer, n_inner, s)
+                                  : sq_dec_launch<SP_DT_F32, 115, SkelL115V3>(P, src, so, dst, dout, din, n_outer, n_inner, s);
     return hipErrorNotSupported;
 }

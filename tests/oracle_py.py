@@ -314,6 +314,19 @@ def hier_attn_decode(q, kpack, vpack, n_kvh, n_ctx, hd, pad, skel_idx, tgt_idx, 
     return scores, out
 
 
+def sqfree_attn_decode(q, kpack, vpack, n_kvh, n_ctx, hd, km, kbc, vbc, rbits, spinor, kq_scale,
+                       want_scores=True, want_out=True):
+    """spo_sqfree_attn_decode: kpack/vpack [n_kvh][n_ctx][B] uint8 (K with kbc, V with vbc)."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    n_q = q.shape[0]
+    scores = np.zeros((n_q, n_ctx), np.float32) if want_scores else None
+    out = np.zeros((n_q, hd), np.float32) if want_out else None
+    lib().spo_sqfree_attn_decode(ptr(q), ptr(np.ascontiguousarray(kpack)), ptr(np.ascontiguousarray(vpack)),
+                                 n_q, n_kvh, n_ctx, hd, C.byref(km.m), C.byref(kbc), C.byref(vbc), rbits,
+                                 int(spinor), C.c_float(kq_scale), ptr(scores), ptr(out))
+    return scores, out
+
+
 def correlation(a, b):
     a = np.ascontiguousarray(a, dtype=np.float32).ravel()
     b = np.ascontiguousarray(b, dtype=np.float32).ravel()

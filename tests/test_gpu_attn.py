@@ -32,9 +32,13 @@ def rel_close(got, ref, tol=1e-3, floor=1e-2):
     assert got.shape == ref.shape
     bound = tol * np.maximum(np.abs(ref), floor * np.abs(ref).max())
     err = np.abs(got - ref)
-    worst = int(np.argmax(err / bound))
+    if not (bound > 0).any():  # an all-zero reference: the result must be exactly zero
+        np.testing.assert_array_equal(got, ref)
+        return
+    ratio = np.divide(err, bound, out=np.where(err > 0, np.inf, 0.0), where=bound > 0)
+    worst = int(np.argmax(ratio))
     assert np.all(err <= bound), ("elementwise", worst, got.ravel()[worst], ref.ravel()[worst],
-                                  float((err / bound).max()))
+                                  float(ratio.max()))
 
 
 ATTN_CASES = [
@@ -166,14 +170,15 @@ def test_band_limited_attention_matches_oracle(n_q, H, n_ctx, path, monkeypatch)
     cc.free()
 
 
-# The shapes the bench times. 8 KV heads at 32768 positions are 1024 splits of
-# 256 positions, more than two blocks per CU, so each matrix-core block folds a
-# run of consecutive splits with an online softmax and prefetches the next
-# split's records while it computes: 32768 gives runs of 2; 16600 (65 splits per
-# head, the last one partial) ends each head with a run of one partial split;
-# 40000 (157 splits per head) gives runs of 3.
-# (4, 1, 40000) and (8, 1, 40000): one KV head, so 40 blocks each write a partial; the last
-# block merges them in runs of 16 (two halves of 20 for GQA 4, one run of 40 for GQA 8)
+# The shapes the bench times. The matrix-core kernel (k_attn_wave) gives each wave
+# one 64-position tile while the context fits one round of 16-wave blocks (one per
+# CU): 8 KV heads at 32768 positions are 4096 tiles on 256 blocks, one tile per wave,
+# and a layer is one launch whose last block per KV head merges the blocks'
+# partials. 16600 (260 tiles per head, the last one partial) ends each head with a
+# partial tile. 40000 (625 tiles per head, 5000 in all) is more than one round, so
+# each wave walks two tiles with an online softmax across them (the multi-tile path).
+# (4, 1, 40000) and (8, 1, 40000): one KV head, so its blocks all count on one
+# counter and the last of them merges every block's partials.
 LONG_CASES = [(32, 8, 32768), (32, 8, 16600), (32, 8, 40000), (4, 1, 40000), (8, 1, 40000)]
 
 

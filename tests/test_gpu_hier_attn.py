@@ -59,6 +59,13 @@ CASES = [
     (96, 2, [4], 2, 6, 257, 0),         # pad 105, GQA 3 (odd: a lone last head), 1-position last chunk
     (256, 2, [5, 5], 1, 1, 1, 0),       # a single position
     (256, 2, [5, 5], 8, 16, 2000, 3),   # configs[4] head layout (8 KV heads, GQA 2), 3 runs of 2-3 chunks
+    # the bench's run sizing (no cap): three resident blocks per CU spread over the KV
+    # heads, so more than 48 runs per head and the merge sums them in several passes
+    (256, 2, [5, 5], 8, 16, 25000, 0),  # configs[4] head layout: 96 runs per head (98 chunks)
+    (256, 2, [5, 5], 1, 2, 25000, 0),   # one KV head: 98 runs of one chunk, three merge passes
+    (256, 2, [5, 5], 1, 2, 75300, 49),  # 49 runs of 6-7 chunks (295 chunks): long online softmax
+                                        # chains and the scores-only instance's K prefetch across
+                                        # chunks, then a second merge pass
 ]
 
 

@@ -248,3 +248,92 @@ def test_hier_record_size_cfg5():
     skel_idx, tgt_idx = O.hier_geometry(pad)
     assert (pad, len(skel_idx), len(tgt_idx)) == (330, 30, 300)
     assert O.hier_bytes(O.band_config(30, [5, 5]), 300, 2) == 103
+
+
+# The benched calls run every block of the persistent (decode) or resident (encode)
+# grid over many 64-vector tiles, with the next tile's rows or records prefetched
+# across tiles. SP_HIP_MAX_BLOCKS caps the grid so that inputs small enough for the
+# CPU oracle take the same multi-tile path: 3 blocks over 4 heads x 900 tokens
+# (60 tiles per side) is 20 tiles per block, the last tile of each head partial.
+@pytest.mark.parametrize("sk_frac,v_bits", [(0.75, [5, 4, 4, 4, 5]), (0.75, [3]), (0.0, [5, 4, 4, 4, 5])])
+def test_sqfree_multi_tile_blocks(sk_frac, v_bits, monkeypatch):
+    """configs[3]'s codec (pad 154, skeleton 115 or 77, 3-bit residual, spinor;
+    K 5/4/4/4/5, V 5/4/4/4/5 as the reference hook mirrors K, or V one 3-bit band
+    as configs[3] asks) through the layer-wide write/read with every block walking
+    ~20 tiles: records and fp32 reconstructions bit-exact against the oracle."""
+    monkeypatch.setenv("SP_HIP_MAX_BLOCKS", "3")
+    say(f"sqfree multi-tile sk_frac={sk_frac} v_bits={v_bits}")
+    hd, H, n, start = 128, 4, 900, 5
+    k16, v16 = W.cfg4_kv(n_heads=H, n_pos=n, hd=hd, seed=57)
+    pad = O.sqfree_pad_dim(hd)
+    sk = int(pad * sk_frac) if sk_frac else pad // 2
+    km = O.Knight(pad, sk)
+    k_bits = [5, 4, 4, 4, 5]
+    kbc, vbc = O.band_config(sk, k_bits), O.band_config(sk, v_bits)
+    cfg = S.config(hd, 1, H, k_bits=k_bits, v_bits=v_bits)
+    cc = S.SqfreeCache(cfg, start + n + 2, rbits=3, spinor=True, sk_k=sk,
+                       stream=torch.cuda.current_stream().cuda_stream)
+    Bk, Bv = cc.c.bytes_per_pos_k, cc.c.bytes_per_pos_v
+    if sk == 115:
+        assert (Bk, Bv) == (100, 100 if len(v_bits) == 5 else 70)
+    stride = H * hd
+    kt, vt = dev(_rows(k16, 0)), dev(_rows(v16, 0))
+    S.check(S.lib().sp_hip_sqfree_write_layer(cc.ref, 0, start, n, p(kt), p(vt), stride, S.DTYPE_F16))
+    ko, vo = empty_f32(n * stride), empty_f32(n * stride)
+    S.check(S.lib().sp_hip_sqfree_read_layer(cc.ref, 0, start, n, p(ko), p(vo), stride, S.DTYPE_F32))
+    ms = cc.c.max_seq_len
+    for name, x16, cache, B, bc, out in (("K", k16, cc.c.d_k_cache, Bk, kbc, ko), ("V", v16, cc.c.d_v_cache, Bv, vbc, vo)):
+        allr = d2h(cache, H * ms * B).reshape(H, ms, B)
+        g = host(out).reshape(n, stride)
+        for h in range(H):
+            ref = O.sqfree_compress_f16(x16[h].view(np.uint16), hd, km, bc, 3, True)
+            rec = O.sqfree_decompress_f32(ref, hd, km, bc, 3, True)
+            np.testing.assert_array_equal(allr[h, start:start + n], ref, err_msg=f"{name} head {h}")
+            assert not allr[h, :start].any() and not allr[h, start + n:].any(), "writes outside the tokens"
+            np.testing.assert_array_equal(g[:, h * hd:(h + 1) * hd].view(np.uint32), rec.view(np.uint32),
+                                          err_msg=f"{name} head {h}")
+    cc.free()
+
+
+@pytest.mark.parametrize("sides", ["k_only", "k_and_v"])
+def test_hier_multi_tile_blocks(sides, monkeypatch):
+    """configs[4]'s hier codec (pad 330, 30 skeleton at 5/5, 300 targets at 2 bits)
+    with the grid capped at 3 blocks: the one-sided encode (2 heads x 1000 tokens,
+    32 tiles) and the two-sided K+V launch of a prefill chunk (64 tiles), then the
+    decode, each block walking 10-22 tiles with the cross-tile prefetch; records and
+    reconstructions bit-exact against the oracle."""
+    monkeypatch.setenv("SP_HIP_MAX_BLOCKS", "3")
+    say(f"hier multi-tile {sides}")
+    hd, H, n, start, rbits = 256, 2, 1000, 3, 2
+    k16, v16 = W.cfg5_kv(n_heads=H, n_pos=n, hd=hd, seed=61)
+    pad = O.sqfree_pad_dim(hd)
+    skel_idx, tgt_idx = O.hier_geometry(pad)
+    skel_bc = O.band_config(len(skel_idx), [5, 5])
+    Wm = W.hier_W(H, len(tgt_idx), len(skel_idx), seed=62)
+    ms = start + n + 1
+    hc = S.HierCache(S.config(hd, 1, H), pad, skel_idx, tgt_idx, S.band_config(len(skel_idx), [5, 5]), rbits, ms, H,
+                     stream=torch.cuda.current_stream().cuda_stream)
+    hc.upload_W(Wm)
+    B = hc.c.bytes_per_pos_k
+    stride = H * hd
+    kt, vt = dev(_rows(k16, 0)), dev(_rows(v16, 0))
+    S.check(S.lib().sp_hip_hier_write_layer(hc.ref, 0, start, n, p(kt), p(vt) if sides == "k_and_v" else None,
+                                            stride, S.DTYPE_F16))
+    ko, vo = empty_f32(n * stride), empty_f32(n * stride)
+    S.check(S.lib().sp_hip_hier_read_layer(hc.ref, 0, start, n, p(ko), p(vo) if sides == "k_and_v" else None,
+                                           stride, S.DTYPE_F32))
+    checks = [("K", k16, hc.c.d_k_cache, ko)]
+    if sides == "k_and_v":
+        checks.append(("V", v16, hc.c.d_v_cache, vo))
+    for name, x16, cache, out in checks:
+        allr = d2h(cache, H * ms * B).reshape(H, ms, B)
+        g = host(out).reshape(n, stride)
+        for h in range(H):
+            ref = O.hier_compress_f16(x16[h].view(np.uint16), hd, pad, skel_idx, tgt_idx, skel_bc, Wm[h], rbits)
+            rec = O.hier_decompress_f32(ref, hd, pad, skel_idx, tgt_idx, skel_bc, Wm[h], rbits)
+            np.testing.assert_array_equal(allr[h, start:start + n], ref, err_msg=f"{name} head {h}")
+            np.testing.assert_array_equal(g[:, h * hd:(h + 1) * hd].view(np.uint32), rec.view(np.uint32),
+                                          err_msg=f"{name} head {h}")
+    if sides == "k_only":
+        assert not d2h(hc.c.d_v_cache, H * ms * B).any(), "V written by a K-only call"
+    hc.free()

@@ -83,11 +83,47 @@ def test_noalloc_refuses_oversized_calls(cache):
     assert rc == -1
     assert b"scratch" in S.lib().sp_hip_last_error()
     assert bool((sc == 7.0).all()) and bool((out == 7.0).all())
-    # one split fewer fits
+    # one split fewer fits, and gives what the workspace entry point gives
     n_kv = 501 * 256
     assert n_q * HD + n_q * ((n_kv + 255) // 256) * (HD + 2) + counters <= cap
     rc = L.sp_hip_attn_decode_bands_noalloc(cache.ref, 0, n_kv, p(qt), n_q, C.c_float(1.0), None, p(out), -1,
                                             stream())
     assert rc == 0
+    ref = empty_f32(n_q * HD)
+    S.check(L.sp_hip_attn_decode_bands(cache.ref, 0, n_kv, p(qt), n_q, C.c_float(1.0), None, p(ref), -1, stream()))
+    got = host(out)
+    assert np.isfinite(got).all() and np.abs(got).max() > 0
+    np.testing.assert_array_equal(got, host(ref))
+
+
+def test_noalloc_under_graph_capture(cache):
+    """The allocation-free call captured in a HIP graph (torch.cuda.graph): an
+    eager call first (it looks up the scratch address), then one captured call,
+    replayed three times with the query buffer refilled between replays, each
+    replay equal to sp_hip_attn_decode_bands on the same query (eager work and
+    synchronisations between the replays)."""
+    L = S.lib()
+    n_kv, n_q = 4096, 32
+    scale = C.c_float(1.0 / math.sqrt(HD))
+    qs = [W.cfg2_q(n_q=n_q, hd=HD, pos=n_kv, seed=s) for s in (5, 6)]
+    qt = dev(qs[0])
+    sc, out = empty_f32(n_q * n_kv), empty_f32(n_q * HD)
+    S.check(L.sp_hip_attn_decode_bands_noalloc(cache.ref, 0, n_kv, p(qt), n_q, scale, p(sc), p(out), -1, stream()))
     torch.cuda.synchronize()
-    assert bool(torch.isfinite(out).all())
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    say("noalloc graph capture")
+    with torch.cuda.graph(g, stream=side):
+        rc = L.sp_hip_attn_decode_bands_noalloc(cache.ref, 0, n_kv, p(qt), n_q, scale, p(sc), p(out), -1,
+                                                C.c_void_p(side.cuda_stream))
+    assert rc == 0, S.lib().sp_hip_last_error()
+    for i in (1, 0, 1):
+        qt.copy_(torch.from_numpy(qs[i]).cuda())
+        sc.fill_(7.0)
+        out.fill_(7.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        s_ref, o_ref = _call(L.sp_hip_attn_decode_bands, cache, n_kv, qt, n_q, -1)
+        np.testing.assert_array_equal(host(sc), s_ref)
+        np.testing.assert_array_equal(host(out), o_ref)
