@@ -302,6 +302,25 @@ int sp_hip_sqfree_calibrate_begin(sp_hip_sqfree_cache_t *cc);
 int sp_hip_sqfree_calibrate_feed(sp_hip_sqfree_cache_t *cc, const void *d_vecs, long long row_stride, int n_vecs,
                                  int dtype);
 int sp_hip_sqfree_calibrate_end(sp_hip_sqfree_cache_t *cc, int *ranking_out, int apply);
+/* Extension: fused decode attention over the sqfree cache's records of one layer
+ * (positions [0, n_kv) of every KV head), the contract of sp_hip_attn_decode:
+ * d_q [n_q][head_dim] fp32 (GQA: query head h reads KV head h / (n_q / n_heads_kv),
+ * at most 8 per KV head), d_scores [n_q][n_kv] = kq_scale * q . K~ and d_out
+ * [n_q][head_dim] = softmax(scores) . V~, with K~ and V~ what sp_hip_sqfree_read_*
+ * returns (the read path of sp_cuda_sqfree_read_one, shannon_prime_sqfree.cu:857-950,
+ * which the reference's hook runs per vector before its attention,
+ * llama-cpp-b8861-full-engine.patch:1205-1207); either output may be NULL (not both).
+ * Nothing is reconstructed: the query moves into the records' coefficient domain
+ * (q~ = V(q zero-padded to pad_dim)) once per query head and each record's skeleton
+ * and residual coefficients (+-prediction + deviation, the spinor sheet's sign) are
+ * dotted in place; sum p V~ is finished by one transform per query head. The
+ * reference's fused op is ship-only (llama_sp_fused_kq.cpp:14-34). Geometry: head_dim
+ * 128 (pad 154), skeleton 77 or 115 with K bands 5/4/4/4/5, V bands 5/4/4/4/5 (the
+ * hook's mirror of K) or, at 115, one 3-bit band; 3-bit residuals; spinor; default
+ * Knight tables. Other geometries return -1. The workspace is allocated on the first
+ * call and grown when a call needs more. 0 or -1. */
+int  sp_hip_sqfree_attn_decode(const sp_hip_sqfree_cache_t *cc, int layer, int n_kv, const float *d_q, int n_q,
+                               float kq_scale, float *d_scores, float *d_out, void *stream);
 /* Host copies of the Knight tables (for tests and calibration tools). */
 int  sp_hip_sqfree_get_tables(const sp_hip_sqfree_cache_t *cc, int *skeleton_idx,
                               int *residual_idx, int *csr_offsets, int *csr_skel_slot,

@@ -249,7 +249,8 @@ k_hier_attn_prep(const SpPlan P, const SpHierAttnArgs A, float *__restrict__ pre
     // through range-checked buffer loads (unconditional: reads past a range return 0),
     // W reaching LDS while the query is transformed
     constexpr int PU = (SP_GEN_MAX_N + NT - 1) / NT;
-    const int nw = nt * ns, nwd = nw >> 1;  // W dwords (an odd count's last half loads alone)
+    const bool has_w = A.W != nullptr;  // no predictor: u = q~_skel
+    const int nw = has_w ? nt * ns : 0, nwd = nw >> 1;  // W dwords (an odd count's last half loads alone)
     const bool w_reg = nwd <= W_DW * NT && ((uintptr_t)Wk & 3) == 0;
     const __amdgpu_buffer_rsrc_t rq =
         __builtin_amdgcn_make_buffer_rsrc((void *)(A.q + (long long)h * A.hd), (short)0, A.hd * 4, 0x00020000);
@@ -266,7 +267,7 @@ k_hier_attn_prep(const SpPlan P, const SpHierAttnArgs A, float *__restrict__ pre
     if (w_reg) {
 #pragma unroll
         for (int u = 0; u < W_DW; u++) wd[u] = __builtin_amdgcn_raw_buffer_load_b32(rw, 4 * (tid + u * NT), 0, 0);
-    } else {
+    } else if (has_w) {
         copy_to_lds<unsigned short, 16>(Ws, Wk, nw, nw, tid);
     }
 #pragma unroll
@@ -287,12 +288,14 @@ k_hier_attn_prep(const SpPlan P, const SpHierAttnArgs A, float *__restrict__ pre
         if (t < nt32) qt[t] = t < nt ? A.kq_scale * c[ti[u]] : 0.0f;
     }
     __syncthreads();
-    // W^T q~_tgt in 8 interleaved partial sums per skeleton coefficient
+    // W^T q~_tgt in 8 interleaved partial sums per skeleton coefficient (0 without W)
     for (int i = tid; i < 8 * ns; i += NT) {
         const int s = i % ns, g = i / ns;
         float acc = 0.0f;
+        if (has_w) {
 #pragma unroll 4
-        for (int t = g; t < nt; t += 8) acc = fmaf(sp_f16_bits_to_f32(Ws[t * ns + s]), qt[t], acc);
+            for (int t = g; t < nt; t += 8) acc = fmaf(sp_f16_bits_to_f32(Ws[t * ns + s]), qt[t], acc);
+        }
         part[g * ns4 + s] = acc;
     }
     __syncthreads();
@@ -780,11 +783,12 @@ k_hier_attn_merge(const SpPlan P, const SpHierAttnArgs A, const float *__restric
     float *e = cs + r4(ns);
     unsigned short *Ws = reinterpret_cast<unsigned short *>(e + r4(n_runs));
     const unsigned short *Wk = reinterpret_cast<const unsigned short *>(A.W) + (long long)kvh * A.w_outer;
-    // W loads while the partials are merged
-    const bool w_reg = nt * ns <= W_STAGE * NT;
+    // W loads while the partials are merged (no predictor: c_tgt is the weighted sum alone)
+    const bool has_w = A.W != nullptr;
+    const bool w_reg = has_w && nt * ns <= W_STAGE * NT;
     RegStage<unsigned short, W_STAGE> wst;
     if (w_reg) wst.load(Wk, nt * ns, tid);
-    else copy_to_lds<unsigned short, 16>(Ws, Wk, nt * ns, nt * ns, tid);
+    else if (has_w) copy_to_lds<unsigned short, 16>(Ws, Wk, nt * ns, nt * ns, tid);
     const float *ph = part + (long long)h * n_runs * pp;
     // range-checked buffer loads (rows past the last run read as 0): unconditional,
     // so every load of a pass is in flight before the first wait
@@ -852,7 +856,7 @@ k_hier_attn_merge(const SpPlan P, const SpHierAttnArgs A, const float *__restric
     }
     if (w_reg) wst.store(Ws, nt * ns, tid);
     __syncthreads();
-    for (int t = tid; t < nt; t += NT) {
+    for (int t = tid; has_w && t < nt; t += NT) {
         float pred = 0.0f;
 #pragma unroll 4
         for (int s = 0; s < ns; s++) pred = fmaf(sp_f16_bits_to_f32(Ws[t * ns + s]), cs[s], pred);
@@ -935,5 +939,32 @@ hipError_t sp_launch_hier_attn(const SpPlan &P, const SpHierAttnArgs &A, float *
     if (A.out) launch_split<true>(P, A, prep, part, n_runs, rb, G, lds_split, s);
     else launch_split<false>(P, A, prep, part, n_runs, rb, G, lds_split, s);
     if (A.out) hipLaunchKernelGGL(k_hier_attn_merge, dim3(A.n_q), dim3(NT), lds_merge, s, P, A, part, n_runs);
+    return hipGetLastError();
+}
+
+// The two launches that do not touch records, for the sqfree attention (A.W may be null).
+static bool prep_merge_args_ok(const SpHierAttnArgs &A) {
+    return A.n_q > 0 && A.n_kvh > 0 && A.n_q % A.n_kvh == 0 && A.n_q / A.n_kvh <= MAX_G && A.pad <= SP_GEN_MAX_N &&
+           A.n_skel + A.n_target <= SP_GEN_MAX_N && A.hd <= A.pad && A.ps == sp_hier_attn_prep_floats(A.n_skel, A.n_target) &&
+           A.pp >= 4 + A.n_skel + A.n_target;
+}
+
+hipError_t sp_launch_hier_attn_prep(const SpPlan &P, const SpHierAttnArgs &A, float *prep, hipStream_t s) {
+    if (!prep_merge_args_ok(A)) return hipErrorInvalidValue;
+    const size_t lds_prep = 4 * (size_t)(r4(A.pad) + r32(A.n_target) + 8 * r4(A.n_skel)) +
+                            (A.W ? 2 * (size_t)A.n_target * A.n_skel : 0);
+    if (lds_prep > 65536) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_hier_attn_prep, dim3(A.n_q), dim3(NT), lds_prep, s, P, A, prep);
+    return hipGetLastError();
+}
+
+hipError_t sp_launch_hier_attn_merge(const SpPlan &P, const SpHierAttnArgs &A, const float *part, int n_runs,
+                                     hipStream_t s) {
+    if (!prep_merge_args_ok(A) || !A.out || n_runs <= 0 || n_runs > MERGE_RUNS_PER_THREAD * NT)
+        return hipErrorInvalidValue;
+    const size_t lds_merge = 4 * (size_t)(r4(A.pad) + r4(A.n_skel) + r4(n_runs)) +
+                             (A.W ? 2 * (size_t)A.n_target * A.n_skel : 0);
+    if (lds_merge > 65536) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_hier_attn_merge, dim3(A.n_q), dim3(NT), lds_merge, s, P, A, part, n_runs);
     return hipGetLastError();
 }

@@ -229,6 +229,31 @@ size_t sp_hier_attn_workspace_floats(const SpHierAttnArgs &A, int n_runs);
 int sp_hier_attn_runs(const SpHierAttnArgs &A, int cus);
 hipError_t sp_launch_hier_attn(const SpPlan &P, const SpHierAttnArgs &A, float *ws, size_t ws_floats, int n_runs,
                                hipStream_t s);
+// The hier attention's query preparation and merge alone (one block per query head),
+// for attention kernels whose records live in the same coefficient domain. A.W may be
+// null: no predictor (u = q~_skel; merged target coefficients = the weighted sums).
+hipError_t sp_launch_hier_attn_prep(const SpPlan &P, const SpHierAttnArgs &A, float *prep, hipStream_t s);
+hipError_t sp_launch_hier_attn_merge(const SpPlan &P, const SpHierAttnArgs &A, const float *part, int n_runs,
+                                     hipStream_t s);
+
+// Fused decode attention over sqfree+spinor records (sp_sqfree_attn.hip): the split
+// kernel's arguments (records of slot (layer, KV head 0), KV head h at + h * slot bytes).
+struct SpSqAttnArgs {
+    const unsigned char *kcache, *vcache;
+    long long k_slot_bytes, v_slot_bytes;
+    float *scores;  // [n_q][n_kv] or null
+    float *out;     // [n_q][hd] or null
+    int n_q, n_kvh, n_kv;
+    int ps, qo, pp;  // prepared-query floats per head, its residual part's offset; partial floats
+};
+// 1..3: the lane specialization serving this geometry (skeleton 77 with 5/4/4/4/5 K and
+// V; 115 with 5/4/4/4/5 K and V; 115 with V one 3-bit band), 0: none
+int sp_sqfree_attn_kind(const SpPlan &KP, const SpPlan &VP, const SpSqGeo &G);
+int sp_sqfree_attn_runs(int n_kvh, int n_kv, int cus);
+// HA: the prep/merge arguments (pad, skeleton/residual index tables as skel_idx /
+// tgt_idx, W null, q, kq_scale, out); ws: prep [n_q * ps] then partials.
+hipError_t sp_launch_sqfree_attn(const SpPlan &KP, const SpPlan &VP, const SpSqGeo &G, const SpHierAttnArgs &HA,
+                                 const SpSqAttnArgs &A, float *ws, size_t ws_floats, int n_runs, hipStream_t s);
 
 // one-vector-per-lane hier kernels for the default geometry at head_dim 256;
 // hipErrorNotSupported (nothing launched) when no specialization fits. src2/dst2:

@@ -935,6 +935,9 @@ struct SqPriv {
     bool calibrating = false;
     std::vector<double> csum, csum2;
     long long cn = 0;
+    // fused attention workspace (prepared queries, run partials), grown on demand
+    float *d_attn_ws = nullptr;
+    size_t attn_ws_floats = 0;
 };
 
 static SpSqGeo sq_geo(const sp_hip_sqfree_cache_t *cc, int is_v) {
@@ -1074,6 +1077,7 @@ extern "C" void sp_hip_sqfree_cache_free(sp_hip_sqfree_cache_t *cc) {
                     cc->d_csr_mu_sign, cc->d_k_cache, cc->d_v_cache};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
+    if (cc->priv && ((SqPriv *)cc->priv)->d_attn_ws) (void)hipFree(((SqPriv *)cc->priv)->d_attn_ws);
     delete (SqPriv *)cc->priv;
     memset(cc, 0, sizeof(*cc));
 }
@@ -1145,6 +1149,82 @@ extern "C" int sp_hip_sqfree_read_layer(const sp_hip_sqfree_cache_t *cc, int lay
                     "sqfree read_layer")) return -1;
     }
     return 0;
+}
+
+extern "C" int sp_hip_sqfree_attn_decode(const sp_hip_sqfree_cache_t *cc, int layer, int n_kv, const float *d_q,
+                                         int n_q, float kq_scale, float *d_scores, float *d_out, void *stream) {
+    if (!sq_slot_ok(cc, layer, 0, 0, n_kv) || n_kv <= 0 || !d_q || n_q <= 0 || (!d_scores && !d_out)) {
+        set_err("sqfree attn: bad args");
+        return -1;
+    }
+    const int H = cc->config.n_heads_kv;
+    if (n_q % H || n_q / H > 8) { set_err("sqfree attn: n_q must be a multiple of n_heads_kv, at most 8 per KV head"); return -1; }
+    SqPriv *pv = (SqPriv *)cc->priv;
+    const SpSqGeo GK = sq_geo(cc, 0);
+    if (!sp_sqfree_attn_kind(pv->kplan, pv->vplan, GK)) {
+        set_err("sqfree attn: no fused kernel for this geometry (needs head_dim 128, pad 154, skeleton 77 or 115 "
+                "with K bands 5/4/4/4/5, V 5/4/4/4/5 or one 3-bit band at 115, 3-bit residuals, spinor, "
+                "default Knight tables)");
+        return -1;
+    }
+    const long long slot0 = (long long)layer * H;
+    SpHierAttnArgs HA;
+    memset(&HA, 0, sizeof(HA));
+    HA.W = nullptr;  // no predictor: the skeleton and residual coefficients are both stored
+    HA.skel_idx = cc->d_skeleton_idx;
+    HA.tgt_idx = cc->d_residual_idx;
+    HA.q = d_q;
+    HA.kq_scale = kq_scale;
+    HA.scores = d_scores;
+    HA.out = d_out;
+    HA.n_q = n_q;
+    HA.n_kvh = H;
+    HA.n_kv = n_kv;
+    HA.hd = cc->config.head_dim;
+    HA.pad = cc->pad_dim;
+    HA.n_skel = cc->sk_k;
+    HA.n_target = cc->n_res;
+    HA.rbits = cc->residual_bits;
+    HA.B = cc->bytes_per_pos_k;
+    HA.ps = sp_hier_attn_prep_floats(HA.n_skel, HA.n_target);
+    HA.pp = (4 + HA.n_skel + HA.n_target + 3) & ~3;
+    SpSqAttnArgs A;
+    A.kcache = cc->d_k_cache + slot0 * cc->max_seq_len * cc->bytes_per_pos_k;
+    A.vcache = cc->d_v_cache + slot0 * cc->max_seq_len * cc->bytes_per_pos_v;
+    A.k_slot_bytes = (long long)cc->max_seq_len * cc->bytes_per_pos_k;
+    A.v_slot_bytes = (long long)cc->max_seq_len * cc->bytes_per_pos_v;
+    A.scores = d_scores;
+    A.out = d_out;
+    A.n_q = n_q;
+    A.n_kvh = H;
+    A.n_kv = n_kv;
+    A.ps = HA.ps;
+    A.qo = (HA.n_skel + 3) & ~3;  // the prepared query's residual part
+    A.pp = HA.pp;
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    int n_runs = sp_sqfree_attn_runs(H, n_kv, cus);
+    // SP_HIP_SQFREE_ATTN_RUNS=n caps the runs per KV head (read at each call; tests use it
+    // to give every run several tiles at small context lengths)
+    if (const char *e = getenv("SP_HIP_SQFREE_ATTN_RUNS")) {
+        const int r = atoi(e);
+        if (r > 0) n_runs = std::min(n_runs, r);
+    }
+    const size_t need = sp_hier_attn_workspace_floats(HA, n_runs);
+    const hipStream_t s = (hipStream_t)(stream ? stream : cc->stream);
+    if (need > pv->attn_ws_floats) {
+        if (pv->d_attn_ws) {
+            if (!hip_ok(hipStreamSynchronize(s), "sqfree attn: sync before growing the workspace")) return -1;
+            (void)hipFree(pv->d_attn_ws);
+            pv->d_attn_ws = nullptr;
+            pv->attn_ws_floats = 0;
+        }
+        if (!hip_ok(hipMalloc((void **)&pv->d_attn_ws, need * sizeof(float)), "hipMalloc sqfree attn workspace")) return -1;
+        pv->attn_ws_floats = need;
+    }
+    return hip_ok(sp_launch_sqfree_attn(pv->kplan, pv->vplan, GK, HA, A, pv->d_attn_ws, pv->attn_ws_floats, n_runs, s),
+                  "sqfree attn") ? 0 : -1;
 }
 
 extern "C" void sp_hip_sqfree_write_k(sp_hip_sqfree_cache_t *cc, int l, int h, int p, const float *d) { sp_hip_sqfree_write_batch(cc, 0, l, h, p, 1, d, SP_DT_F32); }

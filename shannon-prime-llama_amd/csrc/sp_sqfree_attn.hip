@@ -1,0 +1,319 @@
+// sp_sqfree_attn.hip -- fused decode attention over sqfree+spinor records (the
+// sqfree cache's K and V arrays) for the shipping geometry: head_dim 128 padded to
+// 154, skeleton 77 or 115 (K bands 5/4/4/4/5; V 5/4/4/4/5, or one 3-bit band at
+// skeleton 115), 3-bit residuals, spinor sheet on.
+//
+// The read path (sp_cuda_sqfree_read_one, shannon_prime_sqfree.cu:857-950) rebuilds
+// the pad coefficients c~ (skeleton values from the bands; residual coefficient r as
+// (sheet_r ? -pred_r : pred_r) + (level_r - centre) * step, pred = the Knight CSR over
+// the dequantized skeleton) and returns V(c~)[0, hd), V the length-154 Vilenkin
+// transform, which is symmetric and its own inverse. So nothing is reconstructed:
+//   * with q~ = kq_scale * V(q zero-padded to 154) (once per query head),
+//     q . K~_t = q~ . c~_t, a dot product in the coefficient domain;
+//   * sum_t p_t V~_t = V(sum_t p_t c~_t)[0, hd): the weighted coefficient sums are
+//     finished by one transform per query head.
+//
+// Three launches per layer: the hier attention's query preparation and merge
+// kernels (sp_hier_attn.hip) with no predictor (W = 0: skeleton slots = the Knight
+// skeleton, target slots = the residual coefficients), and the split kernel below:
+// block (KV head, run) is one wave walking the run's 64-position tiles, lane =
+// position, the record decoded into the lane's registers exactly as the read path
+// decodes it (compile-time Knight CSR and record fields), the scores as dot products
+// with the prepared queries, an online softmax across the run's tiles, and the
+// weighted coefficient sums through LDS (the wave's coefficients transposed so that
+// each lane sums one coefficient over the tile's 64 positions).
+#include "sp_sqfree_lane.h"
+
+namespace {
+
+constexpr int PAD = 154;
+constexpr int RBITS = 3;
+
+// The record's pad coefficients in [skeleton slot s | residual r] order: the same
+// arithmetic, in the same order, as k_sqfree_decode_lane before its transform.
+template <int SK, class SL, int DW>
+__device__ __forceinline__ void sq_coefficients(const uint32_t (&rec)[DW], float (&e)[PAD]) {
+    using G = SqRec<PAD, SK, RBITS, true, SL>;
+    constexpr int NR = PAD - SK;
+    float sk[SK];
+    dequant_bands<SL, false, true>(rec, SL::nb, sk);
+#pragma unroll
+    for (int s = 0; s < SK; s++) e[s] = sk[s];
+    const float mag = __uint_as_float(rec_get32(rec, G::mag_byte));
+    constexpr int L = 1 << RBITS;
+    const float center = 0.5f * (float)(L - 1);
+    const float sat = mag * (float)RBITS;
+    const float step = sp_div(2.0f * sat, (float)(L - 1));
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        float p = csr_predict<PAD, SK>(sk, r);
+        if (rec_extract(rec, G::sheet_bit + r, 1)) p = -p;
+        const float d = ((float)rec_extract(rec, G::res_bit + r * RBITS, RBITS) - center) * step;
+        e[SK + r] = p + d;
+    }
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    return v;
+}
+__device__ __forceinline__ float wave_add(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+constexpr int EP = 65;  // LDS row pitch (floats) of the transposed coefficient chunk
+
+// Scores, online softmax and the V records' weighted coefficient sums. Block
+// (kvh, run) takes tiles run, run + n_runs, ... of KV head kvh (64 positions each).
+// prep: the G query heads of KV head kvh at prep + (kvh * G + h) * ps:
+// [q~ at the skeleton slots (r4(SK)) | q~ at the residual coefficients | ...], qo the
+// residual part's offset. Partial per (query head, run) at part + ((h0 + h) * n_runs
+// + run) * pp: [m, l, 0, 0, sum p c~ (PAD coefficients, skeleton then residuals)].
+// OUT = false: scores only.
+template <int SK, class SLK, class SLV, int GM, bool OUT>
+__global__ void __launch_bounds__(64)
+k_sqfree_attn_split(const unsigned char *__restrict__ kc, const unsigned char *__restrict__ vc, long long k_slot,
+                    long long v_slot, int n_kv, int G, const float *__restrict__ prep, int ps, int qo,
+                    float *__restrict__ scores, float *__restrict__ part, int pp, int n_runs) {
+    using GK = SqRec<PAD, SK, RBITS, true, SLK>;
+    using GV = SqRec<PAD, SK, RBITS, true, SLV>;
+    constexpr int NCK = RecTile<GK>::NCK > RecTile<GV>::NCK ? RecTile<GK>::NCK : RecTile<GV>::NCK;
+    constexpr int C2 = PAD - 128;  // coefficients of the third 64-coefficient chunk
+    constexpr int HG = (GM + 1) / 2;  // heads per lane in the third chunk (two lanes per coefficient)
+    static_assert(C2 > 0 && 2 * C2 <= 64, "three chunks of at most 64 coefficients");
+    __shared__ __attribute__((aligned(16))) unsigned char stage[NCK * 1024 + 16];
+    __shared__ float E[64 * EP];
+    __shared__ __attribute__((aligned(16))) float Pw[64 * GM];
+    const int kvh = blockIdx.x, run = blockIdx.y, lane = threadIdx.x;
+    const int h0 = kvh * G;
+    const int tpo = (n_kv + 63) / 64;
+    const int n_tiles = (int)gridDim.x * tpo;
+    const TileMap M{tpo, n_kv};
+    const float *__restrict__ pq = prep + (long long)h0 * ps;
+
+    float m_run[GM], l_run[GM];
+    float acc0[GM], acc1[GM], acc2[HG];
+#pragma unroll
+    for (int h = 0; h < GM; h++) {
+        m_run[h] = -INFINITY;
+        l_run[h] = 0.0f;
+        acc0[h] = acc1[h] = 0.0f;
+    }
+#pragma unroll
+    for (int h = 0; h < HG; h++) acc2[h] = 0.0f;
+    // third chunk: coefficient 128 + c2i for heads hh * HG .. hh * HG + HG - 1
+    const int c2i = lane % C2, hh = lane / C2;
+    const bool c2_on = hh < (GM > 1 ? 2 : 1);
+
+    RecTile<GK> Rk;
+    int c = run;
+    if (c < tpo) rec_tile_load<GK>(Rk, kc, k_slot, M, kvh * tpo + c, n_tiles, lane);
+    for (; c < tpo; c += n_runs) {
+        const int t = kvh * tpo + c;
+        RecTile<GV> Rv;
+        if (OUT) rec_tile_load<GV>(Rv, vc, v_slot, M, t, n_tiles, lane);
+        __syncthreads();  // the previous tile is done with the stage
+        rec_tile_stage<GK>(Rk, stage, M, t, lane);
+        __syncthreads();
+        uint32_t rk[GK::dwords];
+        rec_from_lds<GK>(rk, stage, lane);
+        if (c + n_runs < tpo) rec_tile_load<GK>(Rk, kc, k_slot, M, t + n_runs, n_tiles, lane);
+        float e[PAD];
+        sq_coefficients<SK, SLK>(rk, e);
+        const int pos = c * 64 + lane;
+        const bool live = pos < n_kv;
+        float s[GM];
+#pragma unroll
+        for (int h = 0; h < GM; h++) {
+            s[h] = -INFINITY;
+            if (h < G) {
+                const float *__restrict__ qh = pq + h * ps;
+                float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+                for (int j = 0; j < SK; j += 2) {
+                    a0 = fmaf(qh[j], e[j], a0);
+                    if (j + 1 < SK) a1 = fmaf(qh[j + 1], e[j + 1], a1);
+                }
+#pragma unroll
+                for (int r = 0; r < PAD - SK; r += 2) {
+                    a0 = fmaf(qh[qo + r], e[SK + r], a0);
+                    if (r + 1 < PAD - SK) a1 = fmaf(qh[qo + r + 1], e[SK + r + 1], a1);
+                }
+                const float v = a0 + a1;
+                if (live) {
+                    s[h] = v;
+                    if (scores) scores[(long long)(h0 + h) * n_kv + pos] = v;
+                }
+            }
+        }
+        if (!OUT) continue;
+        // ---- online softmax over the tile (wave-wide per head) ----
+        float alpha[GM];
+#pragma unroll
+        for (int h = 0; h < GM; h++) {
+            alpha[h] = 1.0f;
+            if (h < G) {
+                const float mn = fmaxf(m_run[h], wave_max(s[h]));
+                alpha[h] = __expf(m_run[h] - mn);
+                const float pr = live ? __expf(s[h] - mn) : 0.0f;
+                l_run[h] = fmaf(l_run[h], alpha[h], wave_add(pr));
+                m_run[h] = mn;
+                Pw[lane * GM + h] = pr;
+            } else {
+                Pw[lane * GM + h] = 0.0f;
+            }
+        }
+        // ---- V records of the tile, then their coefficients ----
+        __syncthreads();  // every lane has read its K record from the stage
+        rec_tile_stage<GV>(Rv, stage, M, t, lane);
+        __syncthreads();
+        uint32_t rv[GV::dwords];
+        rec_from_lds<GV>(rv, stage, lane);
+        float ev[PAD];
+        sq_coefficients<SK, SLV>(rv, ev);
+#pragma unroll
+        for (int h = 0; h < GM; h++) {
+            acc0[h] *= alpha[h];
+            acc1[h] *= alpha[h];
+        }
+#pragma unroll
+        for (int k = 0; k < HG; k++) {
+            float a = 1.0f;
+#pragma unroll
+            for (int h = 0; h < GM; h++)
+                if (h == hh * HG + k) a = alpha[h];
+            acc2[k] *= a;
+        }
+        // ---- weighted coefficient sums: chunk of 64 coefficients transposed through
+        // LDS (row = coefficient, column = position), lane = coefficient ----
+#pragma unroll
+        for (int ch = 0; ch < 3; ch++) {
+            const int i0 = 64 * ch, n_i = ch < 2 ? 64 : C2;
+#pragma unroll
+            for (int i = 0; i < 64; i++)
+                if (i < n_i) E[i * EP + lane] = ev[i0 + i];
+            __syncthreads();
+            if (ch == 0) {
+#pragma unroll 4
+                for (int p = 0; p < 64; p++) {
+                    const float ei = E[lane * EP + p];
+#pragma unroll
+                    for (int h = 0; h < GM; h++) acc0[h] = fmaf(Pw[p * GM + h], ei, acc0[h]);
+                }
+            } else if (ch == 1) {
+#pragma unroll 4
+                for (int p = 0; p < 64; p++) {
+                    const float ei = E[lane * EP + p];
+#pragma unroll
+                    for (int h = 0; h < GM; h++) acc1[h] = fmaf(Pw[p * GM + h], ei, acc1[h]);
+                }
+            } else if (c2_on) {
+                // hh * HG + k < GM for every lane with c2_on (two halves of HG heads)
+#pragma unroll 4
+                for (int p = 0; p < 64; p++) {
+                    const float ei = E[c2i * EP + p];
+#pragma unroll
+                    for (int k = 0; k < HG; k++) acc2[k] = fmaf(Pw[p * GM + hh * HG + k], ei, acc2[k]);
+                }
+            }
+            __syncthreads();
+        }
+    }
+    if (!OUT) return;
+    // ---- the run's partial per query head ----
+#pragma unroll
+    for (int h = 0; h < GM; h++) {
+        if (h >= G) continue;
+        float *dst = part + ((long long)(h0 + h) * n_runs + run) * pp;
+        if (lane == 0) {
+            dst[0] = m_run[h];
+            dst[1] = l_run[h];
+            dst[2] = 0.0f;
+            dst[3] = 0.0f;
+        }
+        dst[4 + lane] = acc0[h];
+        dst[4 + 64 + lane] = acc1[h];
+    }
+    if (c2_on) {
+#pragma unroll
+        for (int k = 0; k < HG; k++) {
+            const int h = hh * HG + k;
+            if (h < G) part[((long long)(h0 + h) * n_runs + run) * pp + 4 + 128 + c2i] = acc2[k];
+        }
+    }
+}
+
+using SkelL77 = Layout<77, 5, 4, 4, 4, 5>;
+using SkelL115 = Layout<115, 5, 4, 4, 4, 5>;
+using SkelL115V3 = Layout<115, 3>;
+
+template <int SK, class SLK, class SLV, int GM>
+void launch_split(const SpSqAttnArgs &A, const float *prep, float *part, int n_runs, hipStream_t s) {
+    const dim3 grid(A.n_kvh, n_runs), block(64);
+    if (A.out)
+        hipLaunchKernelGGL((k_sqfree_attn_split<SK, SLK, SLV, GM, true>), grid, block, 0, s, A.kcache, A.vcache,
+                           A.k_slot_bytes, A.v_slot_bytes, A.n_kv, A.n_q / A.n_kvh, prep, A.ps, A.qo, A.scores, part,
+                           A.pp, n_runs);
+    else
+        hipLaunchKernelGGL((k_sqfree_attn_split<SK, SLK, SLV, GM, false>), grid, block, 0, s, A.kcache, A.vcache,
+                           A.k_slot_bytes, A.v_slot_bytes, A.n_kv, A.n_q / A.n_kvh, prep, A.ps, A.qo, A.scores, part,
+                           A.pp, n_runs);
+}
+
+template <int SK, class SLK, class SLV>
+void launch_split_g(const SpSqAttnArgs &A, const float *prep, float *part, int n_runs, hipStream_t s) {
+    const int G = A.n_q / A.n_kvh;
+    if (G <= 1) launch_split<SK, SLK, SLV, 1>(A, prep, part, n_runs, s);
+    else if (G <= 2) launch_split<SK, SLK, SLV, 2>(A, prep, part, n_runs, s);
+    else if (G <= 4) launch_split<SK, SLK, SLV, 4>(A, prep, part, n_runs, s);
+    else launch_split<SK, SLK, SLV, 8>(A, prep, part, n_runs, s);
+}
+
+template <class SL>
+bool bands_are(const SpPlan &P) {
+    if (P.n_bands != SL::nb || P.total_bytes != SL::total) return false;
+    for (int b = 0; b < SL::nb; b++)
+        if (P.band_bits[b] != SL::bits[b] || P.band_off[b] != SL::off(b) || P.band_sz[b] != SL::sz(b)) return false;
+    return true;
+}
+
+}  // namespace
+
+// Which split kernel serves this cache geometry (0: none).
+int sp_sqfree_attn_kind(const SpPlan &KP, const SpPlan &VP, const SpSqGeo &G) {
+    if (!G.default_tables || G.hd != 128 || G.pad != PAD || G.rbits != RBITS || !G.spinor) return 0;
+    if (G.sk_k == 77 && bands_are<SkelL77>(KP) && bands_are<SkelL77>(VP)) return 1;
+    if (G.sk_k == 115 && bands_are<SkelL115>(KP) && bands_are<SkelL115>(VP)) return 2;
+    if (G.sk_k == 115 && bands_are<SkelL115>(KP) && bands_are<SkelL115V3>(VP)) return 3;
+    return 0;
+}
+
+// Runs per KV head: every run gets at least one tile and the blocks that are
+// resident at once (six one-wave blocks per CU) spread over the KV heads.
+int sp_sqfree_attn_runs(int n_kvh, int n_kv, int cus) {
+    const int tpo = (n_kv + 63) / 64;
+    const int per_head = std::max(1, (6 * cus) / std::max(1, n_kvh));
+    return std::max(1, std::min(std::min(tpo, per_head), 1024));
+}
+
+hipError_t sp_launch_sqfree_attn(const SpPlan &KP, const SpPlan &VP, const SpSqGeo &G, const SpHierAttnArgs &HA,
+                                 const SpSqAttnArgs &A, float *ws, size_t ws_floats, int n_runs, hipStream_t s) {
+    const int kind = sp_sqfree_attn_kind(KP, VP, G);
+    if (!kind || A.n_kv <= 0 || A.n_q <= 0 || A.n_kvh <= 0 || A.n_q % A.n_kvh || A.n_q / A.n_kvh > 8 ||
+        n_runs <= 0 || n_runs > 1024 || A.pp < 4 + PAD || A.ps != HA.ps || A.pp != HA.pp)
+        return hipErrorInvalidValue;
+    if (sp_hier_attn_workspace_floats(HA, n_runs) > ws_floats) return hipErrorInvalidValue;
+    float *prep = ws;
+    float *part = ws + (size_t)A.n_q * A.ps;
+    hipError_t e = sp_launch_hier_attn_prep(KP, HA, prep, s);
+    if (e != hipSuccess) return e;
+    if (kind == 1) launch_split_g<77, SkelL77, SkelL77>(A, prep, part, n_runs, s);
+    else if (kind == 2) launch_split_g<115, SkelL115, SkelL115>(A, prep, part, n_runs, s);
+    else launch_split_g<115, SkelL115, SkelL115V3>(A, prep, part, n_runs, s);
+    e = hipGetLastError();
+    if (e != hipSuccess || !A.out) return e;
+    return sp_launch_hier_attn_merge(KP, HA, part, n_runs, s);
+}
