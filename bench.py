@@ -198,6 +198,31 @@ def bench_variants(torch, S, L, stream, reps=3):
         "v_dec": rate(n3, hd3, vB3, timed(lambda: S.check(L.sp_hip_read_all(c3.ref, 0, N3, None, P(y), S.DTYPE_F16, -1)))),
         "record_bytes": [kB3, vB3]}
     c3.free()
+    # configs[2] decode: the same 16 sequences x 4096 cells, one sequence per cache layer (32 heads,
+    # MHA), fused decompress-attention for every sequence of one layer step (16 calls, 32 query heads
+    # each) through the general kernel (hd 96: Vilenkin 2^5*3)
+    NS3, NP3 = 16, 4096
+    c3d = S.ShipCache(S.config(hd3, NS3, H3, k_bits=(5, 4, 4), v_bits=(5,)), NP3, stream.cuda_stream)
+    xs = x.view(H3, NS3, NP3, hd3).transpose(0, 1).contiguous()  # [sequence][head][cell][d]
+    S.check(L.sp_hip_write_all(c3d.ref, 0, NP3, P(xs), P(xs), S.DTYPE_F16), "cfg2 prefill")
+    del xs
+    q3 = torch.randn((NS3, H3, hd3), generator=g, device="cuda")
+    o3 = torch.empty((NS3, H3, hd3), device="cuda")
+    sc3 = C.c_float(1.0 / math.sqrt(hd3))
+
+    def dec16():
+        for sq in range(NS3):
+            S.check(L.sp_hip_attn_decode(c3d.ref, sq, NP3, P(q3[sq]), H3, sc3, None, P(o3[sq]), sp), "cfg2 attn")
+    t16 = timed(dec16)
+    rec3 = NS3 * H3 * NP3 * (kB3 + vB3)
+    out["cfg3_hd96_decode"] = {
+        "step_layer_us": round(t16 * 1e6, 1), "us_per_token_32_layers": round(32 * t16 * 1e6, 1),
+        "decode_tokens_per_s": round(NS3 / (32 * t16), 1), "record_gbs": round(rec3 / t16 / 1e9, 1),
+        "record_floor_us": round(rec3 / (HBM_PEAK_GBS * 1e3), 1),
+        "fp16_floor_us": round(NS3 * H3 * NP3 * 2 * hd3 * 2 / (HBM_PEAK_GBS * 1e3), 1),
+        "layout": f"{NS3} sequences x {NP3} positions x {H3} heads (MHA), hd {hd3}, K 5/4/4 + V 5 records "
+                  f"({kB3} + {vB3} B); per layer step: {NS3} fused attention calls (general kernel)"}
+    c3d.free()
     del x, y
     # configs[1] post-decode hook on the device: sp_hip_roundtrip_cells over one layer's 8 heads,
     # K as cache rows and V transposed (v_trans), for a 1-token decode step and a 2048-cell prefill chunk
@@ -307,29 +332,66 @@ def bench_variants(torch, S, L, stream, reps=3):
     cd.free()
     c1.free()
     del kt, vt, krow, vrow, ko, vo
-    # sqfree+spinor, 12 layers x 4 KV heads x 65536 cells (4 x 16384), hd 128 -> pad 154
+    # sqfree+spinor, 12 layers x 4 KV heads x 65536 cells (4 x 16384), hd 128 -> pad 154,
+    # skeleton 0.75 * 154 = 115, K 5/4/4/4/5, V one 3-bit band (as configs[3] asks; the reference hook
+    # mirrors K's bands into V instead), 3-bit residuals
     L4, H4, N4 = 12, 4, 65536
     bits4 = (5, 4, 4, 4, 5)
-    cfg = S.config(128, L4, H4, k_bits=bits4, v_bits=bits4)
+    cfg = S.config(128, L4, H4, k_bits=bits4, v_bits=(3,))
     pad4 = L.sp_sqfree_pad_dim(128)
     c4 = S.SqfreeCache(cfg, N4, rbits=3, spinor=True, sk_k=int(pad4 * 0.75), stream=stream.cuda_stream)
     # rows in llama.cpp's cache layout: [layer][cell][head * hd + d]; one launch per layer and side
     x = (torch.randn((L4, N4, H4 * 128), generator=g, device="cuda")).half()
     y = torch.empty_like(x)
-    B4 = c4.c.bytes_per_pos_k
+    B4, B4v = c4.c.bytes_per_pos_k, c4.c.bytes_per_pos_v
 
-    def sq_write():
-        for layer in range(L4):
-            S.check(L.sp_hip_sqfree_write_layer(c4.ref, layer, 0, N4, P(x[layer]), None, H4 * 128, S.DTYPE_F16))
+    def sq_call(fn, is_v, buf):
+        def f():
+            for layer in range(L4):
+                a, b = (None, P(buf[layer])) if is_v else (P(buf[layer]), None)
+                S.check(fn(c4.ref, layer, 0, N4, a, b, H4 * 128, S.DTYPE_F16))
+        return f
 
-    def sq_read():
-        for layer in range(L4):
-            S.check(L.sp_hip_sqfree_read_layer(c4.ref, layer, 0, N4, P(y[layer]), None, H4 * 128, S.DTYPE_F16))
+    nv4 = L4 * H4 * N4
+    r_ke = rate(nv4, 128, B4, timed(sq_call(L.sp_hip_sqfree_write_layer, 0, x)))
+    r_ve = rate(nv4, 128, B4v, timed(sq_call(L.sp_hip_sqfree_write_layer, 1, x)))
+    r_kd = rate(nv4, 128, B4, timed(sq_call(L.sp_hip_sqfree_read_layer, 0, y)))
+    r_vd = rate(nv4, 128, B4v, timed(sq_call(L.sp_hip_sqfree_read_layer, 1, y)))
+    out["cfg4_sqfree_spinor"] = {"enc": r_ke, "dec": r_kd, "v_enc": r_ve, "v_dec": r_vd,
+                                 "record_bytes": [B4, B4v], "pad_dim": pad4, "skeleton": c4.c.sk_k,
+                                 "calls": f"{L4} layers x {H4} heads x {N4} positions, one call per layer and side "
+                                          f"(enc/dec: K 5/4/4/4/5; v_enc/v_dec: V one 3-bit band)"}
+    # configs[3] decode: fused attention over the sqfree records, batch 4 (layers 0-3 of the cache
+    # above are the four sequences; each holds 4 KV heads x 16384 positions of K and V), 32 query heads
+    # per sequence (GQA 8)
+    NA4, NQ4, NB4 = 16384, 32, 4
+    c4a = S.SqfreeCache(S.config(128, NB4, H4, k_bits=bits4, v_bits=(3,)), NA4, rbits=3, spinor=True,
+                        sk_k=int(pad4 * 0.75), stream=stream.cuda_stream)
+    for sq in range(NB4):
+        S.check(L.sp_hip_sqfree_write_layer(c4a.ref, sq, 0, NA4, P(x[sq, :NA4]), P(x[sq, NA4:2 * NA4]), H4 * 128,
+                                            S.DTYPE_F16))
+    q4 = torch.randn((NB4, NQ4, 128), generator=g, device="cuda")
+    o4 = torch.empty((NB4, NQ4, 128), device="cuda")
+    s4 = torch.empty((NQ4, NA4), device="cuda")
+    sc4 = C.c_float(1.0 / math.sqrt(128))
+    t_one = timed(lambda: S.check(L.sp_hip_sqfree_attn_decode(c4a.ref, 0, NA4, P(q4[0]), NQ4, sc4, None, P(o4[0]),
+                                                              sp)))
+    t_kq4 = timed(lambda: S.check(L.sp_hip_sqfree_attn_decode(c4a.ref, 0, NA4, P(q4[0]), NQ4, sc4, P(s4), None, sp)))
 
-    out["cfg4_sqfree_spinor"] = {"enc": rate(L4 * H4 * N4, 128, B4, timed(sq_write)),
-                                 "dec": rate(L4 * H4 * N4, 128, B4, timed(sq_read)),
-                                 "record_bytes": B4, "pad_dim": pad4, "skeleton": c4.c.sk_k,
-                                 "calls": f"{L4} layers x {H4} heads x {N4} positions, one call per layer (K)"}
+    def dec4():
+        for sq in range(NB4):
+            S.check(L.sp_hip_sqfree_attn_decode(c4a.ref, sq, NA4, P(q4[sq]), NQ4, sc4, None, P(o4[sq]), sp))
+    t_b4 = timed(dec4)
+    rec4 = H4 * NA4 * (B4 + B4v)
+    out["cfg4_sqfree_fused_attn"] = {
+        "layer_us": round(t_one * 1e6, 1), "kq_only_layer_us": round(t_kq4 * 1e6, 1),
+        "batch4_step_layer_us": round(t_b4 * 1e6, 1), "us_per_step_48_layers": round(48 * t_b4 * 1e6, 1),
+        "decode_tokens_per_s_48_layers": round(NB4 / (48 * t_b4), 1),
+        "record_gbs": round(rec4 / t_one / 1e9, 1), "record_floor_us": round(rec4 / (HBM_PEAK_GBS * 1e3), 2),
+        "fp16_layer_floor_us": round(H4 * NA4 * 2 * 128 * 2 / (HBM_PEAK_GBS * 1e3), 2),
+        "layout": f"{H4} KV heads x {NA4} positions, {NQ4} query heads (GQA 8), K {B4} B + V {B4v} B records "
+                  f"(pad {pad4}, skeleton {c4a.c.sk_k}); layer_us per sequence, batch4_step = {NB4} calls"}
+    c4a.free()
     c4.free()
     del x, y
     # hier, hd 256 -> pad 330, 8 KV heads x (8 x 131072) cells of one layer in one launch per side
@@ -380,19 +442,23 @@ def bench_variants(torch, S, L, stream, reps=3):
                                ("read_k", lambda i: L.sp_llama_read_k(ctx, 1, i % 8, i, fp(outv))),
                                ("read_v", lambda i: L.sp_llama_read_v(ctx, 1, i % 8, i, fp(outv)))):
                 # the first calls load each kernel's code object (records at odd positions of a
-                # 50 B V record are not 16 B aligned and take the row kernel): keep them untimed
-                for i in range(8):
+                # 50 B V record are not 16 B aligned and take the row kernel) and allocate the
+                # staging buffers: 64 untimed calls, then the median of individually timed ones
+                for i in range(64):
                     call(i)
-                t0 = time.perf_counter()
+                per = []
                 for i in range(n_calls):
+                    t0 = time.perf_counter()
                     call(i)
-                times[name] = (time.perf_counter() - t0) / n_calls * 1e6
+                    per.append(time.perf_counter() - t0)
+                times[name] = float(np.median(per)) * 1e6
             L.sp_llama_free(ctx)
             per_tok = 32 * 8 * (times["write_k"] + times["write_v"] + times["read_k"] + times["read_v"])
             out["cfg1_hook_per_vector"] = {
-                "us_per_call": {k: round(v, 2) for k, v in times.items()},
+                "us_per_call_median": {k: round(v, 2) for k, v in times.items()},
                 "us_per_token_32x8_write_and_read": round(per_tok, 1),
-                "layout": "bridge backend hip, hd 128, one fp32 vector per call (host pointer), synchronous"}
+                "layout": "bridge backend hip, hd 128, one fp32 vector per call (host pointer), synchronous; "
+                          "steady state: median of 256 calls after 64 untimed"}
     finally:
         for k, v in saved.items():
             if v is None:

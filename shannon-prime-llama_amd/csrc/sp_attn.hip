@@ -17,6 +17,8 @@
 //                     GQA group.
 //   3. k_attn_combine: merge splits (log-sum-exp), one inverse VHT2 per head.
 // No full-precision K or V is materialized anywhere.
+#include <stdlib.h>
+
 #include "sp_internal.h"
 
 
@@ -253,6 +255,23 @@ hipError_t sp_launch_attn_decode(const SpPlan &KP, const SpPlan &VP, const int *
         const hipError_t we = sp_launch_attn_wave(
             KP, VP, order, A, part, ws_floats - (size_t)A.n_q * A.hd - SP_ATTN_COUNTERS - SP_ATTN_COUNTER_STRIDE, cnt, s);
         if (we != hipErrorNotSupported) return we;
+    }
+    {
+        // hd 96 / hd 64 shipping layouts: the one-position-per-lane split kernel
+        // (sp_attn_lane.hip) between the same query preparation and combine
+        // (SP_HIP_NO_LANE_ATTN=1, read at each call, keeps them on the kernel below)
+        const char *off = getenv("SP_HIP_NO_LANE_ATTN");
+        const size_t part_floats = ws_floats - (size_t)A.n_q * A.hd - SP_ATTN_COUNTERS - SP_ATTN_COUNTER_STRIDE;
+        const int n_runs = (off && off[0] == '1') ? 0 : sp_attn_lane_runs(KP, VP, A, part_floats);
+        if (n_runs > 0) {
+            hipLaunchKernelGGL(k_attn_prep, dim3(A.n_q), dim3(64), 0, s, KP, order, A.q, A.hd, A.kq_scale, qt);
+            const hipError_t le = sp_launch_attn_lane_split(KP, VP, A, qt, part, n_runs, s);
+            if (le != hipSuccess) return le;
+            if (want_out)
+                hipLaunchKernelGGL(k_attn_combine, dim3(A.n_q), dim3(COMB_THREADS), 0, s, VP, part, n_runs, A.hd,
+                                   A.out);
+            return hipGetLastError();
+        }
     }
     hipLaunchKernelGGL(k_attn_prep, dim3(A.n_q), dim3(64), 0, s, KP, order, A.q, A.hd, A.kq_scale, qt);
     const size_t lds = (size_t)((ATT_CHUNK * A.kB + 8 + 15) & ~15) + (size_t)ATT_CHUNK * A.vB + 8;

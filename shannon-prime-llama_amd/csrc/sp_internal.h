@@ -329,6 +329,12 @@ hipError_t sp_launch_attn_decode(const SpPlan &KP, const SpPlan &VP, const int *
                                  const SpAttnArgs &A, float *workspace, size_t ws_floats,
                                  hipStream_t s);
 size_t sp_attn_workspace_floats(int n_q, int hd, int max_kv);
+// One-position-per-lane split kernel for the hd 96 (K 5/4/4, V 5) and hd 64 (K 5/5/4/3,
+// V 3) layouts (sp_attn_lane.hip): runs per KV head that fit part_floats (0: no lane
+// kernel for these layouts), and the launch writing [m, l, o~[hd]] per (query head, run).
+int sp_attn_lane_runs(const SpPlan &KP, const SpPlan &VP, const SpAttnArgs &A, size_t part_floats);
+hipError_t sp_launch_attn_lane_split(const SpPlan &KP, const SpPlan &VP, const SpAttnArgs &A, const float *qt,
+                                     float *part, int n_runs, hipStream_t s);
 // Checks the arguments of a decode-attention call on one layer of a ship cache
 // and fills its launch arguments and K/V plans (band limit applied); -1 with the
 // error message set for bad arguments (sp_runtime.cpp).

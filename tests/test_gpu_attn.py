@@ -54,15 +54,22 @@ ATTN_CASES = [
 ]
 
 
-@pytest.mark.parametrize("path", ["mfma", "general"])
+def general_kernel_only(monkeypatch):
+    """Route decode attention to the general kernel (sp_attn.hip's split kernel)."""
+    monkeypatch.setenv("SP_HIP_NO_MFMA_ATTN", "1")
+    monkeypatch.setenv("SP_HIP_NO_LANE_ATTN", "1")
+
+
+@pytest.mark.parametrize("path", ["default", "general"])
 @pytest.mark.parametrize("n_q,H,n_ctx,hd,mob", ATTN_CASES)
 def test_fused_attention_matches_oracle(n_q, H, n_ctx, hd, mob, path, monkeypatch):
-    """hd 128 with K 5/5/4/3 and V 3-bit runs the matrix-core kernel unless
-    SP_HIP_NO_MFMA_ATTN=1 routes it to the general one; both meet 1e-3."""
+    """The default launch runs the matrix-core kernel at hd 128 (K 5/5/4/3, V 3-bit),
+    the one-position-per-lane kernel at hd 64 and the general kernel at hd 256;
+    path "general" forces the general kernel everywhere. All meet 1e-3."""
     if path == "general":
-        monkeypatch.setenv("SP_HIP_NO_MFMA_ATTN", "1")
-    elif hd != 128:
-        pytest.skip("matrix-core kernel covers head_dim 128 only")
+        general_kernel_only(monkeypatch)
+    elif hd == 256:
+        pytest.skip("the default launch at head_dim 256 is the general kernel (path general)")
     say(f"attn path={path} n_q={n_q} H={H} n_ctx={n_ctx} hd={hd} mob={mob}")
     k16, v16 = W.cfg2_kv(n_heads=H, n_pos=n_ctx, hd=hd, seed=n_ctx)
     q = W.cfg2_q(n_q=n_q, hd=hd, pos=n_ctx, seed=n_ctx + 1)
@@ -95,15 +102,25 @@ def test_fused_attention_matches_oracle(n_q, H, n_ctx, hd, mob, path, monkeypatc
     cc.free()
 
 
-@pytest.mark.parametrize("n_q,H,n_ctx,k_bits,v_bits", [
-    (32, 32, 300, (5, 4, 4), (5,)),      # configs[2] (Phi-3-mini, MHA) at the bridge's hd-96 bands
-    (16, 4, 1037, (5, 5, 4, 3), (3,)),   # the shipping bands at hd 96, GQA 4
+@pytest.mark.parametrize("path", ["default", "general"])
+@pytest.mark.parametrize("n_q,H,n_ctx,k_bits,v_bits,runs", [
+    (32, 32, 300, (5, 4, 4), (5,), 0),      # configs[2] (Phi-3-mini, MHA) at the bridge's hd-96 bands
+    (32, 32, 4096, (5, 4, 4), (5,), 0),     # configs[2]'s per-sequence shape: 64 tiles per head
+    (16, 4, 3000, (5, 4, 4), (5,), 3),      # GQA 4, runs of 15-16 tiles, a ragged last tile
+    (24, 8, 777, (5, 4, 4), (5,), 0),       # GQA 3
+    (16, 4, 1037, (5, 5, 4, 3), (3,), 0),   # the shipping bands at hd 96, GQA 4 (general kernel only)
 ])
-def test_hd96_attention_matches_oracle(n_q, H, n_ctx, k_bits, v_bits):
-    """head_dim 96 (Vilenkin 2^5 * 3) through the general kernel: scores and output
-    within 1e-3 of the oracle, several splits and a ragged last one."""
+def test_hd96_attention_matches_oracle(n_q, H, n_ctx, k_bits, v_bits, runs, path, monkeypatch):
+    """head_dim 96 (Vilenkin 2^5 * 3): the bridge's bands (K 5/4/4 + Mobius, V 5) run
+    the one-position-per-lane kernel by default, other bands the general kernel;
+    scores and output within 1e-3 of the oracle, several splits or runs and a ragged
+    last tile."""
     hd = 96
-    say(f"attn hd96 n_q={n_q} H={H} n_ctx={n_ctx} k={k_bits} v={v_bits}")
+    if path == "general":
+        general_kernel_only(monkeypatch)
+    if runs:
+        monkeypatch.setenv("SP_HIP_ATTN_LANE_RUNS", str(runs))
+    say(f"attn hd96 path={path} n_q={n_q} H={H} n_ctx={n_ctx} k={k_bits} v={v_bits}")
     k16, v16 = W.cfg3_kv(n_heads=H, n_pos=n_ctx, hd=hd, seed=n_ctx)
     q = W.cfg2_q(n_q=n_q, hd=hd, pos=n_ctx, seed=n_ctx + 1)
     cfg = S.config(hd, 1, H, k_bits=k_bits, v_bits=v_bits)
@@ -125,6 +142,14 @@ def test_hd96_attention_matches_oracle(n_q, H, n_ctx, k_bits, v_bits):
     torch.cuda.synchronize()
     rel_close(host(sc).reshape(n_q, n_ctx), s_ref)
     rel_close(host(out).reshape(n_q, hd), o_ref)
+    # band limits: K and V bands >= max_bands read as 0
+    for mb in (2, 1):
+        s_b, o_b = O.attn_decode(q, kref, vref, H, n_ctx, kbc, vbc, order, scale, max_bands=mb)
+        sc, out = empty_f32(n_q * n_ctx), empty_f32(n_q * hd)
+        S.check(S.lib().sp_hip_attn_decode_bands(cc.ref, 0, n_ctx, p(qt), n_q, C.c_float(scale), p(sc), p(out), mb,
+                                                 stream()))
+        rel_close(host(sc).reshape(n_q, n_ctx), s_b)
+        rel_close(host(out).reshape(n_q, hd), o_b)
     cc.free()
 
 
@@ -135,7 +160,7 @@ def test_band_limited_attention_matches_oracle(n_q, H, n_ctx, path, monkeypatch)
     over the partial reconstructions (1e-3); a limit of 4 or -1 equals the full call
     bit for bit."""
     if path == "general":
-        monkeypatch.setenv("SP_HIP_NO_MFMA_ATTN", "1")
+        general_kernel_only(monkeypatch)
     hd = 128
     k16, v16 = W.cfg2_kv(n_heads=H, n_pos=n_ctx, hd=hd, seed=n_ctx + 3)
     q = W.cfg2_q(n_q=n_q, hd=hd, pos=n_ctx, seed=n_ctx + 4)
