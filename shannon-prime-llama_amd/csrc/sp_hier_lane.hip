@@ -33,14 +33,6 @@ struct HierGeoC {
 template <int PAD, int NS>
 __device__ constexpr HierGeoC<PAD, NS> kHier{};
 
-template <int NT, int RBITS, class SL>
-struct HierRec {
-    static constexpr int mag_byte = SL::total;
-    static constexpr int res_bit = 8 * (SL::total + 4);
-    static constexpr int total = SL::total + 4 + (NT * RBITS + 7) / 8;
-    static constexpr int dwords = (total + 3) / 4;
-};
-
 // Two predictions at once: a0 += w0.lo*x0, a1 += w1.lo*x0, a0 += w0.hi*x1,
 // a1 += w1.hi*x1, each step rounded once. v_fma_mix widens the fp16 weight (from
 // a scalar register) exactly and rounds w*x + 0 (the + 0 turns a -0 product into

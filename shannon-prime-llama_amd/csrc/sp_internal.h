@@ -236,6 +236,14 @@ hipError_t sp_launch_hier_attn_prep(const SpPlan &P, const SpHierAttnArgs &A, fl
 hipError_t sp_launch_hier_attn_merge(const SpPlan &P, const SpHierAttnArgs &A, const float *part, int n_runs,
                                      hipStream_t s);
 
+// One-position-per-lane split kernel of the hier attention (sp_hier_attn_lane.hip) for
+// hd 256 / pad 330 / skeleton 30 at 5/5 bits / 300 targets at 2 bits: whether it serves
+// the call, its runs per KV head, and prep + split + merge.
+bool sp_hier_attn_lane_ok(const SpPlan &P, const SpHierAttnArgs &A);
+int sp_hier_attn_lane_runs(const SpHierAttnArgs &A, int cus);
+hipError_t sp_launch_hier_attn_lane(const SpPlan &P, const SpHierAttnArgs &A, float *ws, size_t ws_floats,
+                                    int n_runs, hipStream_t s);
+
 // Fused decode attention over sqfree+spinor records (sp_sqfree_attn.hip): the split
 // kernel's arguments (records of slot (layer, KV head 0), KV head h at + h * slot bytes).
 struct SpSqAttnArgs {

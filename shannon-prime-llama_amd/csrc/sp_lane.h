@@ -720,6 +720,16 @@ __device__ __forceinline__ void tile_rows_out(const float (&x)[N], unsigned char
     }
 }
 
+// Hier record [skeleton bands][mag f32 LE][NT residual levels, LSB-first]
+// (shannon_prime_hier.cu:331-335), for skeleton band layout SL.
+template <int NT, int RBITS, class SL>
+struct HierRec {
+    static constexpr int mag_byte = SL::total;
+    static constexpr int res_bit = 8 * (SL::total + 4);
+    static constexpr int total = SL::total + 4 + (NT * RBITS + 7) / 8;
+    static constexpr int dwords = (total + 3) / 4;
+};
+
 // ---- host side ----
 // Persistent grid size: enough single-wave blocks for several resident waves
 // per SIMD on every CU (queried once per process).

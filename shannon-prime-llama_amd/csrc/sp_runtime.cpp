@@ -1532,9 +1532,18 @@ extern "C" int sp_hip_hier_attn_decode(const sp_hip_hier_cache_t *hc, int layer,
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
         cus = 256;
-    int n_runs = sp_hier_attn_runs(A, cus);
+    // The 256-position chunk kernel serves every geometry up to its LDS limit (at pad 330,
+    // at most 4 query heads per KV head). Past it, the one-position-per-lane split kernel
+    // serves the configs[4] geometry (hd 256, pad 330, skeleton 30 at 5/5 bits, 300 targets
+    // at 2 bits) with up to 8; it is the slower of the two where both fit (measured at
+    // 189 vs 169 us per layer), and SP_HIP_HIER_ATTN_LANE=1 (read at each call)
+    // selects it wherever it fits, for tests.
+    const char *lane_on = getenv("SP_HIP_HIER_ATTN_LANE");
+    const bool lane = sp_hier_attn_lane_ok(pv->plan, A) &&
+                      ((lane_on && lane_on[0] == '1') || (A.pad == 330 && n_q / H > 4));
+    int n_runs = lane ? sp_hier_attn_lane_runs(A, cus) : sp_hier_attn_runs(A, cus);
     // SP_HIP_HIER_ATTN_RUNS=n caps the runs per KV head (read at each call; tests use it to
-    // give every run several chunks at small context lengths)
+    // give every run several chunks or tiles at small context lengths)
     if (const char *e = getenv("SP_HIP_HIER_ATTN_RUNS")) {
         const int r = atoi(e);
         if (r > 0) n_runs = std::min(n_runs, r);
@@ -1551,6 +1560,9 @@ extern "C" int sp_hip_hier_attn_decode(const sp_hip_hier_cache_t *hc, int layer,
         if (!hip_ok(hipMalloc((void **)&pv->d_attn_ws, need * sizeof(float)), "hipMalloc hier attn workspace")) return -1;
         pv->attn_ws_floats = need;
     }
+    if (lane)
+        return hip_ok(sp_launch_hier_attn_lane(pv->plan, A, pv->d_attn_ws, pv->attn_ws_floats, n_runs, s),
+                      "hier attn (lane)") ? 0 : -1;
     return hip_ok(sp_launch_hier_attn(pv->plan, A, pv->d_attn_ws, pv->attn_ws_floats, n_runs, s), "hier attn") ? 0 : -1;
 }
 

@@ -52,13 +52,17 @@ def _hier_cache(hd, rbits, skel_bits, H, n_kv, seed, layers=2):
 
 
 CASES = [
-    # hd, rbits, skeleton bands, H, n_q, n_kv, runs cap
+    # hd, rbits, skeleton bands, H, n_q, n_kv, runs cap (chunks of 256 positions for the
+    # chunk kernel, tiles of 64 for the lane kernel)
     (256, 2, [5, 5], 2, 4, 300, 0),     # configs[4] geometry, GQA 2, a partial second chunk
     (256, 2, [5, 5], 2, 4, 1100, 2),    # two runs of 2-3 chunks each: online softmax across chunks
     (64, 3, [5, 4], 2, 2, 517, 1),      # pad 66, 3-bit levels straddling bytes, one run of 3 chunks
     (96, 2, [4], 2, 6, 257, 0),         # pad 105, GQA 3 (odd: a lone last head), 1-position last chunk
     (256, 2, [5, 5], 1, 1, 1, 0),       # a single position
     (256, 2, [5, 5], 8, 16, 2000, 3),   # configs[4] head layout (8 KV heads, GQA 2), 3 runs of 2-3 chunks
+    (256, 2, [5, 5], 2, 8, 700, 2),     # GQA 4: two head pairs per window item
+    (256, 2, [5, 5], 1, 8, 333, 0),     # GQA 8: window and skeleton items in two rounds per lane
+    (256, 2, [5, 5], 2, 6, 260, 1),     # GQA 3: a pair with one real head
     # the bench's run sizing (no cap): three resident blocks per CU spread over the KV
     # heads, so more than 48 runs per head and the merge sums them in several passes
     (256, 2, [5, 5], 8, 16, 25000, 0),  # configs[4] head layout: 96 runs per head (98 chunks)
@@ -69,11 +73,21 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("path", ["default", "lane"])
 @pytest.mark.parametrize("hd,rbits,skel_bits,H,n_q,n_kv,runs", CASES)
-def test_hier_attention_matches_oracle(hd, rbits, skel_bits, H, n_q, n_kv, runs, monkeypatch):
+def test_hier_attention_matches_oracle(hd, rbits, skel_bits, H, n_q, n_kv, runs, path, monkeypatch):
+    """The default launch runs the 256-position chunk kernel, and past its LDS limit
+    (more than 4 query heads per KV head at pad 330) the one-position-per-lane split
+    kernel of the configs[4] geometry (hd 256, skeleton 5/5, 2-bit targets); path "lane"
+    selects the lane kernel wherever it fits (SP_HIP_HIER_ATTN_LANE=1)."""
+    lane_geo = hd == 256 and rbits == 2 and list(skel_bits) == [5, 5]
+    if path == "lane":
+        if not lane_geo:
+            pytest.skip("the lane kernel serves the configs[4] geometry only")
+        monkeypatch.setenv("SP_HIP_HIER_ATTN_LANE", "1")
     if runs:
         monkeypatch.setenv("SP_HIP_HIER_ATTN_RUNS", str(runs))
-    say(f"hier attn hd={hd} rbits={rbits} bands={skel_bits} H={H} n_q={n_q} n_kv={n_kv} runs={runs}")
+    say(f"hier attn path={path} hd={hd} rbits={rbits} bands={skel_bits} H={H} n_q={n_q} n_kv={n_kv} runs={runs}")
     hc, (pad, sk, tg, bc, Wl), kp, vp = _hier_cache(hd, rbits, skel_bits, H, n_kv, seed=hd + n_kv)
     q = W.cfg2_q(n_q=n_q, hd=hd, pos=n_kv, seed=n_kv + 7)
     scale = 1.0 / math.sqrt(hd)
