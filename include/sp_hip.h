@@ -207,6 +207,22 @@ int sp_hip_attn_decode_bands_noalloc(const sp_hip_cache_t *cc, int layer, int n_
                                      float *d_scores, float *d_out, int max_bands, void *stream);
 size_t sp_hip_attn_noalloc_max_floats(void);
 
+/* Batched decode attention: n_seq sequences (1..64) of one layer in one launch sequence.
+ * No counterpart in the reference, whose fused op (llama_sp_kq_compute,
+ * llama_sp_fused_kq.cpp:83-165) runs one sequence per graph node; this is the same
+ * contract for llama.cpp's unified cache holding several sequences, each a range of
+ * cells. Sequence s attends positions [seq_start[s], seq_start[s] + seq_len[s]) of every
+ * KV head (host arrays; ranges inside [0, max_seq_len), non-empty, may overlap) with its
+ * own queries d_q[s] ([n_seq][n_q][head_dim] fp32): d_out [n_seq][n_q][head_dim] and
+ * d_scores, sequence s's [n_q][seq_len[s]] block starting at element
+ * n_q * (seq_len[0] + ... + seq_len[s-1]). Results equal n_seq separate calls over those
+ * ranges. The hd 96 (K 5/4/4, V 5) and hd 64 (K 5/5/4/3, V 3) layouts run every sequence
+ * in one launch each of the query preparation, the split kernel and the combine (workspace
+ * grown on demand); other layouts run the single-sequence kernels once per sequence. */
+int sp_hip_attn_decode_seqs(const sp_hip_cache_t *cc, int layer, int n_seq, const int *seq_start,
+                            const int *seq_len, const float *d_q, int n_q, float kq_scale, float *d_scores,
+                            float *d_out, void *stream);
+
 /* Memory report to stderr (sp_cuda_print_memory, shannon_prime_cuda.h:140-141): the
  * records' MiB against an fp16 K+V cache of the same shape. */
 void sp_hip_print_memory(const sp_hip_cache_t *cc);
@@ -321,6 +337,12 @@ int sp_hip_sqfree_calibrate_end(sp_hip_sqfree_cache_t *cc, int *ranking_out, int
  * call and grown when a call needs more. 0 or -1. */
 int  sp_hip_sqfree_attn_decode(const sp_hip_sqfree_cache_t *cc, int layer, int n_kv, const float *d_q, int n_q,
                                float kq_scale, float *d_scores, float *d_out, void *stream);
+/* Batched form (the sequence, query, score and output layout of sp_hip_attn_decode_seqs):
+ * every sequence in one launch each of the query preparation, the split kernel and the
+ * merge. No counterpart in the reference. */
+int  sp_hip_sqfree_attn_decode_seqs(const sp_hip_sqfree_cache_t *cc, int layer, int n_seq, const int *seq_start,
+                                    const int *seq_len, const float *d_q, int n_q, float kq_scale,
+                                    float *d_scores, float *d_out, void *stream);
 /* Host copies of the Knight tables (for tests and calibration tools). */
 int  sp_hip_sqfree_get_tables(const sp_hip_sqfree_cache_t *cc, int *skeleton_idx,
                               int *residual_idx, int *csr_offsets, int *csr_skel_slot,
@@ -402,6 +424,13 @@ int  sp_hip_hier_read_layer(const sp_hip_hier_cache_t *hc, int layer, int start_
  * first call and grown when a call needs more. 0 or -1. */
 int  sp_hip_hier_attn_decode(const sp_hip_hier_cache_t *hc, int layer, int n_kv, const float *d_q, int n_q,
                              float kq_scale, float *d_scores, float *d_out, void *stream);
+/* Batched form (the sequence, query, score and output layout of sp_hip_attn_decode_seqs):
+ * the batch of a decode step in one launch each of the query preparation (n_seq * n_q
+ * blocks), the split kernel (grid: KV head x run x sequence) and the merge. No counterpart
+ * in the reference. */
+int  sp_hip_hier_attn_decode_seqs(const sp_hip_hier_cache_t *hc, int layer, int n_seq, const int *seq_start,
+                                  const int *seq_len, const float *d_q, int n_q, float kq_scale, float *d_scores,
+                                  float *d_out, void *stream);
 
 /* ======================================================================== */
 /* System 1/2 dual cache (DualKvCache, kv_cache.h:238-310,                  */

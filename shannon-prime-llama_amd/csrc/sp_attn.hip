@@ -231,6 +231,23 @@ k_attn_combine(const SpPlan VP, const float *__restrict__ ws, int n_splits, int 
         for (int k = tid; k < hd; k += SP_WAVE) out[(long long)h * hd + k] = c[k];
 }
 
+hipError_t sp_launch_attn_lane_seqs(const SpPlan &KP, const SpPlan &VP, const int *order, const SpAttnArgs &A,
+                                    const SpSeqTab &T, float *ws, size_t ws_floats, int n_runs, hipStream_t s) {
+    const size_t n_rows = (size_t)T.n_seq * A.n_q;
+    if (T.n_seq < 1 || T.n_seq > SP_ATTN_MAX_SEQ || n_runs <= 0 || n_runs > ATT_MAX_SPLITS ||
+        n_rows * A.hd + n_rows * n_runs * (A.hd + 2) > ws_floats)
+        return hipErrorInvalidValue;
+    float *qt = ws;
+    float *part = ws + n_rows * A.hd;
+    hipLaunchKernelGGL(k_attn_prep, dim3((unsigned)n_rows), dim3(64), 0, s, KP, order, A.q, A.hd, A.kq_scale, qt);
+    const hipError_t le = sp_launch_attn_lane_split(KP, VP, A, T, qt, part, n_runs, s);
+    if (le != hipSuccess) return le;
+    if (A.out)
+        hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)n_rows), dim3(COMB_THREADS), 0, s, VP, part, n_runs, A.hd,
+                           A.out);
+    return hipGetLastError();
+}
+
 size_t sp_attn_workspace_floats(int n_q, int hd, int max_kv) {
     const int n_splits = (max_kv + ATT_CHUNK - 1) / ATT_CHUNK;
     return (size_t)n_q * hd + (size_t)n_q * n_splits * (hd + 2) + SP_ATTN_COUNTERS + SP_ATTN_COUNTER_STRIDE;
@@ -264,13 +281,13 @@ hipError_t sp_launch_attn_decode(const SpPlan &KP, const SpPlan &VP, const int *
         const size_t part_floats = ws_floats - (size_t)A.n_q * A.hd - SP_ATTN_COUNTERS - SP_ATTN_COUNTER_STRIDE;
         const int n_runs = (off && off[0] == '1') ? 0 : sp_attn_lane_runs(KP, VP, A, part_floats);
         if (n_runs > 0) {
-            hipLaunchKernelGGL(k_attn_prep, dim3(A.n_q), dim3(64), 0, s, KP, order, A.q, A.hd, A.kq_scale, qt);
-            const hipError_t le = sp_launch_attn_lane_split(KP, VP, A, qt, part, n_runs, s);
-            if (le != hipSuccess) return le;
-            if (want_out)
-                hipLaunchKernelGGL(k_attn_combine, dim3(A.n_q), dim3(COMB_THREADS), 0, s, VP, part, n_runs, A.hd,
-                                   A.out);
-            return hipGetLastError();
+            SpSeqTab T;
+            T.n_seq = 1;
+            T.max_len = A.n_kv;
+            T.start[0] = 0;
+            T.len[0] = A.n_kv;
+            T.soff[0] = 0;
+            return sp_launch_attn_lane_seqs(KP, VP, order, A, T, workspace, ws_floats, n_runs, s);
         }
     }
     hipLaunchKernelGGL(k_attn_prep, dim3(A.n_q), dim3(64), 0, s, KP, order, A.q, A.hd, A.kq_scale, qt);

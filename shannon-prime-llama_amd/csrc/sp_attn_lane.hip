@@ -35,9 +35,9 @@ __device__ __forceinline__ float wadd(float v) {
 // queries [n_q][hd] (record order). K bands >= kmb and V bands >= vmb read as 0.
 template <class LK, class LV, int GM, bool OUT>
 __global__ void __launch_bounds__(64)
-k_attn_lane_split(const unsigned char *__restrict__ kc, const unsigned char *__restrict__ vc, long long k_slot,
-                  long long v_slot, int n_kv, int G, const float *__restrict__ qt, float *__restrict__ scores,
-                  float *__restrict__ part, int n_runs, int kmb, int vmb) {
+k_attn_lane_split(const unsigned char *__restrict__ kc0, const unsigned char *__restrict__ vc0, long long k_slot,
+                  long long v_slot, const SpSeqTab T, int G, const float *__restrict__ qt0, float *__restrict__ scores0,
+                  float *__restrict__ part0, int n_runs, int kmb, int vmb) {
     constexpr int HD = LK::hd;
     static_assert(LV::hd == HD, "K and V layouts share head_dim");
     constexpr int NCK = RecTile<LK>::NCK > RecTile<LV>::NCK ? RecTile<LK>::NCK : RecTile<LV>::NCK;
@@ -49,6 +49,14 @@ k_attn_lane_split(const unsigned char *__restrict__ kc, const unsigned char *__r
     __shared__ float E[64 * EP];
     __shared__ __attribute__((aligned(16))) float Pw[64 * GM];
     const int kvh = blockIdx.x, run = blockIdx.y, lane = threadIdx.x;
+    // sequence blockIdx.z: its positions, prepared queries, score rows and partials
+    const int seq = blockIdx.z, n_q = (int)gridDim.x * G, n_kv = T.len[seq];
+    const unsigned char *__restrict__ kc = kc0 + (long long)T.start[seq] * LK::total;
+    const unsigned char *__restrict__ vc = vc0 + (long long)T.start[seq] * LV::total;
+    const long long s_stride = T.len[seq];
+    float *__restrict__ scores = scores0 ? scores0 + T.soff[seq] : nullptr;
+    const float *__restrict__ qt = qt0 + (long long)seq * n_q * HD;
+    float *__restrict__ part = part0 + (long long)seq * n_q * n_runs * (HD + 2);
     const int h0 = kvh * G;
     const int tpo = (n_kv + 63) / 64;
     const int n_tiles = (int)gridDim.x * tpo;
@@ -101,7 +109,7 @@ k_attn_lane_split(const unsigned char *__restrict__ kc, const unsigned char *__r
                 const float v = a0 + a1;
                 if (live) {
                     s[h] = v;
-                    if (scores) scores[(long long)(h0 + h) * n_kv + pos] = v;
+                    if (scores) scores[(long long)(h0 + h) * s_stride + pos] = v;
                 }
             }
         }
@@ -187,24 +195,26 @@ k_attn_lane_split(const unsigned char *__restrict__ kc, const unsigned char *__r
 }
 
 template <class LK, class LV, int GM>
-void launch_lane(const SpAttnArgs &A, const float *qt, float *part, int n_runs, int kmb, int vmb, hipStream_t s) {
-    const dim3 grid(A.n_kvh, n_runs), block(64);
+void launch_lane(const SpAttnArgs &A, const SpSeqTab &T, const float *qt, float *part, int n_runs, int kmb, int vmb,
+                 hipStream_t s) {
+    const dim3 grid(A.n_kvh, n_runs, T.n_seq), block(64);
     const int G = A.n_q / A.n_kvh;
     if (A.out)
         hipLaunchKernelGGL((k_attn_lane_split<LK, LV, GM, true>), grid, block, 0, s, A.kpack, A.vpack,
-                           A.k_head_stride, A.v_head_stride, A.n_kv, G, qt, A.scores, part, n_runs, kmb, vmb);
+                           A.k_head_stride, A.v_head_stride, T, G, qt, A.scores, part, n_runs, kmb, vmb);
     else
         hipLaunchKernelGGL((k_attn_lane_split<LK, LV, GM, false>), grid, block, 0, s, A.kpack, A.vpack,
-                           A.k_head_stride, A.v_head_stride, A.n_kv, G, qt, A.scores, part, n_runs, kmb, vmb);
+                           A.k_head_stride, A.v_head_stride, T, G, qt, A.scores, part, n_runs, kmb, vmb);
 }
 
 template <class LK, class LV>
-void launch_lane_g(const SpAttnArgs &A, const float *qt, float *part, int n_runs, int kmb, int vmb, hipStream_t s) {
+void launch_lane_g(const SpAttnArgs &A, const SpSeqTab &T, const float *qt, float *part, int n_runs, int kmb, int vmb,
+                   hipStream_t s) {
     const int G = A.n_q / A.n_kvh;
-    if (G <= 1) launch_lane<LK, LV, 1>(A, qt, part, n_runs, kmb, vmb, s);
-    else if (G <= 2) launch_lane<LK, LV, 2>(A, qt, part, n_runs, kmb, vmb, s);
-    else if (G <= 4) launch_lane<LK, LV, 4>(A, qt, part, n_runs, kmb, vmb, s);
-    else launch_lane<LK, LV, 8>(A, qt, part, n_runs, kmb, vmb, s);
+    if (G <= 1) launch_lane<LK, LV, 1>(A, T, qt, part, n_runs, kmb, vmb, s);
+    else if (G <= 2) launch_lane<LK, LV, 2>(A, T, qt, part, n_runs, kmb, vmb, s);
+    else if (G <= 4) launch_lane<LK, LV, 4>(A, T, qt, part, n_runs, kmb, vmb, s);
+    else launch_lane<LK, LV, 8>(A, T, qt, part, n_runs, kmb, vmb, s);
 }
 
 template <class LY>
@@ -225,7 +235,7 @@ using V64 = Layout<64, 3>;
 // Runs per KV head for the lane split kernel: at most the workspace's partial rows,
 // at least one tile per run, and about six resident one-wave blocks per CU spread
 // over the KV heads. 0 when no lane kernel serves the call's layouts.
-int sp_attn_lane_runs(const SpPlan &KP, const SpPlan &VP, const SpAttnArgs &A, size_t part_floats) {
+int sp_attn_lane_runs(const SpPlan &KP, const SpPlan &VP, const SpAttnArgs &A, size_t part_floats, int n_seq) {
     const bool ok = (plan_is<K96>(KP) && plan_is<V96>(VP)) || (plan_is<K64>(KP) && plan_is<V64>(VP));
     if (!ok || A.n_q % A.n_kvh || A.n_q / A.n_kvh > 8) return 0;
     if (((uintptr_t)A.kpack % 4) || ((uintptr_t)A.vpack % 4) || (A.k_head_stride % 4) || (A.v_head_stride % 4))
@@ -238,8 +248,8 @@ int sp_attn_lane_runs(const SpPlan &KP, const SpPlan &VP, const SpAttnArgs &A, s
         cus = n;
     }
     const int tpo = (A.n_kv + 63) / 64;
-    const long long cap = (long long)(part_floats / ((size_t)A.n_q * (A.hd + 2)));
-    long long r = std::min<long long>(tpo, std::max(1, (6 * cus) / A.n_kvh));
+    const long long cap = (long long)(part_floats / ((size_t)n_seq * A.n_q * (A.hd + 2)));
+    long long r = std::min<long long>(tpo, std::max(1, (6 * cus) / (A.n_kvh * n_seq)));
     r = std::min<long long>(r, std::min<long long>(cap, 4096));
     // SP_HIP_ATTN_LANE_RUNS=n caps the runs per KV head (read at each call; tests use it
     // to give every run several tiles at small context lengths)
@@ -250,12 +260,13 @@ int sp_attn_lane_runs(const SpPlan &KP, const SpPlan &VP, const SpAttnArgs &A, s
     return r > 0 ? (int)r : 0;
 }
 
-hipError_t sp_launch_attn_lane_split(const SpPlan &KP, const SpPlan &VP, const SpAttnArgs &A, const float *qt,
-                                     float *part, int n_runs, hipStream_t s) {
-    if (n_runs <= 0) return hipErrorInvalidValue;
-    if (plan_is<K96>(KP) && plan_is<V96>(VP)) launch_lane_g<K96, V96>(A, qt, part, n_runs, KP.max_bands, VP.max_bands, s);
+hipError_t sp_launch_attn_lane_split(const SpPlan &KP, const SpPlan &VP, const SpAttnArgs &A, const SpSeqTab &T,
+                                     const float *qt, float *part, int n_runs, hipStream_t s) {
+    if (n_runs <= 0 || T.n_seq < 1 || T.n_seq > SP_ATTN_MAX_SEQ) return hipErrorInvalidValue;
+    if (plan_is<K96>(KP) && plan_is<V96>(VP))
+        launch_lane_g<K96, V96>(A, T, qt, part, n_runs, KP.max_bands, VP.max_bands, s);
     else if (plan_is<K64>(KP) && plan_is<V64>(VP))
-        launch_lane_g<K64, V64>(A, qt, part, n_runs, KP.max_bands, VP.max_bands, s);
+        launch_lane_g<K64, V64>(A, T, qt, part, n_runs, KP.max_bands, VP.max_bands, s);
     else return hipErrorNotSupported;
     return hipGetLastError();
 }

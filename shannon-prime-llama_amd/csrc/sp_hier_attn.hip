@@ -237,8 +237,8 @@ k_hier_attn_prep(const SpPlan P, const SpHierAttnArgs A, float *__restrict__ pre
     __shared__ float wsum[NT / SP_WAVE];
     __shared__ float cas_s[SP_CAS_TOTAL];
     __shared__ float tsm[SP_GEN_MAX_N];
-    const int h = blockIdx.x, tid = threadIdx.x;
-    const int G = A.n_q / A.n_kvh, kvh = h / G;
+    const int h = blockIdx.x, tid = threadIdx.x;  // query row h of n_seq * n_q
+    const int G = A.n_q / A.n_kvh, kvh = (h % A.n_q) / G;
     const int ns = A.n_skel, nt = A.n_target, ns4 = r4(ns), nt32 = r32(nt);
     float *c = reinterpret_cast<float *>(dsm);
     float *qt = c + r4(A.pad);
@@ -337,10 +337,20 @@ k_hier_attn_prep(const SpPlan P, const SpHierAttnArgs A, float *__restrict__ pre
 // into registers while the current chunk's scores run.
 template <int RB, int GM, bool OUT>
 __global__ void __launch_bounds__(NT, 3)
-k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A, const float *__restrict__ prep, float *__restrict__ part,
-                  int n_runs) {
+k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, const float *__restrict__ prep0,
+                  float *__restrict__ part0, int n_runs) {
     extern __shared__ __attribute__((aligned(16))) unsigned char dsm[];
     const int kvh = blockIdx.x, run = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    // sequence blockIdx.z: its positions, prepared queries, partials and score rows
+    const int seq = blockIdx.z;
+    SpHierAttnArgs A = A0;
+    A.kcache += (long long)T.start[seq] * A0.B;
+    A.vcache += (long long)T.start[seq] * A0.B;
+    A.n_kv = T.len[seq];
+    const long long s_stride = T.len[seq];
+    if (A0.scores) A.scores += T.soff[seq];
+    const float *__restrict__ prep = prep0 + (long long)seq * A0.n_q * A0.ps;
+    float *__restrict__ part = part0 + (long long)seq * A0.n_q * n_runs * A0.pp;
     const int G = A.n_q / A.n_kvh, h0 = kvh * G;
     const int ns = A.n_skel, nt = A.n_target, B = A.B, nb = P.n_bands;
     const int qo = prep_qt_off(ns), so = prep_sum_off(ns, nt);
@@ -560,8 +570,8 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A, const float *__restric
                 sc[ha * CH + tid] = s0;
                 if (hb != ha) sc[hb * CH + tid] = s1;
                 if (A.scores) {
-                    A.scores[(long long)(h0 + ha) * A.n_kv + c0 + tid] = s0;
-                    if (hb != ha) A.scores[(long long)(h0 + hb) * A.n_kv + c0 + tid] = s1;
+                    A.scores[(long long)(h0 + ha) * s_stride + c0 + tid] = s0;
+                    if (hb != ha) A.scores[(long long)(h0 + hb) * s_stride + c0 + tid] = s1;
                 }
             }
         }
@@ -726,32 +736,32 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A, const float *__restric
         }
     }
     if (RB > 0) {
-        // position groups' sums through LDS: T [npg_t][G][n_win * LPW], S [npg_s][G][ns]
+        // position groups' sums through LDS: Tr [npg_t][G][n_win * LPW], Sr [npg_s][G][ns]
         const int tw = n_win * LPW;
-        float *T = reinterpret_cast<float *>(dsm);
-        float *S = T + npg_t * G * tw;
+        float *Tr = reinterpret_cast<float *>(dsm);
+        float *Sr = Tr + npg_t * G * tw;
         __syncthreads();  // the last chunk is done with the staging memory
         if (t_on) {
 #pragma unroll
-            for (int k = 0; k < LPW; k++) T[(t_pg * G + t_ha) * tw + t_w * LPW + k] = fmaf(-centre, twsum[0], tacc[k][0]);
+            for (int k = 0; k < LPW; k++) Tr[(t_pg * G + t_ha) * tw + t_w * LPW + k] = fmaf(-centre, twsum[0], tacc[k][0]);
             if (t_hb != t_ha) {
 #pragma unroll
                 for (int k = 0; k < LPW; k++)
-                    T[(t_pg * G + t_hb) * tw + t_w * LPW + k] = fmaf(-centre, twsum[1], tacc[k][1]);
+                    Tr[(t_pg * G + t_hb) * tw + t_w * LPW + k] = fmaf(-centre, twsum[1], tacc[k][1]);
             }
         }
         if (s_on) {
-            S[(s_pg * G + s_ha) * ns + s_s] = sacc[0];
-            if (s_hb != s_ha) S[(s_pg * G + s_hb) * ns + s_s] = sacc[1];
+            Sr[(s_pg * G + s_ha) * ns + s_s] = sacc[0];
+            if (s_hb != s_ha) Sr[(s_pg * G + s_hb) * ns + s_s] = sacc[1];
         }
         __syncthreads();
         for (int i = tid; i < G * (ns + nt); i += NT) {
             const int h = i / (ns + nt), j = i - h * (ns + nt);
             float v = 0.0f;
             if (j < ns)
-                for (int g = 0; g < npg_s; g++) v += S[(g * G + h) * ns + j];
+                for (int g = 0; g < npg_s; g++) v += Sr[(g * G + h) * ns + j];
             else
-                for (int g = 0; g < npg_t; g++) v += T[(g * G + h) * tw + (j - ns)];
+                for (int g = 0; g < npg_t; g++) v += Tr[(g * G + h) * tw + (j - ns)];
             part[((long long)(h0 + h) * n_runs + run) * pp + 4 + j] = v;
         }
     } else {
@@ -775,8 +785,8 @@ k_hier_attn_merge(const SpPlan P, const SpHierAttnArgs A, const float *__restric
     __shared__ float red[2 * (NT / SP_WAVE)];
     __shared__ float cas_s[SP_CAS_TOTAL];
     __shared__ float tsm[SP_GEN_MAX_N];
-    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int G = A.n_q / A.n_kvh, kvh = h / G;
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;  // row h of n_seq * n_q
+    const int G = A.n_q / A.n_kvh, kvh = (h % A.n_q) / G;
     const int ns = A.n_skel, nt = A.n_target, pp = A.pp;
     float *c = reinterpret_cast<float *>(dsm);
     float *cs = c + r4(A.pad);
@@ -879,44 +889,45 @@ int window_bits(const SpHierAttnArgs &A) {
 
 // The split kernel's instance for this call's level width and output mode.
 template <bool OUT>
-void launch_split(const SpPlan &P, const SpHierAttnArgs &A, const float *prep, float *part, int n_runs, int rb, int G,
-                  size_t lds_split, hipStream_t s) {
-    const dim3 grid(A.n_kvh, n_runs);
+void launch_split(const SpPlan &P, const SpHierAttnArgs &A, const SpSeqTab &T, const float *prep, float *part,
+                  int n_runs, int rb, int G, size_t lds_split, hipStream_t s) {
+    const dim3 grid(A.n_kvh, n_runs, T.n_seq);
     if (rb == 2 && G <= 2)
-        hipLaunchKernelGGL((k_hier_attn_split<2, 2, OUT>), grid, dim3(NT), lds_split, s, P, A, prep, part, n_runs);
+        hipLaunchKernelGGL((k_hier_attn_split<2, 2, OUT>), grid, dim3(NT), lds_split, s, P, A, T, prep, part, n_runs);
     else if (rb == 2)
-        hipLaunchKernelGGL((k_hier_attn_split<2, MAX_G, OUT>), grid, dim3(NT), lds_split, s, P, A, prep, part, n_runs);
+        hipLaunchKernelGGL((k_hier_attn_split<2, MAX_G, OUT>), grid, dim3(NT), lds_split, s, P, A, T, prep, part, n_runs);
     else if (rb == 4)
-        hipLaunchKernelGGL((k_hier_attn_split<4, MAX_G, OUT>), grid, dim3(NT), lds_split, s, P, A, prep, part, n_runs);
+        hipLaunchKernelGGL((k_hier_attn_split<4, MAX_G, OUT>), grid, dim3(NT), lds_split, s, P, A, T, prep, part, n_runs);
     else if (rb == 8)
-        hipLaunchKernelGGL((k_hier_attn_split<8, MAX_G, OUT>), grid, dim3(NT), lds_split, s, P, A, prep, part, n_runs);
+        hipLaunchKernelGGL((k_hier_attn_split<8, MAX_G, OUT>), grid, dim3(NT), lds_split, s, P, A, T, prep, part, n_runs);
     else
-        hipLaunchKernelGGL((k_hier_attn_split<0, MAX_G, OUT>), grid, dim3(NT), lds_split, s, P, A, prep, part, n_runs);
+        hipLaunchKernelGGL((k_hier_attn_split<0, MAX_G, OUT>), grid, dim3(NT), lds_split, s, P, A, T, prep, part, n_runs);
 }
 
 }  // namespace
 
 int sp_hier_attn_prep_floats(int n_skel, int n_target) { return prep_sum_off(n_skel, n_target) + 4; }
 
-size_t sp_hier_attn_workspace_floats(const SpHierAttnArgs &A, int n_runs) {
-    return (size_t)A.n_q * A.ps + (size_t)A.n_q * n_runs * A.pp;
+size_t sp_hier_attn_workspace_floats(const SpHierAttnArgs &A, int n_runs, int n_seq) {
+    return (size_t)n_seq * ((size_t)A.n_q * A.ps + (size_t)A.n_q * n_runs * A.pp);
 }
 
-// Runs per KV head: the blocks that are resident at once (three per CU) spread
-// over the KV heads, so the split kernel runs in one round.
-int sp_hier_attn_runs(const SpHierAttnArgs &A, int cus) {
+// Runs per KV head and sequence: the blocks that are resident at once (three per CU)
+// spread over the sequences' KV heads, so the split kernel runs in one round.
+int sp_hier_attn_runs(const SpHierAttnArgs &A, int cus, int n_seq) {
     const int n_chunks = (A.n_kv + CH - 1) / CH;
-    const int per_head = std::max(1, (3 * cus) / std::max(1, A.n_kvh));
+    const int per_head = std::max(1, (3 * cus) / std::max(1, A.n_kvh * n_seq));
     return std::max(1, std::min(std::min(n_chunks, per_head), MERGE_RUNS_PER_THREAD * NT));
 }
 
-hipError_t sp_launch_hier_attn(const SpPlan &P, const SpHierAttnArgs &A, float *ws, size_t ws_floats, int n_runs,
-                               hipStream_t s) {
+hipError_t sp_launch_hier_attn(const SpPlan &P, const SpHierAttnArgs &A, const SpSeqTab &T, float *ws,
+                               size_t ws_floats, int n_runs, hipStream_t s) {
     if (A.n_kv <= 0 || A.n_q <= 0 || A.n_kvh <= 0 || A.n_q % A.n_kvh || A.n_q / A.n_kvh > MAX_G ||
         A.pad > SP_GEN_MAX_N || A.n_skel + A.n_target > SP_GEN_MAX_N || A.hd > A.pad || n_runs <= 0 ||
         A.ps != sp_hier_attn_prep_floats(A.n_skel, A.n_target) || A.pp < 4 + A.n_skel + A.n_target)
         return hipErrorInvalidValue;
-    if (sp_hier_attn_workspace_floats(A, n_runs) > ws_floats || n_runs > MERGE_RUNS_PER_THREAD * NT)
+    if (T.n_seq < 1 || T.n_seq > SP_ATTN_MAX_SEQ || sp_hier_attn_workspace_floats(A, n_runs, T.n_seq) > ws_floats ||
+        n_runs > MERGE_RUNS_PER_THREAD * NT)
         return hipErrorInvalidValue;
     const int G = A.n_q / A.n_kvh;
     const int rb = window_bits(A);
@@ -934,11 +945,12 @@ hipError_t sp_launch_hier_attn(const SpPlan &P, const SpHierAttnArgs &A, float *
     const size_t lds_merge = 4 * (size_t)(r4(A.pad) + r4(A.n_skel) + r4(n_runs)) + 2 * (size_t)A.n_target * A.n_skel;
     if (lds_prep > 65536 || lds_split > 65536 || lds_merge > 65536) return hipErrorInvalidValue;
     float *prep = ws;
-    float *part = ws + (size_t)A.n_q * A.ps;
-    hipLaunchKernelGGL(k_hier_attn_prep, dim3(A.n_q), dim3(NT), lds_prep, s, P, A, prep);
-    if (A.out) launch_split<true>(P, A, prep, part, n_runs, rb, G, lds_split, s);
-    else launch_split<false>(P, A, prep, part, n_runs, rb, G, lds_split, s);
-    if (A.out) hipLaunchKernelGGL(k_hier_attn_merge, dim3(A.n_q), dim3(NT), lds_merge, s, P, A, part, n_runs);
+    float *part = ws + (size_t)T.n_seq * A.n_q * A.ps;
+    hipLaunchKernelGGL(k_hier_attn_prep, dim3(T.n_seq * A.n_q), dim3(NT), lds_prep, s, P, A, prep);
+    if (A.out) launch_split<true>(P, A, T, prep, part, n_runs, rb, G, lds_split, s);
+    else launch_split<false>(P, A, T, prep, part, n_runs, rb, G, lds_split, s);
+    if (A.out)
+        hipLaunchKernelGGL(k_hier_attn_merge, dim3(T.n_seq * A.n_q), dim3(NT), lds_merge, s, P, A, part, n_runs);
     return hipGetLastError();
 }
 
@@ -949,22 +961,22 @@ static bool prep_merge_args_ok(const SpHierAttnArgs &A) {
            A.pp >= 4 + A.n_skel + A.n_target;
 }
 
-hipError_t sp_launch_hier_attn_prep(const SpPlan &P, const SpHierAttnArgs &A, float *prep, hipStream_t s) {
-    if (!prep_merge_args_ok(A)) return hipErrorInvalidValue;
+hipError_t sp_launch_hier_attn_prep(const SpPlan &P, const SpHierAttnArgs &A, int n_seq, float *prep, hipStream_t s) {
+    if (!prep_merge_args_ok(A) || n_seq < 1) return hipErrorInvalidValue;
     const size_t lds_prep = 4 * (size_t)(r4(A.pad) + r32(A.n_target) + 8 * r4(A.n_skel)) +
                             (A.W ? 2 * (size_t)A.n_target * A.n_skel : 0);
     if (lds_prep > 65536) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_hier_attn_prep, dim3(A.n_q), dim3(NT), lds_prep, s, P, A, prep);
+    hipLaunchKernelGGL(k_hier_attn_prep, dim3(n_seq * A.n_q), dim3(NT), lds_prep, s, P, A, prep);
     return hipGetLastError();
 }
 
-hipError_t sp_launch_hier_attn_merge(const SpPlan &P, const SpHierAttnArgs &A, const float *part, int n_runs,
-                                     hipStream_t s) {
-    if (!prep_merge_args_ok(A) || !A.out || n_runs <= 0 || n_runs > MERGE_RUNS_PER_THREAD * NT)
+hipError_t sp_launch_hier_attn_merge(const SpPlan &P, const SpHierAttnArgs &A, int n_seq, const float *part,
+                                     int n_runs, hipStream_t s) {
+    if (!prep_merge_args_ok(A) || !A.out || n_seq < 1 || n_runs <= 0 || n_runs > MERGE_RUNS_PER_THREAD * NT)
         return hipErrorInvalidValue;
     const size_t lds_merge = 4 * (size_t)(r4(A.pad) + r4(A.n_skel) + r4(n_runs)) +
                              (A.W ? 2 * (size_t)A.n_target * A.n_skel : 0);
     if (lds_merge > 65536) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_hier_attn_merge, dim3(A.n_q), dim3(NT), lds_merge, s, P, A, part, n_runs);
+    hipLaunchKernelGGL(k_hier_attn_merge, dim3(n_seq * A.n_q), dim3(NT), lds_merge, s, P, A, part, n_runs);
     return hipGetLastError();
 }

@@ -49,9 +49,9 @@ __device__ __forceinline__ uint32_t lds_word(const unsigned char *base, int o) {
 // part: per (query head, run) [m, l, 0, 0, c_skel (30), dev (300)] (pp floats).
 template <int GM, bool OUT>
 __global__ void __launch_bounds__(64)
-k_hier_attn_lane(const unsigned char *__restrict__ kc, const unsigned char *__restrict__ vc, long long slot_bytes,
-                 int n_kv, int G, const float *__restrict__ prep, int ps, float *__restrict__ scores,
-                 float *__restrict__ part, int pp, int n_runs) {
+k_hier_attn_lane(const unsigned char *__restrict__ kc0, const unsigned char *__restrict__ vc0, long long slot_bytes,
+                 const SpSeqTab T, int G, const float *__restrict__ prep0, int ps, float *__restrict__ scores0,
+                 float *__restrict__ part0, int pp, int n_runs) {
     constexpr int NCK = RecTile<HR>::NCK;
     constexpr int NHP = (GM + 1) / 2;                         // head pairs
     constexpr int IT = NWIN * NHP, IS = NS * NHP;             // target-window and skeleton items
@@ -65,6 +65,14 @@ k_hier_attn_lane(const unsigned char *__restrict__ kc, const unsigned char *__re
     __shared__ __attribute__((aligned(16))) float psb[2 * 64 * GM];  // p * scale_b (V skeleton bands)
     __shared__ __attribute__((aligned(16))) float qs[GM * PQ];        // the G prepared queries
     const int kvh = blockIdx.x, run = blockIdx.y, lane = threadIdx.x;
+    // sequence blockIdx.z: its positions, prepared queries, score rows and partials
+    const int seq = blockIdx.z, n_q = (int)gridDim.x * G, n_kv = T.len[seq];
+    const unsigned char *__restrict__ kc = kc0 + (long long)T.start[seq] * HR::total;
+    const unsigned char *__restrict__ vc = vc0 + (long long)T.start[seq] * HR::total;
+    const long long s_stride = T.len[seq];
+    float *__restrict__ scores = scores0 ? scores0 + T.soff[seq] : nullptr;
+    const float *__restrict__ prep = prep0 + (long long)seq * n_q * ps;
+    float *__restrict__ part = part0 + (long long)seq * n_q * n_runs * pp;
     const int h0 = kvh * G;
     const int tpo = (n_kv + 63) / 64;
     const int n_tiles = (int)gridDim.x * tpo;
@@ -157,7 +165,7 @@ k_hier_attn_lane(const unsigned char *__restrict__ kc, const unsigned char *__re
                 const float v = fmaf(step, d[h] - centre * qs[h * PQ + SO], a[h]);
                 if (live) {
                     s[h] = v;
-                    if (scores) scores[(long long)(h0 + h) * n_kv + pos] = v;
+                    if (scores) scores[(long long)(h0 + h) * s_stride + pos] = v;
                 }
             }
         }
@@ -270,8 +278,8 @@ k_hier_attn_lane(const unsigned char *__restrict__ kc, const unsigned char *__re
     }
     if (!OUT) return;
     // ---- the run's partial per query head: groups summed through LDS ----
-    float *T = reinterpret_cast<float *>(stage);   // [NGT][GM][NWIN * LPW]
-    float *S = T + NGT * GM * NWIN * LPW;          // [NGS][GM][NS]
+    float *Tr = reinterpret_cast<float *>(stage);  // [NGT][GM][NWIN * LPW]
+    float *Sr = Tr + NGT * GM * NWIN * LPW;        // [NGS][GM][NS]
     __syncthreads();  // the last tile is done with the stage
 #pragma unroll
     for (int r = 0; r < RT; r++) {
@@ -285,7 +293,7 @@ k_hier_attn_lane(const unsigned char *__restrict__ kc, const unsigned char *__re
             if (h >= GM) continue;
 #pragma unroll
             for (int k = 0; k < LPW; k++)
-                T[(tg * GM + h) * (NWIN * LPW) + w * LPW + k] = fmaf(-centre, tws[r][q], tacc[r][k][q]);
+                Tr[(tg * GM + h) * (NWIN * LPW) + w * LPW + k] = fmaf(-centre, tws[r][q], tacc[r][k][q]);
         }
     }
 #pragma unroll
@@ -297,7 +305,7 @@ k_hier_attn_lane(const unsigned char *__restrict__ kc, const unsigned char *__re
 #pragma unroll
         for (int q = 0; q < 2; q++) {
             const int h = 2 * hp + q;
-            if (h < GM) S[(sg * GM + h) * NS + j] = sacc[r][q];
+            if (h < GM) Sr[(sg * GM + h) * NS + j] = sacc[r][q];
         }
     }
     __syncthreads();
@@ -313,10 +321,10 @@ k_hier_attn_lane(const unsigned char *__restrict__ kc, const unsigned char *__re
             float v = 0.0f;
             if (j < NS) {
 #pragma unroll
-                for (int g = 0; g < NGS; g++) v += S[(g * GM + h) * NS + j];
+                for (int g = 0; g < NGS; g++) v += Sr[(g * GM + h) * NS + j];
             } else {
 #pragma unroll
-                for (int g = 0; g < NGT; g++) v += T[(g * GM + h) * (NWIN * LPW) + (j - NS)];
+                for (int g = 0; g < NGT; g++) v += Tr[(g * GM + h) * (NWIN * LPW) + (j - NS)];
             }
             dst[4 + j] = v;
         }
@@ -324,15 +332,15 @@ k_hier_attn_lane(const unsigned char *__restrict__ kc, const unsigned char *__re
 }
 
 template <int GM>
-void launch_g(const SpHierAttnArgs &A, const float *prep, float *part, int n_runs, hipStream_t s) {
-    const dim3 grid(A.n_kvh, n_runs), block(64);
+void launch_g(const SpHierAttnArgs &A, const SpSeqTab &T, const float *prep, float *part, int n_runs, hipStream_t s) {
+    const dim3 grid(A.n_kvh, n_runs, T.n_seq), block(64);
     const int G = A.n_q / A.n_kvh;
     if (A.out)
-        hipLaunchKernelGGL((k_hier_attn_lane<GM, true>), grid, block, 0, s, A.kcache, A.vcache, A.slot_bytes, A.n_kv,
-                           G, prep, A.ps, A.scores, part, A.pp, n_runs);
+        hipLaunchKernelGGL((k_hier_attn_lane<GM, true>), grid, block, 0, s, A.kcache, A.vcache, A.slot_bytes, T, G,
+                           prep, A.ps, A.scores, part, A.pp, n_runs);
     else
-        hipLaunchKernelGGL((k_hier_attn_lane<GM, false>), grid, block, 0, s, A.kcache, A.vcache, A.slot_bytes,
-                           A.n_kv, G, prep, A.ps, A.scores, part, A.pp, n_runs);
+        hipLaunchKernelGGL((k_hier_attn_lane<GM, false>), grid, block, 0, s, A.kcache, A.vcache, A.slot_bytes, T, G,
+                           prep, A.ps, A.scores, part, A.pp, n_runs);
 }
 
 }  // namespace
@@ -353,25 +361,26 @@ bool sp_hier_attn_lane_ok(const SpPlan &P, const SpHierAttnArgs &A) {
 
 // Runs per KV head: at least one tile per run, about six resident one-wave blocks
 // per CU spread over the KV heads, at most the merge's limit.
-int sp_hier_attn_lane_runs(const SpHierAttnArgs &A, int cus) {
+int sp_hier_attn_lane_runs(const SpHierAttnArgs &A, int cus, int n_seq) {
     const int tpo = (A.n_kv + 63) / 64;
-    const int per_head = std::max(1, (6 * cus) / std::max(1, A.n_kvh));
+    const int per_head = std::max(1, (6 * cus) / std::max(1, A.n_kvh * n_seq));
     return std::max(1, std::min(std::min(tpo, per_head), 1024));
 }
 
-hipError_t sp_launch_hier_attn_lane(const SpPlan &P, const SpHierAttnArgs &A, float *ws, size_t ws_floats,
-                                    int n_runs, hipStream_t s) {
-    if (n_runs <= 0 || n_runs > 1024 || sp_hier_attn_workspace_floats(A, n_runs) > ws_floats)
+hipError_t sp_launch_hier_attn_lane(const SpPlan &P, const SpHierAttnArgs &A, const SpSeqTab &T, float *ws,
+                                    size_t ws_floats, int n_runs, hipStream_t s) {
+    if (n_runs <= 0 || n_runs > 1024 || T.n_seq < 1 || T.n_seq > SP_ATTN_MAX_SEQ ||
+        sp_hier_attn_workspace_floats(A, n_runs, T.n_seq) > ws_floats)
         return hipErrorInvalidValue;
     float *prep = ws;
-    float *part = ws + (size_t)A.n_q * A.ps;
-    hipError_t e = sp_launch_hier_attn_prep(P, A, prep, s);
+    float *part = ws + (size_t)T.n_seq * A.n_q * A.ps;
+    hipError_t e = sp_launch_hier_attn_prep(P, A, T.n_seq, prep, s);
     if (e != hipSuccess) return e;
     const int G = A.n_q / A.n_kvh;
-    if (G <= 2) launch_g<2>(A, prep, part, n_runs, s);
-    else if (G <= 4) launch_g<4>(A, prep, part, n_runs, s);
-    else launch_g<8>(A, prep, part, n_runs, s);
+    if (G <= 2) launch_g<2>(A, T, prep, part, n_runs, s);
+    else if (G <= 4) launch_g<4>(A, T, prep, part, n_runs, s);
+    else launch_g<8>(A, T, prep, part, n_runs, s);
     e = hipGetLastError();
     if (e != hipSuccess || !A.out) return e;
-    return sp_launch_hier_attn_merge(P, A, part, n_runs, s);
+    return sp_launch_hier_attn_merge(P, A, T.n_seq, part, n_runs, s);
 }

@@ -209,6 +209,20 @@ struct SpHierGeo {
     int default_geo;         // skeleton/targets are sp_hier_default_geometry's
 };
 
+// Sequences of one batched decode-attention call: sequence s attends positions
+// [start[s], start[s] + len[s]) of the layer with its own n_q query rows (llama.cpp's
+// unified cache, each sequence a range of cells); its scores are [n_q][len[s]] at
+// element soff[s] = n_q * (len[0] + ... + len[s-1]). Passed by value to the split
+// kernels (blockIdx.z = sequence); a single-sequence call is {1, n_kv, {0}, {n_kv}, {0}}.
+#define SP_ATTN_MAX_SEQ 64
+struct SpSeqTab {
+    int n_seq;
+    int max_len;  // the longest sequence
+    int start[SP_ATTN_MAX_SEQ];
+    int len[SP_ATTN_MAX_SEQ];
+    long long soff[SP_ATTN_MAX_SEQ];
+};
+
 // Fused decode attention over hier records (sp_hier_attn.hip).
 struct SpHierAttnArgs {
     const unsigned char *kcache, *vcache;  // records of slot (layer, KV head 0); KV head h at + h * slot_bytes
@@ -224,25 +238,29 @@ struct SpHierAttnArgs {
     int ps;                                // floats per query head of the prepared query
     int pp;                                // floats per (query head, run) partial
 };
+// Batched calls: A describes one sequence's shape (n_q query rows per sequence, n_kv the
+// longest sequence); q and out hold n_seq blocks of n_q rows, scores the sequences'
+// [n_q][len] blocks at T.soff, the workspace n_seq blocks of prepared queries and partials.
 int sp_hier_attn_prep_floats(int n_skel, int n_target);  // the value SpHierAttnArgs::ps must hold
-size_t sp_hier_attn_workspace_floats(const SpHierAttnArgs &A, int n_runs);
-int sp_hier_attn_runs(const SpHierAttnArgs &A, int cus);
-hipError_t sp_launch_hier_attn(const SpPlan &P, const SpHierAttnArgs &A, float *ws, size_t ws_floats, int n_runs,
-                               hipStream_t s);
-// The hier attention's query preparation and merge alone (one block per query head),
-// for attention kernels whose records live in the same coefficient domain. A.W may be
-// null: no predictor (u = q~_skel; merged target coefficients = the weighted sums).
-hipError_t sp_launch_hier_attn_prep(const SpPlan &P, const SpHierAttnArgs &A, float *prep, hipStream_t s);
-hipError_t sp_launch_hier_attn_merge(const SpPlan &P, const SpHierAttnArgs &A, const float *part, int n_runs,
-                                     hipStream_t s);
+size_t sp_hier_attn_workspace_floats(const SpHierAttnArgs &A, int n_runs, int n_seq = 1);
+int sp_hier_attn_runs(const SpHierAttnArgs &A, int cus, int n_seq = 1);
+hipError_t sp_launch_hier_attn(const SpPlan &P, const SpHierAttnArgs &A, const SpSeqTab &T, float *ws,
+                               size_t ws_floats, int n_runs, hipStream_t s);
+// The hier attention's query preparation and merge alone (one block per query head of
+// every sequence), for attention kernels whose records live in the same coefficient
+// domain. A.W may be null: no predictor (u = q~_skel; merged target coefficients = the
+// weighted sums).
+hipError_t sp_launch_hier_attn_prep(const SpPlan &P, const SpHierAttnArgs &A, int n_seq, float *prep, hipStream_t s);
+hipError_t sp_launch_hier_attn_merge(const SpPlan &P, const SpHierAttnArgs &A, int n_seq, const float *part,
+                                     int n_runs, hipStream_t s);
 
 // One-position-per-lane split kernel of the hier attention (sp_hier_attn_lane.hip) for
 // hd 256 / pad 330 / skeleton 30 at 5/5 bits / 300 targets at 2 bits: whether it serves
 // the call, its runs per KV head, and prep + split + merge.
 bool sp_hier_attn_lane_ok(const SpPlan &P, const SpHierAttnArgs &A);
-int sp_hier_attn_lane_runs(const SpHierAttnArgs &A, int cus);
-hipError_t sp_launch_hier_attn_lane(const SpPlan &P, const SpHierAttnArgs &A, float *ws, size_t ws_floats,
-                                    int n_runs, hipStream_t s);
+int sp_hier_attn_lane_runs(const SpHierAttnArgs &A, int cus, int n_seq = 1);
+hipError_t sp_launch_hier_attn_lane(const SpPlan &P, const SpHierAttnArgs &A, const SpSeqTab &T, float *ws,
+                                    size_t ws_floats, int n_runs, hipStream_t s);
 
 // Fused decode attention over sqfree+spinor records (sp_sqfree_attn.hip): the split
 // kernel's arguments (records of slot (layer, KV head 0), KV head h at + h * slot bytes).
@@ -257,11 +275,12 @@ struct SpSqAttnArgs {
 // 1..3: the lane specialization serving this geometry (skeleton 77 with 5/4/4/4/5 K and
 // V; 115 with 5/4/4/4/5 K and V; 115 with V one 3-bit band), 0: none
 int sp_sqfree_attn_kind(const SpPlan &KP, const SpPlan &VP, const SpSqGeo &G);
-int sp_sqfree_attn_runs(int n_kvh, int n_kv, int cus);
+int sp_sqfree_attn_runs(int n_kvh, int n_kv, int cus, int n_seq = 1);
 // HA: the prep/merge arguments (pad, skeleton/residual index tables as skel_idx /
-// tgt_idx, W null, q, kq_scale, out); ws: prep [n_q * ps] then partials.
+// tgt_idx, W null, q, kq_scale, out); ws: prep [n_seq * n_q * ps] then partials.
 hipError_t sp_launch_sqfree_attn(const SpPlan &KP, const SpPlan &VP, const SpSqGeo &G, const SpHierAttnArgs &HA,
-                                 const SpSqAttnArgs &A, float *ws, size_t ws_floats, int n_runs, hipStream_t s);
+                                 const SpSqAttnArgs &A, const SpSeqTab &T, float *ws, size_t ws_floats, int n_runs,
+                                 hipStream_t s);
 
 // one-vector-per-lane hier kernels for the default geometry at head_dim 256;
 // hipErrorNotSupported (nothing launched) when no specialization fits. src2/dst2:
@@ -340,9 +359,14 @@ size_t sp_attn_workspace_floats(int n_q, int hd, int max_kv);
 // One-position-per-lane split kernel for the hd 96 (K 5/4/4, V 5) and hd 64 (K 5/5/4/3,
 // V 3) layouts (sp_attn_lane.hip): runs per KV head that fit part_floats (0: no lane
 // kernel for these layouts), and the launch writing [m, l, o~[hd]] per (query head, run).
-int sp_attn_lane_runs(const SpPlan &KP, const SpPlan &VP, const SpAttnArgs &A, size_t part_floats);
-hipError_t sp_launch_attn_lane_split(const SpPlan &KP, const SpPlan &VP, const SpAttnArgs &A, const float *qt,
-                                     float *part, int n_runs, hipStream_t s);
+int sp_attn_lane_runs(const SpPlan &KP, const SpPlan &VP, const SpAttnArgs &A, size_t part_floats, int n_seq = 1);
+hipError_t sp_launch_attn_lane_split(const SpPlan &KP, const SpPlan &VP, const SpAttnArgs &A, const SpSeqTab &T,
+                                     const float *qt, float *part, int n_runs, hipStream_t s);
+// Batched decode attention through the query preparation, the lane split kernel and the
+// combine (hd 96 / hd 64 layouts): q, out [n_seq][n_q][hd], scores at T.soff;
+// ws holds n_seq * n_q * hd prepared-query floats, then the partials.
+hipError_t sp_launch_attn_lane_seqs(const SpPlan &KP, const SpPlan &VP, const int *order, const SpAttnArgs &A,
+                                    const SpSeqTab &T, float *ws, size_t ws_floats, int n_runs, hipStream_t s);
 // Checks the arguments of a decode-attention call on one layer of a ship cache
 // and fills its launch arguments and K/V plans (band limit applied); -1 with the
 // error message set for bad arguments (sp_runtime.cpp).

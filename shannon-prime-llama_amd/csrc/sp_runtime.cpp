@@ -435,6 +435,9 @@ struct ShipPriv {
     float *ws = nullptr;
     size_t ws_floats = 0;
     int max_q = 0;
+    // batched (multi-sequence) attention workspace, grown on demand
+    float *seq_ws = nullptr;
+    size_t seq_ws_floats = 0;
     // K coefficient-order calibration: fp64 sums of the fed vectors' transforms
     bool calibrating = false;
     std::vector<double> csum, csum2;
@@ -542,6 +545,7 @@ extern "C" void sp_hip_cache_free(sp_hip_cache_t *cc) {
     ShipPriv *pv = (ShipPriv *)cc->priv;
     if (pv) {
         if (pv->ws) (void)hipFree(pv->ws);
+        if (pv->seq_ws) (void)hipFree(pv->seq_ws);
         if (pv->stage_d) (void)hipFree(pv->stage_d);
         if (pv->stage_h) (void)hipHostFree(pv->stage_h);
         delete pv;
@@ -829,6 +833,52 @@ extern "C" int sp_hip_read_all(const sp_hip_cache_t *cc, int start_pos, int n_po
 // ===========================================================================
 // fused attention
 // ===========================================================================
+// Sequence table of a (batched) attention call: n_seq ranges [start, start + len) of
+// [0, max_seq), each non-empty; scores packed [n_q][len] per sequence. False (error set)
+// otherwise.
+static bool seq_tab(int n_seq, const int *start, const int *len, int max_seq, int n_q, SpSeqTab *T,
+                    const char *who) {
+    if (n_seq < 1 || n_seq > SP_ATTN_MAX_SEQ || !start || !len) {
+        set_err("%s: 1..%d sequences with start and length arrays", who, SP_ATTN_MAX_SEQ);
+        return false;
+    }
+    memset(T, 0, sizeof(*T));
+    T->n_seq = n_seq;
+    long long off = 0;
+    for (int i = 0; i < n_seq; i++) {
+        if (start[i] < 0 || len[i] <= 0 || (long long)start[i] + len[i] > max_seq) {
+            set_err("%s: sequence %d [%d, %d + %d) outside [0, %d)", who, i, start[i], start[i], len[i], max_seq);
+            return false;
+        }
+        T->start[i] = start[i];
+        T->len[i] = len[i];
+        T->soff[i] = off;
+        off += (long long)n_q * len[i];
+        T->max_len = std::max(T->max_len, len[i]);
+    }
+    return true;
+}
+
+// Grow a stream-ordered workspace to `need` floats (a sync on the stream before freeing).
+static bool grow_ws(float **ws, size_t *have, size_t need, hipStream_t s, const char *who) {
+    if (need <= *have) return true;
+    if (*ws) {
+        if (!hip_ok(hipStreamSynchronize(s), who)) return false;
+        (void)hipFree(*ws);
+        *ws = nullptr;
+        *have = 0;
+    }
+    if (!hip_ok(hipMalloc((void **)ws, need * sizeof(float)), who)) return false;
+    *have = need;
+    return true;
+}
+
+static int cu_count() {
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    return cus;
+}
 // Launch arguments of one layer's decode attention over the cache's records.
 int sp_attn_prepare(const sp_hip_cache_t *cc, int layer, int n_kv, const float *d_q, int n_q, float kq_scale,
                     float *d_scores, float *d_out, int max_bands, SpAttnArgs *out_args, SpPlan *out_kp,
@@ -878,6 +928,48 @@ extern "C" int sp_hip_attn_decode_bands(const sp_hip_cache_t *cc, int layer, int
 extern "C" int sp_hip_attn_decode(const sp_hip_cache_t *cc, int layer, int n_kv, const float *d_q,
                                   int n_q, float kq_scale, float *d_scores, float *d_out, void *stream) {
     return sp_hip_attn_decode_bands(cc, layer, n_kv, d_q, n_q, kq_scale, d_scores, d_out, -1, stream);
+}
+
+extern "C" int sp_hip_attn_decode_seqs(const sp_hip_cache_t *cc, int layer, int n_seq, const int *seq_start,
+                                       const int *seq_len, const float *d_q, int n_q, float kq_scale, float *d_scores,
+                                       float *d_out, void *stream) {
+    if (!cc || !cc->priv) { set_err("attn seqs: bad cache"); return -1; }
+    SpSeqTab T;
+    if (!seq_tab(n_seq, seq_start, seq_len, cc->max_seq_len, n_q, &T, "attn seqs")) return -1;
+    SpAttnArgs A;
+    SpPlan kp, vp;
+    if (sp_attn_prepare(cc, layer, T.max_len, d_q, n_q, kq_scale, d_scores, d_out, -1, &A, &kp, &vp)) return -1;
+    if (!d_scores && !d_out) { set_err("attn seqs: no output"); return -1; }
+    ShipPriv *pv = (ShipPriv *)cc->priv;
+    const hipStream_t s = (hipStream_t)(stream ? stream : cc->stream);
+    // the one-position-per-lane layouts (hd 96 / hd 64): every sequence in one launch each of
+    // the query preparation, the split kernel and the combine
+    const char *off = getenv("SP_HIP_NO_LANE_ATTN");
+    int n_runs = (off && off[0] == '1') ? 0 : sp_attn_lane_runs(kp, vp, A, (size_t)1 << 40, n_seq);
+    for (int i = 0; i < n_seq && n_runs > 0; i++)  // the lane kernel's dword-aligned record bases, per sequence
+        if (((long long)T.start[i] * A.kB) % 4 || ((long long)T.start[i] * A.vB) % 4) n_runs = 0;
+    if (n_runs > 0) {
+        const size_t rows = (size_t)n_seq * n_q;
+        if (!grow_ws(&pv->seq_ws, &pv->seq_ws_floats, rows * A.hd + rows * n_runs * (A.hd + 2), s,
+                     "attn seqs workspace")) return -1;
+        return hip_ok(sp_launch_attn_lane_seqs(kp, vp, cc->d_mobius_order, A, T, pv->seq_ws, pv->seq_ws_floats, n_runs, s),
+                      "attn seqs") ? 0 : -1;
+    }
+    // otherwise one single-sequence launch sequence per sequence (the matrix-core kernel
+    // merges its partials inside its own launch), each over its range of records
+    if (n_q > pv->max_q) { set_err("attn seqs: n_q %d > %d", n_q, pv->max_q); return -1; }
+    for (int i = 0; i < n_seq; i++) {
+        SpAttnArgs Ai = A;
+        Ai.kpack += (long long)T.start[i] * A.kB;
+        Ai.vpack += (long long)T.start[i] * A.vB;
+        Ai.n_kv = T.len[i];
+        Ai.q = d_q + (size_t)i * n_q * A.hd;
+        Ai.scores = d_scores ? d_scores + T.soff[i] : nullptr;
+        Ai.out = d_out ? d_out + (size_t)i * n_q * A.hd : nullptr;
+        if (!hip_ok(sp_launch_attn_decode(kp, vp, cc->d_mobius_order, Ai, pv->ws, pv->ws_floats, s), "attn seqs"))
+            return -1;
+    }
+    return 0;
 }
 
 extern "C" int sp_hip_attn_decode_all_layers(const sp_hip_cache_t *cc, int n_kv, const float *d_q, int n_q,
@@ -1151,12 +1243,15 @@ extern "C" int sp_hip_sqfree_read_layer(const sp_hip_sqfree_cache_t *cc, int lay
     return 0;
 }
 
-extern "C" int sp_hip_sqfree_attn_decode(const sp_hip_sqfree_cache_t *cc, int layer, int n_kv, const float *d_q,
-                                         int n_q, float kq_scale, float *d_scores, float *d_out, void *stream) {
-    if (!sq_slot_ok(cc, layer, 0, 0, n_kv) || n_kv <= 0 || !d_q || n_q <= 0 || (!d_scores && !d_out)) {
+extern "C" int sp_hip_sqfree_attn_decode_seqs(const sp_hip_sqfree_cache_t *cc, int layer, int n_seq,
+                                              const int *seq_start, const int *seq_len, const float *d_q, int n_q,
+                                              float kq_scale, float *d_scores, float *d_out, void *stream) {
+    if (!cc || !cc->priv || layer < 0 || layer >= cc->config.n_layers || !d_q || n_q <= 0 || (!d_scores && !d_out)) {
         set_err("sqfree attn: bad args");
         return -1;
     }
+    SpSeqTab T;
+    if (!seq_tab(n_seq, seq_start, seq_len, cc->max_seq_len, n_q, &T, "sqfree attn")) return -1;
     const int H = cc->config.n_heads_kv;
     if (n_q % H || n_q / H > 8) { set_err("sqfree attn: n_q must be a multiple of n_heads_kv, at most 8 per KV head"); return -1; }
     SqPriv *pv = (SqPriv *)cc->priv;
@@ -1179,7 +1274,7 @@ extern "C" int sp_hip_sqfree_attn_decode(const sp_hip_sqfree_cache_t *cc, int la
     HA.out = d_out;
     HA.n_q = n_q;
     HA.n_kvh = H;
-    HA.n_kv = n_kv;
+    HA.n_kv = T.max_len;
     HA.hd = cc->config.head_dim;
     HA.pad = cc->pad_dim;
     HA.n_skel = cc->sk_k;
@@ -1197,34 +1292,28 @@ extern "C" int sp_hip_sqfree_attn_decode(const sp_hip_sqfree_cache_t *cc, int la
     A.out = d_out;
     A.n_q = n_q;
     A.n_kvh = H;
-    A.n_kv = n_kv;
+    A.n_kv = T.max_len;
     A.ps = HA.ps;
     A.qo = (HA.n_skel + 3) & ~3;  // the prepared query's residual part
     A.pp = HA.pp;
-    int dev = 0, cus = 256;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-        cus = 256;
-    int n_runs = sp_sqfree_attn_runs(H, n_kv, cus);
+    int n_runs = sp_sqfree_attn_runs(H, T.max_len, cu_count(), n_seq);
     // SP_HIP_SQFREE_ATTN_RUNS=n caps the runs per KV head (read at each call; tests use it
     // to give every run several tiles at small context lengths)
     if (const char *e = getenv("SP_HIP_SQFREE_ATTN_RUNS")) {
         const int r = atoi(e);
         if (r > 0) n_runs = std::min(n_runs, r);
     }
-    const size_t need = sp_hier_attn_workspace_floats(HA, n_runs);
     const hipStream_t s = (hipStream_t)(stream ? stream : cc->stream);
-    if (need > pv->attn_ws_floats) {
-        if (pv->d_attn_ws) {
-            if (!hip_ok(hipStreamSynchronize(s), "sqfree attn: sync before growing the workspace")) return -1;
-            (void)hipFree(pv->d_attn_ws);
-            pv->d_attn_ws = nullptr;
-            pv->attn_ws_floats = 0;
-        }
-        if (!hip_ok(hipMalloc((void **)&pv->d_attn_ws, need * sizeof(float)), "hipMalloc sqfree attn workspace")) return -1;
-        pv->attn_ws_floats = need;
-    }
-    return hip_ok(sp_launch_sqfree_attn(pv->kplan, pv->vplan, GK, HA, A, pv->d_attn_ws, pv->attn_ws_floats, n_runs, s),
-                  "sqfree attn") ? 0 : -1;
+    if (!grow_ws(&pv->d_attn_ws, &pv->attn_ws_floats, sp_hier_attn_workspace_floats(HA, n_runs, n_seq), s,
+                 "sqfree attn workspace")) return -1;
+    return hip_ok(sp_launch_sqfree_attn(pv->kplan, pv->vplan, GK, HA, A, T, pv->d_attn_ws, pv->attn_ws_floats,
+                                        n_runs, s), "sqfree attn") ? 0 : -1;
+}
+
+extern "C" int sp_hip_sqfree_attn_decode(const sp_hip_sqfree_cache_t *cc, int layer, int n_kv, const float *d_q,
+                                         int n_q, float kq_scale, float *d_scores, float *d_out, void *stream) {
+    const int start = 0;
+    return sp_hip_sqfree_attn_decode_seqs(cc, layer, 1, &start, &n_kv, d_q, n_q, kq_scale, d_scores, d_out, stream);
 }
 
 extern "C" void sp_hip_sqfree_write_k(sp_hip_sqfree_cache_t *cc, int l, int h, int p, const float *d) { sp_hip_sqfree_write_batch(cc, 0, l, h, p, 1, d, SP_DT_F32); }
@@ -1495,13 +1584,16 @@ extern "C" int sp_hip_hier_read_layer(const sp_hip_hier_cache_t *hc, int layer, 
     return 0;
 }
 
-extern "C" int sp_hip_hier_attn_decode(const sp_hip_hier_cache_t *hc, int layer, int n_kv, const float *d_q,
-                                       int n_q, float kq_scale, float *d_scores, float *d_out, void *stream) {
-    if (!hier_slot_ok(hc, layer, 0, 0, n_kv) || n_kv <= 0 || !d_q || n_q <= 0 || (!d_scores && !d_out) ||
+extern "C" int sp_hip_hier_attn_decode_seqs(const sp_hip_hier_cache_t *hc, int layer, int n_seq, const int *seq_start,
+                                            const int *seq_len, const float *d_q, int n_q, float kq_scale,
+                                            float *d_scores, float *d_out, void *stream) {
+    if (!hc || !hc->priv || layer < 0 || layer >= hc->config.n_layers || !d_q || n_q <= 0 || (!d_scores && !d_out) ||
         (long long)(layer + 1) * hc->config.n_heads_kv > hc->n_slots) {
         set_err("hier attn: bad args");
         return -1;
     }
+    SpSeqTab T;
+    if (!seq_tab(n_seq, seq_start, seq_len, hc->max_seq_len, n_q, &T, "hier attn")) return -1;
     const int H = hc->config.n_heads_kv;
     if (n_q % H || n_q / H > 8) { set_err("hier attn: n_q must be a multiple of n_heads_kv, at most 8 per KV head"); return -1; }
     HierPriv *pv = (HierPriv *)hc->priv;
@@ -1520,7 +1612,7 @@ extern "C" int sp_hip_hier_attn_decode(const sp_hip_hier_cache_t *hc, int layer,
     A.out = d_out;
     A.n_q = n_q;
     A.n_kvh = H;
-    A.n_kv = n_kv;
+    A.n_kv = T.max_len;
     A.hd = hc->config.head_dim;
     A.pad = hc->pad_dim;
     A.n_skel = hc->n_skeleton;
@@ -1529,9 +1621,7 @@ extern "C" int sp_hip_hier_attn_decode(const sp_hip_hier_cache_t *hc, int layer,
     A.B = G.bytes;
     A.ps = sp_hier_attn_prep_floats(A.n_skel, A.n_target);
     A.pp = (4 + A.n_skel + A.n_target + 3) & ~3;
-    int dev = 0, cus = 256;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-        cus = 256;
+    const int cus = cu_count();
     // The 256-position chunk kernel serves every geometry up to its LDS limit (at pad 330,
     // at most 4 query heads per KV head). Past it, the one-position-per-lane split kernel
     // serves the configs[4] geometry (hd 256, pad 330, skeleton 30 at 5/5 bits, 300 targets
@@ -1541,29 +1631,26 @@ extern "C" int sp_hip_hier_attn_decode(const sp_hip_hier_cache_t *hc, int layer,
     const char *lane_on = getenv("SP_HIP_HIER_ATTN_LANE");
     const bool lane = sp_hier_attn_lane_ok(pv->plan, A) &&
                       ((lane_on && lane_on[0] == '1') || (A.pad == 330 && n_q / H > 4));
-    int n_runs = lane ? sp_hier_attn_lane_runs(A, cus) : sp_hier_attn_runs(A, cus);
+    int n_runs = lane ? sp_hier_attn_lane_runs(A, cus, n_seq) : sp_hier_attn_runs(A, cus, n_seq);
     // SP_HIP_HIER_ATTN_RUNS=n caps the runs per KV head (read at each call; tests use it to
     // give every run several chunks or tiles at small context lengths)
     if (const char *e = getenv("SP_HIP_HIER_ATTN_RUNS")) {
         const int r = atoi(e);
         if (r > 0) n_runs = std::min(n_runs, r);
     }
-    const size_t need = sp_hier_attn_workspace_floats(A, n_runs);
     const hipStream_t s = (hipStream_t)(stream ? stream : hc->stream);
-    if (need > pv->attn_ws_floats) {
-        if (pv->d_attn_ws) {
-            if (!hip_ok(hipStreamSynchronize(s), "hier attn: sync before growing the workspace")) return -1;
-            (void)hipFree(pv->d_attn_ws);
-            pv->d_attn_ws = nullptr;
-            pv->attn_ws_floats = 0;
-        }
-        if (!hip_ok(hipMalloc((void **)&pv->d_attn_ws, need * sizeof(float)), "hipMalloc hier attn workspace")) return -1;
-        pv->attn_ws_floats = need;
-    }
+    if (!grow_ws(&pv->d_attn_ws, &pv->attn_ws_floats, sp_hier_attn_workspace_floats(A, n_runs, n_seq), s,
+                 "hier attn workspace")) return -1;
     if (lane)
-        return hip_ok(sp_launch_hier_attn_lane(pv->plan, A, pv->d_attn_ws, pv->attn_ws_floats, n_runs, s),
+        return hip_ok(sp_launch_hier_attn_lane(pv->plan, A, T, pv->d_attn_ws, pv->attn_ws_floats, n_runs, s),
                       "hier attn (lane)") ? 0 : -1;
-    return hip_ok(sp_launch_hier_attn(pv->plan, A, pv->d_attn_ws, pv->attn_ws_floats, n_runs, s), "hier attn") ? 0 : -1;
+    return hip_ok(sp_launch_hier_attn(pv->plan, A, T, pv->d_attn_ws, pv->attn_ws_floats, n_runs, s), "hier attn") ? 0 : -1;
+}
+
+extern "C" int sp_hip_hier_attn_decode(const sp_hip_hier_cache_t *hc, int layer, int n_kv, const float *d_q,
+                                       int n_q, float kq_scale, float *d_scores, float *d_out, void *stream) {
+    const int start = 0;
+    return sp_hip_hier_attn_decode_seqs(hc, layer, 1, &start, &n_kv, d_q, n_q, kq_scale, d_scores, d_out, stream);
 }
 
 extern "C" int sp_hip_hier_calibrate_begin(sp_hip_hier_cache_t *hc) {

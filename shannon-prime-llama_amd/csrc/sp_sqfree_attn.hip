@@ -75,9 +75,9 @@ constexpr int EP = 65;  // LDS row pitch (floats) of the transposed coefficient 
 // OUT = false: scores only.
 template <int SK, class SLK, class SLV, int GM, bool OUT>
 __global__ void __launch_bounds__(64)
-k_sqfree_attn_split(const unsigned char *__restrict__ kc, const unsigned char *__restrict__ vc, long long k_slot,
-                    long long v_slot, int n_kv, int G, const float *__restrict__ prep, int ps, int qo,
-                    float *__restrict__ scores, float *__restrict__ part, int pp, int n_runs) {
+k_sqfree_attn_split(const unsigned char *__restrict__ kc0, const unsigned char *__restrict__ vc0, long long k_slot,
+                    long long v_slot, const SpSeqTab T, int G, const float *__restrict__ prep0, int ps, int qo,
+                    float *__restrict__ scores0, float *__restrict__ part0, int pp, int n_runs) {
     using GK = SqRec<PAD, SK, RBITS, true, SLK>;
     using GV = SqRec<PAD, SK, RBITS, true, SLV>;
     constexpr int NCK = RecTile<GK>::NCK > RecTile<GV>::NCK ? RecTile<GK>::NCK : RecTile<GV>::NCK;
@@ -88,6 +88,14 @@ k_sqfree_attn_split(const unsigned char *__restrict__ kc, const unsigned char *_
     __shared__ float E[64 * EP];
     __shared__ __attribute__((aligned(16))) float Pw[64 * GM];
     const int kvh = blockIdx.x, run = blockIdx.y, lane = threadIdx.x;
+    // sequence blockIdx.z: its positions, prepared queries, score rows and partials
+    const int seq = blockIdx.z, n_q = (int)gridDim.x * G, n_kv = T.len[seq];
+    const unsigned char *__restrict__ kc = kc0 + (long long)T.start[seq] * GK::total;
+    const unsigned char *__restrict__ vc = vc0 + (long long)T.start[seq] * GV::total;
+    const long long s_stride = T.len[seq];
+    float *__restrict__ scores = scores0 ? scores0 + T.soff[seq] : nullptr;
+    const float *__restrict__ prep = prep0 + (long long)seq * n_q * ps;
+    float *__restrict__ part = part0 + (long long)seq * n_q * n_runs * pp;
     const int h0 = kvh * G;
     const int tpo = (n_kv + 63) / 64;
     const int n_tiles = (int)gridDim.x * tpo;
@@ -145,7 +153,7 @@ k_sqfree_attn_split(const unsigned char *__restrict__ kc, const unsigned char *_
                 const float v = a0 + a1;
                 if (live) {
                     s[h] = v;
-                    if (scores) scores[(long long)(h0 + h) * n_kv + pos] = v;
+                    if (scores) scores[(long long)(h0 + h) * s_stride + pos] = v;
                 }
             }
         }
@@ -251,25 +259,27 @@ using SkelL115 = Layout<115, 5, 4, 4, 4, 5>;
 using SkelL115V3 = Layout<115, 3>;
 
 template <int SK, class SLK, class SLV, int GM>
-void launch_split(const SpSqAttnArgs &A, const float *prep, float *part, int n_runs, hipStream_t s) {
-    const dim3 grid(A.n_kvh, n_runs), block(64);
+void launch_split(const SpSqAttnArgs &A, const SpSeqTab &T, const float *prep, float *part, int n_runs,
+                  hipStream_t s) {
+    const dim3 grid(A.n_kvh, n_runs, T.n_seq), block(64);
     if (A.out)
         hipLaunchKernelGGL((k_sqfree_attn_split<SK, SLK, SLV, GM, true>), grid, block, 0, s, A.kcache, A.vcache,
-                           A.k_slot_bytes, A.v_slot_bytes, A.n_kv, A.n_q / A.n_kvh, prep, A.ps, A.qo, A.scores, part,
+                           A.k_slot_bytes, A.v_slot_bytes, T, A.n_q / A.n_kvh, prep, A.ps, A.qo, A.scores, part,
                            A.pp, n_runs);
     else
         hipLaunchKernelGGL((k_sqfree_attn_split<SK, SLK, SLV, GM, false>), grid, block, 0, s, A.kcache, A.vcache,
-                           A.k_slot_bytes, A.v_slot_bytes, A.n_kv, A.n_q / A.n_kvh, prep, A.ps, A.qo, A.scores, part,
+                           A.k_slot_bytes, A.v_slot_bytes, T, A.n_q / A.n_kvh, prep, A.ps, A.qo, A.scores, part,
                            A.pp, n_runs);
 }
 
 template <int SK, class SLK, class SLV>
-void launch_split_g(const SpSqAttnArgs &A, const float *prep, float *part, int n_runs, hipStream_t s) {
+void launch_split_g(const SpSqAttnArgs &A, const SpSeqTab &T, const float *prep, float *part, int n_runs,
+                    hipStream_t s) {
     const int G = A.n_q / A.n_kvh;
-    if (G <= 1) launch_split<SK, SLK, SLV, 1>(A, prep, part, n_runs, s);
-    else if (G <= 2) launch_split<SK, SLK, SLV, 2>(A, prep, part, n_runs, s);
-    else if (G <= 4) launch_split<SK, SLK, SLV, 4>(A, prep, part, n_runs, s);
-    else launch_split<SK, SLK, SLV, 8>(A, prep, part, n_runs, s);
+    if (G <= 1) launch_split<SK, SLK, SLV, 1>(A, T, prep, part, n_runs, s);
+    else if (G <= 2) launch_split<SK, SLK, SLV, 2>(A, T, prep, part, n_runs, s);
+    else if (G <= 4) launch_split<SK, SLK, SLV, 4>(A, T, prep, part, n_runs, s);
+    else launch_split<SK, SLK, SLV, 8>(A, T, prep, part, n_runs, s);
 }
 
 template <class SL>
@@ -293,27 +303,29 @@ int sp_sqfree_attn_kind(const SpPlan &KP, const SpPlan &VP, const SpSqGeo &G) {
 
 // Runs per KV head: every run gets at least one tile and the blocks that are
 // resident at once (six one-wave blocks per CU) spread over the KV heads.
-int sp_sqfree_attn_runs(int n_kvh, int n_kv, int cus) {
+int sp_sqfree_attn_runs(int n_kvh, int n_kv, int cus, int n_seq) {
     const int tpo = (n_kv + 63) / 64;
-    const int per_head = std::max(1, (6 * cus) / std::max(1, n_kvh));
+    const int per_head = std::max(1, (6 * cus) / std::max(1, n_kvh * n_seq));
     return std::max(1, std::min(std::min(tpo, per_head), 1024));
 }
 
 hipError_t sp_launch_sqfree_attn(const SpPlan &KP, const SpPlan &VP, const SpSqGeo &G, const SpHierAttnArgs &HA,
-                                 const SpSqAttnArgs &A, float *ws, size_t ws_floats, int n_runs, hipStream_t s) {
+                                 const SpSqAttnArgs &A, const SpSeqTab &T, float *ws, size_t ws_floats, int n_runs,
+                                 hipStream_t s) {
     const int kind = sp_sqfree_attn_kind(KP, VP, G);
     if (!kind || A.n_kv <= 0 || A.n_q <= 0 || A.n_kvh <= 0 || A.n_q % A.n_kvh || A.n_q / A.n_kvh > 8 ||
-        n_runs <= 0 || n_runs > 1024 || A.pp < 4 + PAD || A.ps != HA.ps || A.pp != HA.pp)
+        n_runs <= 0 || n_runs > 1024 || A.pp < 4 + PAD || A.ps != HA.ps || A.pp != HA.pp || T.n_seq < 1 ||
+        T.n_seq > SP_ATTN_MAX_SEQ)
         return hipErrorInvalidValue;
-    if (sp_hier_attn_workspace_floats(HA, n_runs) > ws_floats) return hipErrorInvalidValue;
+    if (sp_hier_attn_workspace_floats(HA, n_runs, T.n_seq) > ws_floats) return hipErrorInvalidValue;
     float *prep = ws;
-    float *part = ws + (size_t)A.n_q * A.ps;
-    hipError_t e = sp_launch_hier_attn_prep(KP, HA, prep, s);
+    float *part = ws + (size_t)T.n_seq * A.n_q * A.ps;
+    hipError_t e = sp_launch_hier_attn_prep(KP, HA, T.n_seq, prep, s);
     if (e != hipSuccess) return e;
-    if (kind == 1) launch_split_g<77, SkelL77, SkelL77>(A, prep, part, n_runs, s);
-    else if (kind == 2) launch_split_g<115, SkelL115, SkelL115>(A, prep, part, n_runs, s);
-    else launch_split_g<115, SkelL115, SkelL115V3>(A, prep, part, n_runs, s);
+    if (kind == 1) launch_split_g<77, SkelL77, SkelL77>(A, T, prep, part, n_runs, s);
+    else if (kind == 2) launch_split_g<115, SkelL115, SkelL115>(A, T, prep, part, n_runs, s);
+    else launch_split_g<115, SkelL115, SkelL115V3>(A, T, prep, part, n_runs, s);
     e = hipGetLastError();
     if (e != hipSuccess || !A.out) return e;
-    return sp_launch_hier_attn_merge(KP, HA, part, n_runs, s);
+    return sp_launch_hier_attn_merge(KP, HA, T.n_seq, part, n_runs, s);
 }

@@ -241,6 +241,8 @@ def lib():
         L.sp_hip_hier_read_layer.argtypes = [vp, i, i, i, vp, vp, ll, i]
         L.sp_hip_hier_attn_decode.argtypes = [vp, i, i, vp, i, f, vp, vp, vp]
         L.sp_hip_sqfree_attn_decode.argtypes = [vp, i, i, vp, i, f, vp, vp, vp]
+        for name in ("sp_hip_attn_decode_seqs", "sp_hip_sqfree_attn_decode_seqs", "sp_hip_hier_attn_decode_seqs"):
+            getattr(L, name).argtypes = [vp, i, i, vp, vp, vp, i, f, vp, vp, vp]
         L.sp_hip_vht2_forward.argtypes = [vp, i, i, i, vp]
         L.sp_hip_band_quantize.argtypes = [vp, vp, vp, i, vp]
         L.sp_hip_band_dequantize.argtypes = [vp, vp, vp, i, vp]

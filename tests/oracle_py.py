@@ -292,7 +292,8 @@ def attn_decode(q, kpack, vpack, n_kvh, n_ctx, kbc, vbc, order, kq_scale, norm=N
     scores = np.zeros((n_q, n_ctx), np.float32) if want_scores else None
     out = np.zeros((n_q, hd), np.float32) if want_out else None
     o = None if order is None else np.ascontiguousarray(order, dtype=np.int32)
-    lib().spo_attn_decode_bands(ptr(q), ptr(np.ascontiguousarray(kpack)), ptr(np.ascontiguousarray(vpack)),
+    kc, vc = np.ascontiguousarray(kpack), np.ascontiguousarray(vpack)  # held across the call
+    lib().spo_attn_decode_bands(ptr(q), ptr(kc), ptr(vc),
                                 n_q, n_kvh, n_ctx, hd, C.byref(kbc), C.byref(vbc), ptr(o), norm,
                                 C.c_float(kq_scale), ptr(scores), ptr(out), max_bands)
     return scores, out
@@ -308,7 +309,8 @@ def hier_attn_decode(q, kpack, vpack, n_kvh, n_ctx, hd, pad, skel_idx, tgt_idx, 
     s = np.ascontiguousarray(skel_idx, dtype=np.int32)
     t = np.ascontiguousarray(tgt_idx, dtype=np.int32)
     w = np.ascontiguousarray(W, dtype=np.uint16)
-    lib().spo_hier_attn_decode(ptr(q), ptr(np.ascontiguousarray(kpack)), ptr(np.ascontiguousarray(vpack)),
+    kc, vc = np.ascontiguousarray(kpack), np.ascontiguousarray(vpack)  # held across the call
+    lib().spo_hier_attn_decode(ptr(q), ptr(kc), ptr(vc),
                                n_q, n_kvh, n_ctx, hd, pad, len(s), ptr(s), len(t), ptr(t), C.byref(skel_bc),
                                ptr(w), rbits, C.c_float(kq_scale), ptr(scores), ptr(out))
     return scores, out
@@ -321,7 +323,8 @@ def sqfree_attn_decode(q, kpack, vpack, n_kvh, n_ctx, hd, km, kbc, vbc, rbits, s
     n_q = q.shape[0]
     scores = np.zeros((n_q, n_ctx), np.float32) if want_scores else None
     out = np.zeros((n_q, hd), np.float32) if want_out else None
-    lib().spo_sqfree_attn_decode(ptr(q), ptr(np.ascontiguousarray(kpack)), ptr(np.ascontiguousarray(vpack)),
+    kc, vc = np.ascontiguousarray(kpack), np.ascontiguousarray(vpack)  # held across the call
+    lib().spo_sqfree_attn_decode(ptr(q), ptr(kc), ptr(vc),
                                  n_q, n_kvh, n_ctx, hd, C.byref(km.m), C.byref(kbc), C.byref(vbc), rbits,
                                  int(spinor), C.c_float(kq_scale), ptr(scores), ptr(out))
     return scores, out

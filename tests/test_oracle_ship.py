@@ -326,3 +326,22 @@ def test_band_limited_attention_oracle_matches_dense_softmax(mb):
     s_all, o_all = O.attn_decode(q, kp, vp, 2, 48, kbc, vbc, order, scale)
     np.testing.assert_array_equal(s4, s_all)
     np.testing.assert_array_equal(o4, o_all)
+
+
+def test_attention_oracle_takes_position_slices():
+    """A sequence's range of a longer cache (a non-contiguous [H][start:start+n] slice)
+    gives the same scores and output as the same records copied contiguously."""
+    k16, v16 = W.cfg2_kv(n_heads=2, n_pos=200, seed=21)
+    q = W.cfg2_q(n_q=4, pos=90, seed=22)
+    kbc, vbc = O.band_config(128, [5, 5, 4, 3]), O.band_config(128, [3])
+    order = O.mobius_order(128)
+    kp = np.stack([O.ship_compress_f16(k16[h].view(np.uint16), kbc, order) for h in range(2)])
+    vp = np.stack([O.ship_compress_f16(v16[h].view(np.uint16), vbc) for h in range(2)])
+    scale = 1 / math.sqrt(128)
+    for _ in range(3):  # allocations between calls would reuse a freed copy's memory
+        s, out = O.attn_decode(q, kp[:, 70:160], vp[:, 70:160], 2, 90, kbc, vbc, order, scale)
+        junk = [np.full(kp[:, 70:160].size, 255, np.uint8) for _ in range(4)]
+        s2, o2 = O.attn_decode(q, kp[:, 70:160].copy(), vp[:, 70:160].copy(), 2, 90, kbc, vbc, order, scale)
+        np.testing.assert_array_equal(s, s2)
+        np.testing.assert_array_equal(out, o2)
+        del junk
