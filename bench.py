@@ -152,6 +152,16 @@ def parity_sample(S, cc, k, v, kr, kB, vB, n_slots):
     return bad
 
 
+def seq_table(starts, lens):
+    """int32 start and length arrays of a batched attention call, each as (array, pointer)."""
+    import numpy as np
+    out = []
+    for v in (starts, lens):
+        a = np.ascontiguousarray(v, dtype=np.int32)
+        out.append((a, C.c_void_p(a.ctypes.data)))
+    return out[0], out[1]
+
+
 def bench_variants(torch, S, L, stream, reps=3):
     """Throughput of the other configs' codec paths at their per-GPU shapes (extra
     fields of the JSON line, not the headline): the configs[1] post-decode round
@@ -197,18 +207,22 @@ def bench_variants(torch, S, L, stream, reps=3):
         "k_dec": rate(n3, hd3, kB3, timed(lambda: S.check(L.sp_hip_read_all(c3.ref, 0, N3, P(y), None, S.DTYPE_F16, -1)))),
         "v_dec": rate(n3, hd3, vB3, timed(lambda: S.check(L.sp_hip_read_all(c3.ref, 0, N3, None, P(y), S.DTYPE_F16, -1)))),
         "record_bytes": [kB3, vB3]}
-    c3.free()
-    # configs[2] decode: the same 16 sequences x 4096 cells, one sequence per cache layer (32 heads,
-    # MHA), fused decompress-attention for every sequence of one layer step (16 calls, 32 query heads
-    # each) through the general kernel (hd 96: Vilenkin 2^5*3)
+    # configs[2] decode, batched: the 16 sequences as position ranges [4096 i, 4096 (i + 1)) of this
+    # layer (K and V records from the writes above), one fused attention call for all of them
     NS3, NP3 = 16, 4096
+    q3 = torch.randn((NS3, H3, hd3), generator=g, device="cuda")
+    o3 = torch.empty((NS3, H3, hd3), device="cuda")
+    sc3 = C.c_float(1.0 / math.sqrt(hd3))
+    st3, ln3 = seq_table([NP3 * i for i in range(NS3)], [NP3] * NS3)
+    t16b = timed(lambda: S.check(L.sp_hip_attn_decode_seqs(c3.ref, 0, NS3, st3[1], ln3[1], P(q3), H3, sc3, None,
+                                                           P(o3), sp), "cfg2 attn seqs"))
+    c3.free()
+    # the same step as 16 single-sequence calls, one sequence per cache layer (distinct records, so
+    # no call reads what an earlier one left in the caches)
     c3d = S.ShipCache(S.config(hd3, NS3, H3, k_bits=(5, 4, 4), v_bits=(5,)), NP3, stream.cuda_stream)
     xs = x.view(H3, NS3, NP3, hd3).transpose(0, 1).contiguous()  # [sequence][head][cell][d]
     S.check(L.sp_hip_write_all(c3d.ref, 0, NP3, P(xs), P(xs), S.DTYPE_F16), "cfg2 prefill")
     del xs
-    q3 = torch.randn((NS3, H3, hd3), generator=g, device="cuda")
-    o3 = torch.empty((NS3, H3, hd3), device="cuda")
-    sc3 = C.c_float(1.0 / math.sqrt(hd3))
 
     def dec16():
         for sq in range(NS3):
@@ -216,12 +230,15 @@ def bench_variants(torch, S, L, stream, reps=3):
     t16 = timed(dec16)
     rec3 = NS3 * H3 * NP3 * (kB3 + vB3)
     out["cfg3_hd96_decode"] = {
-        "step_layer_us": round(t16 * 1e6, 1), "us_per_token_32_layers": round(32 * t16 * 1e6, 1),
-        "decode_tokens_per_s": round(NS3 / (32 * t16), 1), "record_gbs": round(rec3 / t16 / 1e9, 1),
+        "step_layer_us": round(t16b * 1e6, 1), "us_per_token_32_layers": round(32 * t16b * 1e6, 1),
+        "decode_tokens_per_s": round(NS3 / (32 * t16b), 1), "record_gbs": round(rec3 / t16b / 1e9, 1),
+        "step_layer_us_16_calls": round(t16 * 1e6, 1),
         "record_floor_us": round(rec3 / (HBM_PEAK_GBS * 1e3), 1),
         "fp16_floor_us": round(NS3 * H3 * NP3 * 2 * hd3 * 2 / (HBM_PEAK_GBS * 1e3), 1),
         "layout": f"{NS3} sequences x {NP3} positions x {H3} heads (MHA), hd {hd3}, K 5/4/4 + V 5 records "
-                  f"({kB3} + {vB3} B); per layer step: {NS3} fused attention calls (general kernel)"}
+                  f"({kB3} + {vB3} B); per layer step: one batched fused attention call "
+                  f"(sp_hip_attn_decode_seqs, one-position-per-lane kernel); step_layer_us_16_calls: "
+                  f"{NS3} single-sequence calls"}
     c3d.free()
     del x, y
     # configs[1] post-decode hook on the device: sp_hip_roundtrip_cells over one layer's 8 heads,
@@ -361,15 +378,14 @@ def bench_variants(torch, S, L, stream, reps=3):
                                  "record_bytes": [B4, B4v], "pad_dim": pad4, "skeleton": c4.c.sk_k,
                                  "calls": f"{L4} layers x {H4} heads x {N4} positions, one call per layer and side "
                                           f"(enc/dec: K 5/4/4/4/5; v_enc/v_dec: V one 3-bit band)"}
-    # configs[3] decode: fused attention over the sqfree records, batch 4 (layers 0-3 of the cache
-    # above are the four sequences; each holds 4 KV heads x 16384 positions of K and V), 32 query heads
-    # per sequence (GQA 8)
+    # configs[3] decode: fused attention over the sqfree records, batch 4: the four sequences are the
+    # position ranges [16384 i, 16384 (i + 1)) of one cache layer (4 KV heads; K and V from distinct
+    # rows), 32 query heads per sequence (GQA 8)
     NA4, NQ4, NB4 = 16384, 32, 4
-    c4a = S.SqfreeCache(S.config(128, NB4, H4, k_bits=bits4, v_bits=(3,)), NA4, rbits=3, spinor=True,
+    c4a = S.SqfreeCache(S.config(128, 1, H4, k_bits=bits4, v_bits=(3,)), NB4 * NA4, rbits=3, spinor=True,
                         sk_k=int(pad4 * 0.75), stream=stream.cuda_stream)
-    for sq in range(NB4):
-        S.check(L.sp_hip_sqfree_write_layer(c4a.ref, sq, 0, NA4, P(x[sq, :NA4]), P(x[sq, NA4:2 * NA4]), H4 * 128,
-                                            S.DTYPE_F16))
+    S.check(L.sp_hip_sqfree_write_layer(c4a.ref, 0, 0, NB4 * NA4, P(x[0, :NB4 * NA4]), P(x[1, :NB4 * NA4]),
+                                        H4 * 128, S.DTYPE_F16))
     q4 = torch.randn((NB4, NQ4, 128), generator=g, device="cuda")
     o4 = torch.empty((NB4, NQ4, 128), device="cuda")
     s4 = torch.empty((NQ4, NA4), device="cuda")
@@ -377,20 +393,20 @@ def bench_variants(torch, S, L, stream, reps=3):
     t_one = timed(lambda: S.check(L.sp_hip_sqfree_attn_decode(c4a.ref, 0, NA4, P(q4[0]), NQ4, sc4, None, P(o4[0]),
                                                               sp)))
     t_kq4 = timed(lambda: S.check(L.sp_hip_sqfree_attn_decode(c4a.ref, 0, NA4, P(q4[0]), NQ4, sc4, P(s4), None, sp)))
-
-    def dec4():
-        for sq in range(NB4):
-            S.check(L.sp_hip_sqfree_attn_decode(c4a.ref, sq, NA4, P(q4[sq]), NQ4, sc4, None, P(o4[sq]), sp))
-    t_b4 = timed(dec4)
+    st4, ln4 = seq_table([NA4 * i for i in range(NB4)], [NA4] * NB4)
+    t_b4 = timed(lambda: S.check(L.sp_hip_sqfree_attn_decode_seqs(c4a.ref, 0, NB4, st4[1], ln4[1], P(q4), NQ4, sc4,
+                                                                  None, P(o4), sp)))
     rec4 = H4 * NA4 * (B4 + B4v)
     out["cfg4_sqfree_fused_attn"] = {
         "layer_us": round(t_one * 1e6, 1), "kq_only_layer_us": round(t_kq4 * 1e6, 1),
         "batch4_step_layer_us": round(t_b4 * 1e6, 1), "us_per_step_48_layers": round(48 * t_b4 * 1e6, 1),
         "decode_tokens_per_s_48_layers": round(NB4 / (48 * t_b4), 1),
-        "record_gbs": round(rec4 / t_one / 1e9, 1), "record_floor_us": round(rec4 / (HBM_PEAK_GBS * 1e3), 2),
+        "record_gbs": round(rec4 / t_one / 1e9, 1), "batch4_record_gbs": round(NB4 * rec4 / t_b4 / 1e9, 1),
+        "record_floor_us": round(rec4 / (HBM_PEAK_GBS * 1e3), 2),
         "fp16_layer_floor_us": round(H4 * NA4 * 2 * 128 * 2 / (HBM_PEAK_GBS * 1e3), 2),
         "layout": f"{H4} KV heads x {NA4} positions, {NQ4} query heads (GQA 8), K {B4} B + V {B4v} B records "
-                  f"(pad {pad4}, skeleton {c4a.c.sk_k}); layer_us per sequence, batch4_step = {NB4} calls"}
+                  f"(pad {pad4}, skeleton {c4a.c.sk_k}); layer_us: one sequence's call; batch4_step: one "
+                  f"batched call (sp_hip_sqfree_attn_decode_seqs) over {NB4} sequences"}
     c4a.free()
     c4.free()
     del x, y
@@ -489,28 +505,25 @@ def bench_variants(torch, S, L, stream, reps=3):
     c6.free()
     c5.free()
     # configs[4] sustained: batch-8 decode interleaved with prefill-chunk compression. Eight
-    # sequences are the eight layers of one cache (131072 positions each, K and V from distinct
-    # rows); one step of a layer decodes all eight (fused attention, 16 query heads each) and
-    # compresses one 2048-token chunk of a ninth sequence's new K and V (8 heads) into its
-    # positions [131072, 133120)
+    # sequences are the position ranges [131072 i, 131072 (i + 1)) of one cache layer (8 KV heads;
+    # K from the rows above, V from their decoded copy); one step of a layer decodes all eight
+    # (one batched fused attention call, 16 query heads each) and compresses one 2048-token chunk of a
+    # ninth sequence's new K and V into the layer's positions [1048576, 1050624)
     NB, CHK = 8, 2048
-    c7 = S.HierCache(S.config(hd5, NB + 1, H5), pad5, sk, tg, S.band_config(n_sk, [5, 5]), 2, NA + CHK,
-                     (NB + 1) * H5, stream=stream.cuda_stream)
-    c7.upload_W(np.tile(Wh.view(np.uint16), (NB + 1, 1, 1)))
-    for sq in range(NB):
-        r0 = (sq * NA) % (N5 - NA)
-        S.check(L.sp_hip_hier_write_layer(c7.ref, sq, 0, NA, P(x[r0:r0 + NA]), P(x[r0 + 1:r0 + 1 + NA]), H5 * hd5,
-                                          S.DTYPE_F16))
+    c7 = S.HierCache(S.config(hd5, 1, H5), pad5, sk, tg, S.band_config(n_sk, [5, 5]), 2, NB * NA + CHK, H5,
+                     stream=stream.cuda_stream)
+    c7.upload_W(Wh.view(np.uint16))
+    S.check(L.sp_hip_hier_write_layer(c7.ref, 0, 0, NB * NA, P(x), P(y), H5 * hd5, S.DTYPE_F16))
     q8 = torch.randn((NB, NQ5, hd5), generator=g, device="cuda")
     o8 = torch.empty((NB, NQ5, hd5), device="cuda")
     kc, vc = x[:CHK], x[CHK:2 * CHK]
+    st8, ln8 = seq_table([NA * i for i in range(NB)], [NA] * NB)
 
     def decode8():
-        for sq in range(NB):
-            S.check(L.sp_hip_hier_attn_decode(c7.ref, sq, NA, P(q8[sq]), NQ5, sc5, None, P(o8[sq]), sp))
+        S.check(L.sp_hip_hier_attn_decode_seqs(c7.ref, 0, NB, st8[1], ln8[1], P(q8), NQ5, sc5, None, P(o8), sp))
 
     def chunk():
-        S.check(L.sp_hip_hier_write_layer(c7.ref, NB, NA, CHK, P(kc), P(vc), H5 * hd5, S.DTYPE_F16))
+        S.check(L.sp_hip_hier_write_layer(c7.ref, 0, NB * NA, CHK, P(kc), P(vc), H5 * hd5, S.DTYPE_F16))
 
     def step():
         decode8()
@@ -522,8 +535,10 @@ def bench_variants(torch, S, L, stream, reps=3):
         "chunk_layer_us": round(t_chunk * 1e6, 1),
         "chunk_vecs_per_s": round(2 * H5 * CHK / t_chunk, 1),
         "decode_tokens_per_s_34_layers": round(NB / (34 * t_step), 1),
+        "decode8_record_gbs": round(NB * rec_b / t_dec8 / 1e9, 1),
         "layout": f"{NB} sequences x {NA} positions x {H5} KV heads, {NQ5} query heads each, hd {hd5} (pad {pad5}); "
-                  f"per layer and step: {NB} fused attention calls, then one {CHK}-token K+V chunk compressed"}
+                  f"per layer and step: one batched fused attention call (sp_hip_hier_attn_decode_seqs) over "
+                  f"{NB} sequences, then one {CHK}-token K+V chunk compressed"}
     c7.free()
     return out
 
