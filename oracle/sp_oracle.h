@@ -37,6 +37,15 @@
  *     the strict spinor comparison, the serial predictor order, the 256-slot
  *     reduction order; mu(n) against known values and the Mertens function;
  *     the Knight CSR against a brute-force divisor enumeration.
+ *   - attention (spo_attn_decode_bands): a dense float64 softmax over the
+ *     separately pinned decompressions, band-limited calls included.
+ *   - hier and sqfree attention (spo_hier_attn_decode, spo_sqfree_attn_decode):
+ *     against their definitions (the pinned decompressions, then a float64
+ *     softmax with the GQA grouping) and against a float64 numpy restatement of
+ *     the coefficient-domain algebra from the record layout alone (zero-padded
+ *     query transform; hier: u = q~_skel + W^T q~_tgt; sqfree: the sheet sign on
+ *     the prediction, step = 2 mag rbits / (L - 1)), tests/test_oracle_hier_attn.py
+ *     and tests/test_oracle_sqfree_attn.py.
  *   - Mobius order, Knight skeleton/CSR construction rule, hier geometry: the
  *     construction rules are NOT fixed by the reference (the builder lives in
  *     the absent core); they are host-side index tables, the tests pin this
