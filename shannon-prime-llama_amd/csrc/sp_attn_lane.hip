@@ -77,13 +77,17 @@ k_attn_lane_split(const unsigned char *__restrict__ kc0, const unsigned char *__
     const int c2i = C2 > 0 ? lane % C2 : 0, hh = C2 > 0 ? lane / C2 : 0;
     const bool c2_on = C2 > 0 && hh < (HALVES ? 2 : 1);
 
+    // both record streams run one tile ahead: the next tile's K loads once this tile's
+    // K records are out of the stage, its V once this tile's V records are
     RecTile<LK> Rk;
+    RecTile<LV> Rv;
     int c = run;
-    if (c < tpo) rec_tile_load<LK>(Rk, kc, k_slot, M, kvh * tpo + c, n_tiles, lane);
+    if (c < tpo) {
+        rec_tile_load<LK>(Rk, kc, k_slot, M, kvh * tpo + c, n_tiles, lane);
+        if (OUT) rec_tile_load<LV>(Rv, vc, v_slot, M, kvh * tpo + c, n_tiles, lane);
+    }
     for (; c < tpo; c += n_runs) {
         const int t = kvh * tpo + c;
-        RecTile<LV> Rv;
-        if (OUT) rec_tile_load<LV>(Rv, vc, v_slot, M, t, n_tiles, lane);
         __syncthreads();  // the previous tile is done with the stage
         rec_tile_stage<LK>(Rk, stage, M, t, lane);
         __syncthreads();
@@ -133,6 +137,7 @@ k_attn_lane_split(const unsigned char *__restrict__ kc0, const unsigned char *__
         __syncthreads();
         uint32_t rv[LV::dwords];
         rec_from_lds<LV>(rv, stage, lane);
+        if (c + n_runs < tpo) rec_tile_load<LV>(Rv, vc, v_slot, M, t + n_runs, n_tiles, lane);
         float ev[HD];
         dequant_bands<LV, false, false>(rv, vmb, ev);
 #pragma unroll

@@ -222,6 +222,72 @@ __device__ __forceinline__ half8_t level_pairs2(uint32_t y) {
     return __builtin_bit_cast(half8_t, v);
 }
 
+typedef __attribute__((address_space(3))) const uint32_t lds_cu32;
+
+// LDS byte address of p (a pointer into the kernel's shared memory) as a plain value:
+// the compiler then folds constant offsets into the LDS reads instead of re-adding
+// the shared array's address at every use.
+__device__ __forceinline__ uint32_t lds_addr(const unsigned char *p) {
+    uint32_t a = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const unsigned char *)p;
+    __asm__ volatile("" : "+v"(a));
+    return a;
+}
+
+// The eight positions' fields of one V row-block operand: position e's field starts
+// at bit sh[e] of the dword pair at LDS byte address ad[e] + off; all sixteen dwords
+// are read before the funnel shifts, so the reads overlap.
+__device__ __forceinline__ void vm_fields(const uint32_t (&ad)[8], const uint32_t (&sh)[8], int off,
+                                          uint32_t (&x)[8]) {
+    uint32_t d[8][2];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        lds_cu32 *w = (lds_cu32 *)(uintptr_t)(ad[e] + off);
+        d[e][0] = w[0];
+        d[e][1] = w[1];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e++) x[e] = __builtin_amdgcn_alignbit(d[e][1], d[e][0], sh[e]);
+}
+
+// The dwords holding eight positions' 2-bit levels (a level's bit offset 8 * byte +
+// 2 * coefficient is even, so it never crosses a dword).
+__device__ __forceinline__ void vm_level_dwords(const uint32_t (&ad)[8], int off, uint32_t (&d)[8]) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) d[e] = *(lds_cu32 *)(uintptr_t)(ad[e] + off);
+}
+
+// A operand of the V level sums (v_mfma_f32_16x16x32_f16, rows = coefficients, K =
+// positions): the lane's 2-bit level at eight positions as fp16 level - 1.5 (exact).
+// With each level shifted to bits 0-1, a byte permute takes the pair (e, e + 1) into
+// bytes 1 and 3, the and-or makes fp16 4 + level in both halves, and a packed subtract
+// of 5.5 centres it.
+__device__ __forceinline__ half8_t vm_levels(const uint32_t (&d)[8], const uint32_t (&sh)[8]) {
+    uint32_t x[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) x[e] = d[e] >> sh[e];
+    u32x4 v;
+#pragma unroll
+    for (int m = 0; m < 4; m++)
+        v[m] = __builtin_amdgcn_bitop3_b32(__builtin_amdgcn_perm(x[2 * m + 1], x[2 * m], 0x040C000Cu), 0x03000300u,
+                                           0x44004400u, 0xEA);
+    return __builtin_bit_cast(half8_t, v) - (_Float16)5.5f;
+}
+
+// The same for a skeleton band's `bits`-bit codes (bits <= 8): fp16 2^bits + code from the
+// code's byte (exponent bits `base`, the code shifted by 10 - bits under `mask`), minus
+// `sub` = 2^bits + the band's offset (exact).
+__device__ __forceinline__ half8_t vm_codes(const uint32_t (&ad)[8], const uint32_t (&sh)[8], int off,
+                                            uint32_t sh10, uint32_t mask, uint32_t base, _Float16 sub) {
+    uint32_t x[8];
+    vm_fields(ad, sh, off, x);
+    u32x4 v;
+#pragma unroll
+    for (int m = 0; m < 4; m++)
+        v[m] = __builtin_amdgcn_bitop3_b32(__builtin_amdgcn_perm(x[2 * m + 1], x[2 * m], 0x0C040C00u) << sh10, mask,
+                                           base, 0xEA);
+    return __builtin_bit_cast(half8_t, v) - sub;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, SP_WAVE);
@@ -335,7 +401,11 @@ k_hier_attn_prep(const SpPlan P, const SpHierAttnArgs A, float *__restrict__ pre
 // Partial per (query head, run): [m, l, -, -, c_skel sum (n_skel), dev sum (n_target)].
 // OUT = false: scores only (no V half), with the next chunk's K records prefetched
 // into registers while the current chunk's scores run.
-template <int RB, int GM, bool OUT>
+// VM (RB == 2, OUT): the V coefficient sums on the matrix cores instead of the window
+// items. pw and psb then hold the weights as fp16 hi and lo rows ([h][hi, lo][CH] and
+// [b][h][hi, lo][CH], the same bytes), scaled by a power of two per chunk; the sums
+// need no position-group reduction at the end of the run.
+template <int RB, int GM, bool OUT, bool VM>
 __global__ void __launch_bounds__(NT, 3)
 k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, const float *__restrict__ prep0,
                   float *__restrict__ part0, int n_runs) {
@@ -453,6 +523,32 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
     const int s_bits = P.band_bits[s_b], s_bo = (s_s - P.band_off[s_b]) * s_bits;
     const int s_byte = P.band_byte_off[s_b] + 2 + (s_bo >> 3), s_bit = s_bo & 7;
     const float s_off = (float)((1 << (s_bits - 1)) - 1);
+
+    // VM: row blocks of 16 coefficients. Target window wv + 4 i (i < VM_TB) belongs to
+    // wave wv: every wave runs VM_TB of them (the launcher takes 4 VM_TB - 3 .. 4 VM_TB
+    // windows; a window past the last reads the record tail and is never written out).
+    // The skeleton bands in blocks of 16 follow: block k to wave (n_win + k) % 4, at most
+    // one per wave (the launcher checks). Sums per (coefficient, column) in the
+    // v_mfma_f32_16x16x32_f16 accumulator layout, kept across the chunks: lane = column
+    // (head jc >> 1, hi / lo part jc & 1) of rows 4 kq .. 4 kq + 3.
+    constexpr int VM_TB = 5;
+    int vm_nsb = 0;
+    if (VM)
+        for (int b = 0; b < nb; b++) vm_nsb += (P.band_sz[b] + 15) >> 4;
+    // this wave's skeleton block (vm_s), band vm_b, coefficients 16 vm_k ..
+    bool vm_s = false;
+    int vm_b = 0, vm_k = 0;
+    if (VM) {
+        int sb = ((wv - n_win) % 4 + 4) % 4;
+        if (sb < vm_nsb) {
+            vm_s = true;
+            while (vm_b + 1 < nb && sb >= ((P.band_sz[vm_b] + 15) >> 4)) sb -= (P.band_sz[vm_b++] + 15) >> 4;
+            vm_k = sb;
+        }
+    }
+    float4_t vacc[VM ? VM_TB : 1], vsk = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < (VM ? VM_TB : 1); i++) vacc[i] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
     const int n_chunks = (A.n_kv + CH - 1) / CH;
     // scores only: chunk ch's K records wait in registers (kst) from the previous chunk on
@@ -631,6 +727,105 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
         const int vdw = (n_t * B + vshift + 3) >> 2;
         copy_to_lds<uint32_t, 32>(rec32, reinterpret_cast<const uint32_t *>(vg - vshift), vdw, vdw + 3, tid);
         __syncthreads();
+        if constexpr (VM) {
+            // ---- weights as fp16 hi + lo rows, scaled by f (a power of two putting the
+            // chunk's largest step or band scale in [2^11, 2^12); every p <= 1) ----
+            const int rb = vshift + tid * B;
+            const bool live = tid < n_t;
+            const float vstep = live ? sp_div(2.0f * __uint_as_float(lds_u32_at(rec, rb + skB)), step_div) : 0.0f;
+            float wmax = vstep;
+            for (int b = 0; b < nb; b++)
+                if (live) wmax = fmaxf(wmax, sp_scale_from_bits(lds_u32_at(rec, rb + P.band_byte_off[b]) & 0xffffu));
+            wmax = sp_wave_max(wmax);
+            if (lane == 0) red[wv] = wmax;
+            __syncthreads();
+            const float f = pow2_norm(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+            _Float16 *pwq = reinterpret_cast<_Float16 *>(pw);
+            _Float16 *psq = reinterpret_cast<_Float16 *>(psb);
+            for (int h = 0; h < G; h++) {
+                const float v = sc[h * CH + tid] * vstep * f;
+                const _Float16 hi = (_Float16)v;
+                pwq[(2 * h) * CH + tid] = hi;
+                pwq[(2 * h + 1) * CH + tid] = (_Float16)(v - (float)hi);
+            }
+            for (int b = 0; b < nb; b++) {
+                const float scale =
+                    live ? sp_scale_from_bits(lds_u32_at(rec, rb + P.band_byte_off[b]) & 0xffffu) : 0.0f;
+                for (int h = 0; h < G; h++) {
+                    const float v = sc[h * CH + tid] * scale * f;
+                    const _Float16 hi = (_Float16)v;
+                    psq[((b * G + h) * 2) * CH + tid] = hi;
+                    psq[((b * G + h) * 2 + 1) * CH + tid] = (_Float16)(v - (float)hi);
+                }
+            }
+            __syncthreads();
+            // ---- the wave's row blocks over the chunk's 32-position groups: rows =
+            // coefficients (lane jc of the block), K = positions 8 kq .. 8 kq + 7 of the
+            // group, columns = (head, hi / lo) ----
+            const int jc = lane & 15, kq = lane >> 4;
+            float ac = 1.0f;  // the column's alpha, times f: the run's sums rescaled to this chunk
+#pragma unroll
+            for (int h = 0; h < GM; h++)
+                if (h == (jc >> 1)) ac = alpha[h];
+            ac *= f;
+#pragma unroll
+            for (int i = 0; i < VM_TB; i++) vacc[i] *= ac;
+            vsk *= ac;
+            // dword address and bit shift of each K position's first row-block field at
+            // group 0 (the groups step by 32 B bytes, a whole number of dwords)
+            uint32_t ta[8], tsh[8], sa[8], ssh[8];
+            const uint32_t rec_lds = lds_addr(rec);
+            const int vbits = P.band_bits[vm_b];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int p0 = vshift + (8 * kq + e) * B;
+                const int tb = 8 * (p0 + skB + 4 + 4 * wv) + 2 * jc;
+                ta[e] = rec_lds + ((uint32_t)(tb >> 5) << 2);
+                tsh[e] = (uint32_t)tb & 31u;
+                const int sbp = 8 * (p0 + P.band_byte_off[vm_b] + 2) + vbits * (16 * vm_k + jc);
+                sa[e] = rec_lds + ((uint32_t)(sbp >> 5) << 2);
+                ssh[e] = (uint32_t)sbp & 31u;
+            }
+            const uint32_t sh10 = 10u - (uint32_t)vbits;
+            const uint32_t smask = (((1u << vbits) - 1u) << sh10) * 0x00010001u;
+            const uint32_t sbase = ((15u + (uint32_t)vbits) << 10) * 0x00010001u;
+            const _Float16 ssub = (_Float16)(float)((1 << vbits) + (1 << (vbits - 1)) - 1);
+            const bool col_on = jc < 2 * G;
+            const _Float16 *bsrow = psq + ((vm_b * G + (jc >> 1)) * 2 + (jc & 1)) * CH;
+            const int ng = (n_t + 31) >> 5;
+            const uint32_t gstep = 32u * (uint32_t)B;  // bytes per group: the addresses advance in place
+            for (int g = 0; g < ng; g++) {
+                const int pq = 32 * g + 8 * kq;
+                half8_t bt = {}, bsk = {};
+                if (col_on) {
+                    bt = *reinterpret_cast<const half8_t *>(pwq + jc * CH + pq);
+                    if (vm_s) bsk = *reinterpret_cast<const half8_t *>(bsrow + pq);
+                }
+                if (vm_s) {
+                    const half8_t a = vm_codes(sa, ssh, 0, sh10, smask, sbase, ssub);
+                    vsk = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bsk, vsk, 0, 0, 0);
+                }
+                // window i + 1's dwords are read while window i converts
+                uint32_t dw[2][8];
+                vm_level_dwords(ta, 0, dw[0]);
+#pragma unroll
+                for (int i = 0; i < VM_TB; i++) {
+                    if (i + 1 < VM_TB) vm_level_dwords(ta, 16 * (i + 1), dw[(i + 1) & 1]);
+                    const half8_t a = vm_levels(dw[i & 1], tsh);
+                    vacc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bt, vacc[i], 0, 0, 0);
+                }
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    ta[e] += gstep;
+                    sa[e] += gstep;
+                }
+            }
+            const float inv_f = 1.0f / f;  // exact: f is a power of two
+#pragma unroll
+            for (int i = 0; i < VM_TB; i++) vacc[i] *= inv_f;
+            vsk *= inv_f;
+            continue;
+        }
         {
             const int rb = vshift + tid * B;
             const bool live = tid < n_t;
@@ -734,6 +929,29 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
             dst[0] = m_run[h];
             dst[1] = l_run[h];
         }
+    }
+    if constexpr (VM) {
+        // hi + lo columns (lane jc and jc + 1), one coefficient per accumulator row
+        const int jc = lane & 15, kq = lane >> 4;
+        const int h = jc >> 1;
+        float *dst = part + ((long long)(h0 + h) * n_runs + run) * pp + 4;
+        const bool col = !(jc & 1) && h < G;
+#pragma unroll
+        for (int i = 0; i < VM_TB; i++) {
+#pragma unroll
+            for (int ii = 0; ii < 4; ii++) {
+                const float v = add_xor1(vacc[i][ii]);
+                const int c = 16 * (wv + 4 * i) + 4 * kq + ii;
+                if (col && c < nt) dst[ns + c] = v;
+            }
+        }
+#pragma unroll
+        for (int ii = 0; ii < 4; ii++) {
+            const float v = add_xor1(vsk[ii]);
+            const int c = 16 * vm_k + 4 * kq + ii;
+            if (vm_s && col && c < P.band_sz[vm_b]) dst[P.band_off[vm_b] + c] = v;
+        }
+        return;
     }
     if (RB > 0) {
         // position groups' sums through LDS: Tr [npg_t][G][n_win * LPW], Sr [npg_s][G][ns]
@@ -887,21 +1105,53 @@ int window_bits(const SpHierAttnArgs &A) {
     return rb;
 }
 
+// Whether the V sums of a full (2-bit level) call run on the matrix cores: skeleton
+// bands of at most 8 bits, at most 4 skeleton row blocks (one per wave), and 17-20
+// target windows (257-320 target coefficients, five windows per wave: a window past the
+// last reads at most 19 bytes past its record, inside the staging memory's 32-byte slack); the launcher
+// takes it up to 4 query heads per KV head (more keep the window items).
+// SP_HIP_HIER_ATTN_VM=0 (read at each call) keeps the window items.
+bool vm_ok(const SpPlan &P, const SpHierAttnArgs &A) {
+    if (A.rbits != 2) return false;
+    int nsb = 0;
+    for (int b = 0; b < P.n_bands; b++) {
+        if (P.band_bits[b] < 1 || P.band_bits[b] > 8) return false;
+        nsb += (P.band_sz[b] + 15) / 16;
+    }
+    const int n_win = (A.n_target * 2 + 31) / 32;  // five per wave, the last wave's fifth maybe past the end
+    if (nsb > 4 || n_win < 17 || n_win > 20) return false;
+    const char *e = getenv("SP_HIP_HIER_ATTN_VM");
+    return !(e && e[0] == '0');
+}
+
 // The split kernel's instance for this call's level width and output mode.
 template <bool OUT>
 void launch_split(const SpPlan &P, const SpHierAttnArgs &A, const SpSeqTab &T, const float *prep, float *part,
-                  int n_runs, int rb, int G, size_t lds_split, hipStream_t s) {
+                  int n_runs, int rb, int G, bool vm, size_t lds_split, hipStream_t s) {
     const dim3 grid(A.n_kvh, n_runs, T.n_seq);
-    if (rb == 2 && G <= 2)
-        hipLaunchKernelGGL((k_hier_attn_split<2, 2, OUT>), grid, dim3(NT), lds_split, s, P, A, T, prep, part, n_runs);
-    else if (rb == 2)
-        hipLaunchKernelGGL((k_hier_attn_split<2, MAX_G, OUT>), grid, dim3(NT), lds_split, s, P, A, T, prep, part, n_runs);
-    else if (rb == 4)
-        hipLaunchKernelGGL((k_hier_attn_split<4, MAX_G, OUT>), grid, dim3(NT), lds_split, s, P, A, T, prep, part, n_runs);
-    else if (rb == 8)
-        hipLaunchKernelGGL((k_hier_attn_split<8, MAX_G, OUT>), grid, dim3(NT), lds_split, s, P, A, T, prep, part, n_runs);
-    else
-        hipLaunchKernelGGL((k_hier_attn_split<0, MAX_G, OUT>), grid, dim3(NT), lds_split, s, P, A, T, prep, part, n_runs);
+    if (rb == 2 && G <= 2) {
+        if (OUT && vm)
+            hipLaunchKernelGGL((k_hier_attn_split<2, 2, OUT, OUT>), grid, dim3(NT), lds_split, s, P, A, T, prep, part,
+                               n_runs);
+        else
+            hipLaunchKernelGGL((k_hier_attn_split<2, 2, OUT, false>), grid, dim3(NT), lds_split, s, P, A, T, prep, part,
+                               n_runs);
+    } else if (rb == 2 && G <= 4 && OUT && vm) {
+        hipLaunchKernelGGL((k_hier_attn_split<2, 4, OUT, OUT>), grid, dim3(NT), lds_split, s, P, A, T, prep, part,
+                           n_runs);
+    } else if (rb == 2) {
+        hipLaunchKernelGGL((k_hier_attn_split<2, MAX_G, OUT, false>), grid, dim3(NT), lds_split, s, P, A, T, prep, part,
+                           n_runs);
+    } else if (rb == 4) {
+        hipLaunchKernelGGL((k_hier_attn_split<4, MAX_G, OUT, false>), grid, dim3(NT), lds_split, s, P, A, T, prep, part,
+                           n_runs);
+    } else if (rb == 8) {
+        hipLaunchKernelGGL((k_hier_attn_split<8, MAX_G, OUT, false>), grid, dim3(NT), lds_split, s, P, A, T, prep, part,
+                           n_runs);
+    } else {
+        hipLaunchKernelGGL((k_hier_attn_split<0, MAX_G, OUT, false>), grid, dim3(NT), lds_split, s, P, A, T, prep, part,
+                           n_runs);
+    }
 }
 
 }  // namespace
@@ -947,8 +1197,9 @@ hipError_t sp_launch_hier_attn(const SpPlan &P, const SpHierAttnArgs &A, const S
     float *prep = ws;
     float *part = ws + (size_t)T.n_seq * A.n_q * A.ps;
     hipLaunchKernelGGL(k_hier_attn_prep, dim3(T.n_seq * A.n_q), dim3(NT), lds_prep, s, P, A, prep);
-    if (A.out) launch_split<true>(P, A, T, prep, part, n_runs, rb, G, lds_split, s);
-    else launch_split<false>(P, A, T, prep, part, n_runs, rb, G, lds_split, s);
+    const bool vm = rb == 2 && vm_ok(P, A);
+    if (A.out) launch_split<true>(P, A, T, prep, part, n_runs, rb, G, vm, lds_split, s);
+    else launch_split<false>(P, A, T, prep, part, n_runs, rb, G, vm, lds_split, s);
     if (A.out)
         hipLaunchKernelGGL(k_hier_attn_merge, dim3(T.n_seq * A.n_q), dim3(NT), lds_merge, s, P, A, part, n_runs);
     return hipGetLastError();

@@ -275,7 +275,8 @@ struct SpSqAttnArgs {
 // 1..3: the lane specialization serving this geometry (skeleton 77 with 5/4/4/4/5 K and
 // V; 115 with 5/4/4/4/5 K and V; 115 with V one 3-bit band), 0: none
 int sp_sqfree_attn_kind(const SpPlan &KP, const SpPlan &VP, const SpSqGeo &G);
-int sp_sqfree_attn_runs(int n_kvh, int n_kv, int cus, int n_seq = 1);
+int sp_sqfree_attn_runs(const SpPlan &KP, const SpPlan &VP, const SpSqGeo &G, int n_q, int n_kvh, int n_kv, int cus,
+                        int n_seq, bool out);
 // HA: the prep/merge arguments (pad, skeleton/residual index tables as skel_idx /
 // tgt_idx, W null, q, kq_scale, out); ws: prep [n_seq * n_q * ps] then partials.
 hipError_t sp_launch_sqfree_attn(const SpPlan &KP, const SpPlan &VP, const SpSqGeo &G, const SpHierAttnArgs &HA,

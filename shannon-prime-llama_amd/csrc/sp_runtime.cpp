@@ -1296,7 +1296,7 @@ extern "C" int sp_hip_sqfree_attn_decode_seqs(const sp_hip_sqfree_cache_t *cc, i
     A.ps = HA.ps;
     A.qo = (HA.n_skel + 3) & ~3;  // the prepared query's residual part
     A.pp = HA.pp;
-    int n_runs = sp_sqfree_attn_runs(H, T.max_len, cu_count(), n_seq);
+    int n_runs = sp_sqfree_attn_runs(pv->kplan, pv->vplan, GK, n_q, H, T.max_len, cu_count(), n_seq, d_out != nullptr);
     // SP_HIP_SQFREE_ATTN_RUNS=n caps the runs per KV head (read at each call; tests use it
     // to give every run several tiles at small context lengths)
     if (const char *e = getenv("SP_HIP_SQFREE_ATTN_RUNS")) {

@@ -116,13 +116,17 @@ k_sqfree_attn_split(const unsigned char *__restrict__ kc0, const unsigned char *
     const int c2i = lane % C2, hh = lane / C2;
     const bool c2_on = hh < (GM > 1 ? 2 : 1);
 
+    // both record streams run one tile ahead: the next tile's K loads once this tile's
+    // K records are out of the stage, its V once this tile's V records are
     RecTile<GK> Rk;
+    RecTile<GV> Rv;
     int c = run;
-    if (c < tpo) rec_tile_load<GK>(Rk, kc, k_slot, M, kvh * tpo + c, n_tiles, lane);
+    if (c < tpo) {
+        rec_tile_load<GK>(Rk, kc, k_slot, M, kvh * tpo + c, n_tiles, lane);
+        if (OUT) rec_tile_load<GV>(Rv, vc, v_slot, M, kvh * tpo + c, n_tiles, lane);
+    }
     for (; c < tpo; c += n_runs) {
         const int t = kvh * tpo + c;
-        RecTile<GV> Rv;
-        if (OUT) rec_tile_load<GV>(Rv, vc, v_slot, M, t, n_tiles, lane);
         __syncthreads();  // the previous tile is done with the stage
         rec_tile_stage<GK>(Rk, stage, M, t, lane);
         __syncthreads();
@@ -180,6 +184,7 @@ k_sqfree_attn_split(const unsigned char *__restrict__ kc0, const unsigned char *
         __syncthreads();
         uint32_t rv[GV::dwords];
         rec_from_lds<GV>(rv, stage, lane);
+        if (c + n_runs < tpo) rec_tile_load<GV>(Rv, vc, v_slot, M, t + n_runs, n_tiles, lane);
         float ev[PAD];
         sq_coefficients<SK, SLV>(rv, ev);
 #pragma unroll
@@ -301,11 +306,39 @@ int sp_sqfree_attn_kind(const SpPlan &KP, const SpPlan &VP, const SpSqGeo &G) {
     return 0;
 }
 
-// Runs per KV head: every run gets at least one tile and the blocks that are
-// resident at once (six one-wave blocks per CU) spread over the KV heads.
-int sp_sqfree_attn_runs(int n_kvh, int n_kv, int cus, int n_seq) {
+namespace {
+// One-wave blocks of the split kernel instance for this call that are resident on a CU
+// at once (its registers and LDS decide; 4 when the runtime cannot say).
+template <int SK, class SLK, class SLV, int GM>
+int resident_per_cu(bool out) {
+    int nb = 0;
+    const hipError_t e =
+        out ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_sqfree_attn_split<SK, SLK, SLV, GM, true>, 64, 0)
+            : hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_sqfree_attn_split<SK, SLK, SLV, GM, false>, 64, 0);
+    return e == hipSuccess && nb > 0 ? nb : 4;
+}
+template <int SK, class SLK, class SLV>
+int resident_per_cu_g(int G, bool out) {
+    if (G <= 1) return resident_per_cu<SK, SLK, SLV, 1>(out);
+    if (G <= 2) return resident_per_cu<SK, SLK, SLV, 2>(out);
+    if (G <= 4) return resident_per_cu<SK, SLK, SLV, 4>(out);
+    return resident_per_cu<SK, SLK, SLV, 8>(out);
+}
+}  // namespace
+
+// Runs per KV head and sequence: the blocks that are resident at once (the split
+// kernel instance's occupancy) spread over the sequences' KV heads, so the launch runs
+// in one round, every run getting at least one tile.
+int sp_sqfree_attn_runs(const SpPlan &KP, const SpPlan &VP, const SpSqGeo &G, int n_q, int n_kvh, int n_kv, int cus,
+                        int n_seq, bool out) {
+    const int kind = sp_sqfree_attn_kind(KP, VP, G);
+    if (!kind || n_kvh <= 0 || n_q % n_kvh) return 1;
+    const int g = n_q / n_kvh;
+    const int per_cu = kind == 1   ? resident_per_cu_g<77, SkelL77, SkelL77>(g, out)
+                       : kind == 2 ? resident_per_cu_g<115, SkelL115, SkelL115>(g, out)
+                                   : resident_per_cu_g<115, SkelL115, SkelL115V3>(g, out);
     const int tpo = (n_kv + 63) / 64;
-    const int per_head = std::max(1, (6 * cus) / std::max(1, n_kvh * n_seq));
+    const int per_head = std::max(1, (per_cu * cus) / std::max(1, n_kvh * n_seq));
     return std::max(1, std::min(std::min(tpo, per_head), 1024));
 }
 
