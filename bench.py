@@ -38,6 +38,23 @@ KERNEL_NAMES = {"k_enc": "k_ship_encode_lane<Layout<128,5,5,4,3>, fp16, Mobius>"
                 "v_dec": "k_ship_decode_lane<Layout<128,3>, fp16>"}
 
 
+# VALU instructions per 64-vector tile of each codec kernel, measured with rocprofv3
+# (SQ_INSTS_VALU per wave over the tiles each wave walks; profiles/valu_codec_kernels.md).
+# A wave64 VALU instruction issues over 4 cycles on a 16-lane SIMD, so at full issue a
+# kernel needs tiles * VALU_PER_TILE * 4 / (SIMDs * engine clock): the VALU-issue bound,
+# which the bit-exact codecs cannot move to the matrix cores.
+VALU_PER_TILE = {"k_enc": 1693, "v_enc": 1608, "k_dec": 1559, "v_dec": 1799,  # configs[1], hd 128
+                 "hd96_k_enc": 2089, "hd96_v_enc": 2087, "hd96_k_dec": 2225, "hd96_v_dec": 2224,
+                 "sqfree_k_enc": 7256, "sqfree_v_enc": 7207, "sqfree_k_dec": 5802, "sqfree_v_dec": 5948,
+                 "hier_enc": 33545, "hier_dec": 31765}
+ENGINE_CLOCK_HZ = 2.4e9  # MI355X peak engine clock
+
+
+def valu_bound_s(n_vec, per_tile, simds):
+    """Seconds the VALU needs at full issue for n_vec vectors at per_tile instructions per 64."""
+    return (n_vec / 64.0) * per_tile * 4.0 / (simds * ENGINE_CLOCK_HZ)
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -187,9 +204,16 @@ def bench_variants(torch, S, L, stream, reps=3):
         torch.cuda.synchronize()
         return a.elapsed_time(b) / reps * 1e-3  # s
 
-    def rate(n_vec, hd, B, t):
-        return {"ms": round(t * 1e3, 4), "vecs_per_s": round(n_vec / t, 1),
-                "gbs": round(n_vec * (2 * hd + B) / t / 1e9, 1)}
+    simds = 4 * torch.cuda.get_device_properties(0).multi_processor_count
+
+    def rate(n_vec, hd, B, t, valu_key=None):
+        r = {"ms": round(t * 1e3, 4), "vecs_per_s": round(n_vec / t, 1),
+             "gbs": round(n_vec * (2 * hd + B) / t / 1e9, 1)}
+        if valu_key:
+            vb = valu_bound_s(n_vec, VALU_PER_TILE[valu_key], simds)
+            r.update({"valu_per_tile": VALU_PER_TILE[valu_key], "valu_bound_ms": round(vb * 1e3, 4),
+                      "valu_frac": round(vb / t, 3)})
+        return r
 
     out = {}
     # one layer of 32 heads x 65536 cells (16 sequences x 4096), hd 96
@@ -202,10 +226,14 @@ def bench_variants(torch, S, L, stream, reps=3):
     kB3, vB3 = c3.c.k_bands.total_bytes, c3.c.v_bands.total_bytes
     n3 = H3 * N3
     out["cfg3_hd96_ship"] = {
-        "k_enc": rate(n3, hd3, kB3, timed(lambda: S.check(L.sp_hip_write_all(c3.ref, 0, N3, P(x), None, S.DTYPE_F16)))),
-        "v_enc": rate(n3, hd3, vB3, timed(lambda: S.check(L.sp_hip_write_all(c3.ref, 0, N3, None, P(x), S.DTYPE_F16)))),
-        "k_dec": rate(n3, hd3, kB3, timed(lambda: S.check(L.sp_hip_read_all(c3.ref, 0, N3, P(y), None, S.DTYPE_F16, -1)))),
-        "v_dec": rate(n3, hd3, vB3, timed(lambda: S.check(L.sp_hip_read_all(c3.ref, 0, N3, None, P(y), S.DTYPE_F16, -1)))),
+        "k_enc": rate(n3, hd3, kB3, timed(lambda: S.check(L.sp_hip_write_all(c3.ref, 0, N3, P(x), None, S.DTYPE_F16))),
+                      "hd96_k_enc"),
+        "v_enc": rate(n3, hd3, vB3, timed(lambda: S.check(L.sp_hip_write_all(c3.ref, 0, N3, None, P(x), S.DTYPE_F16))),
+                      "hd96_v_enc"),
+        "k_dec": rate(n3, hd3, kB3, timed(lambda: S.check(L.sp_hip_read_all(c3.ref, 0, N3, P(y), None, S.DTYPE_F16, -1))),
+                      "hd96_k_dec"),
+        "v_dec": rate(n3, hd3, vB3, timed(lambda: S.check(L.sp_hip_read_all(c3.ref, 0, N3, None, P(y), S.DTYPE_F16, -1))),
+                      "hd96_v_dec"),
         "record_bytes": [kB3, vB3]}
     # configs[2] decode, batched: the 16 sequences as position ranges [4096 i, 4096 (i + 1)) of this
     # layer (K and V records from the writes above), one fused attention call for all of them
@@ -370,10 +398,10 @@ def bench_variants(torch, S, L, stream, reps=3):
         return f
 
     nv4 = L4 * H4 * N4
-    r_ke = rate(nv4, 128, B4, timed(sq_call(L.sp_hip_sqfree_write_layer, 0, x)))
-    r_ve = rate(nv4, 128, B4v, timed(sq_call(L.sp_hip_sqfree_write_layer, 1, x)))
-    r_kd = rate(nv4, 128, B4, timed(sq_call(L.sp_hip_sqfree_read_layer, 0, y)))
-    r_vd = rate(nv4, 128, B4v, timed(sq_call(L.sp_hip_sqfree_read_layer, 1, y)))
+    r_ke = rate(nv4, 128, B4, timed(sq_call(L.sp_hip_sqfree_write_layer, 0, x)), "sqfree_k_enc")
+    r_ve = rate(nv4, 128, B4v, timed(sq_call(L.sp_hip_sqfree_write_layer, 1, x)), "sqfree_v_enc")
+    r_kd = rate(nv4, 128, B4, timed(sq_call(L.sp_hip_sqfree_read_layer, 0, y)), "sqfree_k_dec")
+    r_vd = rate(nv4, 128, B4v, timed(sq_call(L.sp_hip_sqfree_read_layer, 1, y)), "sqfree_v_dec")
     out["cfg4_sqfree_spinor"] = {"enc": r_ke, "dec": r_kd, "v_enc": r_ve, "v_dec": r_vd,
                                  "record_bytes": [B4, B4v], "pad_dim": pad4, "skeleton": c4.c.sk_k,
                                  "calls": f"{L4} layers x {H4} heads x {N4} positions, one call per layer and side "
@@ -434,8 +462,8 @@ def bench_variants(torch, S, L, stream, reps=3):
     def hi_read():
         S.check(L.sp_hip_hier_read_layer(c5.ref, 0, 0, N5, P(y), None, H5 * hd5, S.DTYPE_F16))
 
-    out["cfg5_hier"] = {"enc": rate(H5 * N5, hd5, B5, timed(hi_write)),
-                        "dec": rate(H5 * N5, hd5, B5, timed(hi_read)),
+    out["cfg5_hier"] = {"enc": rate(H5 * N5, hd5, B5, timed(hi_write), "hier_enc"),
+                        "dec": rate(H5 * N5, hd5, B5, timed(hi_read), "hier_dec"),
                         "record_bytes": B5, "pad_dim": pad5, "skeleton": n_sk,
                         "calls": f"1 layer x {H5} heads x {N5} positions, one call (K)"}
     # the reference caller's per-vector hook path through the bridge (host pointers): one
@@ -636,6 +664,16 @@ def main():
                                            "read from the committed profile, not measured in this run",
                          "bytes_per_launch": n_vec * per[dom], "avg_ms": round(kern_ms[dom], 4)},
         })
+        simds = 4 * torch.cuda.get_device_properties(0).multi_processor_count
+        vb = {n: valu_bound_s(n_vec, VALU_PER_TILE[n], simds) * 1e3 for n in steps}
+        result["valu_issue"] = {
+            "per_tile": {n: VALU_PER_TILE[n] for n in steps},
+            "bound_ms": {n: round(t, 4) for n, t in vb.items()},
+            "frac": {n: round(vb[n] / kern_ms[n], 3) for n in steps},
+            "step_bound_ms": round(sum(vb.values()), 4),
+            "note": "VALU-issue bound of each bit-exact codec kernel (instructions per 64-vector tile from "
+                    "rocprofv3 SQ_INSTS_VALU, profiles/valu_codec_kernels.md; 4 cycles per wave64 "
+                    "instruction per SIMD at 2.4 GHz); the step's sum exceeds its 1.34 ms HBM floor"}
     if args.only in ("attn", "all"):
         # fused decode attention over the compressed 32K cache, all 32 layers per token
         if args.only == "attn":
