@@ -11,8 +11,9 @@
 // 64-position tiles: lane = position, the record dequantized into the lane's
 // registers (compile-time band layout), the scores as dot products with the prepared
 // queries (scalar loads), an online softmax across the run's tiles, and the V
-// coefficient sums through an LDS transpose (each lane sums one coefficient over the
-// tile's 64 positions). Partials [m, l, o~[hd]] per (query head, run), the layout
+// coefficient sums through an LDS transpose in chunks of 32 coefficients (lanes c and
+// c + 32 sum coefficient c over the tile's two halves of 32 positions, added at the end
+// of the run). Partials [m, l, o~[hd]] per (query head, run), the layout
 // k_attn_combine merges.
 #include "sp_lane.h"
 
@@ -31,6 +32,27 @@ __device__ __forceinline__ float wadd(float v) {
     return v;
 }
 
+// A record's codes centred, in record order, without their band scales: x = code -
+// (2^(bits-1) - 1), exact (the magic-number conversion of dequant_bands), and each
+// band's scale, 0 for bands >= max_bands (the read-as-0 rule; a finite sum times 0
+// adds nothing). Attention applies a K band's scale once to the band's dot product
+// and folds the V scale into the softmax weight, so no coefficient pays a multiply
+// or a band-limit select.
+template <class LY, int DWR>
+__device__ __forceinline__ void codes_centred(const uint32_t (&rec)[DWR], int max_bands, float (&x)[LY::hd],
+                                              float (&sc)[LY::nb]) {
+#pragma unroll
+    for (int b = 0; b < LY::nb; b++) {
+        const int off = LY::off(b), sz = LY::sz(b), bits = LY::bits[b];
+        const int bo = LY::byte_off(b);
+        sc[b] = b < max_bands ? sp_scale_from_bits(rec_extract(rec, 8 * bo, 16)) : 0.0f;
+        const float bias = 12582912.0f + (float)((1 << (bits - 1)) - 1);
+#pragma unroll
+        for (int e = 0; e < sz; e++)
+            x[off + e] = __uint_as_float(rec_extract(rec, 8 * (bo + 2) + e * bits, bits) | 0x4B400000u) - bias;
+    }
+}
+
 // Block (kvh, run) takes tiles run, run + n_runs, ... of KV head kvh. qt: prepared
 // queries [n_q][hd] (record order). K bands >= kmb and V bands >= vmb read as 0.
 template <class LK, class LV, int GM, bool OUT>
@@ -40,13 +62,14 @@ k_attn_lane_split(const unsigned char *__restrict__ kc0, const unsigned char *__
                   float *__restrict__ part0, int n_runs, int kmb, int vmb) {
     constexpr int HD = LK::hd;
     static_assert(LV::hd == HD, "K and V layouts share head_dim");
+    static_assert(LV::nb == 1, "V's scale rides on the softmax weight: one band");
     constexpr int NCK = RecTile<LK>::NCK > RecTile<LV>::NCK ? RecTile<LK>::NCK : RecTile<LV>::NCK;
-    constexpr int NFULL = HD / 64;            // full 64-coefficient chunks
-    constexpr int C2 = HD - 64 * NFULL;       // coefficients of the last, partial chunk
-    constexpr bool HALVES = C2 > 0 && 2 * C2 <= 64 && GM > 1;  // two lanes per coefficient there
-    constexpr int HG = HALVES ? (GM + 1) / 2 : GM;
+    // V sums in chunks of 32 coefficients: lane (c, half) = (lane & 31, lane >> 5) sums
+    // coefficient 32 ch + c over the tile's positions 32 half .. 32 half + 31
+    constexpr int NCH = HD / 32;
+    static_assert(HD % 32 == 0, "whole 32-coefficient chunks");
     __shared__ __attribute__((aligned(16))) unsigned char stage[NCK * 1024 + 16];
-    __shared__ float E[64 * EP];
+    __shared__ float E[32 * EP];
     __shared__ __attribute__((aligned(16))) float Pw[64 * GM];
     const int kvh = blockIdx.x, run = blockIdx.y, lane = threadIdx.x;
     // sequence blockIdx.z: its positions, prepared queries, score rows and partials
@@ -64,18 +87,15 @@ k_attn_lane_split(const unsigned char *__restrict__ kc0, const unsigned char *__
     const float *__restrict__ pq = qt + (long long)h0 * HD;
 
     float m_run[GM], l_run[GM];
-    float acc[NFULL > 0 ? NFULL : 1][GM], acc2[HG];
+    float acc[NCH][GM];
 #pragma unroll
     for (int h = 0; h < GM; h++) {
         m_run[h] = -INFINITY;
         l_run[h] = 0.0f;
 #pragma unroll
-        for (int c = 0; c < (NFULL > 0 ? NFULL : 1); c++) acc[c][h] = 0.0f;
+        for (int ch = 0; ch < NCH; ch++) acc[ch][h] = 0.0f;
     }
-#pragma unroll
-    for (int k = 0; k < HG; k++) acc2[k] = 0.0f;
-    const int c2i = C2 > 0 ? lane % C2 : 0, hh = C2 > 0 ? lane / C2 : 0;
-    const bool c2_on = C2 > 0 && hh < (HALVES ? 2 : 1);
+    const int vc_i = lane & 31, vp0 = 32 * (lane >> 5);
 
     // both record streams run one tile ahead: the next tile's K loads once this tile's
     // K records are out of the stage, its V once this tile's V records are
@@ -94,8 +114,8 @@ k_attn_lane_split(const unsigned char *__restrict__ kc0, const unsigned char *__
         uint32_t rk[LK::dwords];
         rec_from_lds<LK>(rk, stage, lane);
         if (c + n_runs < tpo) rec_tile_load<LK>(Rk, kc, k_slot, M, t + n_runs, n_tiles, lane);
-        float e[HD];
-        dequant_bands<LK, false, false>(rk, kmb, e);  // record order, bands past kmb read as 0
+        float e[HD], ks[LK::nb];
+        codes_centred<LK>(rk, kmb, e, ks);  // record order; bands past kmb scale 0
         const int pos = c * 64 + lane;
         const bool live = pos < n_kv;
         float s[GM];
@@ -104,13 +124,17 @@ k_attn_lane_split(const unsigned char *__restrict__ kc0, const unsigned char *__
             s[h] = -INFINITY;
             if (h < G) {
                 const float *__restrict__ qh = pq + h * HD;
-                float a0 = 0.0f, a1 = 0.0f;
+                float v = 0.0f;
 #pragma unroll
-                for (int j = 0; j < HD; j += 2) {
-                    a0 = fmaf(qh[j], e[j], a0);
-                    a1 = fmaf(qh[j + 1], e[j + 1], a1);
+                for (int b = 0; b < LK::nb; b++) {
+                    float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+                    for (int j = LK::off(b); j < LK::off(b) + LK::sz(b); j += 2) {
+                        a0 = fmaf(qh[j], e[j], a0);
+                        if (j + 1 < LK::off(b) + LK::sz(b)) a1 = fmaf(qh[j + 1], e[j + 1], a1);
+                    }
+                    v = fmaf(ks[b], a0 + a1, v);
                 }
-                const float v = a0 + a1;
                 if (live) {
                     s[h] = v;
                     if (scores) scores[(long long)(h0 + h) * s_stride + pos] = v;
@@ -138,47 +162,32 @@ k_attn_lane_split(const unsigned char *__restrict__ kc0, const unsigned char *__
         uint32_t rv[LV::dwords];
         rec_from_lds<LV>(rv, stage, lane);
         if (c + n_runs < tpo) rec_tile_load<LV>(Rv, vc, v_slot, M, t + n_runs, n_tiles, lane);
-        float ev[HD];
-        dequant_bands<LV, false, false>(rv, vmb, ev);
+        // V's one band: centred codes here, its scale in this position's weights
+        float ev[HD], vs[1];
+        codes_centred<LV>(rv, vmb, ev, vs);
+#pragma unroll
+        for (int h = 0; h < GM; h++) Pw[lane * GM + h] *= vs[0];
 #pragma unroll
         for (int h = 0; h < GM; h++)
 #pragma unroll
-            for (int cc = 0; cc < (NFULL > 0 ? NFULL : 1); cc++) acc[cc][h] *= alpha[h];
+            for (int ch = 0; ch < NCH; ch++) acc[ch][h] *= alpha[h];
 #pragma unroll
-        for (int k = 0; k < HG; k++) {
-            float a = 1.0f;
+        for (int ch = 0; ch < NCH; ch++) {
 #pragma unroll
-            for (int h = 0; h < GM; h++)
-                if (h == hh * HG + k) a = alpha[h];
-            acc2[k] *= a;
-        }
-#pragma unroll
-        for (int ch = 0; ch < NFULL + (C2 > 0 ? 1 : 0); ch++) {
-            const int i0 = 64 * ch, n_i = ch < NFULL ? 64 : C2;
-#pragma unroll
-            for (int i = 0; i < 64; i++)
-                if (i < n_i) E[i * EP + lane] = ev[i0 + i];
+            for (int i = 0; i < 32; i++) E[i * EP + lane] = ev[32 * ch + i];
             __syncthreads();
-            if (ch < NFULL) {
 #pragma unroll 4
-                for (int p = 0; p < 64; p++) {
-                    const float ei = E[lane * EP + p];
+            for (int p = 0; p < 32; p++) {
+                const float ei = E[vc_i * EP + vp0 + p];
 #pragma unroll
-                    for (int h = 0; h < GM; h++) acc[ch][h] = fmaf(Pw[p * GM + h], ei, acc[ch][h]);
-                }
-            } else if (c2_on) {
-#pragma unroll 4
-                for (int p = 0; p < 64; p++) {
-                    const float ei = E[c2i * EP + p];
-#pragma unroll
-                    for (int k = 0; k < HG; k++) acc2[k] = fmaf(Pw[p * GM + hh * HG + k], ei, acc2[k]);
-                }
+                for (int h = 0; h < GM; h++) acc[ch][h] = fmaf(Pw[(vp0 + p) * GM + h], ei, acc[ch][h]);
             }
             __syncthreads();
         }
     }
     if (!OUT) return;
-    // ---- the run's partial per query head: [m, l, o~[hd]] ----
+    // ---- the run's partial per query head: [m, l, o~[hd]], the two position halves
+    // of each coefficient added across lanes c and c + 32 ----
 #pragma unroll
     for (int h = 0; h < GM; h++) {
         if (h >= G) continue;
@@ -188,13 +197,9 @@ k_attn_lane_split(const unsigned char *__restrict__ kc0, const unsigned char *__
             dst[1] = l_run[h];
         }
 #pragma unroll
-        for (int cc = 0; cc < NFULL; cc++) dst[2 + 64 * cc + lane] = acc[cc][h];
-    }
-    if (c2_on) {
-#pragma unroll
-        for (int k = 0; k < HG; k++) {
-            const int h = hh * HG + k;
-            if (h < G) part[((long long)(h0 + h) * n_runs + run) * (HD + 2) + 2 + 64 * NFULL + c2i] = acc2[k];
+        for (int ch = 0; ch < NCH; ch++) {
+            const float v = acc[ch][h] + __shfl_xor(acc[ch][h], 32, 64);
+            if (lane < 32) dst[2 + 32 * ch + lane] = v;
         }
     }
 }
@@ -235,11 +240,31 @@ using V96 = Layout<96, 5>;
 using K64 = Layout<64, 5, 5, 4, 3>;
 using V64 = Layout<64, 3>;
 
+// One-wave blocks of the instance for this call resident on a CU at once (registers
+// and LDS decide; 4 when the runtime cannot say).
+template <class LK, class LV, int GM>
+int resident_per_cu(bool out) {
+    int nb = 0;
+    const hipError_t e = out ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_attn_lane_split<LK, LV, GM, true>,
+                                                                           64, 0)
+                             : hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_attn_lane_split<LK, LV, GM, false>,
+                                                                           64, 0);
+    return e == hipSuccess && nb > 0 ? nb : 4;
+}
+template <class LK, class LV>
+int resident_per_cu_g(int G, bool out) {
+    if (G <= 1) return resident_per_cu<LK, LV, 1>(out);
+    if (G <= 2) return resident_per_cu<LK, LV, 2>(out);
+    if (G <= 4) return resident_per_cu<LK, LV, 4>(out);
+    return resident_per_cu<LK, LV, 8>(out);
+}
+
 }  // namespace
 
-// Runs per KV head for the lane split kernel: at most the workspace's partial rows,
-// at least one tile per run, and about six resident one-wave blocks per CU spread
-// over the KV heads. 0 when no lane kernel serves the call's layouts.
+// Runs per KV head and sequence for the lane split kernel: at most the workspace's
+// partial rows, at least one tile per run, and the instance's resident one-wave blocks
+// spread over the sequences' KV heads (one round). 0 when no lane kernel serves the
+// call's layouts.
 int sp_attn_lane_runs(const SpPlan &KP, const SpPlan &VP, const SpAttnArgs &A, size_t part_floats, int n_seq) {
     const bool ok = (plan_is<K96>(KP) && plan_is<V96>(VP)) || (plan_is<K64>(KP) && plan_is<V64>(VP));
     if (!ok || A.n_q % A.n_kvh || A.n_q / A.n_kvh > 8) return 0;
@@ -254,7 +279,10 @@ int sp_attn_lane_runs(const SpPlan &KP, const SpPlan &VP, const SpAttnArgs &A, s
     }
     const int tpo = (A.n_kv + 63) / 64;
     const long long cap = (long long)(part_floats / ((size_t)n_seq * A.n_q * (A.hd + 2)));
-    long long r = std::min<long long>(tpo, std::max(1, (6 * cus) / (A.n_kvh * n_seq)));
+    const int G = A.n_q / A.n_kvh;
+    const int per_cu = plan_is<K96>(KP) ? resident_per_cu_g<K96, V96>(G, A.out != nullptr)
+                                        : resident_per_cu_g<K64, V64>(G, A.out != nullptr);
+    long long r = std::min<long long>(tpo, std::max(1, (per_cu * cus) / (A.n_kvh * n_seq)));
     r = std::min<long long>(r, std::min<long long>(cap, 4096));
     // SP_HIP_ATTN_LANE_RUNS=n caps the runs per KV head (read at each call; tests use it
     // to give every run several tiles at small context lengths)

@@ -195,6 +195,47 @@ def test_band_limited_attention_matches_oracle(n_q, H, n_ctx, path, monkeypatch)
     cc.free()
 
 
+@pytest.mark.parametrize("hd,k_bits,v_bits,n_q,H,n_ctx", [
+    (96, (5, 4, 4), (5,), 8, 2, 700),        # configs[2]'s bands: the lane kernel's three K bands
+    (64, (5, 5, 4, 3), (3,), 12, 4, 333),    # hd 64 shipping bands, GQA 3
+])
+def test_lane_band_limited_attention_matches_oracle(hd, k_bits, v_bits, n_q, H, n_ctx):
+    """The one-position-per-lane kernel's band limits (sp_hip_attn_decode_bands): K bands
+    past the limit, and V when the limit is 0, read as 0, against the oracle over the
+    partial reconstructions (1e-3); the full band count and -1 equal the full call."""
+    k16, v16 = W.cfg3_kv(n_heads=H, n_pos=n_ctx, hd=hd, seed=n_ctx + 5)
+    q = W.cfg2_q(n_q=n_q, hd=hd, pos=n_ctx, seed=n_ctx + 6)
+    cc = S.ShipCache(S.config(hd, 1, H, k_bits=k_bits, v_bits=v_bits), n_ctx + 1,
+                     stream=torch.cuda.current_stream().cuda_stream)
+    L = S.lib()
+    for h in range(H):
+        kt, vt = dev(k16[h].view(np.uint16)), dev(v16[h].view(np.uint16))
+        S.check(L.sp_hip_write_k_batch_f16(cc.ref, 0, h, 0, n_ctx, p(kt)))
+        S.check(L.sp_hip_write_v_batch_f16(cc.ref, 0, h, 0, n_ctx, p(vt)))
+    kbc, vbc = O.band_config(hd, list(k_bits)), O.band_config(hd, list(v_bits))
+    order = O.mobius_order(hd)
+    kref = np.stack([O.ship_compress_f16(k16[h].view(np.uint16), kbc, order) for h in range(H)])
+    vref = np.stack([O.ship_compress_f16(v16[h].view(np.uint16), vbc) for h in range(H)])
+    scale = 1.0 / math.sqrt(hd)
+    qt = dev(q)
+    sc_full, out_full = empty_f32(n_q * n_ctx), empty_f32(n_q * hd)
+    S.check(L.sp_hip_attn_decode(cc.ref, 0, n_ctx, p(qt), n_q, C.c_float(scale), p(sc_full), p(out_full), stream()))
+    nb = len(k_bits)
+    for mb in list(range(nb)) + [nb, -1]:
+        say(f"lane attn bands hd={hd} n_q={n_q} H={H} n_ctx={n_ctx} max_bands={mb}")
+        sc, out = empty_f32(n_q * n_ctx), empty_f32(n_q * hd)
+        S.check(L.sp_hip_attn_decode_bands(cc.ref, 0, n_ctx, p(qt), n_q, C.c_float(scale), p(sc), p(out), mb,
+                                           stream()))
+        if mb in (nb, -1):
+            np.testing.assert_array_equal(host(sc), host(sc_full))
+            np.testing.assert_array_equal(host(out), host(out_full))
+            continue
+        s_ref, o_ref = O.attn_decode(q, kref, vref, H, n_ctx, kbc, vbc, order, scale, max_bands=mb)
+        rel_close(host(sc).reshape(n_q, n_ctx), s_ref)
+        rel_close(host(out).reshape(n_q, hd), o_ref)
+    cc.free()
+
+
 # The shapes the bench times. The matrix-core kernel (k_attn_wave) gives each wave
 # one 64-position tile while the context fits one round of 16-wave blocks (one per
 # CU): 8 KV heads at 32768 positions are 4096 tiles on 256 blocks, one tile per wave,
