@@ -74,7 +74,7 @@ constexpr int EP = 65;  // LDS row pitch (floats) of the transposed coefficient 
 // + run) * pp: [m, l, 0, 0, sum p c~ (PAD coefficients, skeleton then residuals)].
 // OUT = false: scores only.
 template <int SK, class SLK, class SLV, int GM, bool OUT>
-__global__ void __launch_bounds__(64)
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2)))
 k_sqfree_attn_split(const unsigned char *__restrict__ kc0, const unsigned char *__restrict__ vc0, long long k_slot,
                     long long v_slot, const SpSeqTab T, int G, const float *__restrict__ prep0, int ps, int qo,
                     float *__restrict__ scores0, float *__restrict__ part0, int pp, int n_runs) {
@@ -116,17 +116,15 @@ k_sqfree_attn_split(const unsigned char *__restrict__ kc0, const unsigned char *
     const int c2i = lane % C2, hh = lane / C2;
     const bool c2_on = hh < (GM > 1 ? 2 : 1);
 
-    // both record streams run one tile ahead: the next tile's K loads once this tile's
-    // K records are out of the stage, its V once this tile's V records are
+    // the K records run one tile ahead (the next tile's load goes out once this tile's
+    // records are out of the stage); a tile's V records load at the tile's start
     RecTile<GK> Rk;
-    RecTile<GV> Rv;
     int c = run;
-    if (c < tpo) {
-        rec_tile_load<GK>(Rk, kc, k_slot, M, kvh * tpo + c, n_tiles, lane);
-        if (OUT) rec_tile_load<GV>(Rv, vc, v_slot, M, kvh * tpo + c, n_tiles, lane);
-    }
+    if (c < tpo) rec_tile_load<GK>(Rk, kc, k_slot, M, kvh * tpo + c, n_tiles, lane);
     for (; c < tpo; c += n_runs) {
         const int t = kvh * tpo + c;
+        RecTile<GV> Rv;
+        if (OUT) rec_tile_load<GV>(Rv, vc, v_slot, M, t, n_tiles, lane);
         __syncthreads();  // the previous tile is done with the stage
         rec_tile_stage<GK>(Rk, stage, M, t, lane);
         __syncthreads();
@@ -184,7 +182,6 @@ k_sqfree_attn_split(const unsigned char *__restrict__ kc0, const unsigned char *
         __syncthreads();
         uint32_t rv[GV::dwords];
         rec_from_lds<GV>(rv, stage, lane);
-        if (c + n_runs < tpo) rec_tile_load<GV>(Rv, vc, v_slot, M, t + n_runs, n_tiles, lane);
         float ev[PAD];
         sq_coefficients<SK, SLV>(rv, ev);
 #pragma unroll
