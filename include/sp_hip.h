@@ -478,41 +478,6 @@ int  sp_hip_dual_read_merged(sp_hip_dual_cache_t *dc, int layer, int kv_len, voi
                              long long row_stride, int dtype);
 
 /* ======================================================================== */
-/* Warm tier: pinned host mirror of one layer's records                     */
-/* (sp_cuda_cold_layer_t and its calls, shannon_prime_cuda.h:236-285)        */
-/* ======================================================================== */
-typedef struct {
-    uint8_t *h_pinned;       /* [n_heads][cap_pos][packed_stride], pinned */
-    int64_t  capacity;       /* bytes of h_pinned */
-    int      packed_stride;  /* record bytes (the band config's total_bytes) */
-    int      n_heads;
-    int      max_seq_len;    /* positions per head in the device slab: its head stride */
-    int64_t  cap_pos;        /* positions per head the mirror holds */
-    int64_t  write_head;     /* ring slot of the next position */
-    int64_t  oldest_pos;     /* oldest position still mirrored; -1 = none yet */
-    int64_t  newest_pos;     /* newest position mirrored */
-    int      ring_mode;      /* 1 once a position past cap_pos has been written */
-    int      initialized;
-} sp_hip_cold_layer_t;
-
-/* Pinned mirror of cap_bytes (0: every position; rounded down to whole positions
- * of all heads, at most max_seq_len of them). The device slab passed to the
- * calls below is one layer of a cache, [n_heads][max_seq_len][packed_stride]
- * (e.g. d_k_cache + layer*n_heads*max_seq_len*k_bytes). */
-int  sp_hip_cold_layer_init(sp_hip_cold_layer_t *cl, int64_t cap_bytes, int packed_stride, int n_heads,
-                            int max_seq_len);
-void sp_hip_cold_layer_free(sp_hip_cold_layer_t *cl);
-/* Async copy of positions [start_pos, start_pos + n_pos) of every head into the
- * ring (position p at slot p % cap_pos); once past cap_pos, the oldest positions
- * are overwritten and oldest_pos advances. */
-int  sp_hip_cold_writeback(sp_hip_cold_layer_t *cl, const void *d_packed, int start_pos, int n_pos, void *stream);
-/* Async copy of positions [0, n_pos) back to the slab; -1 when any of them is no
- * longer mirrored (the reference refuses every restore once its ring wrapped). */
-int  sp_hip_cold_restore(const sp_hip_cold_layer_t *cl, void *d_packed, int n_pos, void *stream);
-void sp_hip_d2h_async(void *dst_host, const void *src_device, int64_t n_bytes, void *stream);
-void sp_hip_h2d_async(void *dst_device, const void *src_host, int64_t n_bytes, void *stream);
-
-/* ======================================================================== */
 /* Disk serialisation, format v3 (KvCache::save_to_disk / load_from_disk,   */
 /* kv_cache.h:132-146, kv_cache.cpp:1533-1585; band-major partial load of   */
 /* the disk-tier notes, CHANGELOG.md)                                       */

@@ -2634,98 +2634,6 @@ extern "C" int sp_hip_hier_cache_load(sp_hip_hier_cache_t *hc, const char *prefi
     return sp_hip_hier_cache_upload_W(hc, W.data()) == 0 ? n : -1;
 }
 
-// ===========================================================================
-// warm tier: pinned host mirror of a layer's records (sp_cuda_cold_layer_t,
-// shannon_prime_cuda.h:236-285, shannon_prime_cuda.cu:680-785)
-// ===========================================================================
-// The device slab of one layer is [n_heads][max_seq][B] (head stride max_seq*B);
-// the mirror is [n_heads][cap_pos][B] with position p at ring slot p % cap_pos,
-// so each copy is one 2-D copy per contiguous ring run (the reference's version
-// copies the slab as position-major bytes, which its head-major slab is not).
-
-extern "C" void sp_hip_d2h_async(void *dst_host, const void *src_device, int64_t n_bytes, void *stream) {
-    (void)hip_ok(hipMemcpyAsync(dst_host, src_device, (size_t)n_bytes, hipMemcpyDeviceToHost, (hipStream_t)stream),
-                 "d2h_async");
-}
-
-extern "C" void sp_hip_h2d_async(void *dst_device, const void *src_host, int64_t n_bytes, void *stream) {
-    (void)hip_ok(hipMemcpyAsync(dst_device, src_host, (size_t)n_bytes, hipMemcpyHostToDevice, (hipStream_t)stream),
-                 "h2d_async");
-}
-
-extern "C" int sp_hip_cold_layer_init(sp_hip_cold_layer_t *cl, int64_t cap_bytes, int packed_stride, int n_heads,
-                                      int max_seq_len) {
-    if (!cl || packed_stride <= 0 || n_heads <= 0 || max_seq_len <= 0) { set_err("cold_init: bad args"); return -1; }
-    memset(cl, 0, sizeof(*cl));
-    const int64_t per_pos = (int64_t)n_heads * packed_stride;
-    int64_t cap_pos = cap_bytes <= 0 ? max_seq_len : cap_bytes / per_pos;  // 0: room for every position
-    if (cap_pos > max_seq_len) cap_pos = max_seq_len;
-    if (cap_pos <= 0) { set_err("cold_init: capacity below one position"); return -1; }
-    if (!hip_ok(hipHostMalloc((void **)&cl->h_pinned, (size_t)(cap_pos * per_pos), hipHostMallocDefault),
-                "cold_init pinned")) return -1;
-    cl->capacity = cap_pos * per_pos;
-    cl->packed_stride = packed_stride;
-    cl->n_heads = n_heads;
-    cl->max_seq_len = max_seq_len;
-    cl->cap_pos = cap_pos;
-    cl->oldest_pos = -1;
-    cl->newest_pos = -1;
-    cl->initialized = 1;
-    return 0;
-}
-
-extern "C" void sp_hip_cold_layer_free(sp_hip_cold_layer_t *cl) {
-    if (!cl) return;
-    if (cl->h_pinned) (void)hipHostFree(cl->h_pinned);
-    cl->h_pinned = nullptr;
-    cl->initialized = 0;
-}
-
-// 2-D copy of positions [p0, p0 + n) of every head between the slab and the ring,
-// split where the ring wraps.
-static bool cold_copy(const sp_hip_cold_layer_t *cl, unsigned char *dev, long long p0, long long n, bool to_host,
-                      hipStream_t s) {
-    const size_t B = (size_t)cl->packed_stride, dpitch = (size_t)cl->max_seq_len * B, hpitch = (size_t)cl->cap_pos * B;
-    while (n > 0) {
-        const long long slot = p0 % cl->cap_pos, run = std::min<long long>(n, cl->cap_pos - slot);
-        unsigned char *h = cl->h_pinned + slot * B, *d = dev + p0 * B;
-        const hipError_t e = to_host
-            ? hipMemcpy2DAsync(h, hpitch, d, dpitch, (size_t)run * B, (size_t)cl->n_heads, hipMemcpyDeviceToHost, s)
-            : hipMemcpy2DAsync(d, dpitch, h, hpitch, (size_t)run * B, (size_t)cl->n_heads, hipMemcpyHostToDevice, s);
-        if (!hip_ok(e, "cold copy")) return false;
-        p0 += run;
-        n -= run;
-    }
-    return true;
-}
-
-extern "C" int sp_hip_cold_writeback(sp_hip_cold_layer_t *cl, const void *d_packed, int start_pos, int n_pos,
-                                     void *stream) {
-    if (!cl || !cl->initialized || !d_packed || n_pos <= 0 || start_pos < 0 ||
-        (long long)start_pos + n_pos > cl->max_seq_len) { set_err("cold_writeback: bad args"); return -1; }
-    // the ring keeps the newest cap_pos positions: copy only those of the range
-    const int64_t newest = std::max<int64_t>(cl->newest_pos, (int64_t)start_pos + n_pos - 1);
-    const int64_t oldest = newest >= cl->cap_pos ? newest - cl->cap_pos + 1 : 0;
-    const long long p0 = std::max<long long>(start_pos, oldest), n = (long long)start_pos + n_pos - p0;
-    if (n > 0 && !cold_copy(cl, (unsigned char *)d_packed, p0, n, true, (hipStream_t)stream)) return -1;
-    cl->newest_pos = newest;
-    cl->oldest_pos = oldest;
-    cl->ring_mode = newest >= cl->cap_pos;
-    cl->write_head = (newest + 1) % cl->cap_pos;
-    return 0;
-}
-
-// Positions [0, n_pos) back to the slab; -1 when some of them have left the ring.
-extern "C" int sp_hip_cold_restore(const sp_hip_cold_layer_t *cl, void *d_packed, int n_pos, void *stream) {
-    if (!cl || !cl->initialized || !d_packed || n_pos <= 0) { set_err("cold_restore: bad args"); return -1; }
-    if (cl->oldest_pos != 0 || n_pos > cl->newest_pos + 1) {
-        set_err("cold_restore: positions [0, %d) are not all in the mirror (oldest %lld, newest %lld)", n_pos,
-                (long long)cl->oldest_pos, (long long)cl->newest_pos);
-        return -1;
-    }
-    return cold_copy(cl, (unsigned char *)d_packed, 0, n_pos, false, (hipStream_t)stream) ? 0 : -1;
-}
-
 // Memory report of a ship cache (sp_cuda_print_memory, shannon_prime_cuda.cu:663-677):
 // record bytes against an fp16 K+V cache of the same shape.
 extern "C" void sp_hip_print_memory(const sp_hip_cache_t *cc) {

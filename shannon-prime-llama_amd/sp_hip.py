@@ -214,12 +214,6 @@ def lib():
         L.sp_shadow_cache_load.argtypes = [vp, cp, u64]
         L.sp_shadow_cache_load_partial.argtypes = [vp, cp, u64, i]
         L.sp_hip_memset.argtypes = [vp, i, C.c_size_t, vp]
-        L.sp_hip_cold_layer_init.argtypes = [vp, C.c_int64, i, i, i]
-        L.sp_hip_cold_layer_free.argtypes = [vp]
-        L.sp_hip_cold_writeback.argtypes = [vp, vp, i, i, vp]
-        L.sp_hip_cold_restore.argtypes = [vp, vp, i, vp]
-        L.sp_hip_d2h_async.argtypes = [vp, vp, C.c_int64, vp]
-        L.sp_hip_h2d_async.argtypes = [vp, vp, C.c_int64, vp]
         L.sp_hip_dual_init.argtypes = [vp, vp, i, vp, f]
         L.sp_hip_dual_free.argtypes = [vp]
         L.sp_hip_dual_route_position.argtypes = [vp, i, f]
