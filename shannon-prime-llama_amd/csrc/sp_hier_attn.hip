@@ -209,16 +209,19 @@ __device__ __forceinline__ float add_xor1(float v) {
     return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));
 }
 
-// Eight 2-bit levels (bits 0..15 of y) -> the A operand slots of v_mfma_f32_16x16x32_f16
-// as fp16 4 + level (exact): level pair m (bits 4m..4m+3) times 2^8 + 2^22 puts the two
-// levels at bits 8-9 and 24-25 (the other copies land outside the mask), and the
-// exponent bits of 4.0 in both halves finish the pair.
-__device__ __forceinline__ half8_t level_pairs2(uint32_t y) {
+// v_perm_b32 selector taking bytes b and b + 1 (b < 4) of the dword pair (hi:lo) into
+// bytes 1 and 3, zeros elsewhere (selector bytes 0-3 pick lo's bytes, 4-7 hi's, 0x0C
+// gives zero).
+__device__ __forceinline__ uint32_t level_bytes_sel(uint32_t b) { return 0x000C000Cu | (b << 8) | ((b + 1u) << 24); }
+
+// Eight 2-bit levels held as byte 1 (levels 0-3 at bits 8 + 2e) and byte 3 (levels
+// 4-7 at bits 24 + 2e) of x -> the A operand slots of v_mfma_f32_16x16x32_f16 as fp16
+// 4 + level (exact): dword m takes levels m and m + 4 (slots 2m and 2m + 1), shifted
+// to bits 8-9 and 24-25, with the exponent bits of 4.0 in both halves.
+__device__ __forceinline__ half8_t level_quads2(uint32_t x) {
     u32x4 v;
 #pragma unroll
-    for (int m = 0; m < 4; m++)
-        v[m] = __builtin_amdgcn_bitop3_b32(__builtin_amdgcn_ubfe(y, 4u * m, 4u) * 0x00400100u, 0x03000300u,
-                                           0x44004400u, 0xEA);
+    for (int m = 0; m < 4; m++) v[m] = __builtin_amdgcn_bitop3_b32(x >> (2 * m), 0x03000300u, 0x44004400u, 0xEA);
     return __builtin_bit_cast(half8_t, v);
 }
 
@@ -258,17 +261,19 @@ __device__ __forceinline__ void vm_level_dwords(const uint32_t (&ad)[8], int off
 
 // A operand of the V level sums (v_mfma_f32_16x16x32_f16, rows = coefficients, K =
 // positions): the lane's 2-bit level at eight positions as fp16 level - 1.5 (exact).
-// With each level shifted to bits 0-1, a byte permute takes the pair (e, e + 1) into
-// bytes 1 and 3, the and-or makes fp16 4 + level in both halves, and a packed subtract
-// of 5.5 centres it.
-__device__ __forceinline__ half8_t vm_levels(const uint32_t (&d)[8], const uint32_t (&sh)[8]) {
-    uint32_t x[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) x[e] = d[e] >> sh[e];
+// Positions m and m + 4 (slots 2m and 2m + 1) have their level at the same bit of their
+// dwords d[m], d[m + 4] (their records are 4 record lengths apart, a whole number of
+// dwords): a byte permute (selector sel[m]) takes the level's byte of each into bytes 1
+// and 3, one shift by k[m] = bit % 8 puts the levels at bits 8-9 and 24-25, the and-or
+// makes fp16 4 + level in both halves, and a packed subtract of 5.5 centres it (centring
+// at the end of a run instead, from a weight sum, lost too much precision over long
+// runs of positions).
+__device__ __forceinline__ half8_t vm_levels(const uint32_t (&d)[8], const uint32_t (&sel)[4],
+                                             const uint32_t (&k)[4]) {
     u32x4 v;
 #pragma unroll
     for (int m = 0; m < 4; m++)
-        v[m] = __builtin_amdgcn_bitop3_b32(__builtin_amdgcn_perm(x[2 * m + 1], x[2 * m], 0x040C000Cu), 0x03000300u,
+        v[m] = __builtin_amdgcn_bitop3_b32(__builtin_amdgcn_perm(d[m + 4], d[m], sel[m]) >> k[m], 0x03000300u,
                                            0x44004400u, 0xEA);
     return __builtin_bit_cast(half8_t, v) - (_Float16)5.5f;
 }
@@ -288,10 +293,30 @@ __device__ __forceinline__ half8_t vm_codes(const uint32_t (&ad)[8], const uint3
     return __builtin_bit_cast(half8_t, v) - sub;
 }
 
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// Wave-wide all-reduce on the VALU (no LDS round trips): DPP quad permutes and row
+// mirrors inside each row of 16 lanes, then the gfx950 row swaps across rows.
+// permlane16/32_swap(v, v) return this lane's value and its partner's (lane ^ 16,
+// lane ^ 32) in an order that depends on the lane, so a commutative op of the two
+// gives every lane the same result. Call with the whole wave active.
+template <class Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+    v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true)));   // quad [1,0,3,2]
+    v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true)));   // quad [2,3,0,1]
+    v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true)));  // row_half_mirror
+    v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true)));  // row_mirror
+    u32x2 t = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = op(__uint_as_float(t[0]), __uint_as_float(t[1]));
+    t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return op(__uint_as_float(t[0]), __uint_as_float(t[1]));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, SP_WAVE);
-    return v;
+    return wave_reduce(v, [](float a, float b) { return a + b; });
+}
+// maximum of non-NaN values
+__device__ __forceinline__ float wave_max(float v) {
+    return wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
 // ---------------------------------------------------------------------------
@@ -443,9 +468,10 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
     // RB == 2: the target dots run on v_mfma_f32_16x16x32_f16 with the levels as the A
     // operand (rows = positions, fp16 4 + level) and q~_tgt as B: column c16 = (head
     // c16 >> 1, hi / lo fp16 part c16 & 1) of q~_tgt scaled by a power of two per head.
-    // bq[j][q4][c16]: the 8 B-operand halves of levels 32 j + 8 q4 .. +7; cin[c16]: the
-    // accumulator start -(4 + centre) * (column sum), which centres the levels; unh: the
-    // inverse scale. The skeleton bands stay on the position threads.
+    // bq[j][q4][c16]: the 8 B-operand halves of levels 32 j + 8 q4 + e, e < 8, in the
+    // A operand's order (slot 2 (e & 3) + (e >> 2): levels e and e + 4 share a dword);
+    // cin[c16]: the accumulator start -(4 + centre) * (column sum), which centres the
+    // levels; unh: the inverse scale. The skeleton bands stay on the position threads.
     constexpr bool KM = RB == 2;
     const int n_kb = r32(nt) / 32;
     u32x4 *bq = reinterpret_cast<u32x4 *>(red + 8 * MAX_G);
@@ -458,7 +484,7 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
         for (int h = wv; h < G; h += NT / SP_WAVE) {
             float am = 0.0f;
             for (int kk = lane; kk < nt; kk += SP_WAVE) am = fmaxf(am, fabsf(prep_s[h * A.ps + qo + kk]));
-            am = sp_wave_max(am);
+            am = wave_max(am);
             if (lane == 0) fh[h] = pow2_norm(am);
         }
         __syncthreads();
@@ -471,7 +497,8 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
             const _Float16 lo = (_Float16)(v - (float)hi);
             const _Float16 x = (c16 & 1) ? lo : hi;
             colsum += (float)x;
-            bqh[(((kk >> 5) * 4 + ((kk >> 3) & 3)) * 16 + c16) * 8 + (kk & 7)] = __builtin_bit_cast(unsigned short, x);
+            bqh[(((kk >> 5) * 4 + ((kk >> 3) & 3)) * 16 + c16) * 8 + 2 * (kk & 3) + ((kk >> 2) & 1)] =
+                __builtin_bit_cast(unsigned short, x);
         }
         psum[(tid >> 4) * 16 + c16] = colsum;
         __syncthreads();
@@ -590,13 +617,19 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
             const int r = lane & 15, q4 = lane >> 4;
             const float ci = cin[r], un = unh[r];
             const bool wr = !(r & 1) && (r >> 1) < G;
+            const uint32_t rec_k = lds_addr(rec);
 #pragma unroll
             for (int sub = 0; sub < 4; sub++) {
                 const int pos0 = 64 * wv + 16 * sub;
                 float4_t acc = {ci, ci, ci, ci};
+                // the lane's 16 level bits of window j start at byte ob + 8 j: a byte permute
+                // with a per-lane selector takes those two bytes of the aligned dword pair
                 const int ob = shift + (pos0 + r) * B + skB + 4 + 2 * q4;
+                const uint32_t ka = rec_k + (uint32_t)(ob & ~3);
+                const uint32_t ksel = level_bytes_sel((uint32_t)ob & 3u);
                 for (int j = 0; j < n_kb; j++) {
-                    const half8_t code = level_pairs2(lds_u32_at(rec, ob + 8 * j));
+                    lds_cu32 *w = (lds_cu32 *)(uintptr_t)(ka + 8u * (uint32_t)j);
+                    const half8_t code = level_quads2(__builtin_amdgcn_perm(w[1], w[0], ksel));
                     const half8_t bv = __builtin_bit_cast(half8_t, bq[(j * 4 + q4) * 16 + r]);
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(code, bv, acc, 0, 0, 0);
                 }
@@ -682,7 +715,7 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
 #pragma unroll
             for (int h = 0; h < GM; h++) {
                 if (h < G) {
-                    const float v = sp_wave_max(mx[h]);
+                    const float v = wave_max(mx[h]);
                     if (lane == 0) red[wv * MAX_G + h] = v;
                 }
             }
@@ -736,17 +769,20 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
             float wmax = vstep;
             for (int b = 0; b < nb; b++)
                 if (live) wmax = fmaxf(wmax, sp_scale_from_bits(lds_u32_at(rec, rb + P.band_byte_off[b]) & 0xffffu));
-            wmax = sp_wave_max(wmax);
+            wmax = wave_max(wmax);
             if (lane == 0) red[wv] = wmax;
             __syncthreads();
             const float f = pow2_norm(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
             _Float16 *pwq = reinterpret_cast<_Float16 *>(pw);
             _Float16 *psq = reinterpret_cast<_Float16 *>(psb);
+            // target weights in the level operand's position order: within each group of
+            // eight, position e at slot 2 (e & 3) + (e >> 2)
+            const int wslot = (tid & ~7) | (2 * (tid & 3)) | ((tid >> 2) & 1);
             for (int h = 0; h < G; h++) {
                 const float v = sc[h * CH + tid] * vstep * f;
                 const _Float16 hi = (_Float16)v;
-                pwq[(2 * h) * CH + tid] = hi;
-                pwq[(2 * h + 1) * CH + tid] = (_Float16)(v - (float)hi);
+                pwq[(2 * h) * CH + wslot] = hi;
+                pwq[(2 * h + 1) * CH + wslot] = (_Float16)(v - (float)hi);
             }
             for (int b = 0; b < nb; b++) {
                 const float scale =
@@ -771,9 +807,10 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
 #pragma unroll
             for (int i = 0; i < VM_TB; i++) vacc[i] *= ac;
             vsk *= ac;
-            // dword address and bit shift of each K position's first row-block field at
-            // group 0 (the groups step by 32 B bytes, a whole number of dwords)
-            uint32_t ta[8], tsh[8], sa[8], ssh[8];
+            // dword address of each K position's first row-block field at group 0 (the
+            // groups step by 32 B bytes, a whole number of dwords), and for the level
+            // windows the byte permute and shift of the position pairs (m, m + 4)
+            uint32_t ta[8], tsel[4], tk[4], sa[8], ssh[8];
             const uint32_t rec_lds = lds_addr(rec);
             const int vbits = P.band_bits[vm_b];
 #pragma unroll
@@ -781,7 +818,11 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
                 const int p0 = vshift + (8 * kq + e) * B;
                 const int tb = 8 * (p0 + skB + 4 + 4 * wv) + 2 * jc;
                 ta[e] = rec_lds + ((uint32_t)(tb >> 5) << 2);
-                tsh[e] = (uint32_t)tb & 31u;
+                if (e < 4) {
+                    const uint32_t bsel = ((uint32_t)tb & 31u) >> 3;
+                    tsel[e] = 0x000C000Cu | (bsel << 8) | ((4u + bsel) << 24);
+                    tk[e] = (uint32_t)tb & 7u;
+                }
                 const int sbp = 8 * (p0 + P.band_byte_off[vm_b] + 2) + vbits * (16 * vm_k + jc);
                 sa[e] = rec_lds + ((uint32_t)(sbp >> 5) << 2);
                 ssh[e] = (uint32_t)sbp & 31u;
@@ -811,7 +852,7 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
 #pragma unroll
                 for (int i = 0; i < VM_TB; i++) {
                     if (i + 1 < VM_TB) vm_level_dwords(ta, 16 * (i + 1), dw[(i + 1) & 1]);
-                    const half8_t a = vm_levels(dw[i & 1], tsh);
+                    const half8_t a = vm_levels(dw[i & 1], tsel, tk);
                     vacc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bt, vacc[i], 0, 0, 0);
                 }
 #pragma unroll
@@ -1033,7 +1074,7 @@ k_hier_attn_merge(const SpPlan P, const SpHierAttnArgs A, const float *__restric
     float mx = -INFINITY;
 #pragma unroll
     for (int u = 0; u < MERGE_RUNS_PER_THREAD; u++) mx = fmaxf(mx, mr[u]);
-    mx = sp_wave_max(mx);
+    mx = wave_max(mx);
     if (lane == 0) red[wv] = mx;
     __syncthreads();
     const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
