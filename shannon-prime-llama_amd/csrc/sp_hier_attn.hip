@@ -90,7 +90,29 @@ struct RegStage {
         }
     }
 };
-constexpr int K_STAGE = 26;  // K record dwords per thread staged through registers (256 x 103 B chunks)
+
+// REC_U * NT record dwords staged through registers by range-checked buffer loads
+// (dwords past n read as 0), so neither the loads nor the LDS stores need a per-element
+// test: the destination holds REC_U * NT dwords and takes them all, zeros included.
+constexpr int REC_U = 26;  // covers a chunk of 256 records of up to 103 B, plus the readers' look-ahead
+struct RecStage {
+    uint32_t v[REC_U];
+    __device__ void load(const uint32_t *__restrict__ src, int n, int tid) {
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void *)src, (short)0, 4 * n, 0x00020000);
+#pragma unroll
+        for (int u = 0; u < REC_U; u++) v[u] = __builtin_amdgcn_raw_buffer_load_b32(r, 4 * (tid + u * NT), 0, 0);
+    }
+    __device__ void store(uint32_t *dst, int tid) const {
+#pragma unroll
+        for (int u = 0; u < REC_U; u++) dst[tid + u * NT] = v[u];
+    }
+};
+// LDS bytes of the record staging for record length B: the chunk with its 32-byte
+// slack, and at least the whole RecStage area.
+__host__ __device__ constexpr int rec_stage_bytes(int B) {
+    return (((CH * B + 32) + 15) & ~15) > 4 * REC_U * NT ? (((CH * B + 32) + 15) & ~15) : 4 * REC_U * NT;
+}
+constexpr int K_STAGE = REC_U;  // K record dwords per thread staged through registers (256 x 103 B chunks)
 constexpr int W_STAGE = 40;  // W elements per thread staged through registers (n_target * n_skel <= 10240)
 constexpr int W_DW = 20;     // W dwords (fp16 pairs) per prep thread staged through registers
 constexpr int MERGE_RUNS_PER_THREAD = 4;  // runs per merge thread (n_runs <= 4 * NT)
@@ -450,7 +472,7 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
     const int ns = A.n_skel, nt = A.n_target, B = A.B, nb = P.n_bands;
     const int qo = prep_qt_off(ns), so = prep_sum_off(ns, nt);
     constexpr bool want_out = OUT;
-    const int rec_bytes = ((CH * B + 32) + 15) & ~15;
+    const int rec_bytes = rec_stage_bytes(B);
     unsigned char *rec = dsm;
     uint32_t *rec32 = reinterpret_cast<uint32_t *>(dsm);
     float *prep_s = reinterpret_cast<float *>(dsm + rec_bytes);
@@ -579,8 +601,10 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
 
     const int n_chunks = (A.n_kv + CH - 1) / CH;
     // scores only: chunk ch's K records wait in registers (kst) from the previous chunk on
-    const bool k_pre = !OUT && (CH * B + 6) / 4 <= K_STAGE * NT;
-    RegStage<uint32_t, K_STAGE> kst;
+    // (the staging's reads cover ndw + 3 dwords: the records and the readers' look-ahead)
+    const bool k_pre = !OUT && (CH * B + 6) / 4 + 3 <= REC_U * NT;
+    const bool rec_fast = (CH * B + 6) / 4 + 3 <= REC_U * NT;  // one RecStage covers a chunk
+    RecStage kst;
     auto k_src = [&](int chn, int &shift_, int &ndw_) {
         const int c0_ = chn * CH, n_t_ = min(CH, A.n_kv - c0_);
         const unsigned char *kg_ = A.kcache + (long long)kvh * A.slot_bytes + (long long)c0_ * B;
@@ -601,13 +625,16 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
         const uint32_t *ksrc = k_src(ch, shift, ndw);
         __syncthreads();  // the previous chunk is done with rec / sc
         if (k_pre) {
-            kst.store(rec32, ndw, tid);
-            if (tid < 3) rec32[ndw + tid] = 0u;  // the bit readers' look-ahead
+            kst.store(rec32, tid);  // zeros past the records: the bit readers' look-ahead
             if (ch + n_runs < n_chunks) {
                 int sh_, nd_;
                 const uint32_t *src_ = k_src(ch + n_runs, sh_, nd_);
                 kst.load(src_, nd_, tid);
             }
+        } else if (rec_fast) {
+            RecStage st;
+            st.load(ksrc, ndw, tid);
+            st.store(rec32, tid);
         } else {
             copy_to_lds<uint32_t, 32>(rec32, ksrc, ndw, ndw + 3, tid);
         }
@@ -758,7 +785,13 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
         const unsigned char *vg = A.vcache + (long long)kvh * A.slot_bytes + (long long)c0 * B;
         const int vshift = (int)((uintptr_t)vg & 3);
         const int vdw = (n_t * B + vshift + 3) >> 2;
-        copy_to_lds<uint32_t, 32>(rec32, reinterpret_cast<const uint32_t *>(vg - vshift), vdw, vdw + 3, tid);
+        if (rec_fast) {
+            RecStage st;
+            st.load(reinterpret_cast<const uint32_t *>(vg - vshift), vdw, tid);
+            st.store(rec32, tid);
+        } else {
+            copy_to_lds<uint32_t, 32>(rec32, reinterpret_cast<const uint32_t *>(vg - vshift), vdw, vdw + 3, tid);
+        }
         __syncthreads();
         if constexpr (VM) {
             // ---- weights as fp16 hi + lo rows, scaled by f (a power of two putting the
@@ -1224,7 +1257,7 @@ hipError_t sp_launch_hier_attn(const SpPlan &P, const SpHierAttnArgs &A, const S
     const int rb = window_bits(A);
     const size_t lds_prep = 4 * (size_t)(r4(A.pad) + r32(A.n_target) + 8 * r4(A.n_skel)) +
                             2 * (size_t)A.n_target * A.n_skel;
-    const size_t rec_bytes = (size_t)(((CH * A.B + 32) + 15) & ~15);
+    const size_t rec_bytes = (size_t)rec_stage_bytes(A.B);
     size_t lds_split = rec_bytes + 4 * ((size_t)G * A.ps + (size_t)(2 + P.n_bands) * G * CH + 8 * MAX_G);
     if (rb == 2) lds_split += (size_t)r32(A.n_target) / 32 * 1024 + 4 * (16 + 16 + 8 + 256);
     if (rb > 0) {
