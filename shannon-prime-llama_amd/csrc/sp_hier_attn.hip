@@ -117,6 +117,22 @@ constexpr int W_STAGE = 40;  // W elements per thread staged through registers (
 constexpr int W_DW = 20;     // W dwords (fp16 pairs) per prep thread staged through registers
 constexpr int MERGE_RUNS_PER_THREAD = 4;  // runs per merge thread (n_runs <= 4 * NT)
 
+// Record geometry of the split kernel: read from the call (GeoRt), or fixed at compile
+// time (GeoCt: NB skeleton bands of SZ codes of BITS bits, band b's bytes at b *
+// band_bytes, then the fp32 magnitude, then NTG 2-bit target levels), which turns the
+// skeleton bit positions and the LDS offsets of the level windows into constants.
+struct GeoRt {
+    static constexpr bool ct = false;
+    static constexpr int nb = 0, sz = 0, bits = 0, band_bytes = 0, skB = 0, ns = 0, nt = 0, B = 0;
+};
+template <int NB, int SZ, int BITS, int NTG>
+struct GeoCt {
+    static constexpr bool ct = true;
+    static constexpr int nb = NB, sz = SZ, bits = BITS, band_bytes = 2 + (SZ * BITS + 7) / 8;
+    static constexpr int skB = NB * band_bytes, ns = NB * SZ, nt = NTG, B = skB + 4 + (2 * NTG + 7) / 8;
+};
+using Geo330 = GeoCt<2, 15, 5, 300>;  // the default hier geometry at pad 330 (hd 256): 103-byte records
+
 // 4 little-endian bytes at LDS byte offset o (any alignment) of a dword-aligned array.
 __device__ __forceinline__ uint32_t lds_u32_at(const unsigned char *base, int o) {
     const uint32_t *w = reinterpret_cast<const uint32_t *>(base + (o & ~3));
@@ -126,6 +142,14 @@ __device__ __forceinline__ uint32_t lds_u32_at(const unsigned char *base, int o)
 // nbits (<= 8) bits at bit `bit` (0..7) of byte offset o.
 __device__ __forceinline__ uint32_t lds_bits_at(const unsigned char *base, int o, int bit, int nbits) {
     return __builtin_amdgcn_ubfe(lds_u32_at(base, o), (uint32_t)bit, (uint32_t)nbits);
+}
+
+// N bits at bit `pos` (a constant after unrolling) of the dword array r.
+template <int N, int W>
+__device__ __forceinline__ uint32_t ct_field(const uint32_t (&r)[W], int pos) {
+    const int w = pos >> 5, sh = pos & 31;
+    if (sh + N <= 32) return __builtin_amdgcn_ubfe(r[w], (uint32_t)sh, (uint32_t)N);
+    return __builtin_amdgcn_ubfe(__builtin_amdgcn_alignbit(r[w + 1], r[w], (uint32_t)sh), 0u, (uint32_t)N);
 }
 
 // LSB-first bit stream starting at byte offset o of a dword-aligned LDS array.
@@ -261,7 +285,7 @@ __device__ __forceinline__ uint32_t lds_addr(const unsigned char *p) {
 // The eight positions' fields of one V row-block operand: position e's field starts
 // at bit sh[e] of the dword pair at LDS byte address ad[e] + off; all sixteen dwords
 // are read before the funnel shifts, so the reads overlap.
-__device__ __forceinline__ void vm_fields(const uint32_t (&ad)[8], const uint32_t (&sh)[8], int off,
+__device__ __forceinline__ void vm_fields(const uint32_t (&ad)[8], const uint32_t (&sh)[8], uint32_t off,
                                           uint32_t (&x)[8]) {
     uint32_t d[8][2];
 #pragma unroll
@@ -276,7 +300,7 @@ __device__ __forceinline__ void vm_fields(const uint32_t (&ad)[8], const uint32_
 
 // The dwords holding eight positions' 2-bit levels (a level's bit offset 8 * byte +
 // 2 * coefficient is even, so it never crosses a dword).
-__device__ __forceinline__ void vm_level_dwords(const uint32_t (&ad)[8], int off, uint32_t (&d)[8]) {
+__device__ __forceinline__ void vm_level_dwords(const uint32_t (&ad)[8], uint32_t off, uint32_t (&d)[8]) {
 #pragma unroll
     for (int e = 0; e < 8; e++) d[e] = *(lds_cu32 *)(uintptr_t)(ad[e] + off);
 }
@@ -303,7 +327,7 @@ __device__ __forceinline__ half8_t vm_levels(const uint32_t (&d)[8], const uint3
 // The same for a skeleton band's `bits`-bit codes (bits <= 8): fp16 2^bits + code from the
 // code's byte (exponent bits `base`, the code shifted by 10 - bits under `mask`), minus
 // `sub` = 2^bits + the band's offset (exact).
-__device__ __forceinline__ half8_t vm_codes(const uint32_t (&ad)[8], const uint32_t (&sh)[8], int off,
+__device__ __forceinline__ half8_t vm_codes(const uint32_t (&ad)[8], const uint32_t (&sh)[8], uint32_t off,
                                             uint32_t sh10, uint32_t mask, uint32_t base, _Float16 sub) {
     uint32_t x[8];
     vm_fields(ad, sh, off, x);
@@ -452,7 +476,7 @@ k_hier_attn_prep(const SpPlan P, const SpHierAttnArgs A, float *__restrict__ pre
 // items. pw and psb then hold the weights as fp16 hi and lo rows ([h][hi, lo][CH] and
 // [b][h][hi, lo][CH], the same bytes), scaled by a power of two per chunk; the sums
 // need no position-group reduction at the end of the run.
-template <int RB, int GM, bool OUT, bool VM>
+template <int RB, int GM, bool OUT, bool VM, class GEO>
 __global__ void __launch_bounds__(NT, 3)
 k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, const float *__restrict__ prep0,
                   float *__restrict__ part0, int n_runs) {
@@ -469,7 +493,13 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
     const float *__restrict__ prep = prep0 + (long long)seq * A0.n_q * A0.ps;
     float *__restrict__ part = part0 + (long long)seq * A0.n_q * n_runs * A0.pp;
     const int G = A.n_q / A.n_kvh, h0 = kvh * G;
-    const int ns = A.n_skel, nt = A.n_target, B = A.B, nb = P.n_bands;
+    const int ns = GEO::ct ? GEO::ns : A.n_skel, nt = GEO::ct ? GEO::nt : A.n_target;
+    const int B = GEO::ct ? GEO::B : A.B, nb = GEO::ct ? GEO::nb : P.n_bands;
+    // band b's layout (constants for a compile-time geometry)
+    auto band_bits = [&](int b) { return GEO::ct ? GEO::bits : (int)P.band_bits[b]; };
+    auto band_off = [&](int b) { return GEO::ct ? b * GEO::sz : (int)P.band_off[b]; };
+    auto band_sz = [&](int b) { return GEO::ct ? GEO::sz : (int)P.band_sz[b]; };
+    auto band_byte_off = [&](int b) { return GEO::ct ? b * GEO::band_bytes : (int)P.band_byte_off[b]; };
     const int qo = prep_qt_off(ns), so = prep_sum_off(ns, nt);
     constexpr bool want_out = OUT;
     const int rec_bytes = rec_stage_bytes(B);
@@ -480,7 +510,7 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
     float *pw = sc + G * CH;
     float *psb = pw + G * CH;
     float *red = psb + nb * G * CH;
-    const int skB = P.total_bytes;
+    const int skB = GEO::ct ? GEO::skB : P.total_bytes;
     const int Lv = 1 << A.rbits;
     const float step_div = (float)(Lv - 1);
     const float centre = sp_div((float)(Lv - 1), 2.0f);
@@ -533,6 +563,22 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
         // the chunk loop's first barrier orders these before their use
     }
 
+    // compile-time geometry: each skeleton band's query sum per head (identical in every
+    // thread; prep_s is visible after the matrix-core setup's barriers)
+    static_assert(!GEO::ct || KM, "the compile-time geometry has 2-bit levels");
+    float qsk[GM][GEO::ct ? GEO::nb : 1];
+    if constexpr (GEO::ct) {
+#pragma unroll
+        for (int h = 0; h < GM; h++)
+#pragma unroll
+            for (int b = 0; b < GEO::nb; b++) {
+                float t = 0.0f;
+                if (h < G)
+                    for (int i = 0; i < GEO::sz; i++) t += prep_s[h * A.ps + b * GEO::sz + i];
+                qsk[h][b] = t;
+            }
+    }
+
     // running softmax state per head (identical in every thread)
     float m_run[GM], l_run[GM];
 #pragma unroll
@@ -568,9 +614,9 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
     const int t_ha = 2 * t_hp, t_hb = min(2 * t_hp + 1, G - 1);
     const int s_ha = 2 * s_hp, s_hb = min(2 * s_hp + 1, G - 1);
     int s_b = 0;
-    while (s_b + 1 < nb && s_s >= P.band_off[s_b + 1]) s_b++;
-    const int s_bits = P.band_bits[s_b], s_bo = (s_s - P.band_off[s_b]) * s_bits;
-    const int s_byte = P.band_byte_off[s_b] + 2 + (s_bo >> 3), s_bit = s_bo & 7;
+    while (s_b + 1 < nb && s_s >= band_off(s_b + 1)) s_b++;
+    const int s_bits = band_bits(s_b), s_bo = (s_s - band_off(s_b)) * s_bits;
+    const int s_byte = band_byte_off(s_b) + 2 + (s_bo >> 3), s_bit = s_bo & 7;
     const float s_off = (float)((1 << (s_bits - 1)) - 1);
 
     // VM: row blocks of 16 coefficients. Target window wv + 4 i (i < VM_TB) belongs to
@@ -583,7 +629,7 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
     constexpr int VM_TB = 5;
     int vm_nsb = 0;
     if (VM)
-        for (int b = 0; b < nb; b++) vm_nsb += (P.band_sz[b] + 15) >> 4;
+        for (int b = 0; b < nb; b++) vm_nsb += (band_sz(b) + 15) >> 4;
     // this wave's skeleton block (vm_s), band vm_b, coefficients 16 vm_k ..
     bool vm_s = false;
     int vm_b = 0, vm_k = 0;
@@ -591,7 +637,7 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
         int sb = ((wv - n_win) % 4 + 4) % 4;
         if (sb < vm_nsb) {
             vm_s = true;
-            while (vm_b + 1 < nb && sb >= ((P.band_sz[vm_b] + 15) >> 4)) sb -= (P.band_sz[vm_b++] + 15) >> 4;
+            while (vm_b + 1 < nb && sb >= ((band_sz(vm_b) + 15) >> 4)) sb -= (band_sz(vm_b++) + 15) >> 4;
             vm_k = sb;
         }
     }
@@ -654,6 +700,8 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
                 const int ob = shift + (pos0 + r) * B + skB + 4 + 2 * q4;
                 const uint32_t ka = rec_k + (uint32_t)(ob & ~3);
                 const uint32_t ksel = level_bytes_sel((uint32_t)ob & 3u);
+                constexpr int KJ_UNROLL = GEO::ct ? 32 : 1;  // constant window offsets when unrolled
+#pragma unroll KJ_UNROLL
                 for (int j = 0; j < n_kb; j++) {
                     lds_cu32 *w = (lds_cu32 *)(uintptr_t)(ka + 8u * (uint32_t)j);
                     const half8_t code = level_quads2(__builtin_amdgcn_perm(w[1], w[0], ksel));
@@ -671,17 +719,50 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
         // ---- scores: thread = position ----
         if (tid < n_t) {
             const int rb = shift + tid * B;
-            const float mag = __uint_as_float(lds_u32_at(rec, rb + skB));
+            // compile-time geometry: the record's skeleton bytes and magnitude as dwords
+            // aligned to the record's start (rsk[k] = record bytes 4k .. 4k + 3)
+            constexpr int SKW = GEO::ct ? (GEO::skB + 4 + 3) / 4 : 1;
+            uint32_t rsk[SKW];
+            if constexpr (GEO::ct) {
+                lds_cu32 *w = (lds_cu32 *)(uintptr_t)(lds_addr(rec) + (uint32_t)(rb & ~3));
+                uint32_t d[SKW + 1];
+#pragma unroll
+                for (int k = 0; k <= SKW; k++) d[k] = w[k];
+                const uint32_t fs = 8u * (uint32_t)(rb & 3);
+#pragma unroll
+                for (int k = 0; k < SKW; k++) rsk[k] = __builtin_amdgcn_alignbit(d[k + 1], d[k], fs);
+            }
+            const float mag = __uint_as_float(GEO::ct ? rsk[SKW - 1] : lds_u32_at(rec, rb + skB));
             const float step = sp_div(2.0f * mag, step_div);
             for (int hp = 0; hp < G; hp += 2) {
                 const int ha = hp, hb = hp + 1 < G ? hp + 1 : hp;
                 const float *ua = prep_s + ha * A.ps, *ub = prep_s + hb * A.ps;
                 float s0 = 0.0f, s1 = 0.0f;
+                if constexpr (GEO::ct) {
+                    // codes at constant bits; the offset 2^(bits-1) - 1 comes off as that
+                    // times the band's query sum (qsk)
+                    constexpr int maxv = (1 << (GEO::bits - 1)) - 1;
+#pragma unroll
+                    for (int b = 0; b < GEO::nb; b++) {
+                        const float scale = sp_scale_from_bits(ct_field<16>(rsk, 8 * b * GEO::band_bytes));
+                        float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+                        for (int i = 0; i < GEO::sz; i++) {
+                            const float cv = (float)ct_field<GEO::bits>(rsk, 8 * (b * GEO::band_bytes + 2) + GEO::bits * i);
+                            a0 = fmaf(ua[b * GEO::sz + i], cv, a0);
+                            a1 = fmaf(ub[b * GEO::sz + i], cv, a1);
+                        }
+                        a0 = fmaf(-(float)maxv, qsk[ha][b], a0);
+                        a1 = fmaf(-(float)maxv, qsk[hb][b], a1);
+                        s0 = fmaf(scale, a0, s0);
+                        s1 = fmaf(scale, a1, s1);
+                    }
+                } else
                 for (int b = 0; b < nb; b++) {
-                    const int bits = P.band_bits[b], off = P.band_off[b], sz = P.band_sz[b];
+                    const int bits = band_bits(b), off = band_off(b), sz = band_sz(b);
                     const int maxv = (1 << (bits - 1)) - 1;
-                    const float scale = sp_scale_from_bits(lds_u32_at(rec, rb + P.band_byte_off[b]) & 0xffffu);
-                    LdsBits br(rec, rb + P.band_byte_off[b] + 2);
+                    const float scale = sp_scale_from_bits(lds_u32_at(rec, rb + band_byte_off(b)) & 0xffffu);
+                    LdsBits br(rec, rb + band_byte_off(b) + 2);
                     float a0 = 0.0f, a1 = 0.0f;
                     for (int i = 0; i < sz; i++) {
                         const float cv = (float)((int)br.get(bits) - maxv);
@@ -801,7 +882,7 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
             const float vstep = live ? sp_div(2.0f * __uint_as_float(lds_u32_at(rec, rb + skB)), step_div) : 0.0f;
             float wmax = vstep;
             for (int b = 0; b < nb; b++)
-                if (live) wmax = fmaxf(wmax, sp_scale_from_bits(lds_u32_at(rec, rb + P.band_byte_off[b]) & 0xffffu));
+                if (live) wmax = fmaxf(wmax, sp_scale_from_bits(lds_u32_at(rec, rb + band_byte_off(b)) & 0xffffu));
             wmax = wave_max(wmax);
             if (lane == 0) red[wv] = wmax;
             __syncthreads();
@@ -819,7 +900,7 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
             }
             for (int b = 0; b < nb; b++) {
                 const float scale =
-                    live ? sp_scale_from_bits(lds_u32_at(rec, rb + P.band_byte_off[b]) & 0xffffu) : 0.0f;
+                    live ? sp_scale_from_bits(lds_u32_at(rec, rb + band_byte_off(b)) & 0xffffu) : 0.0f;
                 for (int h = 0; h < G; h++) {
                     const float v = sc[h * CH + tid] * scale * f;
                     const _Float16 hi = (_Float16)v;
@@ -845,7 +926,7 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
             // windows the byte permute and shift of the position pairs (m, m + 4)
             uint32_t ta[8], tsel[4], tk[4], sa[8], ssh[8];
             const uint32_t rec_lds = lds_addr(rec);
-            const int vbits = P.band_bits[vm_b];
+            const int vbits = band_bits(vm_b);
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 const int p0 = vshift + (8 * kq + e) * B;
@@ -856,42 +937,64 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
                     tsel[e] = 0x000C000Cu | (bsel << 8) | ((4u + bsel) << 24);
                     tk[e] = (uint32_t)tb & 7u;
                 }
-                const int sbp = 8 * (p0 + P.band_byte_off[vm_b] + 2) + vbits * (16 * vm_k + jc);
+                const int sbp = 8 * (p0 + band_byte_off(vm_b) + 2) + vbits * (16 * vm_k + jc);
                 sa[e] = rec_lds + ((uint32_t)(sbp >> 5) << 2);
                 ssh[e] = (uint32_t)sbp & 31u;
+                if (GEO::ct) {
+                    if (e < 4) {
+                        // one register per address pair: the unrolled groups' reads add constants
+                        __asm__ volatile("" : "+v"(ta[e]), "+v"(sa[e]));
+                    } else {
+                        // position e - 4's fields lie 4 records (B dwords) earlier at the same bits
+                        ta[e] = ta[e - 4] + 4u * GEO::B;
+                        sa[e] = sa[e - 4] + 4u * GEO::B;
+                    }
+                }
             }
             const uint32_t sh10 = 10u - (uint32_t)vbits;
             const uint32_t smask = (((1u << vbits) - 1u) << sh10) * 0x00010001u;
             const uint32_t sbase = ((15u + (uint32_t)vbits) << 10) * 0x00010001u;
             const _Float16 ssub = (_Float16)(float)((1 << vbits) + (1 << (vbits - 1)) - 1);
             const bool col_on = jc < 2 * G;
-            const _Float16 *bsrow = psq + ((vm_b * G + (jc >> 1)) * 2 + (jc & 1)) * CH;
+            // columns past the heads read a live column's weights (finite values whose sums
+            // are never written out), so every lane loads without a branch
+            const int jr = col_on ? jc : jc & 1;
+            const _Float16 *btrow = pwq + jr * CH;
+            const _Float16 *bsrow = psq + ((vm_b * G + (jr >> 1)) * 2 + (jr & 1)) * CH;
             const int ng = (n_t + 31) >> 5;
             const uint32_t gstep = 32u * (uint32_t)B;  // bytes per group: the addresses advance in place
-            for (int g = 0; g < ng; g++) {
+            // group g's fields sit goff bytes past group 0's
+            auto group = [&](int g, uint32_t goff) {
                 const int pq = 32 * g + 8 * kq;
-                half8_t bt = {}, bsk = {};
-                if (col_on) {
-                    bt = *reinterpret_cast<const half8_t *>(pwq + jc * CH + pq);
-                    if (vm_s) bsk = *reinterpret_cast<const half8_t *>(bsrow + pq);
-                }
+                const half8_t bt = *reinterpret_cast<const half8_t *>(btrow + pq);
                 if (vm_s) {
-                    const half8_t a = vm_codes(sa, ssh, 0, sh10, smask, sbase, ssub);
+                    const half8_t bsk = *reinterpret_cast<const half8_t *>(bsrow + pq);
+                    const half8_t a = vm_codes(sa, ssh, goff, sh10, smask, sbase, ssub);
                     vsk = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bsk, vsk, 0, 0, 0);
                 }
                 // window i + 1's dwords are read while window i converts
                 uint32_t dw[2][8];
-                vm_level_dwords(ta, 0, dw[0]);
+                vm_level_dwords(ta, goff, dw[0]);
 #pragma unroll
                 for (int i = 0; i < VM_TB; i++) {
-                    if (i + 1 < VM_TB) vm_level_dwords(ta, 16 * (i + 1), dw[(i + 1) & 1]);
+                    if (i + 1 < VM_TB) vm_level_dwords(ta, goff + 16u * (i + 1), dw[(i + 1) & 1]);
                     const half8_t a = vm_levels(dw[i & 1], tsel, tk);
                     vacc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bt, vacc[i], 0, 0, 0);
                 }
+            };
+            if constexpr (GEO::ct) {
+                // every group's offsets are constants: the LDS reads carry them
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    ta[e] += gstep;
-                    sa[e] += gstep;
+                for (int g = 0; g < CH / 32; g++)
+                    if (g < ng) group(g, (uint32_t)(g * 32 * GEO::B));
+            } else {
+                for (int g = 0; g < ng; g++) {
+                    group(g, 0u);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        ta[e] += gstep;
+                        sa[e] += gstep;
+                    }
                 }
             }
             const float inv_f = 1.0f / f;  // exact: f is a power of two
@@ -907,7 +1010,7 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
             for (int h = 0; h < G; h++) pw[h * CH + tid] = sc[h * CH + tid] * vstep;
             for (int b = 0; b < nb; b++) {
                 const float scale =
-                    live ? sp_scale_from_bits(lds_u32_at(rec, rb + P.band_byte_off[b]) & 0xffffu) : 0.0f;
+                    live ? sp_scale_from_bits(lds_u32_at(rec, rb + band_byte_off(b)) & 0xffffu) : 0.0f;
                 for (int h = 0; h < G; h++) psb[(b * G + h) * CH + tid] = sc[h * CH + tid] * scale;
             }
         }
@@ -969,10 +1072,10 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
                 const float *wrow;
                 if (j < ns) {
                     int b = 0;
-                    while (b + 1 < nb && j >= P.band_off[b + 1]) b++;
-                    bits = P.band_bits[b];
-                    const int bo = (j - P.band_off[b]) * bits;
-                    byte0 = P.band_byte_off[b] + 2 + (bo >> 3);
+                    while (b + 1 < nb && j >= band_off(b + 1)) b++;
+                    bits = band_bits(b);
+                    const int bo = (j - band_off(b)) * bits;
+                    byte0 = band_byte_off(b) + 2 + (bo >> 3);
                     bit0 = bo & 7;
                     offv = (float)((1 << (bits - 1)) - 1);
                     wrow = psb + b * G * CH;
@@ -1023,7 +1126,7 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
         for (int ii = 0; ii < 4; ii++) {
             const float v = add_xor1(vsk[ii]);
             const int c = 16 * vm_k + 4 * kq + ii;
-            if (vm_s && col && c < P.band_sz[vm_b]) dst[P.band_off[vm_b] + c] = v;
+            if (vm_s && col && c < band_sz(vm_b)) dst[band_off(vm_b) + c] = v;
         }
         return;
     }
@@ -1198,34 +1301,50 @@ bool vm_ok(const SpPlan &P, const SpHierAttnArgs &A) {
     return !(e && e[0] == '0');
 }
 
-// The split kernel's instance for this call's level width and output mode.
+// Whether the call's record geometry is Geo330's (the compile-time instances then run).
+// SP_HIP_HIER_ATTN_CT=0 (read at each call) keeps the runtime-geometry instances.
+bool geo330(const SpPlan &P, const SpHierAttnArgs &A) {
+    using Gc = Geo330;
+    if (A.rbits != 2 || A.n_skel != Gc::ns || A.n_target != Gc::nt || A.B != Gc::B || P.n_bands != Gc::nb ||
+        P.total_bytes != Gc::skB)
+        return false;
+    for (int b = 0; b < Gc::nb; b++)
+        if (P.band_bits[b] != Gc::bits || P.band_sz[b] != Gc::sz || P.band_off[b] != b * Gc::sz ||
+            P.band_byte_off[b] != b * Gc::band_bytes)
+            return false;
+    const char *e = getenv("SP_HIP_HIER_ATTN_CT");
+    return !(e && e[0] == '0');
+}
+
+// The split kernel's instance for this call's level width, output mode and geometry.
 template <bool OUT>
 void launch_split(const SpPlan &P, const SpHierAttnArgs &A, const SpSeqTab &T, const float *prep, float *part,
-                  int n_runs, int rb, int G, bool vm, size_t lds_split, hipStream_t s) {
+                  int n_runs, int rb, int G, bool vm, bool ct, size_t lds_split, hipStream_t s) {
     const dim3 grid(A.n_kvh, n_runs, T.n_seq);
-    if (rb == 2 && G <= 2) {
-        if (OUT && vm)
-            hipLaunchKernelGGL((k_hier_attn_split<2, 2, OUT, OUT>), grid, dim3(NT), lds_split, s, P, A, T, prep, part,
-                               n_runs);
-        else
-            hipLaunchKernelGGL((k_hier_attn_split<2, 2, OUT, false>), grid, dim3(NT), lds_split, s, P, A, T, prep, part,
-                               n_runs);
-    } else if (rb == 2 && G <= 4 && OUT && vm) {
-        hipLaunchKernelGGL((k_hier_attn_split<2, 4, OUT, OUT>), grid, dim3(NT), lds_split, s, P, A, T, prep, part,
-                           n_runs);
+#define SP_SPLIT(RB_, GM_, VM_, GEO_)                                                                              \
+    hipLaunchKernelGGL((k_hier_attn_split<RB_, GM_, OUT, VM_, GEO_>), grid, dim3(NT), lds_split, s, P, A, T, prep, \
+                       part, n_runs)
+    // ct (the compile-time geometry) comes with the matrix-core V sums at up to 4 query
+    // heads per KV head, so a call's scores-only and full instances share their score code
+    if (ct && G <= 2) {
+        SP_SPLIT(2, 2, OUT, Geo330);
+    } else if (ct && G <= 4) {
+        SP_SPLIT(2, 4, OUT, Geo330);
+    } else if (rb == 2 && G <= 2) {
+        if (OUT && vm) SP_SPLIT(2, 2, OUT, GeoRt);
+        else SP_SPLIT(2, 2, false, GeoRt);
+    } else if (OUT && rb == 2 && G <= 4 && vm) {
+        if constexpr (OUT) SP_SPLIT(2, 4, true, GeoRt);
     } else if (rb == 2) {
-        hipLaunchKernelGGL((k_hier_attn_split<2, MAX_G, OUT, false>), grid, dim3(NT), lds_split, s, P, A, T, prep, part,
-                           n_runs);
+        SP_SPLIT(2, MAX_G, false, GeoRt);
     } else if (rb == 4) {
-        hipLaunchKernelGGL((k_hier_attn_split<4, MAX_G, OUT, false>), grid, dim3(NT), lds_split, s, P, A, T, prep, part,
-                           n_runs);
+        SP_SPLIT(4, MAX_G, false, GeoRt);
     } else if (rb == 8) {
-        hipLaunchKernelGGL((k_hier_attn_split<8, MAX_G, OUT, false>), grid, dim3(NT), lds_split, s, P, A, T, prep, part,
-                           n_runs);
+        SP_SPLIT(8, MAX_G, false, GeoRt);
     } else {
-        hipLaunchKernelGGL((k_hier_attn_split<0, MAX_G, OUT, false>), grid, dim3(NT), lds_split, s, P, A, T, prep, part,
-                           n_runs);
+        SP_SPLIT(0, MAX_G, false, GeoRt);
     }
+#undef SP_SPLIT
 }
 
 }  // namespace
@@ -1272,8 +1391,9 @@ hipError_t sp_launch_hier_attn(const SpPlan &P, const SpHierAttnArgs &A, const S
     float *part = ws + (size_t)T.n_seq * A.n_q * A.ps;
     hipLaunchKernelGGL(k_hier_attn_prep, dim3(T.n_seq * A.n_q), dim3(NT), lds_prep, s, P, A, prep);
     const bool vm = rb == 2 && vm_ok(P, A);
-    if (A.out) launch_split<true>(P, A, T, prep, part, n_runs, rb, G, vm, lds_split, s);
-    else launch_split<false>(P, A, T, prep, part, n_runs, rb, G, vm, lds_split, s);
+    const bool ct = vm && G <= 4 && geo330(P, A);
+    if (A.out) launch_split<true>(P, A, T, prep, part, n_runs, rb, G, vm, ct, lds_split, s);
+    else launch_split<false>(P, A, T, prep, part, n_runs, rb, G, vm, ct, lds_split, s);
     if (A.out)
         hipLaunchKernelGGL(k_hier_attn_merge, dim3(T.n_seq * A.n_q), dim3(NT), lds_merge, s, P, A, part, n_runs);
     return hipGetLastError();

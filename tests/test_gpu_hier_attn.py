@@ -73,20 +73,27 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("path", ["default", "lane", "window"])
+@pytest.mark.parametrize("path", ["default", "runtime", "lane", "window"])
 @pytest.mark.parametrize("hd,rbits,skel_bits,H,n_q,n_kv,runs", CASES)
 def test_hier_attention_matches_oracle(hd, rbits, skel_bits, H, n_q, n_kv, runs, path, monkeypatch):
     """The default launch runs the 256-position chunk kernel (2-bit levels at up to 4
     query heads per KV head: the V coefficient sums on the matrix cores), and past its
     LDS limit (more than 4 query heads per KV head at pad 330) the one-position-per-lane
-    split kernel of the configs[4] geometry (hd 256, skeleton 5/5, 2-bit targets); path
-    "lane" selects the lane kernel wherever it fits (SP_HIP_HIER_ATTN_LANE=1), path
-    "window" keeps the chunk kernel's V sums on the VALU (SP_HIP_HIER_ATTN_VM=0)."""
+    split kernel of the configs[4] geometry (hd 256, skeleton 5/5, 2-bit targets). At
+    that geometry the chunk kernel runs its compile-time-geometry instance; path
+    "runtime" keeps the instance that reads the geometry from the call
+    (SP_HIP_HIER_ATTN_CT=0), path "lane" selects the lane kernel wherever it fits
+    (SP_HIP_HIER_ATTN_LANE=1), path "window" keeps the chunk kernel's V sums on the VALU
+    (SP_HIP_HIER_ATTN_VM=0)."""
     lane_geo = hd == 256 and rbits == 2 and list(skel_bits) == [5, 5]
     if path == "lane":
         if not lane_geo:
             pytest.skip("the lane kernel serves the configs[4] geometry only")
         monkeypatch.setenv("SP_HIP_HIER_ATTN_LANE", "1")
+    if path == "runtime":
+        if not lane_geo or n_q // H > 4:
+            pytest.skip("the compile-time instances serve the configs[4] geometry at up to 4 query heads per KV head")
+        monkeypatch.setenv("SP_HIP_HIER_ATTN_CT", "0")
     if path == "window":
         if rbits != 2 or n_q // H > 4:
             pytest.skip("the matrix-core V sums serve 2-bit levels at up to 4 query heads per KV head")
