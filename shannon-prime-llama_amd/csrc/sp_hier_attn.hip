@@ -205,17 +205,23 @@ __device__ __forceinline__ void vil_stage(const float *src, float *dst, int n, i
     }
 }
 
+// The plan's cas tables, one entry per thread, loaded at kernel entry (so the load
+// overlaps the kernel's other first loads) and stored to LDS before the transform.
+static_assert(SP_CAS_TOTAL <= NT, "one cas entry per thread");
+__device__ __forceinline__ float cas_entry(const SpPlan &P, int tid) { return tid < SP_CAS_TOTAL ? P.cas[tid] : 0.0f; }
+
 // Transform of c[0, n) in LDS by the whole block (tmp: n more floats of LDS): the
-// stages of sp_transform_lds (same arithmetic), ping-ponging between c and tmp,
-// with the cas tables copied to LDS (cas_s, SP_CAS_TOTAL floats) first. The
-// result ends in c. Ends with a barrier.
-__device__ __forceinline__ void transform_block(float *c, float *tmp, int n, const SpPlan &P, float *cas_s, int tid) {
+// stages of sp_transform_lds (same arithmetic), ping-ponging between c and tmp, with
+// this thread's cas entry (cas_entry) stored to LDS (cas_s, SP_CAS_TOTAL floats)
+// first. The result ends in c. Ends with a barrier.
+__device__ __forceinline__ void transform_block(float *c, float *tmp, int n, const SpPlan &P, float *cas_s, float cas_v,
+                                                int tid) {
     if ((n & (n - 1)) == 0 || P.skip_transform) {
         sp_transform_lds(c, n, P, tid < SP_WAVE ? tid : n);
         __syncthreads();
         return;
     }
-    for (int i = tid; i < SP_CAS_TOTAL; i += NT) cas_s[i] = P.cas[i];
+    if (tid < SP_CAS_TOTAL) cas_s[tid] = cas_v;
     __syncthreads();
     float *src = c, *dst = tmp;
     int stride = 1;
@@ -395,6 +401,7 @@ k_hier_attn_prep(const SpPlan P, const SpHierAttnArgs A, float *__restrict__ pre
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)Wk, (short)0, nwd * 4, 0x00020000);
     float qv[PU];
     int ti[PU];
+    const float cas_v = cas_entry(P, tid);
 #pragma unroll
     for (int u = 0; u < PU; u++) {
         qv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rq, 4 * (tid + u * NT), 0, 0));
@@ -411,7 +418,7 @@ k_hier_attn_prep(const SpPlan P, const SpHierAttnArgs A, float *__restrict__ pre
     for (int u = 0; u < PU; u++)
         if (tid + u * NT < A.pad) c[tid + u * NT] = qv[u];  // zero past hd (out of range)
     __syncthreads();
-    transform_block(c, tsm, A.pad, P, cas_s, tid);
+    transform_block(c, tsm, A.pad, P, cas_s, cas_v, tid);
     if (w_reg) {
         uint32_t *Ws32 = reinterpret_cast<uint32_t *>(Ws);
 #pragma unroll
@@ -1199,6 +1206,24 @@ k_hier_attn_merge(const SpPlan P, const SpHierAttnArgs A, const float *__restric
     // so every load of a pass is in flight before the first wait
     const __amdgpu_buffer_rsrc_t rp =
         __builtin_amdgcn_make_buffer_rsrc((void *)ph, (short)0, n_runs * pp * 4, 0x00020000);
+    // coefficients j0 = tid and j1 = tid + NT together, MP runs of each per load pass;
+    // the first pass goes out at entry with the m, l loads, the coefficient indices and
+    // the cas entry, so the block waits on memory once before its arithmetic
+    constexpr int MP = 96;
+    const int ncoef = ns + nt;
+    float v0[MP], v1[MP];
+    auto load_pass = [&](int j0, int r0) {
+#pragma unroll
+        for (int k = 0; k < MP; k++) {
+            v0[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, (4 + j0) * 4, (r0 + k) * pp * 4, 0));
+            v1[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, (4 + j0 + NT) * 4, (r0 + k) * pp * 4, 0));
+        }
+    };
+    auto coef_idx = [&](int j) { return j < ns ? A.skel_idx[j] : A.tgt_idx[j - ns]; };
+    load_pass(tid, 0);
+    const int ci0 = tid < ncoef ? coef_idx(tid) : 0, ci1 = tid + NT < ncoef ? coef_idx(tid + NT) : 0;
+    const int ti0 = tid < nt ? A.tgt_idx[tid] : 0, ti1 = tid + NT < nt ? A.tgt_idx[tid + NT] : 0;
+    const float cas_v = cas_entry(P, tid);
     float mr[MERGE_RUNS_PER_THREAD], lr[MERGE_RUNS_PER_THREAD];
 #pragma unroll
     for (int u = 0; u < MERGE_RUNS_PER_THREAD; u++) {
@@ -1224,23 +1249,16 @@ k_hier_attn_merge(const SpPlan P, const SpHierAttnArgs A, const float *__restric
     }
     l = wave_sum(l);
     if (lane == 0) red[NT / SP_WAVE + wv] = l;
-    __syncthreads();
-    const float inv_l = sp_div(1.0f, (red[4] + red[5]) + (red[6] + red[7]));
     for (int k = tid; k < A.pad; k += NT) c[k] = 0.0f;
     __syncthreads();
-    // coefficients j0 = tid and j1 = tid + NT together, 48 runs of each in flight
-    for (int j0 = tid; j0 < ns + nt; j0 += 2 * NT) {
+    const float inv_l = sp_div(1.0f, (red[4] + red[5]) + (red[6] + red[7]));
+    for (int j0 = tid; j0 < ncoef; j0 += 2 * NT) {
         const int j1 = j0 + NT;
         float s0 = 0.0f, s1 = 0.0f;
-        for (int r0 = 0; r0 < n_runs; r0 += 48) {
-            float v0[48], v1[48];
+        for (int r0 = 0; r0 < n_runs; r0 += MP) {
+            if (j0 != tid || r0 != 0) load_pass(j0, r0);
 #pragma unroll
-            for (int k = 0; k < 48; k++) {
-                v0[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, (4 + j0) * 4, (r0 + k) * pp * 4, 0));
-                v1[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, (4 + j1) * 4, (r0 + k) * pp * 4, 0));
-            }
-#pragma unroll
-            for (int k = 0; k < 48; k++) {
+            for (int k = 0; k < MP; k++) {
                 const float w = r0 + k < n_runs ? e[r0 + k] : 0.0f;
                 s0 = fmaf(v0[k], w, s0);
                 s1 = fmaf(v1[k], w, s1);  // (j1 past the coefficients: discarded below)
@@ -1249,14 +1267,11 @@ k_hier_attn_merge(const SpPlan P, const SpHierAttnArgs A, const float *__restric
 #pragma unroll
         for (int q = 0; q < 2; q++) {
             const int j = q == 0 ? j0 : j1;
-            if (j >= ns + nt) continue;
+            if (j >= ncoef) continue;
             const float sj = (q == 0 ? s0 : s1) * inv_l;
-            if (j < ns) {
-                cs[j] = sj;
-                c[A.skel_idx[j]] = sj;
-            } else {
-                c[A.tgt_idx[j - ns]] = sj;  // the dev part; W c_skel is added below
-            }
+            const int ci = j0 == tid ? (q == 0 ? ci0 : ci1) : coef_idx(j);
+            if (j < ns) cs[j] = sj;
+            c[ci] = sj;  // targets: the dev part; W c_skel is added below
         }
     }
     if (w_reg) wst.store(Ws, nt * ns, tid);
@@ -1265,10 +1280,10 @@ k_hier_attn_merge(const SpPlan P, const SpHierAttnArgs A, const float *__restric
         float pred = 0.0f;
 #pragma unroll 4
         for (int s = 0; s < ns; s++) pred = fmaf(sp_f16_bits_to_f32(Ws[t * ns + s]), cs[s], pred);
-        c[A.tgt_idx[t]] += pred;
+        c[t == tid ? ti0 : t == tid + NT ? ti1 : A.tgt_idx[t]] += pred;
     }
     __syncthreads();
-    transform_block(c, tsm, A.pad, P, cas_s, tid);
+    transform_block(c, tsm, A.pad, P, cas_s, cas_v, tid);
     for (int k = tid; k < A.hd; k += NT) A.out[(long long)h * A.hd + k] = c[k];
 }
 
