@@ -231,6 +231,42 @@ k_attn_combine(const SpPlan VP, const float *__restrict__ ws, int n_splits, int 
         for (int k = tid; k < hd; k += SP_WAVE) out[(long long)h * hd + k] = c[k];
 }
 
+// The same merge for rows of at most 64 splits by one wave per row: split `lane`'s m and
+// l, a wave-wide max and sum (lane shuffles), the row's elements by lane (i = lane,
+// lane + 64, ...), each summed over the splits in order, then the inverse transform.
+// A batch of short sequences has a few splits per row, so the 1024-thread block of
+// k_attn_combine would be mostly idle and its block reductions the cost.
+__global__ void __launch_bounds__(64)
+k_attn_combine_wave(const SpPlan VP, const float *__restrict__ ws, int n_splits, int hd, float *__restrict__ out) {
+    __shared__ float e_s[SP_WAVE];
+    __shared__ float c[ATT_MAX_HD];
+    const int h = blockIdx.x, lane = threadIdx.x;
+    const long long row = hd + 2;
+    const float *base = ws + (long long)h * n_splits * row;
+    const bool live = lane < n_splits;
+    const float m = live ? base[lane * row] : -INFINITY;
+    const float lv = live ? base[lane * row + 1] : 0.0f;
+    float M = m;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, SP_WAVE));
+    const float e = live ? __expf(m - M) : 0.0f;
+    float L = lv * e;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) L += __shfl_xor(L, o, SP_WAVE);
+    e_s[lane] = e;
+    __syncthreads();
+    const float invL = 1.0f / L;
+    for (int i = lane; i < hd; i += SP_WAVE) {
+        float acc = 0.0f;
+#pragma unroll 8
+        for (int sp = 0; sp < n_splits; sp++) acc = fmaf(base[sp * row + 2 + i], e_s[sp], acc);
+        c[i] = acc * invL;
+    }
+    __syncthreads();
+    sp_transform_lds(c, hd, VP, lane);
+    for (int k = lane; k < hd; k += SP_WAVE) out[(long long)h * hd + k] = c[k];
+}
+
 hipError_t sp_launch_attn_lane_seqs(const SpPlan &KP, const SpPlan &VP, const int *order, const SpAttnArgs &A,
                                     const SpSeqTab &T, float *ws, size_t ws_floats, int n_runs, hipStream_t s) {
     const size_t n_rows = (size_t)T.n_seq * A.n_q;
@@ -242,7 +278,10 @@ hipError_t sp_launch_attn_lane_seqs(const SpPlan &KP, const SpPlan &VP, const in
     hipLaunchKernelGGL(k_attn_prep, dim3((unsigned)n_rows), dim3(64), 0, s, KP, order, A.q, A.hd, A.kq_scale, qt);
     const hipError_t le = sp_launch_attn_lane_split(KP, VP, A, T, qt, part, n_runs, s);
     if (le != hipSuccess) return le;
-    if (A.out)
+    if (A.out && n_runs <= SP_WAVE)
+        hipLaunchKernelGGL(k_attn_combine_wave, dim3((unsigned)n_rows), dim3(SP_WAVE), 0, s, VP, part, n_runs, A.hd,
+                           A.out);
+    else if (A.out)
         hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)n_rows), dim3(COMB_THREADS), 0, s, VP, part, n_runs, A.hd,
                            A.out);
     return hipGetLastError();
