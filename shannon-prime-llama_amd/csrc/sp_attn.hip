@@ -32,10 +32,22 @@ k_attn_prep(const SpPlan KP, const int *__restrict__ order, const float *__restr
             float kq_scale, float *__restrict__ qt) {
     __shared__ float c[ATT_MAX_HD];
     const int h = blockIdx.x, lane = threadIdx.x;
+    // the order entries load with the query row, not after the transform
+    constexpr int EPL = ATT_MAX_HD / SP_WAVE;
+    int src[EPL];
+#pragma unroll
+    for (int u = 0; u < EPL; u++) {
+        const int k = lane + u * SP_WAVE;
+        src[u] = (order && k < hd) ? order[k] : k;
+    }
     for (int k = lane; k < hd; k += SP_WAVE) c[k] = q[(long long)h * hd + k];
     __syncthreads();
     sp_transform_lds(c, hd, KP, lane);
-    for (int k = lane; k < hd; k += SP_WAVE) qt[(long long)h * hd + k] = kq_scale * (order ? c[order[k]] : c[k]);
+#pragma unroll
+    for (int u = 0; u < EPL; u++) {
+        const int k = lane + u * SP_WAVE;
+        if (k < hd) qt[(long long)h * hd + k] = kq_scale * c[src[u]];
+    }
 }
 
 __device__ __forceinline__ void att_tile_load(unsigned char *lds, const unsigned char *g, int nbytes,
