@@ -192,12 +192,20 @@ struct LdsBits {
 // element per thread: dst[e] = isp * sum_jj C[k][jj] src[base + jj*stride] for
 // e = base + k*stride (the same sums, in the same order, as a whole group per
 // thread, with p times the parallelism), the p x p cas matrix C read from LDS.
+// floor(a / d) for 0 <= a < 2^20 and 1 <= d < 2^10 from the float reciprocal of d:
+// (a + 0.5) / d lies at least 1/(2d) from an integer, far beyond the rounding of the
+// reciprocal and the product, so the truncation is exact (an integer division by a
+// runtime divisor costs ~30 VALU instructions).
+__device__ __forceinline__ int div_small(int a, float inv_d) { return (int)(((float)a + 0.5f) * inv_d); }
+
 template <int p>
 __device__ __forceinline__ void vil_stage(const float *src, float *dst, int n, int stride, const float *C, float isp,
                                           int tid) {
     const int block = stride * p;
+    const float inv_block = 1.0f / (float)block, inv_stride = 1.0f / (float)stride;
     for (int e = tid; e < n; e += NT) {
-        const int b0 = (e / block) * block, r = e - b0, k = r / stride, base = b0 + (r - k * stride);
+        const int b0 = div_small(e, inv_block) * block, r = e - b0, k = div_small(r, inv_stride);
+        const int base = b0 + (r - k * stride);
         float sum = 0.0f;
 #pragma unroll
         for (int jj = 0; jj < p; jj++) sum += C[k * p + jj] * src[base + jj * stride];
@@ -1212,11 +1220,15 @@ k_hier_attn_merge(const SpPlan P, const SpHierAttnArgs A, const float *__restric
     constexpr int MP = 96;
     const int ncoef = ns + nt;
     float v0[MP], v1[MP];
+    // a coefficient past the last reads at an offset past the buffer (0, with no traffic);
+    // a run past the last reads the last run's row again (finite, and its weight is 0)
     auto load_pass = [&](int j0, int r0) {
+        const int o0 = j0 < ncoef ? (4 + j0) * 4 : 0x40000000, o1 = j0 + NT < ncoef ? (4 + j0 + NT) * 4 : 0x40000000;
 #pragma unroll
         for (int k = 0; k < MP; k++) {
-            v0[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, (4 + j0) * 4, (r0 + k) * pp * 4, 0));
-            v1[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, (4 + j0 + NT) * 4, (r0 + k) * pp * 4, 0));
+            const int rr = min(r0 + k, n_runs - 1);
+            v0[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, o0, rr * pp * 4, 0));
+            v1[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, o1, rr * pp * 4, 0));
         }
     };
     auto coef_idx = [&](int j) { return j < ns ? A.skel_idx[j] : A.tgt_idx[j - ns]; };
