@@ -188,16 +188,16 @@ struct LdsBits {
     }
 };
 
-// One Vilenkin stage of radix p from src to dst (stride `stride`), one output
-// element per thread: dst[e] = isp * sum_jj C[k][jj] src[base + jj*stride] for
-// e = base + k*stride (the same sums, in the same order, as a whole group per
-// thread, with p times the parallelism), the p x p cas matrix C read from LDS.
 // floor(a / d) for 0 <= a < 2^20 and 1 <= d < 2^10 from the float reciprocal of d:
 // (a + 0.5) / d lies at least 1/(2d) from an integer, far beyond the rounding of the
 // reciprocal and the product, so the truncation is exact (an integer division by a
 // runtime divisor costs ~30 VALU instructions).
 __device__ __forceinline__ int div_small(int a, float inv_d) { return (int)(((float)a + 0.5f) * inv_d); }
 
+// One Vilenkin stage of radix p from src to dst (stride `stride`), one output
+// element per thread: dst[e] = isp * sum_jj C[k][jj] src[base + jj*stride] for
+// e = base + k*stride (the same sums, in the same order, as a whole group per
+// thread, with p times the parallelism), the p x p cas matrix C read from LDS.
 template <int p>
 __device__ __forceinline__ void vil_stage(const float *src, float *dst, int n, int stride, const float *C, float isp,
                                           int tid) {

@@ -26,3 +26,23 @@ def test_quantizer_arithmetic_is_exact(tmp_path):
     assert lines[-1] == "OK"
     assert sum("div_by_level" in ln for ln in lines) == 7  # m = 1, 3, ..., 127
     assert all(" 0 mismatches" in ln for ln in lines[:-1])
+
+
+def test_float_reciprocal_division_is_exact():
+    """The block transforms of the fused attention's prep and merge kernels
+    (shannon-prime-llama_amd/csrc/sp_hier_attn.hip: div_small) take floor(a / d) as
+    trunc((a + 0.5) * fl(1 / d)) in fp32. Checked against integer division for every
+    a < 4096 and d < 1024 (the transforms use a, d <= 330), and at the stated limits
+    a < 2^20 for a spread of divisors."""
+    import numpy as np
+
+    a = np.arange(4096, dtype=np.int64)
+    for d in range(1, 1024):
+        inv = np.float32(1.0) / np.float32(d)
+        got = ((a.astype(np.float32) + np.float32(0.5)) * inv).astype(np.int64)
+        assert np.array_equal(got, a // d), d
+    big = np.arange(0, 1 << 20, 7, dtype=np.int64)
+    for d in (1, 2, 3, 5, 7, 11, 330, 1000, 1021, 1023):
+        inv = np.float32(1.0) / np.float32(d)
+        got = ((big.astype(np.float32) + np.float32(0.5)) * inv).astype(np.int64)
+        assert np.array_equal(got, big // d), d
