@@ -21,16 +21,9 @@ namespace {
 
 constexpr int EP = 65;  // LDS row pitch (floats) of the transposed coefficient chunk
 
-__device__ __forceinline__ float wmax(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-    return v;
-}
-__device__ __forceinline__ float wadd(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-    return v;
-}
+// wave reductions on DPP and the row swaps (every lane active at each call)
+__device__ __forceinline__ float wmax(float v) { return sp_wave_max_dpp(v); }
+__device__ __forceinline__ float wadd(float v) { return sp_wave_sum_dpp(v); }
 
 // A record's codes centred, in record order, without their band scales: x = code -
 // (2^(bits-1) - 1), exact (the magic-number conversion of dequant_bands), and each

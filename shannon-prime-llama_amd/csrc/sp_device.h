@@ -124,6 +124,31 @@ __device__ __forceinline__ int sp_rint_sat(float x) {
 // Correctly rounded fp32 division (IEEE), independent of fast-math flags.
 __device__ __forceinline__ float sp_div(float a, float b) { return __fdiv_rn(a, b); }
 
+// Wave-wide all-reduce on the VALU (no LDS round trips): DPP quad permutes and row
+// mirrors inside each row of 16 lanes, then the gfx950 row swaps across rows.
+// permlane16/32_swap(v, v) return this lane's value and its partner's (lane ^ 16,
+// lane ^ 32) in an order that depends on the lane, so a commutative op of the two
+// gives every lane the same result. Call with the whole wave active.
+template <class Op>
+__device__ __forceinline__ float sp_wave_allreduce(float v, Op op) {
+    typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+    v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true)));   // quad [1,0,3,2]
+    v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true)));   // quad [2,3,0,1]
+    v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true)));  // row_half_mirror
+    v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true)));  // row_mirror
+    u32x2_t t = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = op(__uint_as_float(t[0]), __uint_as_float(t[1]));
+    t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return op(__uint_as_float(t[0]), __uint_as_float(t[1]));
+}
+// sum and maximum (of non-NaN values) over the wave, every lane active
+__device__ __forceinline__ float sp_wave_sum_dpp(float v) {
+    return sp_wave_allreduce(v, [](float a, float b) { return a + b; });
+}
+__device__ __forceinline__ float sp_wave_max_dpp(float v) {
+    return sp_wave_allreduce(v, [](float a, float b) { return fmaxf(a, b); });
+}
+
 // Wave-wide max of non-NaN values.
 __device__ __forceinline__ float sp_wave_max(float v) {
 #pragma unroll

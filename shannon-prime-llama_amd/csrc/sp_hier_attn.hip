@@ -353,31 +353,9 @@ __device__ __forceinline__ half8_t vm_codes(const uint32_t (&ad)[8], const uint3
     return __builtin_bit_cast(half8_t, v) - sub;
 }
 
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-
-// Wave-wide all-reduce on the VALU (no LDS round trips): DPP quad permutes and row
-// mirrors inside each row of 16 lanes, then the gfx950 row swaps across rows.
-// permlane16/32_swap(v, v) return this lane's value and its partner's (lane ^ 16,
-// lane ^ 32) in an order that depends on the lane, so a commutative op of the two
-// gives every lane the same result. Call with the whole wave active.
-template <class Op>
-__device__ __forceinline__ float wave_reduce(float v, Op op) {
-    v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true)));   // quad [1,0,3,2]
-    v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true)));   // quad [2,3,0,1]
-    v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true)));  // row_half_mirror
-    v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true)));  // row_mirror
-    u32x2 t = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = op(__uint_as_float(t[0]), __uint_as_float(t[1]));
-    t = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return op(__uint_as_float(t[0]), __uint_as_float(t[1]));
-}
-__device__ __forceinline__ float wave_sum(float v) {
-    return wave_reduce(v, [](float a, float b) { return a + b; });
-}
-// maximum of non-NaN values
-__device__ __forceinline__ float wave_max(float v) {
-    return wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
-}
+// wave reductions on DPP and the row swaps (every lane active at each call)
+__device__ __forceinline__ float wave_sum(float v) { return sp_wave_sum_dpp(v); }
+__device__ __forceinline__ float wave_max(float v) { return sp_wave_max_dpp(v); }
 
 // ---------------------------------------------------------------------------
 // Query preparation. Dynamic LDS: c[pad], qt[r32(n_target)], part[8][r4(n_skel)]

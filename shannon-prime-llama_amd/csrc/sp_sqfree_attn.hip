@@ -53,16 +53,9 @@ __device__ __forceinline__ void sq_coefficients(const uint32_t (&rec)[DW], float
     }
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-    return v;
-}
-__device__ __forceinline__ float wave_add(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-    return v;
-}
+// wave reductions on DPP and the row swaps (every lane active at each call)
+__device__ __forceinline__ float wave_max(float v) { return sp_wave_max_dpp(v); }
+__device__ __forceinline__ float wave_add(float v) { return sp_wave_sum_dpp(v); }
 
 constexpr int EP = 65;  // LDS row pitch (floats) of the transposed coefficient chunk
 
