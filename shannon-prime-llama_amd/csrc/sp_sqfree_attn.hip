@@ -109,13 +109,13 @@ k_sqfree_attn_split(const unsigned char *__restrict__ kc0, const unsigned char *
     const int c2i = lane % C2, hh = lane / C2;
     const bool c2_on = hh < (GM > 1 ? 2 : 1);
 
-    // the K records run one tile ahead (the next tile's load goes out once this tile's
-    // records are out of the stage); a tile's V records load at the tile's start
-    RecTile<GK> Rk;
-    int c = run;
-    if (c < tpo) rec_tile_load<GK>(Rk, kc, k_slot, M, kvh * tpo + c, n_tiles, lane);
-    for (; c < tpo; c += n_runs) {
+    // a tile's K and V records load at the tile's start (holding the next tile's K records
+    // through a tile took the registers that keep the full instances from spilling at two
+    // waves per SIMD; the other wave hides the load)
+    for (int c = run; c < tpo; c += n_runs) {
         const int t = kvh * tpo + c;
+        RecTile<GK> Rk;
+        rec_tile_load<GK>(Rk, kc, k_slot, M, t, n_tiles, lane);
         RecTile<GV> Rv;
         if (OUT) rec_tile_load<GV>(Rv, vc, v_slot, M, t, n_tiles, lane);
         __syncthreads();  // the previous tile is done with the stage
@@ -123,7 +123,6 @@ k_sqfree_attn_split(const unsigned char *__restrict__ kc0, const unsigned char *
         __syncthreads();
         uint32_t rk[GK::dwords];
         rec_from_lds<GK>(rk, stage, lane);
-        if (c + n_runs < tpo) rec_tile_load<GK>(Rk, kc, k_slot, M, t + n_runs, n_tiles, lane);
         float e[PAD];
         sq_coefficients<SK, SLK>(rk, e);
         const int pos = c * 64 + lane;
