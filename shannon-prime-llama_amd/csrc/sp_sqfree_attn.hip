@@ -77,8 +77,13 @@ k_sqfree_attn_split(const unsigned char *__restrict__ kc0, const unsigned char *
     constexpr int C2 = PAD - 128;  // coefficients of the third 64-coefficient chunk
     constexpr int HG = (GM + 1) / 2;  // heads per lane in the third chunk (two lanes per coefficient)
     static_assert(C2 > 0 && 2 * C2 <= 64, "three chunks of at most 64 coefficients");
-    __shared__ __attribute__((aligned(16))) unsigned char stage[NCK * 1024 + 16];
-    __shared__ float E[64 * EP];
+    // the record stage and the transposed coefficient chunks share their memory: in
+    // this one-wave block the stage's last reads (the V records) come before the first
+    // chunk's writes, and the next tile's K records are staged after the last chunk's
+    // barrier; the smaller block fits 8 per CU (two waves per SIMD) instead of 6
+    __shared__ __attribute__((aligned(16))) float E[OUT ? 64 * EP : (NCK * 1024 + 16 + 3) / 4];
+    static_assert(NCK * 1024 + 16 <= 64 * EP * 4, "the record stage fits the chunk memory");
+    unsigned char *const stage = reinterpret_cast<unsigned char *>(E);
     __shared__ __attribute__((aligned(16))) float Pw[64 * GM];
     const int kvh = blockIdx.x, run = blockIdx.y, lane = threadIdx.x;
     // sequence blockIdx.z: its positions, prepared queries, score rows and partials
