@@ -179,7 +179,7 @@ def seq_table(starts, lens):
     return out[0], out[1]
 
 
-def bench_variants(torch, S, L, stream, reps=3):
+def bench_variants(torch, S, L, stream, reps=10):
     """Throughput of the other configs' codec paths at their per-GPU shapes (extra
     fields of the JSON line, not the headline): the configs[1] post-decode round
     trip over cache cells (one decode token, a 2048-cell prefill chunk; bytes count
