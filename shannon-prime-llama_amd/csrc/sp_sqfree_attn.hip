@@ -22,6 +22,8 @@
 // with the prepared queries, an online softmax across the run's tiles, and the
 // weighted coefficient sums through LDS (the wave's coefficients transposed so that
 // each lane sums one coefficient over the tile's 64 positions).
+#include <cstdlib>
+
 #include "sp_sqfree_lane.h"
 
 namespace {
@@ -69,7 +71,7 @@ constexpr int EP = 65;  // LDS row pitch (floats) of the transposed coefficient 
 template <int SK, class SLK, class SLV, int GM, bool OUT>
 __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2)))
 k_sqfree_attn_split(const unsigned char *__restrict__ kc0, const unsigned char *__restrict__ vc0, long long k_slot,
-                    long long v_slot, const SpSeqTab T, int G, const float *__restrict__ prep0, int ps, int qo,
+                    long long v_slot, const SpSeqTab T, int G, int hs, const float *__restrict__ prep0, int ps, int qo,
                     float *__restrict__ scores0, float *__restrict__ part0, int pp, int n_runs) {
     using GK = SqRec<PAD, SK, RBITS, true, SLK>;
     using GV = SqRec<PAD, SK, RBITS, true, SLV>;
@@ -85,7 +87,8 @@ k_sqfree_attn_split(const unsigned char *__restrict__ kc0, const unsigned char *
     static_assert(NCK * 1024 + 16 <= 64 * EP * 4, "the record stage fits the chunk memory");
     unsigned char *const stage = reinterpret_cast<unsigned char *>(E);
     __shared__ __attribute__((aligned(16))) float Pw[64 * GM];
-    const int kvh = blockIdx.x, run = blockIdx.y, lane = threadIdx.x;
+    // block x: head group x (query heads x G .. x G + G - 1) of KV head x / hs
+    const int hb = blockIdx.x, kvh = hb / hs, run = blockIdx.y, lane = threadIdx.x;
     // sequence blockIdx.z: its positions, prepared queries, score rows and partials
     const int seq = blockIdx.z, n_q = (int)gridDim.x * G, n_kv = T.len[seq];
     const unsigned char *__restrict__ kc = kc0 + (long long)T.start[seq] * GK::total;
@@ -94,9 +97,9 @@ k_sqfree_attn_split(const unsigned char *__restrict__ kc0, const unsigned char *
     float *__restrict__ scores = scores0 ? scores0 + T.soff[seq] : nullptr;
     const float *__restrict__ prep = prep0 + (long long)seq * n_q * ps;
     float *__restrict__ part = part0 + (long long)seq * n_q * n_runs * pp;
-    const int h0 = kvh * G;
+    const int h0 = hb * G;
     const int tpo = (n_kv + 63) / 64;
-    const int n_tiles = (int)gridDim.x * tpo;
+    const int n_tiles = ((int)gridDim.x / hs) * tpo;
     const TileMap M{tpo, n_kv};
     const float *__restrict__ pq = prep + (long long)h0 * ps;
 
@@ -257,28 +260,28 @@ using SkelL77 = Layout<77, 5, 4, 4, 4, 5>;
 using SkelL115 = Layout<115, 5, 4, 4, 4, 5>;
 using SkelL115V3 = Layout<115, 3>;
 
+// hs head groups per KV head (1 or 2): block x takes the query heads of group x.
 template <int SK, class SLK, class SLV, int GM>
-void launch_split(const SpSqAttnArgs &A, const SpSeqTab &T, const float *prep, float *part, int n_runs,
+void launch_split(const SpSqAttnArgs &A, const SpSeqTab &T, const float *prep, float *part, int n_runs, int hs,
                   hipStream_t s) {
-    const dim3 grid(A.n_kvh, n_runs, T.n_seq), block(64);
+    const dim3 grid(A.n_kvh * hs, n_runs, T.n_seq), block(64);
+    const int G = A.n_q / A.n_kvh / hs;
     if (A.out)
         hipLaunchKernelGGL((k_sqfree_attn_split<SK, SLK, SLV, GM, true>), grid, block, 0, s, A.kcache, A.vcache,
-                           A.k_slot_bytes, A.v_slot_bytes, T, A.n_q / A.n_kvh, prep, A.ps, A.qo, A.scores, part,
-                           A.pp, n_runs);
+                           A.k_slot_bytes, A.v_slot_bytes, T, G, hs, prep, A.ps, A.qo, A.scores, part, A.pp, n_runs);
     else
         hipLaunchKernelGGL((k_sqfree_attn_split<SK, SLK, SLV, GM, false>), grid, block, 0, s, A.kcache, A.vcache,
-                           A.k_slot_bytes, A.v_slot_bytes, T, A.n_q / A.n_kvh, prep, A.ps, A.qo, A.scores, part,
-                           A.pp, n_runs);
+                           A.k_slot_bytes, A.v_slot_bytes, T, G, hs, prep, A.ps, A.qo, A.scores, part, A.pp, n_runs);
 }
 
 template <int SK, class SLK, class SLV>
-void launch_split_g(const SpSqAttnArgs &A, const SpSeqTab &T, const float *prep, float *part, int n_runs,
+void launch_split_g(const SpSqAttnArgs &A, const SpSeqTab &T, const float *prep, float *part, int n_runs, int hs,
                     hipStream_t s) {
-    const int G = A.n_q / A.n_kvh;
-    if (G <= 1) launch_split<SK, SLK, SLV, 1>(A, T, prep, part, n_runs, s);
-    else if (G <= 2) launch_split<SK, SLK, SLV, 2>(A, T, prep, part, n_runs, s);
-    else if (G <= 4) launch_split<SK, SLK, SLV, 4>(A, T, prep, part, n_runs, s);
-    else launch_split<SK, SLK, SLV, 8>(A, T, prep, part, n_runs, s);
+    const int G = A.n_q / A.n_kvh / hs;
+    if (G <= 1) launch_split<SK, SLK, SLV, 1>(A, T, prep, part, n_runs, hs, s);
+    else if (G <= 2) launch_split<SK, SLK, SLV, 2>(A, T, prep, part, n_runs, hs, s);
+    else if (G <= 4) launch_split<SK, SLK, SLV, 4>(A, T, prep, part, n_runs, hs, s);
+    else launch_split<SK, SLK, SLV, 8>(A, T, prep, part, n_runs, hs, s);
 }
 
 template <class SL>
@@ -311,6 +314,15 @@ int resident_per_cu(bool out) {
             : hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_sqfree_attn_split<SK, SLK, SLV, GM, false>, 64, 0);
     return e == hipSuccess && nb > 0 ? nb : 4;
 }
+// compute units of the current device (256 when the runtime cannot say)
+int device_cus() {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+        n = 256;
+    return n;
+}
+
 template <int SK, class SLK, class SLV>
 int resident_per_cu_g(int G, bool out) {
     if (G <= 1) return resident_per_cu<SK, SLK, SLV, 1>(out);
@@ -349,9 +361,24 @@ hipError_t sp_launch_sqfree_attn(const SpPlan &KP, const SpPlan &VP, const SpSqG
     float *part = ws + (size_t)T.n_seq * A.n_q * A.ps;
     hipError_t e = sp_launch_hier_attn_prep(KP, HA, T.n_seq, prep, s);
     if (e != hipSuccess) return e;
-    if (kind == 1) launch_split_g<77, SkelL77, SkelL77>(A, T, prep, part, n_runs, s);
-    else if (kind == 2) launch_split_g<115, SkelL115, SkelL115>(A, T, prep, part, n_runs, s);
-    else launch_split_g<115, SkelL115, SkelL115V3>(A, T, prep, part, n_runs, s);
+    // Two head groups per KV head when twice the blocks still run in one resident round
+    // (a single sequence leaves half the wave slots empty otherwise): each tile's records
+    // are then decoded twice, for half the heads each.
+    int hs = 1;
+    const int gq = A.n_q / A.n_kvh;
+    if (gq % 2 == 0) {
+        const bool out = A.out != nullptr;
+        const int per_cu = kind == 1   ? resident_per_cu_g<77, SkelL77, SkelL77>(gq / 2, out)
+                           : kind == 2 ? resident_per_cu_g<115, SkelL115, SkelL115>(gq / 2, out)
+                                       : resident_per_cu_g<115, SkelL115, SkelL115V3>(gq / 2, out);
+        if (2LL * A.n_kvh * n_runs * T.n_seq <= (long long)per_cu * device_cus()) hs = 2;
+        // SP_HIP_SQFREE_ATTN_GROUPS=1 (read at each call) keeps one group (tests cover both)
+        const char *eg = getenv("SP_HIP_SQFREE_ATTN_GROUPS");
+        if (eg && eg[0] == '1') hs = 1;
+    }
+    if (kind == 1) launch_split_g<77, SkelL77, SkelL77>(A, T, prep, part, n_runs, hs, s);
+    else if (kind == 2) launch_split_g<115, SkelL115, SkelL115>(A, T, prep, part, n_runs, hs, s);
+    else launch_split_g<115, SkelL115, SkelL115V3>(A, T, prep, part, n_runs, hs, s);
     e = hipGetLastError();
     if (e != hipSuccess || !A.out) return e;
     return sp_launch_hier_attn_merge(KP, HA, T.n_seq, part, n_runs, s);

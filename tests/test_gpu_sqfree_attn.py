@@ -67,11 +67,17 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("groups", ["auto", "one"])
 @pytest.mark.parametrize("sk,v_bits,H,n_q,n_kv,runs", CASES)
-def test_sqfree_attention_matches_oracle(sk, v_bits, H, n_q, n_kv, runs, monkeypatch):
+def test_sqfree_attention_matches_oracle(sk, v_bits, H, n_q, n_kv, runs, groups, monkeypatch):
+    """groups "auto": the launcher splits each KV head's query heads over two blocks when
+    twice the blocks still fit one resident round (these sizes always do, at an even
+    GQA); "one" keeps one block per KV head and run (SP_HIP_SQFREE_ATTN_GROUPS=1)."""
     if runs:
         monkeypatch.setenv("SP_HIP_SQFREE_ATTN_RUNS", str(runs))
-    say(f"sqfree attn sk={sk} v_bits={v_bits} H={H} n_q={n_q} n_kv={n_kv} runs={runs}")
+    if groups == "one":
+        monkeypatch.setenv("SP_HIP_SQFREE_ATTN_GROUPS", "1")
+    say(f"sqfree attn sk={sk} v_bits={v_bits} H={H} n_q={n_q} n_kv={n_kv} runs={runs} groups={groups}")
     cc, km, kbc, vbc, kp, vp = _sqfree_cache(sk, v_bits, H, n_kv, seed=sk + n_kv)
     hd = 128
     q = W.cfg2_q(n_q=n_q, hd=hd, pos=n_kv, seed=n_kv + 3)
