@@ -61,16 +61,31 @@ typedef const __attribute__((address_space(4))) uint32_t *wptr_t;
 
 // pred = sum_s (float)W[t][s] * sk[s] from 0.0f, s ascending, separately
 // rounded products and adds (kernel_hier_predict, shannon_prime_hier.cu:74-92),
-// for targets t and t+1 (rows w0, w1 as fp16 pairs). after: a value the pair is
-// ordered behind (the +0.0f starts come from an asm that takes it as an operand).
-template <int NS>
-__device__ __forceinline__ void hier_predict2(wptr_t w0, wptr_t w1, const float (&sk)[NS], float after, float &r0,
-                                              float &r1) {
+// for targets t and t+1: w holds row t's NS/2 fp16 pairs, then row t+1's (in
+// scalar registers). after: a value the pair is ordered behind (the +0.0f
+// starts come from an asm that takes it as an operand).
+//
+// With MORE, the rows of the next pair are loaded into wn after the first
+// products: the wait for w (loaded one pair earlier) comes before those
+// products, and a scalar-load wait covers every scalar load in flight, so rows
+// loaded before it would be waited for there too. The scheduling barriers keep
+// the loads in that place; loaded where their own pair starts, each pair's rows
+// left the wave (one per SIMD) waiting ~600 times per tile.
+template <int NS, bool MORE>
+__device__ __forceinline__ void hier_predict2(const uint32_t (&w)[NS], uint32_t (&wn)[NS], wptr_t next,
+                                              const float (&sk)[NS], float after, float &r0, float &r1) {
     static_assert(NS % 2 == 0, "rows of fp16 pairs");
     float a0, a1;
     __asm__("v_mov_b32 %0, 0\n\tv_mov_b32 %1, 0" : "=v"(a0), "=v"(a1) : "v"(after));
+    wmac2x2(a0, a1, w[0], w[NS / 2], sk[0], sk[1]);
+    if constexpr (MORE) {
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int s = 0; s < NS; s += 2) wmac2x2(a0, a1, w0[s / 2], w1[s / 2], sk[s], sk[s + 1]);
+        for (int i = 0; i < NS; i++) wn[i] = next[i];
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int s = 2; s < NS; s += 2) wmac2x2(a0, a1, w[s / 2], w[NS / 2 + s / 2], sk[s], sk[s + 1]);
     r0 = a0, r1 = a1;
 }
 
@@ -196,13 +211,25 @@ k_hier_encode_lane(const void *__restrict__ src, long long so, long long si, uns
         // the predictions of targets r, r+1 start after deviation r-1 exists, so
         // the target coefficients are consumed pair by pair: without the ordering
         // the subtractions sink to the tree sum and everything spills
+        // W rows of pairs r and r + 2 alternate between wa and wb
+        static_assert(NT % 4 == 0, "two target pairs per step");
+        constexpr int RW = NS / 2;
+        uint32_t wa[NS], wb[NS];
+#pragma unroll
+        for (int i = 0; i < NS; i++) wa[i] = w32[i];
         float dv[NT];
 #pragma unroll
-        for (int r = 0; r < NT; r += 2) {
+        for (int r = 0; r < NT; r += 4) {
             float p0, p1;
-            hier_predict2<NS>(w32 + r * (NS / 2), w32 + (r + 1) * (NS / 2), sk, r > 0 ? dv[r - 1] : sk[0], p0, p1);
+            hier_predict2<NS, true>(wa, wb, w32 + (r + 2) * RW, sk, r > 0 ? dv[r - 1] : sk[0], p0, p1);
             dv[r] = c[HG.tgt[r]] - p0;
             dv[r + 1] = c[HG.tgt[r + 1]] - p1;
+            if (r + 4 < NT)
+                hier_predict2<NS, true>(wb, wa, w32 + (r + 4) * RW, sk, dv[r + 1], p0, p1);
+            else
+                hier_predict2<NS, false>(wb, wa, w32, sk, dv[r + 1], p0, p1);
+            dv[r + 2] = c[HG.tgt[r + 2]] - p0;
+            dv[r + 3] = c[HG.tgt[r + 3]] - p1;
         }
         float mag = sp_div(tree256_sum<NT, true>(dv), (float)NT);
         mag = mag < 1e-12f ? 1e-12f : mag;
@@ -272,10 +299,21 @@ k_hier_decode_lane(const unsigned char *__restrict__ src, long long so, void *__
         int o, i0, nv;
         M.at(t, o, i0, nv);
         const wptr_t w32 = (wptr_t)(W + (long long)__builtin_amdgcn_readfirstlane(o) * w_outer);
+        // W rows of pairs r and r + 2 alternate between wa and wb
+        static_assert(NT % 4 == 0, "two target pairs per step");
+        constexpr int RW = NS / 2;
+        uint32_t wa[NS], wb[NS];
+#pragma unroll
+        for (int i = 0; i < NS; i++) wa[i] = w32[i];
 #pragma unroll
         for (int r = 0; r < NT; r += 2) {
             float p0, p1;
-            hier_predict2<NS>(w32 + r * (NS / 2), w32 + (r + 1) * (NS / 2), sk, sk[0], p0, p1);
+            uint32_t(&w)[NS] = (r & 2) ? wb : wa;
+            uint32_t(&wn)[NS] = (r & 2) ? wa : wb;
+            if (r + 2 < NT)
+                hier_predict2<NS, true>(w, wn, w32 + (r + 2) * RW, sk, sk[0], p0, p1);
+            else
+                hier_predict2<NS, false>(w, wn, w32, sk, sk[0], p0, p1);
             c[HG.tgt[r]] = p0 + ((float)rec_extract(rec, G::res_bit + r * RBITS, RBITS) - center) * step;
             c[HG.tgt[r + 1]] = p1 + ((float)rec_extract(rec, G::res_bit + (r + 1) * RBITS, RBITS) - center) * step;
         }
