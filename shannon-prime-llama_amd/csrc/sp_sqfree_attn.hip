@@ -59,6 +59,18 @@ __device__ __forceinline__ void sq_coefficients(const uint32_t (&rec)[DW], float
 __device__ __forceinline__ float wave_max(float v) { return sp_wave_max_dpp(v); }
 __device__ __forceinline__ float wave_add(float v) { return sp_wave_sum_dpp(v); }
 
+// The score factors of one query head in chunks of at most 16: the skeleton part
+// (SK factors) then the residual part (PAD - SK), a chunk never spanning both.
+template <int SK, int PAD>
+struct QChunks {
+    static constexpr int NS = (SK + 15) / 16, NR = (PAD - SK + 15) / 16, N = NS + NR;
+    // coefficient index of chunk k's first factor, and the chunk's factor count
+    static constexpr int first(int k) { return k < NS ? 16 * k : SK + 16 * (k - NS); }
+    static constexpr int size(int k) {
+        return k < NS ? (SK - 16 * k < 16 ? SK - 16 * k : 16) : (PAD - SK - 16 * (k - NS) < 16 ? PAD - SK - 16 * (k - NS) : 16);
+    }
+};
+
 constexpr int EP = 65;  // LDS row pitch (floats) of the transposed coefficient chunk
 
 // Scores, online softmax and the V records' weighted coefficient sums. Block
@@ -140,17 +152,36 @@ k_sqfree_attn_split(const unsigned char *__restrict__ kc0, const unsigned char *
         for (int h = 0; h < GM; h++) {
             s[h] = -INFINITY;
             if (h < G) {
+                // q~ . e: the head's factors are wave-uniform and arrive by scalar loads,
+                // 16 at a time. In the full instances chunk k + 1 is loaded after the first
+                // product of chunk k (a scalar-load wait covers every scalar load in flight,
+                // so the next chunk cannot go out before the wait for the current one):
+                // 2% faster there; the scores-only instances measured 4% slower with it and
+                // keep the compiler's placement.
                 const float *__restrict__ qh = pq + h * ps;
+                using QC = QChunks<SK, PAD>;
+                float qa[16], qb[16];
+#pragma unroll
+                for (int i = 0; i < QC::size(0); i++) qa[i] = qh[i];
                 float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
-                for (int j = 0; j < SK; j += 2) {
-                    a0 = fmaf(qh[j], e[j], a0);
-                    if (j + 1 < SK) a1 = fmaf(qh[j + 1], e[j + 1], a1);
-                }
+                for (int k = 0; k < QC::N; k++) {
+                    float(&q)[16] = (k & 1) ? qb : qa;
+                    float(&qn)[16] = (k & 1) ? qa : qb;
+                    const int e0 = QC::first(k);
+                    a0 = fmaf(q[0], e[e0], a0);
+                    if (k + 1 < QC::N) {
+                        const float *__restrict__ qs = qh + (k + 1 < QC::NS ? 16 * (k + 1) : qo + 16 * (k + 1 - QC::NS));
+                        if constexpr (OUT) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int r = 0; r < PAD - SK; r += 2) {
-                    a0 = fmaf(qh[qo + r], e[SK + r], a0);
-                    if (r + 1 < PAD - SK) a1 = fmaf(qh[qo + r + 1], e[SK + r + 1], a1);
+                        for (int i = 0; i < QC::size(k + 1); i++) qn[i] = qs[i];
+                        if constexpr (OUT) __builtin_amdgcn_sched_barrier(0);
+                    }
+#pragma unroll
+                    for (int i = 1; i < QC::size(k); i++) {
+                        if (i & 1) a1 = fmaf(q[i], e[e0 + i], a1);
+                        else a0 = fmaf(q[i], e[e0 + i], a0);
+                    }
                 }
                 const float v = a0 + a1;
                 if (live) {
