@@ -70,27 +70,6 @@ __device__ __forceinline__ void copy_to_lds(T *dst, const T *__restrict__ src, i
     }
 }
 
-// Up to U * NT elements staged through registers: the loads go out first (load),
-// the LDS stores come later (store), so other work hides the loads' latency.
-template <typename T, int U>
-struct RegStage {
-    T v[U];
-    __device__ void load(const T *__restrict__ src, int n, int tid) {
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int i = tid + u * NT;
-            v[u] = i < n ? src[i] : T(0);
-        }
-    }
-    __device__ void store(T *dst, int n, int tid) const {
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int i = tid + u * NT;
-            if (i < n) dst[i] = v[u];
-        }
-    }
-};
-
 // REC_U * NT record dwords staged through registers by range-checked buffer loads
 // (dwords past n read as 0), so neither the loads nor the LDS stores need a per-element
 // test: the destination holds REC_U * NT dwords and takes them all, zeros included.
@@ -113,7 +92,7 @@ __host__ __device__ constexpr int rec_stage_bytes(int B) {
     return (((CH * B + 32) + 15) & ~15) > 4 * REC_U * NT ? (((CH * B + 32) + 15) & ~15) : 4 * REC_U * NT;
 }
 constexpr int K_STAGE = REC_U;  // K record dwords per thread staged through registers (256 x 103 B chunks)
-constexpr int W_STAGE = 40;  // W elements per thread staged through registers (n_target * n_skel <= 10240)
+constexpr int W_Q = 5;       // 16-byte W loads (8 fp16 each) per merge thread: n_target * n_skel <= 10240
 constexpr int W_DW = 20;     // W dwords (fp16 pairs) per prep thread staged through registers
 constexpr int MERGE_RUNS_PER_THREAD = 4;  // runs per merge thread (n_runs <= 4 * NT)
 
@@ -1166,13 +1145,15 @@ k_hier_attn_split(const SpPlan P, const SpHierAttnArgs A0, const SpSeqTab T, con
 
 // ---------------------------------------------------------------------------
 // Merge of the runs' partials for query head blockIdx.x, then c and its transform.
-// Dynamic LDS: c[pad], cs[n_skel], e[n_runs] floats, then the KV head's W fp16.
+// Dynamic LDS: c[pad], cs[n_skel], e[n_runs] floats, then the KV head's W fp16 (rounded up
+// to whole 16-byte chunks). The partial rows' pitch pp is a multiple of 4 floats.
 __global__ void __launch_bounds__(NT)
 k_hier_attn_merge(const SpPlan P, const SpHierAttnArgs A, const float *__restrict__ part, int n_runs) {
     extern __shared__ __attribute__((aligned(16))) unsigned char dsm[];
     __shared__ float red[2 * (NT / SP_WAVE)];
     __shared__ float cas_s[SP_CAS_TOTAL];
     __shared__ float tsm[SP_GEN_MAX_N];
+    __shared__ float red4[4 * NT];  // the run groups' coefficient sums
     const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;  // row h of n_seq * n_q
     const int G = A.n_q / A.n_kvh, kvh = (h % A.n_q) / G;
     const int ns = A.n_skel, nt = A.n_target, pp = A.pp;
@@ -1181,39 +1162,14 @@ k_hier_attn_merge(const SpPlan P, const SpHierAttnArgs A, const float *__restric
     float *e = cs + r4(ns);
     unsigned short *Ws = reinterpret_cast<unsigned short *>(e + r4(n_runs));
     const unsigned short *Wk = reinterpret_cast<const unsigned short *>(A.W) + (long long)kvh * A.w_outer;
-    // W loads while the partials are merged (no predictor: c_tgt is the weighted sum alone)
-    const bool has_w = A.W != nullptr;
-    const bool w_reg = has_w && nt * ns <= W_STAGE * NT;
-    RegStage<unsigned short, W_STAGE> wst;
-    if (w_reg) wst.load(Wk, nt * ns, tid);
-    else if (has_w) copy_to_lds<unsigned short, 16>(Ws, Wk, nt * ns, nt * ns, tid);
     const float *ph = part + (long long)h * n_runs * pp;
-    // range-checked buffer loads (rows past the last run read as 0): unconditional,
-    // so every load of a pass is in flight before the first wait
+    // range-checked buffer loads: rows past the last run and offsets past the buffer read
+    // as 0 with no traffic, so every load of a pass is unconditional and in flight
+    // before the first wait
     const __amdgpu_buffer_rsrc_t rp =
         __builtin_amdgcn_make_buffer_rsrc((void *)ph, (short)0, n_runs * pp * 4, 0x00020000);
-    // coefficients j0 = tid and j1 = tid + NT together, MP runs of each per load pass;
-    // the first pass goes out at entry with the m, l loads, the coefficient indices and
-    // the cas entry, so the block waits on memory once before its arithmetic
-    constexpr int MP = 96;
-    const int ncoef = ns + nt;
-    float v0[MP], v1[MP];
-    // a coefficient past the last reads at an offset past the buffer (0, with no traffic);
-    // a run past the last reads the last run's row again (finite, and its weight is 0)
-    auto load_pass = [&](int j0, int r0) {
-        const int o0 = j0 < ncoef ? (4 + j0) * 4 : 0x40000000, o1 = j0 + NT < ncoef ? (4 + j0 + NT) * 4 : 0x40000000;
-#pragma unroll
-        for (int k = 0; k < MP; k++) {
-            const int rr = min(r0 + k, n_runs - 1);
-            v0[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, o0, rr * pp * 4, 0));
-            v1[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, o1, rr * pp * 4, 0));
-        }
-    };
-    auto coef_idx = [&](int j) { return j < ns ? A.skel_idx[j] : A.tgt_idx[j - ns]; };
-    load_pass(tid, 0);
-    const int ci0 = tid < ncoef ? coef_idx(tid) : 0, ci1 = tid + NT < ncoef ? coef_idx(tid + NT) : 0;
-    const int ti0 = tid < nt ? A.tgt_idx[tid] : 0, ti1 = tid + NT < nt ? A.tgt_idx[tid + NT] : 0;
-    const float cas_v = cas_entry(P, tid);
+    // the runs' m and l first: their round trip gates the first barrier, and loads
+    // complete in issue order
     float mr[MERGE_RUNS_PER_THREAD], lr[MERGE_RUNS_PER_THREAD];
 #pragma unroll
     for (int u = 0; u < MERGE_RUNS_PER_THREAD; u++) {
@@ -1222,6 +1178,41 @@ k_hier_attn_merge(const SpPlan P, const SpHierAttnArgs A, const float *__restric
         lr[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, r * pp * 4 + 4, 0, 0));
         if (r >= n_runs) mr[u] = -INFINITY;
     }
+    // W (no predictor: c_tgt is the weighted sum alone) in 16-byte loads while the
+    // partials are merged, stored to LDS after the sums
+    const bool has_w = A.W != nullptr;
+    const bool w_reg = has_w && nt * ns <= W_Q * 8 * NT;
+    u32x4 wq[W_Q];
+    if (w_reg) {
+        const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void *)Wk, (short)0, 2 * nt * ns, 0x00020000);
+#pragma unroll
+        for (int u = 0; u < W_Q; u++)
+            wq[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, (tid + u * NT) * 16, 0, 0));
+    } else if (has_w) {
+        copy_to_lds<unsigned short, 16>(Ws, Wk, nt * ns, nt * ns, tid);
+    }
+    // coefficient sums: thread tid takes the quad q = tid % NQ (coefficients 4q..4q+3,
+    // one 16-byte load per run; the row pitch is a multiple of 4 floats) over the runs
+    // g, g + RG, ... of run group g = tid / NQ; the RG groups' sums meet in LDS
+    const int ncoef = ns + nt, NQ = (ncoef + 3) >> 2, RG = min(NT / NQ, 8);
+    const int q = tid % NQ, g = tid / NQ;
+    const int qo = g < RG ? (4 + 4 * q) * 4 : 0x40000000;
+    const int KR = g < RG ? (n_runs - g + RG - 1) / RG : 0;  // this thread's runs
+    constexpr int MP4 = 48;
+    u32x4 v[MP4];
+    auto load_pass = [&](int k0) {
+#pragma unroll
+        for (int k = 0; k < MP4; k++) {
+            const int r = g + RG * (k0 + k);
+            v[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 rp, k0 + k < KR ? qo : 0x40000000, min(r, n_runs - 1) * pp * 4, 0));
+        }
+    };
+    load_pass(0);
+    auto coef_idx = [&](int j) { return j < ns ? A.skel_idx[j] : A.tgt_idx[j - ns]; };
+    const int ci0 = tid < ncoef ? coef_idx(tid) : 0, ci1 = tid + NT < ncoef ? coef_idx(tid + NT) : 0;
+    const int ti0 = tid < nt ? A.tgt_idx[tid] : 0, ti1 = tid + NT < nt ? A.tgt_idx[tid + NT] : 0;
+    const float cas_v = cas_entry(P, tid);
     float mx = -INFINITY;
 #pragma unroll
     for (int u = 0; u < MERGE_RUNS_PER_THREAD; u++) mx = fmaxf(mx, mr[u]);
@@ -1242,29 +1233,37 @@ k_hier_attn_merge(const SpPlan P, const SpHierAttnArgs A, const float *__restric
     for (int k = tid; k < A.pad; k += NT) c[k] = 0.0f;
     __syncthreads();
     const float inv_l = sp_div(1.0f, (red[4] + red[5]) + (red[6] + red[7]));
-    for (int j0 = tid; j0 < ncoef; j0 += 2 * NT) {
-        const int j1 = j0 + NT;
-        float s0 = 0.0f, s1 = 0.0f;
-        for (int r0 = 0; r0 < n_runs; r0 += MP) {
-            if (j0 != tid || r0 != 0) load_pass(j0, r0);
+    float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k0 = 0; k0 < KR; k0 += MP4) {
+        if (k0 > 0) load_pass(k0);
 #pragma unroll
-            for (int k = 0; k < MP; k++) {
-                const float w = r0 + k < n_runs ? e[r0 + k] : 0.0f;
-                s0 = fmaf(v0[k], w, s0);
-                s1 = fmaf(v1[k], w, s1);  // (j1 past the coefficients: discarded below)
-            }
-        }
+        for (int k = 0; k < MP4; k++) {
+            const float w = k0 + k < KR ? e[g + RG * (k0 + k)] : 0.0f;
 #pragma unroll
-        for (int q = 0; q < 2; q++) {
-            const int j = q == 0 ? j0 : j1;
-            if (j >= ncoef) continue;
-            const float sj = (q == 0 ? s0 : s1) * inv_l;
-            const int ci = j0 == tid ? (q == 0 ? ci0 : ci1) : coef_idx(j);
-            if (j < ns) cs[j] = sj;
-            c[ci] = sj;  // targets: the dev part; W c_skel is added below
+            for (int i = 0; i < 4; i++) s4[i] = fmaf(__uint_as_float(v[k][i]), w, s4[i]);
         }
     }
-    if (w_reg) wst.store(Ws, nt * ns, tid);
+    if (g < RG) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) red4[g * 4 * NQ + 4 * q + i] = s4[i];
+    }
+    __syncthreads();
+    for (int j = tid; j < ncoef; j += NT) {
+        float sj = 0.0f;
+        for (int gg = 0; gg < RG; gg++) sj += red4[gg * 4 * NQ + j];
+        sj *= inv_l;
+        const int ci = j == tid ? ci0 : j == tid + NT ? ci1 : coef_idx(j);
+        if (j < ns) cs[j] = sj;
+        c[ci] = sj;  // targets: the dev part; W c_skel is added below
+    }
+    if (w_reg) {
+        u32x4 *Wq = reinterpret_cast<u32x4 *>(Ws);
+#pragma unroll
+        for (int u = 0; u < W_Q; u++) {
+            const int i = tid + u * NT;
+            if (i * 8 < nt * ns) Wq[i] = wq[u];
+        }
+    }
     __syncthreads();
     for (int t = tid; has_w && t < nt; t += NT) {
         float pred = 0.0f;
@@ -1368,11 +1367,14 @@ int sp_hier_attn_runs(const SpHierAttnArgs &A, int cus, int n_seq) {
     return std::max(1, std::min(std::min(n_chunks, per_head), MERGE_RUNS_PER_THREAD * NT));
 }
 
+// LDS bytes of the merge's W copy: whole 16-byte chunks (the register path stores them so).
+static size_t w_lds_bytes(const SpHierAttnArgs &A) { return (2 * (size_t)A.n_target * A.n_skel + 15) & ~(size_t)15; }
+
 hipError_t sp_launch_hier_attn(const SpPlan &P, const SpHierAttnArgs &A, const SpSeqTab &T, float *ws,
                                size_t ws_floats, int n_runs, hipStream_t s) {
     if (A.n_kv <= 0 || A.n_q <= 0 || A.n_kvh <= 0 || A.n_q % A.n_kvh || A.n_q / A.n_kvh > MAX_G ||
         A.pad > SP_GEN_MAX_N || A.n_skel + A.n_target > SP_GEN_MAX_N || A.hd > A.pad || n_runs <= 0 ||
-        A.ps != sp_hier_attn_prep_floats(A.n_skel, A.n_target) || A.pp < 4 + A.n_skel + A.n_target)
+        A.ps != sp_hier_attn_prep_floats(A.n_skel, A.n_target) || A.pp < 4 + A.n_skel + A.n_target || A.pp % 4)
         return hipErrorInvalidValue;
     if (T.n_seq < 1 || T.n_seq > SP_ATTN_MAX_SEQ || sp_hier_attn_workspace_floats(A, n_runs, T.n_seq) > ws_floats ||
         n_runs > MERGE_RUNS_PER_THREAD * NT)
@@ -1390,7 +1392,7 @@ hipError_t sp_launch_hier_attn(const SpPlan &P, const SpHierAttnArgs &A, const S
         const size_t red_b = 4 * ((size_t)npg_t * G * n_win * (32 / rb) + (size_t)npg_s * G * A.n_skel);
         lds_split = std::max(lds_split, red_b);
     }
-    const size_t lds_merge = 4 * (size_t)(r4(A.pad) + r4(A.n_skel) + r4(n_runs)) + 2 * (size_t)A.n_target * A.n_skel;
+    const size_t lds_merge = 4 * (size_t)(r4(A.pad) + r4(A.n_skel) + r4(n_runs)) + w_lds_bytes(A);
     if (lds_prep > 65536 || lds_split > 65536 || lds_merge > 65536) return hipErrorInvalidValue;
     float *prep = ws;
     float *part = ws + (size_t)T.n_seq * A.n_q * A.ps;
@@ -1408,7 +1410,7 @@ hipError_t sp_launch_hier_attn(const SpPlan &P, const SpHierAttnArgs &A, const S
 static bool prep_merge_args_ok(const SpHierAttnArgs &A) {
     return A.n_q > 0 && A.n_kvh > 0 && A.n_q % A.n_kvh == 0 && A.n_q / A.n_kvh <= MAX_G && A.pad <= SP_GEN_MAX_N &&
            A.n_skel + A.n_target <= SP_GEN_MAX_N && A.hd <= A.pad && A.ps == sp_hier_attn_prep_floats(A.n_skel, A.n_target) &&
-           A.pp >= 4 + A.n_skel + A.n_target;
+           A.pp >= 4 + A.n_skel + A.n_target && A.pp % 4 == 0;
 }
 
 hipError_t sp_launch_hier_attn_prep(const SpPlan &P, const SpHierAttnArgs &A, int n_seq, float *prep, hipStream_t s) {
@@ -1424,8 +1426,7 @@ hipError_t sp_launch_hier_attn_merge(const SpPlan &P, const SpHierAttnArgs &A, i
                                      int n_runs, hipStream_t s) {
     if (!prep_merge_args_ok(A) || !A.out || n_seq < 1 || n_runs <= 0 || n_runs > MERGE_RUNS_PER_THREAD * NT)
         return hipErrorInvalidValue;
-    const size_t lds_merge = 4 * (size_t)(r4(A.pad) + r4(A.n_skel) + r4(n_runs)) +
-                             (A.W ? 2 * (size_t)A.n_target * A.n_skel : 0);
+    const size_t lds_merge = 4 * (size_t)(r4(A.pad) + r4(A.n_skel) + r4(n_runs)) + (A.W ? w_lds_bytes(A) : 0);
     if (lds_merge > 65536) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_hier_attn_merge, dim3(n_seq * A.n_q), dim3(NT), lds_merge, s, P, A, part, n_runs);
     return hipGetLastError();
