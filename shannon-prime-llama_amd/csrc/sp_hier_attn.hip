@@ -1200,12 +1200,14 @@ k_hier_attn_merge(const SpPlan P, const SpHierAttnArgs A, const float *__restric
     const int KR = g < RG ? (n_runs - g + RG - 1) / RG : 0;  // this thread's runs
     constexpr int MP4 = 48;
     u32x4 v[MP4];
+    // (the run differs between the lanes of a wave, so its row offset goes in the
+    // per-lane offset, not the wave-uniform one)
     auto load_pass = [&](int k0) {
 #pragma unroll
         for (int k = 0; k < MP4; k++) {
             const int r = g + RG * (k0 + k);
             v[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                 rp, k0 + k < KR ? qo : 0x40000000, min(r, n_runs - 1) * pp * 4, 0));
+                                                 rp, k0 + k < KR ? qo + r * pp * 4 : 0x40000000, 0, 0));
         }
     };
     load_pass(0);
