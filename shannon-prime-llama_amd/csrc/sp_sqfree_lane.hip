@@ -236,7 +236,12 @@ hipError_t sq_dec_launch(const SpPlan &P, const unsigned char *src, long long so
     const long long n_tiles = (long long)n_outer * tpo;
     constexpr long long esz = DT == SP_DT_F16 ? 2 : 4;
     if (n_tiles > 0x7fffffffLL || din < 128 || 64 * din * esz + 128 * esz > 0x7fffffffLL) return hipErrorNotSupported;
-    const dim3 grid((unsigned)std::min<long long>(n_tiles, persistent_blocks())), block(64);
+    // several skeleton bands (a longer tile): a resident grid at two waves per SIMD, each
+    // block prefetching its next tile's records (one layer at sk 115: 46.8 -> 43.5 us); one
+    // band (a shorter tile): the persistent grid, whose second round of blocks was faster
+    // there (39.6 vs 43.6 us)
+    const int nb_max = SL::nb > 1 ? resident_blocks(2) : persistent_blocks();
+    const dim3 grid((unsigned)std::min<long long>(n_tiles, nb_max)), block(64);
     hipLaunchKernelGGL((k_sqfree_decode_lane<DT, 128, 154, SK, 3, true, SL>), grid, block, 0, s, src, so, dst, dout,
                        din, n_inner, tpo, (int)n_tiles, xf_const(P));
     return hipGetLastError();
