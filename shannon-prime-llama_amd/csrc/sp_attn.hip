@@ -258,16 +258,20 @@ k_attn_combine_wave(const SpPlan VP, const float *__restrict__ ws, int n_splits,
     const bool live = lane < n_splits;
     const float m = live ? base[lane * row] : -INFINITY;
     const float lv = live ? base[lane * row + 1] : 0.0f;
-    // the first CW splits' elements load at entry with m and l, so the row waits on
-    // memory once; later splits (rows of more than CW) load in the sum below
+    // rows of at most CW splits (a batch of short sequences) load their elements at
+    // entry with m and l, so the row waits on memory once; longer rows load them in the
+    // sum below (their loads at entry measured slower)
     constexpr int CW = 8, EPL = ATT_MAX_HD / SP_WAVE;
+    const bool pre = n_splits <= CW;
     float pv[CW][EPL];
+    if (pre) {
 #pragma unroll
-    for (int sp = 0; sp < CW; sp++) {
+        for (int sp = 0; sp < CW; sp++) {
 #pragma unroll
-        for (int u = 0; u < EPL; u++) {
-            const int i = lane + u * SP_WAVE;
-            pv[sp][u] = sp < n_splits && i < hd ? base[sp * row + 2 + i] : 0.0f;
+            for (int u = 0; u < EPL; u++) {
+                const int i = lane + u * SP_WAVE;
+                pv[sp][u] = sp < n_splits && i < hd ? base[sp * row + 2 + i] : 0.0f;
+            }
         }
     }
     float M = m;
@@ -280,16 +284,24 @@ k_attn_combine_wave(const SpPlan VP, const float *__restrict__ ws, int n_splits,
     e_s[lane] = e;
     __syncthreads();
     const float invL = 1.0f / L;
+    if (pre) {
 #pragma unroll
-    for (int u = 0; u < EPL; u++) {
-        const int i = lane + u * SP_WAVE;
-        if (i >= hd) continue;
-        float acc = 0.0f;
+        for (int u = 0; u < EPL; u++) {
+            const int i = lane + u * SP_WAVE;
+            if (i >= hd) continue;
+            float acc = 0.0f;
 #pragma unroll
-        for (int sp = 0; sp < CW; sp++)
-            if (sp < n_splits) acc = fmaf(pv[sp][u], e_s[sp], acc);
-        for (int sp = CW; sp < n_splits; sp++) acc = fmaf(base[sp * row + 2 + i], e_s[sp], acc);
-        c[i] = acc * invL;
+            for (int sp = 0; sp < CW; sp++)
+                if (sp < n_splits) acc = fmaf(pv[sp][u], e_s[sp], acc);
+            c[i] = acc * invL;
+        }
+    } else {
+        for (int i = lane; i < hd; i += SP_WAVE) {
+            float acc = 0.0f;
+#pragma unroll 8
+            for (int sp = 0; sp < n_splits; sp++) acc = fmaf(base[sp * row + 2 + i], e_s[sp], acc);
+            c[i] = acc * invL;
+        }
     }
     __syncthreads();
     sp_transform_lds(c, hd, VP, lane);
