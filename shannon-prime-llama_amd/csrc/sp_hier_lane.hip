@@ -54,6 +54,23 @@ __device__ __forceinline__ void wmac2x2(float &a0, float &a1, uint32_t w0, uint3
             : "s"(w0), "s"(w1), "v"(x0), "v"(x1));
 }
 
+// The first step of wmac2x2 for sums started at +0.0f: 0 + w*x rounds to w*x + 0,
+// which is what v_fma_mix gives (never -0), so the sums start at the first products
+// and the two zero moves and first adds drop out. after: a value the pair is ordered
+// behind (an operand the block does not read).
+__device__ __forceinline__ void wmac2x2_first(float &a0, float &a1, uint32_t w0, uint32_t w1, float x0, float x1,
+                                              float after) {
+    float p0, p1;
+    __asm__("v_fma_mix_f32 %0, %4, %6, 0 op_sel_hi:[1,0,0]\n\t"
+            "v_fma_mix_f32 %1, %5, %6, 0 op_sel_hi:[1,0,0]\n\t"
+            "v_fma_mix_f32 %2, %4, %7, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+            "v_fma_mix_f32 %3, %5, %7, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+            "v_add_f32 %0, %0, %2\n\t"
+            "v_add_f32 %1, %1, %3"
+            : "=&v"(a0), "=&v"(a1), "=&v"(p0), "=&v"(p1)
+            : "s"(w0), "s"(w1), "v"(x0), "v"(x1), "v"(after));
+}
+
 // W is read through the constant address space: the tile-uniform row address
 // then always becomes scalar loads (the scalar cache), whatever the compiler
 // can prove about the kernel's other stores.
@@ -62,8 +79,8 @@ typedef const __attribute__((address_space(4))) uint32_t *wptr_t;
 // pred = sum_s (float)W[t][s] * sk[s] from 0.0f, s ascending, separately
 // rounded products and adds (kernel_hier_predict, shannon_prime_hier.cu:74-92),
 // for targets t and t+1: w holds row t's NS/2 fp16 pairs, then row t+1's (in
-// scalar registers). after: a value the pair is ordered behind (the +0.0f
-// starts come from an asm that takes it as an operand).
+// scalar registers). after: a value the pair is ordered behind (the first
+// products come from an asm that takes it as an operand).
 //
 // With MORE, the rows of the next pair are loaded into wn after the first
 // products: the wait for w (loaded one pair earlier) comes before those
@@ -76,8 +93,7 @@ __device__ __forceinline__ void hier_predict2(const uint32_t (&w)[NS], uint32_t 
                                               const float (&sk)[NS], float after, float &r0, float &r1) {
     static_assert(NS % 2 == 0, "rows of fp16 pairs");
     float a0, a1;
-    __asm__("v_mov_b32 %0, 0\n\tv_mov_b32 %1, 0" : "=v"(a0), "=v"(a1) : "v"(after));
-    wmac2x2(a0, a1, w[0], w[NS / 2], sk[0], sk[1]);
+    wmac2x2_first(a0, a1, w[0], w[NS / 2], sk[0], sk[1], after);
     if constexpr (MORE) {
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -241,11 +257,14 @@ k_hier_encode_lane(const void *__restrict__ src, long long so, long long si, uns
         const float step = sp_div(2.0f * mag, (float)(L - 1));
         const float center = sp_div((float)(L - 1), 2.0f);
         const float inv_step = (step > 0.0f) ? sp_div(1.0f, step) : 0.0f;
+        // cl + 1.5 * 2^23 rounds cl (in [0, L-1]) to the nearest integer, ties to even,
+        // as rint does, into the low mantissa bits; rec_add_code sums it into the
+        // (still zero) residual field with the exponent bits cancelled
 #pragma unroll
         for (int r = 0; r < NT; r++) {
             const float v = dv[r] * inv_step + center;
             const float cl = fminf(fmaxf(v, 0.0f), (float)(L - 1));
-            rec_insert(rec, G::res_bit + r * RBITS, RBITS, (uint32_t)__builtin_rintf(cl));
+            rec_add_code(rec, G::res_bit + r * RBITS, RBITS, __float_as_uint(cl + 12582912.0f), 0);
         }
         tile_records_out<G::total, 64 * RP>(rec, rows, dp, dout, M, t, lane);
     }
