@@ -141,6 +141,32 @@ __device__ __forceinline__ uint32_t rec_get32(const uint32_t (&rec)[DW], int byt
     return sh ? __builtin_amdgcn_alignbit(rec[d + 1], rec[d], sh) : rec[d];
 }
 
+// a + b with |.| applied to the operands flagged (source modifiers of one v_add_f32;
+// the same rounding as the separate absolute values and add)
+template <bool AA, bool AB>
+__device__ __forceinline__ float add_abs_mod(float a, float b) {
+    if constexpr (!AA && !AB) return a + b;
+    float r;
+    if constexpr (AA && AB) __asm__("v_add_f32_e64 %0, |%1|, |%2|" : "=v"(r) : "v"(a), "v"(b));
+    else if constexpr (AA) __asm__("v_add_f32_e64 %0, |%1|, %2" : "=v"(r) : "v"(a), "v"(b));
+    else __asm__("v_add_f32_e64 %0, %1, |%2|" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
+// Whether slot t of tree256_sum<N> still holds a raw v[t] after stage s (s = 256: the
+// v[t + 256] pass, then 128..1): every slot's first add applies the |.| it owes.
+template <int N>
+__device__ constexpr bool tree_slot_raw(int t, int s) {
+    if (t + 256 < N) return false;  // paired with v[t + 256] first
+    int n = N < 256 ? N : 256;
+    for (int k = 128; k >= s && k > 0; k >>= 1) {
+        if (t < k && t + k < n) return false;  // accumulated at stage k
+        if (t >= k && t < n) return false;     // added into slot t - k at stage k
+        n = n < k ? n : k;
+    }
+    return true;
+}
+
 // Sum in the order of the reference's 256-slot block reductions over n values
 // (slot t accumulates v[t], v[t + 256] from 0.0f, then slot[t] += slot[t + s]
 // for s = 128..1); slots at or past n hold +0.0f, so adding them is skipped.
@@ -153,19 +179,41 @@ __device__ __forceinline__ float tree256_sum(const float *v) {
     static_assert(N <= 512, "at most two values per slot");
     constexpr int NS = N < 256 ? N : 256;
     float sl[NS];
+    if constexpr (ABS) {
+        // the absolute values ride on the first add each term takes part in
 #pragma unroll
-    for (int t = 0; t < NS; t++) sl[t] = ABS ? fabsf(v[t]) : v[t];
+        for (int t = 0; t < NS; t++) sl[t] = t + 256 < N ? add_abs_mod<true, true>(v[t], v[t + 256]) : v[t];
+        int n = NS;
 #pragma unroll
-    for (int t = 0; t + 256 < N; t++) sl[t] = sl[t] + (ABS ? fabsf(v[t + 256]) : v[t + 256]);
-    int n = NS;
+        for (int s = 128; s > 0; s >>= 1) {
 #pragma unroll
-    for (int s = 128; s > 0; s >>= 1) {
+            for (int t = 0; t < s; t++) {
+                if (t + s < n) {
+                    const bool ra = tree_slot_raw<N>(t, 2 * s), rb = tree_slot_raw<N>(t + s, 2 * s);
+                    if (ra && rb) sl[t] = add_abs_mod<true, true>(sl[t], sl[t + s]);
+                    else if (ra) sl[t] = add_abs_mod<true, false>(sl[t], sl[t + s]);
+                    else if (rb) sl[t] = add_abs_mod<false, true>(sl[t], sl[t + s]);
+                    else sl[t] = sl[t] + sl[t + s];
+                }
+            }
+            n = n < s ? n : s;
+        }
+        return tree_slot_raw<N>(0, 1) ? fabsf(sl[0]) : sl[0];
+    } else {
 #pragma unroll
-        for (int t = 0; t < s; t++)
-            if (t + s < n) sl[t] = sl[t] + sl[t + s];
-        n = n < s ? n : s;
+        for (int t = 0; t < NS; t++) sl[t] = v[t];
+#pragma unroll
+        for (int t = 0; t + 256 < N; t++) sl[t] = sl[t] + v[t + 256];
+        int n = NS;
+#pragma unroll
+        for (int s = 128; s > 0; s >>= 1) {
+#pragma unroll
+            for (int t = 0; t < s; t++)
+                if (t + s < n) sl[t] = sl[t] + sl[t + s];
+            n = n < s ? n : s;
+        }
+        return sl[0] + 0.0f;
     }
-    return ABS ? sl[0] : sl[0] + 0.0f;
 }
 
 // p=2 VHT2 over a register-resident vector: stages len = 1, 2, ..., HD/2 in
