@@ -64,12 +64,13 @@ CASES = [
     (256, 2, [5, 5], 1, 8, 333, 0),     # GQA 8: window and skeleton items in two rounds per lane
     (256, 2, [5, 5], 2, 6, 260, 1),     # GQA 3: a pair with one real head
     # the bench's run sizing (no cap): three resident blocks per CU spread over the KV
-    # heads, so more than 48 runs per head and the merge sums them in several passes
+    # heads, so about 96 runs per head, which the merge splits over its run groups
     (256, 2, [5, 5], 8, 16, 25000, 0),  # configs[4] head layout: 96 runs per head (98 chunks)
-    (256, 2, [5, 5], 1, 2, 25000, 0),   # one KV head: 98 runs of one chunk, three merge passes
+    (256, 2, [5, 5], 1, 2, 25000, 0),   # one KV head: 98 runs of one chunk, three run groups of
+                                        # 32-33 runs each in the merge
     (256, 2, [5, 5], 1, 2, 75300, 49),  # 49 runs of 6-7 chunks (295 chunks): long online softmax
                                         # chains and the scores-only instance's K prefetch across
-                                        # chunks, then a second merge pass
+                                        # chunks
 ]
 
 
