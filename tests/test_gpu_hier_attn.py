@@ -68,6 +68,8 @@ CASES = [
     (256, 2, [5, 5], 8, 16, 25000, 0),  # configs[4] head layout: 96 runs per head (98 chunks)
     (256, 2, [5, 5], 1, 2, 25000, 0),   # one KV head: 98 runs of one chunk, three run groups of
                                         # 32-33 runs each in the merge
+    (256, 2, [5, 5], 1, 2, 40000, 0),   # 157 runs: each merge run group (3 x 48 loads a pass)
+                                        # takes a second pass
     (256, 2, [5, 5], 1, 2, 75300, 49),  # 49 runs of 6-7 chunks (295 chunks): long online softmax
                                         # chains and the scores-only instance's K prefetch across
                                         # chunks

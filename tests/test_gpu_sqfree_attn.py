@@ -64,6 +64,8 @@ CASES = [
     (115, [3], 2, 10, 333, 2),                # GQA 5
     (77, [5, 4, 4, 4, 5], 3, 3, 64, 0),       # MHA, exactly one tile
     (115, [3], 1, 8, 1, 0),                   # a single position
+    (115, [3], 1, 8, 20000, 0),               # 313 runs of one tile: each merge run group (6 x 48
+                                              # loads a pass) takes a second pass
 ]
 
 
