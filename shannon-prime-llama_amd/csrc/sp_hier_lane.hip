@@ -71,6 +71,44 @@ __device__ __forceinline__ void wmac2x2_first(float &a0, float &a1, uint32_t w0,
             : "s"(w0), "s"(w1), "v"(x0), "v"(x1), "v"(after));
 }
 
+// Three predictions at once: the wmac2x2 steps for targets t, t+1, t+2 (three
+// independent chains, so each add has two free slots after its product).
+__device__ __forceinline__ void wmac3x2(float &a0, float &a1, float &a2, uint32_t w0, uint32_t w1, uint32_t w2,
+                                        float x0, float x1) {
+    float p0, p1, p2;
+    __asm__("v_fma_mix_f32 %3, %6, %9, 0 op_sel_hi:[1,0,0]\n\t"
+            "v_fma_mix_f32 %4, %7, %9, 0 op_sel_hi:[1,0,0]\n\t"
+            "v_fma_mix_f32 %5, %8, %9, 0 op_sel_hi:[1,0,0]\n\t"
+            "v_add_f32 %0, %0, %3\n\t"
+            "v_add_f32 %1, %1, %4\n\t"
+            "v_add_f32 %2, %2, %5\n\t"
+            "v_fma_mix_f32 %3, %6, %10, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+            "v_fma_mix_f32 %4, %7, %10, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+            "v_fma_mix_f32 %5, %8, %10, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+            "v_add_f32 %0, %0, %3\n\t"
+            "v_add_f32 %1, %1, %4\n\t"
+            "v_add_f32 %2, %2, %5"
+            : "+v"(a0), "+v"(a1), "+v"(a2), "=&v"(p0), "=&v"(p1), "=&v"(p2)
+            : "s"(w0), "s"(w1), "s"(w2), "v"(x0), "v"(x1));
+}
+
+// The first step of wmac3x2 for sums started at +0.0f (see wmac2x2_first).
+__device__ __forceinline__ void wmac3x2_first(float &a0, float &a1, float &a2, uint32_t w0, uint32_t w1,
+                                              uint32_t w2, float x0, float x1, float after) {
+    float p0, p1, p2;
+    __asm__("v_fma_mix_f32 %0, %6, %9, 0 op_sel_hi:[1,0,0]\n\t"
+            "v_fma_mix_f32 %1, %7, %9, 0 op_sel_hi:[1,0,0]\n\t"
+            "v_fma_mix_f32 %2, %8, %9, 0 op_sel_hi:[1,0,0]\n\t"
+            "v_fma_mix_f32 %3, %6, %10, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+            "v_fma_mix_f32 %4, %7, %10, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+            "v_fma_mix_f32 %5, %8, %10, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+            "v_add_f32 %0, %0, %3\n\t"
+            "v_add_f32 %1, %1, %4\n\t"
+            "v_add_f32 %2, %2, %5"
+            : "=&v"(a0), "=&v"(a1), "=&v"(a2), "=&v"(p0), "=&v"(p1), "=&v"(p2)
+            : "s"(w0), "s"(w1), "s"(w2), "v"(x0), "v"(x1), "v"(after));
+}
+
 // W is read through the constant address space: the tile-uniform row address
 // then always becomes scalar loads (the scalar cache), whatever the compiler
 // can prove about the kernel's other stores.
@@ -103,6 +141,28 @@ __device__ __forceinline__ void hier_predict2(const uint32_t (&w)[NS], uint32_t 
 #pragma unroll
     for (int s = 2; s < NS; s += 2) wmac2x2(a0, a1, w[s / 2], w[NS / 2 + s / 2], sk[s], sk[s + 1]);
     r0 = a0, r1 = a1;
+}
+
+// The same for targets t, t+1, t+2 (w: the three rows, NS/2 pairs each): one wait
+// for three rows, with three targets' products (~180 instructions) in front of the
+// next wait instead of two targets' (~120).
+template <int NS, bool MORE>
+__device__ __forceinline__ void hier_predict3(const uint32_t (&w)[3 * NS / 2], uint32_t (&wn)[3 * NS / 2],
+                                              wptr_t next, const float (&sk)[NS], float after, float &r0,
+                                              float &r1, float &r2) {
+    static_assert(NS % 2 == 0, "rows of fp16 pairs");
+    constexpr int RW = NS / 2;
+    float a0, a1, a2;
+    wmac3x2_first(a0, a1, a2, w[0], w[RW], w[2 * RW], sk[0], sk[1], after);
+    if constexpr (MORE) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 3 * RW; i++) wn[i] = next[i];
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int s = 2; s < NS; s += 2) wmac3x2(a0, a1, a2, w[s / 2], w[RW + s / 2], w[2 * RW + s / 2], sk[s], sk[s + 1]);
+    r0 = a0, r1 = a1, r2 = a2;
 }
 
 // fp16 halves H of a and b: a + b rounded once (exact widening).
@@ -227,25 +287,27 @@ k_hier_encode_lane(const void *__restrict__ src, long long so, long long si, uns
         // the predictions of targets r, r+1 start after deviation r-1 exists, so
         // the target coefficients are consumed pair by pair: without the ordering
         // the subtractions sink to the tree sum and everything spills
-        // W rows of pairs r and r + 2 alternate between wa and wb
-        static_assert(NT % 4 == 0, "two target pairs per step");
+        // W rows of target triples r and r + 3 alternate between wa and wb
+        static_assert(NT % 6 == 0, "two target triples per step");
         constexpr int RW = NS / 2;
-        uint32_t wa[NS], wb[NS];
+        uint32_t wa[3 * RW], wb[3 * RW];
 #pragma unroll
-        for (int i = 0; i < NS; i++) wa[i] = w32[i];
+        for (int i = 0; i < 3 * RW; i++) wa[i] = w32[i];
         float dv[NT];
 #pragma unroll
-        for (int r = 0; r < NT; r += 4) {
-            float p0, p1;
-            hier_predict2<NS, true>(wa, wb, w32 + (r + 2) * RW, sk, r > 0 ? dv[r - 1] : sk[0], p0, p1);
+        for (int r = 0; r < NT; r += 6) {
+            float p0, p1, p2;
+            hier_predict3<NS, true>(wa, wb, w32 + (r + 3) * RW, sk, r > 0 ? dv[r - 1] : sk[0], p0, p1, p2);
             dv[r] = c[HG.tgt[r]] - p0;
             dv[r + 1] = c[HG.tgt[r + 1]] - p1;
-            if (r + 4 < NT)
-                hier_predict2<NS, true>(wb, wa, w32 + (r + 4) * RW, sk, dv[r + 1], p0, p1);
+            dv[r + 2] = c[HG.tgt[r + 2]] - p2;
+            if (r + 6 < NT)
+                hier_predict3<NS, true>(wb, wa, w32 + (r + 6) * RW, sk, dv[r + 2], p0, p1, p2);
             else
-                hier_predict2<NS, false>(wb, wa, w32, sk, dv[r + 1], p0, p1);
-            dv[r + 2] = c[HG.tgt[r + 2]] - p0;
-            dv[r + 3] = c[HG.tgt[r + 3]] - p1;
+                hier_predict3<NS, false>(wb, wa, w32, sk, dv[r + 2], p0, p1, p2);
+            dv[r + 3] = c[HG.tgt[r + 3]] - p0;
+            dv[r + 4] = c[HG.tgt[r + 4]] - p1;
+            dv[r + 5] = c[HG.tgt[r + 5]] - p2;
         }
         float mag = sp_div(tree256_sum<NT, true>(dv), (float)NT);
         mag = mag < 1e-12f ? 1e-12f : mag;
@@ -318,23 +380,24 @@ k_hier_decode_lane(const unsigned char *__restrict__ src, long long so, void *__
         int o, i0, nv;
         M.at(t, o, i0, nv);
         const wptr_t w32 = (wptr_t)(W + (long long)__builtin_amdgcn_readfirstlane(o) * w_outer);
-        // W rows of pairs r and r + 2 alternate between wa and wb
-        static_assert(NT % 4 == 0, "two target pairs per step");
+        // W rows of target triples r and r + 3 alternate between wa and wb
+        static_assert(NT % 6 == 0, "two target triples per step");
         constexpr int RW = NS / 2;
-        uint32_t wa[NS], wb[NS];
+        uint32_t wa[3 * RW], wb[3 * RW];
 #pragma unroll
-        for (int i = 0; i < NS; i++) wa[i] = w32[i];
+        for (int i = 0; i < 3 * RW; i++) wa[i] = w32[i];
 #pragma unroll
-        for (int r = 0; r < NT; r += 2) {
-            float p0, p1;
-            uint32_t(&w)[NS] = (r & 2) ? wb : wa;
-            uint32_t(&wn)[NS] = (r & 2) ? wa : wb;
-            if (r + 2 < NT)
-                hier_predict2<NS, true>(w, wn, w32 + (r + 2) * RW, sk, sk[0], p0, p1);
+        for (int r = 0; r < NT; r += 3) {
+            float p[3];
+            uint32_t(&w)[3 * RW] = ((r / 3) & 1) ? wb : wa;
+            uint32_t(&wn)[3 * RW] = ((r / 3) & 1) ? wa : wb;
+            if (r + 3 < NT)
+                hier_predict3<NS, true>(w, wn, w32 + (r + 3) * RW, sk, sk[0], p[0], p[1], p[2]);
             else
-                hier_predict2<NS, false>(w, wn, w32, sk, sk[0], p0, p1);
-            c[HG.tgt[r]] = p0 + ((float)rec_extract(rec, G::res_bit + r * RBITS, RBITS) - center) * step;
-            c[HG.tgt[r + 1]] = p1 + ((float)rec_extract(rec, G::res_bit + (r + 1) * RBITS, RBITS) - center) * step;
+                hier_predict3<NS, false>(w, wn, w32, sk, sk[0], p[0], p[1], p[2]);
+#pragma unroll
+            for (int k = 0; k < 3; k++)
+                c[HG.tgt[r + k]] = p[k] + ((float)rec_extract(rec, G::res_bit + (r + k) * RBITS, RBITS) - center) * step;
         }
         vil_stages<PAD, 0, 1>(c, K);
         if constexpr (LISTED)
