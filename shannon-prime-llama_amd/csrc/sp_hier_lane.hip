@@ -33,46 +33,13 @@ struct HierGeoC {
 template <int PAD, int NS>
 __device__ constexpr HierGeoC<PAD, NS> kHier{};
 
-// Two predictions at once: a0 += w0.lo*x0, a1 += w1.lo*x0, a0 += w0.hi*x1,
-// a1 += w1.hi*x1, each step rounded once. v_fma_mix widens the fp16 weight (from
-// a scalar register) exactly and rounds w*x + 0 (the + 0 turns a -0 product into
-// +0, which a running sum started at +0.0f cannot tell apart: such a sum is
-// never -0), then v_add_f32. The two independent chains give each add a free
-// slot after its product; one asm block keeps products next to their adds, so
-// the predictions stay serial chains in registers.
-__device__ __forceinline__ void wmac2x2(float &a0, float &a1, uint32_t w0, uint32_t w1, float x0, float x1) {
-    float p0, p1;
-    __asm__("v_fma_mix_f32 %2, %4, %6, 0 op_sel_hi:[1,0,0]\n\t"
-            "v_fma_mix_f32 %3, %5, %6, 0 op_sel_hi:[1,0,0]\n\t"
-            "v_add_f32 %0, %0, %2\n\t"
-            "v_add_f32 %1, %1, %3\n\t"
-            "v_fma_mix_f32 %2, %4, %7, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
-            "v_fma_mix_f32 %3, %5, %7, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
-            "v_add_f32 %0, %0, %2\n\t"
-            "v_add_f32 %1, %1, %3"
-            : "+v"(a0), "+v"(a1), "=&v"(p0), "=&v"(p1)
-            : "s"(w0), "s"(w1), "v"(x0), "v"(x1));
-}
-
-// The first step of wmac2x2 for sums started at +0.0f: 0 + w*x rounds to w*x + 0,
-// which is what v_fma_mix gives (never -0), so the sums start at the first products
-// and the two zero moves and first adds drop out. after: a value the pair is ordered
-// behind (an operand the block does not read).
-__device__ __forceinline__ void wmac2x2_first(float &a0, float &a1, uint32_t w0, uint32_t w1, float x0, float x1,
-                                              float after) {
-    float p0, p1;
-    __asm__("v_fma_mix_f32 %0, %4, %6, 0 op_sel_hi:[1,0,0]\n\t"
-            "v_fma_mix_f32 %1, %5, %6, 0 op_sel_hi:[1,0,0]\n\t"
-            "v_fma_mix_f32 %2, %4, %7, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
-            "v_fma_mix_f32 %3, %5, %7, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
-            "v_add_f32 %0, %0, %2\n\t"
-            "v_add_f32 %1, %1, %3"
-            : "=&v"(a0), "=&v"(a1), "=&v"(p0), "=&v"(p1)
-            : "s"(w0), "s"(w1), "v"(x0), "v"(x1), "v"(after));
-}
-
-// Three predictions at once: the wmac2x2 steps for targets t, t+1, t+2 (three
-// independent chains, so each add has two free slots after its product).
+// Three predictions at once: ak += wk.lo*x0, then ak += wk.hi*x1 for k = 0..2, each
+// step rounded once. v_fma_mix widens the fp16 weight (from a scalar register)
+// exactly and rounds w*x + 0 (the + 0 turns a -0 product into +0, which a running
+// sum started at +0.0f cannot tell apart: such a sum is never -0), then v_add_f32.
+// The three independent chains give each add two free slots after its product; one
+// asm block keeps products next to their adds, so the predictions stay serial chains
+// in registers.
 __device__ __forceinline__ void wmac3x2(float &a0, float &a1, float &a2, uint32_t w0, uint32_t w1, uint32_t w2,
                                         float x0, float x1) {
     float p0, p1, p2;
@@ -92,7 +59,10 @@ __device__ __forceinline__ void wmac3x2(float &a0, float &a1, float &a2, uint32_
             : "s"(w0), "s"(w1), "s"(w2), "v"(x0), "v"(x1));
 }
 
-// The first step of wmac3x2 for sums started at +0.0f (see wmac2x2_first).
+// The first step of wmac3x2 for sums started at +0.0f: 0 + w*x rounds to w*x + 0,
+// which is what v_fma_mix gives (never -0), so the sums start at the first products
+// (no zero moves, no first adds). after: a value the triple is ordered behind (an
+// operand the block does not read).
 __device__ __forceinline__ void wmac3x2_first(float &a0, float &a1, float &a2, uint32_t w0, uint32_t w1,
                                               uint32_t w2, float x0, float x1, float after) {
     float p0, p1, p2;
@@ -114,38 +84,19 @@ __device__ __forceinline__ void wmac3x2_first(float &a0, float &a1, float &a2, u
 // can prove about the kernel's other stores.
 typedef const __attribute__((address_space(4))) uint32_t *wptr_t;
 
-// pred = sum_s (float)W[t][s] * sk[s] from 0.0f, s ascending, separately
-// rounded products and adds (kernel_hier_predict, shannon_prime_hier.cu:74-92),
-// for targets t and t+1: w holds row t's NS/2 fp16 pairs, then row t+1's (in
-// scalar registers). after: a value the pair is ordered behind (the first
-// products come from an asm that takes it as an operand).
+// pred = sum_s (float)W[t][s] * sk[s] from 0.0f, s ascending, separately rounded
+// products and adds (kernel_hier_predict, shannon_prime_hier.cu:74-92), for targets
+// t, t+1, t+2: w holds their three rows, NS/2 fp16 pairs each, in scalar registers.
+// after: a value the triple is ordered behind.
 //
-// With MORE, the rows of the next pair are loaded into wn after the first
-// products: the wait for w (loaded one pair earlier) comes before those
-// products, and a scalar-load wait covers every scalar load in flight, so rows
-// loaded before it would be waited for there too. The scheduling barriers keep
-// the loads in that place; loaded where their own pair starts, each pair's rows
-// left the wave (one per SIMD) waiting ~600 times per tile.
-template <int NS, bool MORE>
-__device__ __forceinline__ void hier_predict2(const uint32_t (&w)[NS], uint32_t (&wn)[NS], wptr_t next,
-                                              const float (&sk)[NS], float after, float &r0, float &r1) {
-    static_assert(NS % 2 == 0, "rows of fp16 pairs");
-    float a0, a1;
-    wmac2x2_first(a0, a1, w[0], w[NS / 2], sk[0], sk[1], after);
-    if constexpr (MORE) {
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < NS; i++) wn[i] = next[i];
-        __builtin_amdgcn_sched_barrier(0);
-    }
-#pragma unroll
-    for (int s = 2; s < NS; s += 2) wmac2x2(a0, a1, w[s / 2], w[NS / 2 + s / 2], sk[s], sk[s + 1]);
-    r0 = a0, r1 = a1;
-}
-
-// The same for targets t, t+1, t+2 (w: the three rows, NS/2 pairs each): one wait
-// for three rows, with three targets' products (~180 instructions) in front of the
-// next wait instead of two targets' (~120).
+// With MORE, the rows of the next triple are loaded into wn after the first
+// products: the wait for w (loaded one triple earlier) comes before those products,
+// and a scalar-load wait covers every scalar load in flight, so rows loaded before it
+// would be waited for there too. The scheduling barriers keep the loads in that
+// place, with three targets' products (~180 VALU instructions) in front of the next
+// wait. Loaded where their own target pair started, the rows left the wave (one per
+// SIMD) waiting ~600 times per tile; one pair ahead, two targets' products covered
+// each wait.
 template <int NS, bool MORE>
 __device__ __forceinline__ void hier_predict3(const uint32_t (&w)[3 * NS / 2], uint32_t (&wn)[3 * NS / 2],
                                               wptr_t next, const float (&sk)[NS], float after, float &r0,
