@@ -46,7 +46,7 @@ KERNEL_NAMES = {"k_enc": "k_ship_encode_lane<Layout<128,5,5,4,3>, fp16, Mobius>"
 VALU_PER_TILE = {"k_enc": 1693, "v_enc": 1608, "k_dec": 1559, "v_dec": 1799,  # configs[1], hd 128
                  "hd96_k_enc": 2089, "hd96_v_enc": 2087, "hd96_k_dec": 2225, "hd96_v_dec": 2224,
                  "sqfree_k_enc": 7256, "sqfree_v_enc": 7207, "sqfree_k_dec": 5802, "sqfree_v_dec": 5948,
-                 "hier_enc": 32570, "hier_dec": 31193}
+                 "hier_enc": 32633, "hier_dec": 31228}
 ENGINE_CLOCK_HZ = 2.4e9  # MI355X peak engine clock
 
 
